@@ -1,0 +1,728 @@
+// C-ABI layer of the delegate (include/elmh.h): contexts, weight upload + repack, scratch, and
+// the dispatch of edgelm's matmul family onto the HIP kernels of elmh_kernels.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "elmh.h"
+#include "elmh_internal.hpp"
+
+using namespace elmh;
+
+struct elmh_weight {
+  DevWeight w;
+};
+
+namespace {
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+
+thread_local std::string g_last_error;
+
+}  // namespace
+
+struct elmh_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  std::string arch;
+  // staging for the host-pointer entry points
+  DevBuf x, y, res;
+  // activation-quantization scratch
+  DevBuf xq, xd, xs;
+  // SwiGLU fallback (gate/up of different layouts)
+  DevBuf gu;
+};
+
+namespace {
+
+int fail(elmh_ctx* c, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  if (c) c->err = buf;
+  return code;
+}
+
+#define HIP_OR_FAIL(ctx, call)                                                                              \
+  do {                                                                                                      \
+    hipError_t e_ = (call);                                                                                 \
+    if (e_ != hipSuccess) return fail((ctx), ELMH_ERR_HIP, "%s: %s", #call, hipGetErrorString(e_));         \
+  } while (0)
+
+bool capturing(elmh_ctx* c) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(c->stream, &st) != hipSuccess) return false;
+  return st != hipStreamCaptureStatusNone;
+}
+
+int ensure(elmh_ctx* c, DevBuf& b, size_t bytes) {
+  if (bytes <= b.cap) return ELMH_OK;
+  if (capturing(c)) return fail(c, ELMH_ERR_ARG, "scratch of %zu bytes needed during graph capture: call elmh_reserve first", bytes);
+  if (b.p) {
+    HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
+    HIP_OR_FAIL(c, hipFree(b.p));
+    b.p = nullptr;
+    b.cap = 0;
+  }
+  const size_t cap = std::max<size_t>(bytes, 4096);
+  if (hipMalloc(&b.p, cap) != hipSuccess) return fail(c, ELMH_ERR_OOM, "hipMalloc(%zu) failed", cap);
+  b.cap = cap;
+  return ELMH_OK;
+}
+
+int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// Row-tile height of the repacked layout: the largest of 32/16/8/4 rows whose tile (all blocks of
+// those rows) stays near 48 KB, so a decode GEMV workgroup streams one contiguous chunk of that size.
+// Depends on dtype and K only, so every weight sharing an input (MATMUL_N, gate/up) agrees.
+int choose_H(int dtype, int64_t K) {
+  const int64_t nb = (K + kBlock - 1) / kBlock;
+  const int64_t per_row = nb * (dtype == ELMH_Q4 ? 20 : 32);
+  for (int H : {32, 16, 8})
+    if (H * per_row <= 48 * 1024) return H;
+  return 4;
+}
+
+bool a8_applies(const DevWeight& w) { return (w.dtype == ELMH_Q8 || w.dtype == ELMH_Q4) && w.cols % kBlock == 0; }
+
+// Largest token count the int8 GEMV takes for these weights, 0 if none.
+int gemv_tokens(const DevWeight& w, int nsel) {
+  const int K = (int)w.cols, nb = (int)w.nb;
+  for (int nt : {4, 2, 1}) {
+    if (nt > gemv_max_tokens(K)) continue;
+    if (gemv_lds_bytes(nt, K, nb, w.H, nsel) <= 64 * 1024) return nt;
+  }
+  return 0;
+}
+
+int check_targets(elmh_ctx* c, int T, int64_t K, int n, elmh_weight* const* w, float* const* y) {
+  if (T < 1 || K < 1) return fail(c, ELMH_ERR_ARG, "bad shape T=%d K=%lld", T, (long long)K);
+  if (n < 1 || !w || !y) return fail(c, ELMH_ERR_ARG, "no targets");
+  for (int i = 0; i < n; ++i) {
+    if (!w[i] || !y[i]) return fail(c, ELMH_ERR_ARG, "target %d: null weight or output", i);
+    if (w[i]->w.cols != K) return fail(c, ELMH_ERR_ARG, "target %d: K=%lld but weight has %lld columns", i, (long long)K, (long long)w[i]->w.cols);
+  }
+  return ELMH_OK;
+}
+
+// ---------------------------------------------------------------- device-pointer dispatch
+
+int run_gemv_group(elmh_ctx* c, const float* x, const int8_t* xq, const float* xd, const int32_t* xs, int T,
+                   int64_t K, const std::vector<int>& idx, elmh_weight* const* w, float* const* y,
+                   const float* const* res) {
+  for (size_t i0 = 0; i0 < idx.size(); i0 += kMaxTargets) {
+    GemvArgs a{};
+    const size_t n = std::min<size_t>(kMaxTargets, idx.size() - i0);
+    int tiles = 0;
+    const DevWeight& w0 = w[idx[i0]]->w;
+    a.H = w0.H;
+    for (size_t j = 0; j < n; ++j) {
+      const DevWeight& wd = w[idx[i0 + j]]->w;
+      a.tg[j] = {wd.data, wd.scales, y[idx[i0 + j]], res ? res[idx[i0 + j]] : nullptr, (int)wd.rows,
+                 (int)(wd.rows_pad / wd.H)};
+      a.tile_start[j] = tiles;
+      tiles += a.tg[j].tiles;
+    }
+    a.tile_start[n] = tiles;
+    a.n_targets = (int)n;
+    a.x = x;
+    a.xq = xq;
+    a.xd = xd;
+    a.xs = xs;
+    a.T = T;
+    a.K = (int)K;
+    a.nb = (int)(K / kBlock);
+    HIP_OR_FAIL(c, launch_gemv_a8(w0.dtype, 0, a, tiles, c->stream));
+  }
+  return ELMH_OK;
+}
+
+int run_gemm_group(elmh_ctx* c, const int8_t* xq, const float* xd, int T, int Tpad, int64_t K,
+                   const std::vector<int>& idx, elmh_weight* const* w, float* const* y, const float* const* res,
+                   int token_mode, int fast) {
+  for (size_t i0 = 0; i0 < idx.size(); i0 += kMaxTargets) {
+    GemmArgs a{};
+    const size_t n = std::min<size_t>(kMaxTargets, idx.size() - i0);
+    int tiles = 0;
+    const DevWeight& w0 = w[idx[i0]]->w;
+    a.H = w0.H;
+    for (size_t j = 0; j < n; ++j) {
+      const DevWeight& wd = w[idx[i0 + j]]->w;
+      a.tg[j] = {wd.data, wd.scales, y[idx[i0 + j]], res ? res[idx[i0 + j]] : nullptr, (int)wd.rows,
+                 (int)(wd.rows_pad / kGemmTileN)};
+      a.tile_start[j] = tiles;
+      tiles += a.tg[j].ntiles;
+    }
+    a.tile_start[n] = tiles;
+    a.n_targets = (int)n;
+    a.xq = xq;
+    a.xd = xd;
+    a.T = T;
+    a.Tpad = Tpad;
+    a.K = (int)K;
+    a.nb = (int)(K / kBlock);
+    a.fast = fast;
+    HIP_OR_FAIL(c, launch_gemm_a8(w0.dtype, 0, token_mode, a, tiles, c->stream));
+  }
+  return ELMH_OK;
+}
+
+int run_f32_group(elmh_ctx* c, const float* x, int T, int64_t K, const std::vector<int>& idx, elmh_weight* const* w,
+                  float* const* y, const float* const* res) {
+  for (size_t i0 = 0; i0 < idx.size(); i0 += kMaxTargets) {
+    F32Args a{};
+    const size_t n = std::min<size_t>(kMaxTargets, idx.size() - i0);
+    int groups = 0;
+    const DevWeight& w0 = w[idx[i0]]->w;
+    a.H = w0.H;
+    for (size_t j = 0; j < n; ++j) {
+      const DevWeight& wd = w[idx[i0 + j]]->w;
+      const int g = (int)((wd.rows + 255) / 256);
+      a.tg[j] = {wd.data, wd.scales, y[idx[i0 + j]], res ? res[idx[i0 + j]] : nullptr, (int)wd.rows, g};
+      a.tile_start[j] = groups;
+      groups += g;
+    }
+    a.tile_start[n] = groups;
+    a.n_targets = (int)n;
+    a.x = x;
+    a.T = T;
+    a.K = (int)K;
+    a.nb = (int)w0.nb;
+    HIP_OR_FAIL(c, launch_f32act(w0.dtype, 0, a, groups, c->stream));
+  }
+  return ELMH_OK;
+}
+
+int quant_frag(elmh_ctx* c, const float* x, int T, int64_t K, int token_mode, int* Tpad_out) {
+  const int Tpad = (int)round_up(T, kGemmTileT);
+  const int64_t nb = K / kBlock;
+  int rc;
+  if ((rc = ensure(c, c->xq, (size_t)Tpad * K))) return rc;
+  if ((rc = ensure(c, c->xd, (size_t)Tpad * nb * sizeof(float)))) return rc;
+  if (token_mode)
+    HIP_OR_FAIL(c, launch_act_quant_frag_token(x, T, Tpad, (int)K, (int8_t*)c->xq.p, (float*)c->xd.p, c->stream));
+  else
+    HIP_OR_FAIL(c, launch_act_quant_frag(x, T, Tpad, (int)K, (int8_t*)c->xq.p, (float*)c->xd.p, c->stream));
+  *Tpad_out = Tpad;
+  return ELMH_OK;
+}
+
+int quant_rows(elmh_ctx* c, const float* x, int T, int64_t K) {
+  const int64_t nb = K / kBlock;
+  int rc;
+  if ((rc = ensure(c, c->xq, (size_t)T * K))) return rc;
+  if ((rc = ensure(c, c->xd, (size_t)T * nb * sizeof(float)))) return rc;
+  if ((rc = ensure(c, c->xs, (size_t)T * nb * sizeof(int32_t)))) return rc;
+  HIP_OR_FAIL(c, launch_act_quant_rows(x, T, (int)K, (int8_t*)c->xq.p, (float*)c->xd.p, (int32_t*)c->xs.p, c->stream));
+  return ELMH_OK;
+}
+
+// Groups target indices by dtype (one kernel instantiation per dtype).
+std::vector<std::vector<int>> by_dtype(int n, elmh_weight* const* w) {
+  std::vector<int> q8, q4;
+  for (int i = 0; i < n; ++i) (w[i]->w.dtype == ELMH_Q8 ? q8 : q4).push_back(i);
+  std::vector<std::vector<int>> g;
+  if (!q8.empty()) g.push_back(q8);
+  if (!q4.empty()) g.push_back(q4);
+  return g;
+}
+
+int run_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight* const* w, float* const* y,
+               const float* const* res, int act, int mode) {
+  int rc = check_targets(c, T, K, n, w, y);
+  if (rc) return rc;
+  if (act < ELMH_ACT_F32 || act > ELMH_ACT_INT8_TOKEN) return fail(c, ELMH_ERR_ARG, "bad act mode %d", act);
+  bool a8 = act != ELMH_ACT_F32;
+  for (int i = 0; i < n; ++i) a8 = a8 && a8_applies(w[i]->w);
+  const auto groups = by_dtype(n, w);
+  if (!a8) {
+    for (const auto& g : groups)
+      if ((rc = run_f32_group(c, x, T, K, g, w, y, res))) return rc;
+    return ELMH_OK;
+  }
+  if (act == ELMH_ACT_INT8_TOKEN) {
+    int Tpad;
+    if ((rc = quant_frag(c, x, T, K, 1, &Tpad))) return rc;
+    for (const auto& g : groups)
+      if ((rc = run_gemm_group(c, (const int8_t*)c->xq.p, (const float*)c->xd.p, T, Tpad, K, g, w, y, res, 1,
+                               mode == ELMH_FAST)))
+        return rc;
+    return ELMH_OK;
+  }
+  int nt = 4;
+  for (int i = 0; i < n; ++i) nt = std::min(nt, gemv_tokens(w[i]->w, 1));
+  if (T <= nt) {
+    const bool qin = K <= 2048;  // small rows: each workgroup quantizes x itself (no extra launch)
+    if (!qin && (rc = quant_rows(c, x, T, K))) return rc;
+    for (const auto& g : groups)
+      if ((rc = run_gemv_group(c, qin ? x : nullptr, qin ? nullptr : (const int8_t*)c->xq.p,
+                               qin ? nullptr : (const float*)c->xd.p, qin ? nullptr : (const int32_t*)c->xs.p, T, K,
+                               g, w, y, res)))
+        return rc;
+    return ELMH_OK;
+  }
+  int Tpad;
+  if ((rc = quant_frag(c, x, T, K, 0, &Tpad))) return rc;
+  for (const auto& g : groups)
+    if ((rc = run_gemm_group(c, (const int8_t*)c->xq.p, (const float*)c->xd.p, T, Tpad, K, g, w, y, res, 0,
+                             mode == ELMH_FAST)))
+      return rc;
+  return ELMH_OK;
+}
+
+int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight* wg, const elmh_weight* wu, float* y,
+               int act, int mode) {
+  if (!wg || !wu || !y) return fail(c, ELMH_ERR_ARG, "swiglu: null weight or output");
+  if (T < 1 || wg->w.cols != K || wu->w.cols != K) return fail(c, ELMH_ERR_ARG, "swiglu: bad shape");
+  if (wg->w.rows != wu->w.rows) return fail(c, ELMH_ERR_ARG, "swiglu: gate and up row counts differ");
+  if (act < ELMH_ACT_F32 || act > ELMH_ACT_INT8_TOKEN) return fail(c, ELMH_ERR_ARG, "bad act mode %d", act);
+  const DevWeight &g = wg->w, &u = wu->w;
+  const bool a8 = act != ELMH_ACT_F32 && a8_applies(g) && a8_applies(u);
+  int rc;
+  if (g.dtype != u.dtype || g.H != u.H) {
+    // different layouts: two matmuls into scratch, then the silu * up epilogue
+    const size_t nel = (size_t)T * g.rows;
+    if ((rc = ensure(c, c->gu, 2 * nel * sizeof(float)))) return rc;
+    float* G = (float*)c->gu.p;
+    float* Uo = G + nel;
+    elmh_weight* ws[2] = {const_cast<elmh_weight*>(wg), const_cast<elmh_weight*>(wu)};
+    float* ys[2] = {G, Uo};
+    if ((rc = run_matmul(c, x, T, K, 2, ws, ys, nullptr, a8 ? act : ELMH_ACT_F32, mode))) return rc;
+    HIP_OR_FAIL(c, launch_silu_mul(G, Uo, y, (int64_t)nel, c->stream));
+    return ELMH_OK;
+  }
+  if (!a8) {
+    F32Args a{};
+    const int groups = (int)((g.rows + 255) / 256);
+    a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, groups};
+    a.tg[1] = {u.data, u.scales, y, nullptr, (int)u.rows, groups};
+    a.tile_start[0] = 0;
+    a.tile_start[1] = groups;
+    a.n_targets = 1;
+    a.H = g.H;
+    a.x = x;
+    a.T = T;
+    a.K = (int)K;
+    a.nb = (int)g.nb;
+    HIP_OR_FAIL(c, launch_f32act(g.dtype, 1, a, groups, c->stream));
+    return ELMH_OK;
+  }
+  const int nt = gemv_tokens(g, 2);
+  if (act == ELMH_ACT_INT8 && T <= nt) {
+    GemvArgs a{};
+    const bool qin = K <= 2048;
+    if (!qin && (rc = quant_rows(c, x, T, K))) return rc;
+    const int tiles = (int)(g.rows_pad / g.H);
+    a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, tiles};
+    a.tg[1] = {u.data, u.scales, y, nullptr, (int)u.rows, tiles};
+    a.n_targets = 2;
+    a.H = g.H;
+    a.x = qin ? x : nullptr;
+    a.xq = qin ? nullptr : (const int8_t*)c->xq.p;
+    a.xd = qin ? nullptr : (const float*)c->xd.p;
+    a.xs = qin ? nullptr : (const int32_t*)c->xs.p;
+    a.T = T;
+    a.K = (int)K;
+    a.nb = (int)(K / kBlock);
+    HIP_OR_FAIL(c, launch_gemv_a8(g.dtype, 1, a, tiles, c->stream));
+    return ELMH_OK;
+  }
+  const int token = act == ELMH_ACT_INT8_TOKEN;
+  int Tpad;
+  if ((rc = quant_frag(c, x, T, K, token, &Tpad))) return rc;
+  GemmArgs a{};
+  const int tiles = (int)(g.rows_pad / kGemmTileN);
+  a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, tiles};
+  a.tg[1] = {u.data, u.scales, y, nullptr, (int)u.rows, tiles};
+  a.n_targets = 2;
+  a.H = g.H;
+  a.xq = (const int8_t*)c->xq.p;
+  a.xd = (const float*)c->xd.p;
+  a.T = T;
+  a.Tpad = Tpad;
+  a.K = (int)K;
+  a.nb = (int)(K / kBlock);
+  a.fast = mode == ELMH_FAST;
+  HIP_OR_FAIL(c, launch_gemm_a8(g.dtype, 1, token, a, tiles, c->stream));
+  return ELMH_OK;
+}
+
+struct DeviceGuard {
+  explicit DeviceGuard(elmh_ctx* c) { (void)hipSetDevice(c->device); }
+};
+
+}  // namespace
+
+// ==================================================================== C ABI
+
+extern "C" {
+
+int elmh_device_count(int* count) {
+  if (!count) return fail(nullptr, ELMH_ERR_ARG, "null count");
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  *count = n;
+  return ELMH_OK;
+}
+
+int elmh_create(int device, elmh_ctx** out) {
+  if (!out) return fail(nullptr, ELMH_ERR_ARG, "null out");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(nullptr, ELMH_ERR_NODEV, "no HIP device");
+  if (device < 0 || device >= n) return fail(nullptr, ELMH_ERR_NODEV, "device %d out of range (%d devices)", device, n);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return fail(nullptr, ELMH_ERR_NODEV, "hipGetDeviceProperties failed");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(nullptr, ELMH_ERR_NODEV, "device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
+  auto* c = new elmh_ctx();
+  c->device = device;
+  c->arch = prop.gcnArchName;
+  if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return fail(nullptr, ELMH_ERR_HIP, "stream creation failed");
+  }
+  *out = c;
+  return ELMH_OK;
+}
+
+void elmh_destroy(elmh_ctx* c) {
+  if (!c) return;
+  DeviceGuard g(c);
+  (void)hipStreamSynchronize(c->stream);
+  for (DevBuf* b : {&c->x, &c->y, &c->res, &c->xq, &c->xd, &c->xs, &c->gu})
+    if (b->p) (void)hipFree(b->p);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+const char* elmh_last_error(const elmh_ctx* c) { return c ? c->err.c_str() : g_last_error.c_str(); }
+
+const char* elmh_device_arch(const elmh_ctx* c) { return c ? c->arch.c_str() : ""; }
+
+int elmh_upload_weight(elmh_ctx* c, int dtype, int64_t rows, int64_t cols, const void* data, const float* scales,
+                       elmh_weight** out) {
+  if (!c || !out) return fail(c, ELMH_ERR_ARG, "null ctx/out");
+  *out = nullptr;
+  if (dtype != ELMH_Q8 && dtype != ELMH_Q4)
+    return fail(c, ELMH_ERR_UNSUPPORTED, "dtype %d: only q8 (1) and q4 (2) weights are uploaded", dtype);
+  if (rows < 1 || cols < 1 || !data || !scales) return fail(c, ELMH_ERR_ARG, "bad weight %lldx%lld", (long long)rows, (long long)cols);
+  if (rows > (1ll << 30) || cols > (1ll << 24)) return fail(c, ELMH_ERR_UNSUPPORTED, "weight too large");
+  if (dtype == ELMH_Q4 && cols % kBlock) return fail(c, ELMH_ERR_ARG, "q4 needs K %% 32 == 0, got K=%lld", (long long)cols);
+  DeviceGuard guard(c);
+  DevWeight w;
+  w.dtype = dtype;
+  w.rows = rows;
+  w.cols = cols;
+  w.nb = (cols + kBlock - 1) / kBlock;
+  w.H = choose_H(dtype, cols);
+  w.rows_pad = round_up(rows, kPadRows);
+  const int G = dtype == ELMH_Q8 ? 32 : 16;
+  w.data_bytes = (size_t)(w.rows_pad * w.nb * G);
+  w.scale_bytes = (size_t)(dtype == ELMH_Q8 ? w.rows_pad : w.rows_pad * w.nb) * sizeof(float);
+  const size_t raw_bytes = (size_t)(dtype == ELMH_Q8 ? rows * cols : rows * (cols / 2));
+  const size_t raw_sbytes = (size_t)(dtype == ELMH_Q8 ? rows : rows * w.nb) * sizeof(float);
+  if (dtype == ELMH_Q4) {
+    // the kernels keep ws/16 (exact for every scale that is 0 or >= 2^-122 in magnitude)
+    const size_t ns = raw_sbytes / sizeof(float);
+    for (size_t i = 0; i < ns; ++i) {
+      const float s = std::fabs(scales[i]);
+      if (!(s == 0.f || (s >= 0x1p-122f && std::isfinite(s))))
+        return fail(c, ELMH_ERR_UNSUPPORTED, "q4 scale %g at %zu is non-finite or below 2^-122", (double)scales[i], i);
+    }
+  }
+  void *raw = nullptr, *raw_s = nullptr;
+  auto cleanup = [&]() {
+    if (raw) (void)hipFree(raw);
+    if (raw_s) (void)hipFree(raw_s);
+    if (w.data) (void)hipFree(w.data);
+    if (w.scales) (void)hipFree(w.scales);
+  };
+  if (hipMalloc((void**)&w.data, w.data_bytes) != hipSuccess || hipMalloc((void**)&w.scales, w.scale_bytes) != hipSuccess ||
+      hipMalloc(&raw, raw_bytes) != hipSuccess || hipMalloc(&raw_s, raw_sbytes) != hipSuccess) {
+    cleanup();
+    return fail(c, ELMH_ERR_OOM, "hipMalloc failed for a %lldx%lld weight", (long long)rows, (long long)cols);
+  }
+  hipError_t e = hipMemcpyAsync(raw, data, raw_bytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(raw_s, scales, raw_sbytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = launch_repack((const uint8_t*)raw, (const float*)raw_s, w, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  (void)hipFree(raw);
+  (void)hipFree(raw_s);
+  raw = raw_s = nullptr;
+  if (e != hipSuccess) {
+    cleanup();
+    return fail(c, ELMH_ERR_HIP, "weight upload: %s", hipGetErrorString(e));
+  }
+  *out = new elmh_weight{w};
+  return ELMH_OK;
+}
+
+int elmh_free_weight(elmh_ctx* c, elmh_weight* w) {
+  if (!w) return ELMH_OK;
+  if (c) {
+    DeviceGuard g(c);
+    (void)hipStreamSynchronize(c->stream);
+  }
+  if (w->w.data) (void)hipFree(w->w.data);
+  if (w->w.scales) (void)hipFree(w->w.scales);
+  delete w;
+  return ELMH_OK;
+}
+
+size_t elmh_weight_bytes(const elmh_weight* w) { return w ? w->w.data_bytes + w->w.scale_bytes : 0; }
+
+int elmh_reserve(elmh_ctx* c, int max_T, int64_t max_K) {
+  if (!c || max_T < 1 || max_K < 1) return fail(c, ELMH_ERR_ARG, "bad reserve");
+  DeviceGuard g(c);
+  const int64_t Tpad = round_up(max_T, kGemmTileT);
+  const int64_t nb = (max_K + kBlock - 1) / kBlock;
+  int rc;
+  if ((rc = ensure(c, c->xq, (size_t)(Tpad * max_K)))) return rc;
+  if ((rc = ensure(c, c->xd, (size_t)(Tpad * nb) * sizeof(float)))) return rc;
+  if ((rc = ensure(c, c->xs, (size_t)(Tpad * nb) * sizeof(int32_t)))) return rc;
+  return ELMH_OK;
+}
+
+int elmh_matmul_dev(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight* const* w, float* const* y,
+                    const float* const* res, int act, int mode) {
+  if (!c || !x) return fail(c, ELMH_ERR_ARG, "null ctx/x");
+  DeviceGuard g(c);
+  return run_matmul(c, x, T, K, n, w, y, res, act, mode);
+}
+
+int elmh_swiglu_dev(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight* wg, const elmh_weight* wu,
+                    float* y, int act, int mode) {
+  if (!c || !x) return fail(c, ELMH_ERR_ARG, "null ctx/x");
+  DeviceGuard g(c);
+  return run_swiglu(c, x, T, K, wg, wu, y, act, mode);
+}
+
+int elmh_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight* const* w, float* const* y,
+                const float* const* res, int act, int mode) {
+  if (!c || !x) return fail(c, ELMH_ERR_ARG, "null ctx/x");
+  int rc = check_targets(c, T, K, n, w, y);
+  if (rc) return rc;
+  DeviceGuard g(c);
+  size_t ytot = 0;
+  for (int i = 0; i < n; ++i) ytot += (size_t)T * w[i]->w.rows;
+  if ((rc = ensure(c, c->x, (size_t)T * K * sizeof(float)))) return rc;
+  if ((rc = ensure(c, c->y, ytot * sizeof(float)))) return rc;
+  bool any_res = false;
+  for (int i = 0; res && i < n; ++i) any_res = any_res || res[i];
+  if (any_res && (rc = ensure(c, c->res, ytot * sizeof(float)))) return rc;
+  HIP_OR_FAIL(c, hipMemcpyAsync(c->x.p, x, (size_t)T * K * sizeof(float), hipMemcpyHostToDevice, c->stream));
+  std::vector<float*> dy(n);
+  std::vector<const float*> dr(n, nullptr);
+  size_t off = 0;
+  for (int i = 0; i < n; ++i) {
+    const size_t cnt = (size_t)T * w[i]->w.rows;
+    dy[i] = (float*)c->y.p + off;
+    if (any_res && res[i]) {
+      dr[i] = (float*)c->res.p + off;
+      HIP_OR_FAIL(c, hipMemcpyAsync((void*)dr[i], res[i], cnt * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    }
+    off += cnt;
+  }
+  if ((rc = run_matmul(c, (const float*)c->x.p, T, K, n, w, dy.data(), any_res ? dr.data() : nullptr, act, mode)))
+    return rc;
+  for (int i = 0; i < n; ++i)
+    HIP_OR_FAIL(c, hipMemcpyAsync(y[i], dy[i], (size_t)T * w[i]->w.rows * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+  HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
+  return ELMH_OK;
+}
+
+int elmh_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight* wg, const elmh_weight* wu, float* y,
+                int act, int mode) {
+  if (!c || !x || !wg || !wu || !y) return fail(c, ELMH_ERR_ARG, "null argument");
+  if (T < 1) return fail(c, ELMH_ERR_ARG, "bad T");
+  DeviceGuard g(c);
+  int rc;
+  const size_t ny = (size_t)T * wg->w.rows;
+  if ((rc = ensure(c, c->x, (size_t)T * K * sizeof(float)))) return rc;
+  if ((rc = ensure(c, c->y, ny * sizeof(float)))) return rc;
+  HIP_OR_FAIL(c, hipMemcpyAsync(c->x.p, x, (size_t)T * K * sizeof(float), hipMemcpyHostToDevice, c->stream));
+  if ((rc = run_swiglu(c, (const float*)c->x.p, T, K, wg, wu, (float*)c->y.p, act, mode))) return rc;
+  HIP_OR_FAIL(c, hipMemcpyAsync(y, c->y.p, ny * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+  HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
+  return ELMH_OK;
+}
+
+int elmh_quantize_act_dev(elmh_ctx* c, const float* x, int T, int64_t K, int8_t* q, float* d, int32_t* s) {
+  if (!c || !x || !q || !d || !s || T < 1 || K < kBlock || K % kBlock) return fail(c, ELMH_ERR_ARG, "bad quantize_act args");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, launch_act_quant_rows(x, T, (int)K, q, d, s, c->stream));
+  return ELMH_OK;
+}
+
+int elmh_gemv_a8_dev(elmh_ctx* c, const int8_t* q, const float* d, const int32_t* s, int T, int64_t K, int n,
+                     elmh_weight* const* w, float* const* y, const float* const* res) {
+  if (!c || !q || !d || !s) return fail(c, ELMH_ERR_ARG, "null argument");
+  int rc = check_targets(c, T, K, n, w, y);
+  if (rc) return rc;
+  for (int i = 0; i < n; ++i)
+    if (!a8_applies(w[i]->w)) return fail(c, ELMH_ERR_ARG, "target %d: int8 GEMV needs K %% 32 == 0", i);
+  int nt = 4;
+  for (int i = 0; i < n; ++i) nt = std::min(nt, gemv_tokens(w[i]->w, 1));
+  if (T > nt) return fail(c, ELMH_ERR_UNSUPPORTED, "int8 GEMV takes at most %d tokens at K=%lld", nt, (long long)K);
+  DeviceGuard g(c);
+  for (const auto& grp : by_dtype(n, w))
+    if ((rc = run_gemv_group(c, nullptr, q, d, s, T, K, grp, w, y, res))) return rc;
+  return ELMH_OK;
+}
+
+int elmh_quantize_act(elmh_ctx* c, const float* x, int T, int64_t K, int8_t* q, float* d) {
+  if (!c || !x || !q || !d || T < 1 || K < kBlock || K % kBlock) return fail(c, ELMH_ERR_ARG, "bad quantize_act args");
+  DeviceGuard g(c);
+  int rc;
+  const int64_t nb = K / kBlock;
+  if ((rc = ensure(c, c->x, (size_t)T * K * sizeof(float)))) return rc;
+  HIP_OR_FAIL(c, hipMemcpyAsync(c->x.p, x, (size_t)T * K * sizeof(float), hipMemcpyHostToDevice, c->stream));
+  if ((rc = quant_rows(c, (const float*)c->x.p, T, K))) return rc;
+  HIP_OR_FAIL(c, hipMemcpyAsync(q, c->xq.p, (size_t)T * K, hipMemcpyDeviceToHost, c->stream));
+  HIP_OR_FAIL(c, hipMemcpyAsync(d, c->xd.p, (size_t)T * nb * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+  HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
+  return ELMH_OK;
+}
+
+int elmh_block_sums(elmh_ctx* c, const int8_t* xq, int T, const elmh_weight* w, int32_t* S) {
+  if (!c || !xq || !w || !S || T < 1) return fail(c, ELMH_ERR_ARG, "null argument");
+  if (!a8_applies(w->w)) return fail(c, ELMH_ERR_ARG, "block sums need K %% 32 == 0");
+  DeviceGuard g(c);
+  int rc;
+  const size_t nS = (size_t)T * w->w.rows * w->w.nb;
+  if ((rc = ensure(c, c->xq, (size_t)T * w->w.cols))) return rc;
+  if ((rc = ensure(c, c->y, nS * sizeof(int32_t)))) return rc;
+  HIP_OR_FAIL(c, hipMemcpyAsync(c->xq.p, xq, (size_t)T * w->w.cols, hipMemcpyHostToDevice, c->stream));
+  HIP_OR_FAIL(c, launch_block_sums(w->w, (const int8_t*)c->xq.p, T, (int32_t*)c->y.p, c->stream));
+  HIP_OR_FAIL(c, hipMemcpyAsync(S, c->y.p, nS * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+  HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
+  return ELMH_OK;
+}
+
+// ---- plumbing ----
+
+int elmh_malloc(elmh_ctx* c, size_t bytes, void** p) {
+  if (!c || !p) return fail(c, ELMH_ERR_ARG, "null argument");
+  DeviceGuard g(c);
+  if (hipMalloc(p, bytes ? bytes : 1) != hipSuccess) return fail(c, ELMH_ERR_OOM, "hipMalloc(%zu) failed", bytes);
+  return ELMH_OK;
+}
+
+int elmh_free(elmh_ctx* c, void* p) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
+  if (p) HIP_OR_FAIL(c, hipFree(p));
+  return ELMH_OK;
+}
+
+int elmh_memcpy_h2d(elmh_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+  HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
+  return ELMH_OK;
+}
+
+int elmh_memcpy_d2h(elmh_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+  HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
+  return ELMH_OK;
+}
+
+int elmh_memset_dev(elmh_ctx* c, void* dst, int value, size_t bytes) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, hipMemsetAsync(dst, value, bytes, c->stream));
+  return ELMH_OK;
+}
+
+int elmh_synchronize(elmh_ctx* c) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
+  return ELMH_OK;
+}
+
+void* elmh_stream(elmh_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+int elmh_event_create(elmh_ctx* c, void** ev) {
+  if (!c || !ev) return fail(c, ELMH_ERR_ARG, "null argument");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, hipEventCreate((hipEvent_t*)ev));
+  return ELMH_OK;
+}
+
+int elmh_event_destroy(elmh_ctx* c, void* ev) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  DeviceGuard g(c);
+  if (ev) HIP_OR_FAIL(c, hipEventDestroy((hipEvent_t)ev));
+  return ELMH_OK;
+}
+
+int elmh_event_record(elmh_ctx* c, void* ev) {
+  if (!c || !ev) return fail(c, ELMH_ERR_ARG, "null argument");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, hipEventRecord((hipEvent_t)ev, c->stream));
+  return ELMH_OK;
+}
+
+int elmh_event_elapsed(elmh_ctx* c, void* a, void* b, float* ms) {
+  if (!c || !a || !b || !ms) return fail(c, ELMH_ERR_ARG, "null argument");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, hipEventSynchronize((hipEvent_t)b));
+  HIP_OR_FAIL(c, hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+  return ELMH_OK;
+}
+
+int elmh_graph_begin(elmh_ctx* c) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  return ELMH_OK;
+}
+
+int elmh_graph_end(elmh_ctx* c, void** exec) {
+  if (!c || !exec) return fail(c, ELMH_ERR_ARG, "null argument");
+  DeviceGuard g(c);
+  hipGraph_t graph = nullptr;
+  HIP_OR_FAIL(c, hipStreamEndCapture(c->stream, &graph));
+  hipGraphExec_t ge = nullptr;
+  hipError_t e = hipGraphInstantiate(&ge, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (e != hipSuccess) return fail(c, ELMH_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+  *exec = ge;
+  return ELMH_OK;
+}
+
+int elmh_graph_launch(elmh_ctx* c, void* exec) {
+  if (!c || !exec) return fail(c, ELMH_ERR_ARG, "null argument");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, hipGraphLaunch((hipGraphExec_t)exec, c->stream));
+  return ELMH_OK;
+}
+
+int elmh_graph_destroy(elmh_ctx* c, void* exec) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  DeviceGuard g(c);
+  if (exec) HIP_OR_FAIL(c, hipGraphExecDestroy((hipGraphExec_t)exec));
+  return ELMH_OK;
+}
+
+}  // extern "C"

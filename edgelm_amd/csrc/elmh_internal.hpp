@@ -1,0 +1,111 @@
+// Internal structures shared by the HIP kernels (elmh_kernels.hip) and the C-ABI layer
+// (elmh_api.cpp). Not part of the public interface (include/elmh.h).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace elmh {
+
+constexpr int kBlock = 32;       // activation block / q4 group (edgelm kActBlock, kernels.hpp:38)
+constexpr int kMaxTargets = 4;   // weights per kernel launch (MATMUL_N with more is split)
+constexpr int kGemvThreads = 256;
+constexpr int kGemmTileN = 64;   // weight rows per GEMM workgroup
+constexpr int kGemmTileT = 64;   // tokens per GEMM workgroup
+constexpr int kPadRows = 64;     // rows_pad is a multiple of this
+
+enum WDType { WQ8 = 1, WQ4 = 2 };
+
+// Device-resident weight in the repacked layout.
+//   data:   [rows_pad/H][nb][H][G] bytes, G = 32 (q8: int8 row segment of one 32-block)
+//                                       G = 16 (q4: the group's 16 bytes exactly as exported)
+//   scales: q8 -> [rows_pad] f32 (per row)
+//           q4 -> [rows_pad/H][nb][H] f32 holding ws/16 (exact: power-of-two scaling)
+// A (row n, block b) item sits at index ((n/H)*nb + b)*H + n%H, so a run of H rows of one
+// block is contiguous and one H-row tile of all blocks is one contiguous chunk.
+struct DevWeight {
+  int dtype = 0;
+  int H = 32;
+  int64_t rows = 0, cols = 0, nb = 0, rows_pad = 0;
+  uint8_t* data = nullptr;
+  float* scales = nullptr;
+  size_t data_bytes = 0, scale_bytes = 0;
+};
+
+__host__ __device__ inline int64_t item_index(int64_t n, int64_t b, int64_t nb, int H) {
+  return ((n / H) * nb + b) * H + (n % H);
+}
+
+// ---------------------------------------------------------------- kernel argument blocks
+
+struct GemvTarget {
+  const uint8_t* data;
+  const float* scales;
+  float* y;          // [T][N]
+  const float* res;  // [T][N] or null
+  int N;
+  int tiles;         // rows_pad / H
+};
+
+struct GemvArgs {
+  GemvTarget tg[kMaxTargets];
+  int tile_start[kMaxTargets + 1];  // prefix sums of tiles (matmul); swiglu uses tg[0]/tg[1]
+  int n_targets;
+  int H;
+  const float* x;     // f32 [T][K] (quantized inside each workgroup) or null
+  const int8_t* xq;   // int8 [T][K] row-major (pre-quantized) when x is null
+  const float* xd;    // f32 [T][nb]
+  const int32_t* xs;  // int32 [T][nb] block sums of q
+  int T, K, nb;
+};
+
+struct GemmTarget {
+  const uint8_t* data;
+  const float* scales;
+  float* y;
+  const float* res;
+  int N;
+  int ntiles;  // rows_pad / kGemmTileN
+};
+
+struct GemmArgs {
+  GemmTarget tg[kMaxTargets];
+  int tile_start[kMaxTargets + 1];
+  int n_targets;
+  int H;
+  const int8_t* xq;  // MFMA B-fragment-major: [Tpad/32][nb][64 lanes][16 B]
+  const float* xd;   // [nb][Tpad] (block mode) or [Tpad] (token mode)
+  int T, Tpad, K, nb;
+  int fast;          // 0: exact sequential mul+add; 1: fused multiply-add
+};
+
+struct F32Args {
+  GemvTarget tg[kMaxTargets];
+  int tile_start[kMaxTargets + 1];  // in units of 256-row groups (gemv) / 64-row groups (gemm)
+  int n_targets;
+  int H;
+  const float* x;  // [T][K]
+  int T, K, nb;
+};
+
+// ---------------------------------------------------------------- launchers (elmh_kernels.hip)
+
+hipError_t launch_repack(const uint8_t* raw, const float* raw_scales, DevWeight& w, hipStream_t s);
+// Row-major activation quantization: xq [T][K], xd [T][nb], xs [T][nb].
+hipError_t launch_act_quant_rows(const float* x, int T, int K, int8_t* xq, float* xd, int32_t* xs, hipStream_t s);
+// Fragment-major activation quantization for the MFMA GEMM: xq [Tpad/32][nb][1024], xd [nb][Tpad]
+// (rows t >= T are written as zeros).
+hipError_t launch_act_quant_frag(const float* x, int T, int Tpad, int K, int8_t* xq, float* xd, hipStream_t s);
+// Per-token scale (extension): xq fragment-major as above, xd [Tpad].
+hipError_t launch_act_quant_frag_token(const float* x, int T, int Tpad, int K, int8_t* xq, float* xd, hipStream_t s);
+
+// Largest T the int8 GEMV path takes for this K (activation rows staged in LDS).
+int gemv_max_tokens(int K);
+size_t gemv_lds_bytes(int nt, int K, int nb, int H, int nsel);
+hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_tiles, hipStream_t s);
+hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs& a, int total_tiles, hipStream_t s);
+hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_groups, hipStream_t s);
+hipError_t launch_silu_mul(const float* g, const float* u, float* y, int64_t n, hipStream_t s);
+// Test hook: S[t][n][b] for pre-quantized row-major activations.
+hipError_t launch_block_sums(const DevWeight& w, const int8_t* xq, int T, int32_t* S, hipStream_t s);
+
+}  // namespace elmh

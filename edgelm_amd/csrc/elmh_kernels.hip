@@ -1,0 +1,802 @@
+// HIP kernels (gfx950) for edgelm's quantized-matmul family: MATMUL / MATMUL_N / MATMUL_ADD /
+// FFN_SWIGLU with q8 per-row or q4 group-32 weights and f32 or dynamic int8 activations.
+//
+// Numerics follow edgelm's cpu backend on its scalar path bit for bit:
+//  * int8 activations (kernels_ref.cpp:23-37): per row, per 32-block amax/127, IEEE divide,
+//    round half away from zero, clamp +-127;
+//  * int8 block sums S_b are exact int32 dot products (v_dot4 / MFMA), order-free;
+//  * the f32 fold over blocks is sequential in block order with separate multiply and add
+//    (kernels_cpu.cpp:159-167, 193-204; this file is compiled with -ffp-contract=off and every
+//    fused multiply-add below is explicit);
+//  * f32-activation paths keep the scalar path's four interleaved accumulators
+//    (kernels_cpu.cpp:32-43, 45-71) and per-group order (73-112);
+//  * silu uses an expf identical to the host libm's (elm_expf.h).
+#include "elm_expf.h"
+#include "elmh_internal.hpp"
+
+namespace elmh {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float silu_exact(float v) { return v / (1.0f + elm_expf(-v)); }
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// Quantizes one 32-element block held by 32 consecutive lanes (element = lane & 31). Every lane of
+// the group gets the block scale d and the block sum of q. Same arithmetic as quantize_act_row.
+__device__ __forceinline__ int quant32(float v, float& d, int& sum) {
+  float a = fabsf(v);
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
+  const float s = a / 127.0f;
+  const float safe = s == 0.f ? 1.f : s;
+  const float vv = v / safe;
+  const float r = copysignf(floorf(fabsf(vv) + 0.5f), vv);
+  const int q = (int)fminf(127.f, fmaxf(-127.f, r));
+  int sm = q;
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) sm += __shfl_xor(sm, off, 32);
+  d = s;
+  sum = sm;
+  return q;
+}
+
+// q4 group bytes -> MFMA int8 operand for half h: 16*q of elements h*16 .. h*16+15
+// (low nibbles for h = 0, high for h = 1). x ^ 8 maps the stored q+8 to q's 4-bit two's
+// complement; placed in the high nibble of a byte it reads as 16*q.
+__device__ __forceinline__ v4i q4_operand16(uint4 w, int h) {
+  const int sh = 4 - 4 * h;
+  v4i r;
+  r.x = (int)(((w.x << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+  r.y = (int)(((w.y << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+  r.z = (int)(((w.z << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+  r.w = (int)(((w.w << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+  return r;
+}
+
+// ---------------------------------------------------------------- weight repack
+
+__global__ void repack_kernel(const uint8_t* __restrict__ raw, const float* __restrict__ raw_scales,
+                              uint8_t* __restrict__ out, float* __restrict__ out_scales, int64_t rows, int64_t cols,
+                              int64_t nb, int64_t rows_pad, int H, int dtype) {
+  const int64_t items = rows_pad * nb;
+  const int G = dtype == WQ8 ? 32 : 16;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < items; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = i / nb, b = i - n * nb;
+    const int64_t dst = item_index(n, b, nb, H);
+    uint8_t* o = out + dst * G;
+    if (dtype == WQ8) {
+      for (int j = 0; j < 32; ++j) {
+        const int64_t k = b * 32 + j;
+        o[j] = (n < rows && k < cols) ? raw[n * cols + k] : 0;
+      }
+    } else {
+      for (int j = 0; j < 16; ++j) o[j] = n < rows ? raw[n * (cols / 2) + b * 16 + j] : 0x88;  // 0x88: q = 0
+      out_scales[dst] = n < rows ? raw_scales[n * nb + b] * 0.0625f : 0.f;
+    }
+  }
+  if (dtype == WQ8)
+    for (int64_t n = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; n < rows_pad; n += (int64_t)gridDim.x * blockDim.x)
+      out_scales[n] = n < rows ? raw_scales[n] : 0.f;
+}
+
+// ---------------------------------------------------------------- activation quantization
+
+// Row-major: 8 blocks per 256-thread workgroup (two per wave).
+__global__ __launch_bounds__(256) void act_quant_rows_kernel(const float* __restrict__ x, int T, int K,
+                                                             int8_t* __restrict__ xq, float* __restrict__ xd,
+                                                             int32_t* __restrict__ xs) {
+  const int nb = K / kBlock;
+  const int g = blockIdx.x * 8 + (threadIdx.x >> 5), l = threadIdx.x & 31;
+  const bool ok = g < T * nb;
+  const int t = ok ? g / nb : 0, b = ok ? g - t * nb : 0;
+  const float v = ok ? x[(int64_t)t * K + b * kBlock + l] : 0.f;
+  float d;
+  int sum;
+  const int q = quant32(v, d, sum);
+  if (!ok) return;
+  xq[(int64_t)t * K + b * kBlock + l] = (int8_t)q;
+  if (l == 0) {
+    xd[(int64_t)t * nb + b] = d;
+    xs[(int64_t)t * nb + b] = sum;
+  }
+}
+
+// Fragment-major for the MFMA GEMM: the 1 KB fragment of (32-token group, block b) holds for lane
+// L = h*32 + t%32 the 16 bytes of elements h*16 .. h*16+15 of token t's block b.
+__global__ __launch_bounds__(256) void act_quant_frag_kernel(const float* __restrict__ x, int T, int Tpad, int K,
+                                                             int8_t* __restrict__ xq, float* __restrict__ xd) {
+  const int nb = K / kBlock;
+  const int g = blockIdx.x * 8 + (threadIdx.x >> 5), l = threadIdx.x & 31;
+  if (g >= Tpad * nb) return;  // whole 32-lane groups leave together
+  const int t = g / nb, b = g - t * nb;
+  const float v = t < T ? x[(int64_t)t * K + b * kBlock + l] : 0.f;
+  float d;
+  int sum;
+  const int q = quant32(v, d, sum);
+  const int h = l >> 4, m = l & 15;
+  xq[(((int64_t)(t >> 5) * nb + b) * 64 + h * 32 + (t & 31)) * 16 + m] = (int8_t)q;
+  if (l == 0) xd[(int64_t)b * Tpad + t] = d;
+}
+
+// Per-token scale (extension): one workgroup per token row.
+__global__ __launch_bounds__(256) void act_quant_frag_token_kernel(const float* __restrict__ x, int T, int Tpad, int K,
+                                                                   int8_t* __restrict__ xq, float* __restrict__ xd) {
+  __shared__ float red[4];
+  const int t = blockIdx.x, nb = K / kBlock;
+  float a = 0.f;
+  if (t < T)
+    for (int k = threadIdx.x; k < K; k += 256) a = fmaxf(a, fabsf(x[(int64_t)t * K + k]));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
+  __syncthreads();
+  a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = a / 127.0f;
+  const float safe = s == 0.f ? 1.f : s;
+  for (int k = threadIdx.x; k < K; k += 256) {
+    int q = 0;
+    if (t < T) {
+      const float vv = x[(int64_t)t * K + k] / safe;
+      const float r = copysignf(floorf(fabsf(vv) + 0.5f), vv);
+      q = (int)fminf(127.f, fmaxf(-127.f, r));
+    }
+    const int b = k >> 5, e = k & 31, h = e >> 4, m = e & 15;
+    xq[(((int64_t)(t >> 5) * nb + b) * 64 + h * 32 + (t & 31)) * 16 + m] = (int8_t)q;
+  }
+  if (threadIdx.x == 0) xd[t] = s;
+}
+
+// ---------------------------------------------------------------- int8 GEMV (decode)
+//
+// One workgroup owns one H-row tile of a weight (both gate and up tiles for SwiGLU): a contiguous
+// chunk of the repacked layout. Phase 1: every (row, block) item's product
+//   q8: p = float(S_b) * xd_b        q4: p/16 = float(S_b) * ((ws_b/16) * xd_b)
+// goes to LDS (each multiply rounds exactly as on the CPU; /16 is exact). Phase 2: one lane per
+// (token, row) folds its products in block order with plain adds, then applies the epilogue.
+// Consecutive lanes take consecutive items, so every weight load instruction reads one
+// contiguous run of the chunk.
+
+template <int WDT, int NT, bool QIN, bool SW>
+__global__ __launch_bounds__(kGemvThreads) void gemv_a8_kernel(const GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int G = WDT == WQ8 ? 32 : 16;
+  constexpr int U = WDT == WQ8 ? 2 : 4;  // items in flight per thread
+  constexpr int NSEL = SW ? 2 : 1;
+  const int K = a.K, nb = a.nb, T = a.T, H = a.H;
+  const int tid = threadIdx.x;
+  const int kpad = (K + 15) & ~15;
+  const int pst = nb | 1;  // odd LDS row stride: the fold's lanes hit distinct banks
+  int8_t* s_q = reinterpret_cast<int8_t*>(smem);
+  float* s_d = reinterpret_cast<float*>(smem + NT * kpad);
+  int* s_s = reinterpret_cast<int*>(s_d + NT * nb);
+  float* s_p = reinterpret_cast<float*>(s_s + NT * nb);
+
+  int ti = 0, tile = blockIdx.x;
+  if (!SW) {
+    while (ti + 1 < a.n_targets && (int)blockIdx.x >= a.tile_start[ti + 1]) ++ti;
+    tile = blockIdx.x - a.tile_start[ti];
+  }
+
+  // phase 0: the activation rows into LDS
+  if (QIN) {
+    const int wave = tid >> 6, half = (tid >> 5) & 1, l = tid & 31;
+    for (int gp = wave; gp * 2 < T * nb; gp += kGemvThreads / 64) {
+      const int g = gp * 2 + half;
+      const bool ok = g < T * nb;
+      const int t = ok ? g / nb : 0, b = ok ? g - t * nb : 0;
+      const float v = ok ? a.x[(int64_t)t * K + b * kBlock + l] : 0.f;
+      float d;
+      int sum;
+      const int q = quant32(v, d, sum);
+      if (ok) {
+        s_q[t * kpad + b * kBlock + l] = (int8_t)q;
+        if (l == 0) {
+          s_d[t * nb + b] = d;
+          s_s[t * nb + b] = sum;
+        }
+      }
+    }
+  } else {
+    for (int t = 0; t < T; ++t) {
+      const int4* src = reinterpret_cast<const int4*>(a.xq + (int64_t)t * K);
+      int4* dst = reinterpret_cast<int4*>(s_q + t * kpad);
+      for (int i = tid; i < K / 16; i += kGemvThreads) dst[i] = src[i];
+      for (int i = tid; i < nb; i += kGemvThreads) {
+        s_d[t * nb + i] = a.xd[(int64_t)t * nb + i];
+        s_s[t * nb + i] = a.xs[(int64_t)t * nb + i];
+      }
+    }
+  }
+  __syncthreads();
+
+  // phase 1: products
+  const int per_sel = H * nb;
+  const int items = NSEL * per_sel;
+  for (int it0 = 0; it0 < items; it0 += kGemvThreads * U) {
+    v4u wv[U][G / 16];
+    float wsc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int it = it0 + u * kGemvThreads + tid;
+      wsc[u] = 0.f;
+      if (it < items) {
+        const int sel = SW ? (it >= per_sel) : 0;
+        const int j = it - sel * per_sel;
+        const GemvTarget& tg = a.tg[SW ? sel : ti];
+        const int64_t gi = (int64_t)tile * per_sel + j;
+        const v4u* src = reinterpret_cast<const v4u*>(tg.data + gi * G);
+        wv[u][0] = __builtin_nontemporal_load(src);
+        if (G == 32) wv[u][G / 16 - 1] = __builtin_nontemporal_load(src + 1);
+        if (WDT == WQ4) wsc[u] = __builtin_nontemporal_load(tg.scales + gi);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int it = it0 + u * kGemvThreads + tid;
+      if (it >= items) continue;
+      const int sel = SW ? (it >= per_sel) : 0;
+      const int j = it - sel * per_sel;
+      const int b = j / H, r = j - b * H;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if (t >= T) break;
+        const int4* aq = reinterpret_cast<const int4*>(s_q + t * kpad + b * kBlock);
+        const int4 a0 = aq[0], a1 = aq[1];
+        float p;
+        if (WDT == WQ8) {
+          const v4u w0 = wv[u][0], w1 = wv[u][G / 16 - 1];
+          int S = sdot4((int)w0.x, a0.x, 0);
+          S = sdot4((int)w0.y, a0.y, S);
+          S = sdot4((int)w0.z, a0.z, S);
+          S = sdot4((int)w0.w, a0.w, S);
+          S = sdot4((int)w1.x, a1.x, S);
+          S = sdot4((int)w1.y, a1.y, S);
+          S = sdot4((int)w1.z, a1.z, S);
+          S = sdot4((int)w1.w, a1.w, S);
+          p = (float)S * s_d[t * nb + b];
+        } else {
+          const v4u w = wv[u][0];
+          // sum_i (nib_i - 8) x_i = sum_i nib_i x_i - 8 * sum_i x_i (nibbles 0..15 are valid int8)
+          int S = -8 * s_s[t * nb + b];
+          S = sdot4((int)(w.x & 0x0F0F0F0Fu), a0.x, S);
+          S = sdot4((int)(w.y & 0x0F0F0F0Fu), a0.y, S);
+          S = sdot4((int)(w.z & 0x0F0F0F0Fu), a0.z, S);
+          S = sdot4((int)(w.w & 0x0F0F0F0Fu), a0.w, S);
+          S = sdot4((int)((w.x >> 4) & 0x0F0F0F0Fu), a1.x, S);
+          S = sdot4((int)((w.y >> 4) & 0x0F0F0F0Fu), a1.y, S);
+          S = sdot4((int)((w.z >> 4) & 0x0F0F0F0Fu), a1.z, S);
+          S = sdot4((int)((w.w >> 4) & 0x0F0F0F0Fu), a1.w, S);
+          p = (float)S * (wsc[u] * s_d[t * nb + b]);
+        }
+        s_p[((sel * NT + t) * H + r) * pst + b] = p;
+      }
+    }
+  }
+  __syncthreads();
+
+  // phase 2: sequential fold per (token, row) and epilogue
+  for (int f = tid; f < T * H; f += kGemvThreads) {
+    const int t = f / H, r = f - t * H;
+    const GemvTarget& tg = a.tg[SW ? 0 : ti];
+    const int n = tile * H + r;
+    if (n >= tg.N) continue;
+    const float* pp = s_p + (t * H + r) * pst;
+    float acc = 0.f;
+#pragma unroll 8
+    for (int b = 0; b < nb; ++b) acc = acc + pp[b];
+    float out = WDT == WQ8 ? acc * tg.scales[n] : acc * 16.0f;
+    if (SW) {
+      const float* pu = s_p + ((NT + t) * H + r) * pst;
+      float accu = 0.f;
+#pragma unroll 8
+      for (int b = 0; b < nb; ++b) accu = accu + pu[b];
+      const float up = WDT == WQ8 ? accu * a.tg[1].scales[n] : accu * 16.0f;
+      out = silu_exact(out) * up;
+    } else if (tg.res) {
+      out = out + tg.res[(int64_t)t * tg.N + n];
+    }
+    tg.y[(int64_t)t * tg.N + n] = out;
+  }
+}
+
+// ---------------------------------------------------------------- int8 MFMA GEMM (prefill)
+//
+// Workgroup = 4 waves computing a 64-row x 64-token output tile; each wave one 32x32 MFMA tile
+// (A = weight rows, B = tokens, so a lane owns one token and 16 rows of the accumulator).
+// v_mfma_i32_32x32x32_i8 covers exactly one 32-block along K, so the block's int32 sums come out
+// whole and the per-block f32 rescale runs on them in block order.
+
+template <int WDT>
+__device__ __forceinline__ v4i load_a_frag(const uint8_t* __restrict__ data, int64_t item, int h) {
+  if (WDT == WQ8) {
+    const uint4 w = *reinterpret_cast<const uint4*>(data + item * 32 + h * 16);
+    v4i r;
+    r.x = (int)w.x;
+    r.y = (int)w.y;
+    r.z = (int)w.z;
+    r.w = (int)w.w;
+    return r;
+  } else {
+    return q4_operand16(*reinterpret_cast<const uint4*>(data + item * 16), h);
+  }
+}
+
+template <int WDT, bool SW, bool TOK>
+__global__ __launch_bounds__(256) void gemm_a8_kernel(const GemmArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave & 1, wt = wave >> 1;
+  int ti = 0, ntile = blockIdx.x;
+  if (!SW) {
+    while (ti + 1 < a.n_targets && (int)blockIdx.x >= a.tile_start[ti + 1]) ++ti;
+    ntile = blockIdx.x - a.tile_start[ti];
+  }
+  const GemmTarget& tg = a.tg[SW ? 0 : ti];
+  const int nb = a.nb, H = a.H;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int n0 = ntile * kGemmTileN + wn * 32;
+  const int t0 = blockIdx.y * kGemmTileT + wt * 32;
+  const int n = n0 + l32;  // the A row this lane supplies
+  const int64_t nbase = (int64_t)(n / H) * nb * H + (n % H);
+  const int8_t* bsrc = a.xq + ((int64_t)(t0 >> 5) * nb * 64 + lane) * 16;
+  const int tcol = t0 + l32;  // the token this lane's accumulators belong to
+  // rows of accumulator i: n0 + 8*(i/4) + 4*h + i%4
+  int64_t sbase[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int nr = n0 + 8 * j + 4 * h;
+    sbase[j] = (int64_t)(nr / H) * nb * H + (nr % H);
+  }
+
+  float acc[16], accu[16];
+  v16i iacc, iaccu;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    acc[i] = 0.f;
+    accu[i] = 0.f;
+    iacc[i] = 0;
+    iaccu[i] = 0;
+  }
+  const v16i zero = iacc;
+
+  v4i A = load_a_frag<WDT>(tg.data, nbase, h);
+  v4i Au = SW ? load_a_frag<WDT>(a.tg[1].data, nbase, h) : A;
+  v4i B = *reinterpret_cast<const v4i*>(bsrc);
+  for (int b = 0; b < nb; ++b) {
+    // prefetch the next block's fragments
+    v4i An = A, Aun = Au, Bn = B;
+    if (b + 1 < nb) {
+      An = load_a_frag<WDT>(tg.data, nbase + (int64_t)(b + 1) * H, h);
+      if (SW) Aun = load_a_frag<WDT>(a.tg[1].data, nbase + (int64_t)(b + 1) * H, h);
+      Bn = *reinterpret_cast<const v4i*>(bsrc + (int64_t)(b + 1) * 1024);
+    }
+    if (TOK && WDT == WQ8) {
+      iacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, iacc, 0, 0, 0);
+      if (SW) iaccu = __builtin_amdgcn_mfma_i32_32x32x32_i8(Au, B, iaccu, 0, 0, 0);
+    } else {
+      const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, zero, 0, 0, 0);
+      v16i Su = zero;
+      if (SW) Su = __builtin_amdgcn_mfma_i32_32x32x32_i8(Au, B, zero, 0, 0, 0);
+      if (WDT == WQ8) {  // block mode: p = float(S) * xd[t,b]
+        const float xdv = a.xd[(int64_t)b * a.Tpad + tcol];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (a.fast) {
+            acc[i] = __builtin_fmaf((float)S[i], xdv, acc[i]);
+            if (SW) accu[i] = __builtin_fmaf((float)Su[i], xdv, accu[i]);
+          } else {
+            acc[i] = acc[i] + (float)S[i] * xdv;
+            if (SW) accu[i] = accu[i] + (float)Su[i] * xdv;
+          }
+        }
+      } else {  // q4: S holds 16*S_b; scales hold ws/16
+        const float xdv = TOK ? 1.0f : a.xd[(int64_t)b * a.Tpad + tcol];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float4 ws = *reinterpret_cast<const float4*>(tg.scales + sbase[j] + (int64_t)b * H);
+          float4 wu = ws;
+          if (SW) wu = *reinterpret_cast<const float4*>(a.tg[1].scales + sbase[j] + (int64_t)b * H);
+          const float wsv[4] = {ws.x, ws.y, ws.z, ws.w};
+          const float wuv[4] = {wu.x, wu.y, wu.z, wu.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = j * 4 + e;
+            const float c = TOK ? wsv[e] : wsv[e] * xdv;
+            if (a.fast) {
+              acc[i] = __builtin_fmaf((float)S[i], c, acc[i]);
+            } else {
+              acc[i] = acc[i] + (float)S[i] * c;
+            }
+            if (SW) {
+              const float cu = TOK ? wuv[e] : wuv[e] * xdv;
+              if (a.fast) {
+                accu[i] = __builtin_fmaf((float)Su[i], cu, accu[i]);
+              } else {
+                accu[i] = accu[i] + (float)Su[i] * cu;
+              }
+            }
+          }
+        }
+      }
+    }
+    A = An;
+    Au = Aun;
+    B = Bn;
+  }
+
+  if (tcol >= a.T) return;
+  const float xdt = TOK ? a.xd[tcol] : 1.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = j * 4 + e;
+      const int nr = n0 + 8 * j + 4 * h + e;
+      if (nr >= tg.N) continue;
+      float out;
+      if (WDT == WQ8) {
+        out = TOK ? ((float)iacc[i] * xdt) * tg.scales[nr] : acc[i] * tg.scales[nr];
+      } else {
+        out = TOK ? acc[i] * xdt : acc[i];
+      }
+      if (SW) {
+        float up;
+        if (WDT == WQ8) {
+          up = TOK ? ((float)iaccu[i] * xdt) * a.tg[1].scales[nr] : accu[i] * a.tg[1].scales[nr];
+        } else {
+          up = TOK ? accu[i] * xdt : accu[i];
+        }
+        out = silu_exact(out) * up;
+      } else if (tg.res) {
+        out = out + tg.res[(int64_t)tcol * tg.N + nr];
+      }
+      tg.y[(int64_t)tcol * tg.N + nr] = out;
+    }
+}
+
+// ---------------------------------------------------------------- f32-activation paths
+
+// T == 1 (kernels_cpu.cpp:366-368, 397-399 with dot_row): one lane per weight row.
+//   q8: ((s0 + s1) + (s2 + s3)) * ws, chains over i mod 4, tail into s0 (dot_q8)
+//   q4: s += (g0 + g1) * ws_g per group, g0/g1 sequential over 16 elements (dot_q4)
+template <int WDT>
+__device__ __forceinline__ float dot_row_f32(const uint8_t* __restrict__ data, const float* __restrict__ scales,
+                                             int n, int H, int nb, int K, const float* __restrict__ sx) {
+  const int64_t nbase = (int64_t)(n / H) * nb * H + (n % H);
+  if (WDT == WQ8) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    int i = 0;
+    for (; i + 4 <= K; i += 4) {
+      const int b = i >> 5;
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(data + (nbase + (int64_t)b * H) * 32 + (i & 31));
+      const float4 xv = *reinterpret_cast<const float4*>(sx + i);
+      s0 = s0 + xv.x * (float)(int8_t)(w & 0xFF);
+      s1 = s1 + xv.y * (float)(int8_t)((w >> 8) & 0xFF);
+      s2 = s2 + xv.z * (float)(int8_t)((w >> 16) & 0xFF);
+      s3 = s3 + xv.w * (float)(int8_t)(w >> 24);
+    }
+    for (; i < K; ++i) {
+      const int b = i >> 5;
+      const int8_t w = *reinterpret_cast<const int8_t*>(data + (nbase + (int64_t)b * H) * 32 + (i & 31));
+      s0 = s0 + sx[i] * (float)w;
+    }
+    return ((s0 + s1) + (s2 + s3)) * scales[n];
+  } else {
+    float s = 0.f;
+    for (int g = 0; g < nb; ++g) {
+      const int64_t item = nbase + (int64_t)g * H;
+      const uint4 wq = *reinterpret_cast<const uint4*>(data + item * 16);
+      const uint32_t wd[4] = {wq.x, wq.y, wq.z, wq.w};
+      float g0 = 0.f, g1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t byte = (wd[i >> 2] >> (8 * (i & 3))) & 0xFF;
+        g0 = g0 + sx[g * 32 + i] * (float)((int)(byte & 0x0F) - 8);
+        g1 = g1 + sx[g * 32 + 16 + i] * (float)((int)(byte >> 4) - 8);
+      }
+      s = s + (g0 + g1) * (scales[item] * 16.0f);
+    }
+    return s;
+  }
+}
+
+template <int WDT, bool SW>
+__global__ __launch_bounds__(256) void gemv_f32act_kernel(const F32Args a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* sx = reinterpret_cast<float*>(smem);
+  const int K = a.K;
+  for (int i = threadIdx.x; i < K; i += 256) sx[i] = a.x[i];
+  __syncthreads();
+  int ti = 0, grp = blockIdx.x;
+  if (!SW) {
+    while (ti + 1 < a.n_targets && (int)blockIdx.x >= a.tile_start[ti + 1]) ++ti;
+    grp = blockIdx.x - a.tile_start[ti];
+  }
+  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  const int n = grp * 256 + threadIdx.x;
+  if (n >= tg.N) return;
+  float out = dot_row_f32<WDT>(tg.data, tg.scales, n, a.H, a.nb, K, sx);
+  if (SW) {
+    const float up = dot_row_f32<WDT>(a.tg[1].data, a.tg[1].scales, n, a.H, a.nb, K, sx);
+    out = silu_exact(out) * up;
+  } else {
+    out = (tg.res ? tg.res[n] : 0.f) + out;
+  }
+  tg.y[n] = out;
+}
+
+// T > 1 (kernels_cpu.cpp:369-371, 401-403): the weight tile is dequantized (float(q) * s, one
+// rounding) and dotted in four interleaved chains (dot_f32_scalar); y = (res or 0) + dot.
+// One lane per weight row, four tokens per lane; x staged through LDS in chunks.
+constexpr int kF32TT = 4;
+constexpr int kF32Chunk = 1024;
+
+template <int WDT>
+__device__ __forceinline__ float4 deq4(const uint8_t* __restrict__ data, const float* __restrict__ scales,
+                                       int64_t nbase, int H, int i, int n) {
+  const int b = i >> 5;
+  const int64_t item = nbase + (int64_t)b * H;
+  float4 r;
+  if (WDT == WQ8) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(data + item * 32 + (i & 31));
+    const float s = scales[n];
+    r.x = (float)(int8_t)(w & 0xFF) * s;
+    r.y = (float)(int8_t)((w >> 8) & 0xFF) * s;
+    r.z = (float)(int8_t)((w >> 16) & 0xFF) * s;
+    r.w = (float)(int8_t)(w >> 24) * s;
+  } else {
+    const int e = i & 31;  // 4 consecutive elements of one half of the group
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(data + item * 16 + (e & 15));
+    const int sh = e >= 16 ? 4 : 0;
+    const float s = scales[item] * 16.0f;
+    r.x = (float)((int)((w >> sh) & 0x0F) - 8) * s;
+    r.y = (float)((int)((w >> (8 + sh)) & 0x0F) - 8) * s;
+    r.z = (float)((int)((w >> (16 + sh)) & 0x0F) - 8) * s;
+    r.w = (float)((int)((w >> (24 + sh)) & 0x0F) - 8) * s;
+  }
+  return r;
+}
+
+template <int WDT>
+__device__ __forceinline__ float deq1(const uint8_t* __restrict__ data, const float* __restrict__ scales,
+                                      int64_t nbase, int H, int i, int n) {
+  const int b = i >> 5;
+  const int64_t item = nbase + (int64_t)b * H;
+  if (WDT == WQ8) return (float)*reinterpret_cast<const int8_t*>(data + item * 32 + (i & 31)) * scales[n];
+  const int e = i & 31;
+  const uint8_t byte = data[item * 16 + (e & 15)];
+  return (float)((int)(e >= 16 ? byte >> 4 : byte & 0x0F) - 8) * (scales[item] * 16.0f);
+}
+
+template <int WDT, bool SW>
+__global__ __launch_bounds__(256) void gemm_f32act_kernel(const F32Args a) {
+  __shared__ __align__(16) float sx[kF32TT][kF32Chunk];
+  int ti = 0, grp = blockIdx.x;
+  if (!SW) {
+    while (ti + 1 < a.n_targets && (int)blockIdx.x >= a.tile_start[ti + 1]) ++ti;
+    grp = blockIdx.x - a.tile_start[ti];
+  }
+  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  const int K = a.K, H = a.H, nb = a.nb, T = a.T;
+  const int t0 = blockIdx.y * kF32TT;
+  const int n = grp * 256 + threadIdx.x;
+  const bool live = n < tg.N;
+  const int nn = live ? n : 0;
+  const int64_t nbase = (int64_t)(nn / H) * nb * H + (nn % H);
+  float s[kF32TT][4], su[kF32TT][4];
+#pragma unroll
+  for (int t = 0; t < kF32TT; ++t)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      s[t][c] = 0.f;
+      su[t][c] = 0.f;
+    }
+  const int kmain = K & ~3;
+  for (int k0 = 0; k0 < K; k0 += kF32Chunk) {
+    const int klen = min(kF32Chunk, K - k0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < kF32TT * kF32Chunk; i += 256) {
+      const int t = i / kF32Chunk, k = i - t * kF32Chunk;
+      sx[t][k] = (t0 + t < T && k < klen) ? a.x[(int64_t)(t0 + t) * K + k0 + k] : 0.f;
+    }
+    __syncthreads();
+    if (!live) continue;
+    const int kend = min(k0 + klen, kmain);
+    for (int i = k0; i < kend; i += 4) {
+      const float4 w = deq4<WDT>(tg.data, tg.scales, nbase, H, i, nn);
+      float4 wu = w;
+      if (SW) wu = deq4<WDT>(a.tg[1].data, a.tg[1].scales, nbase, H, i, nn);
+#pragma unroll
+      for (int t = 0; t < kF32TT; ++t) {
+        const float4 xv = *reinterpret_cast<const float4*>(&sx[t][i - k0]);
+        s[t][0] = s[t][0] + xv.x * w.x;
+        s[t][1] = s[t][1] + xv.y * w.y;
+        s[t][2] = s[t][2] + xv.z * w.z;
+        s[t][3] = s[t][3] + xv.w * w.w;
+        if (SW) {
+          su[t][0] = su[t][0] + xv.x * wu.x;
+          su[t][1] = su[t][1] + xv.y * wu.y;
+          su[t][2] = su[t][2] + xv.z * wu.z;
+          su[t][3] = su[t][3] + xv.w * wu.w;
+        }
+      }
+    }
+    for (int i = max(k0, kmain); i < k0 + klen; ++i) {  // tail (K % 4) into the first chain
+      const float w = deq1<WDT>(tg.data, tg.scales, nbase, H, i, nn);
+      const float wu = SW ? deq1<WDT>(a.tg[1].data, a.tg[1].scales, nbase, H, i, nn) : w;
+#pragma unroll
+      for (int t = 0; t < kF32TT; ++t) {
+        s[t][0] = s[t][0] + sx[t][i - k0] * w;
+        if (SW) su[t][0] = su[t][0] + sx[t][i - k0] * wu;
+      }
+    }
+  }
+  if (!live) return;
+#pragma unroll
+  for (int t = 0; t < kF32TT; ++t) {
+    const int tt = t0 + t;
+    if (tt >= T) break;
+    const float dot = (s[t][0] + s[t][1]) + (s[t][2] + s[t][3]);
+    float out;
+    if (SW) {
+      const float g = 0.f + dot;
+      const float u = 0.f + ((su[t][0] + su[t][1]) + (su[t][2] + su[t][3]));
+      out = silu_exact(g) * u;
+    } else {
+      out = (tg.res ? tg.res[(int64_t)tt * tg.N + n] : 0.f) + dot;
+    }
+    tg.y[(int64_t)tt * tg.N + n] = out;
+  }
+}
+
+__global__ void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y,
+                                int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    y[i] = silu_exact(g[i]) * u[i];
+}
+
+// Test hook: S[t][n][b] (exact int32 block sums) from row-major int8 activations.
+__global__ void block_sums_kernel(const uint8_t* __restrict__ data, int dtype, int64_t N, int nb, int H,
+                                  const int8_t* __restrict__ xq, int T, int32_t* __restrict__ S) {
+  const int64_t total = (int64_t)T * N * nb;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = i % nb, n = (i / nb) % N, t = i / (nb * N);
+    const int64_t item = item_index(n, b, nb, H);
+    const int8_t* xb = xq + t * (int64_t)nb * 32 + b * 32;
+    int s = 0;
+    if (dtype == WQ8) {
+      const int8_t* w = reinterpret_cast<const int8_t*>(data + item * 32);
+      for (int e = 0; e < 32; ++e) s += (int)w[e] * (int)xb[e];
+    } else {
+      const uint8_t* w = data + item * 16;
+      for (int e = 0; e < 16; ++e) s += ((int)(w[e] & 0x0F) - 8) * (int)xb[e] + ((int)(w[e] >> 4) - 8) * (int)xb[e + 16];
+    }
+    S[i] = s;
+  }
+}
+
+inline int grid_for(int64_t n, int threads, int cap = 65536) {
+  const int64_t g = (n + threads - 1) / threads;
+  return (int)(g < 1 ? 1 : (g > cap ? cap : g));
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- launchers
+
+hipError_t launch_repack(const uint8_t* raw, const float* raw_scales, DevWeight& w, hipStream_t s) {
+  const int64_t items = w.rows_pad * w.nb;
+  repack_kernel<<<grid_for(items, 256), 256, 0, s>>>(raw, raw_scales, w.data, w.scales, w.rows, w.cols, w.nb,
+                                                      w.rows_pad, w.H, w.dtype);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_rows(const float* x, int T, int K, int8_t* xq, float* xd, int32_t* xs, hipStream_t s) {
+  const int blocks = T * (K / kBlock);
+  act_quant_rows_kernel<<<(blocks + 7) / 8, 256, 0, s>>>(x, T, K, xq, xd, xs);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_frag(const float* x, int T, int Tpad, int K, int8_t* xq, float* xd, hipStream_t s) {
+  const int blocks = Tpad * (K / kBlock);
+  act_quant_frag_kernel<<<(blocks + 7) / 8, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_frag_token(const float* x, int T, int Tpad, int K, int8_t* xq, float* xd, hipStream_t s) {
+  act_quant_frag_token_kernel<<<Tpad, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
+  return hipGetLastError();
+}
+
+int gemv_max_tokens(int K) {
+  if (K <= 4096) return 4;
+  if (K <= 8192) return 2;
+  return 1;
+}
+
+size_t gemv_lds_bytes(int nt, int K, int nb, int H, int nsel) {
+  const size_t kpad = (size_t)((K + 15) & ~15);
+  return nt * kpad + (size_t)nt * nb * 8 + (size_t)nsel * nt * H * (nb | 1) * 4;
+}
+
+template <int WDT, int NT, bool QIN, bool SW>
+static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
+  const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.H, SW ? 2 : 1);
+  if (lds > 64 * 1024) return hipErrorInvalidValue;
+  gemv_a8_kernel<WDT, NT, QIN, SW><<<tiles, kGemvThreads, lds, s>>>(a);
+  return hipGetLastError();
+}
+
+template <int WDT, int NT, bool SW>
+static hipError_t gemv_q(const GemvArgs& a, int tiles, hipStream_t s) {
+  return a.x ? gemv_go<WDT, NT, true, SW>(a, tiles, s) : gemv_go<WDT, NT, false, SW>(a, tiles, s);
+}
+
+template <int WDT, bool SW>
+static hipError_t gemv_nt(const GemvArgs& a, int tiles, hipStream_t s) {
+  if (a.T <= 1) return gemv_q<WDT, 1, SW>(a, tiles, s);
+  if (a.T <= 2) return gemv_q<WDT, 2, SW>(a, tiles, s);
+  return gemv_q<WDT, 4, SW>(a, tiles, s);
+}
+
+hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_tiles, hipStream_t s) {
+  if (a.T > 4) return hipErrorInvalidValue;
+  if (dtype == WQ8) return swiglu ? gemv_nt<WQ8, true>(a, total_tiles, s) : gemv_nt<WQ8, false>(a, total_tiles, s);
+  return swiglu ? gemv_nt<WQ4, true>(a, total_tiles, s) : gemv_nt<WQ4, false>(a, total_tiles, s);
+}
+
+template <int WDT, bool SW, bool TOK>
+static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
+  dim3 grid(tiles, a.Tpad / kGemmTileT);
+  gemm_a8_kernel<WDT, SW, TOK><<<grid, 256, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs& a, int total_tiles, hipStream_t s) {
+  if (dtype == WQ8) {
+    if (token_mode) return swiglu ? gemm_go<WQ8, true, true>(a, total_tiles, s) : gemm_go<WQ8, false, true>(a, total_tiles, s);
+    return swiglu ? gemm_go<WQ8, true, false>(a, total_tiles, s) : gemm_go<WQ8, false, false>(a, total_tiles, s);
+  }
+  if (token_mode) return swiglu ? gemm_go<WQ4, true, true>(a, total_tiles, s) : gemm_go<WQ4, false, true>(a, total_tiles, s);
+  return swiglu ? gemm_go<WQ4, true, false>(a, total_tiles, s) : gemm_go<WQ4, false, false>(a, total_tiles, s);
+}
+
+hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_groups, hipStream_t s) {
+  if (a.T == 1) {
+    const size_t lds = (size_t)((a.K + 3) & ~3) * 4;
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    if (dtype == WQ8) {
+      if (swiglu) gemv_f32act_kernel<WQ8, true><<<total_groups, 256, lds, s>>>(a);
+      else gemv_f32act_kernel<WQ8, false><<<total_groups, 256, lds, s>>>(a);
+    } else {
+      if (swiglu) gemv_f32act_kernel<WQ4, true><<<total_groups, 256, lds, s>>>(a);
+      else gemv_f32act_kernel<WQ4, false><<<total_groups, 256, lds, s>>>(a);
+    }
+  } else {
+    dim3 grid(total_groups, (a.T + kF32TT - 1) / kF32TT);
+    if (dtype == WQ8) {
+      if (swiglu) gemm_f32act_kernel<WQ8, true><<<grid, 256, 0, s>>>(a);
+      else gemm_f32act_kernel<WQ8, false><<<grid, 256, 0, s>>>(a);
+    } else {
+      if (swiglu) gemm_f32act_kernel<WQ4, true><<<grid, 256, 0, s>>>(a);
+      else gemm_f32act_kernel<WQ4, false><<<grid, 256, 0, s>>>(a);
+    }
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const float* g, const float* u, float* y, int64_t n, hipStream_t s) {
+  silu_mul_kernel<<<grid_for(n, 256), 256, 0, s>>>(g, u, y, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_block_sums(const DevWeight& w, const int8_t* xq, int T, int32_t* S, hipStream_t s) {
+  block_sums_kernel<<<grid_for((int64_t)T * w.rows * w.nb, 256), 256, 0, s>>>(w.data, w.dtype, w.rows, (int)w.nb, w.H,
+                                                                              xq, T, S);
+  return hipGetLastError();
+}
+
+}  // namespace elmh

@@ -1,0 +1,140 @@
+/*
+ * elmh — C ABI of the MI355X quantized-matmul delegate for edgelm.
+ *
+ * This is the boundary a HIP backend inside edgelm binds: edgelm's Backend::supports/run
+ * (include/edgelm/backend.hpp:30-36) for MATMUL, MATMUL_N, MATMUL_ADD and FFN_SWIGLU reach
+ * the GPU only through these calls (edgelm_amd/host/hip_backend.cpp is that backend).
+ * Plain C types only; every call returns an elmh_status and never throws; the message of
+ * the last failure is available from elmh_last_error().
+ *
+ * Numerics (edgelm reference, adarsh-sgh/edgelm):
+ *  - weights: q8 = int8 [N,K] + f32 scale per row; q4 = 16 bytes per 32-group (element j
+ *    in the low nibble of byte j, element j+16 in the high nibble, value q+8) + f32 scale
+ *    per (row, group) — the export layout of tools/elm.py:41-71 / model.cpp:150-190;
+ *  - ELMH_ACT_INT8: each activation row is quantized per 32-element block exactly like
+ *    quantize_act_row (kernels_ref.cpp:23-37); int32 block sums are exact and the f32
+ *    result equals the cpu backend's scalar path (kernels_cpu.cpp:138-228) bit for bit
+ *    in ELMH_EXACT mode;
+ *  - ELMH_ACT_F32: f32 activations, same order of float operations as the scalar
+ *    dot_q8 / dot_q4 (T == 1) and dequantize + dot_f32 (T > 1) paths
+ *    (kernels_cpu.cpp:32-123, 254-290);
+ *  - FFN_SWIGLU: y = silu(x.Wg^T) * (x.Wu^T), silu(v) = v / (1 + expf(-v))
+ *    (kernels_cpu.cpp:292, 379-411).
+ *
+ * Threading: one HIP stream per context; a context is not thread-safe. Host-pointer entry
+ * points are synchronous (outputs are in host memory on return, as Backend::run requires);
+ * *_dev entry points take device pointers and are stream-ordered on the context's stream.
+ */
+#ifndef ELMH_H
+#define ELMH_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  ELMH_OK = 0,
+  ELMH_ERR_ARG = 1,          /* bad argument (shape, dtype, null pointer) */
+  ELMH_ERR_HIP = 2,          /* a HIP runtime call failed */
+  ELMH_ERR_NODEV = 3,        /* no usable gfx950 device */
+  ELMH_ERR_UNSUPPORTED = 4,  /* valid request outside what the kernels implement */
+  ELMH_ERR_OOM = 5
+} elmh_status;
+
+/* weight dtypes: the values of edgelm's DType (include/edgelm/graph.hpp:17) */
+enum { ELMH_F32 = 0, ELMH_Q8 = 1, ELMH_Q4 = 2 };
+
+/* activation handling */
+enum {
+  ELMH_ACT_F32 = 0,        /* Session act_quant = false (runtime.hpp:25) */
+  ELMH_ACT_INT8 = 1,       /* act_quant = true: per-row x per-32-block int8 (kernels.hpp:38-48) */
+  ELMH_ACT_INT8_TOKEN = 2  /* extension, no counterpart in edgelm: one int8 scale per row */
+};
+
+/* f32 rescale order of the int8 GEMM (T > 4) */
+enum {
+  ELMH_EXACT = 0, /* sequential multiply then add per 32-block: bit-identical to the cpu backend */
+  ELMH_FAST = 1   /* fused multiply-add per 32-block: within 1e-6 relative, not bit-identical */
+};
+
+typedef struct elmh_ctx elmh_ctx;
+typedef struct elmh_weight elmh_weight;
+
+/* ---- context (replaces nothing in edgelm: the cpu backend needs no device state) ---- */
+int elmh_device_count(int* count);
+int elmh_create(int device, elmh_ctx** out);
+void elmh_destroy(elmh_ctx* ctx);
+/* Message of the last failed call on ctx (ctx may be NULL: last failure on this thread). */
+const char* elmh_last_error(const elmh_ctx* ctx);
+/* Name of the device architecture the context runs on (e.g. "gfx950"). */
+const char* elmh_device_arch(const elmh_ctx* ctx);
+
+/* ---- weights: one upload per edgelm weight Tensor (graph.hpp:33-45) ----
+ * Copies data/scales (host pointers, edgelm's export layout) into HBM in the repacked layout;
+ * the host buffers are not retained. K must be a multiple of 32 for q4. */
+int elmh_upload_weight(elmh_ctx* ctx, int dtype, int64_t rows, int64_t cols, const void* data,
+                       const float* scales, elmh_weight** out);
+int elmh_free_weight(elmh_ctx* ctx, elmh_weight* w);
+/* Device bytes held by the weight (data + scales, after padding). */
+size_t elmh_weight_bytes(const elmh_weight* w);
+
+/* ---- MATMUL / MATMUL_N / MATMUL_ADD (cpu::matmul, kernels_cpu.cpp:339-377) ----
+ * For each target i: y[i][T, N_i] = (residual[i] ? residual[i] : 0) + x[T, K] . W_i^T.
+ * x is quantized once for all targets (int8 modes). residual may be NULL, or residual[i]
+ * NULL for a target without one. Host pointers; synchronous. */
+int elmh_matmul(elmh_ctx* ctx, const float* x, int T, int64_t K, int n_targets, elmh_weight* const* w,
+                float* const* y, const float* const* residual, int act, int mode);
+
+/* ---- FFN_SWIGLU (cpu::swiglu, kernels_cpu.cpp:379-411) ----
+ * y[T, N] = silu(x . Wg^T) * (x . Wu^T). Host pointers; synchronous. */
+int elmh_swiglu(elmh_ctx* ctx, const float* x, int T, int64_t K, const elmh_weight* wg, const elmh_weight* wu,
+                float* y, int act, int mode);
+
+/* ---- device-resident variants: same semantics, device pointers, asynchronous on the context
+ * stream (no host synchronization; capturable in a HIP graph once scratch is reserved). */
+int elmh_reserve(elmh_ctx* ctx, int max_T, int64_t max_K);
+int elmh_matmul_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, int n_targets, elmh_weight* const* w,
+                    float* const* y, const float* const* residual, int act, int mode);
+int elmh_swiglu_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, const elmh_weight* wg,
+                    const elmh_weight* wu, float* y, int act, int mode);
+
+/* ---- pre-quantized activations (the ActBuf of kernels.hpp:39-44, row-major) ----
+ * elmh_quantize_act_dev writes q [T, K] int8, d [T, K/32] f32 and s [T, K/32] int32 block
+ * sums of q; elmh_gemv_a8_dev runs the T <= 4 int8 GEMV of MATMUL/MATMUL_ADD on them
+ * (row_a8 with a shared ActBuf, kernels_cpu.cpp:207-220). */
+int elmh_quantize_act_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, int8_t* q, float* d, int32_t* s);
+int elmh_gemv_a8_dev(elmh_ctx* ctx, const int8_t* q, const float* d, const int32_t* s, int T, int64_t K,
+                     int n_targets, elmh_weight* const* w, float* const* y, const float* const* residual);
+
+/* ---- test hooks ----
+ * quantize_act_row on the device (host pointers; q [T,K], d [T,K/32]). */
+int elmh_quantize_act(elmh_ctx* ctx, const float* x, int T, int64_t K, int8_t* q, float* d);
+/* Exact int32 block sums S[t][n][b] = sum_i wq * xq over 32-block b (host pointers;
+ * xq [T,K] int8 row-major; S [T, N, K/32]). */
+int elmh_block_sums(elmh_ctx* ctx, const int8_t* xq, int T, const elmh_weight* w, int32_t* S);
+
+/* ---- device memory, stream and timing plumbing for callers without a runtime of their own ---- */
+int elmh_malloc(elmh_ctx* ctx, size_t bytes, void** dptr);
+int elmh_free(elmh_ctx* ctx, void* dptr);
+int elmh_memcpy_h2d(elmh_ctx* ctx, void* dst, const void* src, size_t bytes);
+int elmh_memcpy_d2h(elmh_ctx* ctx, void* dst, const void* src, size_t bytes);
+int elmh_memset_dev(elmh_ctx* ctx, void* dst, int value, size_t bytes);
+int elmh_synchronize(elmh_ctx* ctx);
+void* elmh_stream(elmh_ctx* ctx); /* the context's hipStream_t */
+/* Events on the context stream: record, then elapsed milliseconds between two records. */
+int elmh_event_create(elmh_ctx* ctx, void** ev);
+int elmh_event_destroy(elmh_ctx* ctx, void* ev);
+int elmh_event_record(elmh_ctx* ctx, void* ev);
+int elmh_event_elapsed(elmh_ctx* ctx, void* start, void* stop, float* ms);
+/* HIP graph capture of the context stream (launch-bound inner loops). */
+int elmh_graph_begin(elmh_ctx* ctx);
+int elmh_graph_end(elmh_ctx* ctx, void** graph_exec);
+int elmh_graph_launch(elmh_ctx* ctx, void* graph_exec);
+int elmh_graph_destroy(elmh_ctx* ctx, void* graph_exec);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ELMH_H */

@@ -1,0 +1,356 @@
+"""TEST INFRASTRUCTURE ONLY: ctypes bindings to the CPU oracle.
+
+Two libraries, both built by ``oracle/Makefile`` (called from ``__graft_entry__.build()``):
+
+* ``liboracle.so`` — this build's plain-C restatement of edgelm's algorithms for the
+  quantized-matmul path (``oracle/oracle.c``; each function cites reference file:line).
+* ``_ref/libedgelm_ref.so`` — edgelm's own C++ compiled from its sources (plus the
+  ``ref_shim.cpp`` C wrappers). Present only where it was built; the built file travels with
+  the tree.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import
+this package, and only as the checker or the CPU baseline. The product (``edgelm_amd``)
+never imports it.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libedgelm_ref.so")
+
+F32, Q8, Q4 = 0, 1, 2
+
+_P = C.c_void_p
+_I64 = C.c_int64
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class _OrcWeight(C.Structure):
+    _fields_ = [("dtype", C.c_int), ("rows", C.c_int64), ("cols", C.c_int64), ("data", C.c_void_p),
+                ("scales", C.c_void_p)]
+
+
+_orc = None
+_ref = None
+
+
+def orc():
+    global _orc
+    if _orc is None:
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError(f"oracle not built: {ORACLE_SO} (run __graft_entry__.build())")
+        _orc = C.CDLL(ORACLE_SO)
+        _orc.orc_round_away.restype = C.c_float
+        _orc.orc_round_away.argtypes = [C.c_float]
+        _orc.orc_silu.restype = C.c_float
+        _orc.orc_silu.argtypes = [C.c_float]
+    return _orc
+
+
+def ref_available():
+    return os.path.exists(REF_SO)
+
+
+def ref():
+    global _ref
+    if _ref is None:
+        if not ref_available():
+            raise RuntimeError(f"reference build missing: {REF_SO}")
+        _ref = C.CDLL(REF_SO)
+        _ref.eref_pool_create.restype = C.c_void_p
+        _ref.eref_pool_create.argtypes = [C.c_int, C.c_int, C.c_int64]
+        _ref.eref_pool_destroy.argtypes = [C.c_void_p]
+        _ref.eref_session_create.restype = C.c_void_p
+        _ref.eref_session_create.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+        for f in ("eref_session_destroy", "eref_session_reset", "eref_session_vocab"):
+            getattr(_ref, f).argtypes = [C.c_void_p]
+        _ref.eref_last_error.restype = C.c_char_p
+        _ref.eref_argmax.restype = C.c_int32
+    return _ref
+
+
+class Weight:
+    """A quantized (or f32) weight held in host numpy arrays, in edgelm's export layout."""
+
+    def __init__(self, dtype, rows, cols, data, scales=None):
+        self.dtype, self.rows, self.cols = dtype, int(rows), int(cols)
+        self.data = np.ascontiguousarray(data)
+        self.scales = None if scales is None else np.ascontiguousarray(scales, dtype=np.float32)
+
+    def orc(self):
+        return _OrcWeight(self.dtype, self.rows, self.cols, self.data.ctypes.data,
+                          None if self.scales is None else self.scales.ctypes.data)
+
+
+# ------------------------------------------------------------------ C restatement
+
+def quantize_q8(w):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    q = np.empty((n, k), np.int8)
+    s = np.empty(n, np.float32)
+    orc().orc_quantize_q8(_ptr(w), _I64(n), _I64(k), _ptr(q), _ptr(s))
+    return q, s
+
+
+def quantize_q4(w):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    q = np.empty((n, k // 2), np.uint8)
+    s = np.empty((n, k // 32), np.float32)
+    orc().orc_quantize_q4(_ptr(w), _I64(n), _I64(k), _ptr(q), _ptr(s))
+    return q, s
+
+
+def make_weight(w, dtype):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    if dtype == F32:
+        return Weight(F32, n, k, w)
+    q, s = quantize_q8(w) if dtype == Q8 else quantize_q4(w)
+    return Weight(dtype, n, k, q, s)
+
+
+def dequantize(wt):
+    out = np.empty((wt.rows, wt.cols), np.float32)
+    ow = wt.orc()
+    for r in range(wt.rows):
+        orc().orc_dequantize_row(C.byref(ow), _I64(r), _ptr(out[r]))
+    return out
+
+
+def quantize_act(x):
+    """Per-row, per-32-block int8 activations: (q int8 [T,K], d f32 [T,K/32])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, K = x.shape
+    q = np.empty((T, K), np.int8)
+    d = np.empty((T, K // 32), np.float32)
+    for t in range(T):
+        orc().orc_quantize_act_row(_ptr(x[t]), _I64(K), _ptr(q[t]), _ptr(d[t]))
+    return q, d
+
+
+def quantize_act_token(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, K = x.shape
+    q = np.empty((T, K), np.int8)
+    d = np.empty(T, np.float32)
+    for t in range(T):
+        orc().orc_quantize_act_row_token(_ptr(x[t]), _I64(K), _ptr(q[t]), _ptr(d[t:t + 1]))
+    return q, d
+
+
+def ref_matmul(x, w, residual=None, act_quant=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    y = np.empty((T, w.rows), np.float32)
+    res = None if residual is None else np.ascontiguousarray(residual, dtype=np.float32)
+    ow = w.orc()
+    orc().orc_ref_matmul(_ptr(x), C.c_int(T), C.byref(ow), _ptr(y), _ptr(res), C.c_int(int(act_quant)))
+    return y
+
+
+def ref_swiglu(x, wg, wu, act_quant=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    y = np.empty((T, wg.rows), np.float32)
+    g, u = wg.orc(), wu.orc()
+    orc().orc_ref_swiglu(_ptr(x), C.c_int(T), C.byref(g), C.byref(u), _ptr(y), C.c_int(int(act_quant)))
+    return y
+
+
+def cpu_matmul(x, weights, residuals=None, act_quant=False):
+    """edgelm cpu::matmul (x86 scalar path) over targets; returns a list of outputs."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    n = len(weights)
+    arr = (_OrcWeight * n)(*[w.orc() for w in weights])
+    ys = [np.empty((T, w.rows), np.float32) for w in weights]
+    yp = (C.c_void_p * n)(*[y.ctypes.data for y in ys])
+    if residuals is not None:
+        residuals = [None if r is None else np.ascontiguousarray(r, dtype=np.float32) for r in residuals]
+        rp = (C.c_void_p * n)(*[None if r is None else r.ctypes.data for r in residuals])
+    else:
+        rp = None
+    orc().orc_cpu_matmul(_ptr(x), C.c_int(T), C.c_int(n), arr, yp, rp, C.c_int(int(act_quant)))
+    return ys
+
+
+def cpu_swiglu(x, wg, wu, act_quant=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    y = np.empty((T, wg.rows), np.float32)
+    g, u = wg.orc(), wu.orc()
+    orc().orc_cpu_swiglu(_ptr(x), C.c_int(T), C.byref(g), C.byref(u), _ptr(y), C.c_int(int(act_quant)))
+    return y
+
+
+def block_sums(xq, w):
+    xq = np.ascontiguousarray(xq, dtype=np.int8)
+    T = xq.shape[0]
+    S = np.empty((T, w.rows, w.cols // 32), np.int32)
+    ow = w.orc()
+    orc().orc_block_sums(_ptr(xq), C.c_int(T), C.byref(ow), _ptr(S))
+    return S
+
+
+def matmul_a8_token(x, w, residual=None):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    y = np.empty((T, w.rows), np.float32)
+    res = None if residual is None else np.ascontiguousarray(residual, dtype=np.float32)
+    ow = w.orc()
+    orc().orc_matmul_a8_token(_ptr(x), C.c_int(T), C.byref(ow), _ptr(y), _ptr(res))
+    return y
+
+
+def silu(v):
+    return orc().orc_silu(C.c_float(v))
+
+
+# ------------------------------------------------------------------ edgelm's own C++ (oracle/_ref)
+
+def rq_quantize_q8(w):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    q = np.empty((n, k), np.int8)
+    s = np.empty(n, np.float32)
+    ref().eref_quantize_q8(_ptr(w), _I64(n), _I64(k), _ptr(q), _ptr(s))
+    return q, s
+
+
+def rq_quantize_q4(w):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    q = np.empty((n, k // 2), np.uint8)
+    s = np.empty((n, k // 32), np.float32)
+    ref().eref_quantize_q4(_ptr(w), _I64(n), _I64(k), _ptr(q), _ptr(s))
+    return q, s
+
+
+def rq_quantize_act(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, K = x.shape
+    q = np.empty((T, K), np.int8)
+    d = np.empty((T, K // 32), np.float32)
+    for t in range(T):
+        ref().eref_quantize_act_row(_ptr(x[t]), _I64(K), _ptr(q[t]), _ptr(d[t]))
+    return q, d
+
+
+def rq_ref_matmul(x, w, residual=None, act_quant=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    y = np.empty((T, w.rows), np.float32)
+    res = None if residual is None else np.ascontiguousarray(residual, dtype=np.float32)
+    ref().eref_ref_matmul(_ptr(x), C.c_int(T), C.c_int(w.dtype), _I64(w.rows), _I64(w.cols), _ptr(w.data),
+                          _ptr(w.scales), _ptr(y), _ptr(res), C.c_int(int(act_quant)))
+    return y
+
+
+def rq_ref_swiglu(x, wg, wu, act_quant=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    y = np.empty((T, wg.rows), np.float32)
+    ref().eref_ref_swiglu(_ptr(x), C.c_int(T), C.c_int(wg.dtype), C.c_int(wu.dtype), _I64(wg.rows), _I64(wg.cols),
+                          _ptr(wg.data), _ptr(wg.scales), _ptr(wu.data), _ptr(wu.scales), _ptr(y),
+                          C.c_int(int(act_quant)))
+    return y
+
+
+class RefPool:
+    """edgelm ThreadPool + per-thread scratch, sized for max_T tokens and max_k."""
+
+    def __init__(self, threads, max_T, max_k):
+        self.h = ref().eref_pool_create(threads, max_T, max_k)
+
+    def close(self):
+        if self.h:
+            ref().eref_pool_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def rq_cpu_matmul(pool, x, weights, residuals=None, act_quant=False, out=None):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    n = len(weights)
+    K = weights[0].cols
+    dt = (C.c_int * n)(*[w.dtype for w in weights])
+    rows = (C.c_int64 * n)(*[w.rows for w in weights])
+    data = (C.c_void_p * n)(*[w.data.ctypes.data for w in weights])
+    sc = (C.c_void_p * n)(*[None if w.scales is None else w.scales.ctypes.data for w in weights])
+    ys = out if out is not None else [np.empty((T, w.rows), np.float32) for w in weights]
+    yp = (C.c_void_p * n)(*[y.ctypes.data for y in ys])
+    rp = None
+    if residuals is not None:
+        rp = (C.c_void_p * n)(*[None if r is None else r.ctypes.data for r in residuals])
+    rc = ref().eref_cpu_matmul(C.c_void_p(pool.h), _ptr(x), C.c_int(T), C.c_int(n), dt, rows, _I64(K), data, sc, yp,
+                               rp, C.c_int(int(act_quant)))
+    if rc:
+        raise RuntimeError(ref().eref_last_error().decode())
+    return ys
+
+
+def rq_cpu_swiglu(pool, x, wg, wu, act_quant=False, out=None):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    y = out if out is not None else np.empty((T, wg.rows), np.float32)
+    rc = ref().eref_cpu_swiglu(C.c_void_p(pool.h), _ptr(x), C.c_int(T), C.c_int(wg.dtype), C.c_int(wu.dtype),
+                               _I64(wg.rows), _I64(wg.cols), _ptr(wg.data), _ptr(wg.scales), _ptr(wu.data),
+                               _ptr(wu.scales), _ptr(y), C.c_int(int(act_quant)))
+    if rc:
+        raise RuntimeError(ref().eref_last_error().decode())
+    return y
+
+
+class RefSession:
+    """edgelm's own Session over an .elm file (loader, fusion passes, partitioner, backends)."""
+
+    def __init__(self, path, backends="cpu", threads=1, max_ctx=256, max_batch=128, all_logits=False,
+                 act_quant=False):
+        self.h = ref().eref_session_create(path.encode(), backends.encode(), threads, max_ctx, max_batch,
+                                           int(all_logits), int(act_quant))
+        if not self.h:
+            raise RuntimeError(ref().eref_last_error().decode())
+        self.vocab = ref().eref_session_vocab(C.c_void_p(self.h))
+        self.all_logits = all_logits
+
+    def forward(self, tokens):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        n = len(tokens)
+        rows = n if self.all_logits else 1
+        out = np.empty((rows, self.vocab), np.float32)
+        if ref().eref_session_forward(C.c_void_p(self.h), _ptr(tokens), C.c_int(n), _ptr(out)):
+            raise RuntimeError(ref().eref_last_error().decode())
+        return out
+
+    def reset(self):
+        ref().eref_session_reset(C.c_void_p(self.h))
+
+    def describe(self):
+        buf = C.create_string_buffer(4096)
+        nops = ref().eref_session_describe(C.c_void_p(self.h), buf, 4096)
+        return nops, buf.value.decode()
+
+    def close(self):
+        if self.h:
+            ref().eref_session_destroy(C.c_void_p(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,180 @@
+// TEST INFRASTRUCTURE ONLY — extern "C" wrappers around edgelm's own C++ (compiled from the
+// reference sources by oracle/Makefile into oracle/_ref/libedgelm_ref.so). Used to pin the C
+// oracle, to generate fixtures, and as bench.py's cpu_baseline ("kind": "reference"). The
+// product never links or loads it.
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "edgelm/backend.hpp"
+#include "edgelm/kernels.hpp"
+#include "edgelm/model.hpp"
+#include "edgelm/runtime.hpp"
+#include "edgelm/thread_pool.hpp"
+#include "edgelm/tokenizer.hpp"
+
+using namespace edgelm;
+
+namespace {
+
+Tensor make_tensor(int dtype, int64_t rows, int64_t cols, const void* data, const float* scales) {
+  Tensor t;
+  t.kind = TensorKind::Weight;
+  t.dtype = static_cast<DType>(dtype);
+  t.rows = rows;
+  t.cols = cols;
+  t.data = data;
+  t.scales = scales;
+  t.group = dtype == 2 ? 32 : dtype == 1 ? static_cast<int>(cols) : 0;
+  return t;
+}
+
+struct Pool {
+  ThreadPool pool;
+  std::vector<std::vector<float>> bufs;
+  std::vector<float*> ptrs;
+  Pool(int threads, int T, int64_t max_k) : pool(threads) {
+    for (int i = 0; i < pool.size(); ++i) bufs.emplace_back(cpu::scratch_floats(T, max_k, 1, 1));
+    for (auto& b : bufs) ptrs.push_back(b.data());
+  }
+};
+
+thread_local std::string g_err;
+
+}  // namespace
+
+extern "C" {
+
+const char* eref_last_error() { return g_err.c_str(); }
+
+void eref_quantize_q8(const float* w, int64_t n, int64_t k, int8_t* out, float* scales) { quantize_q8(w, n, k, out, scales); }
+void eref_quantize_q4(const float* w, int64_t n, int64_t k, uint8_t* out, float* scales) { quantize_q4(w, n, k, out, scales); }
+void eref_dequantize_row(int dtype, int64_t rows, int64_t cols, const void* data, const float* scales, int64_t row,
+                         float* out) {
+  Tensor t = make_tensor(dtype, rows, cols, data, scales);
+  dequantize_row(t, row, out);
+}
+void eref_quantize_act_row(const float* x, int64_t k, int8_t* q, float* d) { quantize_act_row(x, k, q, d); }
+
+void eref_ref_matmul(const float* x, int T, int dtype, int64_t rows, int64_t cols, const void* data, const float* scales,
+                     float* y, const float* residual, int act_quant) {
+  Tensor t = make_tensor(dtype, rows, cols, data, scales);
+  ref::matmul(x, T, t, y, residual, act_quant != 0);
+}
+
+void eref_ref_swiglu(const float* x, int T, int dtype_g, int dtype_u, int64_t rows, int64_t cols, const void* dg,
+                     const float* sg, const void* du, const float* su, float* y, int act_quant) {
+  Tensor g = make_tensor(dtype_g, rows, cols, dg, sg), u = make_tensor(dtype_u, rows, cols, du, su);
+  ref::swiglu(x, T, g, u, y, act_quant != 0);
+}
+
+void eref_set_simd(int on) { cpu::set_simd(on != 0); }
+
+void* eref_pool_create(int threads, int max_T, int64_t max_k) { return new Pool(threads, max_T, max_k); }
+void eref_pool_destroy(void* p) { delete static_cast<Pool*>(p); }
+
+// cpu::matmul over n targets. dtypes/rows/data/scales/y/residual are arrays of length n.
+int eref_cpu_matmul(void* pool, const float* x, int T, int n, const int* dtypes, const int64_t* rows, int64_t cols,
+                    const void* const* data, const float* const* scales, float* const* y, const float* const* residual,
+                    int act_quant) {
+  try {
+    Pool* p = static_cast<Pool*>(pool);
+    std::vector<Tensor> ts;
+    for (int i = 0; i < n; ++i) ts.push_back(make_tensor(dtypes[i], rows[i], cols, data[i], scales[i]));
+    std::vector<MatmulTarget> tg;
+    for (int i = 0; i < n; ++i) tg.push_back({&ts[i], y[i], residual ? residual[i] : nullptr});
+    std::vector<int8_t> q(static_cast<size_t>(T) * cols);
+    std::vector<float> d(static_cast<size_t>(T) * (cols / kActBlock + 1));
+    ActBuf aq{q.data(), d.data()};
+    cpu::matmul(x, T, tg, &p->pool, p->ptrs.data(), act_quant ? &aq : nullptr);
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return 1;
+  }
+}
+
+int eref_cpu_swiglu(void* pool, const float* x, int T, int dtype_g, int dtype_u, int64_t rows, int64_t cols,
+                    const void* dg, const float* sg, const void* du, const float* su, float* y, int act_quant) {
+  try {
+    Pool* p = static_cast<Pool*>(pool);
+    Tensor g = make_tensor(dtype_g, rows, cols, dg, sg), u = make_tensor(dtype_u, rows, cols, du, su);
+    std::vector<int8_t> q(static_cast<size_t>(T) * cols);
+    std::vector<float> d(static_cast<size_t>(T) * (cols / kActBlock + 1));
+    ActBuf aq{q.data(), d.data()};
+    cpu::swiglu(x, T, g, u, y, &p->pool, p->ptrs.data(), act_quant ? &aq : nullptr);
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return 1;
+  }
+}
+
+// ---- whole-model runs through the reference's own loader, passes, partitioner and Session ----
+
+struct RefRun {
+  Model model;
+  std::unique_ptr<Session> session;
+};
+
+// Loads an .elm file and builds a Session. backends: comma-separated preference list.
+void* eref_session_create(const char* path, const char* backends, int threads, int max_ctx, int max_batch,
+                          int all_logits, int act_quant) {
+  try {
+    auto r = std::make_unique<RefRun>();
+    r->model = Model::load(path);
+    SessionOptions o;
+    o.backends.clear();
+    std::string s(backends);
+    size_t pos = 0;
+    while (pos <= s.size()) {
+      const size_t c = s.find(',', pos);
+      const std::string b = s.substr(pos, c == std::string::npos ? std::string::npos : c - pos);
+      if (!b.empty()) o.backends.push_back(b);
+      if (c == std::string::npos) break;
+      pos = c + 1;
+    }
+    o.threads = threads;
+    o.max_ctx = max_ctx;
+    o.max_batch = max_batch;
+    o.all_logits = all_logits != 0;
+    o.act_quant = act_quant != 0;
+    r->session = std::make_unique<Session>(r->model, o);
+    return r.release();
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return nullptr;
+  }
+}
+
+void eref_session_destroy(void* h) { delete static_cast<RefRun*>(h); }
+void eref_session_reset(void* h) { static_cast<RefRun*>(h)->session->reset(); }
+int eref_session_vocab(void* h) { return static_cast<RefRun*>(h)->model.cfg.vocab; }
+
+// forward(tokens, n); copies rows*vocab logits into out (rows = all_logits ? n : 1).
+int eref_session_forward(void* h, const int32_t* tokens, int n, float* out) {
+  try {
+    RefRun* r = static_cast<RefRun*>(h);
+    const float* lg = r->session->forward(tokens, n, n > 1 ? "prefill" : "decode");
+    const int rows = r->session->options().all_logits ? n : 1;
+    std::memcpy(out, lg, sizeof(float) * static_cast<size_t>(rows) * r->model.cfg.vocab);
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return 1;
+  }
+}
+
+int32_t eref_argmax(const float* logits, int n) { return argmax(logits, n); }
+
+// describe_partitions of the session's graph (for partition-count parity tests)
+int eref_session_describe(void* h, char* buf, int cap) {
+  RefRun* r = static_cast<RefRun*>(h);
+  const std::string s = describe_partitions(r->session->graph(), r->session->partitions());
+  std::strncpy(buf, s.c_str(), static_cast<size_t>(cap) - 1);
+  buf[cap - 1] = 0;
+  return static_cast<int>(r->session->graph().ops.size());
+}
+
+}  // extern "C"
