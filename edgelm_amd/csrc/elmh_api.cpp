@@ -85,16 +85,21 @@ int ensure(elmh_ctx* c, DevBuf& b, size_t bytes) {
 
 int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
-// Row-tile height of the repacked layout: the largest of 32/16/8/4 rows whose tile (all blocks of
-// those rows) stays near 48 KB, so a decode GEMV workgroup streams one contiguous chunk of that size.
-// Depends on dtype and K only, so every weight sharing an input (MATMUL_N, gate/up) agrees.
+// Row-tile height of the repacked layout, chosen from dtype and K only (so every weight sharing an
+// input — MATMUL_N, gate/up — agrees). Short rows (K <= 2048) use 8-row tiles: many small decode
+// workgroups with at most two items per thread. Long rows use the tallest tile whose items fit the
+// streaming GEMV's registers (q4: 2048 items of 16 B, q8: 1024 items of 32 B), at least 4 rows.
 int choose_H(int dtype, int64_t K) {
   const int64_t nb = (K + kBlock - 1) / kBlock;
-  const int64_t per_row = nb * (dtype == ELMH_Q4 ? 20 : 32);
+  if (K <= 2048) return 8;
+  const int64_t cap = dtype == ELMH_Q4 ? 2048 : 1024;
   for (int H : {32, 16, 8})
-    if (H * per_row <= 48 * 1024) return H;
+    if (H * nb <= cap) return H;
   return 4;
 }
+
+// Small-matrix decode path (workgroups quantize x themselves) vs the streaming path.
+bool use_small_gemv(int T, int64_t K) { return K <= 2048 && gemv_qin_ok(T, (int)K); }
 
 bool a8_applies(const DevWeight& w) { return (w.dtype == ELMH_Q8 || w.dtype == ELMH_Q4) && w.cols % kBlock == 0; }
 
@@ -103,7 +108,9 @@ int gemv_tokens(const DevWeight& w, int nsel) {
   const int K = (int)w.cols, nb = (int)w.nb;
   for (int nt : {4, 2, 1}) {
     if (nt > gemv_max_tokens(K)) continue;
-    if (gemv_lds_bytes(nt, K, nb, w.H, nsel) <= 64 * 1024) return nt;
+    if (gemv_lds_bytes(nt, K, nb, w.H, nsel) > 64 * 1024) continue;
+    if (!use_small_gemv(nt, K) && gemv_stream_ipt(w.dtype, nsel * w.H * nb) == 0) continue;
+    return nt;
   }
   return 0;
 }
@@ -138,6 +145,7 @@ int run_gemv_group(elmh_ctx* c, const float* x, const int8_t* xq, const float* x
     }
     a.tile_start[n] = tiles;
     a.n_targets = (int)n;
+    a.total_tiles = tiles;
     a.x = x;
     a.xq = xq;
     a.xd = xd;
@@ -265,7 +273,7 @@ int run_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight
   int nt = 4;
   for (int i = 0; i < n; ++i) nt = std::min(nt, gemv_tokens(w[i]->w, 1));
   if (T <= nt) {
-    const bool qin = K <= 2048;  // small rows: each workgroup quantizes x itself (no extra launch)
+    const bool qin = use_small_gemv(T, K);  // small rows: each workgroup quantizes x itself
     if (!qin && (rc = quant_rows(c, x, T, K))) return rc;
     for (const auto& g : groups)
       if ((rc = run_gemv_group(c, qin ? x : nullptr, qin ? nullptr : (const int8_t*)c->xq.p,
@@ -323,12 +331,13 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
   const int nt = gemv_tokens(g, 2);
   if (act == ELMH_ACT_INT8 && T <= nt) {
     GemvArgs a{};
-    const bool qin = K <= 2048;
+    const bool qin = use_small_gemv(T, K);
     if (!qin && (rc = quant_rows(c, x, T, K))) return rc;
     const int tiles = (int)(g.rows_pad / g.H);
     a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, tiles};
     a.tg[1] = {u.data, u.scales, y, nullptr, (int)u.rows, tiles};
     a.n_targets = 2;
+    a.total_tiles = tiles;
     a.H = g.H;
     a.x = qin ? x : nullptr;
     a.xq = qin ? nullptr : (const int8_t*)c->xq.p;

@@ -50,6 +50,7 @@ struct GemvArgs {
   GemvTarget tg[kMaxTargets];
   int tile_start[kMaxTargets + 1];  // prefix sums of tiles (matmul); swiglu uses tg[0]/tg[1]
   int n_targets;
+  int total_tiles;
   int H;
   const float* x;     // f32 [T][K] (quantized inside each workgroup) or null
   const int8_t* xq;   // int8 [T][K] row-major (pre-quantized) when x is null
@@ -100,6 +101,10 @@ hipError_t launch_act_quant_frag_token(const float* x, int T, int Tpad, int K, i
 
 // Largest T the int8 GEMV path takes for this K (activation rows staged in LDS).
 int gemv_max_tokens(int K);
+// True if a workgroup may quantize T rows of K activations itself (small-matrix GEMV).
+bool gemv_qin_ok(int T, int K);
+// Items per thread of the streaming GEMV for a tile of `items` items (0: too many).
+int gemv_stream_ipt(int dtype, int items);
 size_t gemv_lds_bytes(int nt, int K, int nb, int H, int nsel);
 hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_tiles, hipStream_t s);
 hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs& a, int total_tiles, hipStream_t s);

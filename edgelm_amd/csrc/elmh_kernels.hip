@@ -152,155 +152,323 @@ __global__ __launch_bounds__(256) void act_quant_frag_token_kernel(const float* 
 
 // ---------------------------------------------------------------- int8 GEMV (decode)
 //
-// One workgroup owns one H-row tile of a weight (both gate and up tiles for SwiGLU): a contiguous
-// chunk of the repacked layout. Phase 1: every (row, block) item's product
+// A workgroup owns one H-row tile of the weight (for SwiGLU the gate and up tiles together): one
+// contiguous chunk of the repacked layout. Every (row, block) item's product
 //   q8: p = float(S_b) * xd_b        q4: p/16 = float(S_b) * ((ws_b/16) * xd_b)
-// goes to LDS (each multiply rounds exactly as on the CPU; /16 is exact). Phase 2: one lane per
-// (token, row) folds its products in block order with plain adds, then applies the epilogue.
+// goes to LDS (each multiply rounds exactly as on the CPU; /16 is exact); then one lane per
+// (token, row) folds its products in block order with plain adds and applies the epilogue.
 // Consecutive lanes take consecutive items, so every weight load instruction reads one
-// contiguous run of the chunk.
+// contiguous run. Every dispatch starts with cold instruction caches, so the kernels are kept
+// short and issue all of their loads before any dependent work.
 
-template <int WDT, int NT, bool QIN, bool SW>
-__global__ __launch_bounds__(kGemvThreads) void gemv_a8_kernel(const GemvArgs a) {
+constexpr int kActRegs = 4;  // int4 of pre-quantized activation per thread (T*K <= 16384)
+
+__device__ __forceinline__ int fold_stride(int nb) {
+  const int p = (nb + 3) & ~3;
+  return ((p >> 2) & 1) ? p : p + 4;  // multiple of 4 (16-byte rows), odd in float4 units
+}
+
+template <int WDT>
+__device__ __forceinline__ float item_product(const v4u w0, const v4u w1, float wsc, const int8_t* act, float xd,
+                                              int xs) {
+  const int4* aq = reinterpret_cast<const int4*>(act);
+  const int4 a0 = aq[0], a1 = aq[1];
+  if (WDT == WQ8) {
+    int S = sdot4((int)w0.x, a0.x, 0);
+    S = sdot4((int)w0.y, a0.y, S);
+    S = sdot4((int)w0.z, a0.z, S);
+    S = sdot4((int)w0.w, a0.w, S);
+    S = sdot4((int)w1.x, a1.x, S);
+    S = sdot4((int)w1.y, a1.y, S);
+    S = sdot4((int)w1.z, a1.z, S);
+    S = sdot4((int)w1.w, a1.w, S);
+    return (float)S * xd;
+  }
+  // sum_i (nib_i - 8) x_i = sum_i nib_i x_i - 8 * sum_i x_i (nibbles 0..15 are valid int8)
+  int S = -8 * xs;
+  S = sdot4((int)(w0.x & 0x0F0F0F0Fu), a0.x, S);
+  S = sdot4((int)(w0.y & 0x0F0F0F0Fu), a0.y, S);
+  S = sdot4((int)(w0.z & 0x0F0F0F0Fu), a0.z, S);
+  S = sdot4((int)(w0.w & 0x0F0F0F0Fu), a0.w, S);
+  S = sdot4((int)((w0.x >> 4) & 0x0F0F0F0Fu), a1.x, S);
+  S = sdot4((int)((w0.y >> 4) & 0x0F0F0F0Fu), a1.y, S);
+  S = sdot4((int)((w0.z >> 4) & 0x0F0F0F0Fu), a1.z, S);
+  S = sdot4((int)((w0.w >> 4) & 0x0F0F0F0Fu), a1.w, S);
+  return (float)S * (wsc * xd);
+}
+
+// Sequential block-order fold of one LDS row of products.
+__device__ __forceinline__ float fold_row(const float* row, int nb) {
+  const float4* pv = reinterpret_cast<const float4*>(row);
+  float acc = 0.f;
+  const int nq = nb >> 2;
+  for (int q = 0; q < nq; ++q) {
+    const float4 v = pv[q];
+    acc = acc + v.x;
+    acc = acc + v.y;
+    acc = acc + v.z;
+    acc = acc + v.w;
+  }
+  for (int b = nq * 4; b < nb; ++b) acc = acc + row[b];
+  return acc;
+}
+
+struct GemvLds {
+  int8_t* q;  // [NT][kpad]
+  float* d;   // [NT][nb]
+  int* s;     // [NT][nb]
+  float* p;   // [NSEL][NT][H][pst]
+  int kpad, pst;
+};
+
+template <int NT>
+__device__ __forceinline__ GemvLds gemv_lds(unsigned char* smem, int K, int nb) {
+  GemvLds L;
+  L.kpad = (K + 15) & ~15;
+  L.pst = fold_stride(nb);
+  L.q = reinterpret_cast<int8_t*>(smem);
+  L.d = reinterpret_cast<float*>(smem + NT * L.kpad);
+  L.s = reinterpret_cast<int*>(L.d + NT * nb);
+  L.p = reinterpret_cast<float*>(smem + NT * L.kpad + ((NT * nb * 8 + 15) & ~15));
+  return L;
+}
+
+// Phase 3 of both GEMV kernels: fold and epilogue for lane tid < T*H.
+template <int WDT, int NT, bool SW>
+__device__ __forceinline__ void gemv_fold(const GemvArgs& a, const GemvLds& L, const GemvTarget& tg, int tile, int tid,
+                                          float e_res, float e_s, float e_su) {
+  const int H = a.H, T = a.T;
+  const int ft = tid / H, fr = tid - ft * H;
+  const int fn = tile * H + fr;
+  if (tid >= T * H || fn >= tg.N) return;
+  float out = fold_row(L.p + (ft * H + fr) * L.pst, a.nb);
+  out = WDT == WQ8 ? out * e_s : out * 16.0f;
+  if (SW) {
+    float up = fold_row(L.p + ((NT + ft) * H + fr) * L.pst, a.nb);
+    up = WDT == WQ8 ? up * e_su : up * 16.0f;
+    out = silu_exact(out) * up;
+  } else if (tg.res) {
+    out = out + e_res;
+  }
+  tg.y[(int64_t)ft * tg.N + fn] = out;
+}
+
+// Small decode GEMV: x quantized inside the workgroup (8 elements per thread, 4 threads per
+// block), at most two items per thread held in registers before the products (longer tiles loop).
+constexpr int kSmallMaxAct = kGemvThreads * 8;
+
+template <int WDT, int NT, bool SW>
+__global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int G = WDT == WQ8 ? 32 : 16;
-  constexpr int U = WDT == WQ8 ? 2 : 4;  // items in flight per thread
-  constexpr int NSEL = SW ? 2 : 1;
-  const int K = a.K, nb = a.nb, T = a.T, H = a.H;
-  const int tid = threadIdx.x;
-  const int kpad = (K + 15) & ~15;
-  const int pst = nb | 1;  // odd LDS row stride: the fold's lanes hit distinct banks
-  int8_t* s_q = reinterpret_cast<int8_t*>(smem);
-  float* s_d = reinterpret_cast<float*>(smem + NT * kpad);
-  int* s_s = reinterpret_cast<int*>(s_d + NT * nb);
-  float* s_p = reinterpret_cast<float*>(s_s + NT * nb);
-
+  const int K = a.K, nb = a.nb, T = a.T, H = a.H, tid = threadIdx.x;
+  const GemvLds L = gemv_lds<NT>(smem, K, nb);
   int ti = 0, tile = blockIdx.x;
   if (!SW) {
-    while (ti + 1 < a.n_targets && (int)blockIdx.x >= a.tile_start[ti + 1]) ++ti;
-    tile = blockIdx.x - a.tile_start[ti];
+    while (ti + 1 < a.n_targets && tile >= a.tile_start[ti + 1]) ++ti;
+    tile -= a.tile_start[ti];
   }
+  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  const int per_sel = H * nb, items = (SW ? 2 : 1) * per_sel;
+  const int nel = T * K;
 
-  // phase 0: the activation rows into LDS
-  if (QIN) {
-    const int wave = tid >> 6, half = (tid >> 5) & 1, l = tid & 31;
-    for (int gp = wave; gp * 2 < T * nb; gp += kGemvThreads / 64) {
-      const int g = gp * 2 + half;
-      const bool ok = g < T * nb;
-      const int t = ok ? g / nb : 0, b = ok ? g - t * nb : 0;
-      const float v = ok ? a.x[(int64_t)t * K + b * kBlock + l] : 0.f;
-      float d;
-      int sum;
-      const int q = quant32(v, d, sum);
-      if (ok) {
-        s_q[t * kpad + b * kBlock + l] = (int8_t)q;
-        if (l == 0) {
-          s_d[t * nb + b] = d;
-          s_s[t * nb + b] = sum;
-        }
+  // 1. activation values (first: their wait does not cover the weight loads issued next)
+  const int e0 = tid * 8;
+  float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+  if (e0 < nel) {
+    x0 = *reinterpret_cast<const float4*>(a.x + e0);
+    x1 = *reinterpret_cast<const float4*>(a.x + e0 + 4);
+  }
+  // 2. weights of this thread's first two items
+  v4u w[2][G / 16];
+  float wsc[2] = {0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int it = u * kGemvThreads + tid;
+    if (it < items) {
+      const int sel = SW ? (it >= per_sel) : 0;
+      const GemvTarget& tw = a.tg[SW ? sel : ti];
+      const int64_t gi = (int64_t)tile * per_sel + (it - sel * per_sel);
+      const v4u* src = reinterpret_cast<const v4u*>(tw.data + gi * G);
+      w[u][0] = src[0];
+      if (G == 32) w[u][G / 16 - 1] = src[1];
+      if (WDT == WQ4) wsc[u] = tw.scales[gi];
+    }
+  }
+  // 3. epilogue operands of the folding lanes
+  float e_res = 0.f, e_s = 1.f, e_su = 1.f;
+  {
+    const int ft = tid / H, fn = tile * H + (tid - ft * H);
+    if (tid < T * H && fn < tg.N) {
+      if (WDT == WQ8) {
+        e_s = tg.scales[fn];
+        if (SW) e_su = a.tg[1].scales[fn];
+      }
+      if (!SW && tg.res) e_res = tg.res[(int64_t)ft * tg.N + fn];
+    }
+  }
+  // 4. quantize: block g = e0 / 32 spread over 4 consecutive lanes
+  for (int pass = 0; pass * kSmallMaxAct < nel; ++pass) {
+    const int e = pass * kSmallMaxAct + e0;
+    if (pass > 0) {
+      x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (e < nel) {
+        x0 = *reinterpret_cast<const float4*>(a.x + e);
+        x1 = *reinterpret_cast<const float4*>(a.x + e + 4);
       }
     }
-  } else {
-    for (int t = 0; t < T; ++t) {
-      const int4* src = reinterpret_cast<const int4*>(a.xq + (int64_t)t * K);
-      int4* dst = reinterpret_cast<int4*>(s_q + t * kpad);
-      for (int i = tid; i < K / 16; i += kGemvThreads) dst[i] = src[i];
-      for (int i = tid; i < nb; i += kGemvThreads) {
-        s_d[t * nb + i] = a.xd[(int64_t)t * nb + i];
-        s_s[t * nb + i] = a.xs[(int64_t)t * nb + i];
+    const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
+    am = fmaxf(am, __shfl_xor(am, 1, 4));
+    am = fmaxf(am, __shfl_xor(am, 2, 4));
+    const float sc = am / 127.0f;
+    const float safe = sc == 0.f ? 1.f : sc;
+    int qs = 0;
+    uint32_t pk[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float vv = v[i] / safe;
+      const int q = (int)fminf(127.f, fmaxf(-127.f, copysignf(floorf(fabsf(vv) + 0.5f), vv)));
+      qs += q;
+      pk[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
+    }
+    qs += __shfl_xor(qs, 1, 4);
+    qs += __shfl_xor(qs, 2, 4);
+    if (e < nel) {
+      const int g = e >> 5, t = g / nb, b = g - t * nb;
+      *reinterpret_cast<uint2*>(L.q + t * L.kpad + b * kBlock + (e & 31)) = make_uint2(pk[0], pk[1]);
+      if ((e & 31) == 0) {
+        L.d[t * nb + b] = sc;
+        L.s[t * nb + b] = qs;
       }
     }
   }
   __syncthreads();
 
-  // phase 1: products
-  const int per_sel = H * nb;
-  const int items = NSEL * per_sel;
-  for (int it0 = 0; it0 < items; it0 += kGemvThreads * U) {
-    v4u wv[U][G / 16];
-    float wsc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int it = it0 + u * kGemvThreads + tid;
-      wsc[u] = 0.f;
-      if (it < items) {
-        const int sel = SW ? (it >= per_sel) : 0;
-        const int j = it - sel * per_sel;
-        const GemvTarget& tg = a.tg[SW ? sel : ti];
-        const int64_t gi = (int64_t)tile * per_sel + j;
-        const v4u* src = reinterpret_cast<const v4u*>(tg.data + gi * G);
-        wv[u][0] = __builtin_nontemporal_load(src);
-        if (G == 32) wv[u][G / 16 - 1] = __builtin_nontemporal_load(src + 1);
-        if (WDT == WQ4) wsc[u] = __builtin_nontemporal_load(tg.scales + gi);
-      }
+  // 5. products
+  for (int it = tid, u = 0; it < items; it += kGemvThreads, ++u) {
+    const int sel = SW ? (it >= per_sel) : 0;
+    const int j = it - sel * per_sel;
+    v4u w0, w1;
+    float ws;
+    if (u < 2) {
+      w0 = u ? w[1][0] : w[0][0];
+      w1 = u ? w[1][G / 16 - 1] : w[0][G / 16 - 1];
+      ws = u ? wsc[1] : wsc[0];
+    } else {
+      const GemvTarget& tw = a.tg[SW ? sel : ti];
+      const int64_t gi = (int64_t)tile * per_sel + j;
+      const v4u* src = reinterpret_cast<const v4u*>(tw.data + gi * G);
+      w0 = src[0];
+      w1 = G == 32 ? src[1] : w0;
+      ws = WDT == WQ4 ? tw.scales[gi] : 0.f;
     }
+    const int b = j / H, r = j - b * H;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int it = it0 + u * kGemvThreads + tid;
-      if (it >= items) continue;
+    for (int t = 0; t < NT; ++t)
+      if (t < T)
+        L.p[((sel * NT + t) * H + r) * L.pst + b] =
+            item_product<WDT>(w0, w1, ws, L.q + t * L.kpad + b * kBlock, L.d[t * nb + b], L.s[t * nb + b]);
+  }
+  __syncthreads();
+  gemv_fold<WDT, NT, SW>(a, L, tg, tile, tid, e_res, e_s, e_su);
+}
+
+// Streaming decode GEMV for large weights: pre-quantized activation; all of the tile's items
+// (at most IPT per thread) are loaded at kernel entry, so a full grid keeps the whole matrix in
+// flight.
+template <int WDT, int NT, bool SW, int IPT>
+__global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int G = WDT == WQ8 ? 32 : 16;
+  const int K = a.K, nb = a.nb, T = a.T, H = a.H, tid = threadIdx.x;
+  const GemvLds L = gemv_lds<NT>(smem, K, nb);
+  int ti = 0, tile = blockIdx.x;
+  if (!SW) {
+    while (ti + 1 < a.n_targets && tile >= a.tile_start[ti + 1]) ++ti;
+    tile -= a.tile_start[ti];
+  }
+  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  const int per_sel = H * nb, items = (SW ? 2 : 1) * per_sel;
+
+  v4u w[IPT][G / 16];
+  float wsc[IPT];
+#pragma unroll
+  for (int u = 0; u < IPT; ++u) {
+    const int it = u * kGemvThreads + tid;
+    wsc[u] = 0.f;
+    if (it < items) {
+      const int sel = SW ? (it >= per_sel) : 0;
+      const GemvTarget& tw = a.tg[SW ? sel : ti];
+      const int64_t gi = (int64_t)tile * per_sel + (it - sel * per_sel);
+      const v4u* src = reinterpret_cast<const v4u*>(tw.data + gi * G);
+      w[u][0] = __builtin_nontemporal_load(src);
+      if (G == 32) w[u][G / 16 - 1] = __builtin_nontemporal_load(src + 1);
+      if (WDT == WQ4) wsc[u] = __builtin_nontemporal_load(tw.scales + gi);
+    }
+  }
+  // then the activation (L2-resident; its LDS staging waits for the weights anyway)
+  const int nq16 = T * K / 16, nblk = T * nb;
+  int4 av[kActRegs];
+#pragma unroll
+  for (int m = 0; m < kActRegs; ++m) {
+    const int e = m * kGemvThreads + tid;
+    av[m] = reinterpret_cast<const int4*>(a.xq)[e < nq16 ? e : 0];
+  }
+  float dv[2];
+  int sv[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int e = m * kGemvThreads + tid;
+    dv[m] = a.xd[e < nblk ? e : 0];
+    sv[m] = a.xs[e < nblk ? e : 0];
+  }
+  float e_res = 0.f, e_s = 1.f, e_su = 1.f;
+  {
+    const int ft = tid / H, fn = tile * H + (tid - ft * H);
+    if (tid < T * H && fn < tg.N) {
+      if (WDT == WQ8) {
+        e_s = tg.scales[fn];
+        if (SW) e_su = a.tg[1].scales[fn];
+      }
+      if (!SW && tg.res) e_res = tg.res[(int64_t)ft * tg.N + fn];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kActRegs; ++m) {
+    const int e = m * kGemvThreads + tid;
+    if (e < nq16) {
+      const int t = (e * 16) / K, k = e * 16 - t * K;
+      *reinterpret_cast<int4*>(L.q + t * L.kpad + k) = av[m];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int e = m * kGemvThreads + tid;
+    if (e < nblk) {
+      L.d[e] = dv[m];
+      L.s[e] = sv[m];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < IPT; ++u) {
+    const int it = u * kGemvThreads + tid;
+    if (it < items) {
       const int sel = SW ? (it >= per_sel) : 0;
       const int j = it - sel * per_sel;
       const int b = j / H, r = j - b * H;
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        if (t >= T) break;
-        const int4* aq = reinterpret_cast<const int4*>(s_q + t * kpad + b * kBlock);
-        const int4 a0 = aq[0], a1 = aq[1];
-        float p;
-        if (WDT == WQ8) {
-          const v4u w0 = wv[u][0], w1 = wv[u][G / 16 - 1];
-          int S = sdot4((int)w0.x, a0.x, 0);
-          S = sdot4((int)w0.y, a0.y, S);
-          S = sdot4((int)w0.z, a0.z, S);
-          S = sdot4((int)w0.w, a0.w, S);
-          S = sdot4((int)w1.x, a1.x, S);
-          S = sdot4((int)w1.y, a1.y, S);
-          S = sdot4((int)w1.z, a1.z, S);
-          S = sdot4((int)w1.w, a1.w, S);
-          p = (float)S * s_d[t * nb + b];
-        } else {
-          const v4u w = wv[u][0];
-          // sum_i (nib_i - 8) x_i = sum_i nib_i x_i - 8 * sum_i x_i (nibbles 0..15 are valid int8)
-          int S = -8 * s_s[t * nb + b];
-          S = sdot4((int)(w.x & 0x0F0F0F0Fu), a0.x, S);
-          S = sdot4((int)(w.y & 0x0F0F0F0Fu), a0.y, S);
-          S = sdot4((int)(w.z & 0x0F0F0F0Fu), a0.z, S);
-          S = sdot4((int)(w.w & 0x0F0F0F0Fu), a0.w, S);
-          S = sdot4((int)((w.x >> 4) & 0x0F0F0F0Fu), a1.x, S);
-          S = sdot4((int)((w.y >> 4) & 0x0F0F0F0Fu), a1.y, S);
-          S = sdot4((int)((w.z >> 4) & 0x0F0F0F0Fu), a1.z, S);
-          S = sdot4((int)((w.w >> 4) & 0x0F0F0F0Fu), a1.w, S);
-          p = (float)S * (wsc[u] * s_d[t * nb + b]);
-        }
-        s_p[((sel * NT + t) * H + r) * pst + b] = p;
-      }
+      for (int t = 0; t < NT; ++t)
+        if (t < T)
+          L.p[((sel * NT + t) * H + r) * L.pst + b] = item_product<WDT>(
+              w[u][0], w[u][G / 16 - 1], wsc[u], L.q + t * L.kpad + b * kBlock, L.d[t * nb + b], L.s[t * nb + b]);
     }
   }
   __syncthreads();
-
-  // phase 2: sequential fold per (token, row) and epilogue
-  for (int f = tid; f < T * H; f += kGemvThreads) {
-    const int t = f / H, r = f - t * H;
-    const GemvTarget& tg = a.tg[SW ? 0 : ti];
-    const int n = tile * H + r;
-    if (n >= tg.N) continue;
-    const float* pp = s_p + (t * H + r) * pst;
-    float acc = 0.f;
-#pragma unroll 8
-    for (int b = 0; b < nb; ++b) acc = acc + pp[b];
-    float out = WDT == WQ8 ? acc * tg.scales[n] : acc * 16.0f;
-    if (SW) {
-      const float* pu = s_p + ((NT + t) * H + r) * pst;
-      float accu = 0.f;
-#pragma unroll 8
-      for (int b = 0; b < nb; ++b) accu = accu + pu[b];
-      const float up = WDT == WQ8 ? accu * a.tg[1].scales[n] : accu * 16.0f;
-      out = silu_exact(out) * up;
-    } else if (tg.res) {
-      out = out + tg.res[(int64_t)t * tg.N + n];
-    }
-    tg.y[(int64_t)t * tg.N + n] = out;
-  }
+  gemv_fold<WDT, NT, SW>(a, L, tg, tile, tid, e_res, e_s, e_su);
 }
 
 // ---------------------------------------------------------------- int8 MFMA GEMM (prefill)
@@ -714,32 +882,56 @@ hipError_t launch_act_quant_frag_token(const float* x, int T, int Tpad, int K, i
 int gemv_max_tokens(int K) {
   if (K <= 4096) return 4;
   if (K <= 8192) return 2;
-  return 1;
+  if (K <= 16384) return 1;
+  return 0;
 }
 
 size_t gemv_lds_bytes(int nt, int K, int nb, int H, int nsel) {
   const size_t kpad = (size_t)((K + 15) & ~15);
-  return nt * kpad + (size_t)nt * nb * 8 + (size_t)nsel * nt * H * (nb | 1) * 4;
+  const size_t p = (size_t)((nb + 3) & ~3);
+  const size_t pst = ((p >> 2) & 1) ? p : p + 4;
+  return nt * kpad + (((size_t)nt * nb * 8 + 15) & ~(size_t)15) + (size_t)nsel * nt * H * pst * 4;
 }
 
-template <int WDT, int NT, bool QIN, bool SW>
-static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
-  const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.H, SW ? 2 : 1);
-  if (lds > 64 * 1024) return hipErrorInvalidValue;
-  gemv_a8_kernel<WDT, NT, QIN, SW><<<tiles, kGemvThreads, lds, s>>>(a);
-  return hipGetLastError();
+bool gemv_qin_ok(int T, int K) { return T * K <= 2 * kSmallMaxAct; }
+
+int gemv_stream_ipt(int dtype, int items) {
+  const int per = (items + kGemvThreads - 1) / kGemvThreads;
+  const int cap = dtype == WQ8 ? 8 : 16;
+  if (per > cap) return 0;
+  return per <= 4 ? 4 : per <= 8 ? 8 : 16;
 }
 
 template <int WDT, int NT, bool SW>
-static hipError_t gemv_q(const GemvArgs& a, int tiles, hipStream_t s) {
-  return a.x ? gemv_go<WDT, NT, true, SW>(a, tiles, s) : gemv_go<WDT, NT, false, SW>(a, tiles, s);
+static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
+  const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.H, SW ? 2 : 1);
+  if (lds > 64 * 1024 || a.T > NT) return hipErrorInvalidValue;
+  if (a.x) {
+    if (!gemv_qin_ok(a.T, a.K) || (a.K & 7)) return hipErrorInvalidValue;
+    gemv_small_kernel<WDT, NT, SW><<<tiles, kGemvThreads, lds, s>>>(a);
+    return hipGetLastError();
+  }
+  if (a.T * a.K > kActRegs * kGemvThreads * 16 || a.T * a.nb > 2 * kGemvThreads) return hipErrorInvalidValue;
+  const int items = (SW ? 2 : 1) * a.H * a.nb;
+  switch (gemv_stream_ipt(WDT, items)) {
+    case 4: gemv_stream_kernel<WDT, NT, SW, 4><<<tiles, kGemvThreads, lds, s>>>(a); break;
+    case 8: gemv_stream_kernel<WDT, NT, SW, 8><<<tiles, kGemvThreads, lds, s>>>(a); break;
+    case 16:
+      if (WDT == WQ4) {
+        gemv_stream_kernel<WDT, NT, SW, 16><<<tiles, kGemvThreads, lds, s>>>(a);
+        break;
+      }
+      return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 template <int WDT, bool SW>
 static hipError_t gemv_nt(const GemvArgs& a, int tiles, hipStream_t s) {
-  if (a.T <= 1) return gemv_q<WDT, 1, SW>(a, tiles, s);
-  if (a.T <= 2) return gemv_q<WDT, 2, SW>(a, tiles, s);
-  return gemv_q<WDT, 4, SW>(a, tiles, s);
+  if (a.T <= 1) return gemv_go<WDT, 1, SW>(a, tiles, s);
+  if (a.T <= 2) return gemv_go<WDT, 2, SW>(a, tiles, s);
+  return gemv_go<WDT, 4, SW>(a, tiles, s);
 }
 
 hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_tiles, hipStream_t s) {
