@@ -98,18 +98,22 @@ int choose_H(int dtype, int64_t K) {
   return 4;
 }
 
-// Small-matrix decode path (workgroups quantize x themselves) vs the streaming path.
-bool use_small_gemv(int T, int64_t K) { return K <= 2048 && gemv_qin_ok(T, (int)K); }
+// Small-matrix decode path (workgroups quantize x themselves) vs the streaming path: short rows and
+// at most ~4 MB of weights per launch.
+bool use_small_gemv(int T, int64_t K, size_t bytes = 0) {
+  return K <= 2048 && gemv_qin_ok(T, (int)K) && bytes <= (4u << 20);
+}
 
 bool a8_applies(const DevWeight& w) { return (w.dtype == ELMH_Q8 || w.dtype == ELMH_Q4) && w.cols % kBlock == 0; }
 
-// Largest token count the int8 GEMV takes for these weights, 0 if none.
-int gemv_tokens(const DevWeight& w, int nsel) {
+// Largest token count the int8 GEMV takes for this weight on the small (workgroup-quantized) or the
+// streaming kernel, 0 if none.
+int gemv_tokens(const DevWeight& w, int nsel, bool small) {
   const int K = (int)w.cols, nb = (int)w.nb;
   for (int nt : {4, 2, 1}) {
     if (nt > gemv_max_tokens(K)) continue;
     if (gemv_lds_bytes(nt, K, nb, w.H, nsel) > 64 * 1024) continue;
-    if (!use_small_gemv(nt, K) && gemv_stream_ipt(w.dtype, nsel * w.H * nb) == 0) continue;
+    if (small ? !use_small_gemv(nt, K) : gemv_stream_ipt(w.dtype, nsel * w.H * nb) == 0) continue;
     return nt;
   }
   return 0;
@@ -127,25 +131,41 @@ int check_targets(elmh_ctx* c, int T, int64_t K, int n, elmh_weight* const* w, f
 
 // ---------------------------------------------------------------- device-pointer dispatch
 
+// Tiles per workgroup of the streaming GEMV: enough items to fill the registers (q8 ~4, q4 ~8 per
+// thread) while keeping at least two workgroups per CU.
+int stream_tpw(const DevWeight& w, int T, int tiles_total, int nsel) {
+  const int per_tile = nsel * w.H * (int)w.nb;
+  const int target = kGemvThreads * (w.dtype == ELMH_Q8 ? 4 : 8);
+  int tpw = std::max(1, target / per_tile);
+  tpw = std::min(tpw, std::max(1, tiles_total / 512));
+  while (tpw > 1 && (T * tpw * w.H > kGemvThreads || gemv_stream_ipt(w.dtype, tpw * per_tile) == 0 ||
+                     gemv_lds_bytes(T, (int)w.cols, (int)w.nb, tpw * w.H, nsel) > 64 * 1024))
+    --tpw;
+  return tpw;
+}
+
 int run_gemv_group(elmh_ctx* c, const float* x, const int8_t* xq, const float* xd, const int32_t* xs, int T,
                    int64_t K, const std::vector<int>& idx, elmh_weight* const* w, float* const* y,
                    const float* const* res) {
   for (size_t i0 = 0; i0 < idx.size(); i0 += kMaxTargets) {
     GemvArgs a{};
     const size_t n = std::min<size_t>(kMaxTargets, idx.size() - i0);
-    int tiles = 0;
     const DevWeight& w0 = w[idx[i0]]->w;
+    int all_tiles = 0;
+    for (size_t j = 0; j < n; ++j) all_tiles += (int)(w[idx[i0 + j]]->w.rows_pad / w0.H);
+    a.tpw = x ? 1 : stream_tpw(w0, T, all_tiles, 1);
+    int wgs = 0;
     a.H = w0.H;
     for (size_t j = 0; j < n; ++j) {
       const DevWeight& wd = w[idx[i0 + j]]->w;
-      a.tg[j] = {wd.data, wd.scales, y[idx[i0 + j]], res ? res[idx[i0 + j]] : nullptr, (int)wd.rows,
-                 (int)(wd.rows_pad / wd.H)};
-      a.tile_start[j] = tiles;
-      tiles += a.tg[j].tiles;
+      const int tiles = (int)(wd.rows_pad / wd.H);
+      a.tg[j] = {wd.data, wd.scales, y[idx[i0 + j]], res ? res[idx[i0 + j]] : nullptr, (int)wd.rows, tiles};
+      a.tile_start[j] = wgs;
+      wgs += (tiles + a.tpw - 1) / a.tpw;
     }
-    a.tile_start[n] = tiles;
+    a.tile_start[n] = wgs;
     a.n_targets = (int)n;
-    a.total_tiles = tiles;
+    a.total_tiles = wgs;
     a.x = x;
     a.xq = xq;
     a.xd = xd;
@@ -153,7 +173,7 @@ int run_gemv_group(elmh_ctx* c, const float* x, const int8_t* xq, const float* x
     a.T = T;
     a.K = (int)K;
     a.nb = (int)(K / kBlock);
-    HIP_OR_FAIL(c, launch_gemv_a8(w0.dtype, 0, a, tiles, c->stream));
+    HIP_OR_FAIL(c, launch_gemv_a8(w0.dtype, 0, a, wgs, c->stream));
   }
   return ELMH_OK;
 }
@@ -270,10 +290,12 @@ int run_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight
         return rc;
     return ELMH_OK;
   }
+  size_t bytes = 0;
+  for (int i = 0; i < n; ++i) bytes += w[i]->w.data_bytes + w[i]->w.scale_bytes;
+  const bool qin = use_small_gemv(T, K, bytes);  // small rows: each workgroup quantizes x itself
   int nt = 4;
-  for (int i = 0; i < n; ++i) nt = std::min(nt, gemv_tokens(w[i]->w, 1));
+  for (int i = 0; i < n; ++i) nt = std::min(nt, gemv_tokens(w[i]->w, 1, qin));
   if (T <= nt) {
-    const bool qin = use_small_gemv(T, K);  // small rows: each workgroup quantizes x itself
     if (!qin && (rc = quant_rows(c, x, T, K))) return rc;
     for (const auto& g : groups)
       if ((rc = run_gemv_group(c, qin ? x : nullptr, qin ? nullptr : (const int8_t*)c->xq.p,
@@ -328,10 +350,10 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
     HIP_OR_FAIL(c, launch_f32act(g.dtype, 1, a, groups, c->stream));
     return ELMH_OK;
   }
-  const int nt = gemv_tokens(g, 2);
+  const bool qin = use_small_gemv(T, K, g.data_bytes + g.scale_bytes + u.data_bytes + u.scale_bytes);
+  const int nt = gemv_tokens(g, 2, qin);
   if (act == ELMH_ACT_INT8 && T <= nt) {
     GemvArgs a{};
-    const bool qin = use_small_gemv(T, K);
     if (!qin && (rc = quant_rows(c, x, T, K))) return rc;
     const int tiles = (int)(g.rows_pad / g.H);
     a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, tiles};
@@ -339,6 +361,7 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
     a.n_targets = 2;
     a.total_tiles = tiles;
     a.H = g.H;
+    a.tpw = 1;
     a.x = qin ? x : nullptr;
     a.xq = qin ? nullptr : (const int8_t*)c->xq.p;
     a.xd = qin ? nullptr : (const float*)c->xd.p;
@@ -585,7 +608,7 @@ int elmh_gemv_a8_dev(elmh_ctx* c, const int8_t* q, const float* d, const int32_t
   for (int i = 0; i < n; ++i)
     if (!a8_applies(w[i]->w)) return fail(c, ELMH_ERR_ARG, "target %d: int8 GEMV needs K %% 32 == 0", i);
   int nt = 4;
-  for (int i = 0; i < n; ++i) nt = std::min(nt, gemv_tokens(w[i]->w, 1));
+  for (int i = 0; i < n; ++i) nt = std::min(nt, gemv_tokens(w[i]->w, 1, false));
   if (T > nt) return fail(c, ELMH_ERR_UNSUPPORTED, "int8 GEMV takes at most %d tokens at K=%lld", nt, (long long)K);
   DeviceGuard g(c);
   for (const auto& grp : by_dtype(n, w))

@@ -52,6 +52,7 @@ struct GemvArgs {
   int n_targets;
   int total_tiles;
   int H;
+  int tpw;            // tiles per workgroup (streaming kernel; tile_start then counts workgroups)
   const float* x;     // f32 [T][K] (quantized inside each workgroup) or null
   const int8_t* xq;   // int8 [T][K] row-major (pre-quantized) when x is null
   const float* xd;    // f32 [T][nb]

@@ -197,17 +197,31 @@ __device__ __forceinline__ float item_product(const v4u w0, const v4u w1, float 
   return (float)S * (wsc * xd);
 }
 
-// Sequential block-order fold of one LDS row of products.
+// Sequential block-order fold of one LDS row of products. The next 16 values are read while the
+// current 16 are added, so long rows (448 blocks at K = 14336) do not wait on LDS every step.
 __device__ __forceinline__ float fold_row(const float* row, int nb) {
   const float4* pv = reinterpret_cast<const float4*>(row);
   float acc = 0.f;
   const int nq = nb >> 2;
-  for (int q = 0; q < nq; ++q) {
+  int q = 0;
+  if (nq >= 4) {
+    float4 c0 = pv[0], c1 = pv[1], c2 = pv[2], c3 = pv[3];
+    for (q = 4; q + 4 <= nq; q += 4) {
+      const float4 n0 = pv[q], n1 = pv[q + 1], n2 = pv[q + 2], n3 = pv[q + 3];
+      acc = acc + c0.x; acc = acc + c0.y; acc = acc + c0.z; acc = acc + c0.w;
+      acc = acc + c1.x; acc = acc + c1.y; acc = acc + c1.z; acc = acc + c1.w;
+      acc = acc + c2.x; acc = acc + c2.y; acc = acc + c2.z; acc = acc + c2.w;
+      acc = acc + c3.x; acc = acc + c3.y; acc = acc + c3.z; acc = acc + c3.w;
+      c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+    }
+    acc = acc + c0.x; acc = acc + c0.y; acc = acc + c0.z; acc = acc + c0.w;
+    acc = acc + c1.x; acc = acc + c1.y; acc = acc + c1.z; acc = acc + c1.w;
+    acc = acc + c2.x; acc = acc + c2.y; acc = acc + c2.z; acc = acc + c2.w;
+    acc = acc + c3.x; acc = acc + c3.y; acc = acc + c3.z; acc = acc + c3.w;
+  }
+  for (; q < nq; ++q) {
     const float4 v = pv[q];
-    acc = acc + v.x;
-    acc = acc + v.y;
-    acc = acc + v.z;
-    acc = acc + v.w;
+    acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
   }
   for (int b = nq * 4; b < nb; ++b) acc = acc + row[b];
   return acc;
@@ -233,24 +247,40 @@ __device__ __forceinline__ GemvLds gemv_lds(unsigned char* smem, int K, int nb) 
   return L;
 }
 
-// Phase 3 of both GEMV kernels: fold and epilogue for lane tid < T*H.
+// Last phase of both GEMV kernels: lane tid < T*R folds row (tid % R) of token (tid / R), where
+// the workgroup's R rows start at weight row n0, and applies the epilogue.
 template <int WDT, int NT, bool SW>
-__device__ __forceinline__ void gemv_fold(const GemvArgs& a, const GemvLds& L, const GemvTarget& tg, int tile, int tid,
-                                          float e_res, float e_s, float e_su) {
-  const int H = a.H, T = a.T;
-  const int ft = tid / H, fr = tid - ft * H;
-  const int fn = tile * H + fr;
-  if (tid >= T * H || fn >= tg.N) return;
-  float out = fold_row(L.p + (ft * H + fr) * L.pst, a.nb);
+__device__ __forceinline__ void gemv_fold(const GemvArgs& a, const GemvLds& L, const GemvTarget& tg, int n0, int R,
+                                          int rows, int tid, float e_res, float e_s, float e_su) {
+  const int ft = tid / R, fr = tid - ft * R;
+  const int fn = n0 + fr;
+  if (tid >= a.T * R || fr >= rows || fn >= tg.N) return;
+  float out = fold_row(L.p + (ft * R + fr) * L.pst, a.nb);
   out = WDT == WQ8 ? out * e_s : out * 16.0f;
   if (SW) {
-    float up = fold_row(L.p + ((NT + ft) * H + fr) * L.pst, a.nb);
+    float up = fold_row(L.p + ((NT + ft) * R + fr) * L.pst, a.nb);
     up = WDT == WQ8 ? up * e_su : up * 16.0f;
     out = silu_exact(out) * up;
   } else if (tg.res) {
     out = out + e_res;
   }
   tg.y[(int64_t)ft * tg.N + fn] = out;
+}
+
+// Epilogue operands (row scale, residual) of a folding lane, loaded early.
+template <int WDT, bool SW>
+__device__ __forceinline__ void gemv_epilogue_operands(const GemvArgs& a, const GemvTarget& tg, int n0, int R, int rows,
+                                                       int tid, float& e_res, float& e_s, float& e_su) {
+  e_res = 0.f;
+  e_s = e_su = 1.f;
+  const int ft = tid / R, fr = tid - ft * R, fn = n0 + fr;
+  if (tid < a.T * R && fr < rows && fn < tg.N) {
+    if (WDT == WQ8) {
+      e_s = tg.scales[fn];
+      if (SW) e_su = a.tg[1].scales[fn];
+    }
+    if (!SW && tg.res) e_res = tg.res[(int64_t)ft * tg.N + fn];
+  }
 }
 
 // Small decode GEMV: x quantized inside the workgroup (8 elements per thread, 4 threads per
@@ -296,17 +326,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
     }
   }
   // 3. epilogue operands of the folding lanes
-  float e_res = 0.f, e_s = 1.f, e_su = 1.f;
-  {
-    const int ft = tid / H, fn = tile * H + (tid - ft * H);
-    if (tid < T * H && fn < tg.N) {
-      if (WDT == WQ8) {
-        e_s = tg.scales[fn];
-        if (SW) e_su = a.tg[1].scales[fn];
-      }
-      if (!SW && tg.res) e_res = tg.res[(int64_t)ft * tg.N + fn];
-    }
-  }
+  float e_res, e_s, e_su;
+  gemv_epilogue_operands<WDT, SW>(a, tg, tile * H, H, H, tid, e_res, e_s, e_su);
   // 4. quantize: block g = e0 / 32 spread over 4 consecutive lanes
   for (int pass = 0; pass * kSmallMaxAct < nel; ++pass) {
     const int e = pass * kSmallMaxAct + e0;
@@ -373,25 +394,30 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
             item_product<WDT>(w0, w1, ws, L.q + t * L.kpad + b * kBlock, L.d[t * nb + b], L.s[t * nb + b]);
   }
   __syncthreads();
-  gemv_fold<WDT, NT, SW>(a, L, tg, tile, tid, e_res, e_s, e_su);
+  gemv_fold<WDT, NT, SW>(a, L, tg, tile * H, H, H, tid, e_res, e_s, e_su);
 }
 
-// Streaming decode GEMV for large weights: pre-quantized activation; all of the tile's items
-// (at most IPT per thread) are loaded at kernel entry, so a full grid keeps the whole matrix in
-// flight.
+// Streaming decode GEMV for large weights: pre-quantized activation; a workgroup takes a.tpw
+// consecutive H-row tiles (one contiguous chunk) and loads all of its items (at most IPT per
+// thread) at kernel entry, so a full grid keeps the whole matrix in flight.
 template <int WDT, int NT, bool SW, int IPT>
 __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int G = WDT == WQ8 ? 32 : 16;
   const int K = a.K, nb = a.nb, T = a.T, H = a.H, tid = threadIdx.x;
   const GemvLds L = gemv_lds<NT>(smem, K, nb);
-  int ti = 0, tile = blockIdx.x;
+  int ti = 0, wg = blockIdx.x;
   if (!SW) {
-    while (ti + 1 < a.n_targets && tile >= a.tile_start[ti + 1]) ++ti;
-    tile -= a.tile_start[ti];
+    while (ti + 1 < a.n_targets && wg >= a.tile_start[ti + 1]) ++ti;
+    wg -= a.tile_start[ti];
   }
   const GemvTarget& tg = a.tg[SW ? 0 : ti];
-  const int per_sel = H * nb, items = (SW ? 2 : 1) * per_sel;
+  const int tile0 = wg * a.tpw;
+  const int ntl = min(a.tpw, tg.tiles - tile0);
+  const int R = a.tpw * H;      // LDS row slots per token
+  const int rows = ntl * H;     // rows this workgroup owns
+  const int per_tile = H * nb, per_sel = ntl * per_tile, items = (SW ? 2 : 1) * per_sel;
+  const int64_t base = (int64_t)tile0 * per_tile;
 
   v4u w[IPT][G / 16];
   float wsc[IPT];
@@ -402,7 +428,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
     if (it < items) {
       const int sel = SW ? (it >= per_sel) : 0;
       const GemvTarget& tw = a.tg[SW ? sel : ti];
-      const int64_t gi = (int64_t)tile * per_sel + (it - sel * per_sel);
+      const int64_t gi = base + (it - sel * per_sel);
       const v4u* src = reinterpret_cast<const v4u*>(tw.data + gi * G);
       w[u][0] = __builtin_nontemporal_load(src);
       if (G == 32) w[u][G / 16 - 1] = __builtin_nontemporal_load(src + 1);
@@ -425,17 +451,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
     dv[m] = a.xd[e < nblk ? e : 0];
     sv[m] = a.xs[e < nblk ? e : 0];
   }
-  float e_res = 0.f, e_s = 1.f, e_su = 1.f;
-  {
-    const int ft = tid / H, fn = tile * H + (tid - ft * H);
-    if (tid < T * H && fn < tg.N) {
-      if (WDT == WQ8) {
-        e_s = tg.scales[fn];
-        if (SW) e_su = a.tg[1].scales[fn];
-      }
-      if (!SW && tg.res) e_res = tg.res[(int64_t)ft * tg.N + fn];
-    }
-  }
+  float e_res, e_s, e_su;
+  gemv_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
 #pragma unroll
   for (int m = 0; m < kActRegs; ++m) {
     const int e = m * kGemvThreads + tid;
@@ -458,17 +475,18 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
     const int it = u * kGemvThreads + tid;
     if (it < items) {
       const int sel = SW ? (it >= per_sel) : 0;
-      const int j = it - sel * per_sel;
-      const int b = j / H, r = j - b * H;
+      const int jj = it - sel * per_sel;
+      const int st = jj / per_tile, j2 = jj - st * per_tile;
+      const int b = j2 / H, r = st * H + (j2 - b * H);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         if (t < T)
-          L.p[((sel * NT + t) * H + r) * L.pst + b] = item_product<WDT>(
+          L.p[((sel * NT + t) * R + r) * L.pst + b] = item_product<WDT>(
               w[u][0], w[u][G / 16 - 1], wsc[u], L.q + t * L.kpad + b * kBlock, L.d[t * nb + b], L.s[t * nb + b]);
     }
   }
   __syncthreads();
-  gemv_fold<WDT, NT, SW>(a, L, tg, tile, tid, e_res, e_s, e_su);
+  gemv_fold<WDT, NT, SW>(a, L, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
 }
 
 // ---------------------------------------------------------------- int8 MFMA GEMM (prefill)
@@ -904,7 +922,7 @@ int gemv_stream_ipt(int dtype, int items) {
 
 template <int WDT, int NT, bool SW>
 static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
-  const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.H, SW ? 2 : 1);
+  const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.x ? a.H : a.tpw * a.H, SW ? 2 : 1);
   if (lds > 64 * 1024 || a.T > NT) return hipErrorInvalidValue;
   if (a.x) {
     if (!gemv_qin_ok(a.T, a.K) || (a.K & 7)) return hipErrorInvalidValue;
@@ -912,7 +930,8 @@ static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
     return hipGetLastError();
   }
   if (a.T * a.K > kActRegs * kGemvThreads * 16 || a.T * a.nb > 2 * kGemvThreads) return hipErrorInvalidValue;
-  const int items = (SW ? 2 : 1) * a.H * a.nb;
+  if (a.tpw < 1 || a.T * a.tpw * a.H > kGemvThreads) return hipErrorInvalidValue;
+  const int items = (SW ? 2 : 1) * a.tpw * a.H * a.nb;
   switch (gemv_stream_ipt(WDT, items)) {
     case 4: gemv_stream_kernel<WDT, NT, SW, 4><<<tiles, kGemvThreads, lds, s>>>(a); break;
     case 8: gemv_stream_kernel<WDT, NT, SW, 8><<<tiles, kGemvThreads, lds, s>>>(a); break;
