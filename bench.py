@@ -270,6 +270,58 @@ def gemm_bench(ctx, E, T, shapes, dt=1, act=None, reps=10):
     return out
 
 
+def e2e_bench(path_dir, P=128, G=64, reps=3, cpu_reference=True):
+    """random-init SmolLM2-135M (q4 g32 + q8 embedding, int8 activations) through this
+    build's Session with backends hip,cpu; edgelm's bench protocol (main.cpp:173-233): LCG prompt,
+    warm-up rep, then the median of `reps` reps of prefill + argmax (TTFT) + G greedy decodes."""
+    from edgelm_amd import elm_format as F
+    from edgelm_amd import host
+    path = os.path.join(path_dir, "smollm2-135m-random.q4.elm")
+    t0 = time.time()
+    F.write_elm(path, F.SMOLLM2_135M, F.random_weights(F.SMOLLM2_135M, 20260101), "q4", embed_dtype="q8")
+    log(f"e2e model written in {time.time() - t0:.1f}s ({os.path.getsize(path) / 1e6:.1f} MB)")
+    prompt = F.lcg_prompt(P, 49152)
+    threads = min(8, os.cpu_count() or 1)
+    m = host.Model(path)
+    s = host.Session(m, "hip,cpu", threads=threads, max_ctx=P + G + 8, max_batch=P, act_quant=True)
+    runs = [s.generate(prompt, G) for _ in range(reps + 1)][1:]
+    med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731
+    out = {"prefill_tok_s": med([P / (r["prefill_ms"] / 1e3) for r in runs]), "ttft_ms": med([r["ttft_ms"] for r in runs]),
+           "decode_tok_s": med([G / (r["decode_ms"] / 1e3) for r in runs]), "prompt": P, "gen": G,
+           "host_threads": threads, "backends": "hip,cpu", "greedy_tokens_head": [int(t) for t in runs[0]["tokens"][:8]]}
+    s.close()
+    log(f"e2e: prefill {out['prefill_tok_s']:.1f} tok/s, TTFT {out['ttft_ms']:.2f} ms, decode {out['decode_tok_s']:.1f} tok/s")
+    if cpu_reference:
+        import oracle as O
+        if O.ref_available():
+            ct = min(16, os.cpu_count() or 1)
+            r = O.RefSession(path, "cpu", threads=ct, max_ctx=P + G + 8, max_batch=P, act_quant=True)
+            def gen_ref():
+                r.reset()
+                t0 = time.perf_counter()
+                lg = r.forward(prompt)
+                t1 = time.perf_counter()
+                tok = int(np.argmax(lg[-1]))
+                t2 = time.perf_counter()
+                toks = [tok]
+                for _ in range(G):
+                    tok = int(np.argmax(r.forward(np.array([tok], np.int32))[-1]))
+                    toks.append(tok)
+                t3 = time.perf_counter()
+                return (t1 - t0) * 1e3, (t2 - t0) * 1e3, (t3 - t2) * 1e3, toks
+            gen_ref()
+            pm, tm, dm, toks = gen_ref()
+            out["cpu_reference"] = {"prefill_tok_s": P / (pm / 1e3), "ttft_ms": tm, "decode_tok_s": G / (dm / 1e3),
+                                    "threads": ct, "kind": "reference",
+                                    "greedy_tokens_match": toks == [int(t) for t in runs[0]["tokens"]]}
+            r.close()
+            log(f"e2e cpu (edgelm cpu backend, {ct} threads): prefill {out['cpu_reference']['prefill_tok_s']:.1f} tok/s, "
+                f"decode {out['cpu_reference']['decode_tok_s']:.1f} tok/s, tokens match: "
+                f"{out['cpu_reference']['greedy_tokens_match']}")
+    os.remove(path)
+    return out
+
+
 def cpu_baseline(budget_s=12.0):
     """edgelm's own cpu backend (oracle/_ref) on this host: the same W4A8 decode-step matmuls."""
     import oracle as O
@@ -340,6 +392,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-8b", action="store_true", help="skip the 8B-shaped sweep")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMMs")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end SmolLM2 session")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -358,6 +411,12 @@ def main():
         sm = [(D + 2 * KV, D), (HID, D), (D, HID), (VOCAB, D)]
         extra["gemm_w8a8_T128"] = gemm_bench(ctx, E, 128, sm)
         extra["gemm_w8a8_T512_8b"] = gemm_bench(ctx, E, 512, [(4096, 4096), (14336, 4096), (4096, 14336)])
+    if not args.no_e2e:
+        import tempfile
+        ctx.close()  # the session opens its own context
+        with tempfile.TemporaryDirectory() as d:
+            extra["e2e_smollm2_w4a8"] = e2e_bench(d, cpu_reference=not args.no_cpu)
+        ctx = E.Context(0)
     # dominant kernel of the headline step: largest total time per step
     dom_name, dom = max(per.items(), key=lambda kv: kv[1]["us"] * kv[1]["calls_per_step"])
     roof = {"kernel": dom_name, "bound": "hbm", "achieved": round(dom["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

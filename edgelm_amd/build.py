@@ -16,6 +16,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "edgelm_amd")
 CSRC = os.path.join(PKG, "csrc")
 HOST = os.path.join(PKG, "host")
+HOST_INC = os.path.join(HOST, "include")
 LIB = os.path.join(PKG, "lib")
 OBJ = os.path.join(PKG, "_build")
 INC = os.path.join(ROOT, "include")
@@ -32,8 +33,10 @@ HIP_FLAGS = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
     f"-I{INC}", f"-I{CSRC}",
 ]
+# Host code: the reference's default build (-O2/-O3, no -march) keeps the x86-64 baseline ISA (SSE2, no
+# FMA), so host float arithmetic rounds like edgelm's scalar path; contraction stays off regardless.
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wextra", "-pthread", f"-I{INC}",
-              f"-I{HOST}"]
+              f"-I{HOST_INC}"]
 
 ELMH_SRCS = ["elmh_kernels.hip", "elmh_api.cpp"]
 

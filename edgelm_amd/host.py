@@ -46,3 +46,130 @@ def quantize_q4(w, threads=0):
     lib().elm_quantize_q4(C.c_void_p(w.ctypes.data), C.c_int64(n), C.c_int64(k), C.c_void_p(q.ctypes.data),
                           C.c_void_p(s.ctypes.data), C.c_int(_threads(threads)))
     return q, s
+
+
+# ------------------------------------------------------------------ models and sessions
+
+def _err():
+    return lib().elm_last_error().decode()
+
+
+def _setup():
+    L = lib()
+    if getattr(L, "_elm_typed", False):
+        return L
+    L.elm_last_error.restype = C.c_char_p
+    L.elm_model_load.restype = C.c_void_p
+    L.elm_model_load.argtypes = [C.c_char_p]
+    L.elm_model_free.argtypes = [C.c_void_p]
+    L.elm_session_create.restype = C.c_void_p
+    L.elm_session_create.argtypes = [C.c_void_p, C.c_char_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+    L.elm_session_destroy.argtypes = [C.c_void_p]
+    for f in ("elm_session_forward", "elm_session_prefill"):
+        getattr(L, f).argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
+    L.elm_session_reset.argtypes = [C.c_void_p]
+    L.elm_session_pos.argtypes = [C.c_void_p]
+    L.elm_session_describe.argtypes = [C.c_void_p, C.c_char_p, C.c_int]
+    L.elm_session_generate.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_double),
+                                       C.POINTER(C.c_double), C.POINTER(C.c_double), C.c_void_p]
+    L.elm_model_config.argtypes = [C.c_void_p, C.c_void_p]
+    L.elm_model_fusion.argtypes = [C.c_void_p, C.c_void_p]
+    L.elm_model_plan.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]
+    L.elm_model_partition.argtypes = [C.c_void_p, C.c_char_p, C.c_int, C.c_char_p, C.c_int]
+    L._elm_typed = True
+    return L
+
+
+class Model:
+    """An .elm file loaded (memory-mapped) by the host library."""
+
+    def __init__(self, path):
+        L = _setup()
+        self.h = L.elm_model_load(path.encode())
+        if not self.h:
+            raise RuntimeError(_err())
+        cfg = np.zeros(10, np.int32)
+        L.elm_model_config(self.h, cfg.ctypes.data)
+        keys = ["vocab", "dim", "hidden", "n_layers", "n_heads", "n_kv_heads", "head_dim", "max_seq", "dtype", "tied"]
+        self.cfg = dict(zip(keys, (int(v) for v in cfg)))
+
+    def fusion(self):
+        o = np.zeros(6, np.int32)
+        if _setup().elm_model_fusion(self.h, o.ctypes.data):
+            raise RuntimeError(_err())
+        return dict(zip(["swiglu", "shared_input", "residual", "rope", "ops_before", "ops_after"], (int(v) for v in o)))
+
+    def plan(self, T, L=1, fuse=True):
+        a, n = C.c_int64(), C.c_int64()
+        rc = _setup().elm_model_plan(self.h, int(fuse), T, L, C.byref(a), C.byref(n))
+        if rc < 0:
+            raise RuntimeError(_err())
+        return bool(rc), a.value, n.value
+
+    def partition(self, backends, fuse=True):
+        buf = C.create_string_buffer(4096)
+        n = _setup().elm_model_partition(self.h, backends.encode(), int(fuse), buf, 4096)
+        if n < 0:
+            raise RuntimeError(_err())
+        return n, buf.value.decode()
+
+    def close(self):
+        if self.h:
+            _setup().elm_model_free(self.h)
+            self.h = None
+
+
+class Session:
+    """edgelm Session on this build's runtime: backends e.g. "hip,cpu" (reference appended last)."""
+
+    def __init__(self, model, backends="hip,cpu", threads=1, max_ctx=256, max_batch=128, all_logits=False,
+                 act_quant=False, fuse=True):
+        L = _setup()
+        self.model = model
+        self.vocab = model.cfg["vocab"]
+        self.all_logits = all_logits
+        self.max_batch = max_batch
+        self.h = L.elm_session_create(model.h, backends.encode(), threads, max_ctx, max_batch, int(all_logits),
+                                      int(act_quant), int(fuse))
+        if not self.h:
+            raise RuntimeError(_err())
+
+    def forward(self, tokens):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        rows = len(tokens) if self.all_logits else 1
+        out = np.empty((rows, self.vocab), np.float32)
+        if _setup().elm_session_forward(self.h, tokens.ctypes.data, len(tokens), out.ctypes.data):
+            raise RuntimeError(_err())
+        return out
+
+    def reset(self):
+        _setup().elm_session_reset(self.h)
+
+    def pos(self):
+        return _setup().elm_session_pos(self.h)
+
+    def describe(self):
+        buf = C.create_string_buffer(4096)
+        n = _setup().elm_session_describe(self.h, buf, 4096)
+        return n, buf.value.decode()
+
+    def generate(self, prompt, gen):
+        """edgelm's bench protocol: prefill, argmax (TTFT), `gen` greedy decode steps."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        pm, tm, dm = C.c_double(), C.c_double(), C.c_double()
+        toks = np.empty(gen + 1, np.int32)
+        if _setup().elm_session_generate(self.h, prompt.ctypes.data, len(prompt), gen, C.byref(pm), C.byref(tm),
+                                         C.byref(dm), toks.ctypes.data):
+            raise RuntimeError(_err())
+        return dict(prefill_ms=pm.value, ttft_ms=tm.value, decode_ms=dm.value, tokens=toks)
+
+    def close(self):
+        if self.h:
+            _setup().elm_session_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,75 @@
+// Delegate interface (reference include/edgelm/backend.hpp:15-51): a backend declares the ops it
+// supports; the partitioner gives each op to the first backend in preference order that claims it
+// and groups consecutive ops into partitions. The names, members and semantics are edgelm's, so the
+// `hip` backend of this build plugs into edgelm's Session unchanged.
+#pragma once
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "edgelm/graph.hpp"
+
+namespace edgelm {
+
+class ThreadPool;
+
+struct RopeTable {
+  int half = 0, max_pos = 0;
+  std::vector<float> cos, sin;  // [pos][half]
+  RopeTable() = default;
+  RopeTable(int head_dim, int max_pos, float theta);
+};
+
+struct KVLayer {  // one layer's cache, [kv_head][pos][head_dim]
+  float* k = nullptr;
+  float* v = nullptr;
+  int max_ctx = 0;
+};
+
+constexpr int kActBlock = 32;
+struct ActBuf {
+  int8_t* q = nullptr;  // [T, K]
+  float* d = nullptr;   // [T, K/32]
+};
+
+struct ExecContext {
+  const Graph* graph = nullptr;
+  std::vector<float*> ptr;  // activation tensor -> host arena address
+  int T = 0, L = 0, pos0 = 0;
+  std::vector<KVLayer> kv;
+  const RopeTable* rope = nullptr;
+  ThreadPool* pool = nullptr;
+  std::vector<float*> scratch;
+  bool act_quant = false;  // int8 activations for q8/q4 matmuls
+  ActBuf aq;               // host scratch the cpu matmuls use; the hip backend ignores it
+  const Tensor& tensor(int i) const { return graph->tensors[i]; }
+  float* f(int i) const { return ptr[i]; }
+  int64_t rows(int i) const;
+};
+
+class Backend {
+ public:
+  virtual ~Backend() = default;
+  virtual const char* name() const = 0;
+  virtual bool supports(const Graph& g, const Op& op) const = 0;
+  virtual void run(const Op& op, ExecContext& ctx) = 0;
+};
+
+std::unique_ptr<Backend> make_reference_backend();
+std::unique_ptr<Backend> make_cpu_backend();
+// The MI355X delegate: MATMUL / MATMUL_N / MATMUL_ADD / FFN_SWIGLU with q8 or q4 weights.
+// Throws if no gfx950 device is usable.
+std::unique_ptr<Backend> make_hip_backend(int device = 0);
+// Same claims as the hip backend but no device: for partition inspection only (run() throws).
+std::unique_ptr<Backend> make_hip_planning_backend();
+std::unique_ptr<Backend> make_backend(const std::string& name);
+
+struct Partition {
+  Backend* backend = nullptr;
+  int begin = 0, end = 0;  // op range [begin, end)
+};
+
+std::vector<Partition> partition_graph(const Graph& g, const std::vector<Backend*>& preference);
+std::string describe_partitions(const Graph& g, const std::vector<Partition>& parts);
+
+}  // namespace edgelm

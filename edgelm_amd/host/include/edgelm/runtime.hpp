@@ -1,0 +1,81 @@
+// Session (reference include/edgelm/runtime.hpp:17-67): a fused, partitioned, memory-planned
+// instance of a model's graph with a preallocated KV cache; forward() runs T tokens through the
+// partitions in op order. The MATMUL family goes to the `hip` backend; the remaining ops run on the
+// host ("cpu" / "reference" backends of this build, which carry no quantized-matmul code at all).
+#pragma once
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "edgelm/backend.hpp"
+#include "edgelm/model.hpp"
+
+namespace edgelm {
+
+// Graph passes (reference passes.hpp:12-38).
+int fuse_swiglu(Graph& g);
+int fuse_shared_input(Graph& g);
+int fuse_residual(Graph& g);
+int fuse_rope_attention(Graph& g);
+struct FusionStats {
+  int swiglu = 0, shared_input = 0, residual = 0, rope = 0;
+  size_t ops_before = 0, ops_after = 0;
+};
+FusionStats optimize(Graph& g);
+
+struct MemoryPlan {
+  std::vector<int64_t> offset, bytes;
+  std::vector<int> first, last;
+  size_t arena_bytes = 0, naive_bytes = 0;
+  int n_planned = 0;
+};
+MemoryPlan plan_memory(const Graph& g, int T, int L);
+bool plan_is_valid(const MemoryPlan& p);
+
+struct SessionOptions {
+  std::vector<std::string> backends{"hip", "cpu"};  // preference order; reference is appended last
+  int threads = 1;
+  int max_ctx = 1024;
+  int max_batch = 128;
+  bool all_logits = false;
+  bool fuse = true;
+  bool act_quant = false;
+};
+
+class Session {
+ public:
+  Session(const Model& model, SessionOptions opt);
+  ~Session();
+  Session(const Session&) = delete;
+  Session& operator=(const Session&) = delete;
+
+  const float* forward(const int32_t* tokens, int n);
+  const float* prefill(const std::vector<int32_t>& tokens);
+  const float* decode(int32_t token) { return forward(&token, 1); }
+  void reset() { pos_ = 0; }
+  int pos() const { return pos_; }
+
+  const Graph& graph() const { return graph_; }
+  const std::vector<Partition>& partitions() const { return parts_; }
+  const MemoryPlan& plan() const { return plan_; }
+  const SessionOptions& options() const { return opt_; }
+  int vocab() const { return model_.cfg.vocab; }
+
+ private:
+  const Model& model_;
+  SessionOptions opt_;
+  Graph graph_;
+  MemoryPlan plan_;
+  std::vector<std::unique_ptr<Backend>> backends_;
+  std::vector<Partition> parts_;
+  std::unique_ptr<ThreadPool> pool_;
+  std::vector<uint8_t> arena_;
+  std::vector<float> kcache_, vcache_;
+  RopeTable rope_;
+  ExecContext ctx_;
+  int pos_ = 0;
+};
+
+int32_t argmax(const float* logits, int n);
+
+}  // namespace edgelm

@@ -1,0 +1,199 @@
+// C API of the host library (include/edgelm_host.h) for callers that are not C++.
+#include <chrono>
+#include <cstring>
+#include <string>
+
+#include "edgelm/runtime.hpp"
+#include "edgelm_host.h"
+
+using namespace edgelm;
+
+struct elm_model {
+  Model m;
+};
+struct elm_session {
+  std::unique_ptr<Session> s;
+};
+
+namespace {
+thread_local std::string g_err;
+
+std::vector<std::string> split(const char* csv) {
+  std::vector<std::string> out;
+  std::string cur;
+  for (const char* p = csv ? csv : ""; *p; ++p) {
+    if (*p == ',') {
+      if (!cur.empty()) out.push_back(cur);
+      cur.clear();
+    } else {
+      cur += *p;
+    }
+  }
+  if (!cur.empty()) out.push_back(cur);
+  return out;
+}
+
+template <class F>
+int guard(F&& f) {
+  try {
+    return f();
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
+void copy_text(const std::string& s, char* buf, int cap) {
+  if (!buf || cap <= 0) return;
+  std::strncpy(buf, s.c_str(), static_cast<size_t>(cap) - 1);
+  buf[cap - 1] = 0;
+}
+
+double ms_between(std::chrono::steady_clock::time_point a, std::chrono::steady_clock::time_point b) {
+  return std::chrono::duration<double, std::milli>(b - a).count();
+}
+}  // namespace
+
+extern "C" {
+
+const char* elm_last_error(void) { return g_err.c_str(); }
+
+elm_model* elm_model_load(const char* path) {
+  try {
+    auto* m = new elm_model{Model::load(path)};
+    return m;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return nullptr;
+  }
+}
+
+void elm_model_free(elm_model* m) { delete m; }
+
+int elm_model_config(const elm_model* m, int* o) {
+  if (!m || !o) return -1;
+  const Config& c = m->m.cfg;
+  const int v[10] = {c.vocab, c.dim, c.hidden, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq,
+                     static_cast<int>(c.weight_dtype), c.tied ? 1 : 0};
+  std::memcpy(o, v, sizeof v);
+  return 0;
+}
+
+int elm_model_fusion(const elm_model* m, int* o) {
+  return guard([&] {
+    Graph g = m->m.graph;
+    const FusionStats s = optimize(g);
+    const int v[6] = {s.swiglu, s.shared_input, s.residual, s.rope, static_cast<int>(s.ops_before),
+                      static_cast<int>(s.ops_after)};
+    std::memcpy(o, v, sizeof v);
+    return 0;
+  });
+}
+
+int elm_model_plan(const elm_model* m, int fuse, int T, int L, int64_t* arena, int64_t* naive) {
+  return guard([&] {
+    Graph g = m->m.graph;
+    if (fuse) optimize(g);
+    const MemoryPlan p = plan_memory(g, T, L);
+    *arena = static_cast<int64_t>(p.arena_bytes);
+    *naive = static_cast<int64_t>(p.naive_bytes);
+    return plan_is_valid(p) ? 1 : 0;
+  });
+}
+
+int elm_model_partition(const elm_model* m, const char* backends, int fuse, char* buf, int cap) {
+  return guard([&] {
+    Graph g = m->m.graph;
+    if (fuse) optimize(g);
+    std::vector<std::unique_ptr<Backend>> owned;
+    for (const std::string& b : split(backends)) {
+      if (b == "reference" || b == "ref") continue;
+      owned.push_back(b == "hip" ? make_hip_planning_backend() : make_backend(b));
+    }
+    owned.push_back(make_reference_backend());
+    std::vector<Backend*> pref;
+    for (auto& b : owned) pref.push_back(b.get());
+    const auto parts = partition_graph(g, pref);
+    copy_text(describe_partitions(g, parts), buf, cap);
+    return static_cast<int>(parts.size());
+  });
+}
+
+elm_session* elm_session_create(const elm_model* m, const char* backends, int threads, int max_ctx, int max_batch,
+                                int all_logits, int act_quant, int fuse) {
+  try {
+    SessionOptions o;
+    o.backends = split(backends);
+    o.threads = threads;
+    o.max_ctx = max_ctx;
+    o.max_batch = max_batch;
+    o.all_logits = all_logits != 0;
+    o.act_quant = act_quant != 0;
+    o.fuse = fuse != 0;
+    auto* s = new elm_session{std::make_unique<Session>(m->m, o)};
+    return s;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return nullptr;
+  }
+}
+
+void elm_session_destroy(elm_session* s) { delete s; }
+
+int elm_session_forward(elm_session* s, const int32_t* tokens, int n, float* out) {
+  return guard([&] {
+    const float* lg = s->s->forward(tokens, n);
+    const int rows = s->s->options().all_logits ? n : 1;
+    if (out) std::memcpy(out, lg, sizeof(float) * static_cast<size_t>(rows) * s->s->vocab());
+    return 0;
+  });
+}
+
+int elm_session_prefill(elm_session* s, const int32_t* tokens, int n, float* out) {
+  return guard([&] {
+    const float* lg = s->s->prefill(std::vector<int32_t>(tokens, tokens + n));
+    const int mb = s->s->options().max_batch;
+    const int last = n % mb ? n % mb : mb;
+    const int rows = s->s->options().all_logits ? last : 1;
+    if (out) std::memcpy(out, lg, sizeof(float) * static_cast<size_t>(rows) * s->s->vocab());
+    return 0;
+  });
+}
+
+int elm_session_reset(elm_session* s) {
+  s->s->reset();
+  return 0;
+}
+
+int elm_session_pos(const elm_session* s) { return s->s->pos(); }
+
+int elm_session_describe(const elm_session* s, char* buf, int cap) {
+  copy_text(describe_partitions(s->s->graph(), s->s->partitions()), buf, cap);
+  return static_cast<int>(s->s->graph().ops.size());
+}
+
+int elm_session_generate(elm_session* s, const int32_t* prompt, int n_prompt, int gen, double* prefill_ms,
+                         double* ttft_ms, double* decode_ms, int32_t* tokens_out) {
+  return guard([&] {
+    Session& ss = *s->s;
+    const int V = ss.vocab();
+    ss.reset();
+    const auto t0 = std::chrono::steady_clock::now();
+    const float* lg = ss.prefill(std::vector<int32_t>(prompt, prompt + n_prompt));
+    const auto t1 = std::chrono::steady_clock::now();
+    int32_t tok = argmax(lg, V);
+    const auto t2 = std::chrono::steady_clock::now();
+    if (tokens_out) tokens_out[0] = tok;
+    for (int i = 0; i < gen; ++i) {
+      tok = argmax(ss.decode(tok), V);
+      if (tokens_out) tokens_out[i + 1] = tok;
+    }
+    const auto t3 = std::chrono::steady_clock::now();
+    *prefill_ms = ms_between(t0, t1);
+    *ttft_ms = ms_between(t0, t2);
+    *decode_ms = ms_between(t2, t3);
+    return 0;
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+"""GPU end to end: sessions of this build's runtime with the `hip` delegate (backends "hip,cpu")
+against edgelm's own Session (compiled from the reference sources into oracle/_ref) on the same .elm
+files. The MATMUL family runs on the GPU, the other ops on the host; logits must be bit-identical to
+edgelm's cpu backend (x86 scalar path) and within 2e-5 of its reference backend
+(test_e2e.cpp:33-75), and greedy tokens must agree on the SmolLM2-135M-shaped random model.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import bits_equal, rel_err
+from edgelm_amd import elm_format as F
+from edgelm_amd import host
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not O.ref_available(), reason="needs oracle/_ref (edgelm's own build)")]
+
+
+@pytest.fixture(scope="module")
+def tiny(tmp_path_factory):
+    d = tmp_path_factory.mktemp("tiny")
+    W = F.random_weights(F.TINY, 1234, sd=0.15, embed_sd=0.5)
+    paths = {}
+    for dt in ("q8", "q4"):
+        p = str(d / f"tiny.{dt}.elm")
+        F.write_elm(p, F.TINY, W, dt)
+        paths[dt] = p
+    return paths
+
+
+def run_all(sess, ids, prefill, batch):
+    out = []
+    for i in range(0, prefill, batch):
+        out.append(sess.forward(ids[i:min(prefill, i + batch)]))
+    for t in ids[prefill:]:
+        out.append(sess.forward(np.array([t], np.int32)))
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("dt", ["q8", "q4"])
+@pytest.mark.parametrize("act", [False, True])
+def test_tiny_logits_bit_identical_to_edgelm(tiny, dt, act):
+    ids = np.random.default_rng(5).integers(0, 320, 40).astype(np.int32)
+    m = host.Model(tiny[dt])
+    variants = [("full prefill", 128, 40, 4), ("chunked prefill (7)", 7, 40, 2), ("prefill 5 + decode", 128, 5, 3),
+                ("decode only", 128, 0, 1)]
+    for name, batch, prefill, threads in variants:
+        print(f"[gpu] e2e tiny {dt} act_int8={act} {name}", flush=True)
+        mine = host.Session(m, "hip,cpu", threads=threads, max_ctx=64, max_batch=batch, all_logits=True,
+                            act_quant=act)
+        ref = O.RefSession(tiny[dt], "cpu", threads=threads, max_ctx=64, max_batch=batch, all_logits=True,
+                           act_quant=act)
+        got, want = run_all(mine, ids, prefill, batch), run_all(ref, ids, prefill, batch)
+        assert bits_equal(got, want), f"{name}: max diff {np.abs(got - want).max()}"
+        assert mine.pos() == 40
+        refb = O.RefSession(tiny[dt], "reference", threads=1, max_ctx=64, max_batch=batch, all_logits=True,
+                            act_quant=act)
+        # f32 activations: within 2e-5 of the reference backend (test_e2e.cpp:72). Int8 activations:
+        # a last-bit difference before quantize_act_row flips an int8 rounding and propagates
+        # (README.md:168-172); edgelm's own cpu backend sits ~6e-3 from its reference backend on this
+        # model, so the bound is edgelm's int8-vs-f32 closeness bound (test_ops.cpp:235-238).
+        assert rel_err(got, run_all(refb, ids, prefill, batch)) < (2e-2 if act else 2e-5)
+        mine.close(), ref.close(), refb.close()
+
+
+def test_tiny_thread_count_invariance(tiny):
+    m = host.Model(tiny["q4"])
+    ids = np.random.default_rng(6).integers(0, 320, 20).astype(np.int32)
+    base = None
+    for th in (1, 2, 3, 8):
+        s = host.Session(m, "hip,cpu", threads=th, max_ctx=64, max_batch=128, all_logits=True, act_quant=True)
+        got = run_all(s, ids, 20, 128)
+        if base is None:
+            base = got
+        assert bits_equal(got, base)
+        s.close()
+
+
+@pytest.fixture(scope="module")
+def smollm(tmp_path_factory):
+    d = tmp_path_factory.mktemp("smollm")
+    p = str(d / "smollm2-135m-random.q4.elm")
+    print("[gpu] writing SmolLM2-135M-shaped random q4 model (q8 embedding)", flush=True)
+    F.write_elm(p, F.SMOLLM2_135M, F.random_weights(F.SMOLLM2_135M, 20260101), "q4", embed_dtype="q8")
+    return p
+
+
+def test_smollm2_greedy_bit_identical_to_edgelm(smollm):
+    """configs[3] protocol: 128-token LCG prompt, then greedy decode (16 steps here), act int8."""
+    prompt = F.lcg_prompt(128, 49152)
+    m = host.Model(smollm)
+    mine = host.Session(m, "hip,cpu", threads=8, max_ctx=160, max_batch=128, act_quant=True)
+    ref = O.RefSession(smollm, "cpu", threads=16, max_ctx=160, max_batch=128, act_quant=True)
+    print("[gpu] e2e smollm2 prefill", flush=True)
+    a, b = mine.forward(prompt), ref.forward(prompt)
+    assert bits_equal(a, b)
+    toks = []
+    t_mine, t_ref = int(np.argmax(a)), int(np.argmax(b))
+    for step in range(16):
+        assert t_mine == t_ref
+        toks.append(t_mine)
+        a = mine.forward(np.array([t_mine], np.int32))
+        b = ref.forward(np.array([t_ref], np.int32))
+        assert bits_equal(a, b), f"step {step}"
+        t_mine, t_ref = int(np.argmax(a)), int(np.argmax(b))
+    print(f"[gpu] greedy tokens {toks}", flush=True)
+    mine.close(), ref.close()

@@ -1,0 +1,91 @@
+"""CPU: the host runtime around the delegate — .elm writing/loading, fusion passes, memory planner,
+partitioner — against edgelm's own loader and passes (oracle/_ref) and the expectations of edgelm's
+tests (test_graph.cpp:182-339)."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from edgelm_amd import elm_format as F
+from edgelm_amd import host
+
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (no /root/reference here)")
+
+
+@pytest.fixture(scope="module")
+def tiny(tmp_path_factory):
+    d = tmp_path_factory.mktemp("tiny")
+    W = F.random_weights(F.TINY, 1234, sd=0.15, embed_sd=0.5)
+    paths = {}
+    for dt in ("f32", "q8", "q4"):
+        p = str(d / f"tiny.{dt}.elm")
+        F.write_elm(p, F.TINY, W, dt)
+        paths[dt] = p
+    return paths
+
+
+def test_loader_config_and_graph(tiny):
+    for dt, code in (("f32", 0), ("q8", 1), ("q4", 2)):
+        m = host.Model(tiny[dt])
+        assert m.cfg["vocab"] == 320 and m.cfg["dim"] == 64 and m.cfg["n_layers"] == 2 and m.cfg["tied"] == 1
+        assert m.cfg["dtype"] == code
+    with pytest.raises(RuntimeError):
+        host.Model(os.path.join(os.path.dirname(tiny["q8"]), "missing.elm"))
+    bad = os.path.join(os.path.dirname(tiny["q8"]), "bad.elm")
+    with open(bad, "wb") as f:
+        f.write(b"definitely not an elm file" + b"." * 200)
+    with pytest.raises(RuntimeError):
+        host.Model(bad)
+
+
+def test_fusion_and_planner(tiny):
+    m = host.Model(tiny["q4"])
+    fz = m.fusion()
+    assert (fz["swiglu"], fz["shared_input"], fz["residual"], fz["rope"]) == (2, 2, 4, 2)
+    assert fz["ops_before"] == 1 + 2 * 16 + 3 and fz["ops_after"] == 1 + 2 * 7 + 3
+    for fuse in (False, True):
+        for T in (1, 16, 128):
+            ok, arena, naive = m.plan(T, 1, fuse)
+            assert ok and arena < naive and arena >= T * 64 * 4
+
+
+@needs_ref
+def test_reference_loader_reads_our_files(tiny):
+    for dt in ("q8", "q4"):
+        r = O.RefSession(tiny[dt], "cpu", threads=1, max_ctx=32, max_batch=8)
+        nops, desc = r.describe()
+        assert nops == 18 and "reference 2 ops" in desc
+        r.close()
+
+
+def test_partitioner_hip_claims_exactly_the_quantized_matmuls(tiny):
+    for dt in ("q8", "q4"):
+        m = host.Model(tiny[dt])
+        n, desc = m.partition("hip,cpu")
+        assert "hip 9 ops" in desc and "cpu 7 ops" in desc and "reference 2 ops" in desc  # per layer 4 + lm_head
+        n2, desc2 = m.partition("hip")  # no cpu: the reference backend takes the rest
+        assert "hip 9 ops" in desc2 and "reference 9 ops" in desc2
+    # f32 weights: not claimed, and no host backend of this build runs a matmul -> loud failure
+    m = host.Model(tiny["f32"])
+    with pytest.raises(RuntimeError, match="no backend supports"):
+        m.partition("hip,cpu")
+
+
+def test_session_without_gpu_fails_loudly(tiny):
+    from edgelm_amd import elmh
+    if elmh.device_count() > 0:
+        pytest.skip("a GPU is present")
+    m = host.Model(tiny["q4"])
+    with pytest.raises(RuntimeError, match="hip backend unavailable"):
+        host.Session(m, "hip,cpu")
+
+
+def test_lcg_prompt_matches_edgelm_bench():
+    # main.cpp:178-184 with vocab 49152 (lo = 1000): first ids recomputed with Python integers
+    p = F.lcg_prompt(4, 49152)
+    x, want = 12345, []
+    for _ in range(4):
+        x = (x * 6364136223846793005 + 1442695040888963407) % 2 ** 64
+        want.append(1000 + (x >> 33) % (49152 - 1000))
+    assert list(p) == want and p.dtype == np.int32
