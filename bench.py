@@ -228,6 +228,21 @@ def sweep_8b(ctx, E, reps=10):
     ms = time_graph(ctx, sweep, reps)
     gbs = total / (ms * 1e-3) / 1e9
     log(f"8B sweep {ms * 1e3:.1f} us for {total / 1e9:.3f} GB -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of peak)")
+    # each op type alone over the 8 layers (includes its activation quantization launch)
+    per_op = {}
+    ops8 = {
+        "MATMUL_N qkv 6144x4096": (lambda l: ctx.matmul_dev(bx.ptr, 1, 4096, [W[f"{l}.q"], W[f"{l}.k"], W[f"{l}.v"]],
+                                                            [by[0].ptr, by[1].ptr, by[2].ptr], act=E.ACT_INT8),
+                                   sum(q_bytes(2, W[f"0.{n}"].rows, 4096) for n in "qkv")),
+        "FFN_SWIGLU 2x14336x4096": (lambda l: ctx.swiglu_dev(bx.ptr, 1, 4096, W[f"{l}.g"], W[f"{l}.u"], by[0].ptr,
+                                                             act=E.ACT_INT8), 2 * q_bytes(2, 14336, 4096)),
+        "MATMUL down 4096x14336": (lambda l: ctx.matmul_dev(bx.ptr, 1, 14336, [W[f"{l}.d"]], [by[1].ptr], act=E.ACT_INT8),
+                                   q_bytes(2, 4096, 14336)),
+    }
+    for name, (fn, nbytes) in ops8.items():
+        ums = time_graph(ctx, lambda: [fn(l) for l in range(8)], reps) / 8
+        per_op[name] = {"us": ums * 1e3, "weight_bytes": nbytes, "GBs": nbytes / (ums * 1e-3) / 1e9}
+        log(f"  8B {name:26s} {ums * 1e3:8.2f} us  {per_op[name]['GBs']:7.0f} GB/s (weights+scales / time, incl. act quant)")
 
     # the down GEMV alone, pre-quantized activation (pure kernel time), all 8 layers
     q = ctx.buffer(14336)
@@ -242,7 +257,7 @@ def sweep_8b(ctx, E, reps=10):
     for b in [bx, q, d, s] + by:
         b.free()
     m.free()
-    return {"sweep_us": ms * 1e3, "bytes": total, "GBs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS,
+    return {"sweep_us": ms * 1e3, "bytes": total, "GBs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "per_op": per_op,
             "down_gemv_us": dms * 1e3, "down_gemv_bytes": dbytes, "down_gemv_GBs": dgbs}
 
 

@@ -161,8 +161,6 @@ __global__ __launch_bounds__(256) void act_quant_frag_token_kernel(const float* 
 // contiguous run. Every dispatch starts with cold instruction caches, so the kernels are kept
 // short and issue all of their loads before any dependent work.
 
-constexpr int kActRegs = 4;  // int4 of pre-quantized activation per thread (T*K <= 16384)
-
 __device__ __forceinline__ int fold_stride(int nb) {
   const int p = (nb + 3) & ~3;
   return ((p >> 2) & 1) ? p : p + 4;  // multiple of 4 (16-byte rows), odd in float4 units
@@ -398,8 +396,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
 }
 
 // Streaming decode GEMV for large weights: pre-quantized activation; a workgroup takes a.tpw
-// consecutive H-row tiles (one contiguous chunk) and loads all of its items (at most IPT per
-// thread) at kernel entry, so a full grid keeps the whole matrix in flight.
+// consecutive H-row tiles (one contiguous chunk). The activation (L2-resident, small) is staged in
+// LDS first; then every weight item of the workgroup (at most IPT per thread) is requested at once
+// and the products consume them in request order, so each item is processed as soon as it lands
+// (vector loads retire in order) while the rest of the tile is still streaming in.
 template <int WDT, int NT, bool SW, int IPT>
 __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -419,6 +419,21 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
   const int per_tile = H * nb, per_sel = ntl * per_tile, items = (SW ? 2 : 1) * per_sel;
   const int64_t base = (int64_t)tile0 * per_tile;
 
+  // 1. activation into LDS
+  const int nq16 = T * K / 16, nblk = T * nb;
+  for (int e = tid; e < nq16; e += kGemvThreads) {
+    const int t = (e * 16) / K, k = e * 16 - t * K;
+    *reinterpret_cast<int4*>(L.q + t * L.kpad + k) = reinterpret_cast<const int4*>(a.xq)[e];
+  }
+  for (int e = tid; e < nblk; e += kGemvThreads) {
+    L.d[e] = a.xd[e];
+    L.s[e] = a.xs[e];
+  }
+  float e_res, e_s, e_su;
+  gemv_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
+  __syncthreads();
+
+  // 2. every weight item of the workgroup in flight
   v4u w[IPT][G / 16];
   float wsc[IPT];
 #pragma unroll
@@ -435,41 +450,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
       if (WDT == WQ4) wsc[u] = __builtin_nontemporal_load(tw.scales + gi);
     }
   }
-  // then the activation (L2-resident; its LDS staging waits for the weights anyway)
-  const int nq16 = T * K / 16, nblk = T * nb;
-  int4 av[kActRegs];
-#pragma unroll
-  for (int m = 0; m < kActRegs; ++m) {
-    const int e = m * kGemvThreads + tid;
-    av[m] = reinterpret_cast<const int4*>(a.xq)[e < nq16 ? e : 0];
-  }
-  float dv[2];
-  int sv[2];
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int e = m * kGemvThreads + tid;
-    dv[m] = a.xd[e < nblk ? e : 0];
-    sv[m] = a.xs[e < nblk ? e : 0];
-  }
-  float e_res, e_s, e_su;
-  gemv_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
-#pragma unroll
-  for (int m = 0; m < kActRegs; ++m) {
-    const int e = m * kGemvThreads + tid;
-    if (e < nq16) {
-      const int t = (e * 16) / K, k = e * 16 - t * K;
-      *reinterpret_cast<int4*>(L.q + t * L.kpad + k) = av[m];
-    }
-  }
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int e = m * kGemvThreads + tid;
-    if (e < nblk) {
-      L.d[e] = dv[m];
-      L.s[e] = sv[m];
-    }
-  }
-  __syncthreads();
+  // 3. products in request order
 #pragma unroll
   for (int u = 0; u < IPT; ++u) {
     const int it = u * kGemvThreads + tid;
@@ -929,7 +910,6 @@ static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
     gemv_small_kernel<WDT, NT, SW><<<tiles, kGemvThreads, lds, s>>>(a);
     return hipGetLastError();
   }
-  if (a.T * a.K > kActRegs * kGemvThreads * 16 || a.T * a.nb > 2 * kGemvThreads) return hipErrorInvalidValue;
   if (a.tpw < 1 || a.T * a.tpw * a.H > kGemvThreads) return hipErrorInvalidValue;
   const int items = (SW ? 2 : 1) * a.tpw * a.H * a.nb;
   switch (gemv_stream_ipt(WDT, items)) {
