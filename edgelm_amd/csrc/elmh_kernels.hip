@@ -281,6 +281,49 @@ __device__ __forceinline__ void gemv_epilogue_operands(const GemvArgs& a, const 
   }
 }
 
+// A value pinned in scalar registers at this point: the compiler can no longer turn a select
+// between such values back into a load through a selected address.
+template <typename V>
+__device__ __forceinline__ V pin_sgpr(V v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
+// A pinned pointer restated as global memory (the pin hides where it came from; without this the
+// accesses through it become flat instructions, which also count against the LDS wait counter).
+template <typename P>
+__device__ __forceinline__ P* pin_global(P* p) {
+  __attribute__((address_space(1))) P* g = (__attribute__((address_space(1))) P*)p;
+  asm volatile("" : "+s"(g));
+  return (P*)g;
+}
+
+// The target owning workgroup `wg` (made relative to it). Every dispatch starts with a cold scalar
+// cache, so the launch arguments are fetched in one batch (fixed offsets only) and the target is
+// picked with uniform selects: a search loop or an indexed access would cost a dependent round
+// trip per step before the first weight load (and a dynamic index into the by-value struct makes
+// the compiler copy it to scratch memory).
+template <bool SW>
+__device__ __forceinline__ GemvTarget gemv_target(const GemvArgs& a, int& wg) {
+  if (SW) return a.tg[0];
+  const int n = pin_sgpr(a.n_targets);
+  const int ts1 = pin_sgpr(a.tile_start[1]), ts2 = pin_sgpr(a.tile_start[2]), ts3 = pin_sgpr(a.tile_start[3]);
+  GemvTarget t[kMaxTargets];
+#pragma unroll
+  for (int i = 0; i < kMaxTargets; ++i) {
+    t[i].data = pin_global(a.tg[i].data);
+    t[i].scales = pin_global(a.tg[i].scales);
+    t[i].y = pin_global(a.tg[i].y);
+    t[i].res = pin_global(a.tg[i].res);
+    t[i].N = pin_sgpr(a.tg[i].N);
+    t[i].tiles = pin_sgpr(a.tg[i].tiles);
+  }
+  const bool g1 = n > 1 && wg >= ts1, g2 = n > 2 && wg >= ts2, g3 = n > 3 && wg >= ts3;
+  GemvTarget r = g3 ? t[3] : g2 ? t[2] : g1 ? t[1] : t[0];
+  wg -= g3 ? ts3 : g2 ? ts2 : g1 ? ts1 : 0;
+  return r;
+}
+
 // Small decode GEMV: x quantized inside the workgroup (8 elements per thread, 4 threads per
 // block), at most two items per thread held in registers before the products (longer tiles loop).
 constexpr int kSmallMaxAct = kGemvThreads * 8;
@@ -291,12 +334,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   constexpr int G = WDT == WQ8 ? 32 : 16;
   const int K = a.K, nb = a.nb, T = a.T, H = a.H, tid = threadIdx.x;
   const GemvLds L = gemv_lds<NT>(smem, K, nb);
-  int ti = 0, tile = blockIdx.x;
-  if (!SW) {
-    while (ti + 1 < a.n_targets && tile >= a.tile_start[ti + 1]) ++ti;
-    tile -= a.tile_start[ti];
-  }
-  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  int tile = blockIdx.x;
+  const GemvTarget tg = gemv_target<SW>(a, tile);
+  const uint8_t* const wd1 = SW ? a.tg[1].data : tg.data;
+  const float* const ws1 = SW ? a.tg[1].scales : tg.scales;
   const int per_sel = H * nb, items = (SW ? 2 : 1) * per_sel;
   const int nel = T * K;
 
@@ -315,12 +356,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
     const int it = u * kGemvThreads + tid;
     if (it < items) {
       const int sel = SW ? (it >= per_sel) : 0;
-      const GemvTarget& tw = a.tg[SW ? sel : ti];
       const int64_t gi = (int64_t)tile * per_sel + (it - sel * per_sel);
-      const v4u* src = reinterpret_cast<const v4u*>(tw.data + gi * G);
+      const v4u* src = reinterpret_cast<const v4u*>((sel ? wd1 : tg.data) + gi * G);
       w[u][0] = src[0];
       if (G == 32) w[u][G / 16 - 1] = src[1];
-      if (WDT == WQ4) wsc[u] = tw.scales[gi];
+      if (WDT == WQ4) wsc[u] = (sel ? ws1 : tg.scales)[gi];
     }
   }
   // 3. epilogue operands of the folding lanes
@@ -377,12 +417,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
       w1 = u ? w[1][G / 16 - 1] : w[0][G / 16 - 1];
       ws = u ? wsc[1] : wsc[0];
     } else {
-      const GemvTarget& tw = a.tg[SW ? sel : ti];
       const int64_t gi = (int64_t)tile * per_sel + j;
-      const v4u* src = reinterpret_cast<const v4u*>(tw.data + gi * G);
+      const v4u* src = reinterpret_cast<const v4u*>((sel ? wd1 : tg.data) + gi * G);
       w0 = src[0];
       w1 = G == 32 ? src[1] : w0;
-      ws = WDT == WQ4 ? tw.scales[gi] : 0.f;
+      ws = WDT == WQ4 ? (sel ? ws1 : tg.scales)[gi] : 0.f;
     }
     const int b = j / H, r = j - b * H;
 #pragma unroll
@@ -395,78 +434,113 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   gemv_fold<WDT, NT, SW>(a, L, tg, tile * H, H, H, tid, e_res, e_s, e_su);
 }
 
+// Activation registers of the streaming GEMV: T * K <= kStreamMaxAct bytes.
+constexpr int kStreamMaxAct = 16384;
+constexpr int kStreamActVec = kStreamMaxAct / 16 / kGemvThreads;
+constexpr int kStreamActBlk = kStreamMaxAct / kBlock / kGemvThreads;
+
 // Streaming decode GEMV for large weights: pre-quantized activation; a workgroup takes a.tpw
-// consecutive H-row tiles (one contiguous chunk). The activation (L2-resident, small) is staged in
-// LDS first; then every weight item of the workgroup (at most IPT per thread) is requested at once
-// and the products consume them in request order, so each item is processed as soon as it lands
-// (vector loads retire in order) while the rest of the tile is still streaming in.
+// consecutive H-row tiles (one contiguous chunk). Its activation is requested first (into
+// registers), then every weight item of the workgroup (at most IPT per thread) at once; vector
+// loads retire in order, so each item's product is computed as soon as it has landed while the
+// rest are still streaming in. One lane per (token, row) then folds its row in block order.
 template <int WDT, int NT, bool SW, int IPT>
 __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int G = WDT == WQ8 ? 32 : 16;
   const int K = a.K, nb = a.nb, T = a.T, H = a.H, tid = threadIdx.x;
   const GemvLds L = gemv_lds<NT>(smem, K, nb);
-  int ti = 0, wg = blockIdx.x;
-  if (!SW) {
-    while (ti + 1 < a.n_targets && wg >= a.tile_start[ti + 1]) ++ti;
-    wg -= a.tile_start[ti];
-  }
-  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  int wg = blockIdx.x;
+  const GemvTarget tg = gemv_target<SW>(a, wg);
   const int tile0 = wg * a.tpw;
   const int ntl = min(a.tpw, tg.tiles - tile0);
   const int R = a.tpw * H;      // LDS row slots per token
   const int rows = ntl * H;     // rows this workgroup owns
   const int per_tile = H * nb, per_sel = ntl * per_tile, items = (SW ? 2 : 1) * per_sel;
   const int64_t base = (int64_t)tile0 * per_tile;
+  // A store the compiler cannot rule out (T is never negative): without one, loads from memory
+  // that nothing in the kernel writes count as invariant and get sunk to their first use, which
+  // would put them behind the waits below instead of all in flight at once.
+  if (T < 0) tg.y[0] = 0.f;
 
-  // 1. activation into LDS
+  // 1. activation into registers (named values: an array here ends up in scratch memory; indices
+  // are clamped rather than tested, so the loads stay unconditional)
   const int nq16 = T * K / 16, nblk = T * nb;
-  for (int e = tid; e < nq16; e += kGemvThreads) {
-    const int t = (e * 16) / K, k = e * 16 - t * K;
-    *reinterpret_cast<int4*>(L.q + t * L.kpad + k) = reinterpret_cast<const int4*>(a.xq)[e];
-  }
-  for (int e = tid; e < nblk; e += kGemvThreads) {
-    L.d[e] = a.xd[e];
-    L.s[e] = a.xs[e];
-  }
-  float e_res, e_s, e_su;
-  gemv_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
-  __syncthreads();
-
+  static_assert(kStreamActVec == 4 && kStreamActBlk == 2, "activation register count");
+  const int4* xq4 = reinterpret_cast<const int4*>(a.xq);
+  const int4 av0 = xq4[min(tid, nq16 - 1)], av1 = xq4[min(kGemvThreads + tid, nq16 - 1)];
+  const int4 av2 = xq4[min(2 * kGemvThreads + tid, nq16 - 1)], av3 = xq4[min(3 * kGemvThreads + tid, nq16 - 1)];
+  const int eb0 = min(tid, nblk - 1), eb1 = min(kGemvThreads + tid, nblk - 1);
+  const float ad0 = a.xd[eb0], ad1 = a.xd[eb1];
+  const int as0 = a.xs[eb0], as1 = a.xs[eb1];
+  asm volatile("" ::: "memory");  // keep the activation loads ahead of the weight loads
   // 2. every weight item of the workgroup in flight
+  const uint8_t* const wd1 = SW ? a.tg[1].data : tg.data;
+  const float* const ws1 = SW ? a.tg[1].scales : tg.scales;
   v4u w[IPT][G / 16];
   float wsc[IPT];
 #pragma unroll
   for (int u = 0; u < IPT; ++u) {
-    const int it = u * kGemvThreads + tid;
+    const int it = min(u * kGemvThreads + tid, items - 1);
+    const int sel = SW ? (it >= per_sel) : 0;
+    const int64_t gi = base + (it - sel * per_sel);
+    const v4u* src = reinterpret_cast<const v4u*>((sel ? wd1 : tg.data) + gi * G);
+    w[u][0] = __builtin_nontemporal_load(src);
+    if (G == 32) w[u][G / 16 - 1] = __builtin_nontemporal_load(src + 1);
     wsc[u] = 0.f;
-    if (it < items) {
-      const int sel = SW ? (it >= per_sel) : 0;
-      const GemvTarget& tw = a.tg[SW ? sel : ti];
-      const int64_t gi = base + (it - sel * per_sel);
-      const v4u* src = reinterpret_cast<const v4u*>(tw.data + gi * G);
-      w[u][0] = __builtin_nontemporal_load(src);
-      if (G == 32) w[u][G / 16 - 1] = __builtin_nontemporal_load(src + 1);
-      if (WDT == WQ4) wsc[u] = __builtin_nontemporal_load(tw.scales + gi);
-    }
+    if (WDT == WQ4) wsc[u] = __builtin_nontemporal_load((sel ? ws1 : tg.scales) + gi);
   }
-  // 3. products in request order
+  asm volatile("" ::: "memory");  // ... and every weight load issued before anything waits
+  // 3. activation into LDS (its loads were issued first, so this waits for none of the weights;
+  // the stores are unconditional, lanes past the end rewrite the last element with its own value)
+  auto put_q = [&](int i, const int4& v) {
+    const int e = min(i * kGemvThreads + tid, nq16 - 1);
+    const int t = (e * 16) / K, k = e * 16 - t * K;
+    *reinterpret_cast<int4*>(L.q + t * L.kpad + k) = v;
+  };
+  put_q(0, av0);
+  put_q(1, av1);
+  put_q(2, av2);
+  put_q(3, av3);
+  L.d[eb0] = ad0;
+  L.s[eb0] = as0;
+  L.d[eb1] = ad1;
+  L.s[eb1] = as1;
+  float e_res, e_s, e_su;
+  gemv_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
+  __syncthreads();
+
+  // 4. products into LDS in request order (each waits only for its own loads). H is a power of two
+  // dividing the workgroup size, so a thread's row within its tile never changes and its block
+  // advances by 256 / H per load step; no integer division per item.
+  const int lgH = __builtin_ctz(H);
+  const int r_in = tid & (H - 1), q0 = tid >> lgH, bpu = kGemvThreads >> lgH;
+  const float inv_nb = 1.0f / (float)nb;
+  const int tstride = R * L.pst, sstride = NT * tstride, prow = r_in * L.pst;
 #pragma unroll
   for (int u = 0; u < IPT; ++u) {
     const int it = u * kGemvThreads + tid;
     if (it < items) {
       const int sel = SW ? (it >= per_sel) : 0;
-      const int jj = it - sel * per_sel;
-      const int st = jj / per_tile, j2 = jj - st * per_tile;
-      const int b = j2 / H, r = st * H + (j2 - b * H);
+      int b = u * bpu + q0 - (sel ? ntl * nb : 0);  // block position across this selection's tiles
+      int off = prow + (sel ? sstride : 0);
+      if (a.tpw > 1) {
+        // tile = floor(b / nb): (b + 0.5) / nb is at least 0.5 / nb away from an integer, far more
+        // than the float error at these sizes (b < 4096)
+        const int st = (int)(((float)b + 0.5f) * inv_nb);
+        b -= st * nb;
+        off += st * H * L.pst;
+      }
+      off += b;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         if (t < T)
-          L.p[((sel * NT + t) * R + r) * L.pst + b] = item_product<WDT>(
-              w[u][0], w[u][G / 16 - 1], wsc[u], L.q + t * L.kpad + b * kBlock, L.d[t * nb + b], L.s[t * nb + b]);
+          L.p[off + t * tstride] = item_product<WDT>(w[u][0], w[u][G / 16 - 1], wsc[u], L.q + t * L.kpad + b * kBlock,
+                                                     L.d[t * nb + b], L.s[t * nb + b]);
     }
   }
   __syncthreads();
+  // 5. one lane per (token, row) folds its row in block order and applies the epilogue
   gemv_fold<WDT, NT, SW>(a, L, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
 }
 
@@ -910,7 +984,9 @@ static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
     gemv_small_kernel<WDT, NT, SW><<<tiles, kGemvThreads, lds, s>>>(a);
     return hipGetLastError();
   }
-  if (a.tpw < 1 || a.T * a.tpw * a.H > kGemvThreads) return hipErrorInvalidValue;
+  if (a.tpw < 1 || a.T * a.tpw * a.H > kGemvThreads || a.T * a.K > kStreamMaxAct || (a.K & 15) ||
+      (a.H & (a.H - 1)) || a.tpw * a.nb > 4096)
+    return hipErrorInvalidValue;
   const int items = (SW ? 2 : 1) * a.tpw * a.H * a.nb;
   switch (gemv_stream_ipt(WDT, items)) {
     case 4: gemv_stream_kernel<WDT, NT, SW, 4><<<tiles, kGemvThreads, lds, s>>>(a); break;
