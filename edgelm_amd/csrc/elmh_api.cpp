@@ -151,17 +151,16 @@ int run_gemv_group(elmh_ctx* c, const float* x, const int8_t* xq, const float* x
     GemvArgs a{};
     const size_t n = std::min<size_t>(kMaxTargets, idx.size() - i0);
     const DevWeight& w0 = w[idx[i0]]->w;
-    int all_tiles = 0;
-    for (size_t j = 0; j < n; ++j) all_tiles += (int)(w[idx[i0 + j]]->w.rows_pad / w0.H);
+    int all_tiles = 0, tiles[kMaxTargets];
+    for (size_t j = 0; j < n; ++j) all_tiles += tiles[j] = (int)(w[idx[i0 + j]]->w.rows_pad / w0.H);
     a.tpw = x ? 1 : stream_tpw(w0, T, all_tiles, 1);
     int wgs = 0;
     a.H = w0.H;
     for (size_t j = 0; j < n; ++j) {
       const DevWeight& wd = w[idx[i0 + j]]->w;
-      const int tiles = (int)(wd.rows_pad / wd.H);
-      a.tg[j] = {wd.data, wd.scales, y[idx[i0 + j]], res ? res[idx[i0 + j]] : nullptr, (int)wd.rows, tiles};
+      a.tg[j] = {wd.data, wd.scales, y[idx[i0 + j]], res ? res[idx[i0 + j]] : nullptr, (int)wd.rows, tiles[j]};
       a.tile_start[j] = wgs;
-      wgs += (tiles + a.tpw - 1) / a.tpw;
+      wgs += (tiles[j] + a.tpw - 1) / a.tpw;
     }
     a.tile_start[n] = wgs;
     a.n_targets = (int)n;

@@ -195,32 +195,39 @@ __device__ __forceinline__ float item_product(const v4u w0, const v4u w1, float 
   return (float)S * (wsc * xd);
 }
 
-// Sequential block-order fold of one LDS row of products. The next 16 values are read while the
-// current 16 are added, so long rows (448 blocks at K = 14336) do not wait on LDS every step.
+// Sequential block-order fold of one LDS row of products. The next 32 values are read while the
+// current 32 are added, so long rows (448 blocks at K = 14336) keep the add chain fed: the chain
+// (one dependent add per block) is the latency that is left after the last weight has arrived.
+__device__ __forceinline__ void add4(float& acc, const float4 v) {
+  acc = acc + v.x;
+  acc = acc + v.y;
+  acc = acc + v.z;
+  acc = acc + v.w;
+}
+
 __device__ __forceinline__ float fold_row(const float* row, int nb) {
+  constexpr int D = 8;  // float4 values in flight
   const float4* pv = reinterpret_cast<const float4*>(row);
   float acc = 0.f;
   const int nq = nb >> 2;
   int q = 0;
-  if (nq >= 4) {
-    float4 c0 = pv[0], c1 = pv[1], c2 = pv[2], c3 = pv[3];
-    for (q = 4; q + 4 <= nq; q += 4) {
-      const float4 n0 = pv[q], n1 = pv[q + 1], n2 = pv[q + 2], n3 = pv[q + 3];
-      acc = acc + c0.x; acc = acc + c0.y; acc = acc + c0.z; acc = acc + c0.w;
-      acc = acc + c1.x; acc = acc + c1.y; acc = acc + c1.z; acc = acc + c1.w;
-      acc = acc + c2.x; acc = acc + c2.y; acc = acc + c2.z; acc = acc + c2.w;
-      acc = acc + c3.x; acc = acc + c3.y; acc = acc + c3.z; acc = acc + c3.w;
-      c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+  if (nq >= D) {
+    float4 c[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) c[i] = pv[i];
+    for (q = D; q + D <= nq; q += D) {
+      float4 n[D];
+#pragma unroll
+      for (int i = 0; i < D; ++i) n[i] = pv[q + i];
+#pragma unroll
+      for (int i = 0; i < D; ++i) add4(acc, c[i]);
+#pragma unroll
+      for (int i = 0; i < D; ++i) c[i] = n[i];
     }
-    acc = acc + c0.x; acc = acc + c0.y; acc = acc + c0.z; acc = acc + c0.w;
-    acc = acc + c1.x; acc = acc + c1.y; acc = acc + c1.z; acc = acc + c1.w;
-    acc = acc + c2.x; acc = acc + c2.y; acc = acc + c2.z; acc = acc + c2.w;
-    acc = acc + c3.x; acc = acc + c3.y; acc = acc + c3.z; acc = acc + c3.w;
+#pragma unroll
+    for (int i = 0; i < D; ++i) add4(acc, c[i]);
   }
-  for (; q < nq; ++q) {
-    const float4 v = pv[q];
-    acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
-  }
+  for (; q < nq; ++q) add4(acc, pv[q]);
   for (int b = nq * 4; b < nb; ++b) acc = acc + row[b];
   return acc;
 }
@@ -298,30 +305,34 @@ __device__ __forceinline__ P* pin_global(P* p) {
   return (P*)g;
 }
 
-// The target owning workgroup `wg` (made relative to it). Every dispatch starts with a cold scalar
-// cache, so the launch arguments are fetched in one batch (fixed offsets only) and the target is
-// picked with uniform selects: a search loop or an indexed access would cost a dependent round
-// trip per step before the first weight load (and a dynamic index into the by-value struct makes
-// the compiler copy it to scratch memory).
+// Target ti (uniform) read through the kernel-argument segment pointer: an indexed access to the
+// by-value argument would make the compiler copy it to scratch memory. The kernel's only argument
+// is the struct, so it sits at offset 0 of the segment.
+__device__ __forceinline__ GemvTarget target_at(const GemvArgs& a, int ti) {
+  (void)a;
+  typedef const GemvArgs __attribute__((address_space(4)))* KernArgs;
+  const KernArgs ka = (KernArgs)__builtin_amdgcn_kernarg_segment_ptr();
+  GemvTarget t;
+  t.data = pin_global(ka->tg[ti].data);
+  t.scales = pin_global(ka->tg[ti].scales);
+  t.y = pin_global(ka->tg[ti].y);
+  t.res = pin_global(ka->tg[ti].res);
+  t.N = ka->tg[ti].N;
+  t.tiles = ka->tg[ti].tiles;
+  return t;
+}
+
+// The target owning workgroup (or tile) index `wg`, which is made relative to that target. The
+// tile starts are fetched with the other launch arguments in one batch of scalar loads; the
+// target's fields then take one more (uniform) load.
 template <bool SW>
 __device__ __forceinline__ GemvTarget gemv_target(const GemvArgs& a, int& wg) {
   if (SW) return a.tg[0];
   const int n = pin_sgpr(a.n_targets);
   const int ts1 = pin_sgpr(a.tile_start[1]), ts2 = pin_sgpr(a.tile_start[2]), ts3 = pin_sgpr(a.tile_start[3]);
-  GemvTarget t[kMaxTargets];
-#pragma unroll
-  for (int i = 0; i < kMaxTargets; ++i) {
-    t[i].data = pin_global(a.tg[i].data);
-    t[i].scales = pin_global(a.tg[i].scales);
-    t[i].y = pin_global(a.tg[i].y);
-    t[i].res = pin_global(a.tg[i].res);
-    t[i].N = pin_sgpr(a.tg[i].N);
-    t[i].tiles = pin_sgpr(a.tg[i].tiles);
-  }
-  const bool g1 = n > 1 && wg >= ts1, g2 = n > 2 && wg >= ts2, g3 = n > 3 && wg >= ts3;
-  GemvTarget r = g3 ? t[3] : g2 ? t[2] : g1 ? t[1] : t[0];
-  wg -= g3 ? ts3 : g2 ? ts2 : g1 ? ts1 : 0;
-  return r;
+  const int ti = (n > 1 && wg >= ts1) + (n > 2 && wg >= ts2) + (n > 3 && wg >= ts3);
+  wg -= ti == 0 ? 0 : ti == 1 ? ts1 : ti == 2 ? ts2 : ts3;
+  return target_at(a, ti);
 }
 
 // Small decode GEMV: x quantized inside the workgroup (8 elements per thread, 4 threads per
@@ -463,17 +474,35 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
   // would put them behind the waits below instead of all in flight at once.
   if (T < 0) tg.y[0] = 0.f;
 
-  // 1. activation into registers (named values: an array here ends up in scratch memory; indices
-  // are clamped rather than tested, so the loads stay unconditional)
+  // 1. activation into LDS before any weight is requested: once the weight loads are queued, an
+  // activation load would wait behind them (the products need it first). Indices are clamped
+  // rather than tested (lanes past the end rewrite the last element with its own value), so the
+  // loads stay unconditional and in registers.
   const int nq16 = T * K / 16, nblk = T * nb;
   static_assert(kStreamActVec == 4 && kStreamActBlk == 2, "activation register count");
-  const int4* xq4 = reinterpret_cast<const int4*>(a.xq);
-  const int4 av0 = xq4[min(tid, nq16 - 1)], av1 = xq4[min(kGemvThreads + tid, nq16 - 1)];
-  const int4 av2 = xq4[min(2 * kGemvThreads + tid, nq16 - 1)], av3 = xq4[min(3 * kGemvThreads + tid, nq16 - 1)];
-  const int eb0 = min(tid, nblk - 1), eb1 = min(kGemvThreads + tid, nblk - 1);
-  const float ad0 = a.xd[eb0], ad1 = a.xd[eb1];
-  const int as0 = a.xs[eb0], as1 = a.xs[eb1];
-  asm volatile("" ::: "memory");  // keep the activation loads ahead of the weight loads
+  {
+    // named values: arrays here end up in scratch memory
+    const int4* xq4 = reinterpret_cast<const int4*>(a.xq);
+    const int e0 = min(tid, nq16 - 1), e1 = min(kGemvThreads + tid, nq16 - 1);
+    const int e2 = min(2 * kGemvThreads + tid, nq16 - 1), e3 = min(3 * kGemvThreads + tid, nq16 - 1);
+    const int4 v0 = xq4[e0], v1 = xq4[e1], v2 = xq4[e2], v3 = xq4[e3];
+    const int eb0 = min(tid, nblk - 1), eb1 = min(kGemvThreads + tid, nblk - 1);
+    const float ad0 = a.xd[eb0], ad1 = a.xd[eb1];
+    const int as0 = a.xs[eb0], as1 = a.xs[eb1];
+    auto put = [&](int e, const int4& v) {
+      const int t = (e * 16) / K, k = e * 16 - t * K;
+      *reinterpret_cast<int4*>(L.q + t * L.kpad + k) = v;
+    };
+    put(e0, v0);
+    put(e1, v1);
+    put(e2, v2);
+    put(e3, v3);
+    L.d[eb0] = ad0;
+    L.s[eb0] = as0;
+    L.d[eb1] = ad1;
+    L.s[eb1] = as1;
+  }
+  asm volatile("" ::: "memory");  // the weight loads below stay behind the activation stores
   // 2. every weight item of the workgroup in flight
   const uint8_t* const wd1 = SW ? a.tg[1].data : tg.data;
   const float* const ws1 = SW ? a.tg[1].scales : tg.scales;
@@ -490,22 +519,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
     wsc[u] = 0.f;
     if (WDT == WQ4) wsc[u] = __builtin_nontemporal_load((sel ? ws1 : tg.scales) + gi);
   }
-  asm volatile("" ::: "memory");  // ... and every weight load issued before anything waits
-  // 3. activation into LDS (its loads were issued first, so this waits for none of the weights;
-  // the stores are unconditional, lanes past the end rewrite the last element with its own value)
-  auto put_q = [&](int i, const int4& v) {
-    const int e = min(i * kGemvThreads + tid, nq16 - 1);
-    const int t = (e * 16) / K, k = e * 16 - t * K;
-    *reinterpret_cast<int4*>(L.q + t * L.kpad + k) = v;
-  };
-  put_q(0, av0);
-  put_q(1, av1);
-  put_q(2, av2);
-  put_q(3, av3);
-  L.d[eb0] = ad0;
-  L.s[eb0] = as0;
-  L.d[eb1] = ad1;
-  L.s[eb1] = as1;
+  asm volatile("" ::: "memory");  // every weight load issued before anything waits
   float e_res, e_s, e_su;
   gemv_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
   __syncthreads();
@@ -584,12 +598,14 @@ __global__ __launch_bounds__(256) void gemm_a8_kernel(const GemmArgs a) {
   const int64_t nbase = (int64_t)(n / H) * nb * H + (n % H);
   const int8_t* bsrc = a.xq + ((int64_t)(t0 >> 5) * nb * 64 + lane) * 16;
   const int tcol = t0 + l32;  // the token this lane's accumulators belong to
-  // rows of accumulator i: n0 + 8*(i/4) + 4*h + i%4
-  int64_t sbase[4];
+  // rows of accumulator i: n0 + 8*(i/4) + 4*h + i%4; scale items of rows nr, nr + 1 and of rows
+  // nr + 2, nr + 3 (each pair shares a row tile: H >= 2 and nr is a multiple of 4)
+  int64_t sbase[4], sbase2[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int nr = n0 + 8 * j + 4 * h;
-    sbase[j] = (int64_t)(nr / H) * nb * H + (nr % H);
+    sbase[j] = item_index(nr, 0, nb, H);
+    sbase2[j] = item_index(nr + 2, 0, nb, H);
   }
 
   float acc[16], accu[16];
@@ -637,11 +653,16 @@ __global__ __launch_bounds__(256) void gemm_a8_kernel(const GemmArgs a) {
         const float xdv = TOK ? 1.0f : a.xd[(int64_t)b * a.Tpad + tcol];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float4 ws = *reinterpret_cast<const float4*>(tg.scales + sbase[j] + (int64_t)b * H);
-          float4 wu = ws;
-          if (SW) wu = *reinterpret_cast<const float4*>(a.tg[1].scales + sbase[j] + (int64_t)b * H);
-          const float wsv[4] = {ws.x, ws.y, ws.z, ws.w};
-          const float wuv[4] = {wu.x, wu.y, wu.z, wu.w};
+          const int64_t o1 = sbase[j] + (int64_t)b * H, o2 = sbase2[j] + (int64_t)b * H;
+          const float2 ws01 = *reinterpret_cast<const float2*>(tg.scales + o1);
+          const float2 ws23 = *reinterpret_cast<const float2*>(tg.scales + o2);
+          float2 wu01 = ws01, wu23 = ws23;
+          if (SW) {
+            wu01 = *reinterpret_cast<const float2*>(a.tg[1].scales + o1);
+            wu23 = *reinterpret_cast<const float2*>(a.tg[1].scales + o2);
+          }
+          const float wsv[4] = {ws01.x, ws01.y, ws23.x, ws23.y};
+          const float wuv[4] = {wu01.x, wu01.y, wu23.x, wu23.y};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int i = j * 4 + e;
@@ -977,8 +998,9 @@ int gemv_stream_ipt(int dtype, int items) {
 
 template <int WDT, int NT, bool SW>
 static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
+  if (a.T > NT) return hipErrorInvalidValue;
   const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.x ? a.H : a.tpw * a.H, SW ? 2 : 1);
-  if (lds > 64 * 1024 || a.T > NT) return hipErrorInvalidValue;
+  if (lds > 64 * 1024) return hipErrorInvalidValue;
   if (a.x) {
     if (!gemv_qin_ok(a.T, a.K) || (a.K & 7)) return hipErrorInvalidValue;
     gemv_small_kernel<WDT, NT, SW><<<tiles, kGemvThreads, lds, s>>>(a);

@@ -203,3 +203,67 @@ def test_errors(ctx):
     with pytest.raises(E.ElmhError) as e:
         ctx.upload(O.F32, 4, 64, np.zeros((4, 64), np.float32), np.zeros(4, np.float32))
     assert e.value.code == E.ERR_UNSUPPORTED
+
+
+# Long rows (K > 2048): the streaming decode GEMV (pre-quantized activation, 4- to 32-row tiles)
+# and the GEMM on the same layout. Ragged row counts exercise partial tiles.
+LONG = [(512, 4096), (264, 14336), (130, 8192)]
+
+
+@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
+@pytest.mark.parametrize("shape", LONG)
+def test_matmul_a8_long_rows(ctx, dt, shape):
+    n, k = shape
+    r = rng(300 + n + k + dt)
+    w = weight(r, n, k, dt)
+    dw = up(ctx, w)
+    for T in [1, 2, 3, 4, 5, 33]:
+        print(f"[gpu] matmul a8 long dt={dt} {n}x{k} T={T}", flush=True)
+        x = r.normal(0, 1, (T, k)).astype(np.float32)
+        res = r.normal(0, 1, (T, n)).astype(np.float32)
+        want = O.cpu_matmul(x, [w], [res], act_quant=True)[0]
+        got = ctx.matmul(x, [dw], [res], act=E.ACT_INT8, mode=E.EXACT)[0]
+        assert bits_equal(got, want), f"T={T} max diff {np.abs(got - want).max()}"
+    dw.free()
+
+
+@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
+def test_matmul_n_and_swiglu_long_rows(ctx, dt):
+    """QKV-shaped MATMUL_N (three targets, one with a residual) and FFN_SWIGLU at K = 4096."""
+    r = rng(7 + dt)
+    k = 4096
+    ws = [weight(r, 512, k, dt), weight(r, 128, k, dt), weight(r, 136, k, dt)]
+    dws = [up(ctx, w) for w in ws]
+    for T in [1, 2, 4]:
+        print(f"[gpu] matmul_n long dt={dt} T={T}", flush=True)
+        x = r.normal(0, 1, (T, k)).astype(np.float32)
+        res = [None, r.normal(0, 1, (T, 128)).astype(np.float32), None]
+        got = ctx.matmul(x, dws, res, act=E.ACT_INT8)
+        want = O.cpu_matmul(x, ws, res, act_quant=True)
+        for i, (g, wv) in enumerate(zip(got, want)):
+            assert bits_equal(g, wv), f"T={T} target {i}"
+    wg, wu = weight(r, 300, k, dt), weight(r, 300, k, dt)
+    dg, du = up(ctx, wg), up(ctx, wu)
+    for T in [1, 2, 3, 4, 9]:
+        print(f"[gpu] swiglu long dt={dt} T={T}", flush=True)
+        x = r.normal(0, 1, (T, k)).astype(np.float32)
+        got = ctx.swiglu(x, dg, du, act=E.ACT_INT8)
+        assert bits_equal(got, O.cpu_swiglu(x, wg, wu, act_quant=True)), f"T={T}"
+    for d in dws + [dg, du]:
+        d.free()
+
+
+@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
+def test_matmul_f32act_long_rows(ctx, dt):
+    """f32 activations at K > 2048 (taller row tiles): GEMV and dequantizing GEMM."""
+    r = rng(400 + dt)
+    for n, k in [(130, 4096), (66, 14336)]:
+        w = weight(r, n, k, dt)
+        dw = up(ctx, w)
+        for T in [1, 3, 17]:
+            print(f"[gpu] matmul f32act long dt={dt} {n}x{k} T={T}", flush=True)
+            x = r.normal(0, 1, (T, k)).astype(np.float32)
+            res = r.normal(0, 1, (T, n)).astype(np.float32)
+            got = ctx.matmul(x, [dw], [res], act=E.ACT_F32)[0]
+            assert bits_equal(got, O.cpu_matmul(x, [w], [res], act_quant=False)[0]), f"T={T}"
+        dw.free()
