@@ -37,3 +37,17 @@ def test_elmh_fails_cleanly_without_device():
     assert lib.elmh_synchronize(None) == elmh.ERR_ARG
     assert lib.elmh_matmul(None, None, 1, 32, 0, None, None, None, 1, 0) == elmh.ERR_ARG
     assert b"null" in lib.elmh_last_error(None)
+
+
+@pytest.mark.skipif(not os.path.isdir("/root/reference/include/edgelm"), reason="edgelm's headers are not on this host")
+def test_hip_backend_compiles_against_edgelm_headers():
+    """The delegate's Backend (edgelm_amd/host/src/hip_backend.cpp) is the file a maintainer drops
+    into edgelm's src/: it must compile against edgelm's own headers, not only against the
+    restated ones the host runtime here uses."""
+    import shutil
+    import subprocess
+    cxx = shutil.which("g++") or "g++"
+    src = os.path.join(ROOT, "edgelm_amd", "host", "src", "hip_backend.cpp")
+    p = subprocess.run([cxx, "-std=c++17", "-fsyntax-only", "-Wall", "-Wextra", "-Werror",
+                        "-I/root/reference/include", f"-I{INCLUDE}", src], capture_output=True, text=True)
+    assert p.returncode == 0, p.stderr
