@@ -458,9 +458,15 @@ def main():
         extra["gemv_8b_w4a8"] = sweep_8b(ctx, E, eager=args.eager)
     if not args.no_gemm:
         sm = [(D + 2 * KV, D), (HID, D), (D, HID), (VOCAB, D)]
+        b8 = [(4096, 4096), (14336, 4096), (4096, 14336)]
+        # W8A8, int8 per-channel weights, per-token int8 activations (ELMH_ACT_INT8_TOKEN)
+        extra["gemm_w8a8_token_T128"] = gemm_bench(ctx, E, 128, sm, act=E.ACT_INT8_TOKEN, eager=args.eager)
+        extra["gemm_w8a8_token_T512_8b"] = gemm_bench(ctx, E, 512, b8, act=E.ACT_INT8_TOKEN, eager=args.eager)
+        # edgelm's parity mode: per-32-block activation scales, block-order f32 rescale (VALU-bound)
         extra["gemm_w8a8_T128"] = gemm_bench(ctx, E, 128, sm, eager=args.eager)
-        extra["gemm_w8a8_T512_8b"] = gemm_bench(ctx, E, 512, [(4096, 4096), (14336, 4096), (4096, 14336)],
-                                                eager=args.eager)
+        extra["gemm_w8a8_T512_8b"] = gemm_bench(ctx, E, 512, b8, eager=args.eager)
+        # W4A8 prefill (the e2e model's layers), parity mode
+        extra["gemm_w4a8_T512_8b"] = gemm_bench(ctx, E, 512, b8, dt=2, eager=args.eager)
     if not args.no_e2e:
         import tempfile
         ctx.close()  # the session opens its own context

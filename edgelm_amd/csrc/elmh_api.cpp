@@ -189,7 +189,7 @@ int run_gemm_group(elmh_ctx* c, const int8_t* xq, const float* xd, int T, int Tp
     for (size_t j = 0; j < n; ++j) {
       const DevWeight& wd = w[idx[i0 + j]]->w;
       a.tg[j] = {wd.data, wd.scales, y[idx[i0 + j]], res ? res[idx[i0 + j]] : nullptr, (int)wd.rows,
-                 (int)(wd.rows_pad / kGemmTileN)};
+                 (int)((wd.rows_pad + kGemmTileN - 1) / kGemmTileN)};
       a.tile_start[j] = tiles;
       tiles += a.tg[j].ntiles;
     }
@@ -375,7 +375,7 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
   int Tpad;
   if ((rc = quant_frag(c, x, T, K, token, &Tpad))) return rc;
   GemmArgs a{};
-  const int tiles = (int)(g.rows_pad / kGemmTileN);
+  const int tiles = (int)((g.rows_pad + kGemmTileN - 1) / kGemmTileN);
   a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, tiles};
   a.tg[1] = {u.data, u.scales, y, nullptr, (int)u.rows, tiles};
   a.n_targets = 2;

@@ -9,8 +9,8 @@ namespace elmh {
 constexpr int kBlock = 32;       // activation block / q4 group (edgelm kActBlock, kernels.hpp:38)
 constexpr int kMaxTargets = 4;   // weights per kernel launch (MATMUL_N with more is split)
 constexpr int kGemvThreads = 256;
-constexpr int kGemmTileN = 64;   // weight rows per GEMM workgroup
-constexpr int kGemmTileT = 64;   // tokens per GEMM workgroup
+constexpr int kGemmTileN = 128;  // weight rows per GEMM workgroup
+constexpr int kGemmTileT = 128;  // tokens per GEMM workgroup
 constexpr int kPadRows = 64;     // rows_pad is a multiple of this
 
 enum WDType { WQ8 = 1, WQ4 = 2 };
@@ -66,7 +66,7 @@ struct GemmTarget {
   float* y;
   const float* res;
   int N;
-  int ntiles;  // rows_pad / kGemmTileN
+  int ntiles;  // ceil(rows_pad / kGemmTileN)
 };
 
 struct GemmArgs {

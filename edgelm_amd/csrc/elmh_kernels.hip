@@ -560,163 +560,286 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
 
 // ---------------------------------------------------------------- int8 MFMA GEMM (prefill)
 //
-// Workgroup = 4 waves computing a 64-row x 64-token output tile; each wave one 32x32 MFMA tile
-// (A = weight rows, B = tokens, so a lane owns one token and 16 rows of the accumulator).
-// v_mfma_i32_32x32x32_i8 covers exactly one 32-block along K, so the block's int32 sums come out
-// whole and the per-block f32 rescale runs on them in block order.
+// Workgroup = 4 waves over a 128-token x 128-row output tile; each wave owns a 64 x 64 quarter as
+// 2 x 2 v_mfma_i32_32x32x32_i8 tiles with A = tokens and B = weight rows (a lane owns one output
+// row of each tile, so the stores run along the row). K advances two 32-blocks per LDS stage,
+// double buffered: the next stage's global loads are in flight while the current stage's MFMAs
+// run, and one barrier per stage separates them. One MFMA spans exactly one 32-block along K, so
+// in the block-scale modes each block's int32 sums come out whole and are rescaled in block order
+// (edgelm's scalar order: multiply then add, or one fused multiply-add in FAST mode); in the
+// per-token q8 mode the int32 sums accumulate across all of K and one rescale finishes.
+// Workgroups are numbered so that each XCD (workgroup index mod 8) takes a contiguous range of
+// (row tile, token tile) pairs, token tile fastest: an XCD's L2 keeps its own weight rows.
 
-template <int WDT>
-__device__ __forceinline__ v4i load_a_frag(const uint8_t* __restrict__ data, int64_t item, int h) {
-  if (WDT == WQ8) {
-    const uint4 w = *reinterpret_cast<const uint4*>(data + item * 32 + h * 16);
-    v4i r;
-    r.x = (int)w.x;
-    r.y = (int)w.y;
-    r.z = (int)w.z;
-    r.w = (int)w.w;
-    return r;
-  } else {
-    return q4_operand16(*reinterpret_cast<const uint4*>(data + item * 16), h);
-  }
+constexpr int kGKS = 2;  // 32-blocks per LDS stage
+static_assert(kGemmTileT == 128 && kGemmTileN == 128, "GEMM tile");
+
+// Target ti (uniform) of a GEMM launch read through the kernel-argument segment pointer.
+__device__ __forceinline__ GemmTarget gemm_target_at(int ti) {
+  typedef const GemmArgs __attribute__((address_space(4)))* KernArgs;
+  const KernArgs ka = (KernArgs)__builtin_amdgcn_kernarg_segment_ptr();
+  GemmTarget t;
+  t.data = pin_global(ka->tg[ti].data);
+  t.scales = pin_global(ka->tg[ti].scales);
+  t.y = pin_global(ka->tg[ti].y);
+  t.res = pin_global(ka->tg[ti].res);
+  t.N = ka->tg[ti].N;
+  t.ntiles = ka->tg[ti].ntiles;
+  return t;
 }
 
 template <int WDT, bool SW, bool TOK>
 __global__ __launch_bounds__(256) void gemm_a8_kernel(const GemmArgs a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wn = wave & 1, wt = wave >> 1;
-  int ti = 0, ntile = blockIdx.x;
-  if (!SW) {
-    while (ti + 1 < a.n_targets && (int)blockIdx.x >= a.tile_start[ti + 1]) ++ti;
-    ntile = blockIdx.x - a.tile_start[ti];
-  }
-  const GemmTarget& tg = a.tg[SW ? 0 : ti];
+  constexpr int NSEL = SW ? 2 : 1;
+  constexpr int WB = WDT == WQ8 ? 2 * kGemmTileN * 16 : kGemmTileN * 16;  // weight bytes per block
+  constexpr bool BLOCKX = !TOK;                                             // per-block activation scales
+  // LDS: the double-buffered stages; after the K loop the SwiGLU epilogue reuses the space
+  struct Stages {
+    int8_t act[2][kGKS][2][kGemmTileT][16];
+    uint8_t w[2][NSEL][kGKS][WB];
+    float xd[2][kGKS][kGemmTileT];
+    float ws[2][NSEL][kGKS][kGemmTileN];
+  };
+  constexpr int kEpBytes = SW ? 4 * 2 * 32 * 32 * 4 : 16;  // per wave: gate and up of one 32x32 tile
+  __shared__ __align__(16) unsigned char Lraw[sizeof(Stages) > kEpBytes ? sizeof(Stages) : kEpBytes];
+  Stages& L = *reinterpret_cast<Stages*>(Lraw);
+  auto& Lact = L.act;
+  auto& Lw = L.w;
+  auto& Lxd = L.xd;
+  auto& Lws = L.ws;
+
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wt = wave >> 1, wr = wave & 1;
   const int nb = a.nb, H = a.H;
-  const int l32 = lane & 31, h = lane >> 5;
-  const int n0 = ntile * kGemmTileN + wn * 32;
-  const int t0 = blockIdx.y * kGemmTileT + wt * 32;
-  const int n = n0 + l32;  // the A row this lane supplies
-  const int64_t nbase = (int64_t)(n / H) * nb * H + (n % H);
-  const int8_t* bsrc = a.xq + ((int64_t)(t0 >> 5) * nb * 64 + lane) * 16;
-  const int tcol = t0 + l32;  // the token this lane's accumulators belong to
-  // rows of accumulator i: n0 + 8*(i/4) + 4*h + i%4; scale items of rows nr, nr + 1 and of rows
-  // nr + 2, nr + 3 (each pair shares a row tile: H >= 2 and nr is a multiple of 4)
-  int64_t sbase[4], sbase2[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int nr = n0 + 8 * j + 4 * h;
-    sbase[j] = item_index(nr, 0, nb, H);
-    sbase2[j] = item_index(nr + 2, 0, nb, H);
-  }
+  // workgroup -> (row tile, token tile)
+  const int n = pin_sgpr(a.n_targets);
+  const int ts1 = pin_sgpr(a.tile_start[1]), ts2 = pin_sgpr(a.tile_start[2]), ts3 = pin_sgpr(a.tile_start[3]);
+  const int ts4 = pin_sgpr(a.tile_start[4]);
+  const int rtn = SW ? a.tg[0].ntiles : n == 1 ? ts1 : n == 2 ? ts2 : n == 3 ? ts3 : ts4;  // row tiles in all
+  const int ntt = a.Tpad / kGemmTileT;
+  const int total = rtn * ntt, chunk = (total + 7) >> 3;
+  const int id = (int)(blockIdx.x & 7) * chunk + (int)(blockIdx.x >> 3);
+  if (id >= total) return;
+  int rt = id / ntt;
+  const int tt = id - rt * ntt;
+  const int ti = SW ? 0 : (n > 1 && rt >= ts1) + (n > 2 && rt >= ts2) + (n > 3 && rt >= ts3);
+  rt -= ti == 0 ? 0 : ti == 1 ? ts1 : ti == 2 ? ts2 : ts3;
+  const GemmTarget tg = SW ? a.tg[0] : gemm_target_at(ti);
+  const int r0 = rt * kGemmTileN, t0 = tt * kGemmTileT;
+  const int rows_pad = (tg.N + kPadRows - 1) / kPadRows * kPadRows;  // the weight's padded rows
+  auto wdata = [&](int s) { return SW && s ? a.tg[1].data : tg.data; };
+  auto wscal = [&](int s) { return SW && s ? a.tg[1].scales : tg.scales; };
 
-  float acc[16], accu[16];
-  v16i iacc, iaccu;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    acc[i] = 0.f;
-    accu[i] = 0.f;
-    iacc[i] = 0;
-    iaccu[i] = 0;
-  }
-  const v16i zero = iacc;
+  // per-thread load assignments
+  const int lrow = tid & (kGemmTileN - 1), lhi = tid >> 7;  // weight row of the tile, half / block
+  const int wrow = min(r0 + lrow, rows_pad - 1);
+  const int64_t rbase = (int64_t)(wrow / H) * nb * H + (wrow % H);  // item of (wrow, block 0)
+  const int ac = tid >> 6, aw = tid & 63;                          // activation: token group, lane slot
 
-  v4i A = load_a_frag<WDT>(tg.data, nbase, h);
-  v4i Au = SW ? load_a_frag<WDT>(a.tg[1].data, nbase, h) : A;
-  v4i B = *reinterpret_cast<const v4i*>(bsrc);
-  for (int b = 0; b < nb; ++b) {
-    // prefetch the next block's fragments
-    v4i An = A, Aun = Au, Bn = B;
-    if (b + 1 < nb) {
-      An = load_a_frag<WDT>(tg.data, nbase + (int64_t)(b + 1) * H, h);
-      if (SW) Aun = load_a_frag<WDT>(a.tg[1].data, nbase + (int64_t)(b + 1) * H, h);
-      Bn = *reinterpret_cast<const v4i*>(bsrc + (int64_t)(b + 1) * 1024);
-    }
-    if (TOK && WDT == WQ8) {
-      iacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, iacc, 0, 0, 0);
-      if (SW) iaccu = __builtin_amdgcn_mfma_i32_32x32x32_i8(Au, B, iaccu, 0, 0, 0);
+  // staging registers of one stage (named values: arrays here end up in scratch memory)
+  static_assert(kGKS == 2, "two blocks per stage");
+  uint4 ra0, ra1, rw00, rw01, rw10, rw11;
+  float rws0 = 0.f, rws1 = 0.f, rxd = 0.f;
+  auto gload = [&](int b0) {
+    const int bb0 = min(b0, nb - 1), bb1 = min(b0 + 1, nb - 1);
+    const int8_t* xs = a.xq + (((int64_t)(t0 >> 5) + ac) * nb) * 1024 + aw * 16;
+    ra0 = *reinterpret_cast<const uint4*>(xs + (int64_t)bb0 * 1024);
+    ra1 = *reinterpret_cast<const uint4*>(xs + (int64_t)bb1 * 1024);
+    if (WDT == WQ8) {
+      rw00 = *reinterpret_cast<const uint4*>(wdata(0) + (rbase + (int64_t)bb0 * H) * 32 + lhi * 16);
+      rw01 = *reinterpret_cast<const uint4*>(wdata(0) + (rbase + (int64_t)bb1 * H) * 32 + lhi * 16);
+      if (SW) {
+        rw10 = *reinterpret_cast<const uint4*>(wdata(1) + (rbase + (int64_t)bb0 * H) * 32 + lhi * 16);
+        rw11 = *reinterpret_cast<const uint4*>(wdata(1) + (rbase + (int64_t)bb1 * H) * 32 + lhi * 16);
+      }
     } else {
-      const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, zero, 0, 0, 0);
-      v16i Su = zero;
-      if (SW) Su = __builtin_amdgcn_mfma_i32_32x32x32_i8(Au, B, zero, 0, 0, 0);
-      if (WDT == WQ8) {  // block mode: p = float(S) * xd[t,b]
-        const float xdv = a.xd[(int64_t)b * a.Tpad + tcol];
+      const int64_t it = rbase + (int64_t)min(b0 + lhi, nb - 1) * H;
+      rw00 = *reinterpret_cast<const uint4*>(wdata(0) + it * 16);
+      rws0 = wscal(0)[it];
+      if (SW) {
+        rw10 = *reinterpret_cast<const uint4*>(wdata(1) + it * 16);
+        rws1 = wscal(1)[it];
+      }
+    }
+    if (BLOCKX) rxd = a.xd[(int64_t)min(b0 + lhi, nb - 1) * a.Tpad + t0 + lrow];
+  };
+  auto lstore = [&](int buf) {
+    *reinterpret_cast<uint4*>(&Lact[buf][0][aw >> 5][ac * 32 + (aw & 31)][0]) = ra0;
+    *reinterpret_cast<uint4*>(&Lact[buf][1][aw >> 5][ac * 32 + (aw & 31)][0]) = ra1;
+    if (WDT == WQ8) {
+      *reinterpret_cast<uint4*>(&Lw[buf][0][0][(lhi * kGemmTileN + lrow) * 16]) = rw00;
+      *reinterpret_cast<uint4*>(&Lw[buf][0][1][(lhi * kGemmTileN + lrow) * 16]) = rw01;
+      if (SW) {
+        *reinterpret_cast<uint4*>(&Lw[buf][NSEL - 1][0][(lhi * kGemmTileN + lrow) * 16]) = rw10;
+        *reinterpret_cast<uint4*>(&Lw[buf][NSEL - 1][1][(lhi * kGemmTileN + lrow) * 16]) = rw11;
+      }
+    } else {
+      *reinterpret_cast<uint4*>(&Lw[buf][0][lhi][lrow * 16]) = rw00;
+      Lws[buf][0][lhi][lrow] = rws0;
+      if (SW) {
+        *reinterpret_cast<uint4*>(&Lw[buf][NSEL - 1][lhi][lrow * 16]) = rw10;
+        Lws[buf][NSEL - 1][lhi][lrow] = rws1;
+      }
+    }
+    if (BLOCKX) Lxd[buf][lhi][lrow] = rxd;
+  };
+
+  v16i iacc[NSEL][2][2];
+  float facc[NSEL][2][2][16];
+#pragma unroll
+  for (int s = 0; s < NSEL; ++s)
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          if (a.fast) {
-            acc[i] = __builtin_fmaf((float)S[i], xdv, acc[i]);
-            if (SW) accu[i] = __builtin_fmaf((float)Su[i], xdv, accu[i]);
-          } else {
-            acc[i] = acc[i] + (float)S[i] * xdv;
-            if (SW) accu[i] = accu[i] + (float)Su[i] * xdv;
-          }
+          iacc[s][mt][nt][i] = 0;
+          facc[s][mt][nt][i] = 0.f;
         }
-      } else {  // q4: S holds 16*S_b; scales hold ws/16
-        const float xdv = TOK ? 1.0f : a.xd[(int64_t)b * a.Tpad + tcol];
+  v16i zero;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t o1 = sbase[j] + (int64_t)b * H, o2 = sbase2[j] + (int64_t)b * H;
-          const float2 ws01 = *reinterpret_cast<const float2*>(tg.scales + o1);
-          const float2 ws23 = *reinterpret_cast<const float2*>(tg.scales + o2);
-          float2 wu01 = ws01, wu23 = ws23;
-          if (SW) {
-            wu01 = *reinterpret_cast<const float2*>(a.tg[1].scales + o1);
-            wu23 = *reinterpret_cast<const float2*>(a.tg[1].scales + o2);
-          }
-          const float wsv[4] = {ws01.x, ws01.y, ws23.x, ws23.y};
-          const float wuv[4] = {wu01.x, wu01.y, wu23.x, wu23.y};
+  for (int i = 0; i < 16; ++i) zero[i] = 0;
+
+  const int nstage = (nb + kGKS - 1) / kGKS;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int st = 0; st < nstage; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nstage) gload((st + 1) * kGKS);
+    const int nvalid = min(kGKS, nb - st * kGKS);
+    for (int kb = 0; kb < nvalid; ++kb) {
+      {
+        v4i A[2];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int i = j * 4 + e;
-            const float c = TOK ? wsv[e] : wsv[e] * xdv;
-            if (a.fast) {
-              acc[i] = __builtin_fmaf((float)S[i], c, acc[i]);
+        for (int mt = 0; mt < 2; ++mt) A[mt] = *reinterpret_cast<const v4i*>(&Lact[buf][kb][h][wt * 64 + mt * 32 + l32][0]);
+#pragma unroll
+        for (int s = 0; s < NSEL; ++s) {
+          v4i B[2];
+          float c[2] = {1.f, 1.f};
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            const int rl = wr * 64 + nt * 32 + l32;
+            if (WDT == WQ8) {
+              B[nt] = *reinterpret_cast<const v4i*>(&Lw[buf][s][kb][(h * kGemmTileN + rl) * 16]);
             } else {
-              acc[i] = acc[i] + (float)S[i] * c;
+              B[nt] = q4_operand16(*reinterpret_cast<const uint4*>(&Lw[buf][s][kb][rl * 16]), h);
+              c[nt] = Lws[buf][s][kb][rl];
             }
-            if (SW) {
-              const float cu = TOK ? wuv[e] : wuv[e] * xdv;
-              if (a.fast) {
-                accu[i] = __builtin_fmaf((float)Su[i], cu, accu[i]);
+          }
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt) {
+            float xv[16];
+            if (BLOCKX) {
+#pragma unroll
+              for (int g = 0; g < 4; ++g) {
+                const float4 x4 = *reinterpret_cast<const float4*>(&Lxd[buf][kb][wt * 64 + mt * 32 + 8 * g + 4 * h]);
+                xv[4 * g] = x4.x;
+                xv[4 * g + 1] = x4.y;
+                xv[4 * g + 2] = x4.z;
+                xv[4 * g + 3] = x4.w;
+              }
+            }
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+              if (TOK && WDT == WQ8) {
+                iacc[s][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[mt], B[nt], iacc[s][mt][nt], 0, 0, 0);
               } else {
-                accu[i] = accu[i] + (float)Su[i] * cu;
+                const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[mt], B[nt], zero, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                  // q8: p = float(S) * xd; q4 (S = 16 * S_b, c = ws / 16): p = float(S) * (c * xd)
+                  const float m = WDT == WQ8 ? xv[i] : BLOCKX ? c[nt] * xv[i] : c[nt];
+                  if (a.fast) {
+                    facc[s][mt][nt][i] = __builtin_fmaf((float)S[i], m, facc[s][mt][nt][i]);
+                  } else {
+                    facc[s][mt][nt][i] = facc[s][mt][nt][i] + (float)S[i] * m;
+                  }
+                }
               }
             }
           }
         }
       }
     }
-    A = An;
-    Au = Aun;
-    B = Bn;
+    if (st + 1 < nstage) lstore(buf ^ 1);
+    __syncthreads();
   }
 
-  if (tcol >= a.T) return;
-  const float xdt = TOK ? a.xd[tcol] : 1.0f;
+  // epilogue: row r (lane), tokens t (accumulator index)
+  if (SW) {
+    // gate and up of each 32x32 tile go through this wave's LDS slice, so that silu (an expf)
+    // is emitted once in a loop rather than once per accumulator
+    float* const ep = reinterpret_cast<float*>(Lraw) + wave * (2 * 32 * 32);
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+    for (int nt = 0; nt < 2; ++nt) {
+      const int r = r0 + wr * 64 + nt * 32 + l32;
+      const int rc = min(r, tg.N - 1);
+      const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
+      const float wsu = WDT == WQ8 ? a.tg[1].scales[rc] : 1.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = j * 4 + e;
-      const int nr = n0 + 8 * j + 4 * h + e;
-      if (nr >= tg.N) continue;
-      float out;
-      if (WDT == WQ8) {
-        out = TOK ? ((float)iacc[i] * xdt) * tg.scales[nr] : acc[i] * tg.scales[nr];
-      } else {
-        out = TOK ? acc[i] * xdt : acc[i];
-      }
-      if (SW) {
-        float up;
-        if (WDT == WQ8) {
-          up = TOK ? ((float)iaccu[i] * xdt) * a.tg[1].scales[nr] : accu[i] * a.tg[1].scales[nr];
-        } else {
-          up = TOK ? accu[i] * xdt : accu[i];
+      for (int mt = 0; mt < 2; ++mt) {
+        const int tb = t0 + wt * 64 + mt * 32 + 4 * h;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int t = tb + 8 * (i >> 2) + (i & 3);
+          const float xdt = TOK ? a.xd[min(t, a.Tpad - 1)] : 1.f;
+          float g, u;
+          if (WDT == WQ8) {
+            g = TOK ? ((float)iacc[0][mt][nt][i] * xdt) * ws : facc[0][mt][nt][i] * ws;
+            u = TOK ? ((float)iacc[NSEL - 1][mt][nt][i] * xdt) * wsu : facc[NSEL - 1][mt][nt][i] * wsu;
+          } else {
+            g = TOK ? facc[0][mt][nt][i] * xdt : facc[0][mt][nt][i];
+            u = TOK ? facc[NSEL - 1][mt][nt][i] * xdt : facc[NSEL - 1][mt][nt][i];
+          }
+          ep[i * 64 + lane] = g;
+          ep[1024 + i * 64 + lane] = u;
         }
-        out = silu_exact(out) * up;
-      } else if (tg.res) {
-        out = out + tg.res[(int64_t)tcol * tg.N + nr];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll 1
+        for (int i = 0; i < 16; ++i) {
+          const int t = tb + 8 * (i >> 2) + (i & 3);
+          const float out = silu_exact(ep[i * 64 + lane]) * ep[1024 + i * 64 + lane];
+          if (r < tg.N && t < a.T) tg.y[(int64_t)t * tg.N + r] = out;
+        }
+        __builtin_amdgcn_wave_barrier();
       }
-      tg.y[(int64_t)tcol * tg.N + nr] = out;
     }
+    return;
+  }
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int r = r0 + wr * 64 + nt * 32 + l32;
+    const int rc = min(r, tg.N - 1);
+    const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
+    const float wsu = WDT == WQ8 && SW ? a.tg[1].scales[rc] : 1.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int t = t0 + wt * 64 + mt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        const float xdt = TOK ? a.xd[min(t, a.Tpad - 1)] : 1.f;
+        float out;
+        if (WDT == WQ8) {
+          out = TOK ? ((float)iacc[0][mt][nt][i] * xdt) * ws : facc[0][mt][nt][i] * ws;
+        } else {
+          out = TOK ? facc[0][mt][nt][i] * xdt : facc[0][mt][nt][i];
+        }
+        if (SW) {
+          float up;
+          if (WDT == WQ8) {
+            up = TOK ? ((float)iacc[NSEL - 1][mt][nt][i] * xdt) * wsu : facc[NSEL - 1][mt][nt][i] * wsu;
+          } else {
+            up = TOK ? facc[NSEL - 1][mt][nt][i] * xdt : facc[NSEL - 1][mt][nt][i];
+          }
+          out = silu_exact(out) * up;
+        } else if (tg.res && r < tg.N && t < a.T) {
+          out = out + tg.res[(int64_t)t * tg.N + r];
+        }
+        if (r < tg.N && t < a.T) tg.y[(int64_t)t * tg.N + r] = out;
+      }
+  }
 }
 
 // ---------------------------------------------------------------- f32-activation paths
@@ -1039,8 +1162,11 @@ hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_ti
 
 template <int WDT, bool SW, bool TOK>
 static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
-  dim3 grid(tiles, a.Tpad / kGemmTileT);
-  gemm_a8_kernel<WDT, SW, TOK><<<grid, 256, 0, s>>>(a);
+  // one workgroup per (row tile, token tile), numbered in 8 XCD-contiguous ranges
+  if (a.Tpad % kGemmTileT || tiles < 1 || tiles != (SW ? a.tg[0].ntiles : a.tile_start[a.n_targets]))
+    return hipErrorInvalidValue;
+  const int total = tiles * (a.Tpad / kGemmTileT);
+  gemm_a8_kernel<WDT, SW, TOK><<<(total + 7) / 8 * 8, 256, 0, s>>>(a);
   return hipGetLastError();
 }
 
