@@ -562,7 +562,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
 //
 // Workgroup = 4 waves over a 128-token x 128-row output tile; each wave owns a 64 x 64 quarter as
 // 2 x 2 v_mfma_i32_32x32x32_i8 tiles with A = tokens and B = weight rows (a lane owns one output
-// row of each tile, so the stores run along the row). K advances two 32-blocks per LDS stage,
+// row of each tile, so the stores run along the row). K advances four 32-blocks per LDS stage,
 // double buffered: the next stage's global loads are in flight while the current stage's MFMAs
 // run, and one barrier per stage separates them. One MFMA spans exactly one 32-block along K, so
 // in the block-scale modes each block's int32 sums come out whole and are rescaled in block order
@@ -571,8 +571,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
 // Workgroups are numbered so that each XCD (workgroup index mod 8) takes a contiguous range of
 // (row tile, token tile) pairs, token tile fastest: an XCD's L2 keeps its own weight rows.
 
-constexpr int kGKS = 2;  // 32-blocks per LDS stage
-static_assert(kGemmTileT == 128 && kGemmTileN == 128, "GEMM tile");
+constexpr int kGKS = 4;  // 32-blocks per LDS stage
+static_assert(kGemmTileT == 128 && kGemmTileN == 128, "GEMM tile: the token padding covers both tile heights");
 
 // Target ti (uniform) of a GEMM launch read through the kernel-argument segment pointer.
 __device__ __forceinline__ GemmTarget gemm_target_at(int ti) {
@@ -588,20 +588,25 @@ __device__ __forceinline__ GemmTarget gemm_target_at(int ti) {
   return t;
 }
 
-template <int WDT, bool SW, bool TOK>
-__global__ __launch_bounds__(256) void gemm_a8_kernel(const GemmArgs a) {
+template <int WDT, bool SW, bool TOK, bool FAST, int MT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT == 2 ? 1 : 2))) void gemm_a8_kernel(
+    const GemmArgs a) {
+  constexpr int TT = 64 * MT;  // tokens per workgroup: 2 waves x MT 32-token MFMA tiles
   constexpr int NSEL = SW ? 2 : 1;
   constexpr int WB = WDT == WQ8 ? 2 * kGemmTileN * 16 : kGemmTileN * 16;  // weight bytes per block
   constexpr bool BLOCKX = !TOK;                                             // per-block activation scales
   // LDS: the double-buffered stages; after the K loop the SwiGLU epilogue reuses the space
+  constexpr int XDN = BLOCKX ? TT : 1;                                      // unused scales take 1 slot
+  constexpr int WSN = WDT == WQ4 ? kGemmTileN : 1;
   struct Stages {
-    int8_t act[2][kGKS][2][kGemmTileT][16];
+    int8_t act[2][kGKS][2][TT][16];
     uint8_t w[2][NSEL][kGKS][WB];
-    float xd[2][kGKS][kGemmTileT];
-    float ws[2][NSEL][kGKS][kGemmTileN];
+    float xd[2][kGKS][XDN];
+    float ws[2][NSEL][kGKS][WSN];
   };
   constexpr int kEpBytes = SW ? 4 * 2 * 32 * 32 * 4 : 16;  // per wave: gate and up of one 32x32 tile
   __shared__ __align__(16) unsigned char Lraw[sizeof(Stages) > kEpBytes ? sizeof(Stages) : kEpBytes];
+  __shared__ __align__(16) float Lxdt[TOK ? TT : 4];
   Stages& L = *reinterpret_cast<Stages*>(Lraw);
   auto& Lact = L.act;
   auto& Lw = L.w;
@@ -616,7 +621,7 @@ __global__ __launch_bounds__(256) void gemm_a8_kernel(const GemmArgs a) {
   const int ts1 = pin_sgpr(a.tile_start[1]), ts2 = pin_sgpr(a.tile_start[2]), ts3 = pin_sgpr(a.tile_start[3]);
   const int ts4 = pin_sgpr(a.tile_start[4]);
   const int rtn = SW ? a.tg[0].ntiles : n == 1 ? ts1 : n == 2 ? ts2 : n == 3 ? ts3 : ts4;  // row tiles in all
-  const int ntt = a.Tpad / kGemmTileT;
+  const int ntt = (a.T + TT - 1) / TT;  // token tiles: each starts below T
   const int total = rtn * ntt, chunk = (total + 7) >> 3;
   const int id = (int)(blockIdx.x & 7) * chunk + (int)(blockIdx.x >> 3);
   if (id >= total) return;
@@ -625,7 +630,7 @@ __global__ __launch_bounds__(256) void gemm_a8_kernel(const GemmArgs a) {
   const int ti = SW ? 0 : (n > 1 && rt >= ts1) + (n > 2 && rt >= ts2) + (n > 3 && rt >= ts3);
   rt -= ti == 0 ? 0 : ti == 1 ? ts1 : ti == 2 ? ts2 : ts3;
   const GemmTarget tg = SW ? a.tg[0] : gemm_target_at(ti);
-  const int r0 = rt * kGemmTileN, t0 = tt * kGemmTileT;
+  const int r0 = rt * kGemmTileN, t0 = tt * TT;
   const int rows_pad = (tg.N + kPadRows - 1) / kPadRows * kPadRows;  // the weight's padded rows
   auto wdata = [&](int s) { return SW && s ? a.tg[1].data : tg.data; };
   auto wscal = [&](int s) { return SW && s ? a.tg[1].scales : tg.scales; };
@@ -634,62 +639,115 @@ __global__ __launch_bounds__(256) void gemm_a8_kernel(const GemmArgs a) {
   const int lrow = tid & (kGemmTileN - 1), lhi = tid >> 7;  // weight row of the tile, half / block
   const int wrow = min(r0 + lrow, rows_pad - 1);
   const int64_t rbase = (int64_t)(wrow / H) * nb * H + (wrow % H);  // item of (wrow, block 0)
-  const int ac = tid >> 6, aw = tid & 63;                          // activation: token group, lane slot
+  // activation: token group ac of the tile, lane slot aw; with 64-token tiles a thread loads blocks
+  // akb and akb + 2 of each stage, with 128-token tiles all four
+  const int ac = MT == 2 ? tid >> 6 : (tid >> 6) & 1, aw = tid & 63, akb = MT == 2 ? 0 : tid >> 7;
 
   // staging registers of one stage (named values: arrays here end up in scratch memory)
-  static_assert(kGKS == 2, "two blocks per stage");
-  uint4 ra0, ra1, rw00, rw01, rw10, rw11;
-  float rws0 = 0.f, rws1 = 0.f, rxd = 0.f;
+  static_assert(kGKS == 4, "four blocks per stage");
+  uint4 ra0, ra1, ra2, ra3, rw00, rw01, rw02, rw03, rw10, rw11, rw12, rw13;
+  float rws00 = 0.f, rws01 = 0.f, rws10 = 0.f, rws11 = 0.f, rxd0 = 0.f, rxd1 = 0.f;
   auto gload = [&](int b0) {
-    const int bb0 = min(b0, nb - 1), bb1 = min(b0 + 1, nb - 1);
     const int8_t* xs = a.xq + (((int64_t)(t0 >> 5) + ac) * nb) * 1024 + aw * 16;
-    ra0 = *reinterpret_cast<const uint4*>(xs + (int64_t)bb0 * 1024);
-    ra1 = *reinterpret_cast<const uint4*>(xs + (int64_t)bb1 * 1024);
+    auto la = [&](uint4& r, int b) { r = *reinterpret_cast<const uint4*>(xs + (int64_t)min(b, nb - 1) * 1024); };
+    if (MT == 2) {
+      la(ra0, b0);
+      la(ra1, b0 + 1);
+      la(ra2, b0 + 2);
+      la(ra3, b0 + 3);
+    } else {
+      la(ra0, b0 + akb);
+      la(ra1, b0 + akb + 2);
+    }
     if (WDT == WQ8) {
-      rw00 = *reinterpret_cast<const uint4*>(wdata(0) + (rbase + (int64_t)bb0 * H) * 32 + lhi * 16);
-      rw01 = *reinterpret_cast<const uint4*>(wdata(0) + (rbase + (int64_t)bb1 * H) * 32 + lhi * 16);
+      // q8: thread (lhi = half, lrow) loads that half of blocks b0..b0+3
+      auto lw = [&](uint4& r, int sl, int b) {
+        r = *reinterpret_cast<const uint4*>(wdata(sl) + (rbase + (int64_t)min(b, nb - 1) * H) * 32 + lhi * 16);
+      };
+      lw(rw00, 0, b0);
+      lw(rw01, 0, b0 + 1);
+      lw(rw02, 0, b0 + 2);
+      lw(rw03, 0, b0 + 3);
       if (SW) {
-        rw10 = *reinterpret_cast<const uint4*>(wdata(1) + (rbase + (int64_t)bb0 * H) * 32 + lhi * 16);
-        rw11 = *reinterpret_cast<const uint4*>(wdata(1) + (rbase + (int64_t)bb1 * H) * 32 + lhi * 16);
+        lw(rw10, 1, b0);
+        lw(rw11, 1, b0 + 1);
+        lw(rw12, 1, b0 + 2);
+        lw(rw13, 1, b0 + 3);
       }
     } else {
-      const int64_t it = rbase + (int64_t)min(b0 + lhi, nb - 1) * H;
-      rw00 = *reinterpret_cast<const uint4*>(wdata(0) + it * 16);
-      rws0 = wscal(0)[it];
+      // q4: thread (lhi, lrow) loads blocks b0 + lhi and b0 + lhi + 2 (16 B and a scale each)
+      auto lw = [&](uint4& r, float& c, int sl, int b) {
+        const int64_t it = rbase + (int64_t)min(b, nb - 1) * H;
+        r = *reinterpret_cast<const uint4*>(wdata(sl) + it * 16);
+        c = wscal(sl)[it];
+      };
+      lw(rw00, rws00, 0, b0 + lhi);
+      lw(rw01, rws01, 0, b0 + lhi + 2);
       if (SW) {
-        rw10 = *reinterpret_cast<const uint4*>(wdata(1) + it * 16);
-        rws1 = wscal(1)[it];
+        lw(rw10, rws10, 1, b0 + lhi);
+        lw(rw11, rws11, 1, b0 + lhi + 2);
       }
     }
-    if (BLOCKX) rxd = a.xd[(int64_t)min(b0 + lhi, nb - 1) * a.Tpad + t0 + lrow];
+    if (BLOCKX && MT == 2) {  // 4 blocks x 128 tokens: blocks lhi and lhi + 2, token lrow
+      rxd0 = a.xd[(int64_t)min(b0 + lhi, nb - 1) * a.Tpad + t0 + lrow];
+      rxd1 = a.xd[(int64_t)min(b0 + lhi + 2, nb - 1) * a.Tpad + t0 + lrow];
+    } else if (BLOCKX) {      // 4 blocks x 64 tokens: block tid / 64, token tid % 64
+      rxd0 = a.xd[(int64_t)min(b0 + (tid >> 6), nb - 1) * a.Tpad + t0 + (tid & 63)];
+    }
   };
   auto lstore = [&](int buf) {
-    *reinterpret_cast<uint4*>(&Lact[buf][0][aw >> 5][ac * 32 + (aw & 31)][0]) = ra0;
-    *reinterpret_cast<uint4*>(&Lact[buf][1][aw >> 5][ac * 32 + (aw & 31)][0]) = ra1;
+    auto sa = [&](const uint4& r, int kb) {
+      *reinterpret_cast<uint4*>(&Lact[buf][kb][aw >> 5][ac * 32 + (aw & 31)][0]) = r;
+    };
+    if (MT == 2) {
+      sa(ra0, 0);
+      sa(ra1, 1);
+      sa(ra2, 2);
+      sa(ra3, 3);
+    } else {
+      sa(ra0, akb);
+      sa(ra1, akb + 2);
+    }
     if (WDT == WQ8) {
-      *reinterpret_cast<uint4*>(&Lw[buf][0][0][(lhi * kGemmTileN + lrow) * 16]) = rw00;
-      *reinterpret_cast<uint4*>(&Lw[buf][0][1][(lhi * kGemmTileN + lrow) * 16]) = rw01;
+      auto sw = [&](const uint4& r, int sl, int kb) {
+        *reinterpret_cast<uint4*>(&Lw[buf][sl][kb][(lhi * kGemmTileN + lrow) * 16]) = r;
+      };
+      sw(rw00, 0, 0);
+      sw(rw01, 0, 1);
+      sw(rw02, 0, 2);
+      sw(rw03, 0, 3);
       if (SW) {
-        *reinterpret_cast<uint4*>(&Lw[buf][NSEL - 1][0][(lhi * kGemmTileN + lrow) * 16]) = rw10;
-        *reinterpret_cast<uint4*>(&Lw[buf][NSEL - 1][1][(lhi * kGemmTileN + lrow) * 16]) = rw11;
+        sw(rw10, NSEL - 1, 0);
+        sw(rw11, NSEL - 1, 1);
+        sw(rw12, NSEL - 1, 2);
+        sw(rw13, NSEL - 1, 3);
       }
     } else {
-      *reinterpret_cast<uint4*>(&Lw[buf][0][lhi][lrow * 16]) = rw00;
-      Lws[buf][0][lhi][lrow] = rws0;
+      auto sw = [&](const uint4& r, float c, int sl, int kb) {
+        *reinterpret_cast<uint4*>(&Lw[buf][sl][kb][lrow * 16]) = r;
+        Lws[buf][sl][kb][lrow] = c;
+      };
+      sw(rw00, rws00, 0, lhi);
+      sw(rw01, rws01, 0, lhi + 2);
       if (SW) {
-        *reinterpret_cast<uint4*>(&Lw[buf][NSEL - 1][lhi][lrow * 16]) = rw10;
-        Lws[buf][NSEL - 1][lhi][lrow] = rws1;
+        sw(rw10, rws10, NSEL - 1, lhi);
+        sw(rw11, rws11, NSEL - 1, lhi + 2);
       }
     }
-    if (BLOCKX) Lxd[buf][lhi][lrow] = rxd;
+    if (BLOCKX && MT == 2) {
+      Lxd[buf][lhi][lrow] = rxd0;
+      Lxd[buf][lhi + 2][lrow] = rxd1;
+    } else if (BLOCKX) {
+      Lxd[buf][tid >> 6][tid & 63] = rxd0;
+    }
   };
 
-  v16i iacc[NSEL][2][2];
-  float facc[NSEL][2][2][16];
+  v16i iacc[NSEL][MT][2];
+  float facc[NSEL][MT][2][16];
 #pragma unroll
   for (int s = 0; s < NSEL; ++s)
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
@@ -701,6 +759,62 @@ __global__ __launch_bounds__(256) void gemm_a8_kernel(const GemmArgs a) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) zero[i] = 0;
 
+  // one 32-block of the current stage: MT x 2 MFMAs per wave (per weight selection)
+  auto block = [&](int buf, int kb) {
+    v4i A[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) A[mt] = *reinterpret_cast<const v4i*>(&Lact[buf][kb][h][wt * 32 * MT + mt * 32 + l32][0]);
+#pragma unroll
+    for (int s = 0; s < NSEL; ++s) {
+      v4i B[2];
+      float c[2] = {1.f, 1.f};
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int rl = wr * 64 + nt * 32 + l32;
+        if (WDT == WQ8) {
+          B[nt] = *reinterpret_cast<const v4i*>(&Lw[buf][s][kb][(h * kGemmTileN + rl) * 16]);
+        } else {
+          B[nt] = q4_operand16(*reinterpret_cast<const uint4*>(&Lw[buf][s][kb][rl * 16]), h);
+          c[nt] = Lws[buf][s][kb][rl];
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float xv[16];
+        if (BLOCKX) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const float4 x4 = *reinterpret_cast<const float4*>(&Lxd[buf][kb][wt * 32 * MT + mt * 32 + 8 * g + 4 * h]);
+            xv[4 * g] = x4.x;
+            xv[4 * g + 1] = x4.y;
+            xv[4 * g + 2] = x4.z;
+            xv[4 * g + 3] = x4.w;
+          }
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          if (TOK && WDT == WQ8) {
+            iacc[s][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[mt], B[nt], iacc[s][mt][nt], 0, 0, 0);
+          } else {
+            const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[mt], B[nt], zero, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              // q8: p = float(S) * xd; q4 (S = 16 * S_b, c = ws / 16): p = float(S) * (c * xd)
+              const float m = WDT == WQ8 ? xv[i] : BLOCKX ? c[nt] * xv[i] : c[nt];
+              if (FAST) {
+                facc[s][mt][nt][i] = __builtin_fmaf((float)S[i], m, facc[s][mt][nt][i]);
+              } else {
+                facc[s][mt][nt][i] = facc[s][mt][nt][i] + (float)S[i] * m;
+              }
+            }
+          }
+        }
+      }
+    }
+  };
+
+  // per-token scales of the tile's 128 tokens (the per-token mode's epilogue reads them from LDS)
+  if (TOK && tid < TT) Lxdt[tid] = a.xd[t0 + tid];
   const int nstage = (nb + kGKS - 1) / kGKS;
   gload(0);
   lstore(0);
@@ -708,66 +822,35 @@ __global__ __launch_bounds__(256) void gemm_a8_kernel(const GemmArgs a) {
   for (int st = 0; st < nstage; ++st) {
     const int buf = st & 1;
     if (st + 1 < nstage) gload((st + 1) * kGKS);
-    const int nvalid = min(kGKS, nb - st * kGKS);
-    for (int kb = 0; kb < nvalid; ++kb) {
-      {
-        v4i A[2];
+    if (st + 1 < nstage || nb % kGKS == 0) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) A[mt] = *reinterpret_cast<const v4i*>(&Lact[buf][kb][h][wt * 64 + mt * 32 + l32][0]);
-#pragma unroll
-        for (int s = 0; s < NSEL; ++s) {
-          v4i B[2];
-          float c[2] = {1.f, 1.f};
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            const int rl = wr * 64 + nt * 32 + l32;
-            if (WDT == WQ8) {
-              B[nt] = *reinterpret_cast<const v4i*>(&Lw[buf][s][kb][(h * kGemmTileN + rl) * 16]);
-            } else {
-              B[nt] = q4_operand16(*reinterpret_cast<const uint4*>(&Lw[buf][s][kb][rl * 16]), h);
-              c[nt] = Lws[buf][s][kb][rl];
-            }
-          }
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt) {
-            float xv[16];
-            if (BLOCKX) {
-#pragma unroll
-              for (int g = 0; g < 4; ++g) {
-                const float4 x4 = *reinterpret_cast<const float4*>(&Lxd[buf][kb][wt * 64 + mt * 32 + 8 * g + 4 * h]);
-                xv[4 * g] = x4.x;
-                xv[4 * g + 1] = x4.y;
-                xv[4 * g + 2] = x4.z;
-                xv[4 * g + 3] = x4.w;
-              }
-            }
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-              if (TOK && WDT == WQ8) {
-                iacc[s][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[mt], B[nt], iacc[s][mt][nt], 0, 0, 0);
-              } else {
-                const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[mt], B[nt], zero, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                  // q8: p = float(S) * xd; q4 (S = 16 * S_b, c = ws / 16): p = float(S) * (c * xd)
-                  const float m = WDT == WQ8 ? xv[i] : BLOCKX ? c[nt] * xv[i] : c[nt];
-                  if (a.fast) {
-                    facc[s][mt][nt][i] = __builtin_fmaf((float)S[i], m, facc[s][mt][nt][i]);
-                  } else {
-                    facc[s][mt][nt][i] = facc[s][mt][nt][i] + (float)S[i] * m;
-                  }
-                }
-              }
-            }
-          }
-        }
-      }
+      for (int kb = 0; kb < kGKS; ++kb) block(buf, kb);
+    } else {
+      for (int kb = 0; kb < nb % kGKS; ++kb) block(buf, kb);
     }
     if (st + 1 < nstage) lstore(buf ^ 1);
     __syncthreads();
   }
 
-  // epilogue: row r (lane), tokens t (accumulator index)
+  // epilogue: row r (lane), tokens t (accumulator index). Stores and residual loads go through
+  // buffer resources that span the tile's valid tokens, and an offset past the end stands for a
+  // row past N: the hardware drops such stores and returns 0 for such loads, so no lane branches.
+  const int tv = min(TT, a.T - t0);  // valid tokens of the tile
+  const uint32_t tbytes = (uint32_t)tv * (uint32_t)tg.N * 4u;
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(tg.y + (int64_t)t0 * tg.N, (short)0, (int)tbytes, 0x00020000);
+  const bool has_res = !SW && tg.res != nullptr;
+  const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(has_res ? tg.res + (int64_t)t0 * tg.N : tg.y), (short)0, has_res ? (int)tbytes : 0, 0x00020000);
+  auto xd_tok = [&](float (&xt)[16], int mt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 x4 = *reinterpret_cast<const float4*>(&Lxdt[wt * 32 * MT + mt * 32 + 8 * g + 4 * h]);
+      xt[4 * g] = x4.x;
+      xt[4 * g + 1] = x4.y;
+      xt[4 * g + 2] = x4.z;
+      xt[4 * g + 3] = x4.w;
+    }
+  };
   if (SW) {
     // gate and up of each 32x32 tile go through this wave's LDS slice, so that silu (an expf)
     // is emitted once in a loop rather than once per accumulator
@@ -779,68 +862,80 @@ __global__ __launch_bounds__(256) void gemm_a8_kernel(const GemmArgs a) {
       const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
       const float wsu = WDT == WQ8 ? a.tg[1].scales[rc] : 1.f;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int tb = t0 + wt * 64 + mt * 32 + 4 * h;
+      for (int mt = 0; mt < MT; ++mt) {
+        float xt[16];
+        if (TOK) xd_tok(xt, mt);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int t = tb + 8 * (i >> 2) + (i & 3);
-          const float xdt = TOK ? a.xd[min(t, a.Tpad - 1)] : 1.f;
           float g, u;
           if (WDT == WQ8) {
-            g = TOK ? ((float)iacc[0][mt][nt][i] * xdt) * ws : facc[0][mt][nt][i] * ws;
-            u = TOK ? ((float)iacc[NSEL - 1][mt][nt][i] * xdt) * wsu : facc[NSEL - 1][mt][nt][i] * wsu;
+            g = TOK ? ((float)iacc[0][mt][nt][i] * xt[i]) * ws : facc[0][mt][nt][i] * ws;
+            u = TOK ? ((float)iacc[NSEL - 1][mt][nt][i] * xt[i]) * wsu : facc[NSEL - 1][mt][nt][i] * wsu;
           } else {
-            g = TOK ? facc[0][mt][nt][i] * xdt : facc[0][mt][nt][i];
-            u = TOK ? facc[NSEL - 1][mt][nt][i] * xdt : facc[NSEL - 1][mt][nt][i];
+            g = TOK ? facc[0][mt][nt][i] * xt[i] : facc[0][mt][nt][i];
+            u = TOK ? facc[NSEL - 1][mt][nt][i] * xt[i] : facc[NSEL - 1][mt][nt][i];
           }
           ep[i * 64 + lane] = g;
           ep[1024 + i * 64 + lane] = u;
         }
         __builtin_amdgcn_wave_barrier();
+        const int tb = wt * 32 * MT + mt * 32 + 4 * h;  // token within the tile
 #pragma unroll 1
         for (int i = 0; i < 16; ++i) {
           const int t = tb + 8 * (i >> 2) + (i & 3);
           const float out = silu_exact(ep[i * 64 + lane]) * ep[1024 + i * 64 + lane];
-          if (r < tg.N && t < a.T) tg.y[(int64_t)t * tg.N + r] = out;
+          const int off = r < tg.N ? (t * tg.N + r) * 4 : 0x7FFFFFF0;
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), ry, off, 0, 0);
         }
         __builtin_amdgcn_wave_barrier();
       }
     }
     return;
   }
+  // the residual choice is uniform: two branch-free copies of the store loop
+  auto store_tiles = [&](auto res_tag) {
+    constexpr bool RES = decltype(res_tag)::value;
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int r = r0 + wr * 64 + nt * 32 + l32;
-    const int rc = min(r, tg.N - 1);
-    const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
-    const float wsu = WDT == WQ8 && SW ? a.tg[1].scales[rc] : 1.f;
+    for (int nt = 0; nt < 2; ++nt) {
+      const int r = r0 + wr * 64 + nt * 32 + l32;
+      const int rc = min(r, tg.N - 1);
+      const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < MT; ++mt) {
+        float xt[16];
+        if (TOK) xd_tok(xt, mt);
+        const int tb = wt * 32 * MT + mt * 32 + 4 * h;
+        float res[16];
+        if (RES) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int t = t0 + wt * 64 + mt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-        const float xdt = TOK ? a.xd[min(t, a.Tpad - 1)] : 1.f;
-        float out;
-        if (WDT == WQ8) {
-          out = TOK ? ((float)iacc[0][mt][nt][i] * xdt) * ws : facc[0][mt][nt][i] * ws;
-        } else {
-          out = TOK ? facc[0][mt][nt][i] * xdt : facc[0][mt][nt][i];
-        }
-        if (SW) {
-          float up;
-          if (WDT == WQ8) {
-            up = TOK ? ((float)iacc[NSEL - 1][mt][nt][i] * xdt) * wsu : facc[NSEL - 1][mt][nt][i] * wsu;
-          } else {
-            up = TOK ? facc[NSEL - 1][mt][nt][i] * xdt : facc[NSEL - 1][mt][nt][i];
+          for (int i = 0; i < 16; ++i) {
+            const int t = tb + 8 * (i >> 2) + (i & 3);
+            const int off = r < tg.N ? (t * tg.N + r) * 4 : 0x7FFFFFF0;
+            res[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, off, 0, 0));
           }
-          out = silu_exact(out) * up;
-        } else if (tg.res && r < tg.N && t < a.T) {
-          out = out + tg.res[(int64_t)t * tg.N + r];
         }
-        if (r < tg.N && t < a.T) tg.y[(int64_t)t * tg.N + r] = out;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int t = tb + 8 * (i >> 2) + (i & 3);
+          const int off = r < tg.N ? (t * tg.N + r) * 4 : 0x7FFFFFF0;
+          float out;
+          if (WDT == WQ8) {
+            out = TOK ? ((float)iacc[0][mt][nt][i] * xt[i]) * ws : facc[0][mt][nt][i] * ws;
+          } else {
+            out = TOK ? facc[0][mt][nt][i] * xt[i] : facc[0][mt][nt][i];
+          }
+          if (RES) out = out + res[i];
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), ry, off, 0, 0);
+        }
       }
-  }
+    }
+  };
+  if (has_res)
+    store_tiles(std::true_type{});
+  else
+    store_tiles(std::false_type{});
 }
+
 
 // ---------------------------------------------------------------- f32-activation paths
 
@@ -1160,16 +1255,41 @@ hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_ti
   return swiglu ? gemv_nt<WQ4, true>(a, total_tiles, s) : gemv_nt<WQ4, false>(a, total_tiles, s);
 }
 
-template <int WDT, bool SW, bool TOK>
-static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
-  // one workgroup per (row tile, token tile), numbered in 8 XCD-contiguous ranges
-  if (a.Tpad % kGemmTileT || tiles < 1 || tiles != (SW ? a.tg[0].ntiles : a.tile_start[a.n_targets]))
-    return hipErrorInvalidValue;
-  const int total = tiles * (a.Tpad / kGemmTileT);
-  gemm_a8_kernel<WDT, SW, TOK><<<(total + 7) / 8 * 8, 256, 0, s>>>(a);
-  return hipGetLastError();
+template <int WDT, bool SW, bool TOK, int MT>
+static void gemm_launch(const GemmArgs& a, dim3 grid, hipStream_t s) {
+  // the per-token q8 accumulation is all-integer: FAST changes nothing there
+  if (a.fast && !(TOK && WDT == WQ8))
+    gemm_a8_kernel<WDT, SW, TOK, true, MT><<<grid, 256, 0, s>>>(a);
+  else
+    gemm_a8_kernel<WDT, SW, TOK, false, MT><<<grid, 256, 0, s>>>(a);
 }
 
+template <int WDT, bool SW, bool TOK>
+static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
+  if (a.Tpad % kGemmTileT || a.T < 1 || a.T > a.Tpad || tiles < 1 ||
+      tiles != (SW ? a.tg[0].ntiles : a.tile_start[a.n_targets]))
+    return hipErrorInvalidValue;
+  // the epilogue's buffer resources span 128 tokens x N floats in 31 bits
+  for (int i = 0; i < (SW ? 2 : a.n_targets); ++i)
+    if (a.tg[i].N < 1 || a.tg[i].N >= (1 << 22)) return hipErrorInvalidValue;
+  // one workgroup per (row tile, token tile), numbered in 8 XCD-contiguous ranges; 64-token tiles
+  // when 128-token tiles would leave compute units idle
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  // token tiles are counted from T, so every tile starts at a valid token (its store range is
+  // min(TT, T - t0) >= 1 tokens)
+  const int t128 = tiles * ((a.T + 127) / 128), t64 = tiles * ((a.T + 63) / 64);
+  bool small = t128 < cus;
+  // ELMH_GEMM_TOKEN_TILE=64 or 128 forces one tile height (both give the same bits)
+  if (const char* ev = getenv("ELMH_GEMM_TOKEN_TILE")) small = ev[0] == '6' ? true : ev[0] == '1' ? false : small;
+  if (small)
+    gemm_launch<WDT, SW, TOK, 1>(a, dim3((t64 + 7) / 8 * 8), s);
+  else
+    gemm_launch<WDT, SW, TOK, 2>(a, dim3((t128 + 7) / 8 * 8), s);
+  return hipGetLastError();
+}
 hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs& a, int total_tiles, hipStream_t s) {
   if (dtype == WQ8) {
     if (token_mode) return swiglu ? gemm_go<WQ8, true, true>(a, total_tiles, s) : gemm_go<WQ8, false, true>(a, total_tiles, s);

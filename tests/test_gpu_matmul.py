@@ -267,3 +267,35 @@ def test_matmul_f32act_long_rows(ctx, dt):
             got = ctx.matmul(x, [dw], [res], act=E.ACT_F32)[0]
             assert bits_equal(got, O.cpu_matmul(x, [w], [res], act_quant=False)[0]), f"T={T}"
         dw.free()
+
+
+@pytest.mark.parametrize("tile", ["64", "128"])
+@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
+def test_gemm_token_tiles(ctx, dt, tile, monkeypatch):
+    """Both GEMM tile heights (64 and 128 tokens, picked by shape unless ELMH_GEMM_TOKEN_TILE forces
+    one) over several token tiles with a ragged last one and a partial last row tile: per-block
+    int8 (exact, fast, residual), per-token int8, MATMUL_N and FFN_SWIGLU."""
+    monkeypatch.setenv("ELMH_GEMM_TOKEN_TILE", tile)
+    r = rng(500 + dt)
+    n, k = 300, 576
+    w, w2 = weight(r, n, k, dt), weight(r, 72, k, dt)
+    wg, wu = weight(r, n, k, dt), weight(r, n, k, dt)
+    dw, dw2, dg, du = up(ctx, w), up(ctx, w2), up(ctx, wg), up(ctx, wu)
+    for T in [65, 130, 257]:
+        print(f"[gpu] gemm tile={tile} dt={dt} T={T}", flush=True)
+        x = r.normal(0, 1, (T, k)).astype(np.float32)
+        res = r.normal(0, 1, (T, n)).astype(np.float32)
+        got = ctx.matmul(x, [dw, dw2], [res, None], act=E.ACT_INT8, mode=E.EXACT)
+        want = O.cpu_matmul(x, [w, w2], [res, None], act_quant=True)
+        assert bits_equal(got[0], want[0]) and bits_equal(got[1], want[1])
+        fast = ctx.matmul(x, [dw], None, act=E.ACT_INT8, mode=E.FAST)[0]
+        assert rel_err(fast, O.cpu_matmul(x, [w], None, act_quant=True)[0]) < 1e-5
+        assert bits_equal(ctx.swiglu(x, dg, du, act=E.ACT_INT8), O.cpu_swiglu(x, wg, wu, act_quant=True))
+        tok = ctx.matmul(x, [dw], [res], act=E.ACT_INT8_TOKEN)[0]
+        assert bits_equal(tok, O.matmul_a8_token(x, w, res))
+        if T == 65:
+            g, u = O.matmul_a8_token(x, wg), O.matmul_a8_token(x, wu)
+            want_sw = np.array([O.silu(float(v)) for v in g.ravel()], np.float32).reshape(g.shape) * u
+            assert bits_equal(ctx.swiglu(x, dg, du, act=E.ACT_INT8_TOKEN), want_sw)
+    for d in (dw, dw2, dg, du):
+        d.free()
