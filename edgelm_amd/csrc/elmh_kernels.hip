@@ -106,48 +106,84 @@ __global__ __launch_bounds__(256) void act_quant_rows_kernel(const float* __rest
 }
 
 // Fragment-major for the MFMA GEMM: the 1 KB fragment of (32-token group, block b) holds for lane
-// L = h*32 + t%32 the 16 bytes of elements h*16 .. h*16+15 of token t's block b.
-__global__ __launch_bounds__(256) void act_quant_frag_kernel(const float* __restrict__ x, int T, int Tpad, int K,
-                                                             int8_t* __restrict__ xq, float* __restrict__ xd) {
-  const int nb = K / kBlock;
-  const int g = blockIdx.x * 8 + (threadIdx.x >> 5), l = threadIdx.x & 31;
-  if (g >= Tpad * nb) return;  // whole 32-lane groups leave together
-  const int t = g / nb, b = g - t * nb;
-  const float v = t < T ? x[(int64_t)t * K + b * kBlock + l] : 0.f;
-  float d;
-  int sum;
-  const int q = quant32(v, d, sum);
-  const int h = l >> 4, m = l & 15;
-  xq[(((int64_t)(t >> 5) * nb + b) * 64 + h * 32 + (t & 31)) * 16 + m] = (int8_t)q;
-  if (l == 0) xd[(int64_t)b * Tpad + t] = d;
+// L = h*32 + t%32 the 16 bytes of elements h*16 .. h*16+15 of token t's block b. A thread owns one
+// such half-block: four float4 loads, edgelm's rounding, one 16-byte store.
+
+// edgelm's rounding of v / safe (quantize_act_row, kernels_ref.cpp:23-37)
+__device__ __forceinline__ uint32_t q8_of(float v, float safe) {
+  const float vv = v / safe;
+  const float r = copysignf(floorf(fabsf(vv) + 0.5f), vv);
+  return (uint32_t)(int)fminf(127.f, fmaxf(-127.f, r)) & 0xFFu;
+}
+__device__ __forceinline__ uint32_t q8x4(float4 v, float safe) {
+  return q8_of(v.x, safe) | (q8_of(v.y, safe) << 8) | (q8_of(v.z, safe) << 16) | (q8_of(v.w, safe) << 24);
+}
+__device__ __forceinline__ float amax4(float4 v, float a) {
+  return fmaxf(fmaxf(fmaxf(a, fabsf(v.x)), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+// floats 4i .. 4i+3 of p; the compiler merges these into 16-byte loads, which the hardware serves
+// at any 4-byte alignment (x may point anywhere into a caller's tensor)
+__device__ __forceinline__ float4 ld4(const float* p, int i) {
+  return make_float4(p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]);
+}
+__device__ __forceinline__ int64_t frag_offset(int t, int b, int h, int nb) {
+  return ((((int64_t)(t >> 5) * nb + b) * 64) + h * 32 + (t & 31)) * 16;
 }
 
-// Per-token scale (extension): one workgroup per token row.
+// Per-32-block scales: lanes 2i and 2i+1 hold the two halves of one block and share its amax.
+__global__ __launch_bounds__(256) void act_quant_frag_kernel(const float* __restrict__ x, int T, int Tpad, int K,
+                                                             int8_t* __restrict__ xq, float* __restrict__ xd) {
+  const int nb = K / kBlock, hb = 2 * nb;
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool live = g < (int64_t)Tpad * hb;  // hb is even: both lanes of a pair agree
+  const int t = live ? (int)(g / hb) : 0;
+  const int rem = live ? (int)(g - (int64_t)t * hb) : 0, b = rem >> 1, h = rem & 1;
+  float4 v[4];
+  const float* src = x + (int64_t)t * K + rem * 16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = live && t < T ? ld4(src, i) : make_float4(0.f, 0.f, 0.f, 0.f);
+  float a = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a = amax4(v[i], a);
+  a = fmaxf(a, __shfl_xor(a, 1, 64));
+  const float sc = a / 127.0f;
+  const float safe = sc == 0.f ? 1.f : sc;
+  const uint4 q = make_uint4(q8x4(v[0], safe), q8x4(v[1], safe), q8x4(v[2], safe), q8x4(v[3], safe));
+  if (!live) return;
+  *reinterpret_cast<uint4*>(xq + frag_offset(t, b, h, nb)) = q;
+  if (h == 0) xd[(int64_t)b * Tpad + t] = sc;
+}
+
+// Per-token scale (extension): one workgroup per token row; the row is read twice (amax, then
+// quantization), the second time from cache.
 __global__ __launch_bounds__(256) void act_quant_frag_token_kernel(const float* __restrict__ x, int T, int Tpad, int K,
                                                                    int8_t* __restrict__ xq, float* __restrict__ xd) {
   __shared__ float red[4];
-  const int t = blockIdx.x, nb = K / kBlock;
+  const int t = blockIdx.x, nb = K / kBlock, hb = 2 * nb;
+  const float* row = x + (int64_t)t * K;
   float a = 0.f;
   if (t < T)
-    for (int k = threadIdx.x; k < K; k += 256) a = fmaxf(a, fabsf(x[(int64_t)t * K + k]));
+    for (int j = threadIdx.x; j < hb; j += 256) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a = amax4(ld4(row + j * 16, i), a);
+    }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
   __syncthreads();
   a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float s = a / 127.0f;
-  const float safe = s == 0.f ? 1.f : s;
-  for (int k = threadIdx.x; k < K; k += 256) {
-    int q = 0;
+  const float sc = a / 127.0f;
+  const float safe = sc == 0.f ? 1.f : sc;
+  for (int j = threadIdx.x; j < hb; j += 256) {
+    uint4 q = make_uint4(0u, 0u, 0u, 0u);
     if (t < T) {
-      const float vv = x[(int64_t)t * K + k] / safe;
-      const float r = copysignf(floorf(fabsf(vv) + 0.5f), vv);
-      q = (int)fminf(127.f, fmaxf(-127.f, r));
+      const float* p = row + j * 16;
+      q = make_uint4(q8x4(ld4(p, 0), safe), q8x4(ld4(p, 1), safe), q8x4(ld4(p, 2), safe),
+                     q8x4(ld4(p, 3), safe));
     }
-    const int b = k >> 5, e = k & 31, h = e >> 4, m = e & 15;
-    xq[(((int64_t)(t >> 5) * nb + b) * 64 + h * 32 + (t & 31)) * 16 + m] = (int8_t)q;
+    *reinterpret_cast<uint4*>(xq + frag_offset(t, j >> 1, j & 1, nb)) = q;
   }
-  if (threadIdx.x == 0) xd[t] = s;
+  if (threadIdx.x == 0) xd[t] = sc;
 }
 
 // ---------------------------------------------------------------- int8 GEMV (decode)
@@ -1181,8 +1217,10 @@ hipError_t launch_act_quant_rows(const float* x, int T, int K, int8_t* xq, float
 }
 
 hipError_t launch_act_quant_frag(const float* x, int T, int Tpad, int K, int8_t* xq, float* xd, hipStream_t s) {
-  const int blocks = Tpad * (K / kBlock);
-  act_quant_frag_kernel<<<(blocks + 7) / 8, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
+  // one thread per half-block
+  const int64_t threads = (int64_t)Tpad * 2 * (K / kBlock);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  act_quant_frag_kernel<<<grid, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
   return hipGetLastError();
 }
 

@@ -299,3 +299,25 @@ def test_gemm_token_tiles(ctx, dt, tile, monkeypatch):
             assert bits_equal(ctx.swiglu(x, dg, du, act=E.ACT_INT8_TOKEN), want_sw)
     for d in (dw, dw2, dg, du):
         d.free()
+
+
+def test_dev_pointer_unaligned_input(ctx):
+    """elmh_matmul_dev takes any 4-byte-aligned device pointer for x (here 4 bytes past a 256-byte
+    boundary): the same bits as the host-pointer call, on the GEMV and both GEMM quantizers."""
+    r = rng(600)
+    n, k = 200, 576
+    w = weight(r, n, k, O.Q8)
+    dw = up(ctx, w)
+    for T in [2, 9, 70]:
+        x = r.normal(0, 1, (T, k)).astype(np.float32)
+        bx = ctx.buffer(x.nbytes + 16)
+        bx.upload(np.concatenate([np.zeros(1, np.float32), x.ravel()]))
+        by = ctx.buffer(T * n * 4)
+        for act in (E.ACT_INT8, E.ACT_INT8_TOKEN):
+            print(f"[gpu] unaligned x T={T} act={act}", flush=True)
+            ctx.matmul_dev(bx.ptr + 4, T, k, [dw], [by.ptr], act=act)
+            got = by.download((T, n), np.float32)
+            assert bits_equal(got, ctx.matmul(x, [dw], None, act=act)[0])
+        bx.free()
+        by.free()
+    dw.free()
