@@ -154,19 +154,35 @@ __global__ __launch_bounds__(256) void act_quant_frag_kernel(const float* __rest
   if (h == 0) xd[(int64_t)b * Tpad + t] = sc;
 }
 
-// Per-token scale (extension): one workgroup per token row; the row is read twice (amax, then
-// quantization), the second time from cache.
+// Per-token scale (extension): one workgroup per token row. NPER > 0: a thread keeps its NPER
+// half-blocks (j = tid + 256 i) in registers between the row amax and the rounding (K <= NPER * 4096);
+// NPER == 0 reads the row twice, the second time from cache.
+template <int NPER>
 __global__ __launch_bounds__(256) void act_quant_frag_token_kernel(const float* __restrict__ x, int T, int Tpad, int K,
                                                                    int8_t* __restrict__ xq, float* __restrict__ xd) {
   __shared__ float red[4];
   const int t = blockIdx.x, nb = K / kBlock, hb = 2 * nb;
   const float* row = x + (int64_t)t * K;
+  constexpr int NR = NPER > 0 ? NPER : 1;
+  float4 v[NR][4];
   float a = 0.f;
-  if (t < T)
+  if (NPER > 0) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int j = threadIdx.x + 256 * i;
+      const bool ok = t < T && j < hb;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v[i][u] = ok ? ld4(row + j * 16, u) : make_float4(0.f, 0.f, 0.f, 0.f);
+        a = amax4(v[i][u], a);
+      }
+    }
+  } else if (t < T) {
     for (int j = threadIdx.x; j < hb; j += 256) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a = amax4(ld4(row + j * 16, i), a);
+      for (int u = 0; u < 4; ++u) a = amax4(ld4(row + j * 16, u), a);
     }
+  }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
@@ -174,14 +190,23 @@ __global__ __launch_bounds__(256) void act_quant_frag_token_kernel(const float* 
   a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float sc = a / 127.0f;
   const float safe = sc == 0.f ? 1.f : sc;
-  for (int j = threadIdx.x; j < hb; j += 256) {
-    uint4 q = make_uint4(0u, 0u, 0u, 0u);
-    if (t < T) {
-      const float* p = row + j * 16;
-      q = make_uint4(q8x4(ld4(p, 0), safe), q8x4(ld4(p, 1), safe), q8x4(ld4(p, 2), safe),
-                     q8x4(ld4(p, 3), safe));
+  if (NPER > 0) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int j = threadIdx.x + 256 * i;
+      if (j < hb)
+        *reinterpret_cast<uint4*>(xq + frag_offset(t, j >> 1, j & 1, nb)) =
+            make_uint4(q8x4(v[i][0], safe), q8x4(v[i][1], safe), q8x4(v[i][2], safe), q8x4(v[i][3], safe));
     }
-    *reinterpret_cast<uint4*>(xq + frag_offset(t, j >> 1, j & 1, nb)) = q;
+  } else {
+    for (int j = threadIdx.x; j < hb; j += 256) {
+      uint4 q = make_uint4(0u, 0u, 0u, 0u);
+      if (t < T) {
+        const float* p = row + j * 16;
+        q = make_uint4(q8x4(ld4(p, 0), safe), q8x4(ld4(p, 1), safe), q8x4(ld4(p, 2), safe), q8x4(ld4(p, 3), safe));
+      }
+      *reinterpret_cast<uint4*>(xq + frag_offset(t, j >> 1, j & 1, nb)) = q;
+    }
   }
   if (threadIdx.x == 0) xd[t] = sc;
 }
@@ -596,18 +621,21 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
 
 // ---------------------------------------------------------------- int8 MFMA GEMM (prefill)
 //
-// Workgroup = 4 waves over a 128-token x 128-row output tile; each wave owns a 64 x 64 quarter as
-// 2 x 2 v_mfma_i32_32x32x32_i8 tiles with A = tokens and B = weight rows (a lane owns one output
-// row of each tile, so the stores run along the row). K advances four 32-blocks per LDS stage,
-// double buffered: the next stage's global loads are in flight while the current stage's MFMAs
-// run, and one barrier per stage separates them. One MFMA spans exactly one 32-block along K, so
-// in the block-scale modes each block's int32 sums come out whole and are rescaled in block order
-// (edgelm's scalar order: multiply then add, or one fused multiply-add in FAST mode); in the
+// Workgroup = 4 waves over a (64 MT)-token x 128-row output tile; each wave owns an (32 MT) x 64 part
+// as MT x 2 v_mfma_i32_32x32x32_i8 tiles with A = tokens and B = weight rows (a lane owns one output
+// row of each tile, so the stores run along the row). One MFMA spans exactly one 32-block along K,
+// so in the block-scale modes each block's int32 sums come out whole and are rescaled in block
+// order (edgelm's scalar order: multiply then add, or one fused multiply-add in FAST mode); in the
 // per-token q8 mode the int32 sums accumulate across all of K and one rescale finishes.
+//
+// K streams through a ring of D LDS slots, one 32-block per slot, filled by global_load_lds
+// (direct to LDS: no staging registers, so D - 1 blocks are in flight). Every wave issues the same
+// P DMA instructions per slot, so "my part of block b has landed" is a fixed vmcnt((D - 2) * P);
+// one barrier per block then makes every part visible and frees the slot computed one block
+// earlier. Issues past the last block repeat the last block, which keeps the count fixed.
 // Workgroups are numbered so that each XCD (workgroup index mod 8) takes a contiguous range of
 // (row tile, token tile) pairs, token tile fastest: an XCD's L2 keeps its own weight rows.
 
-constexpr int kGKS = 4;  // 32-blocks per LDS stage
 static_assert(kGemmTileT == 128 && kGemmTileN == 128, "GEMM tile: the token padding covers both tile heights");
 
 // Target ti (uniform) of a GEMM launch read through the kernel-argument segment pointer.
@@ -624,30 +652,59 @@ __device__ __forceinline__ GemmTarget gemm_target_at(int ti) {
   return t;
 }
 
+typedef __attribute__((address_space(3))) unsigned char* LdsBytes;
+
+// One global_load_lds of 16 (or 4) bytes per active lane into LDS at dst + 16 (4) * lane (dst is
+// wave-uniform: it goes to M0). Written as asm so that the compiler's wait-count pass does not
+// track it (it would drain every in-flight load before each LDS read); the kernel waits for these
+// loads itself (wait_vm) and drains them all before its LDS is reused or released.
+__device__ __forceinline__ void dma16(const void* src, unsigned char* dst) {
+  const unsigned m0 = (unsigned)(size_t)(LdsBytes)dst;
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* src, unsigned char* dst) {
+  const unsigned m0 = (unsigned)(size_t)(LdsBytes)dst;
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) only (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4] << 14)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// workgroup barrier that orders LDS accesses in the compiler's view without waiting for loads
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int WDT, bool SW, bool TOK, int MT>
+struct GemmRing {
+  static constexpr int TT = 64 * MT;
+  static constexpr int NSEL = SW ? 2 : 1;
+  static constexpr bool BLOCKX = !TOK;
+  static constexpr int ACT = TT * 32;                                    // [TT/32 groups][2 halves][32][16]
+  static constexpr int WSEL = WDT == WQ8 ? kGemmTileN * 32 : kGemmTileN * 20;  // q8 [2][128][16]; q4 [128][16] + [128] f32
+  static constexpr int XD = BLOCKX ? TT * 4 : 0;
+  static constexpr int SLOT = ACT + NSEL * WSEL + XD;
+  static constexpr int D = (76 * 1024) / SLOT < 4 ? 4 : (76 * 1024) / SLOT;  // ring depth
+  static constexpr int P = 1 + NSEL + (BLOCKX ? 1 : 0);                        // DMA instructions per wave per slot
+  static constexpr int EP = SW ? 4 * 2 * 32 * 32 * 4 : 16;                     // SwiGLU epilogue: gate and up per wave
+  static constexpr int BYTES = D * SLOT > EP ? D * SLOT : EP;
+  static_assert((D - 2) * P < 64, "vmcnt range");
+};
+
 template <int WDT, bool SW, bool TOK, bool FAST, int MT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT == 2 ? 1 : 2))) void gemm_a8_kernel(
     const GemmArgs a) {
-  constexpr int TT = 64 * MT;  // tokens per workgroup: 2 waves x MT 32-token MFMA tiles
-  constexpr int NSEL = SW ? 2 : 1;
-  constexpr int WB = WDT == WQ8 ? 2 * kGemmTileN * 16 : kGemmTileN * 16;  // weight bytes per block
-  constexpr bool BLOCKX = !TOK;                                             // per-block activation scales
-  // LDS: the double-buffered stages; after the K loop the SwiGLU epilogue reuses the space
-  constexpr int XDN = BLOCKX ? TT : 1;                                      // unused scales take 1 slot
-  constexpr int WSN = WDT == WQ4 ? kGemmTileN : 1;
-  struct Stages {
-    int8_t act[2][kGKS][2][TT][16];
-    uint8_t w[2][NSEL][kGKS][WB];
-    float xd[2][kGKS][XDN];
-    float ws[2][NSEL][kGKS][WSN];
-  };
-  constexpr int kEpBytes = SW ? 4 * 2 * 32 * 32 * 4 : 16;  // per wave: gate and up of one 32x32 tile
-  __shared__ __align__(16) unsigned char Lraw[sizeof(Stages) > kEpBytes ? sizeof(Stages) : kEpBytes];
+  typedef GemmRing<WDT, SW, TOK, MT> R;
+  constexpr int TT = R::TT, NSEL = R::NSEL, D = R::D;
+  constexpr bool BLOCKX = R::BLOCKX;
+  __shared__ __align__(16) unsigned char ring[R::BYTES];
   __shared__ __align__(16) float Lxdt[TOK ? TT : 4];
-  Stages& L = *reinterpret_cast<Stages*>(Lraw);
-  auto& Lact = L.act;
-  auto& Lw = L.w;
-  auto& Lxd = L.xd;
-  auto& Lws = L.ws;
 
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wt = wave >> 1, wr = wave & 1;
@@ -671,111 +728,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
   auto wdata = [&](int s) { return SW && s ? a.tg[1].data : tg.data; };
   auto wscal = [&](int s) { return SW && s ? a.tg[1].scales : tg.scales; };
 
-  // per-thread load assignments
-  const int lrow = tid & (kGemmTileN - 1), lhi = tid >> 7;  // weight row of the tile, half / block
-  const int wrow = min(r0 + lrow, rows_pad - 1);
+  // DMA roles. Activation: 1 KB fragment (group, block) = [half][32 tokens][16 B], the same layout
+  // in HBM and in the slot; wave w copies group w (MT = 2) or half w & 1 of group w >> 1 (MT = 1,
+  // lanes 0-31). Weights: lane row (w & 1) * 64 + lane; q8 half w >> 1, q4 data (w < 2) or scale.
+  const int drow = (wave & 1) * 64 + lane;
+  const int wrow = min(r0 + drow, rows_pad - 1);
   const int64_t rbase = (int64_t)(wrow / H) * nb * H + (wrow % H);  // item of (wrow, block 0)
-  // activation: token group ac of the tile, lane slot aw; with 64-token tiles a thread loads blocks
-  // akb and akb + 2 of each stage, with 128-token tiles all four
-  const int ac = MT == 2 ? tid >> 6 : (tid >> 6) & 1, aw = tid & 63, akb = MT == 2 ? 0 : tid >> 7;
-
-  // staging registers of one stage (named values: arrays here end up in scratch memory)
-  static_assert(kGKS == 4, "four blocks per stage");
-  uint4 ra0, ra1, ra2, ra3, rw00, rw01, rw02, rw03, rw10, rw11, rw12, rw13;
-  float rws00 = 0.f, rws01 = 0.f, rws10 = 0.f, rws11 = 0.f, rxd0 = 0.f, rxd1 = 0.f;
-  auto gload = [&](int b0) {
-    const int8_t* xs = a.xq + (((int64_t)(t0 >> 5) + ac) * nb) * 1024 + aw * 16;
-    auto la = [&](uint4& r, int b) { r = *reinterpret_cast<const uint4*>(xs + (int64_t)min(b, nb - 1) * 1024); };
-    if (MT == 2) {
-      la(ra0, b0);
-      la(ra1, b0 + 1);
-      la(ra2, b0 + 2);
-      la(ra3, b0 + 3);
-    } else {
-      la(ra0, b0 + akb);
-      la(ra1, b0 + akb + 2);
-    }
-    if (WDT == WQ8) {
-      // q8: thread (lhi = half, lrow) loads that half of blocks b0..b0+3
-      auto lw = [&](uint4& r, int sl, int b) {
-        r = *reinterpret_cast<const uint4*>(wdata(sl) + (rbase + (int64_t)min(b, nb - 1) * H) * 32 + lhi * 16);
-      };
-      lw(rw00, 0, b0);
-      lw(rw01, 0, b0 + 1);
-      lw(rw02, 0, b0 + 2);
-      lw(rw03, 0, b0 + 3);
-      if (SW) {
-        lw(rw10, 1, b0);
-        lw(rw11, 1, b0 + 1);
-        lw(rw12, 1, b0 + 2);
-        lw(rw13, 1, b0 + 3);
-      }
-    } else {
-      // q4: thread (lhi, lrow) loads blocks b0 + lhi and b0 + lhi + 2 (16 B and a scale each)
-      auto lw = [&](uint4& r, float& c, int sl, int b) {
-        const int64_t it = rbase + (int64_t)min(b, nb - 1) * H;
-        r = *reinterpret_cast<const uint4*>(wdata(sl) + it * 16);
-        c = wscal(sl)[it];
-      };
-      lw(rw00, rws00, 0, b0 + lhi);
-      lw(rw01, rws01, 0, b0 + lhi + 2);
-      if (SW) {
-        lw(rw10, rws10, 1, b0 + lhi);
-        lw(rw11, rws11, 1, b0 + lhi + 2);
+  const int8_t* const xg = a.xq + (int64_t)((t0 >> 5) + (MT == 2 ? wave : wave >> 1)) * nb * 1024 +
+                           (MT == 2 ? lane * 16 : (wave & 1) * 512 + l32 * 16);
+  auto issue = [&](int blk, int slot) {
+    blk = min(blk, nb - 1);
+    unsigned char* sb = ring + slot * R::SLOT;
+    if (MT == 2 || lane < 32) dma16(xg + (int64_t)blk * 1024, sb + wave * (MT == 2 ? 1024 : 512));
+    const int64_t it = rbase + (int64_t)blk * H;
+#pragma unroll
+    for (int sl = 0; sl < NSEL; ++sl) {
+      unsigned char* wb = sb + R::ACT + sl * R::WSEL;
+      if (WDT == WQ8) {
+        dma16(wdata(sl) + it * 32 + (wave >> 1) * 16, wb + wave * 1024);
+      } else if (wave < 2) {
+        dma16(wdata(sl) + it * 16, wb + wave * 1024);
+      } else {
+        dma4(wscal(sl) + it, wb + 2048 + (wave - 2) * 256);
       }
     }
-    if (BLOCKX && MT == 2) {  // 4 blocks x 128 tokens: blocks lhi and lhi + 2, token lrow
-      rxd0 = a.xd[(int64_t)min(b0 + lhi, nb - 1) * a.Tpad + t0 + lrow];
-      rxd1 = a.xd[(int64_t)min(b0 + lhi + 2, nb - 1) * a.Tpad + t0 + lrow];
-    } else if (BLOCKX) {      // 4 blocks x 64 tokens: block tid / 64, token tid % 64
-      rxd0 = a.xd[(int64_t)min(b0 + (tid >> 6), nb - 1) * a.Tpad + t0 + (tid & 63)];
-    }
-  };
-  auto lstore = [&](int buf) {
-    auto sa = [&](const uint4& r, int kb) {
-      *reinterpret_cast<uint4*>(&Lact[buf][kb][aw >> 5][ac * 32 + (aw & 31)][0]) = r;
-    };
-    if (MT == 2) {
-      sa(ra0, 0);
-      sa(ra1, 1);
-      sa(ra2, 2);
-      sa(ra3, 3);
-    } else {
-      sa(ra0, akb);
-      sa(ra1, akb + 2);
-    }
-    if (WDT == WQ8) {
-      auto sw = [&](const uint4& r, int sl, int kb) {
-        *reinterpret_cast<uint4*>(&Lw[buf][sl][kb][(lhi * kGemmTileN + lrow) * 16]) = r;
-      };
-      sw(rw00, 0, 0);
-      sw(rw01, 0, 1);
-      sw(rw02, 0, 2);
-      sw(rw03, 0, 3);
-      if (SW) {
-        sw(rw10, NSEL - 1, 0);
-        sw(rw11, NSEL - 1, 1);
-        sw(rw12, NSEL - 1, 2);
-        sw(rw13, NSEL - 1, 3);
-      }
-    } else {
-      auto sw = [&](const uint4& r, float c, int sl, int kb) {
-        *reinterpret_cast<uint4*>(&Lw[buf][sl][kb][lrow * 16]) = r;
-        Lws[buf][sl][kb][lrow] = c;
-      };
-      sw(rw00, rws00, 0, lhi);
-      sw(rw01, rws01, 0, lhi + 2);
-      if (SW) {
-        sw(rw10, rws10, NSEL - 1, lhi);
-        sw(rw11, rws11, NSEL - 1, lhi + 2);
-      }
-    }
-    if (BLOCKX && MT == 2) {
-      Lxd[buf][lhi][lrow] = rxd0;
-      Lxd[buf][lhi + 2][lrow] = rxd1;
-    } else if (BLOCKX) {
-      Lxd[buf][tid >> 6][tid & 63] = rxd0;
-    }
+    if (BLOCKX && lane < TT / 4)
+      dma4(a.xd + (int64_t)blk * a.Tpad + t0 + wave * (TT / 4) + lane, sb + R::ACT + NSEL * R::WSEL + wave * TT);
   };
 
   v16i iacc[NSEL][MT][2];
@@ -795,32 +773,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
 #pragma unroll
   for (int i = 0; i < 16; ++i) zero[i] = 0;
 
-  // one 32-block of the current stage: MT x 2 MFMAs per wave (per weight selection)
-  auto block = [&](int buf, int kb) {
+  // one 32-block from a slot: MT x 2 MFMAs per wave (per weight selection)
+  auto block = [&](int slot) {
+    const unsigned char* sb = ring + slot * R::SLOT;
     v4i A[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) A[mt] = *reinterpret_cast<const v4i*>(&Lact[buf][kb][h][wt * 32 * MT + mt * 32 + l32][0]);
+    for (int mt = 0; mt < MT; ++mt) A[mt] = *reinterpret_cast<const v4i*>(sb + ((wt * MT + mt) * 64 + lane) * 16);
 #pragma unroll
     for (int s = 0; s < NSEL; ++s) {
+      const unsigned char* wb = sb + R::ACT + s * R::WSEL;
       v4i B[2];
       float c[2] = {1.f, 1.f};
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         const int rl = wr * 64 + nt * 32 + l32;
         if (WDT == WQ8) {
-          B[nt] = *reinterpret_cast<const v4i*>(&Lw[buf][s][kb][(h * kGemmTileN + rl) * 16]);
+          B[nt] = *reinterpret_cast<const v4i*>(wb + (h * kGemmTileN + rl) * 16);
         } else {
-          B[nt] = q4_operand16(*reinterpret_cast<const uint4*>(&Lw[buf][s][kb][rl * 16]), h);
-          c[nt] = Lws[buf][s][kb][rl];
+          B[nt] = q4_operand16(*reinterpret_cast<const uint4*>(wb + rl * 16), h);
+          c[nt] = reinterpret_cast<const float*>(wb + 2048)[rl];
         }
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         float xv[16];
         if (BLOCKX) {
+          const float* xs = reinterpret_cast<const float*>(sb + R::ACT + NSEL * R::WSEL);
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const float4 x4 = *reinterpret_cast<const float4*>(&Lxd[buf][kb][wt * 32 * MT + mt * 32 + 8 * g + 4 * h]);
+            const float4 x4 = *reinterpret_cast<const float4*>(&xs[wt * 32 * MT + mt * 32 + 8 * g + 4 * h]);
             xv[4 * g] = x4.x;
             xv[4 * g + 1] = x4.y;
             xv[4 * g + 2] = x4.z;
@@ -849,24 +830,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
     }
   };
 
-  // per-token scales of the tile's 128 tokens (the per-token mode's epilogue reads them from LDS)
+  // per-token scales of the tile's tokens (the per-token mode's epilogue reads them from LDS)
   if (TOK && tid < TT) Lxdt[tid] = a.xd[t0 + tid];
-  const int nstage = (nb + kGKS - 1) / kGKS;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int st = 0; st < nstage; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < nstage) gload((st + 1) * kGKS);
-    if (st + 1 < nstage || nb % kGKS == 0) {
 #pragma unroll
-      for (int kb = 0; kb < kGKS; ++kb) block(buf, kb);
-    } else {
-      for (int kb = 0; kb < nb % kGKS; ++kb) block(buf, kb);
-    }
-    if (st + 1 < nstage) lstore(buf ^ 1);
-    __syncthreads();
+  for (int i = 0; i < D - 1; ++i) issue(i, i);
+  int cs = 0, is = D - 1;  // slot to compute, slot to fill
+  for (int b = 0; b < nb; ++b) {
+    wait_vm<(D - 2) * R::P>();  // this wave's part of block b has landed
+    lds_barrier();              // every wave's part has; every wave is done with block b - 1
+    issue(b + D - 1, is);
+    block(cs);
+    cs = cs + 1 == D ? 0 : cs + 1;
+    is = is + 1 == D ? 0 : is + 1;
   }
+  wait_vm<0>();  // the repeated last-block issues have landed before the ring is reused or freed
+  lds_barrier();
 
   // epilogue: row r (lane), tokens t (accumulator index). Stores and residual loads go through
   // buffer resources that span the tile's valid tokens, and an offset past the end stands for a
@@ -890,7 +868,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
   if (SW) {
     // gate and up of each 32x32 tile go through this wave's LDS slice, so that silu (an expf)
     // is emitted once in a loop rather than once per accumulator
-    float* const ep = reinterpret_cast<float*>(Lraw) + wave * (2 * 32 * 32);
+    float* const ep = reinterpret_cast<float*>(ring) + wave * (2 * 32 * 32);
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int r = r0 + wr * 64 + nt * 32 + l32;
@@ -971,7 +949,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
   else
     store_tiles(std::false_type{});
 }
-
 
 // ---------------------------------------------------------------- f32-activation paths
 
@@ -1225,7 +1202,15 @@ hipError_t launch_act_quant_frag(const float* x, int T, int Tpad, int K, int8_t*
 }
 
 hipError_t launch_act_quant_frag_token(const float* x, int T, int Tpad, int K, int8_t* xq, float* xd, hipStream_t s) {
-  act_quant_frag_token_kernel<<<Tpad, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
+  const int hb = 2 * (K / kBlock);  // half-blocks per row
+  if (hb <= 256)
+    act_quant_frag_token_kernel<1><<<Tpad, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
+  else if (hb <= 512)
+    act_quant_frag_token_kernel<2><<<Tpad, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
+  else if (hb <= 1024)
+    act_quant_frag_token_kernel<4><<<Tpad, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
+  else
+    act_quant_frag_token_kernel<0><<<Tpad, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
   return hipGetLastError();
 }
 
