@@ -130,27 +130,28 @@ __device__ __forceinline__ int64_t frag_offset(int t, int b, int h, int nb) {
   return ((((int64_t)(t >> 5) * nb + b) * 64) + h * 32 + (t & 31)) * 16;
 }
 
-// Per-32-block scales: lanes 2i and 2i+1 hold the two halves of one block and share its amax.
+// Per-32-block scales. Workgroup = (32-token group g, blocks 4 y .. 4 y + 3); wave w takes block
+// b = 4 y + w and lane L = h*32 + t%32 the 16 elements of half h of token t's block b, so each wave
+// writes one whole 1 KB fragment; the block scale comes from the amax of lanes L and L ^ 32.
 __global__ __launch_bounds__(256) void act_quant_frag_kernel(const float* __restrict__ x, int T, int Tpad, int K,
                                                              int8_t* __restrict__ xq, float* __restrict__ xd) {
-  const int nb = K / kBlock, hb = 2 * nb;
-  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const bool live = g < (int64_t)Tpad * hb;  // hb is even: both lanes of a pair agree
-  const int t = live ? (int)(g / hb) : 0;
-  const int rem = live ? (int)(g - (int64_t)t * hb) : 0, b = rem >> 1, h = rem & 1;
+  const int nb = K / kBlock, g = blockIdx.x, lane = threadIdx.x & 63;
+  const int b = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (b >= nb) return;  // whole waves
+  const int h = lane >> 5, t = g * 32 + (lane & 31);
+  const bool ok = t < T;
+  const float* src = x + (int64_t)t * K + b * kBlock + h * 16;
   float4 v[4];
-  const float* src = x + (int64_t)t * K + rem * 16;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = live && t < T ? ld4(src, i) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int i = 0; i < 4; ++i) v[i] = ok ? ld4(src, i) : make_float4(0.f, 0.f, 0.f, 0.f);
   float a = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) a = amax4(v[i], a);
-  a = fmaxf(a, __shfl_xor(a, 1, 64));
+  a = fmaxf(a, __shfl_xor(a, 32, 64));
   const float sc = a / 127.0f;
   const float safe = sc == 0.f ? 1.f : sc;
-  const uint4 q = make_uint4(q8x4(v[0], safe), q8x4(v[1], safe), q8x4(v[2], safe), q8x4(v[3], safe));
-  if (!live) return;
-  *reinterpret_cast<uint4*>(xq + frag_offset(t, b, h, nb)) = q;
+  *reinterpret_cast<uint4*>(xq + ((int64_t)(g * nb + b) * 64 + lane) * 16) =
+      make_uint4(q8x4(v[0], safe), q8x4(v[1], safe), q8x4(v[2], safe), q8x4(v[3], safe));
   if (h == 0) xd[(int64_t)b * Tpad + t] = sc;
 }
 
@@ -730,8 +731,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
 
   // DMA roles. Activation: 1 KB fragment (group, block) = [half][32 tokens][16 B], the same layout
   // in HBM and in the slot; wave w copies group w (MT = 2) or half w & 1 of group w >> 1 (MT = 1,
-  // lanes 0-31). Weights: lane row (w & 1) * 64 + lane; q8 half w >> 1, q4 data (w < 2) or scale.
-  const int drow = (wave & 1) * 64 + lane;
+  // lanes 0-31). q8 weights: the slot holds 16-byte position p = 2 r + (h ^ bit 3 of r) for half h
+  // of row r, so that wave w's lanes read rows 32 w .. 32 w + 31 as consecutive 16-byte chunks of
+  // the repacked layout, and 16 lanes reading one half of 16 rows touch every LDS bank once.
+  // q4 weights: lane row (w & 1) * 64 + lane, data (w < 2) or scale.
+  const int drow = WDT == WQ8 ? wave * 32 + (lane >> 1) : (wave & 1) * 64 + lane;
+  const int dhalf = (lane & 1) ^ ((drow >> 3) & 1);  // q8: the half that lane fills
   const int wrow = min(r0 + drow, rows_pad - 1);
   const int64_t rbase = (int64_t)(wrow / H) * nb * H + (wrow % H);  // item of (wrow, block 0)
   const int8_t* const xg = a.xq + (int64_t)((t0 >> 5) + (MT == 2 ? wave : wave >> 1)) * nb * 1024 +
@@ -745,7 +750,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
     for (int sl = 0; sl < NSEL; ++sl) {
       unsigned char* wb = sb + R::ACT + sl * R::WSEL;
       if (WDT == WQ8) {
-        dma16(wdata(sl) + it * 32 + (wave >> 1) * 16, wb + wave * 1024);
+        dma16(wdata(sl) + it * 32 + dhalf * 16, wb + wave * 1024);
       } else if (wave < 2) {
         dma16(wdata(sl) + it * 16, wb + wave * 1024);
       } else {
@@ -788,7 +793,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
       for (int nt = 0; nt < 2; ++nt) {
         const int rl = wr * 64 + nt * 32 + l32;
         if (WDT == WQ8) {
-          B[nt] = *reinterpret_cast<const v4i*>(wb + (h * kGemmTileN + rl) * 16);
+          B[nt] = *reinterpret_cast<const v4i*>(wb + (2 * rl + (h ^ ((rl >> 3) & 1))) * 16);
         } else {
           B[nt] = q4_operand16(*reinterpret_cast<const uint4*>(wb + rl * 16), h);
           c[nt] = reinterpret_cast<const float*>(wb + 2048)[rl];
@@ -1194,9 +1199,7 @@ hipError_t launch_act_quant_rows(const float* x, int T, int K, int8_t* xq, float
 }
 
 hipError_t launch_act_quant_frag(const float* x, int T, int Tpad, int K, int8_t* xq, float* xd, hipStream_t s) {
-  // one thread per half-block
-  const int64_t threads = (int64_t)Tpad * 2 * (K / kBlock);
-  const dim3 grid((unsigned)((threads + 255) / 256));
+  const dim3 grid(Tpad / 32, (K / kBlock + 3) / 4);
   act_quant_frag_kernel<<<grid, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
   return hipGetLastError();
 }
