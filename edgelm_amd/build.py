@@ -38,7 +38,7 @@ HIP_FLAGS = [
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wextra", "-pthread", f"-I{INC}",
               f"-I{HOST_INC}"]
 
-ELMH_SRCS = ["elmh_kernels.hip", "elmh_api.cpp"]
+ELMH_SRCS = ["elmh_kernels.hip", "elmh_layer.hip", "elmh_api.cpp"]
 
 
 def _run(cmd):

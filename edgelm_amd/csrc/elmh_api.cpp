@@ -679,8 +679,50 @@ int elmh_memcpy_d2h(elmh_ctx* c, void* dst, const void* src, size_t bytes) {
 
 int elmh_memset_dev(elmh_ctx* c, void* dst, int value, size_t bytes) {
   if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  if (bytes && !dst) return fail(c, ELMH_ERR_ARG, "null dst");
   DeviceGuard g(c);
-  HIP_OR_FAIL(c, hipMemsetAsync(dst, value, bytes, c->stream));
+  HIP_OR_FAIL(c, launch_fill(dst, value, bytes, c->stream));
+  return ELMH_OK;
+}
+
+int elmh_memcpy_d2d(elmh_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  if (bytes && (!dst || !src)) return fail(c, ELMH_ERR_ARG, "null dst/src");
+  DeviceGuard g(c);
+  if (bytes) HIP_OR_FAIL(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, c->stream));
+  return ELMH_OK;
+}
+
+int elmh_embed_dev(elmh_ctx* c, const int32_t* tokens, int T, const elmh_weight* table, float* y) {
+  if (!c || !tokens || !table || !y) return fail(c, ELMH_ERR_ARG, "null ctx/tokens/table/y");
+  if (T < 1) return fail(c, ELMH_ERR_ARG, "embed: T must be >= 1");
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, launch_embed(tokens, T, table->w, y, c->stream));
+  return ELMH_OK;
+}
+
+int elmh_rmsnorm_dev(elmh_ctx* c, const float* x, const float* w, float* y, int rows, int dim, float eps) {
+  if (!c || !x || !w || !y) return fail(c, ELMH_ERR_ARG, "null ctx/x/w/y");
+  if (rows < 1 || dim < 1 || dim > 16384) return fail(c, ELMH_ERR_ARG, "rmsnorm: rows %d, dim %d (1 .. 16384)", rows, dim);
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, launch_rmsnorm(x, w, y, rows, dim, eps, c->stream));
+  return ELMH_OK;
+}
+
+int elmh_attention_dev(elmh_ctx* c, const float* q, const float* k, const float* v, float* out, int T, int pos0,
+                       int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache, int max_ctx,
+                       const float* rope_cos, const float* rope_sin) {
+  if (!c || !q || !k || !v || !out || !k_cache || !v_cache) return fail(c, ELMH_ERR_ARG, "attention: null pointer");
+  if (T < 1 || pos0 < 0 || (int64_t)pos0 + T > max_ctx)
+    return fail(c, ELMH_ERR_ARG, "attention: context overflow (pos0 %d + T %d > max_ctx %d)", pos0, T, max_ctx);
+  if (n_heads < 1 || n_kv < 1 || n_heads % n_kv || head_dim < 4 || head_dim % 4 || head_dim > 512)
+    return fail(c, ELMH_ERR_ARG, "attention: heads %d / kv heads %d / head_dim %d", n_heads, n_kv, head_dim);
+  if (!rope_cos != !rope_sin) return fail(c, ELMH_ERR_ARG, "attention: rope_cos and rope_sin go together");
+  if (attention_lds_bytes(head_dim, pos0 + T) > 65536)
+    return fail(c, ELMH_ERR_UNSUPPORTED, "attention: %d positions exceed the kernel's LDS", pos0 + T);
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, launch_attention(q, k, v, out, T, pos0, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx, rope_cos,
+                                  rope_sin, c->stream));
   return ELMH_OK;
 }
 

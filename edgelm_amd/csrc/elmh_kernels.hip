@@ -658,14 +658,16 @@ typedef __attribute__((address_space(3))) unsigned char* LdsBytes;
 // One global_load_lds of 16 (or 4) bytes per active lane into LDS at dst + 16 (4) * lane (dst is
 // wave-uniform: it goes to M0). Written as asm so that the compiler's wait-count pass does not
 // track it (it would drain every in-flight load before each LDS read); the kernel waits for these
-// loads itself (wait_vm) and drains them all before its LDS is reused or released.
+// loads itself (wait_vm) and drains them all before its LDS is reused or released. M0 is a
+// register the compiler reserves and does not save around asm; the GEMM kernel makes no other use
+// of it (its code references M0 only inside these statements), so the write disturbs nothing.
 __device__ __forceinline__ void dma16(const void* src, unsigned char* dst) {
   const unsigned m0 = (unsigned)(size_t)(LdsBytes)dst;
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
 }
 __device__ __forceinline__ void dma4(const void* src, unsigned char* dst) {
   const unsigned m0 = (unsigned)(size_t)(LdsBytes)dst;
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory");
 }
 
 // s_waitcnt vmcnt(N) only (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4] << 14)

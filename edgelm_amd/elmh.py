@@ -205,6 +205,27 @@ class Context:
         self._check(lib().elmh_gemv_a8_dev(self.h, C.c_void_p(q_ptr), C.c_void_p(d_ptr), C.c_void_p(s_ptr), C.c_int(T),
                                            C.c_int64(K), C.c_int(n), wp, yp, rp))
 
+    # ---- the rest of a layer (device pointers; same float order as edgelm's cpu backend)
+    def embed_dev(self, tok_ptr, T, table, y_ptr):
+        self._check(lib().elmh_embed_dev(self.h, C.c_void_p(tok_ptr), C.c_int(T), table.h, C.c_void_p(y_ptr)))
+
+    def rmsnorm_dev(self, x_ptr, w_ptr, y_ptr, rows, dim, eps):
+        self._check(lib().elmh_rmsnorm_dev(self.h, C.c_void_p(x_ptr), C.c_void_p(w_ptr), C.c_void_p(y_ptr),
+                                           C.c_int(rows), C.c_int(dim), C.c_float(eps)))
+
+    def attention_dev(self, q_ptr, k_ptr, v_ptr, out_ptr, T, pos0, n_heads, n_kv, head_dim, kc_ptr, vc_ptr, max_ctx,
+                      cos_ptr=None, sin_ptr=None):
+        self._check(lib().elmh_attention_dev(
+            self.h, C.c_void_p(q_ptr), C.c_void_p(k_ptr), C.c_void_p(v_ptr), C.c_void_p(out_ptr), C.c_int(T),
+            C.c_int(pos0), C.c_int(n_heads), C.c_int(n_kv), C.c_int(head_dim), C.c_void_p(kc_ptr), C.c_void_p(vc_ptr),
+            C.c_int(max_ctx), C.c_void_p(cos_ptr), C.c_void_p(sin_ptr)))
+
+    def memcpy_d2d(self, dst_ptr, src_ptr, nbytes):
+        self._check(lib().elmh_memcpy_d2d(self.h, C.c_void_p(dst_ptr), C.c_void_p(src_ptr), C.c_size_t(nbytes)))
+
+    def memset_dev(self, dst_ptr, value, nbytes):
+        self._check(lib().elmh_memset_dev(self.h, C.c_void_p(dst_ptr), C.c_int(value), C.c_size_t(nbytes)))
+
     def buffer(self, nbytes):
         return DevBuffer(self, nbytes)
 

@@ -108,6 +108,25 @@ int elmh_quantize_act_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, int8_
 int elmh_gemv_a8_dev(elmh_ctx* ctx, const int8_t* q, const float* d, const int32_t* s, int T, int64_t K,
                      int n_targets, elmh_weight* const* w, float* const* y, const float* const* residual);
 
+/* ---- the rest of a layer on the device (device pointers, asynchronous on the context stream) ----
+ * Same float operations in the same order as edgelm's cpu backend, so results are bit-identical.
+ *
+ * EMBED (the reference backend's EMBED = dequantize_row per token, model.cpp:192-218):
+ * y[t, :] = dequantize_row(table, tokens[t]) for a q8 or q4 table uploaded with
+ * elmh_upload_weight; token ids must lie in [0, rows) (the caller checks, as edgelm does). */
+int elmh_embed_dev(elmh_ctx* ctx, const int32_t* tokens, int T, const elmh_weight* table, float* y);
+/* RMSNORM (cpu::rmsnorm, kernels_cpu.cpp:326-335): y = x * (1 / sqrt(dot_f32(x, x) / dim + eps)) * w
+ * per row, dot_f32 in the four-accumulator order of dot_f32_scalar (kernels_cpu.cpp:30-43). */
+int elmh_rmsnorm_dev(elmh_ctx* ctx, const float* x, const float* w, float* y, int rows, int dim, float eps);
+/* ATTENTION (cpu::attention, kernels_cpu.cpp:417-488; AttnArgs, kernels.hpp:28-36): appends this
+ * step's keys (rotated when rope_cos/rope_sin, the RopeTable's [pos][head_dim/2] arrays, are given)
+ * and values to the cache [n_kv][max_ctx][head_dim] at positions pos0 .. pos0+T-1, then
+ * out[t, h] = softmax over positions 0 .. pos0+t of (rotated q . k_j) / sqrt(head_dim), applied to v.
+ * q [T, n_heads*head_dim], k/v [T, n_kv*head_dim]. */
+int elmh_attention_dev(elmh_ctx* ctx, const float* q, const float* k, const float* v, float* out, int T, int pos0,
+                       int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache, int max_ctx,
+                       const float* rope_cos, const float* rope_sin);
+
 /* ---- test hooks ----
  * quantize_act_row on the device (host pointers; q [T,K], d [T,K/32]). */
 int elmh_quantize_act(elmh_ctx* ctx, const float* x, int T, int64_t K, int8_t* q, float* d);
@@ -120,7 +139,10 @@ int elmh_malloc(elmh_ctx* ctx, size_t bytes, void** dptr);
 int elmh_free(elmh_ctx* ctx, void* dptr);
 int elmh_memcpy_h2d(elmh_ctx* ctx, void* dst, const void* src, size_t bytes);
 int elmh_memcpy_d2h(elmh_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Device fill (a kernel, so it may be captured in a HIP graph) and device-to-device copy; both
+ * asynchronous on the context stream. LAST_ROWS (backends.cpp, reference) is one such copy. */
 int elmh_memset_dev(elmh_ctx* ctx, void* dst, int value, size_t bytes);
+int elmh_memcpy_d2d(elmh_ctx* ctx, void* dst, const void* src, size_t bytes);
 int elmh_synchronize(elmh_ctx* ctx);
 void* elmh_stream(elmh_ctx* ctx); /* the context's hipStream_t */
 /* Events on the context stream: record, then elapsed milliseconds between two records. */

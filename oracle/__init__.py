@@ -214,7 +214,65 @@ def silu(v):
     return orc().orc_silu(C.c_float(v))
 
 
+# ------------------------------------------------------------------ layer ops (cpu backend)
+
+def _layer_call(lib, prefix, q, k, v, pos0, n_heads, n_kv, kc, vc, rope_arg):
+    q, k, v = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v))
+    T = q.shape[0]
+    hd = q.shape[1] // n_heads
+    out = np.empty_like(q)
+    args = [_ptr(q), _ptr(k), _ptr(v), _ptr(out), C.c_int(T), C.c_int(pos0), C.c_int(n_heads), C.c_int(n_kv),
+            C.c_int(hd), _ptr(kc), _ptr(vc), C.c_int(kc.shape[1])] + rope_arg
+    getattr(lib, prefix + "_attention")(*args)
+    return out
+
+
+def rope_table(head_dim, max_pos, theta):
+    """kernels_ref.cpp:11-21: (cos, sin) [max_pos, head_dim/2]."""
+    c = np.empty((max_pos, head_dim // 2), np.float32)
+    s = np.empty_like(c)
+    orc().orc_rope_table(C.c_int(head_dim), C.c_int(max_pos), C.c_float(theta), _ptr(c), _ptr(s))
+    return c, s
+
+
+def rmsnorm(x, w, eps):
+    """cpu::rmsnorm (kernels_cpu.cpp:326-335), x86 scalar dot_f32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    y = np.empty_like(x)
+    orc().orc_rmsnorm(_ptr(x), _ptr(w), _ptr(y), C.c_int(x.shape[0]), C.c_int(x.shape[1]), C.c_float(eps))
+    return y
+
+
+def attention(q, k, v, pos0, n_heads, n_kv, kc, vc, rope=None):
+    """cpu::attention (kernels_cpu.cpp:417-488). kc/vc: float32 [n_kv, max_ctx, hd] caches, updated
+    in place. rope: (cos, sin) from rope_table, or None."""
+    r = [None, None] if rope is None else [np.ascontiguousarray(rope[0]), np.ascontiguousarray(rope[1])]
+    return _layer_call(orc(), "orc", q, k, v, pos0, n_heads, n_kv, kc, vc, [_ptr(r[0]), _ptr(r[1])])
+
+
 # ------------------------------------------------------------------ edgelm's own C++ (oracle/_ref)
+
+def rq_rope_table(head_dim, max_pos, theta):
+    c = np.empty((max_pos, head_dim // 2), np.float32)
+    s = np.empty_like(c)
+    ref().eref_rope_table(C.c_int(head_dim), C.c_int(max_pos), C.c_float(theta), _ptr(c), _ptr(s))
+    return c, s
+
+
+def rq_rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    y = np.empty_like(x)
+    ref().eref_rmsnorm(_ptr(x), _ptr(w), _ptr(y), C.c_int(x.shape[0]), C.c_int(x.shape[1]), C.c_float(eps))
+    return y
+
+
+def rq_attention(q, k, v, pos0, n_heads, n_kv, kc, vc, theta=None):
+    """edgelm's cpu::attention; theta None: no rotary embedding, else a RopeTable(hd, max_ctx, theta)."""
+    return _layer_call(ref(), "eref", q, k, v, pos0, n_heads, n_kv, kc, vc,
+                       [C.c_int(0 if theta is None else 1), C.c_float(0.0 if theta is None else theta)])
+
 
 def rq_quantize_q8(w):
     w = np.ascontiguousarray(w, dtype=np.float32)

@@ -409,3 +409,88 @@ void orc_matmul_a8_token(const float* x, int T, const orc_weight* w, float* y, c
   }
   free(q);
 }
+
+/* ------------------------------------------------------------------ layer ops (cpu backend) */
+
+/* kernels_ref.cpp:11-21: the RopeTable, computed in double, [pos][head_dim/2] */
+void orc_rope_table(int head_dim, int max_pos, float theta, float* cos_out, float* sin_out) {
+  const int half = head_dim / 2;
+  for (int p = 0; p < max_pos; ++p)
+    for (int i = 0; i < half; ++i) {
+      const double inv = pow((double)theta, -2.0 * i / head_dim);
+      const double a = p * inv;
+      cos_out[(int64_t)p * half + i] = (float)cos(a);
+      sin_out[(int64_t)p * half + i] = (float)sin(a);
+    }
+}
+
+/* kernels_cpu.cpp:326-335 with dot_f32_scalar: inv = 1 / sqrt(dot(x, x) / dim + eps), y = x * inv * w */
+void orc_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * dim;
+    const float inv = 1.0f / sqrtf(dot_f32_scalar(xr, xr, dim) / dim + eps);
+    for (int i = 0; i < dim; ++i) y[r * dim + i] = xr[i] * inv * w[i];
+  }
+}
+
+/* kernels_cpu.cpp:417-488 (serial): append this step's keys (rotated when rcos != NULL) and values
+ * to the cache [n_kv][max_ctx][hd], then one task per (token, head). */
+void orc_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0, int n_heads, int n_kv,
+                   int hd, float* kc, float* vc, int max_ctx, const float* rcos, const float* rsin) {
+  const int h2 = hd / 2, kvd = n_kv * hd, qd = n_heads * hd, grp = n_heads / n_kv;
+  const int64_t mc = max_ctx;
+  for (int t = 0; t < T; ++t) {
+    const int pos = pos0 + t;
+    for (int h = 0; h < n_kv; ++h) {
+      const float* ks = k + (int64_t)t * kvd + h * hd;
+      float* kd = kc + (h * mc + pos) * hd;
+      if (rcos) {
+        const float* c = rcos + (int64_t)pos * h2;
+        const float* sn = rsin + (int64_t)pos * h2;
+        for (int i = 0; i < h2; ++i) {
+          kd[i] = ks[i] * c[i] - ks[i + h2] * sn[i];
+          kd[i + h2] = ks[i + h2] * c[i] + ks[i] * sn[i];
+        }
+      } else {
+        memcpy(kd, ks, sizeof(float) * hd);
+      }
+      memcpy(vc + (h * mc + pos) * hd, v + (int64_t)t * kvd + h * hd, sizeof(float) * hd);
+    }
+  }
+  const float scale = 1.0f / sqrtf((float)hd);
+  float* qbuf = (float*)malloc(sizeof(float) * (size_t)hd);
+  float* sc = (float*)malloc(sizeof(float) * (size_t)(pos0 + T));
+  for (int64_t idx = 0; idx < (int64_t)T * n_heads; ++idx) {
+    const int t = (int)(idx / n_heads), h = (int)(idx % n_heads), pos = pos0 + t;
+    const float* qs = q + (int64_t)t * qd + h * hd;
+    if (rcos) {
+      const float* c = rcos + (int64_t)pos * h2;
+      const float* sn = rsin + (int64_t)pos * h2;
+      for (int i = 0; i < h2; ++i) {
+        qbuf[i] = qs[i] * c[i] - qs[i + h2] * sn[i];
+        qbuf[i + h2] = qs[i + h2] * c[i] + qs[i] * sn[i];
+      }
+      qs = qbuf;
+    }
+    const float* kh = kc + (int64_t)(h / grp) * mc * hd;
+    const float* vh = vc + (int64_t)(h / grp) * mc * hd;
+    const int n = pos + 1;
+    float mx = -INFINITY;
+    for (int j = 0; j < n; ++j) {
+      sc[j] = dot_f32_scalar(qs, kh + (int64_t)j * hd, hd) * scale;
+      mx = fmax_std(mx, sc[j]);
+    }
+    float sum = 0.f;
+    for (int j = 0; j < n; ++j) sum += (sc[j] = expf(sc[j] - mx));
+    const float inv = 1.0f / sum;
+    float* o = out + (int64_t)t * qd + h * hd;
+    for (int i = 0; i < hd; ++i) o[i] = 0.f;
+    for (int j = 0; j < n; ++j) {
+      const float p = sc[j] * inv;
+      const float* vj = vh + (int64_t)j * hd;
+      for (int i = 0; i < hd; ++i) o[i] += p * vj[i];
+    }
+  }
+  free(qbuf);
+  free(sc);
+}

@@ -70,6 +70,14 @@ void orc_quantize_act_row_token(const float* x, int64_t k, int8_t* q, float* d);
  *   q4: out = (sum_b (float)S_b * ws[n,b]) * d_t, sequential over b (mul, add) */
 void orc_matmul_a8_token(const float* x, int T, const orc_weight* w, float* y, const float* residual);
 
+/* kernels_ref.cpp:11-21: RopeTable cos/sin [max_pos][head_dim/2], computed in double */
+void orc_rope_table(int head_dim, int max_pos, float theta, float* cos_out, float* sin_out);
+/* kernels_cpu.cpp:326-335 (cpu::rmsnorm, x86 scalar dot_f32) */
+void orc_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps);
+/* kernels_cpu.cpp:417-488 (cpu::attention, serial); rcos/rsin NULL: no rotary embedding */
+void orc_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0, int n_heads, int n_kv,
+                   int hd, float* kc, float* vc, int max_ctx, const float* rcos, const float* rsin);
+
 #ifdef __cplusplus
 }
 #endif

@@ -177,4 +177,36 @@ int eref_session_describe(void* h, char* buf, int cap) {
   return static_cast<int>(r->session->graph().ops.size());
 }
 
+
+// RopeTable (kernels_ref.cpp:11-21), cpu::rmsnorm (kernels_cpu.cpp:326-335) and cpu::attention
+// (kernels_cpu.cpp:417-488) as edgelm runs them (no pool: serial).
+void eref_rope_table(int head_dim, int max_pos, float theta, float* cos_out, float* sin_out) {
+  RopeTable rt(head_dim, max_pos, theta);
+  std::memcpy(cos_out, rt.cos.data(), rt.cos.size() * sizeof(float));
+  std::memcpy(sin_out, rt.sin.data(), rt.sin.size() * sizeof(float));
+}
+void eref_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps) {
+  cpu::rmsnorm(x, w, y, rows, dim, eps, nullptr);
+}
+void eref_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0, int n_heads, int n_kv,
+                    int hd, float* kc, float* vc, int max_ctx, int rope, float theta) {
+  RopeTable rt(hd, max_ctx, theta);
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.T = T;
+  a.pos0 = pos0;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv;
+  a.head_dim = hd;
+  a.cache.k = kc;
+  a.cache.v = vc;
+  a.cache.max_ctx = max_ctx;
+  a.rope = rope ? &rt : nullptr;
+  std::vector<float> scratch(static_cast<size_t>(max_ctx) + hd + 16);
+  float* sp = scratch.data();
+  cpu::attention(a, nullptr, &sp);
+}
 }  // extern "C"

@@ -8,6 +8,7 @@ build is absent. Inputs come from numpy's default_rng with the seeds below; outp
                                   reference's own int8 test (make_tiny.py:448-450)
   cpu::matmul / cpu::swiglu       (kernels_cpu.cpp:339-411), act f32 and int8, x86 scalar path
   ref::matmul / ref::swiglu       (kernels_ref.cpp:58-80, 153-160)
+  RopeTable, cpu::rmsnorm, cpu::attention (kernels_ref.cpp:11-21, kernels_cpu.cpp:326-335, 417-488)
 Shapes and token counts follow tests/test_ops.cpp:119-154 and 192-240.
 
     python tests/golden/gen_fixtures.py
@@ -22,6 +23,33 @@ sys.path.insert(0, ROOT)
 import oracle as O  # noqa: E402
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "edgelm_ref_vectors.npz")
+
+
+ATTN_CALLS = [(0, 5), (5, 1), (6, 3)]  # (pos0, T): prefill, decode, chunk
+
+
+def layer_fixtures(out):
+    """RopeTable (kernels_ref.cpp:11-21), cpu::rmsnorm (kernels_cpu.cpp:326-335) and cpu::attention
+    (kernels_cpu.cpp:417-488) on SmolLM2-135M's head shape (9 query / 3 KV heads of 64)."""
+    rng = np.random.default_rng(20260102)
+    out["rope.cos"], out["rope.sin"] = O.rq_rope_table(64, 40, 100000.0)
+    for i, (rows, dim) in enumerate([(4, 578), (3, 576), (2, 7)]):
+        x = rng.normal(0, 1, (rows, dim)).astype(np.float32)
+        w = rng.normal(1, 0.1, dim).astype(np.float32)
+        out[f"rms{i}.x"], out[f"rms{i}.w"] = x, w
+        out[f"rms{i}.y"] = O.rq_rmsnorm(x, w, 1e-5)
+    nh, nkv, hd, mc = 9, 3, 64, 24
+    for rope in (0, 1):
+        kc = np.zeros((nkv, mc, hd), np.float32)
+        vc = np.zeros_like(kc)
+        for j, (pos0, T) in enumerate(ATTN_CALLS):
+            p = f"attn{rope}.{j}."
+            q = rng.normal(0, 1, (T, nh * hd)).astype(np.float32)
+            k = rng.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+            v = rng.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+            out[p + "q"], out[p + "k"], out[p + "v"] = q, k, v
+            out[p + "out"] = O.rq_attention(q, k, v, pos0, nh, nkv, kc, vc, 100000.0 if rope else None)
+        out[f"attn{rope}.kc"], out[f"attn{rope}.vc"] = kc, vc
 
 
 def main():
@@ -63,6 +91,7 @@ def main():
         out[p + "ref"] = O.rq_ref_matmul(x, W, res, aq)
         out[p + "ref_sw"] = O.rq_ref_swiglu(x, W, Wu, aq)
     pool.close()
+    layer_fixtures(out)
     np.savez_compressed(OUT, **out)
     print(f"wrote {OUT}: {len(out)} arrays, {os.path.getsize(OUT)} bytes")
 

@@ -1,0 +1,112 @@
+"""GPU parity of the non-matmul layer ops (edgelm_amd/csrc/elmh_layer.hip through the C ABI)
+against the CPU oracle, which restates edgelm's cpu backend and is pinned against edgelm's own
+C++ (tests/test_oracle_layer.py). Bar: bit-identical outputs and KV caches.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import bits_equal
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(ctx, a):
+    a = np.ascontiguousarray(a)
+    b = ctx.buffer(max(a.nbytes, 4))
+    b.upload(a)
+    return b
+
+
+@pytest.mark.parametrize("dim", [576, 578, 1, 64, 1536])
+def test_rmsnorm_bit_exact(ctx, dim):
+    r = np.random.default_rng(dim)
+    for rows in (1, 3, 130):
+        print(f"[gpu] rmsnorm dim={dim} rows={rows}", flush=True)
+        x = r.normal(0, 2, (rows, dim)).astype(np.float32)
+        x[0, : min(dim, 5)] = 0.0
+        w = r.normal(1, 0.2, dim).astype(np.float32)
+        bx, bw, by = dev(ctx, x), dev(ctx, w), ctx.buffer(x.nbytes)
+        ctx.rmsnorm_dev(bx.ptr, bw.ptr, by.ptr, rows, dim, 1e-5)
+        assert bits_equal(by.download(x.shape, np.float32), O.rmsnorm(x, w, 1e-5))
+        for b in (bx, bw, by):
+            b.free()
+
+
+@pytest.mark.parametrize("shape", [(9, 3, 64, 160), (4, 4, 32, 48), (8, 1, 128, 40)])
+@pytest.mark.parametrize("rope", [False, True])
+def test_attention_bit_exact(ctx, shape, rope):
+    """A session's sequence of calls: prefill, decodes and a chunk, KV cache carried on the GPU."""
+    nh, nkv, hd, mc = shape
+    r = np.random.default_rng(nh * 100 + hd + int(rope))
+    tab = O.rope_table(hd, mc, 100000.0) if rope else None
+    kc = np.zeros((nkv, mc, hd), np.float32)
+    vc = np.zeros_like(kc)
+    bkc, bvc = dev(ctx, kc), dev(ctx, vc)
+    bcos, bsin = (dev(ctx, tab[0]), dev(ctx, tab[1])) if rope else (None, None)
+    pos = 0
+    for T in (17, 1, 1, 5, 1, 9):
+        if pos + T > mc:
+            break
+        print(f"[gpu] attention {shape} rope={rope} pos0={pos} T={T}", flush=True)
+        q = r.normal(0, 1, (T, nh * hd)).astype(np.float32)
+        k = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+        v = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+        bq, bk, bv, bo = dev(ctx, q), dev(ctx, k), dev(ctx, v), ctx.buffer(q.nbytes)
+        ctx.attention_dev(bq.ptr, bk.ptr, bv.ptr, bo.ptr, T, pos, nh, nkv, hd, bkc.ptr, bvc.ptr, mc,
+                          bcos.ptr if rope else None, bsin.ptr if rope else None)
+        want = O.attention(q, k, v, pos, nh, nkv, kc, vc, tab)
+        assert bits_equal(bo.download(q.shape, np.float32), want), f"pos0={pos} T={T}"
+        for b in (bq, bk, bv, bo):
+            b.free()
+        pos += T
+    assert bits_equal(bkc.download(kc.shape, np.float32), kc)
+    assert bits_equal(bvc.download(vc.shape, np.float32), vc)
+    for b in [bkc, bvc] + ([bcos, bsin] if rope else []):
+        b.free()
+
+
+def test_attention_rejects_bad_shapes(ctx):
+    from edgelm_amd import elmh as E
+    b = ctx.buffer(4096)
+    for args in [(1, 8, 9, 3, 64, 8),    # pos0 + T > max_ctx
+                 (1, 0, 9, 4, 64, 8),    # heads not a multiple of kv heads
+                 (1, 0, 9, 3, 62, 8)]:   # head_dim not a multiple of 4
+        T, pos0, nh, nkv, hd, mc = args
+        with pytest.raises(E.ElmhError) as e:
+            ctx.attention_dev(b.ptr, b.ptr, b.ptr, b.ptr, T, pos0, nh, nkv, hd, b.ptr, b.ptr, mc)
+        assert e.value.code == E.ERR_ARG
+    b.free()
+
+
+@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
+def test_embed_bit_exact(ctx, dt):
+    r = np.random.default_rng(30 + dt)
+    rows, cols = 300, 576
+    w = O.make_weight(r.normal(0, 0.5, (rows, cols)).astype(np.float32), dt)
+    dw = ctx.upload(w.dtype, w.rows, w.cols, w.data, w.scales)
+    full = O.dequantize(w)
+    for toks in ([0], [rows - 1, 5, 5, 123], list(r.integers(0, rows, 70))):
+        print(f"[gpu] embed dt={dt} T={len(toks)}", flush=True)
+        t = np.array(toks, np.int32)
+        bt, by = dev(ctx, t), ctx.buffer(len(toks) * cols * 4)
+        ctx.embed_dev(bt.ptr, len(toks), dw, by.ptr)
+        assert bits_equal(by.download((len(toks), cols), np.float32), full[t])
+        bt.free()
+        by.free()
+    dw.free()
+
+
+def test_fill_and_copy(ctx):
+    b = ctx.buffer(1031)
+    b.upload(np.arange(1031, dtype=np.uint8))
+    ctx.memset_dev(b.ptr + 3, 0xAB, 1021)
+    got = b.download((1031,), np.uint8)
+    want = np.arange(1031, dtype=np.uint8)
+    want[3:1024] = 0xAB
+    assert np.array_equal(got, want)
+    c = ctx.buffer(1031)
+    ctx.memcpy_d2d(c.ptr, b.ptr, 1031)
+    assert np.array_equal(c.download((1031,), np.uint8), want)
+    b.free()
+    c.free()
