@@ -318,8 +318,9 @@ def gemm_bench(ctx, E, T, shapes, dt=1, act=None, reps=10, eager=False):
 
 def e2e_bench(path_dir, P=128, G=64, reps=3, cpu_reference=True):
     """random-init SmolLM2-135M (q4 g32 + q8 embedding, int8 activations) through this
-    build's Session with backends hip,cpu; edgelm's bench protocol (main.cpp:173-233): LCG prompt,
-    warm-up rep, then the median of `reps` reps of prefill + argmax (TTFT) + G greedy decodes."""
+    build's Session, backends "hip,cpu" (whole model on the GPU) and "hip-matmul,cpu" (matmuls on the
+    GPU); edgelm's bench protocol (main.cpp:173-233): LCG prompt, warm-up rep, then the median of
+    `reps` reps of prefill + argmax (TTFT) + G greedy decodes."""
     from edgelm_amd import elm_format as F
     from edgelm_amd import host
     path = os.path.join(path_dir, "smollm2-135m-random.q4.elm")
@@ -329,14 +330,25 @@ def e2e_bench(path_dir, P=128, G=64, reps=3, cpu_reference=True):
     prompt = F.lcg_prompt(P, 49152)
     threads = min(8, os.cpu_count() or 1)
     m = host.Model(path)
-    s = host.Session(m, "hip,cpu", threads=threads, max_ctx=P + G + 8, max_batch=P, act_quant=True)
-    runs = [s.generate(prompt, G) for _ in range(reps + 1)][1:]
     med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731
-    out = {"prefill_tok_s": med([P / (r["prefill_ms"] / 1e3) for r in runs]), "ttft_ms": med([r["ttft_ms"] for r in runs]),
-           "decode_tok_s": med([G / (r["decode_ms"] / 1e3) for r in runs]), "prompt": P, "gen": G,
-           "host_threads": threads, "backends": "hip,cpu", "greedy_tokens_head": [int(t) for t in runs[0]["tokens"][:8]]}
-    s.close()
-    log(f"e2e: prefill {out['prefill_tok_s']:.1f} tok/s, TTFT {out['ttft_ms']:.2f} ms, decode {out['decode_tok_s']:.1f} tok/s")
+
+    def session_bench(backends):
+        s = host.Session(m, backends, threads=threads, max_ctx=P + G + 8, max_batch=P, act_quant=True)
+        runs = [s.generate(prompt, G) for _ in range(reps + 1)][1:]
+        s.close()
+        r = {"prefill_tok_s": med([P / (x["prefill_ms"] / 1e3) for x in runs]), "ttft_ms": med([x["ttft_ms"] for x in runs]),
+             "decode_tok_s": med([G / (x["decode_ms"] / 1e3) for x in runs]), "backends": backends}
+        log(f"e2e {backends}: prefill {r['prefill_tok_s']:.1f} tok/s, TTFT {r['ttft_ms']:.2f} ms, "
+            f"decode {r['decode_tok_s']:.1f} tok/s")
+        return r, runs
+
+    # the whole model on the GPU (activations and KV cache resident in HBM)
+    out, runs = session_bench("hip,cpu")
+    out.update({"prompt": P, "gen": G, "host_threads": threads,
+                "greedy_tokens_head": [int(t) for t in runs[0]["tokens"][:8]]})
+    # matmuls only on the GPU, the rest on the host cores (activations cross PCIe around every matmul)
+    out["matmul_only"], runs_mm = session_bench("hip-matmul,cpu")
+    out["matmul_only"]["greedy_tokens_match"] = bool(np.array_equal(runs_mm[0]["tokens"], runs[0]["tokens"]))
     if cpu_reference:
         import oracle as O
         if O.ref_available():

@@ -47,21 +47,31 @@ struct ExecContext {
   int64_t rows(int i) const;
 };
 
+struct Partition;
+
 class Backend {
  public:
   virtual ~Backend() = default;
   virtual const char* name() const = 0;
   virtual bool supports(const Graph& g, const Op& op) const = 0;
   virtual void run(const Op& op, ExecContext& ctx) = 0;
+  // Optional (default: nothing), called once by the Session after partitioning: lets a device
+  // backend keep activations on its device between its own consecutive ops and copy to the host
+  // arena only what other backends read. Source-compatible with edgelm's Backend.
+  virtual void prepare(const Graph&, const std::vector<Partition>&) {}
 };
 
 std::unique_ptr<Backend> make_reference_backend();
 std::unique_ptr<Backend> make_cpu_backend();
-// The MI355X delegate: MATMUL / MATMUL_N / MATMUL_ADD / FFN_SWIGLU with q8 or q4 weights.
+// The MI355X delegate ("hip"): MATMUL / MATMUL_N / MATMUL_ADD / FFN_SWIGLU with q8 or q4 weights,
+// EMBED (q8/q4 table), RMSNORM, ATTENTION and LAST_ROWS, activations kept in HBM between its ops.
 // Throws if no gfx950 device is usable.
 std::unique_ptr<Backend> make_hip_backend(int device = 0);
-// Same claims as the hip backend but no device: for partition inspection only (run() throws).
-std::unique_ptr<Backend> make_hip_planning_backend();
+// "hip-matmul": the matmul family only (the template of edgelm's MatmulOnlyBackend).
+std::unique_ptr<Backend> make_hip_matmul_backend(int device = 0);
+// Same claims as the hip (layer_ops) or hip-matmul backend but no device: for partition
+// inspection only (run() throws).
+std::unique_ptr<Backend> make_hip_planning_backend(bool layer_ops = true);
 std::unique_ptr<Backend> make_backend(const std::string& name);
 
 struct Partition {

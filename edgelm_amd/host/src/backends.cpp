@@ -113,6 +113,7 @@ std::unique_ptr<Backend> make_backend(const std::string& name) {
   if (name == "reference" || name == "ref") return make_reference_backend();
   if (name == "cpu") return make_cpu_backend();
   if (name == "hip") return make_hip_backend(0);
+  if (name == "hip-matmul") return make_hip_matmul_backend(0);
   throw std::runtime_error("edgelm: unknown backend " + name);
 }
 

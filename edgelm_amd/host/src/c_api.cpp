@@ -108,7 +108,7 @@ int elm_model_partition(const elm_model* m, const char* backends, int fuse, char
     std::vector<std::unique_ptr<Backend>> owned;
     for (const std::string& b : split(backends)) {
       if (b == "reference" || b == "ref") continue;
-      owned.push_back(b == "hip" ? make_hip_planning_backend() : make_backend(b));
+      owned.push_back(b == "hip" || b == "hip-matmul" ? make_hip_planning_backend(b == "hip") : make_backend(b));
     }
     owned.push_back(make_reference_backend());
     std::vector<Backend*> pref;

@@ -1,8 +1,19 @@
 // The MI355X delegate as an edgelm Backend (reference interface backend.hpp:30-36; template
-// MatmulOnlyBackend, backends.cpp:137-150). It claims MATMUL, MATMUL_N, MATMUL_ADD and FFN_SWIGLU
-// when every weight of the op is q8 or q4, uploads each weight tensor to HBM once (repacked) on
-// first use, and runs the op through the C ABI of include/elmh.h. run() is synchronous: outputs
-// are in the host arena when it returns, as edgelm's Session requires (runtime.cpp:66-76).
+// MatmulOnlyBackend, backends.cpp:137-150), in two flavours:
+//   "hip"         MATMUL, MATMUL_N, MATMUL_ADD, FFN_SWIGLU (q8 or q4 weights) and the rest of a
+//                 layer: EMBED (q8/q4 table), RMSNORM, ATTENTION (RoPE and KV cache on the
+//                 device) and LAST_ROWS;
+//   "hip-matmul"  the matmul family only (the cpu backend runs the rest).
+//
+// With prepare() (the optional hook this build's Backend adds; not virtual in edgelm's, where it is
+// simply never called) activations stay in HBM between consecutive hip ops: prepare() marks which
+// activation tensors hip ops produce and which another backend reads or the graph outputs, and
+// run() uploads an input produced on the host once per forward, keeps every output on the device
+// and copies an output into the host arena only when the host needs it. Without prepare(), as
+// inside an unmodified edgelm Session, run() uploads every input and copies every output back.
+// Either way the host has what it needs when run() returns (edgelm's contract: runtime.cpp:66-76).
+// Weights are uploaded to HBM once, on first use (matmul weights repacked; RMSNORM weights f32).
+#include <cstring>
 #include <unordered_map>
 
 #include "edgelm/backend.hpp"
@@ -11,66 +22,208 @@
 namespace edgelm {
 namespace {
 
+bool matmul_family(OpType t) {
+  return t == OpType::MATMUL || t == OpType::MATMUL_N || t == OpType::MATMUL_ADD || t == OpType::FFN_SWIGLU;
+}
+
 class HipBackend : public Backend {
  public:
   // device < 0: planning only (supports() answers, run() throws) — for partition inspection on a
   // host without a GPU.
-  explicit HipBackend(int device) {
+  HipBackend(int device, bool layer_ops) : layer_ops_(layer_ops) {
     if (device < 0) return;
     if (elmh_create(device, &ctx_) != ELMH_OK)
       throw std::runtime_error(std::string("edgelm: hip backend unavailable: ") + elmh_last_error(nullptr));
   }
   ~HipBackend() override {
+    if (!ctx_) return;
     for (auto& kv : weights_) elmh_free_weight(ctx_, kv.second);
-    if (ctx_) elmh_destroy(ctx_);
+    for (auto& kv : f32w_) elmh_free(ctx_, kv.second);
+    for (Buf& b : act_) elmh_free(ctx_, b.p);
+    for (Layer& l : kv_) {
+      elmh_free(ctx_, l.k);
+      elmh_free(ctx_, l.v);
+    }
+    elmh_free(ctx_, rope_cos_);
+    elmh_free(ctx_, rope_sin_);
+    elmh_destroy(ctx_);
   }
 
-  const char* name() const override { return "hip"; }
+  const char* name() const override { return layer_ops_ ? "hip" : "hip-matmul"; }
 
   bool supports(const Graph& g, const Op& op) const override {
-    size_t first = 1, count = 0;
+    if (matmul_family(op.type)) {
+      const size_t count = op.type == OpType::MATMUL_N ? op.out.size() : op.type == OpType::FFN_SWIGLU ? 2 : 1;
+      if (op.in.size() < 1 + count) return false;
+      for (size_t i = 1; i <= count; ++i)
+        if (!quantized(g.tensors[op.in[i]])) return false;
+      return true;
+    }
+    if (!layer_ops_) return false;
     switch (op.type) {
-      case OpType::MATMUL:
-      case OpType::MATMUL_ADD: count = 1; break;
-      case OpType::MATMUL_N: count = op.out.size(); break;
-      case OpType::FFN_SWIGLU: count = 2; break;
+      case OpType::EMBED: return op.in.size() == 2 && quantized(g.tensors[op.in[1]]);
+      case OpType::RMSNORM: {
+        const Tensor& w = g.tensors[op.in[1]];
+        return w.is_weight() && w.dtype == DType::F32 && g.tensors[op.in[0]].cols <= 16384;
+      }
+      case OpType::ATTENTION: {
+        const int nh = op.iattr[1], nkv = op.iattr[2];
+        if (nh < 1 || nkv < 1 || nh % nkv) return false;
+        const int64_t hd = g.tensors[op.in[0]].cols / nh;
+        return hd >= 4 && hd % 4 == 0 && hd <= 512;
+      }
+      case OpType::LAST_ROWS: return true;
       default: return false;
     }
-    if (op.in.size() < first + count) return false;
-    for (size_t i = first; i < first + count; ++i) {
-      const Tensor& w = g.tensors[op.in[i]];
-      if (!w.is_weight() || (w.dtype != DType::Q8 && w.dtype != DType::Q4)) return false;
-      if (w.dtype == DType::Q4 && w.cols % 32) return false;
-    }
-    return true;
+  }
+
+  void prepare(const Graph& g, const std::vector<Partition>& parts) {  // overrides where Backend declares it
+    const size_t nt = g.tensors.size();
+    on_dev_.assign(nt, 0);
+    host_needed_.assign(nt, 0);
+    for (const Partition& p : parts)
+      for (int i = p.begin; i < p.end; ++i) {
+        const Op& op = g.ops[i];
+        if (p.backend == this) {
+          for (int t : op.out) on_dev_[t] = 1;
+        } else {
+          for (int t : op.in) host_needed_[t] = 1;
+        }
+      }
+    if (g.output >= 0) host_needed_[g.output] = 1;
+    act_.assign(nt, Buf{});
+    first_op_ = -1;
+    for (const Partition& p : parts)
+      if (p.backend == this && (first_op_ < 0 || p.begin < first_op_)) first_op_ = p.begin;
+    prepared_ = true;
   }
 
   void run(const Op& op, ExecContext& c) override {
     if (!ctx_) throw std::runtime_error("edgelm: hip backend created for planning only");
-    const int T = static_cast<int>(c.rows(op.in[0]));
-    const int64_t K = c.tensor(op.in[1]).cols;
-    const int act = c.act_quant ? ELMH_ACT_INT8 : ELMH_ACT_F32;
-    int rc = ELMH_OK;
-    if (op.type == OpType::FFN_SWIGLU) {
-      rc = elmh_swiglu(ctx_, c.f(op.in[0]), T, K, weight(c.tensor(op.in[1])), weight(c.tensor(op.in[2])),
-                       c.f(op.out[0]), act, ELMH_EXACT);
-    } else {
-      const size_t n = op.type == OpType::MATMUL_N ? op.out.size() : 1;
-      w_.resize(n);
-      y_.resize(n);
-      r_.assign(n, nullptr);
-      for (size_t i = 0; i < n; ++i) {
-        w_[i] = weight(c.tensor(op.in[1 + i]));
-        y_[i] = c.f(op.out[i]);
+    if (!prepared_) unprepared(*c.graph);
+    if (&op - c.graph->ops.data() == first_op_) ++epoch_;  // a new forward
+    switch (op.type) {
+      case OpType::FFN_SWIGLU: {
+        const int T = static_cast<int>(c.rows(op.in[0]));
+        const int64_t K = c.tensor(op.in[1]).cols;
+        check(elmh_swiglu_dev(ctx_, in(op.in[0], c), T, K, weight(c.tensor(op.in[1])), weight(c.tensor(op.in[2])),
+                              out(op.out[0], c), act(c), ELMH_EXACT),
+              op);
+        break;
       }
-      if (op.type == OpType::MATMUL_ADD) r_[0] = c.f(op.in[2]);
-      rc = elmh_matmul(ctx_, c.f(op.in[0]), T, K, static_cast<int>(n), w_.data(), y_.data(),
-                       op.type == OpType::MATMUL_ADD ? r_.data() : nullptr, act, ELMH_EXACT);
+      case OpType::MATMUL:
+      case OpType::MATMUL_N:
+      case OpType::MATMUL_ADD: {
+        const int T = static_cast<int>(c.rows(op.in[0]));
+        const int64_t K = c.tensor(op.in[1]).cols;
+        const size_t n = op.type == OpType::MATMUL_N ? op.out.size() : 1;
+        w_.resize(n);
+        y_.resize(n);
+        r_.assign(n, nullptr);
+        const float* x = in(op.in[0], c);
+        for (size_t i = 0; i < n; ++i) {
+          w_[i] = weight(c.tensor(op.in[1 + i]));
+          y_[i] = out(op.out[i], c);
+        }
+        if (op.type == OpType::MATMUL_ADD) r_[0] = in(op.in[2], c);
+        check(elmh_matmul_dev(ctx_, x, T, K, static_cast<int>(n), w_.data(), y_.data(),
+                              op.type == OpType::MATMUL_ADD ? r_.data() : nullptr, act(c), ELMH_EXACT),
+              op);
+        break;
+      }
+      case OpType::EMBED: {
+        const Tensor& table = c.tensor(op.in[1]);
+        const int32_t* tok = reinterpret_cast<const int32_t*>(c.f(op.in[0]));
+        for (int t = 0; t < c.T; ++t)
+          EDGELM_CHECK(tok[t] >= 0 && tok[t] < table.rows, "token id out of range");
+        check(elmh_embed_dev(ctx_, reinterpret_cast<const int32_t*>(in(op.in[0], c)), c.T, weight(table),
+                             out(op.out[0], c)),
+              op);
+        break;
+      }
+      case OpType::RMSNORM: {
+        const int rows = static_cast<int>(c.rows(op.in[0])), dim = static_cast<int>(c.tensor(op.in[0]).cols);
+        check(elmh_rmsnorm_dev(ctx_, in(op.in[0], c), f32_weight(c.tensor(op.in[1])), out(op.out[0], c), rows, dim,
+                               op.fattr[0]),
+              op);
+        break;
+      }
+      case OpType::ATTENTION: attention(op, c); break;
+      case OpType::LAST_ROWS: {
+        const int64_t cols = c.tensor(op.in[0]).cols, skip = c.rows(op.in[0]) - c.rows(op.out[0]);
+        EDGELM_CHECK(skip >= 0, "LAST_ROWS: L > T");
+        const float* src = in(op.in[0], c) + skip * cols;
+        check(elmh_memcpy_d2d(ctx_, out(op.out[0], c), src, bytes(op.out[0], c)), op);
+        break;
+      }
+      default: throw std::runtime_error(std::string("edgelm: hip: unsupported op ") + op_name(op.type));
     }
-    if (rc != ELMH_OK) throw std::runtime_error(std::string("edgelm: hip ") + op_name(op.type) + ": " + elmh_last_error(ctx_));
+    for (int t : op.out)
+      if (host_needed_[t]) check(elmh_memcpy_d2h(ctx_, c.f(t), act_[t].p, bytes(t, c)), op);
+    if (!prepared_) ++epoch_;  // no residency: every op uploads its inputs afresh
   }
 
  private:
+  struct Buf {
+    void* p = nullptr;
+    size_t cap = 0;
+    uint64_t epoch = 0;  // forward in which a host-produced tensor was last uploaded
+  };
+  struct Layer {
+    float* k = nullptr;
+    float* v = nullptr;
+  };
+
+  // no prepare() call (an edgelm Session without the hook): nothing is known to be on the device
+  // and the host may read every output
+  void unprepared(const Graph& g) {
+    if (act_.size() == g.tensors.size()) return;
+    on_dev_.assign(g.tensors.size(), 0);
+    host_needed_.assign(g.tensors.size(), 1);
+    act_.assign(g.tensors.size(), Buf{});
+    first_op_ = -1;
+  }
+
+  static bool quantized(const Tensor& w) {
+    return w.is_weight() && (w.dtype == DType::Q8 || (w.dtype == DType::Q4 && w.cols % 32 == 0));
+  }
+  int act(const ExecContext& c) const { return c.act_quant ? ELMH_ACT_INT8 : ELMH_ACT_F32; }
+  void check(int rc, const Op& op) const {
+    if (rc != ELMH_OK) throw std::runtime_error(std::string("edgelm: hip ") + op_name(op.type) + ": " + elmh_last_error(ctx_));
+  }
+  size_t bytes(int t, const ExecContext& c) const {
+    return static_cast<size_t>(c.rows(t) * c.tensor(t).cols) * sizeof(float);
+  }
+  void* alloc(size_t n) {
+    void* p = nullptr;
+    if (elmh_malloc(ctx_, n, &p) != ELMH_OK) throw std::runtime_error(std::string("edgelm: hip: ") + elmh_last_error(ctx_));
+    return p;
+  }
+  // device buffer of activation t, large enough for this forward's rows
+  float* buffer(int t, const ExecContext& c) {
+    Buf& b = act_[t];
+    const size_t n = bytes(t, c);
+    if (b.cap < n) {
+      if (b.p) elmh_free(ctx_, b.p);
+      b.p = alloc(n);
+      b.cap = n;
+      b.epoch = 0;
+    }
+    return static_cast<float*>(b.p);
+  }
+  float* out(int t, const ExecContext& c) { return buffer(t, c); }
+  // an input on the device: produced there by an earlier hip op, or uploaded from the host arena
+  // (once per forward)
+  const float* in(int t, const ExecContext& c) {
+    float* p = buffer(t, c);
+    if (!on_dev_[t] && act_[t].epoch != epoch_) {
+      if (elmh_memcpy_h2d(ctx_, p, c.f(t), bytes(t, c)) != ELMH_OK)
+        throw std::runtime_error(std::string("edgelm: hip upload of ") + c.tensor(t).name + ": " + elmh_last_error(ctx_));
+      act_[t].epoch = epoch_;
+    }
+    return p;
+  }
+
   elmh_weight* weight(const Tensor& t) {
     auto it = weights_.find(&t);
     if (it != weights_.end()) return it->second;
@@ -80,9 +233,67 @@ class HipBackend : public Backend {
     weights_.emplace(&t, w);
     return w;
   }
+  const float* f32_weight(const Tensor& t) {
+    auto it = f32w_.find(&t);
+    if (it != f32w_.end()) return static_cast<const float*>(it->second);
+    const size_t n = static_cast<size_t>(t.rows * t.cols) * sizeof(float);
+    void* p = alloc(n);
+    if (elmh_memcpy_h2d(ctx_, p, t.data, n) != ELMH_OK)
+      throw std::runtime_error(std::string("edgelm: hip upload of ") + t.name + ": " + elmh_last_error(ctx_));
+    f32w_.emplace(&t, p);
+    return static_cast<const float*>(p);
+  }
 
+  // cpu::attention's arguments (backends.cpp attn_args) with the cache and the rope table in HBM
+  void attention(const Op& op, ExecContext& c) {
+    const int layer = op.iattr[0], nh = op.iattr[1], nkv = op.iattr[2];
+    EDGELM_CHECK(layer >= 0 && layer < static_cast<int>(c.kv.size()), "attention: bad layer");
+    const int T = static_cast<int>(c.rows(op.in[0]));
+    const int hd = static_cast<int>(c.tensor(op.in[0]).cols) / nh;
+    const int mc = c.kv[layer].max_ctx;
+    if (kv_.size() < c.kv.size()) kv_.resize(c.kv.size());
+    Layer& l = kv_[layer];
+    if (!l.k) {
+      const size_t n = static_cast<size_t>(nkv) * mc * hd * sizeof(float);
+      l.k = static_cast<float*>(alloc(n));
+      l.v = static_cast<float*>(alloc(n));
+      check(elmh_memset_dev(ctx_, l.k, 0, n), op);
+      check(elmh_memset_dev(ctx_, l.v, 0, n), op);
+    }
+    const float *rc = nullptr, *rs = nullptr;
+    if (op.iattr[3]) {
+      EDGELM_CHECK(c.rope && c.rope->half * 2 == hd, "attention: rope table does not match head_dim");
+      if (!rope_cos_) {
+        const size_t n = c.rope->cos.size() * sizeof(float);
+        rope_cos_ = static_cast<float*>(alloc(n));
+        rope_sin_ = static_cast<float*>(alloc(n));
+        check(elmh_memcpy_h2d(ctx_, rope_cos_, c.rope->cos.data(), n), op);
+        check(elmh_memcpy_h2d(ctx_, rope_sin_, c.rope->sin.data(), n), op);
+        rope_pos_ = c.rope->max_pos;
+      }
+      EDGELM_CHECK(c.pos0 + T <= rope_pos_, "position beyond rope table");
+      rc = rope_cos_;
+      rs = rope_sin_;
+    }
+    const float* q = in(op.in[0], c);
+    const float* k = in(op.in[1], c);
+    const float* v = in(op.in[2], c);
+    check(elmh_attention_dev(ctx_, q, k, v, out(op.out[0], c), T, c.pos0, nh, nkv, hd, l.k, l.v, mc, rc, rs), op);
+  }
+
+  bool layer_ops_;
   elmh_ctx* ctx_ = nullptr;
+  bool prepared_ = false;
+  int first_op_ = -1;
+  uint64_t epoch_ = 0;
+  std::vector<char> on_dev_, host_needed_;
+  std::vector<Buf> act_;
+  std::vector<Layer> kv_;
+  float* rope_cos_ = nullptr;
+  float* rope_sin_ = nullptr;
+  int rope_pos_ = 0;
   std::unordered_map<const Tensor*, elmh_weight*> weights_;
+  std::unordered_map<const Tensor*, void*> f32w_;
   std::vector<elmh_weight*> w_;
   std::vector<float*> y_;
   std::vector<const float*> r_;
@@ -90,7 +301,8 @@ class HipBackend : public Backend {
 
 }  // namespace
 
-std::unique_ptr<Backend> make_hip_backend(int device) { return std::make_unique<HipBackend>(device); }
-std::unique_ptr<Backend> make_hip_planning_backend() { return std::make_unique<HipBackend>(-1); }
+std::unique_ptr<Backend> make_hip_backend(int device) { return std::make_unique<HipBackend>(device, true); }
+std::unique_ptr<Backend> make_hip_matmul_backend(int device) { return std::make_unique<HipBackend>(device, false); }
+std::unique_ptr<Backend> make_hip_planning_backend(bool layer_ops) { return std::make_unique<HipBackend>(-1, layer_ops); }
 
 }  // namespace edgelm

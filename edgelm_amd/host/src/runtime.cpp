@@ -22,6 +22,7 @@ Session::Session(const Model& model, SessionOptions opt) : model_(model), opt_(s
   std::vector<Backend*> pref;
   for (auto& b : backends_) pref.push_back(b.get());
   parts_ = partition_graph(graph_, pref);
+  for (auto& b : backends_) b->prepare(graph_, parts_);
 
   const int L = opt_.all_logits ? opt_.max_batch : 1;
   plan_ = plan_memory(graph_, opt_.max_batch, L);

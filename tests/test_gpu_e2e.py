@@ -1,8 +1,10 @@
-"""GPU end to end: sessions of this build's runtime with the `hip` delegate (backends "hip,cpu")
-against edgelm's own Session (compiled from the reference sources into oracle/_ref) on the same .elm
-files. The MATMUL family runs on the GPU, the other ops on the host; logits must be bit-identical to
-edgelm's cpu backend (x86 scalar path), close to its reference backend (2e-5 with f32 activations,
-test_e2e.cpp:33-75), and greedy tokens must agree on the SmolLM2-135M-shaped random model.
+"""GPU end to end: sessions of this build's runtime with the `hip` delegate against edgelm's own
+Session (compiled from the reference sources into oracle/_ref) on the same .elm files. Backends
+"hip,cpu" run the whole quantized model on the GPU (activations and KV cache resident in HBM);
+"hip-matmul,cpu" run the MATMUL family on the GPU and the other ops on the host. Logits must be
+bit-identical to edgelm's cpu backend (x86 scalar path), close to its reference backend (2e-5 with
+f32 activations, test_e2e.cpp:33-75), and greedy tokens must agree on the SmolLM2-135M-shaped
+random model.
 """
 import numpy as np
 import pytest
@@ -37,16 +39,17 @@ def run_all(sess, ids, prefill, batch):
     return np.concatenate(out)
 
 
+@pytest.mark.parametrize("backends", ["hip,cpu", "hip-matmul,cpu"])
 @pytest.mark.parametrize("dt", ["q8", "q4"])
 @pytest.mark.parametrize("act", [False, True])
-def test_tiny_logits_bit_identical_to_edgelm(tiny, dt, act):
+def test_tiny_logits_bit_identical_to_edgelm(tiny, dt, act, backends):
     ids = np.random.default_rng(5).integers(0, 320, 40).astype(np.int32)
     m = host.Model(tiny[dt])
     variants = [("full prefill", 128, 40, 4), ("chunked prefill (7)", 7, 40, 2), ("prefill 5 + decode", 128, 5, 3),
                 ("decode only", 128, 0, 1)]
     for name, batch, prefill, threads in variants:
-        print(f"[gpu] e2e tiny {dt} act_int8={act} {name}", flush=True)
-        mine = host.Session(m, "hip,cpu", threads=threads, max_ctx=64, max_batch=batch, all_logits=True,
+        print(f"[gpu] e2e tiny {backends} {dt} act_int8={act} {name}", flush=True)
+        mine = host.Session(m, backends, threads=threads, max_ctx=64, max_batch=batch, all_logits=True,
                             act_quant=act)
         ref = O.RefSession(tiny[dt], "cpu", threads=threads, max_ctx=64, max_batch=batch, all_logits=True,
                            act_quant=act)

@@ -59,13 +59,17 @@ def test_reference_loader_reads_our_files(tiny):
         r.close()
 
 
-def test_partitioner_hip_claims_exactly_the_quantized_matmuls(tiny):
+def test_partitioner_hip_claims(tiny):
     for dt in ("q8", "q4"):
         m = host.Model(tiny[dt])
-        n, desc = m.partition("hip,cpu")
-        assert "hip 9 ops" in desc and "cpu 7 ops" in desc and "reference 2 ops" in desc  # per layer 4 + lm_head
-        n2, desc2 = m.partition("hip")  # no cpu: the reference backend takes the rest
-        assert "hip 9 ops" in desc2 and "reference 9 ops" in desc2
+        # hip-matmul: exactly the quantized matmuls (per layer 4, plus the LM head)
+        n, desc = m.partition("hip-matmul,cpu")
+        assert "hip-matmul 9 ops" in desc and "cpu 7 ops" in desc and "reference 2 ops" in desc
+        n2, desc2 = m.partition("hip-matmul")  # no cpu: the reference backend takes the rest
+        assert "hip-matmul 9 ops" in desc2 and "reference 9 ops" in desc2
+        # hip: the whole quantized model (EMBED, RMSNORM, ATTENTION, LAST_ROWS too) in one partition
+        n3, desc3 = m.partition("hip,cpu")
+        assert n3 == 1 and "hip 18 ops in 1" in desc3
     # f32 weights: not claimed, and no host backend of this build runs a matmul -> loud failure
     m = host.Model(tiny["f32"])
     with pytest.raises(RuntimeError, match="no backend supports"):
