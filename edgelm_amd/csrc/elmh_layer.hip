@@ -61,11 +61,13 @@ __device__ __forceinline__ float dot4(const float* __restrict__ a, const float* 
 }
 
 // Step 1 of cpu::attention: this step's keys (rotated when cos/sin are given) and values go to the
-// cache [kv_head][pos][hd]. One workgroup per (token, kv head).
+// cache [kv_head][pos][hd]. One workgroup per (token, kv head). pos_dev (if not null) holds pos0 in
+// device memory, so that a captured decode step replays at any position.
 __global__ __launch_bounds__(64) void kv_append_kernel(const float* __restrict__ k, const float* __restrict__ v,
                                                        float* __restrict__ kc, float* __restrict__ vc, int pos0,
-                                                       int n_kv, int hd, int max_ctx, const float* __restrict__ rcos,
-                                                       const float* __restrict__ rsin) {
+                                                       const int* __restrict__ pos_dev, int n_kv, int hd, int max_ctx,
+                                                       const float* __restrict__ rcos, const float* __restrict__ rsin) {
+  if (pos_dev) pos0 = *pos_dev;
   const int t = blockIdx.x / n_kv, h = blockIdx.x - t * n_kv, pos = pos0 + t, h2 = hd / 2;
   const float* ks = k + ((int64_t)t * n_kv + h) * hd;
   const float* vs = v + ((int64_t)t * n_kv + h) * hd;
@@ -84,61 +86,206 @@ __global__ __launch_bounds__(64) void kv_append_kernel(const float* __restrict__
   for (int i = threadIdx.x; i < hd; i += 64) vd[i] = vs[i];
 }
 
-// Step 2 of cpu::attention: one wave per (query token t, head h) over positions 0 .. pos0 + t.
-//   q rotated into LDS; sc[j] = dot_f32(q, k_j) * scale in parallel over j; mx = max sc;
-//   e_j = expf(sc[j] - mx); sum = e_0 + e_1 + ... in order (one lane); inv = 1 / sum;
-//   lane i: o_i = 0, then o_i += (e_j * inv) * v_j[i] in increasing j.
-// LDS: hd floats of q, then pos0 + T floats of scores.
-__global__ __launch_bounds__(64) void attention_kernel(const float* __restrict__ q, float* __restrict__ out,
-                                                       const float* __restrict__ kc, const float* __restrict__ vc,
-                                                       int pos0, int n_heads, int n_kv, int hd, int max_ctx,
-                                                       const float* __restrict__ rcos, const float* __restrict__ rsin) {
+// Step 2 of cpu::attention: one 256-thread workgroup per (query token t, head h) over positions
+// 0 .. pos0 + t, every float operation in cpu::attention's order:
+//   q rotated into LDS; thread j computes sc[j] = dot_f32(q, k_j) * scale (its key row's loads all
+//   in flight at once); mx = max sc; e_j = expf(sc[j] - mx); thread 0 sums e_0 + e_1 + ... in
+//   order, inv = 1 / sum; every thread forms p_j = e_j * inv; then lane i of wave 0 runs
+//   o_i = 0, o_i += p_j * v_j[i] in increasing j.
+// The values go through LDS transposed, [dim][position] with a row stride of 4 (mod 8) floats, so
+// that lane i reads four positions of its dim with one conflict-free 16-byte read; they move in
+// chunks of whole positions (a multiple of 4), kAttnVF float4 per thread: the first chunk's loads
+// are issued at the start, after q's, and chunk c + 1 is loaded into registers while wave 0
+// accumulates chunk c.
+// LDS (dynamic): q [hd], scores [n_cap], one transposed value chunk [hd][stride].
+constexpr int kAttnThreads = 256;
+constexpr int kAttnVF = 12;                           // float4 of values per thread per chunk
+constexpr int kAttnChunkF4 = kAttnThreads * kAttnVF;  // 48 KB: 192 positions of head size 64
+
+__device__ __forceinline__ int attn_chunk_pos(int hd) { return (kAttnChunkF4 / (hd / 4)) & ~3; }
+__device__ __host__ __forceinline__ int attn_stride(int cpos) {
+  const int s = (cpos + 3) & ~3;
+  return (s / 4) % 2 ? s : s + 4;
+}
+
+__device__ __forceinline__ float dot_row(const float* __restrict__ q, const float* __restrict__ k, int hd) {
+  if (hd == 64) {  // the common head size: all 16 loads issued before the first product
+    float4 kv[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) kv[u] = reinterpret_cast<const float4*>(k)[u];
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      s0 = s0 + q[4 * u] * kv[u].x;
+      s1 = s1 + q[4 * u + 1] * kv[u].y;
+      s2 = s2 + q[4 * u + 2] * kv[u].z;
+      s3 = s3 + q[4 * u + 3] * kv[u].w;
+    }
+    return (s0 + s1) + (s2 + s3);
+  }
+  return dot4(q, k, hd);
+}
+
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ q, float* __restrict__ out,
+                                                                 const float* __restrict__ kc,
+                                                                 const float* __restrict__ vc, int pos0,
+                                                                 const int* __restrict__ pos_dev, int n_heads, int n_kv,
+                                                                 int hd, int max_ctx, int n_cap,
+                                                                 const float* __restrict__ rcos,
+                                                                 const float* __restrict__ rsin) {
   extern __shared__ float lds[];
+  if (pos_dev) pos0 = *pos_dev;
+  const int hdp = (hd + 3) & ~3;
   float* qb = lds;
-  float* sc = lds + ((hd + 3) & ~3);
+  float* sc = lds + hdp;
+  float* vt = sc + ((n_cap + 3) & ~3);
+  __shared__ float red[kAttnThreads / 64];
   __shared__ float inv_s;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int t = blockIdx.x / n_heads, h = blockIdx.x - t * n_heads, pos = pos0 + t, h2 = hd / 2, n = pos + 1;
   const int qd = n_heads * hd, grp = n_heads / n_kv;
+  // q first: the rotation needs it before anything else
   const float* qs = q + (int64_t)t * qd + h * hd;
+  float qa = 0.f, qb2 = 0.f, cr = 0.f, sr = 0.f;
+  const int iq = tid < hd ? tid : 0;
   if (rcos) {
-    const float* c = rcos + (int64_t)pos * h2;
-    const float* s = rsin + (int64_t)pos * h2;
-    for (int i = lane; i < h2; i += 64) {
-      qb[i] = qs[i] * c[i] - qs[i + h2] * s[i];
-      qb[i + h2] = qs[i + h2] * c[i] + qs[i] * s[i];
-    }
+    const int ih = tid < h2 ? tid : 0;
+    qa = qs[ih];
+    qb2 = qs[ih + h2];
+    cr = rcos[(int64_t)pos * h2 + ih];
+    sr = rsin[(int64_t)pos * h2 + ih];
   } else {
-    for (int i = lane; i < hd; i += 64) qb[i] = qs[i];
+    qa = qs[iq];
+  }
+  const float* kh = kc + (int64_t)(h / grp) * max_ctx * hd;
+  const float4* vh4 = reinterpret_cast<const float4*>(vc + (int64_t)(h / grp) * max_ctx * hd);
+  const int hd4 = hd / 4, cpos = attn_chunk_pos(hd), cf4 = cpos * hd4, vstride = attn_stride(cpos);
+  const int total4 = n * hd4;  // the values to read, as float4 (hd % 4 == 0)
+  // head size 64: this thread's first key row in flight from the start
+  float4 kr[16];
+  if (hd == 64) {
+    const float4* k4 = reinterpret_cast<const float4*>(kh + (int64_t)min(tid, n - 1) * hd);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) kr[u] = k4[u];
+  }
+  // chunk 0 of the values, also in flight from the start
+  float4 vr[kAttnVF];
+#pragma unroll
+  for (int u = 0; u < kAttnVF; ++u) {
+    const int f = tid + u * kAttnThreads;
+    vr[u] = f < min(total4, cf4) ? vh4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (rcos) {
+    if (tid < h2) {
+      qb[tid] = qa * cr - qb2 * sr;
+      qb[tid + h2] = qb2 * cr + qa * sr;
+    }
+  } else if (tid < hd) {
+    qb[tid] = qa;
   }
   __syncthreads();
-  const float* kh = kc + (int64_t)(h / grp) * max_ctx * hd;
-  const float* vh = vc + (int64_t)(h / grp) * max_ctx * hd;
   const float scale = 1.0f / sqrtf((float)hd);
   float mx = -INFINITY;
-  for (int j = lane; j < n; j += 64) {
-    const float s = dot4(qb, kh + (int64_t)j * hd, hd) * scale;
-    sc[j] = s;
-    mx = fmaxf(mx, s);
+  for (int j = tid; j < n; j += kAttnThreads) {
+    float d;
+    if (hd == 64 && j == tid) {  // the preloaded row: dot_f32_scalar's order
+      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        s0 = s0 + qb[4 * u] * kr[u].x;
+        s1 = s1 + qb[4 * u + 1] * kr[u].y;
+        s2 = s2 + qb[4 * u + 2] * kr[u].z;
+        s3 = s3 + qb[4 * u + 3] * kr[u].w;
+      }
+      d = (s0 + s1) + (s2 + s3);
+    } else {
+      d = dot_row(qb, kh + (int64_t)j * hd, hd);
+    }
+    const float sj = d * scale;
+    sc[j] = sj;
+    mx = fmaxf(mx, sj);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  for (int j = lane; j < n; j += 64) sc[j] = elm_expf(sc[j] - mx);
+  if (lane == 0) red[wave] = mx;
   __syncthreads();
-  if (lane == 0) {
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  for (int j = tid; j < n; j += kAttnThreads) sc[j] = elm_expf(sc[j] - mx);
+  __syncthreads();
+  if (tid == 0) {  // e_0 + e_1 + ... in order, read 16 bytes at a time
     float sum = 0.f;
+    const float4* s4 = reinterpret_cast<const float4*>(sc);
+    int j = 0;
 #pragma unroll 8
-    for (int j = 0; j < n; ++j) sum = sum + sc[j];
+    for (; j + 4 <= n; j += 4) {
+      const float4 e = s4[j >> 2];
+      sum = sum + e.x;
+      sum = sum + e.y;
+      sum = sum + e.z;
+      sum = sum + e.w;
+    }
+    for (; j < n; ++j) sum = sum + sc[j];
     inv_s = 1.0f / sum;
   }
   __syncthreads();
-  const float inv = inv_s;
-  float* o = out + (int64_t)t * qd + h * hd;
-  for (int i = lane; i < hd; i += 64) {
-    float acc = 0.f;
+  {
+    const float inv = inv_s;
+    for (int j = tid; j < n; j += kAttnThreads) sc[j] = sc[j] * inv;  // p_j
+  }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // wave 0: outputs lane, lane + 64, ... (hd <= 256)
+  for (int f0 = 0; f0 < total4; f0 += cf4) {
+    // transpose this thread's float4 (position j, dims 4 d .. 4 d + 3) into vt[dim][j - j0]
+#pragma unroll
+    for (int u = 0; u < kAttnVF; ++u) {
+      const int rel = tid + u * kAttnThreads;
+      if (rel < cf4) {
+        const int jj = rel / hd4, d4 = (rel - jj * hd4) * 4;
+        vt[(d4 + 0) * vstride + jj] = vr[u].x;
+        vt[(d4 + 1) * vstride + jj] = vr[u].y;
+        vt[(d4 + 2) * vstride + jj] = vr[u].z;
+        vt[(d4 + 3) * vstride + jj] = vr[u].w;
+      }
+    }
+    __syncthreads();  // the chunk (and, the first time, every p_j) is in LDS
+    const int fn = f0 + cf4;
+    if (fn < total4) {
+#pragma unroll
+      for (int u = 0; u < kAttnVF; ++u) {
+        const int rel = tid + u * kAttnThreads;
+        vr[u] = rel < cf4 && fn + rel < total4 ? vh4[fn + rel] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    if (wave == 0) {
+      const int j0 = f0 / hd4, m = min(cpos, n - j0);
+      const float4* p4 = reinterpret_cast<const float4*>(sc + j0);  // j0 is a multiple of 4
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = lane + 64 * r;
+        if (i < hd) {
+          const float* vrow = vt + i * vstride;
+          const float4* v4 = reinterpret_cast<const float4*>(vrow);
+          float a = acc[r];
+          int jj = 0;
 #pragma unroll 4
-    for (int j = 0; j < n; ++j) acc = acc + (sc[j] * inv) * vh[(int64_t)j * hd + i];
-    o[i] = acc;
+          for (; jj + 4 <= m; jj += 4) {
+            const float4 pv = p4[jj >> 2], vv = v4[jj >> 2];
+            a = a + pv.x * vv.x;
+            a = a + pv.y * vv.y;
+            a = a + pv.z * vv.z;
+            a = a + pv.w * vv.w;
+          }
+          for (; jj < m; ++jj) a = a + sc[j0 + jj] * vrow[jj];
+          acc[r] = a;
+        }
+      }
+    }
+    __syncthreads();  // wave 0 is done with the chunk before it is overwritten
+  }
+  float* o = out + (int64_t)t * qd + h * hd;
+  if (wave == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (lane + 64 * r < hd) o[lane + 64 * r] = acc[r];
   }
 }
 
@@ -200,16 +347,21 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, in
   return hipGetLastError();
 }
 
-size_t attention_lds_bytes(int hd, int n_max) { return ((size_t)((hd + 3) & ~3) + (size_t)n_max) * sizeof(float); }
+size_t attention_lds_bytes(int hd, int n_max) {
+  const int cpos = (kAttnChunkF4 / (hd / 4)) & ~3;
+  return ((size_t)((hd + 3) & ~3) + (size_t)((n_max + 3) & ~3) + (size_t)hd * attn_stride(cpos)) * sizeof(float);
+}
 
-hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0, int n_heads,
-                            int n_kv, int hd, float* kc, float* vc, int max_ctx, const float* rcos, const float* rsin,
-                            hipStream_t s) {
-  kv_append_kernel<<<T * n_kv, 64, 0, s>>>(k, v, kc, vc, pos0, n_kv, hd, max_ctx, rcos, rsin);
+hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
+                            const int* pos_dev, int n_heads, int n_kv, int hd, float* kc, float* vc, int max_ctx,
+                            const float* rcos, const float* rsin, hipStream_t s) {
+  // with the position in device memory the score buffer covers the whole cache
+  const int n_cap = pos_dev ? max_ctx : pos0 + T;  // score slots
+  kv_append_kernel<<<T * n_kv, 64, 0, s>>>(k, v, kc, vc, pos0, pos_dev, n_kv, hd, max_ctx, rcos, rsin);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  attention_kernel<<<T * n_heads, 64, attention_lds_bytes(hd, pos0 + T), s>>>(q, out, kc, vc, pos0, n_heads, n_kv, hd,
-                                                                              max_ctx, rcos, rsin);
+  attention_kernel<<<T * n_heads, kAttnThreads, attention_lds_bytes(hd, n_cap), s>>>(
+      q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin);
   return hipGetLastError();
 }
 

@@ -59,6 +59,10 @@ class Backend {
   // backend keep activations on its device between its own consecutive ops and copy to the host
   // arena only what other backends read. Source-compatible with edgelm's Backend.
   virtual void prepare(const Graph&, const std::vector<Partition>&) {}
+  // Optional (default: false = not handled): run the whole partition at once (a device backend may
+  // replay it as a captured graph). Returning true means every op of the partition ran and the
+  // host arena holds what other backends read, as after run().
+  virtual bool run_partition(const Partition&, ExecContext&) { return false; }
 };
 
 std::unique_ptr<Backend> make_reference_backend();

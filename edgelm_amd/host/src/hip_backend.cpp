@@ -13,7 +13,16 @@
 // inside an unmodified edgelm Session, run() uploads every input and copies every output back.
 // Either way the host has what it needs when run() returns (edgelm's contract: runtime.cpp:66-76).
 // Weights are uploaded to HBM once, on first use (matmul weights repacked; RMSNORM weights f32).
+//
+// run_partition() (the other optional hook) replays a decode step (T = 1) of a whole partition as
+// one HIP graph: the first such step runs op by op (allocating buffers and uploading weights), the
+// second is captured, with attention reading the position from device memory; every later step
+// uploads the host-side inputs (token ids) and the position, launches the graph, and copies back
+// what the host reads (the logits). A buffer that has to grow (a longer prefill) drops the graphs.
+// EDGELM_HIP_GRAPHS=0 turns graphs off.
+#include <cstdlib>
 #include <cstring>
+#include <map>
 #include <unordered_map>
 
 #include "edgelm/backend.hpp"
@@ -31,12 +40,16 @@ class HipBackend : public Backend {
   // device < 0: planning only (supports() answers, run() throws) — for partition inspection on a
   // host without a GPU.
   HipBackend(int device, bool layer_ops) : layer_ops_(layer_ops) {
+    const char* g = std::getenv("EDGELM_HIP_GRAPHS");
+    graphs_on_ = !(g && g[0] == '0');
     if (device < 0) return;
     if (elmh_create(device, &ctx_) != ELMH_OK)
       throw std::runtime_error(std::string("edgelm: hip backend unavailable: ") + elmh_last_error(nullptr));
   }
   ~HipBackend() override {
     if (!ctx_) return;
+    drop_graphs();
+    elmh_free(ctx_, pos_dev_);
     for (auto& kv : weights_) elmh_free_weight(ctx_, kv.second);
     for (auto& kv : f32w_) elmh_free(ctx_, kv.second);
     for (Buf& b : act_) elmh_free(ctx_, b.p);
@@ -70,7 +83,7 @@ class HipBackend : public Backend {
         const int nh = op.iattr[1], nkv = op.iattr[2];
         if (nh < 1 || nkv < 1 || nh % nkv) return false;
         const int64_t hd = g.tensors[op.in[0]].cols / nh;
-        return hd >= 4 && hd % 4 == 0 && hd <= 512;
+        return hd >= 4 && hd % 4 == 0 && hd <= 256;
       }
       case OpType::LAST_ROWS: return true;
       default: return false;
@@ -96,6 +109,47 @@ class HipBackend : public Backend {
     for (const Partition& p : parts)
       if (p.backend == this && (first_op_ < 0 || p.begin < first_op_)) first_op_ = p.begin;
     prepared_ = true;
+  }
+
+  // overrides where Backend declares it; false: the Session runs the partition op by op
+  bool run_partition(const Partition& p, ExecContext& c) {
+    if (!graphs_on_ || !ctx_ || !prepared_ || c.T != 1 || c.L != 1) return false;
+    const Graph& g = *c.graph;
+    StepGraph& sg = graphs_[p.begin];
+    if (!sg.exec && sg.warm == 0) {  // warm-up: allocations and uploads happen op by op
+      for (int i = p.begin; i < p.end; ++i) run(g.ops[i], c);
+      sg.warm = 1;
+      return true;
+    }
+    step_checks(p, c);
+    upload_step_inputs(p, c);
+    if (!sg.exec) {
+      capturing_ = true;
+      const uint64_t gen = buffer_gen_;
+      int rc = elmh_graph_begin(ctx_);
+      if (rc == ELMH_OK) {
+        try {
+          for (int i = p.begin; i < p.end; ++i) run(g.ops[i], c);
+        } catch (...) {
+          void* dead = nullptr;
+          elmh_graph_end(ctx_, &dead);
+          if (dead) elmh_graph_destroy(ctx_, dead);
+          capturing_ = false;
+          throw;
+        }
+        rc = elmh_graph_end(ctx_, &sg.exec);
+      }
+      capturing_ = false;
+      if (rc != ELMH_OK) throw std::runtime_error(std::string("edgelm: hip graph capture: ") + elmh_last_error(ctx_));
+      if (gen != buffer_gen_) throw std::runtime_error("edgelm: hip graph capture: a buffer moved while capturing");
+    }
+    if (elmh_graph_launch(ctx_, sg.exec) != ELMH_OK)
+      throw std::runtime_error(std::string("edgelm: hip graph launch: ") + elmh_last_error(ctx_));
+    for (int i = p.begin; i < p.end; ++i)
+      for (int t : g.ops[i].out)
+        if (host_needed_[t] && elmh_memcpy_d2h(ctx_, c.f(t), act_[t].p, bytes(t, c)) != ELMH_OK)
+          throw std::runtime_error(std::string("edgelm: hip download: ") + elmh_last_error(ctx_));
+    return true;
   }
 
   void run(const Op& op, ExecContext& c) override {
@@ -158,6 +212,7 @@ class HipBackend : public Backend {
       }
       default: throw std::runtime_error(std::string("edgelm: hip: unsupported op ") + op_name(op.type));
     }
+    if (capturing_) return;  // the replay copies host-needed outputs after the launch
     for (int t : op.out)
       if (host_needed_[t]) check(elmh_memcpy_d2h(ctx_, c.f(t), act_[t].p, bytes(t, c)), op);
     if (!prepared_) ++epoch_;  // no residency: every op uploads its inputs afresh
@@ -173,6 +228,47 @@ class HipBackend : public Backend {
     float* k = nullptr;
     float* v = nullptr;
   };
+  struct StepGraph {
+    int warm = 0;
+    void* exec = nullptr;
+  };
+
+  void drop_graphs() {
+    for (auto& kv : graphs_)
+      if (kv.second.exec) elmh_graph_destroy(ctx_, kv.second.exec);
+    graphs_.clear();
+  }
+  // what run() checks on the host each time, for a replayed step: token ids and positions in range
+  void step_checks(const Partition& p, const ExecContext& c) const {
+    const Graph& g = *c.graph;
+    for (int i = p.begin; i < p.end; ++i) {
+      const Op& op = g.ops[i];
+      if (op.type == OpType::EMBED) {
+        const int32_t tok = *reinterpret_cast<const int32_t*>(c.f(op.in[0]));
+        EDGELM_CHECK(tok >= 0 && tok < c.tensor(op.in[1]).rows, "token id out of range");
+      } else if (op.type == OpType::ATTENTION) {
+        EDGELM_CHECK(c.pos0 + 1 <= c.kv[op.iattr[0]].max_ctx, "context overflow");
+        EDGELM_CHECK(!op.iattr[3] || c.pos0 + 1 <= rope_pos_, "position beyond rope table");
+      }
+    }
+  }
+  // a replayed step's inputs that come from the host (token ids; anything another backend made)
+  // and the position the graph's attention reads
+  void upload_step_inputs(const Partition& p, const ExecContext& c) {
+    const Graph& g = *c.graph;
+    for (int i = p.begin; i < p.end; ++i)
+      for (int t : g.ops[i].in)
+        if (!c.tensor(t).is_weight() && !on_dev_[t] &&
+            elmh_memcpy_h2d(ctx_, act_[t].p, c.f(t), bytes(t, c)) != ELMH_OK)
+          throw std::runtime_error(std::string("edgelm: hip upload: ") + elmh_last_error(ctx_));
+    bool attn = false;
+    for (int i = p.begin; i < p.end; ++i) attn = attn || g.ops[i].type == OpType::ATTENTION;
+    if (!attn) return;
+    if (!pos_dev_) pos_dev_ = static_cast<int32_t*>(alloc(sizeof(int32_t)));
+    const int32_t pos = c.pos0;
+    if (elmh_memcpy_h2d(ctx_, pos_dev_, &pos, sizeof pos) != ELMH_OK)
+      throw std::runtime_error(std::string("edgelm: hip upload: ") + elmh_last_error(ctx_));
+  }
 
   // no prepare() call (an edgelm Session without the hook): nothing is known to be on the device
   // and the host may read every output
@@ -204,7 +300,12 @@ class HipBackend : public Backend {
     Buf& b = act_[t];
     const size_t n = bytes(t, c);
     if (b.cap < n) {
-      if (b.p) elmh_free(ctx_, b.p);
+      if (capturing_) throw std::runtime_error("edgelm: hip: buffer growth during graph capture");
+      if (b.p) {
+        elmh_free(ctx_, b.p);
+        drop_graphs();  // captured graphs hold the old address
+        ++buffer_gen_;
+      }
       b.p = alloc(n);
       b.cap = n;
       b.epoch = 0;
@@ -216,7 +317,7 @@ class HipBackend : public Backend {
   // (once per forward)
   const float* in(int t, const ExecContext& c) {
     float* p = buffer(t, c);
-    if (!on_dev_[t] && act_[t].epoch != epoch_) {
+    if (!on_dev_[t] && !capturing_ && act_[t].epoch != epoch_) {
       if (elmh_memcpy_h2d(ctx_, p, c.f(t), bytes(t, c)) != ELMH_OK)
         throw std::runtime_error(std::string("edgelm: hip upload of ") + c.tensor(t).name + ": " + elmh_last_error(ctx_));
       act_[t].epoch = epoch_;
@@ -278,10 +379,18 @@ class HipBackend : public Backend {
     const float* q = in(op.in[0], c);
     const float* k = in(op.in[1], c);
     const float* v = in(op.in[2], c);
-    check(elmh_attention_dev(ctx_, q, k, v, out(op.out[0], c), T, c.pos0, nh, nkv, hd, l.k, l.v, mc, rc, rs), op);
+    if (capturing_)  // the replayed step reads its position from device memory
+      check(elmh_attention_step_dev(ctx_, q, k, v, out(op.out[0], c), pos_dev_, nh, nkv, hd, l.k, l.v, mc, rc, rs), op);
+    else
+      check(elmh_attention_dev(ctx_, q, k, v, out(op.out[0], c), T, c.pos0, nh, nkv, hd, l.k, l.v, mc, rc, rs), op);
   }
 
   bool layer_ops_;
+  bool graphs_on_ = true;
+  bool capturing_ = false;
+  uint64_t buffer_gen_ = 0;
+  std::map<int, StepGraph> graphs_;  // by the partition's first op
+  int32_t* pos_dev_ = nullptr;
   elmh_ctx* ctx_ = nullptr;
   bool prepared_ = false;
   int first_op_ = -1;

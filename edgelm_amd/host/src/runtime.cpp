@@ -55,7 +55,8 @@ const float* Session::forward(const int32_t* tokens, int n) {
   ctx_.pos0 = pos_;
   std::memcpy(ctx_.ptr[graph_.input], tokens, sizeof(int32_t) * static_cast<size_t>(n));
   for (const Partition& p : parts_)
-    for (int i = p.begin; i < p.end; ++i) p.backend->run(graph_.ops[i], ctx_);
+    if (!p.backend->run_partition(p, ctx_))
+      for (int i = p.begin; i < p.end; ++i) p.backend->run(graph_.ops[i], ctx_);
   pos_ += n;
   return ctx_.ptr[graph_.output];
 }

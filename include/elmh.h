@@ -126,6 +126,13 @@ int elmh_rmsnorm_dev(elmh_ctx* ctx, const float* x, const float* w, float* y, in
 int elmh_attention_dev(elmh_ctx* ctx, const float* q, const float* k, const float* v, float* out, int T, int pos0,
                        int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache, int max_ctx,
                        const float* rope_cos, const float* rope_sin);
+/* One decode token (T = 1) of elmh_attention_dev with its position pos0 read from device memory
+ * (*pos_dev, in [0, max_ctx)), so that a decode step captured in a HIP graph replays at every
+ * position. No counterpart in edgelm: it serves callers that replay graphs (this build's hip
+ * backend). The caller keeps *pos_dev within the cache and the rope table. */
+int elmh_attention_step_dev(elmh_ctx* ctx, const float* q, const float* k, const float* v, float* out,
+                            const int32_t* pos_dev, int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache,
+                            int max_ctx, const float* rope_cos, const float* rope_sin);
 
 /* ---- test hooks ----
  * quantize_act_row on the device (host pointers; q [T,K], d [T,K/32]). */

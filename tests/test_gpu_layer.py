@@ -33,11 +33,19 @@ def test_rmsnorm_bit_exact(ctx, dim):
             b.free()
 
 
-@pytest.mark.parametrize("shape", [(9, 3, 64, 160), (4, 4, 32, 48), (8, 1, 128, 40)])
+ATTN_SHAPES = [(9, 3, 64, 160, (17, 1, 1, 5, 1, 9)), (4, 4, 32, 48, (17, 1, 1, 5, 1, 9)),
+               (8, 1, 128, 40, (17, 1, 1, 5, 1, 9)),
+               # head_dim 20: value chunks of 204 whole positions; more positions than threads
+               (6, 2, 20, 320, (257, 1, 30, 1)),
+               # a long prefill: several value chunks and score rows per thread
+               (9, 3, 64, 420, (400, 1, 1))]
+
+
+@pytest.mark.parametrize("shape", ATTN_SHAPES, ids=[f"{s[0]}x{s[1]}x{s[2]}" for s in ATTN_SHAPES])
 @pytest.mark.parametrize("rope", [False, True])
 def test_attention_bit_exact(ctx, shape, rope):
     """A session's sequence of calls: prefill, decodes and a chunk, KV cache carried on the GPU."""
-    nh, nkv, hd, mc = shape
+    nh, nkv, hd, mc, steps = shape
     r = np.random.default_rng(nh * 100 + hd + int(rope))
     tab = O.rope_table(hd, mc, 100000.0) if rope else None
     kc = np.zeros((nkv, mc, hd), np.float32)
@@ -45,10 +53,10 @@ def test_attention_bit_exact(ctx, shape, rope):
     bkc, bvc = dev(ctx, kc), dev(ctx, vc)
     bcos, bsin = (dev(ctx, tab[0]), dev(ctx, tab[1])) if rope else (None, None)
     pos = 0
-    for T in (17, 1, 1, 5, 1, 9):
+    for T in steps:
         if pos + T > mc:
             break
-        print(f"[gpu] attention {shape} rope={rope} pos0={pos} T={T}", flush=True)
+        print(f"[gpu] attention {shape[:4]} rope={rope} pos0={pos} T={T}", flush=True)
         q = r.normal(0, 1, (T, nh * hd)).astype(np.float32)
         k = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
         v = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
