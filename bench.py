@@ -452,9 +452,11 @@ def main():
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMMs")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end SmolLM2 session")
     ap.add_argument("--eager", action="store_true",
-                    help="no HIP graphs (for kernel tracing): the step rate becomes host-bound, per-kernel "
-                         "event timings are unchanged")
+                    help="no HIP graphs, in the benchmarks or the e2e sessions (for kernel tracing): the step "
+                         "rate becomes host-bound, per-kernel event timings are unchanged")
     args = ap.parse_args()
+    if args.eager:  # the e2e sessions' decode graphs too
+        os.environ["EDGELM_HIP_GRAPHS"] = "0"
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (this delegate has no multi-GPU path); got --gpus {args.gpus}, "

@@ -14,9 +14,10 @@
 // Either way the host has what it needs when run() returns (edgelm's contract: runtime.cpp:66-76).
 // Weights are uploaded to HBM once, on first use (matmul weights repacked; RMSNORM weights f32).
 //
-// run_partition() (the other optional hook) replays a decode step (T = 1) of a whole partition as
-// one HIP graph: the first such step runs op by op (allocating buffers and uploading weights), the
-// second is captured, with attention reading the position from device memory; every later step
+// run_partition() (the other optional hook) replays a decode step (T = 1) of a whole partition of
+// at least kMinGraphOps ops as one HIP graph: the first such step runs op by op (allocating
+// buffers and uploading weights), the second is captured, with attention reading the position
+// from device memory; every later step
 // uploads the host-side inputs (token ids) and the position, launches the graph, and copies back
 // what the host reads (the logits). A buffer that has to grow (a longer prefill) drops the graphs.
 // EDGELM_HIP_GRAPHS=0 turns graphs off.
@@ -113,7 +114,8 @@ class HipBackend : public Backend {
 
   // overrides where Backend declares it; false: the Session runs the partition op by op
   bool run_partition(const Partition& p, ExecContext& c) {
-    if (!graphs_on_ || !ctx_ || !prepared_ || c.T != 1 || c.L != 1) return false;
+    // a graph launch costs ~100 us of host time: only long partitions gain from replaying one
+    if (!graphs_on_ || !ctx_ || !prepared_ || c.T != 1 || c.L != 1 || p.end - p.begin < kMinGraphOps) return false;
     const Graph& g = *c.graph;
     StepGraph& sg = graphs_[p.begin];
     if (!sg.exec && sg.warm == 0) {  // warm-up: allocations and uploads happen op by op
@@ -228,6 +230,9 @@ class HipBackend : public Backend {
     float* k = nullptr;
     float* v = nullptr;
   };
+  // Partitions of a few ops (the hip-matmul flavour's, between host-run ops) gain less from one
+  // graph launch than the launch itself costs: they run op by op.
+  static constexpr int kMinGraphOps = 16;
   struct StepGraph {
     int warm = 0;
     void* exec = nullptr;
