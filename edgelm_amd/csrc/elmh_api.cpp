@@ -113,7 +113,9 @@ int gemv_tokens(const DevWeight& w, int nsel, bool small) {
   for (int nt : {4, 2, 1}) {
     if (nt > gemv_max_tokens(K)) continue;
     if (gemv_lds_bytes(nt, K, nb, w.H, nsel) > 64 * 1024) continue;
-    if (small ? !use_small_gemv(nt, K) : gemv_stream_ipt(w.dtype, nsel * w.H * nb) == 0) continue;
+    if (small ? !use_small_gemv(nt, K)
+              : gemv_stream_ipt(w.dtype, nsel * w.H * nb) == 0 || nt * w.H > kStreamFoldLanes)
+      continue;
     return nt;
   }
   return 0;
@@ -138,7 +140,7 @@ int stream_tpw(const DevWeight& w, int T, int tiles_total, int nsel) {
   const int target = kGemvThreads * (w.dtype == ELMH_Q8 ? 4 : 8);
   int tpw = std::max(1, target / per_tile);
   tpw = std::min(tpw, std::max(1, tiles_total / 512));
-  while (tpw > 1 && (T * tpw * w.H > kGemvThreads || gemv_stream_ipt(w.dtype, tpw * per_tile) == 0 ||
+  while (tpw > 1 && (T * tpw * w.H > kStreamFoldLanes || gemv_stream_ipt(w.dtype, tpw * per_tile) == 0 ||
                      gemv_lds_bytes(T, (int)w.cols, (int)w.nb, tpw * w.H, nsel) > 64 * 1024))
     --tpw;
   return tpw;

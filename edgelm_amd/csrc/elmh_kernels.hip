@@ -507,18 +507,76 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   gemv_fold<WDT, NT, SW>(a, L, tg, tile * H, H, H, tid, e_res, e_s, e_su);
 }
 
-// Activation registers of the streaming GEMV: T * K <= kStreamMaxAct bytes.
+// Streaming GEMV: T * K <= kStreamMaxAct activation bytes (staged in LDS).
 constexpr int kStreamMaxAct = 16384;
-constexpr int kStreamActVec = kStreamMaxAct / 16 / kGemvThreads;
-constexpr int kStreamActBlk = kStreamMaxAct / kBlock / kGemvThreads;
+
+typedef __attribute__((address_space(3))) unsigned char* LdsBytes;
+
+// One global_load_lds of 16 (or 4) bytes per active lane into LDS at dst + 16 (4) * lane (dst is
+// wave-uniform: it goes to M0). Written as asm so that the compiler's wait-count pass does not
+// track it (it would drain every in-flight load before each LDS read); the kernel waits for these
+// loads itself (wait_vm) and drains them all before its LDS is reused or released. M0 is a
+// register the compiler reserves and does not save around asm; the kernels that use these (the
+// streaming GEMV and the GEMM) make no other use of it (their code references M0 only inside
+// these statements), so the write disturbs nothing.
+__device__ __forceinline__ void dma16(const void* src, unsigned char* dst) {
+  const unsigned m0 = (unsigned)(size_t)(LdsBytes)dst;
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* src, unsigned char* dst) {
+  const unsigned m0 = (unsigned)(size_t)(LdsBytes)dst;
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory");
+}
+
+// s_waitcnt vmcnt(N) only (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4] << 14)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// workgroup barrier that orders LDS accesses in the compiler's view without waiting for loads
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Adds row[b0 .. b1) to acc in block order. Up to 64 values (one batch of a row with 4-row
+// tiles) are read before the first add, so the chain waits for LDS once; longer ranges repeat.
+__device__ __forceinline__ float fold_range(float acc, const float* row, int b0, int b1) {
+  int b = b0;
+  for (; b < b1 && (b & 3); ++b) acc = acc + row[b];
+  while (b + 4 <= b1) {
+    const int ng = min((b1 - b) >> 2, 16);  // whole float4 groups this round
+    float4 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (i < ng) v[i] = *reinterpret_cast<const float4*>(row + b + 4 * i);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (i < ng) add4(acc, v[i]);
+    b += 4 * ng;
+  }
+  for (; b < b1; ++b) acc = acc + row[b];
+  return acc;
+}
 
 // Streaming decode GEMV for large weights: pre-quantized activation; a workgroup takes a.tpw
-// consecutive H-row tiles (one contiguous chunk). Its activation is requested first (into
-// registers), then every weight item of the workgroup (at most IPT per thread) at once; vector
-// loads retire in order, so each item's product is computed as soon as it has landed while the
-// rest are still streaming in. One lane per (token, row) then folds its row in block order.
-template <int WDT, int NT, bool SW, int IPT>
-__global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArgs a) {
+// consecutive H-row tiles (one contiguous chunk). NPW producer waves (P = 64 NPW threads)
+// request the activation (copied straight into LDS) and then every weight item of the workgroup
+// (at most IPT per thread), so nothing waits before the last request is out; vector loads retire
+// in order, so the activation lands first. Item batch u (items u*P .. u*P+P-1: blocks u*P/H .. of
+// each row) is multiplied as soon as it has landed and its products go to LDS. One more wave
+// only folds: after batch u's barrier, one of its lanes per (token, row) adds the blocks of its
+// row that the batch completed, in block order. The sequential fold (one dependent add per block,
+// 448 per row at K = 14336) thus runs beside the products while later batches stream in, and
+// only the last batch's share is left once the last weight has arrived. Without the fold wave
+// (FW false: short rows, where the extra wave costs more than the chain) the producers fold at
+// the end, one lane per (token, row).
+template <int WDT, int NT, bool SW, int IPT, int NPW, int DEPTH, bool FW>
+__global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const GemvArgs a) {
+  constexpr int P = 64 * NPW;  // producer threads
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int G = WDT == WQ8 ? 32 : 16;
   const int K = a.K, nb = a.nb, T = a.T, H = a.H, tid = threadIdx.x;
@@ -530,49 +588,83 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
   const int R = a.tpw * H;      // LDS row slots per token
   const int rows = ntl * H;     // rows this workgroup owns
   const int per_tile = H * nb, per_sel = ntl * per_tile, items = (SW ? 2 : 1) * per_sel;
+  const int lgH = __builtin_ctz(H), bpu = P >> lgH;
+  const bool producer = tid < P;  // waves 0 .. NPW-1; wave NPW folds (FW)
+
+  if (FW && !producer) {
+    // fold wave: lane (ft, fr) owns row fr of token ft; gate (or the only weight) and up chains.
+    // Batch u completes, for a row of local tile tl, blocks below (u + 1) P / H - tl nb (gate)
+    // and below that minus ntl nb (up).
+    // The chain is one dependent add per block: let this wave issue ahead of the producers
+    // whenever it is ready, or it waits its turn behind their products on the same SIMD.
+    __builtin_amdgcn_s_setprio(3);
+    const int lane = tid - P;
+    const int ft = lane / R, fr = lane - ft * R, ftl = fr >> lgH;
+    const bool folder = lane < T * R && fr < rows;
+    const float* const frow_g = L.p + (ft * R + fr) * L.pst;
+    const float* const frow_u = L.p + ((NT + ft) * R + fr) * L.pst;
+    float e_res, e_s, e_su;
+    gemv_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, lane, e_res, e_s, e_su);
+    float acc_g = 0.f, acc_u = 0.f;
+    int done_g = 0, done_u = 0;
+    __syncthreads();  // activation in LDS
+    for (int u = 0; u < IPT; ++u) {
+      __syncthreads();  // batch u's products in LDS
+      if (folder) {
+        const int lim = (u + 1) * bpu - ftl * nb;
+        const int ng = min(max(lim, 0), nb);
+        acc_g = fold_range(acc_g, frow_g, done_g, ng);
+        done_g = ng;
+        if (SW) {
+          const int nu = min(max(lim - ntl * nb, 0), nb);
+          acc_u = fold_range(acc_u, frow_u, done_u, nu);
+          done_u = nu;
+        }
+      }
+    }
+    if (!folder) return;
+    const int fn = tile0 * H + fr;
+    if (fn >= tg.N) return;
+    float out = WDT == WQ8 ? acc_g * e_s : acc_g * 16.0f;
+    if (SW) {
+      const float up = WDT == WQ8 ? acc_u * e_su : acc_u * 16.0f;
+      out = silu_exact(out) * up;
+    } else if (tg.res) {
+      out = out + e_res;
+    }
+    tg.y[(int64_t)ft * tg.N + fn] = out;
+    return;
+  }
+
   const int64_t base = (int64_t)tile0 * per_tile;
   // A store the compiler cannot rule out (T is never negative): without one, loads from memory
   // that nothing in the kernel writes count as invariant and get sunk to their first use, which
   // would put them behind the waits below instead of all in flight at once.
   if (T < 0) tg.y[0] = 0.f;
 
-  // 1. activation into LDS before any weight is requested: once the weight loads are queued, an
-  // activation load would wait behind them (the products need it first). Indices are clamped
-  // rather than tested (lanes past the end rewrite the last element with its own value), so the
-  // loads stay unconditional and in registers.
-  const int nq16 = T * K / 16, nblk = T * nb;
-  static_assert(kStreamActVec == 4 && kStreamActBlk == 2, "activation register count");
+  // 1. activation (int8 values, block scales and, for q4, block sums) straight into LDS, where
+  // its rows are contiguous (K % 16 == 0): wave w copies chunks w, w + NPW, ... of 1 KB (256 B).
   {
-    // named values: arrays here end up in scratch memory
-    const int4* xq4 = reinterpret_cast<const int4*>(a.xq);
-    const int e0 = min(tid, nq16 - 1), e1 = min(kGemvThreads + tid, nq16 - 1);
-    const int e2 = min(2 * kGemvThreads + tid, nq16 - 1), e3 = min(3 * kGemvThreads + tid, nq16 - 1);
-    const int4 v0 = xq4[e0], v1 = xq4[e1], v2 = xq4[e2], v3 = xq4[e3];
-    const int eb0 = min(tid, nblk - 1), eb1 = min(kGemvThreads + tid, nblk - 1);
-    const float ad0 = a.xd[eb0], ad1 = a.xd[eb1];
-    const int as0 = a.xs[eb0], as1 = a.xs[eb1];
-    auto put = [&](int e, const int4& v) {
-      const int t = (e * 16) / K, k = e * 16 - t * K;
-      *reinterpret_cast<int4*>(L.q + t * L.kpad + k) = v;
-    };
-    put(e0, v0);
-    put(e1, v1);
-    put(e2, v2);
-    put(e3, v3);
-    L.d[eb0] = ad0;
-    L.s[eb0] = as0;
-    L.d[eb1] = ad1;
-    L.s[eb1] = as1;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int nq = T * K, nd = T * nb;
+    for (int c = wave; c * 1024 < nq; c += NPW)
+      if (c * 1024 + lane * 16 < nq) dma16(a.xq + c * 1024 + lane * 16, (unsigned char*)L.q + c * 1024);
+    for (int c = wave; c * 64 < nd; c += NPW)
+      if (c * 64 + lane < nd) {
+        dma4(a.xd + c * 64 + lane, (unsigned char*)(L.d + c * 64));
+        if (WDT == WQ4) dma4(a.xs + c * 64 + lane, (unsigned char*)(L.s + c * 64));
+      }
   }
-  asm volatile("" ::: "memory");  // the weight loads below stay behind the activation stores
-  // 2. every weight item of the workgroup in flight
+  asm volatile("" ::: "memory");  // the weight requests below stay behind the activation's
+  // 2. weight items of the first DEPTH batches in flight; batch u + DEPTH is requested once batch
+  // u's products are out, so a wave whose requests stall (full memory queues) has already done
+  // every product whose data has arrived. Requests past the last item repeat it.
   const uint8_t* const wd1 = SW ? a.tg[1].data : tg.data;
   const float* const ws1 = SW ? a.tg[1].scales : tg.scales;
   v4u w[IPT][G / 16];
   float wsc[IPT];
-#pragma unroll
-  for (int u = 0; u < IPT; ++u) {
-    const int it = min(u * kGemvThreads + tid, items - 1);
+  auto request = [&](int u) {
+    const int it = min(u * P + tid, items - 1);
     const int sel = SW ? (it >= per_sel) : 0;
     const int64_t gi = base + (it - sel * per_sel);
     const v4u* src = reinterpret_cast<const v4u*>((sel ? wd1 : tg.data) + gi * G);
@@ -580,44 +672,55 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_stream_kernel(const GemvArg
     if (G == 32) w[u][G / 16 - 1] = __builtin_nontemporal_load(src + 1);
     wsc[u] = 0.f;
     if (WDT == WQ4) wsc[u] = __builtin_nontemporal_load((sel ? ws1 : tg.scales) + gi);
-  }
-  asm volatile("" ::: "memory");  // every weight load issued before anything waits
-  float e_res, e_s, e_su;
-  gemv_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
+  };
+  constexpr int D0 = DEPTH < IPT ? DEPTH : IPT;
+#pragma unroll
+  for (int u = 0; u < D0; ++u) request(u);
+  asm volatile("" ::: "memory");  // these loads issued before anything waits
+  // 3. the activation has landed once at most this wave's weight loads (two per item) are still
+  // in flight; the barrier makes every wave's part visible
+  wait_vm<2 * D0>();
   __syncthreads();
+  float e_res = 0.f, e_s = 1.f, e_su = 1.f;
+  if (!FW) gemv_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
 
-  // 4. products into LDS in request order (each waits only for its own loads). H is a power of two
-  // dividing the workgroup size, so a thread's row within its tile never changes and its block
-  // advances by 256 / H per load step; no integer division per item.
-  const int lgH = __builtin_ctz(H);
-  const int r_in = tid & (H - 1), q0 = tid >> lgH, bpu = kGemvThreads >> lgH;
+  // 4. products into LDS in request order (each waits only for its own loads), one barrier per
+  // batch. H is a power of two dividing P, so a thread's row within its tile never changes and
+  // its block advances by P / H per batch; no integer division per item.
+  const int r_in = tid & (H - 1), q0 = tid >> lgH;
   const float inv_nb = 1.0f / (float)nb;
   const int tstride = R * L.pst, sstride = NT * tstride, prow = r_in * L.pst;
 #pragma unroll
-  for (int u = 0; u < IPT; ++u) {
-    const int it = u * kGemvThreads + tid;
-    if (it < items) {
-      const int sel = SW ? (it >= per_sel) : 0;
-      int b = u * bpu + q0 - (sel ? ntl * nb : 0);  // block position across this selection's tiles
-      int off = prow + (sel ? sstride : 0);
-      if (a.tpw > 1) {
-        // tile = floor(b / nb): (b + 0.5) / nb is at least 0.5 / nb away from an integer, far more
-        // than the float error at these sizes (b < 4096)
-        const int st = (int)(((float)b + 0.5f) * inv_nb);
-        b -= st * nb;
-        off += st * H * L.pst;
-      }
-      off += b;
+  for (int u = 0; u < IPT; ++u) {  // every batch, also empty ones: straight-line code, exact waits
+    {
+      const int it = u * P + tid;
+      if (it < items) {
+        const int sel = SW ? (it >= per_sel) : 0;
+        int b = u * bpu + q0 - (sel ? ntl * nb : 0);  // block position across this selection's tiles
+        int off = prow + (sel ? sstride : 0);
+        if (a.tpw > 1) {
+          // tile = floor(b / nb): (b + 0.5) / nb is at least 0.5 / nb away from an integer, far
+          // more than the float error at these sizes (b < 4096)
+          const int st = (int)(((float)b + 0.5f) * inv_nb);
+          b -= st * nb;
+          off += st * H * L.pst;
+        }
+        off += b;
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
-        if (t < T)
-          L.p[off + t * tstride] = item_product<WDT>(w[u][0], w[u][G / 16 - 1], wsc[u], L.q + t * L.kpad + b * kBlock,
-                                                     L.d[t * nb + b], L.s[t * nb + b]);
+        for (int t = 0; t < NT; ++t)
+          if (t < T)
+            L.p[off + t * tstride] = item_product<WDT>(w[u][0], w[u][G / 16 - 1], wsc[u], L.q + t * L.kpad + b * kBlock,
+                                                       L.d[t * nb + b], L.s[t * nb + b]);
+      }
     }
+    if (u + DEPTH < IPT) request(u + DEPTH);
+    if (FW) __syncthreads();  // also waits for this wave's product writes
   }
-  __syncthreads();
-  // 5. one lane per (token, row) folds its row in block order and applies the epilogue
-  gemv_fold<WDT, NT, SW>(a, L, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
+  if (!FW) {
+    // 5. one lane per (token, row) folds its row in block order and applies the epilogue
+    __syncthreads();
+    gemv_fold<WDT, NT, SW>(a, L, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
+  }
 }
 
 // ---------------------------------------------------------------- int8 MFMA GEMM (prefill)
@@ -651,37 +754,6 @@ __device__ __forceinline__ GemmTarget gemm_target_at(int ti) {
   t.N = ka->tg[ti].N;
   t.ntiles = ka->tg[ti].ntiles;
   return t;
-}
-
-typedef __attribute__((address_space(3))) unsigned char* LdsBytes;
-
-// One global_load_lds of 16 (or 4) bytes per active lane into LDS at dst + 16 (4) * lane (dst is
-// wave-uniform: it goes to M0). Written as asm so that the compiler's wait-count pass does not
-// track it (it would drain every in-flight load before each LDS read); the kernel waits for these
-// loads itself (wait_vm) and drains them all before its LDS is reused or released. M0 is a
-// register the compiler reserves and does not save around asm; the GEMM kernel makes no other use
-// of it (its code references M0 only inside these statements), so the write disturbs nothing.
-__device__ __forceinline__ void dma16(const void* src, unsigned char* dst) {
-  const unsigned m0 = (unsigned)(size_t)(LdsBytes)dst;
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
-}
-__device__ __forceinline__ void dma4(const void* src, unsigned char* dst) {
-  const unsigned m0 = (unsigned)(size_t)(LdsBytes)dst;
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory");
-}
-
-// s_waitcnt vmcnt(N) only (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4] << 14)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// workgroup barrier that orders LDS accesses in the compiler's view without waiting for loads
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 template <int WDT, bool SW, bool TOK, int MT>
@@ -1235,11 +1307,28 @@ size_t gemv_lds_bytes(int nt, int K, int nb, int H, int nsel) {
 
 bool gemv_qin_ok(int T, int K) { return T * K <= 2 * kSmallMaxAct; }
 
-int gemv_stream_ipt(int dtype, int items) {
-  const int per = (items + kGemvThreads - 1) / kGemvThreads;
+int gemv_stream_ipt(int dtype, int items, int producers) {
+  const int per = (items + producers - 1) / producers;
   const int cap = dtype == WQ8 ? 8 : 16;
   if (per > cap) return 0;
   return per <= 4 ? 4 : per <= 8 ? 8 : 16;
+}
+
+template <int WDT, int NT, bool SW, int NPW, bool FW>
+static hipError_t stream_launch(const GemvArgs& a, int wgs, size_t lds, int items, hipStream_t s) {
+  constexpr int threads = 64 * (NPW + FW);
+  switch (gemv_stream_ipt(WDT, items, 64 * NPW)) {
+    case 4: gemv_stream_kernel<WDT, NT, SW, 4, NPW, FW ? 2 : 4, FW><<<wgs, threads, lds, s>>>(a); break;
+    case 8: gemv_stream_kernel<WDT, NT, SW, 8, NPW, FW ? 2 : 4, FW><<<wgs, threads, lds, s>>>(a); break;
+    case 16:
+      if (WDT == WQ4) {
+        gemv_stream_kernel<WDT, NT, SW, 16, NPW, FW ? 2 : 4, FW><<<wgs, threads, lds, s>>>(a);
+        break;
+      }
+      return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 template <int WDT, int NT, bool SW>
@@ -1252,22 +1341,12 @@ static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
     gemv_small_kernel<WDT, NT, SW><<<tiles, kGemvThreads, lds, s>>>(a);
     return hipGetLastError();
   }
-  if (a.tpw < 1 || a.T * a.tpw * a.H > kGemvThreads || a.T * a.K > kStreamMaxAct || (a.K & 15) ||
-      (a.H & (a.H - 1)) || a.tpw * a.nb > 4096)
+  if (a.tpw < 1 || a.T * a.tpw * a.H > kStreamFoldLanes || a.T * a.K > kStreamMaxAct || (a.K & 15) ||
+      (a.H & (a.H - 1)) || a.H > 64 * kStreamProducerWaves || a.tpw * a.nb > 4096)
     return hipErrorInvalidValue;
   const int items = (SW ? 2 : 1) * a.tpw * a.H * a.nb;
-  switch (gemv_stream_ipt(WDT, items)) {
-    case 4: gemv_stream_kernel<WDT, NT, SW, 4><<<tiles, kGemvThreads, lds, s>>>(a); break;
-    case 8: gemv_stream_kernel<WDT, NT, SW, 8><<<tiles, kGemvThreads, lds, s>>>(a); break;
-    case 16:
-      if (WDT == WQ4) {
-        gemv_stream_kernel<WDT, NT, SW, 16><<<tiles, kGemvThreads, lds, s>>>(a);
-        break;
-      }
-      return hipErrorInvalidValue;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  if (a.nb > kStreamFoldWaveBlocks) return stream_launch<WDT, NT, SW, kStreamProducerWaves, true>(a, tiles, lds, items, s);
+  return stream_launch<WDT, NT, SW, kStreamProducerWaves, false>(a, tiles, lds, items, s);
 }
 
 template <int WDT, bool SW>

@@ -254,6 +254,30 @@ def test_matmul_n_and_swiglu_long_rows(ctx, dt):
 
 
 @pytest.mark.parametrize("dt", [O.Q8, O.Q4])
+def test_matmul_n_and_swiglu_fold_wave_rows(ctx, dt):
+    """Rows of more than 256 blocks (K = 14336, decode): the GEMV folds in a wave of its own while
+    the weights stream; MATMUL_N with ragged targets and a residual, and FFN_SWIGLU."""
+    r = rng(11 + dt)
+    k = 14336
+    ws = [weight(r, 260, k, dt), weight(r, 36, k, dt), weight(r, 68, k, dt)]
+    dws = [up(ctx, w) for w in ws]
+    print(f"[gpu] matmul_n fold-wave dt={dt}", flush=True)
+    x = r.normal(0, 1, (1, k)).astype(np.float32)
+    res = [None, r.normal(0, 1, (1, 36)).astype(np.float32), None]
+    got = ctx.matmul(x, dws, res, act=E.ACT_INT8)
+    want = O.cpu_matmul(x, ws, res, act_quant=True)
+    for i, (g, wv) in enumerate(zip(got, want)):
+        assert bits_equal(g, wv), f"target {i}"
+    wg, wu = weight(r, 132, k, dt), weight(r, 132, k, dt)
+    dg, du = up(ctx, wg), up(ctx, wu)
+    print(f"[gpu] swiglu fold-wave dt={dt}", flush=True)
+    got = ctx.swiglu(x, dg, du, act=E.ACT_INT8)
+    assert bits_equal(got, O.cpu_swiglu(x, wg, wu, act_quant=True))
+    for d in dws + [dg, du]:
+        d.free()
+
+
+@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
 def test_matmul_f32act_long_rows(ctx, dt):
     """f32 activations at K > 2048 (taller row tiles): GEMV and dequantizing GEMM."""
     r = rng(400 + dt)
