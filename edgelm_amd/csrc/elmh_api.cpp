@@ -87,11 +87,13 @@ int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
 // Row-tile height of the repacked layout, chosen from dtype and K only (so every weight sharing an
 // input — MATMUL_N, gate/up — agrees). Short rows (K <= 2048) use 8-row tiles: many small decode
-// workgroups with at most two items per thread. Long rows use the tallest tile whose items fit the
-// streaming GEMV's registers (q4: 2048 items of 16 B, q8: 1024 items of 32 B), at least 4 rows.
+// workgroups with at most two items per thread. Rows of more than kStreamFoldWaveBlocks blocks
+// also use 8-row tiles (the streaming GEMV's seven producer waves take a tile in eight batches).
+// Other long rows use the tallest tile whose items fit the streaming GEMV's batches (q4: 2048
+// items of 16 B, q8: 1024 items of 32 B), at least 4 rows.
 int choose_H(int dtype, int64_t K) {
   const int64_t nb = (K + kBlock - 1) / kBlock;
-  if (K <= 2048) return 8;
+  if (K <= 2048 || nb > kStreamFoldWaveBlocks) return 8;
   const int64_t cap = dtype == ELMH_Q4 ? 2048 : 1024;
   for (int H : {32, 16, 8})
     if (H * nb <= cap) return H;
@@ -114,7 +116,7 @@ int gemv_tokens(const DevWeight& w, int nsel, bool small) {
     if (nt > gemv_max_tokens(K)) continue;
     if (gemv_lds_bytes(nt, K, nb, w.H, nsel) > 64 * 1024) continue;
     if (small ? !use_small_gemv(nt, K)
-              : gemv_stream_ipt(w.dtype, nsel * w.H * nb) == 0 || nt * w.H > kStreamFoldLanes)
+              : gemv_stream_ipt(w.dtype, nsel * w.H * nb, stream_producers(nb)) == 0 || nt * w.H > kStreamFoldLanes)
       continue;
     return nt;
   }
@@ -140,7 +142,7 @@ int stream_tpw(const DevWeight& w, int T, int tiles_total, int nsel) {
   const int target = kGemvThreads * (w.dtype == ELMH_Q8 ? 4 : 8);
   int tpw = std::max(1, target / per_tile);
   tpw = std::min(tpw, std::max(1, tiles_total / 512));
-  while (tpw > 1 && (T * tpw * w.H > kStreamFoldLanes || gemv_stream_ipt(w.dtype, tpw * per_tile) == 0 ||
+  while (tpw > 1 && (T * tpw * w.H > kStreamFoldLanes || gemv_stream_ipt(w.dtype, tpw * per_tile, stream_producers((int)w.nb)) == 0 ||
                      gemv_lds_bytes(T, (int)w.cols, (int)w.nb, tpw * w.H, nsel) > 64 * 1024))
     --tpw;
   return tpw;

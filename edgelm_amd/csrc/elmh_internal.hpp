@@ -9,13 +9,16 @@ namespace elmh {
 constexpr int kBlock = 32;       // activation block / q4 group (edgelm kActBlock, kernels.hpp:38)
 constexpr int kMaxTargets = 4;   // weights per kernel launch (MATMUL_N with more is split)
 constexpr int kGemvThreads = 256;
-// streaming GEMV: kStreamProducerWaves producer waves plus one wave whose lanes fold (token, row)
-// pairs
-constexpr int kStreamProducerWaves = 4;
-// Rows of more blocks than this get the fold wave (and two weight batches in flight per producer
-// wave; shorter rows keep four).
-constexpr int kStreamFoldWaveBlocks = 256;
+// Streaming GEMV: producer waves plus, for rows of more than kStreamFoldWaveBlocks blocks, one
+// wave whose lanes fold (token, row) pairs while the weights stream (seven producer waves and two
+// weight batches in flight per wave there; four producer waves and four batches otherwise).
 constexpr int kStreamFoldLanes = 64;
+constexpr int kStreamFoldWaveBlocks = 256;
+constexpr int kStreamWavesShort = 4;
+constexpr int kStreamWavesLong = 7;
+inline int stream_producers(int nb) {
+  return 64 * (nb > kStreamFoldWaveBlocks ? kStreamWavesLong : kStreamWavesShort);
+}
 constexpr int kGemmTileN = 128;  // weight rows per GEMM workgroup
 constexpr int kGemmTileT = 128;  // tokens per GEMM workgroup
 constexpr int kPadRows = 64;     // rows_pad is a multiple of this
@@ -112,7 +115,7 @@ int gemv_max_tokens(int K);
 // True if a workgroup may quantize T rows of K activations itself (small-matrix GEMV).
 bool gemv_qin_ok(int T, int K);
 // Items per thread of the streaming GEMV for a tile of `items` items (0: too many).
-int gemv_stream_ipt(int dtype, int items, int producers = 64 * kStreamProducerWaves);
+int gemv_stream_ipt(int dtype, int items, int producers);
 size_t gemv_lds_bytes(int nt, int K, int nb, int H, int nsel);
 hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_tiles, hipStream_t s);
 hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs& a, int total_tiles, hipStream_t s);

@@ -1342,11 +1342,11 @@ static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
     return hipGetLastError();
   }
   if (a.tpw < 1 || a.T * a.tpw * a.H > kStreamFoldLanes || a.T * a.K > kStreamMaxAct || (a.K & 15) ||
-      (a.H & (a.H - 1)) || a.H > 64 * kStreamProducerWaves || a.tpw * a.nb > 4096)
+      (a.H & (a.H - 1)) || a.H > 64 || a.tpw * a.nb > 4096)
     return hipErrorInvalidValue;
   const int items = (SW ? 2 : 1) * a.tpw * a.H * a.nb;
-  if (a.nb > kStreamFoldWaveBlocks) return stream_launch<WDT, NT, SW, kStreamProducerWaves, true>(a, tiles, lds, items, s);
-  return stream_launch<WDT, NT, SW, kStreamProducerWaves, false>(a, tiles, lds, items, s);
+  if (a.nb > kStreamFoldWaveBlocks) return stream_launch<WDT, NT, SW, kStreamWavesLong, true>(a, tiles, lds, items, s);
+  return stream_launch<WDT, NT, SW, kStreamWavesShort, false>(a, tiles, lds, items, s);
 }
 
 template <int WDT, bool SW>
