@@ -756,7 +756,7 @@ __device__ __forceinline__ GemmTarget gemm_target_at(int ti) {
   return t;
 }
 
-template <int WDT, bool SW, bool TOK, int MT>
+template <int WDT, bool SW, bool TOK, int MT, int KBO>
 struct GemmRing {
   static constexpr int TT = 64 * MT;
   static constexpr int NSEL = SW ? 2 : 1;
@@ -767,15 +767,19 @@ struct GemmRing {
   static constexpr int SLOT = ACT + NSEL * WSEL + XD;
   static constexpr int D = (76 * 1024) / SLOT < 4 ? 4 : (76 * 1024) / SLOT;  // ring depth
   static constexpr int P = 1 + NSEL + (BLOCKX ? 1 : 0);                        // DMA instructions per wave per slot
+  // blocks per barrier: the per-token q8 loop is a few MFMAs per block, so its barrier, fragment
+  // reads and DMA issues are grouped over KB blocks (the ring then runs D - 2 KB blocks ahead)
+  static constexpr int KB = KBO ? KBO : TOK && WDT == WQ8 && !SW ? (MT == 1 ? 4 : 2) : 1;
+  static_assert(D >= 2 * KB + 1, "ring too shallow for the block group");
   static constexpr int EP = SW ? 4 * 2 * 32 * 32 * 4 : 16;                     // SwiGLU epilogue: gate and up per wave
   static constexpr int BYTES = D * SLOT > EP ? D * SLOT : EP;
-  static_assert((D - 2) * P < 64, "vmcnt range");
+  static_assert((D - 2 * KB) * P < 64, "vmcnt range");
 };
 
-template <int WDT, bool SW, bool TOK, bool FAST, int MT>
+template <int WDT, bool SW, bool TOK, bool FAST, int MT, int KBO = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT == 2 ? 1 : 2))) void gemm_a8_kernel(
     const GemmArgs a) {
-  typedef GemmRing<WDT, SW, TOK, MT> R;
+  typedef GemmRing<WDT, SW, TOK, MT, KBO> R;
   constexpr int TT = R::TT, NSEL = R::NSEL, D = R::D;
   constexpr bool BLOCKX = R::BLOCKX;
   __shared__ __align__(16) unsigned char ring[R::BYTES];
@@ -911,16 +915,61 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
 
   // per-token scales of the tile's tokens (the per-token mode's epilogue reads them from LDS)
   if (TOK && tid < TT) Lxdt[tid] = a.xd[t0 + tid];
+  if constexpr (R::KB == 1) {
 #pragma unroll
-  for (int i = 0; i < D - 1; ++i) issue(i, i);
-  int cs = 0, is = D - 1;  // slot to compute, slot to fill
-  for (int b = 0; b < nb; ++b) {
-    wait_vm<(D - 2) * R::P>();  // this wave's part of block b has landed
-    lds_barrier();              // every wave's part has; every wave is done with block b - 1
-    issue(b + D - 1, is);
-    block(cs);
-    cs = cs + 1 == D ? 0 : cs + 1;
-    is = is + 1 == D ? 0 : is + 1;
+    for (int i = 0; i < D - 1; ++i) issue(i, i);
+    int cs = 0, is = D - 1;  // slot to compute, slot to fill
+    for (int b = 0; b < nb; ++b) {
+      wait_vm<(D - 2) * R::P>();  // this wave's part of block b has landed
+      lds_barrier();              // every wave's part has; every wave is done with block b - 1
+      issue(b + D - 1, is);
+      block(cs);
+      cs = cs + 1 == D ? 0 : cs + 1;
+      is = is + 1 == D ? 0 : is + 1;
+    }
+  } else {
+    // per-token q8: block j lives in slot j % D; a group computes blocks b .. b + KB - 1 after
+    // refilling the slots the previous group read. Fragments of the whole group are read before
+    // its MFMAs; blocks past the last (their slots repeat it) are read but add zero.
+    constexpr int KB = R::KB;
+#pragma unroll
+    for (int i = 0; i < D - KB; ++i) issue(i, i);
+    int cs = 0, is = D - KB;
+    for (int b = 0; b < nb; b += KB) {
+      wait_vm<(D - 2 * KB) * R::P>();  // this wave's parts of blocks b .. b + KB - 1 have landed
+      lds_barrier();                   // every wave's have; every wave is done with the last group
+#pragma unroll
+      for (int k = 0; k < KB; ++k) {
+        issue(b + D - KB + k, is);
+        is = is + 1 == D ? 0 : is + 1;
+      }
+      v4i A[KB][MT], B[KB][2];
+#pragma unroll
+      for (int k = 0; k < KB; ++k) {
+        const int sl = cs + k < D ? cs + k : cs + k - D;
+        const unsigned char* sb = ring + sl * R::SLOT;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) A[k][mt] = *reinterpret_cast<const v4i*>(sb + ((wt * MT + mt) * 64 + lane) * 16);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const int rl = wr * 64 + nt * 32 + l32;
+          B[k][nt] = *reinterpret_cast<const v4i*>(sb + R::ACT + (2 * rl + (h ^ ((rl >> 3) & 1))) * 16);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // every fragment read of the group ahead of its MFMAs
+#pragma unroll
+      for (int k = 0; k < KB; ++k) {
+        const bool ok = b + k < nb;  // uniform; a block past the last adds zero
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const v4i a4 = ok ? A[k][mt] : v4i{0, 0, 0, 0};
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt)
+            iacc[0][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, B[k][nt], iacc[0][mt][nt], 0, 0, 0);
+        }
+      }
+      cs = cs + KB < D ? cs + KB : cs + KB - D;
+    }
   }
   wait_vm<0>();  // the repeated last-block issues have landed before the ring is reused or freed
   lds_barrier();

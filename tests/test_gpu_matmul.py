@@ -298,14 +298,15 @@ def test_matmul_f32act_long_rows(ctx, dt):
 def test_gemm_token_tiles(ctx, dt, tile, monkeypatch):
     """Both GEMM tile heights (64 and 128 tokens, picked by shape unless ELMH_GEMM_TOKEN_TILE forces
     one) over several token tiles with a ragged last one and a partial last row tile: per-block
-    int8 (exact, fast, residual), per-token int8, MATMUL_N and FFN_SWIGLU."""
+    int8 (exact, fast, residual), per-token int8 (block groups with a partial last group: K = 576
+    is 18 blocks), MATMUL_N and FFN_SWIGLU."""
     monkeypatch.setenv("ELMH_GEMM_TOKEN_TILE", tile)
     r = rng(500 + dt)
     n, k = 300, 576
     w, w2 = weight(r, n, k, dt), weight(r, 72, k, dt)
     wg, wu = weight(r, n, k, dt), weight(r, n, k, dt)
     dw, dw2, dg, du = up(ctx, w), up(ctx, w2), up(ctx, wg), up(ctx, wu)
-    for T in [65, 130, 257]:
+    for T in [65, 130, 257, 512]:
         print(f"[gpu] gemm tile={tile} dt={dt} T={T}", flush=True)
         x = r.normal(0, 1, (T, k)).astype(np.float32)
         res = r.normal(0, 1, (T, n)).astype(np.float32)
@@ -315,14 +316,33 @@ def test_gemm_token_tiles(ctx, dt, tile, monkeypatch):
         fast = ctx.matmul(x, [dw], None, act=E.ACT_INT8, mode=E.FAST)[0]
         assert rel_err(fast, O.cpu_matmul(x, [w], None, act_quant=True)[0]) < 1e-5
         assert bits_equal(ctx.swiglu(x, dg, du, act=E.ACT_INT8), O.cpu_swiglu(x, wg, wu, act_quant=True))
-        tok = ctx.matmul(x, [dw], [res], act=E.ACT_INT8_TOKEN)[0]
-        assert bits_equal(tok, O.matmul_a8_token(x, w, res))
+        tok = ctx.matmul(x, [dw, dw2], [res, None], act=E.ACT_INT8_TOKEN)
+        assert bits_equal(tok[0], O.matmul_a8_token(x, w, res)) and bits_equal(tok[1], O.matmul_a8_token(x, w2))
         if T == 65:
             g, u = O.matmul_a8_token(x, wg), O.matmul_a8_token(x, wu)
             want_sw = np.array([O.silu(float(v)) for v in g.ravel()], np.float32).reshape(g.shape) * u
             assert bits_equal(ctx.swiglu(x, dg, du, act=E.ACT_INT8_TOKEN), want_sw)
     for d in (dw, dw2, dg, du):
         d.free()
+
+
+@pytest.mark.parametrize("tile", ["64", "128"])
+def test_gemm_token_odd_block_count(ctx, tile, monkeypatch):
+    """Per-token q8 GEMM at K = 1568 (49 blocks): the last group of 4 (64-token tiles) or 2
+    (128-token tiles) blocks per barrier holds one real block and repeats of it that must add
+    nothing."""
+    monkeypatch.setenv("ELMH_GEMM_TOKEN_TILE", tile)
+    r = rng(600)
+    n, k = 200, 1568
+    w = weight(r, n, k, O.Q8)
+    dw = up(ctx, w)
+    for T in [130, 257]:
+        print(f"[gpu] gemm per-token odd nb tile={tile} T={T}", flush=True)
+        x = r.normal(0, 1, (T, k)).astype(np.float32)
+        res = r.normal(0, 1, (T, n)).astype(np.float32)
+        got = ctx.matmul(x, [dw], [res], act=E.ACT_INT8_TOKEN)[0]
+        assert bits_equal(got, O.matmul_a8_token(x, w, res))
+    dw.free()
 
 
 def test_dev_pointer_unaligned_input(ctx):
