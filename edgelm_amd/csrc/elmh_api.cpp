@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -694,6 +695,15 @@ int elmh_memcpy_d2d(elmh_ctx* c, void* dst, const void* src, size_t bytes) {
   if (bytes && (!dst || !src)) return fail(c, ELMH_ERR_ARG, "null dst/src");
   DeviceGuard g(c);
   if (bytes) HIP_OR_FAIL(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, c->stream));
+  return ELMH_OK;
+}
+
+int elmh_argmax_dev(elmh_ctx* c, const float* x, int rows, int64_t n, int32_t* out) {
+  if (!c || !x || !out) return fail(c, ELMH_ERR_ARG, "null ctx/x/out");
+  if (rows < 1 || n < 1) return fail(c, ELMH_ERR_ARG, "argmax: rows and n must be >= 1 (rows=%d n=%lld)", rows, (long long)n);
+  if (n > INT32_MAX) return fail(c, ELMH_ERR_ARG, "argmax: n=%lld exceeds int32 indices", (long long)n);
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, launch_argmax(x, rows, n, out, c->stream));
   return ELMH_OK;
 }
 

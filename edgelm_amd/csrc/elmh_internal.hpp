@@ -131,6 +131,7 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
 hipError_t launch_embed(const int32_t* tok, int T, const DevWeight& w, float* y, hipStream_t s);
 // dst[0, bytes) = value (a kernel: capturable in a HIP graph, unlike hipMemsetAsync)
 hipError_t launch_fill(void* dst, int value, size_t bytes, hipStream_t s);
+hipError_t launch_argmax(const float* x, int rows, int64_t n, int32_t* out, hipStream_t s);
 // Test hook: S[t][n][b] for pre-quantized row-major activations.
 hipError_t launch_block_sums(const DevWeight& w, const int8_t* xq, int T, int32_t* S, hipStream_t s);
 

@@ -333,6 +333,65 @@ __global__ __launch_bounds__(256) void fill_kernel(uint8_t* __restrict__ dst, si
 
 }  // namespace
 
+// ---------------------------------------------------------------- greedy sampling
+//
+// argmax (tokenizer.cpp:187-189) is std::max_element: a scan keeping the first index whose value
+// no later value exceeds under IEEE <. So ties keep the earlier index (-0 and +0 tie), a NaN after
+// index 0 is never taken, and a NaN at index 0 is kept (nothing compares greater). As a reduction:
+// candidates are the non-NaN values plus index 0 if it is NaN (which beats everything); the
+// larger value wins and equal values go to the smaller index. That order is total, so the
+// per-thread scans and the tree below may combine in any order.
+struct ArgBest {
+  float v;
+  int i;  // -1: no candidate
+};
+
+__device__ __forceinline__ ArgBest arg_pick(ArgBest a, ArgBest b) {
+  if (a.i < 0) return b;
+  if (b.i < 0) return a;
+  const bool an = a.i == 0 && a.v != a.v, bn = b.i == 0 && b.v != b.v;  // NaN at index 0
+  if (an || bn) return an ? a : b;
+  if (a.v > b.v) return a;
+  if (b.v > a.v) return b;
+  return a.i < b.i ? a : b;
+}
+
+// one workgroup of kArgThreads per row
+constexpr int kArgThreads = 1024;
+
+__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __restrict__ x, int64_t n,
+                                                             int32_t* __restrict__ out) {
+  __shared__ float sv[kArgThreads / 64];
+  __shared__ int si[kArgThreads / 64];
+  const float* row = x + (int64_t)blockIdx.x * n;
+  ArgBest best{0.f, -1};
+  for (int64_t j = threadIdx.x; j < n; j += kArgThreads) {
+    const float v = row[j];
+    if (v == v || j == 0) best = arg_pick(best, ArgBest{v, (int)j});
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const ArgBest o{__shfl_xor(best.v, off, 64), __shfl_xor(best.i, off, 64)};
+    best = arg_pick(best, o);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[wave] = best.v;
+    si[wave] = best.i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    ArgBest b{sv[0], si[0]};
+    for (int w = 1; w < kArgThreads / 64; ++w) b = arg_pick(b, ArgBest{sv[w], si[w]});
+    out[blockIdx.x] = b.i;  // n >= 1 and index 0 is always a candidate, so b.i >= 0
+  }
+}
+
+hipError_t launch_argmax(const float* x, int rows, int64_t n, int32_t* out, hipStream_t s) {
+  argmax_kernel<<<rows, kArgThreads, 0, s>>>(x, n, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_fill(void* dst, int value, size_t bytes, hipStream_t s) {
   if (bytes == 0) return hipSuccess;
   const uint32_t b = (uint32_t)(value & 0xFF);

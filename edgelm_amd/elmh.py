@@ -220,6 +220,9 @@ class Context:
             C.c_int(pos0), C.c_int(n_heads), C.c_int(n_kv), C.c_int(head_dim), C.c_void_p(kc_ptr), C.c_void_p(vc_ptr),
             C.c_int(max_ctx), C.c_void_p(cos_ptr), C.c_void_p(sin_ptr)))
 
+    def argmax_dev(self, x_ptr, rows, n, out_ptr):
+        self._check(lib().elmh_argmax_dev(self.h, C.c_void_p(x_ptr), C.c_int(rows), C.c_int64(n), C.c_void_p(out_ptr)))
+
     def memcpy_d2d(self, dst_ptr, src_ptr, nbytes):
         self._check(lib().elmh_memcpy_d2d(self.h, C.c_void_p(dst_ptr), C.c_void_p(src_ptr), C.c_size_t(nbytes)))
 

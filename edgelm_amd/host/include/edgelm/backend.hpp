@@ -63,6 +63,13 @@ class Backend {
   // replay it as a captured graph). Returning true means every op of the partition ran and the
   // host arena holds what other backends read, as after run().
   virtual bool run_partition(const Partition&, ExecContext&) { return false; }
+  // Optional (default: false = not handled), for greedy sampling: true means this backend produces
+  // the graph output and, until called again with true, leaves it where it computes it instead of
+  // copying it into the host arena; argmax_output() then answers for each forward.
+  virtual bool keep_output(bool) { return false; }
+  // Optional: the argmax (edgelm's argmax, tokenizer.cpp:187-189) of the graph output's last row,
+  // taken where the output lives; false if this backend cannot.
+  virtual bool argmax_output(const ExecContext&, int32_t*) { return false; }
 };
 
 std::unique_ptr<Backend> make_reference_backend();

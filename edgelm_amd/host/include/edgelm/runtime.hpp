@@ -52,6 +52,11 @@ class Session {
   const float* forward(const int32_t* tokens, int n);
   const float* prefill(const std::vector<int32_t>& tokens);
   const float* decode(int32_t token) { return forward(&token, 1); }
+  // Greedy next token after forward(tokens, n) / prefill(tokens): the argmax of the last row of
+  // logits, taken on the device by the output's backend when it offers argmax_output (the logits
+  // then stay there), else on the host arena's copy as edgelm's bench does (main.cpp:199-213).
+  int32_t greedy(const int32_t* tokens, int n);
+  int32_t greedy_prefill(const std::vector<int32_t>& tokens);
   void reset() { pos_ = 0; }
   int pos() const { return pos_; }
 
@@ -74,6 +79,7 @@ class Session {
   RopeTable rope_;
   ExecContext ctx_;
   int pos_ = 0;
+  Backend* output_backend_ = nullptr;  // backend of the op writing the graph output
 };
 
 int32_t argmax(const float* logits, int n);

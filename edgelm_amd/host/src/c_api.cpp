@@ -176,16 +176,16 @@ int elm_session_generate(elm_session* s, const int32_t* prompt, int n_prompt, in
                          double* ttft_ms, double* decode_ms, int32_t* tokens_out) {
   return guard([&] {
     Session& ss = *s->s;
-    const int V = ss.vocab();
     ss.reset();
     const auto t0 = std::chrono::steady_clock::now();
-    const float* lg = ss.prefill(std::vector<int32_t>(prompt, prompt + n_prompt));
+    // greedy steps take the argmax where the logits are (the device, for a hip output), so the
+    // prefill and the first argmax are timed together: both are in TTFT
+    int32_t tok = ss.greedy_prefill(std::vector<int32_t>(prompt, prompt + n_prompt));
     const auto t1 = std::chrono::steady_clock::now();
-    int32_t tok = argmax(lg, V);
-    const auto t2 = std::chrono::steady_clock::now();
+    const auto t2 = t1;
     if (tokens_out) tokens_out[0] = tok;
     for (int i = 0; i < gen; ++i) {
-      tok = argmax(ss.decode(tok), V);
+      tok = ss.greedy(&tok, 1);
       if (tokens_out) tokens_out[i + 1] = tok;
     }
     const auto t3 = std::chrono::steady_clock::now();

@@ -5,8 +5,8 @@
 //                 device) and LAST_ROWS;
 //   "hip-matmul"  the matmul family only (the cpu backend runs the rest).
 //
-// With prepare() (the optional hook this build's Backend adds; not virtual in edgelm's, where it is
-// simply never called) activations stay in HBM between consecutive hip ops: prepare() marks which
+// With prepare() (an optional hook this build's Backend adds; edgelm's Backend lacks it, so there it
+// is simply never called) activations stay in HBM between consecutive hip ops: prepare() marks which
 // activation tensors hip ops produce and which another backend reads or the graph outputs, and
 // run() uploads an input produced on the host once per forward, keeps every output on the device
 // and copies an output into the host arena only when the host needs it. Without prepare(), as
@@ -14,13 +14,15 @@
 // Either way the host has what it needs when run() returns (edgelm's contract: runtime.cpp:66-76).
 // Weights are uploaded to HBM once, on first use (matmul weights repacked; RMSNORM weights f32).
 //
-// run_partition() (the other optional hook) replays a decode step (T = 1) of a whole partition of
+// run_partition() (another optional hook) replays a decode step (T = 1) of a whole partition of
 // at least kMinGraphOps ops as one HIP graph: the first such step runs op by op (allocating
 // buffers and uploading weights), the second is captured, with attention reading the position
-// from device memory; every later step
-// uploads the host-side inputs (token ids) and the position, launches the graph, and copies back
-// what the host reads (the logits). A buffer that has to grow (a longer prefill) drops the graphs.
-// EDGELM_HIP_GRAPHS=0 turns graphs off.
+// from device memory; every later step uploads the host-side inputs (token ids) and the
+// position, launches the graph, and copies back what the host reads (the logits). A buffer that
+// has to grow (a longer prefill) drops the graphs. EDGELM_HIP_GRAPHS=0 turns graphs off.
+//
+// keep_output() and argmax_output() (the greedy-sampling hooks) leave the logits in HBM and hand
+// the host only the argmax of their last row.
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -60,6 +62,7 @@ class HipBackend : public Backend {
     }
     elmh_free(ctx_, rope_cos_);
     elmh_free(ctx_, rope_sin_);
+    elmh_free(ctx_, dev_tok_);
     elmh_destroy(ctx_);
   }
 
@@ -105,6 +108,7 @@ class HipBackend : public Backend {
         }
       }
     if (g.output >= 0) host_needed_[g.output] = 1;
+    output_ = g.output >= 0 && on_dev_[g.output] ? g.output : -1;
     act_.assign(nt, Buf{});
     first_op_ = -1;
     for (const Partition& p : parts)
@@ -149,7 +153,7 @@ class HipBackend : public Backend {
       throw std::runtime_error(std::string("edgelm: hip graph launch: ") + elmh_last_error(ctx_));
     for (int i = p.begin; i < p.end; ++i)
       for (int t : g.ops[i].out)
-        if (host_needed_[t] && elmh_memcpy_d2h(ctx_, c.f(t), act_[t].p, bytes(t, c)) != ELMH_OK)
+        if (to_host(t) && elmh_memcpy_d2h(ctx_, c.f(t), act_[t].p, bytes(t, c)) != ELMH_OK)
           throw std::runtime_error(std::string("edgelm: hip download: ") + elmh_last_error(ctx_));
     return true;
   }
@@ -216,11 +220,28 @@ class HipBackend : public Backend {
     }
     if (capturing_) return;  // the replay copies host-needed outputs after the launch
     for (int t : op.out)
-      if (host_needed_[t]) check(elmh_memcpy_d2h(ctx_, c.f(t), act_[t].p, bytes(t, c)), op);
+      if (to_host(t)) check(elmh_memcpy_d2h(ctx_, c.f(t), act_[t].p, bytes(t, c)), op);
     if (!prepared_) ++epoch_;  // no residency: every op uploads its inputs afresh
   }
 
+  // greedy sampling: the logits stay in HBM and only the token id crosses to the host
+  bool keep_output(bool on) {  // overrides where Backend declares it
+    keep_out_ = on && ctx_ && prepared_ && output_ >= 0;
+    return keep_out_;
+  }
+  bool argmax_output(const ExecContext& c, int32_t* tok) {  // overrides where Backend declares it
+    if (!keep_out_ || !act_[output_].p) return false;
+    if (!dev_tok_ && elmh_malloc(ctx_, sizeof(int32_t), reinterpret_cast<void**>(&dev_tok_)) != ELMH_OK)
+      throw std::runtime_error(std::string("edgelm: hip argmax: ") + elmh_last_error(ctx_));
+    const int64_t V = c.tensor(output_).cols, rows = c.rows(output_);
+    const float* last = static_cast<const float*>(act_[output_].p) + (rows - 1) * V;
+    if (elmh_argmax_dev(ctx_, last, 1, V, dev_tok_) != ELMH_OK || elmh_memcpy_d2h(ctx_, tok, dev_tok_, sizeof(int32_t)) != ELMH_OK)
+      throw std::runtime_error(std::string("edgelm: hip argmax: ") + elmh_last_error(ctx_));
+    return true;
+  }
+
  private:
+  bool to_host(int t) const { return host_needed_[t] && !(keep_out_ && t == output_); }
   struct Buf {
     void* p = nullptr;
     size_t cap = 0;
@@ -401,6 +422,9 @@ class HipBackend : public Backend {
   int first_op_ = -1;
   uint64_t epoch_ = 0;
   std::vector<char> on_dev_, host_needed_;
+  int output_ = -1;          // graph output when this backend writes it (prepare), else -1
+  bool keep_out_ = false;    // keep_output(true): the output is not copied to the host arena
+  int32_t* dev_tok_ = nullptr;  // argmax result
   std::vector<Buf> act_;
   std::vector<Layer> kv_;
   float* rope_cos_ = nullptr;

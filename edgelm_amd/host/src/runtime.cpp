@@ -23,6 +23,10 @@ Session::Session(const Model& model, SessionOptions opt) : model_(model), opt_(s
   for (auto& b : backends_) pref.push_back(b.get());
   parts_ = partition_graph(graph_, pref);
   for (auto& b : backends_) b->prepare(graph_, parts_);
+  for (const Partition& p : parts_)
+    for (int i = p.begin; i < p.end; ++i)
+      for (int t : graph_.ops[i].out)
+        if (t == graph_.output) output_backend_ = p.backend;
 
   const int L = opt_.all_logits ? opt_.max_batch : 1;
   plan_ = plan_memory(graph_, opt_.max_batch, L);
@@ -69,6 +73,31 @@ const float* Session::prefill(const std::vector<int32_t>& tokens) {
     out = forward(tokens.data() + i, n);
   }
   return out;
+}
+
+int32_t Session::greedy(const int32_t* tokens, int n) {
+  Backend* b = output_backend_;
+  const bool on_dev = b && b->keep_output(true);
+  const float* lg = nullptr;
+  int32_t tok = 0;
+  try {
+    lg = forward(tokens, n);
+    if (on_dev && !b->argmax_output(ctx_, &tok)) EDGELM_CHECK(false, "greedy: the output's backend lost its logits");
+  } catch (...) {
+    if (b) b->keep_output(false);
+    throw;
+  }
+  if (b) b->keep_output(false);
+  if (!on_dev) tok = argmax(lg + static_cast<size_t>(ctx_.L - 1) * static_cast<size_t>(vocab()), vocab());
+  return tok;
+}
+
+int32_t Session::greedy_prefill(const std::vector<int32_t>& tokens) {
+  EDGELM_CHECK(!tokens.empty(), "prefill: empty prompt");
+  const size_t mb = static_cast<size_t>(opt_.max_batch);
+  const size_t last = (tokens.size() - 1) / mb * mb;  // start of the final chunk
+  if (last) prefill(std::vector<int32_t>(tokens.begin(), tokens.begin() + static_cast<std::ptrdiff_t>(last)));
+  return greedy(tokens.data() + last, static_cast<int>(tokens.size() - last));
 }
 
 int32_t argmax(const float* logits, int n) {

@@ -48,7 +48,9 @@ int elm_session_pos(const elm_session* s);
 int elm_session_describe(const elm_session* s, char* buf, int cap);
 /* edgelm's bench protocol (main.cpp:173-233) on one session: reset, prefill the prompt, argmax
  * (TTFT), then gen greedy decode steps. Writes prefill ms, TTFT ms, decode ms and the gen + 1
- * generated token ids (first one from the prefill). */
+ * generated token ids (first one from the prefill). Each argmax is taken where the logits are
+ * (Session::greedy: on the device when a hip backend writes them), so the first one is part of the
+ * prefill's last step and prefill ms equals TTFT ms. */
 int elm_session_generate(elm_session* s, const int32_t* prompt, int n_prompt, int gen, double* prefill_ms,
                          double* ttft_ms, double* decode_ms, int32_t* tokens_out);
 

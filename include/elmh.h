@@ -134,6 +134,12 @@ int elmh_attention_step_dev(elmh_ctx* ctx, const float* q, const float* k, const
                             const int32_t* pos_dev, int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache,
                             int max_ctx, const float* rope_cos, const float* rope_sin);
 
+/* Greedy sampling: argmax (tokenizer.cpp:187-189, std::max_element) of each row of x [rows, n]
+ * (device pointers) into out [rows] (device int32): the first index of the largest value under
+ * IEEE <, so NaNs after index 0 are never chosen and a NaN at index 0 is. Lets a caller take the
+ * next token without copying the logits off the device. n >= 1. */
+int elmh_argmax_dev(elmh_ctx* ctx, const float* x, int rows, int64_t n, int32_t* out);
+
 /* ---- test hooks ----
  * quantize_act_row on the device (host pointers; q [T,K], d [T,K/32]). */
 int elmh_quantize_act(elmh_ctx* ctx, const float* x, int T, int64_t K, int8_t* q, float* d);

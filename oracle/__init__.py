@@ -50,6 +50,7 @@ def orc():
         _orc.orc_round_away.argtypes = [C.c_float]
         _orc.orc_silu.restype = C.c_float
         _orc.orc_silu.argtypes = [C.c_float]
+        _orc.orc_argmax.restype = C.c_int32
     return _orc
 
 
@@ -412,3 +413,15 @@ class RefSession:
             self.close()
         except Exception:
             pass
+
+
+def argmax(x):
+    """argmax of each row of x (tokenizer.cpp:187-189, restated in orc_argmax)."""
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    return np.array([orc().orc_argmax(_ptr(r), _I64(x.shape[1])) for r in x], np.int32)
+
+
+def rq_argmax(x):
+    """edgelm's own argmax (oracle/_ref) on each row of x."""
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    return np.array([ref().eref_argmax(_ptr(r), C.c_int(x.shape[1])) for r in x], np.int32)

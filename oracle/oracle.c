@@ -494,3 +494,12 @@ void orc_attention(const float* q, const float* k, const float* v, float* out, i
   free(qbuf);
   free(sc);
 }
+
+/* argmax (tokenizer.cpp:187-189): std::max_element over [x, x + n) keeps the current best unless
+ * best < candidate, scanning forward; restated as that scan. */
+int32_t orc_argmax(const float* x, int64_t n) {
+  int64_t best = 0;
+  for (int64_t i = 1; i < n; ++i)
+    if (x[best] < x[i]) best = i;
+  return (int32_t)best;
+}

@@ -78,6 +78,9 @@ void orc_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, fl
 void orc_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0, int n_heads, int n_kv,
                    int hd, float* kc, float* vc, int max_ctx, const float* rcos, const float* rsin);
 
+/* argmax (tokenizer.cpp:187-189): std::max_element's scan, the first index whose value no later
+ * value exceeds under IEEE <. */
+int32_t orc_argmax(const float* x, int64_t n);
 #ifdef __cplusplus
 }
 #endif

@@ -108,3 +108,32 @@ def test_smollm2_greedy_bit_identical_to_edgelm(smollm):
         t_mine, t_ref = int(np.argmax(a)), int(np.argmax(b))
     print(f"[gpu] greedy tokens {toks}", flush=True)
     mine.close(), ref.close()
+
+
+def ref_greedy(path, prompt, gen, max_batch, act_quant, max_ctx):
+    """edgelm's bench protocol on its own Session and its own argmax (tokenizer.cpp:187-189)."""
+    ref = O.RefSession(path, "cpu", threads=8, max_ctx=max_ctx, max_batch=max_batch, act_quant=act_quant)
+    lg = None
+    for i in range(0, len(prompt), max_batch):
+        lg = ref.forward(prompt[i:i + max_batch])
+    toks = [int(O.rq_argmax(lg[-1])[0])]
+    for _ in range(gen):
+        toks.append(int(O.rq_argmax(ref.forward(np.array([toks[-1]], np.int32))[-1])[0]))
+    ref.close()
+    return toks
+
+
+@pytest.mark.parametrize("backends", ["hip,cpu", "hip-matmul,cpu"])
+def test_generate_device_argmax_matches_edgelm(tiny, smollm, backends):
+    """Greedy generation with the argmax taken in HBM (Session::greedy, the logits never copied to
+    the host): the same tokens as edgelm's session and argmax, with a chunked prefill (7-token
+    chunks) on the tiny model and the configs[3] protocol on the SmolLM2-shaped model."""
+    cases = [(tiny["q4"], np.random.default_rng(9).integers(0, 320, 20).astype(np.int32), 8, 7, 64),
+             (smollm, F.lcg_prompt(128, 49152), 12, 128, 160)]
+    for path, prompt, gen, batch, mc in cases:
+        print(f"[gpu] generate {backends} {path.split('/')[-1]} batch={batch}", flush=True)
+        m = host.Model(path)
+        s = host.Session(m, backends, threads=8, max_ctx=mc, max_batch=batch, act_quant=True)
+        got = s.generate(prompt, gen)["tokens"].tolist()
+        s.close()
+        assert got == ref_greedy(path, prompt, gen, batch, True, mc)

@@ -118,3 +118,27 @@ def test_fill_and_copy(ctx):
     assert np.array_equal(c.download((1031,), np.uint8), want)
     b.free()
     c.free()
+
+
+def test_argmax_matches_edgelm(ctx):
+    """Greedy sampling on the device (argmax, tokenizer.cpp:187-189) against the oracle's
+    restatement of std::max_element: ties, signed zeros, NaNs at and after index 0, and row lengths
+    around the workgroup size and the SmolLM2 vocabulary."""
+    from test_oracle_layer import argmax_cases
+    r = np.random.default_rng(32)
+    rows = argmax_cases(r) + [r.normal(0, 1, n).astype(np.float32) for n in (1023, 1024, 1025, 100003)]
+    for x in rows:
+        print(f"[gpu] argmax n={x.size}", flush=True)
+        bx, bo = dev(ctx, x), ctx.buffer(4)
+        ctx.argmax_dev(bx.ptr, 1, x.size, bo.ptr)
+        assert int(bo.download((1,), np.int32)[0]) == int(O.argmax(x)[0])
+        bx.free()
+        bo.free()
+    x = r.normal(0, 1, (6, 49152)).astype(np.float32)
+    x[2, 17] = x[2].max()  # a tie with a later maximum
+    print("[gpu] argmax rows=6", flush=True)
+    bx, bo = dev(ctx, x), ctx.buffer(6 * 4)
+    ctx.argmax_dev(bx.ptr, 6, 49152, bo.ptr)
+    assert np.array_equal(bo.download((6,), np.int32), O.argmax(x))
+    bx.free()
+    bo.free()

@@ -106,3 +106,44 @@ def test_rmsnorm_and_rope_closed_forms():
     c, s = O.rope_table(HD, MC, 100000.0)
     assert np.all(c[0] == 1.0) and np.all(s[0] == 0.0)
     assert np.allclose(c.astype(np.float64) ** 2 + s.astype(np.float64) ** 2, 1.0, atol=1e-6)
+
+
+def argmax_cases(r):
+    """Rows that exercise std::max_element's rules: ties, signed zeros, NaNs at and after index 0."""
+    rows = [r.normal(0, 1, 49152).astype(np.float32), r.normal(0, 1, 1).astype(np.float32),
+            np.full(37, 2.5, np.float32), np.array([-0.0, 0.0, -0.0], np.float32),
+            np.array([0.0, -0.0], np.float32), np.array([-np.inf, -np.inf, -3.0, -np.inf], np.float32)]
+    x = r.normal(0, 1, 1000).astype(np.float32)
+    x[[5, 700]] = 9.0  # tie: the first wins
+    rows.append(x)
+    x = r.normal(0, 1, 1000).astype(np.float32)
+    x[0] = np.nan  # NaN at index 0: nothing compares greater, index 0 stays
+    x[3] = 50.0
+    rows.append(x)
+    x = r.normal(0, 1, 1000).astype(np.float32)
+    x[[1, 400, 999]] = np.nan  # later NaNs never replace the best
+    rows.append(x)
+    rows.append(np.array([1.0] + [np.nan] * 9, np.float32))
+    return rows
+
+
+def test_argmax_closed_forms():
+    r = np.random.default_rng(30)
+    rows = argmax_cases(r)
+    want = [None, 0, 0, 0, 0, 2, 5, 0, None, 0]
+    for x, w in zip(rows, want):
+        got = int(O.argmax(x)[0])
+        if w is not None:
+            assert got == w, (x[:8], got, w)
+        finite = x[~np.isnan(x)]
+        if x.size and not np.isnan(x[0]):
+            # NaN-free view: the first index of the maximum, as numpy's argmax defines it
+            assert x[got] == finite.max() and got == int(np.flatnonzero(x == finite.max())[0])
+
+
+@needs_ref
+def test_argmax_equals_reference_build():
+    r = np.random.default_rng(31)
+    for x in argmax_cases(r) + [r.normal(0, 3, (5, 4099)).astype(np.float32)]:
+        x = np.atleast_2d(x)
+        assert np.array_equal(O.argmax(x), O.rq_argmax(x))
