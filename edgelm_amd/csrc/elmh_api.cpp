@@ -682,6 +682,39 @@ int elmh_memcpy_d2h(elmh_ctx* c, void* dst, const void* src, size_t bytes) {
   return ELMH_OK;
 }
 
+int elmh_host_alloc(elmh_ctx* c, size_t bytes, void** ptr) {
+  if (!c || !ptr) return fail(c, ELMH_ERR_ARG, "null ctx/ptr");
+  *ptr = nullptr;
+  DeviceGuard g(c);
+  if (hipHostMalloc(ptr, std::max<size_t>(bytes, 64), hipHostMallocDefault) != hipSuccess)
+    return fail(c, ELMH_ERR_OOM, "hipHostMalloc(%zu) failed", bytes);
+  return ELMH_OK;
+}
+
+int elmh_host_free(elmh_ctx* c, void* ptr) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  if (!ptr) return ELMH_OK;
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, hipHostFree(ptr));
+  return ELMH_OK;
+}
+
+int elmh_memcpy_h2d_async(elmh_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  if (bytes && (!dst || !src)) return fail(c, ELMH_ERR_ARG, "null dst/src");
+  DeviceGuard g(c);
+  if (bytes) HIP_OR_FAIL(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+  return ELMH_OK;
+}
+
+int elmh_memcpy_d2h_async(elmh_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  if (bytes && (!dst || !src)) return fail(c, ELMH_ERR_ARG, "null dst/src");
+  DeviceGuard g(c);
+  if (bytes) HIP_OR_FAIL(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+  return ELMH_OK;
+}
+
 int elmh_memset_dev(elmh_ctx* c, void* dst, int value, size_t bytes) {
   if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
   if (bytes && !dst) return fail(c, ELMH_ERR_ARG, "null dst");

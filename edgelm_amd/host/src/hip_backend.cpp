@@ -63,6 +63,7 @@ class HipBackend : public Backend {
     elmh_free(ctx_, rope_cos_);
     elmh_free(ctx_, rope_sin_);
     elmh_free(ctx_, dev_tok_);
+    release_pins();
     elmh_destroy(ctx_);
   }
 
@@ -110,6 +111,8 @@ class HipBackend : public Backend {
     if (g.output >= 0) host_needed_[g.output] = 1;
     output_ = g.output >= 0 && on_dev_[g.output] ? g.output : -1;
     act_.assign(nt, Buf{});
+    release_pins();
+    pin_.assign(nt, Pin{});
     first_op_ = -1;
     for (const Partition& p : parts)
       if (p.backend == this && (first_op_ < 0 || p.begin < first_op_)) first_op_ = p.begin;
@@ -153,8 +156,8 @@ class HipBackend : public Backend {
       throw std::runtime_error(std::string("edgelm: hip graph launch: ") + elmh_last_error(ctx_));
     for (int i = p.begin; i < p.end; ++i)
       for (int t : g.ops[i].out)
-        if (to_host(t) && elmh_memcpy_d2h(ctx_, c.f(t), act_[t].p, bytes(t, c)) != ELMH_OK)
-          throw std::runtime_error(std::string("edgelm: hip download: ") + elmh_last_error(ctx_));
+        if (to_host(t)) download(t, c);
+    flush();
     return true;
   }
 
@@ -220,7 +223,8 @@ class HipBackend : public Backend {
     }
     if (capturing_) return;  // the replay copies host-needed outputs after the launch
     for (int t : op.out)
-      if (to_host(t)) check(elmh_memcpy_d2h(ctx_, c.f(t), act_[t].p, bytes(t, c)), op);
+      if (to_host(t)) download(t, c);
+    flush();
     if (!prepared_) ++epoch_;  // no residency: every op uploads its inputs afresh
   }
 
@@ -237,11 +241,80 @@ class HipBackend : public Backend {
     const float* last = static_cast<const float*>(act_[output_].p) + (rows - 1) * V;
     if (elmh_argmax_dev(ctx_, last, 1, V, dev_tok_) != ELMH_OK || elmh_memcpy_d2h(ctx_, tok, dev_tok_, sizeof(int32_t)) != ELMH_OK)
       throw std::runtime_error(std::string("edgelm: hip argmax: ") + elmh_last_error(ctx_));
+    synced();  // a synchronous copy: every earlier transfer has completed
     return true;
   }
 
  private:
   bool to_host(int t) const { return host_needed_[t] && !(keep_out_ && t == output_); }
+
+  // Host <-> device transfers of activations go through pinned staging buffers, one per tensor, as
+  // stream-ordered copies: an op's uploads, kernels and downloads are enqueued together and waited
+  // for once (flush). A staging buffer still used by a copy in flight is reused only after a wait.
+  struct Pin {
+    void* p = nullptr;
+    size_t cap = 0;
+    bool busy = false;  // an async copy may still read or write it
+  };
+  struct Download {
+    Pin* pin;
+    void* host;
+    size_t n;
+  };
+  void synced() {
+    for (Pin* b : busy_) b->busy = false;
+    busy_.clear();
+  }
+  void wait_all() {
+    if (busy_.empty()) return;
+    if (elmh_synchronize(ctx_) != ELMH_OK) throw std::runtime_error(std::string("edgelm: hip sync: ") + elmh_last_error(ctx_));
+    synced();
+  }
+  void* staging(Pin& b, size_t n) {
+    if (b.busy) wait_all();
+    if (n > b.cap) {
+      elmh_host_free(ctx_, b.p);
+      b.p = nullptr;
+      b.cap = 0;
+      if (elmh_host_alloc(ctx_, n, &b.p) != ELMH_OK)
+        throw std::runtime_error(std::string("edgelm: hip pinned staging: ") + elmh_last_error(ctx_));
+      b.cap = n;
+    }
+    return b.p;
+  }
+  void upload(Pin& b, void* dev, const void* host, size_t n) {
+    void* h = staging(b, n);
+    std::memcpy(h, host, n);
+    if (elmh_memcpy_h2d_async(ctx_, dev, h, n) != ELMH_OK)
+      throw std::runtime_error(std::string("edgelm: hip upload: ") + elmh_last_error(ctx_));
+    b.busy = true;
+    busy_.push_back(&b);
+  }
+  void download(int t, const ExecContext& c) {
+    const size_t n = bytes(t, c);
+    void* h = staging(pin_[t], n);
+    if (elmh_memcpy_d2h_async(ctx_, h, act_[t].p, n) != ELMH_OK)
+      throw std::runtime_error(std::string("edgelm: hip download: ") + elmh_last_error(ctx_));
+    pin_[t].busy = true;
+    busy_.push_back(&pin_[t]);
+    downs_.push_back({&pin_[t], c.f(t), n});
+  }
+  void flush() {  // wait for the enqueued downloads and move them into the host arena
+    if (downs_.empty()) return;
+    wait_all();
+    for (const Download& d : downs_) std::memcpy(d.host, d.pin->p, d.n);
+    downs_.clear();
+  }
+  void release_pins() {
+    if (!ctx_) return;
+    if (!busy_.empty()) elmh_synchronize(ctx_);
+    synced();
+    downs_.clear();
+    for (Pin& b : pin_) elmh_host_free(ctx_, b.p);
+    pin_.clear();
+    elmh_host_free(ctx_, pin_pos_.p);
+    pin_pos_ = Pin{};
+  }
   struct Buf {
     void* p = nullptr;
     size_t cap = 0;
@@ -284,16 +357,13 @@ class HipBackend : public Backend {
     const Graph& g = *c.graph;
     for (int i = p.begin; i < p.end; ++i)
       for (int t : g.ops[i].in)
-        if (!c.tensor(t).is_weight() && !on_dev_[t] &&
-            elmh_memcpy_h2d(ctx_, act_[t].p, c.f(t), bytes(t, c)) != ELMH_OK)
-          throw std::runtime_error(std::string("edgelm: hip upload: ") + elmh_last_error(ctx_));
+        if (!c.tensor(t).is_weight() && !on_dev_[t]) upload(pin_[t], act_[t].p, c.f(t), bytes(t, c));
     bool attn = false;
     for (int i = p.begin; i < p.end; ++i) attn = attn || g.ops[i].type == OpType::ATTENTION;
     if (!attn) return;
     if (!pos_dev_) pos_dev_ = static_cast<int32_t*>(alloc(sizeof(int32_t)));
     const int32_t pos = c.pos0;
-    if (elmh_memcpy_h2d(ctx_, pos_dev_, &pos, sizeof pos) != ELMH_OK)
-      throw std::runtime_error(std::string("edgelm: hip upload: ") + elmh_last_error(ctx_));
+    upload(pin_pos_, pos_dev_, &pos, sizeof pos);
   }
 
   // no prepare() call (an edgelm Session without the hook): nothing is known to be on the device
@@ -303,6 +373,8 @@ class HipBackend : public Backend {
     on_dev_.assign(g.tensors.size(), 0);
     host_needed_.assign(g.tensors.size(), 1);
     act_.assign(g.tensors.size(), Buf{});
+    release_pins();
+    pin_.assign(g.tensors.size(), Pin{});
     first_op_ = -1;
   }
 
@@ -344,8 +416,7 @@ class HipBackend : public Backend {
   const float* in(int t, const ExecContext& c) {
     float* p = buffer(t, c);
     if (!on_dev_[t] && !capturing_ && act_[t].epoch != epoch_) {
-      if (elmh_memcpy_h2d(ctx_, p, c.f(t), bytes(t, c)) != ELMH_OK)
-        throw std::runtime_error(std::string("edgelm: hip upload of ") + c.tensor(t).name + ": " + elmh_last_error(ctx_));
+      upload(pin_[t], p, c.f(t), bytes(t, c));
       act_[t].epoch = epoch_;
     }
     return p;
@@ -425,6 +496,10 @@ class HipBackend : public Backend {
   int output_ = -1;          // graph output when this backend writes it (prepare), else -1
   bool keep_out_ = false;    // keep_output(true): the output is not copied to the host arena
   int32_t* dev_tok_ = nullptr;  // argmax result
+  std::vector<Pin> pin_;           // staging per activation tensor
+  Pin pin_pos_;                    // staging of the decode position
+  std::vector<Pin*> busy_;         // staging buffers of copies in flight
+  std::vector<Download> downs_;    // downloads awaiting flush()
   std::vector<Buf> act_;
   std::vector<Layer> kv_;
   float* rope_cos_ = nullptr;

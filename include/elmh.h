@@ -152,6 +152,16 @@ int elmh_malloc(elmh_ctx* ctx, size_t bytes, void** dptr);
 int elmh_free(elmh_ctx* ctx, void* dptr);
 int elmh_memcpy_h2d(elmh_ctx* ctx, void* dst, const void* src, size_t bytes);
 int elmh_memcpy_d2h(elmh_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Pinned host memory and stream-ordered copies, for a caller that moves activations between its
+ * host arena and the device at every op (edgelm's Session hands backends host pointers op by op,
+ * runtime.cpp:66-76): staged through pinned memory, an op's uploads, kernels and downloads are
+ * enqueued together and waited for once (elmh_synchronize). An async copy returns once enqueued;
+ * its host buffer must stay untouched, and its destination unread, until elmh_synchronize. No
+ * counterpart in edgelm. */
+int elmh_host_alloc(elmh_ctx* ctx, size_t bytes, void** ptr);
+int elmh_host_free(elmh_ctx* ctx, void* ptr);
+int elmh_memcpy_h2d_async(elmh_ctx* ctx, void* dst, const void* src, size_t bytes);
+int elmh_memcpy_d2h_async(elmh_ctx* ctx, void* dst, const void* src, size_t bytes);
 /* Device fill (a kernel, so it may be captured in a HIP graph) and device-to-device copy; both
  * asynchronous on the context stream. LAST_ROWS (backends.cpp, reference) is one such copy. */
 int elmh_memset_dev(elmh_ctx* ctx, void* dst, int value, size_t bytes);
