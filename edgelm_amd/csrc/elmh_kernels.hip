@@ -1078,6 +1078,205 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
     store_tiles(std::false_type{});
 }
 
+// ---------------------------------------------------------------- int8 MFMA GEMM, small problems
+//
+// For GEMMs too small to give the LDS-ring kernel enough workgroups (SmolLM2-sized prefill: 576 to
+// 1536 rows at T = 128 are 5 to 24 ring workgroups on 256 CUs), every wave owns one 32-token x
+// 32-row output tile on its own: 4 independent waves per workgroup, no LDS ring and no barriers.
+// Each lane loads its MFMA operands straight into registers (the activation fragment's 16 bytes,
+// its weight row's 16 bytes of the block, the block scales), kWaveDepth blocks ahead, and the
+// per-block int32 sums are rescaled in block order exactly as in the ring kernel, so both give
+// the same bits. Waves sharing a token group or a row group share their operands through L2.
+constexpr int kWaveDepth = 4;
+constexpr int kWaveTile = 32;
+
+template <int WDT, bool SW, bool TOK>
+struct WaveOps {
+  static constexpr int NSEL = SW ? 2 : 1;
+  static constexpr bool BLOCKX = !TOK;
+  v4i A;
+  v4i B[NSEL];
+  float c[NSEL];                // q4: ws / 16 of the lane's row and block
+  float xv[BLOCKX ? 16 : 1];    // block scales of the lane's 16 tokens
+};
+
+template <int WDT, bool SW, bool TOK, bool FAST, int DEPTH = kWaveDepth>
+__global__ __launch_bounds__(256) void gemm_wave_kernel(const GemmArgs a) {
+  typedef WaveOps<WDT, SW, TOK> Ops;
+  constexpr int NSEL = Ops::NSEL;
+  constexpr bool BLOCKX = Ops::BLOCKX;
+  __shared__ __align__(16) float ep_all[SW ? 4 * 2 * 32 * 32 : 4];
+  __shared__ float xdt_all[TOK ? 4 * 32 : 4];
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int nb = a.nb, H = a.H;
+  const int ngroups = (a.T + kWaveTile - 1) / kWaveTile;
+  // wave -> (target, 32-row tile, token group), token group fastest
+  int rt = (int)blockIdx.x * 4 + wave;
+  const int g = rt % ngroups;
+  rt /= ngroups;
+  int ti = 0;
+  const int n = SW ? 1 : a.n_targets;
+  for (; ti < n; ++ti) {
+    const int c = (a.tg[ti].N + kWaveTile - 1) / kWaveTile;
+    if (rt < c) break;
+    rt -= c;
+  }
+  if (ti >= n) return;  // past the last tile (uniform per wave; no barrier below)
+  const GemmTarget tg = SW ? a.tg[0] : gemm_target_at(ti);
+  const int r0 = rt * kWaveTile, t0 = g * kWaveTile;
+  const int rows_pad = (tg.N + kPadRows - 1) / kPadRows * kPadRows;
+  const int wrow = min(r0 + l32, rows_pad - 1);
+  const int64_t rbase = (int64_t)(wrow / H) * nb * H + (wrow % H);  // item of (wrow, block 0)
+  const uint8_t* const wd[2] = {tg.data, SW ? a.tg[1].data : tg.data};
+  const float* const wsc[2] = {tg.scales, SW ? a.tg[1].scales : tg.scales};
+  const int8_t* const xg = a.xq + (int64_t)g * nb * 1024 + lane * 16;
+
+  auto load = [&](int blk, Ops& o) {
+    blk = min(blk, nb - 1);
+    o.A = *reinterpret_cast<const v4i*>(xg + (int64_t)blk * 1024);
+    const int64_t it = rbase + (int64_t)blk * H;
+#pragma unroll
+    for (int s = 0; s < NSEL; ++s) {
+      if (WDT == WQ8) {
+        o.B[s] = *reinterpret_cast<const v4i*>(wd[s] + it * 32 + h * 16);
+        o.c[s] = 1.f;
+      } else {
+        o.B[s] = q4_operand16(*reinterpret_cast<const uint4*>(wd[s] + it * 16), h);
+        o.c[s] = wsc[s][it];
+      }
+    }
+    if (BLOCKX) {
+      const float* xs = a.xd + (int64_t)blk * a.Tpad + t0 + 4 * h;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 x4 = *reinterpret_cast<const float4*>(xs + 8 * q);
+        o.xv[4 * q] = x4.x;
+        o.xv[4 * q + 1] = x4.y;
+        o.xv[4 * q + 2] = x4.z;
+        o.xv[4 * q + 3] = x4.w;
+      }
+    }
+  };
+
+  v16i iacc[NSEL];
+  float facc[NSEL][16];
+  v16i zero;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) zero[i] = 0;
+#pragma unroll
+  for (int s = 0; s < NSEL; ++s) {
+    iacc[s] = zero;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) facc[s][i] = 0.f;
+  }
+  // the int32 sums of a block; the rescale then folds them in block order
+  auto sums = [&](const Ops& o, v16i (&S)[NSEL]) {
+#pragma unroll
+    for (int s = 0; s < NSEL; ++s) S[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.A, o.B[s], zero, 0, 0, 0);
+  };
+  auto rescale = [&](const Ops& o, const v16i (&S)[NSEL]) {
+#pragma unroll
+    for (int s = 0; s < NSEL; ++s)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        // q8: p = float(S) * xd; q4 (S = 16 * S_b, c = ws / 16): p = float(S) * (c * xd)
+        const float m = WDT == WQ8 ? o.xv[BLOCKX ? i : 0] : BLOCKX ? o.c[s] * o.xv[i] : o.c[s];
+        if (FAST) {
+          facc[s][i] = __builtin_fmaf((float)S[s][i], m, facc[s][i]);
+        } else {
+          facc[s][i] = facc[s][i] + (float)S[s][i] * m;
+        }
+      }
+  };
+
+  // DEPTH register sets; block b lives in set b % DEPTH (named by the unrolled index). A group's
+  // MFMAs are issued back to back (they do not depend on one another's rescale), then rescaled in
+  // block order; blocks past the last are neither accumulated nor rescaled (uniform branches).
+  Ops ops[DEPTH];
+#pragma unroll
+  for (int k = 0; k < DEPTH; ++k) load(k, ops[k]);
+  for (int b0 = 0; b0 < nb; b0 += DEPTH) {
+    if (TOK && WDT == WQ8) {
+#pragma unroll
+      for (int k = 0; k < DEPTH; ++k) {
+        if (b0 + k < nb)
+#pragma unroll
+          for (int s = 0; s < NSEL; ++s) iacc[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ops[k].A, ops[k].B[s], iacc[s], 0, 0, 0);
+        load(b0 + k + DEPTH, ops[k]);  // unconditional (clamped): exact wait counts
+      }
+    } else {
+      v16i S[DEPTH][NSEL];
+#pragma unroll
+      for (int k = 0; k < DEPTH; ++k) sums(ops[k], S[k]);
+#pragma unroll
+      for (int k = 0; k < DEPTH; ++k) {
+        if (b0 + k < nb) rescale(ops[k], S[k]);
+        load(b0 + k + DEPTH, ops[k]);
+      }
+    }
+  }
+
+  // epilogue: row r0 + l32 (lane), tokens t0 + 8 (i / 4) + 4 h + i % 4 (accumulator i)
+  const int r = r0 + l32;
+  const int rc = min(r, tg.N - 1);
+  const int tv = min(kWaveTile, a.T - t0);
+  const uint32_t tbytes = (uint32_t)tv * (uint32_t)tg.N * 4u;
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(tg.y + (int64_t)t0 * tg.N, (short)0, (int)tbytes, 0x00020000);
+  const int tb = 4 * h;
+  float xt[16];
+  if (TOK) {
+    float* xdt = xdt_all + wave * 32;
+    if (lane < 32) xdt[lane] = a.xd[t0 + lane];
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xt[i] = xdt[tb + 8 * (i >> 2) + (i & 3)];
+  }
+  auto value = [&](int s, int i, float ws) {
+    if (WDT == WQ8) return TOK ? ((float)iacc[s][i] * xt[i]) * ws : facc[s][i] * ws;
+    return TOK ? facc[s][i] * xt[i] : facc[s][i];
+  };
+  if (SW) {
+    // gate and up through this wave's LDS slice, so that silu (an expf) is emitted once in a loop
+    float* const ep = ep_all + wave * (2 * 32 * 32);
+    const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
+    const float wsu = WDT == WQ8 ? a.tg[1].scales[rc] : 1.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      ep[i * 64 + lane] = value(0, i, ws);
+      ep[1024 + i * 64 + lane] = value(NSEL - 1, i, wsu);
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll 1
+    for (int i = 0; i < 16; ++i) {
+      const int t = tb + 8 * (i >> 2) + (i & 3);
+      const float out = silu_exact(ep[i * 64 + lane]) * ep[1024 + i * 64 + lane];
+      const int off = r < tg.N ? (t * tg.N + r) * 4 : 0x7FFFFFF0;
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), ry, off, 0, 0);
+    }
+    return;
+  }
+  const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
+  const bool has_res = tg.res != nullptr;
+  const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(has_res ? tg.res + (int64_t)t0 * tg.N : tg.y), (short)0, has_res ? (int)tbytes : 0, 0x00020000);
+  float res[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int t = tb + 8 * (i >> 2) + (i & 3);
+    const int off = r < tg.N ? (t * tg.N + r) * 4 : 0x7FFFFFF0;
+    res[i] = has_res ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, off, 0, 0)) : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int t = tb + 8 * (i >> 2) + (i & 3);
+    const int off = r < tg.N ? (t * tg.N + r) * 4 : 0x7FFFFFF0;
+    float out = value(0, i, ws);
+    if (has_res) out = out + res[i];
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), ry, off, 0, 0);
+  }
+}
+
 // ---------------------------------------------------------------- f32-activation paths
 
 // T == 1 (kernels_cpu.cpp:366-368, 397-399 with dot_row): one lane per weight row.
@@ -1421,6 +1620,18 @@ static void gemm_launch(const GemmArgs& a, dim3 grid, hipStream_t s) {
 }
 
 template <int WDT, bool SW, bool TOK>
+static void gemm_wave_launch(const GemmArgs& a, hipStream_t s) {
+  int rows = 0;
+  for (int i = 0; i < (SW ? 1 : a.n_targets); ++i) rows += (a.tg[i].N + kWaveTile - 1) / kWaveTile;
+  const int waves = rows * ((a.T + kWaveTile - 1) / kWaveTile);
+  const dim3 grid((waves + 3) / 4);
+  if (a.fast && !(TOK && WDT == WQ8))
+    gemm_wave_kernel<WDT, SW, TOK, true><<<grid, 256, 0, s>>>(a);
+  else
+    gemm_wave_kernel<WDT, SW, TOK, false><<<grid, 256, 0, s>>>(a);
+}
+
+template <int WDT, bool SW, bool TOK>
 static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
   if (a.Tpad % kGemmTileT || a.T < 1 || a.T > a.Tpad || tiles < 1 ||
       tiles != (SW ? a.tg[0].ntiles : a.tile_start[a.n_targets]))
@@ -1438,8 +1649,19 @@ static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
   // min(TT, T - t0) >= 1 tokens)
   const int t128 = tiles * ((a.T + 127) / 128), t64 = tiles * ((a.T + 63) / 64);
   bool small = t128 < cus;
-  // ELMH_GEMM_TOKEN_TILE=64 or 128 forces one tile height (both give the same bits)
-  if (const char* ev = getenv("ELMH_GEMM_TOKEN_TILE")) small = ev[0] == '6' ? true : ev[0] == '1' ? false : small;
+  // problems that give the ring kernel fewer workgroups than half the CUs: one wave per 32 x 32 tile
+  bool wave = t64 < cus / 2;
+  // ELMH_GEMM_TOKEN_TILE=64 or 128 forces the ring kernel with one tile height; ELMH_GEMM_KERNEL=wave
+  // or ring forces the kernel (all give the same bits)
+  if (const char* ev = getenv("ELMH_GEMM_TOKEN_TILE")) {
+    small = ev[0] == '6' ? true : ev[0] == '1' ? false : small;
+    wave = false;
+  }
+  if (const char* ev = getenv("ELMH_GEMM_KERNEL")) wave = ev[0] == 'w' ? true : ev[0] == 'r' ? false : wave;
+  if (wave) {
+    gemm_wave_launch<WDT, SW, TOK>(a, s);
+    return hipGetLastError();
+  }
   if (small)
     gemm_launch<WDT, SW, TOK, 1>(a, dim3((t64 + 7) / 8 * 8), s);
   else

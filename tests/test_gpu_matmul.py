@@ -326,6 +326,38 @@ def test_gemm_token_tiles(ctx, dt, tile, monkeypatch):
         d.free()
 
 
+@pytest.mark.parametrize("kernel", ["wave", "ring"])
+@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
+def test_gemm_kernels_small_and_ragged(ctx, dt, kernel, monkeypatch):
+    """Both GEMM kernels forced (ELMH_GEMM_KERNEL): the one-wave-per-32x32-tile kernel that small
+    problems select, and the LDS-ring kernel. Ragged rows and tokens (partial 32-row and 32-token
+    tiles), MATMUL_N with a residual, FFN_SWIGLU, per-block exact and fast, per-token, and an odd
+    block count."""
+    monkeypatch.setenv("ELMH_GEMM_KERNEL", kernel)
+    r = rng(700 + dt)
+    for n, n2, k in [(300, 40, 576), (70, 33, 1568)]:
+        w, w2 = weight(r, n, k, dt), weight(r, n2, k, dt)
+        wg, wu = weight(r, n, k, dt), weight(r, n, k, dt)
+        dw, dw2, dg, du = up(ctx, w), up(ctx, w2), up(ctx, wg), up(ctx, wu)
+        for T in [5, 33, 128, 130]:
+            print(f"[gpu] gemm kernel={kernel} dt={dt} {n}x{k} T={T}", flush=True)
+            x = r.normal(0, 1, (T, k)).astype(np.float32)
+            res = r.normal(0, 1, (T, n)).astype(np.float32)
+            got = ctx.matmul(x, [dw, dw2], [res, None], act=E.ACT_INT8, mode=E.EXACT)
+            want = O.cpu_matmul(x, [w, w2], [res, None], act_quant=True)
+            assert bits_equal(got[0], want[0]) and bits_equal(got[1], want[1])
+            fast = ctx.matmul(x, [dw], None, act=E.ACT_INT8, mode=E.FAST)[0]
+            assert rel_err(fast, O.cpu_matmul(x, [w], None, act_quant=True)[0]) < 1e-5
+            assert bits_equal(ctx.swiglu(x, dg, du, act=E.ACT_INT8), O.cpu_swiglu(x, wg, wu, act_quant=True))
+            tok = ctx.matmul(x, [dw, dw2], [res, None], act=E.ACT_INT8_TOKEN)
+            assert bits_equal(tok[0], O.matmul_a8_token(x, w, res)) and bits_equal(tok[1], O.matmul_a8_token(x, w2))
+            g, u = O.matmul_a8_token(x, wg), O.matmul_a8_token(x, wu)
+            want_sw = np.array([O.silu(float(v)) for v in g.ravel()], np.float32).reshape(g.shape) * u
+            assert bits_equal(ctx.swiglu(x, dg, du, act=E.ACT_INT8_TOKEN), want_sw)
+        for d in (dw, dw2, dg, du):
+            d.free()
+
+
 @pytest.mark.parametrize("tile", ["64", "128"])
 def test_gemm_token_odd_block_count(ctx, tile, monkeypatch):
     """Per-token q8 GEMM at K = 1568 (49 blocks): the last group of 4 (64-token tiles) or 2
