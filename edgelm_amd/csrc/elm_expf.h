@@ -1,9 +1,8 @@
 // expf restated from the published ARM optimized-routines method (Szabolcs Nagy, 2017; the
 // algorithm glibc >= 2.28 ships as expf): 2^(k/32) from a 32-entry table times a cubic in the
 // reduced argument, all in double precision, with the FMA contraction glibc's x86-64 FMA build
-// uses. The table entries are 2^(i/32) correctly rounded to double, minus (i << 47), computed
-// independently. Verified identical to the host libm's expf on all 2^32 inputs; edgelm's
-// silu (kernels_cpu.cpp:292) calls that expf, so device SwiGLU epilogues reproduce it bit for bit.
+// uses. Verified identical to the host libm's expf on all 2^32 inputs; edgelm's silu
+// (kernels_cpu.cpp:292) calls that expf, so device SwiGLU epilogues reproduce it bit for bit.
 #pragma once
 #include <stdint.h>
 
@@ -27,26 +26,31 @@ ELM_HOSTDEV static inline uint32_t elm_f2u(float f) {
   return v.u;
 }
 
+// Table entry i of the method: the bits of 2^(i/32) correctly rounded to double, minus (i << 47).
+// Computed without a table or a branch, so that lanes of one wave with different i do not split
+// into 32 paths: 2^(i/32) = sqrt(2) * e^(t ln2 / 32) with t = i - 16, by a degree-13 Taylor
+// polynomial (c_n = sqrt(2) (ln2/32)^n / n!, rounded to double) in Horner form with FMA. Over
+// the 32 values of i the result is either the correctly rounded value or one ulp above it; bit i
+// of kElmExp2Fix marks the latter. The exhaustive expf test covers every entry.
 ELM_HOSTDEV static inline uint64_t elm_exp2_tab(uint32_t i) {
-  // switch instead of a table in memory: the value is selected without a data load.
-  switch (i & 31) {
-    case 0: return 0x3ff0000000000000ull;  case 1: return 0x3fefd9b0d3158574ull;
-    case 2: return 0x3fefb5586cf9890full;  case 3: return 0x3fef9301d0125b51ull;
-    case 4: return 0x3fef72b83c7d517bull;  case 5: return 0x3fef54873168b9aaull;
-    case 6: return 0x3fef387a6e756238ull;  case 7: return 0x3fef1e9df51fdee1ull;
-    case 8: return 0x3fef06fe0a31b715ull;  case 9: return 0x3feef1a7373aa9cbull;
-    case 10: return 0x3feedea64c123422ull; case 11: return 0x3feece086061892dull;
-    case 12: return 0x3feebfdad5362a27ull; case 13: return 0x3feeb42b569d4f82ull;
-    case 14: return 0x3feeab07dd485429ull; case 15: return 0x3feea47eb03a5585ull;
-    case 16: return 0x3feea09e667f3bcdull; case 17: return 0x3fee9f75e8ec5f74ull;
-    case 18: return 0x3feea11473eb0187ull; case 19: return 0x3feea589994cce13ull;
-    case 20: return 0x3feeace5422aa0dbull; case 21: return 0x3feeb737b0cdc5e5ull;
-    case 22: return 0x3feec49182a3f090ull; case 23: return 0x3feed503b23e255dull;
-    case 24: return 0x3feee89f995ad3adull; case 25: return 0x3feeff76f2fb5e47ull;
-    case 26: return 0x3fef199bdd85529cull; case 27: return 0x3fef3720dcef9069ull;
-    case 28: return 0x3fef5818dcfba487ull; case 29: return 0x3fef7c97337b9b5full;
-    case 30: return 0x3fefa4afa2a490daull; default: return 0x3fefd0765b6e4540ull;
-  }
+  const uint32_t kElmExp2Fix = 0x915055e4u;
+  i &= 31;
+  const double t = (double)(int)i - 16.0;
+  double y = 0x1.108170a304abp-104;
+  y = __builtin_fma(y, t, 0x1.3f6da49237698p-95);
+  y = __builtin_fma(y, t, 0x1.59a0d25f61fc7p-86);
+  y = __builtin_fma(y, t, 0x1.56cff45438d97p-77);
+  y = __builtin_fma(y, t, 0x1.351bc8299ee8fp-68);
+  y = __builtin_fma(y, t, 0x1.f5b1687066adap-60);
+  y = __builtin_fma(y, t, 0x1.69e51ed115674p-51);
+  y = __builtin_fma(y, t, 0x1.c8d752e2475fdp-43);
+  y = __builtin_fma(y, t, 0x1.ee4fd234aabe3p-35);
+  y = __builtin_fma(y, t, 0x1.bdb696e8a0afcp-27);
+  y = __builtin_fma(y, t, 0x1.41839eb881562p-19);
+  y = __builtin_fma(y, t, 0x1.5be298adf0352p-12);
+  y = __builtin_fma(y, t, 0x1.f5e46537ab907p-6);
+  y = __builtin_fma(y, t, 0x1.6a09e667f3bcdp+0);
+  return elm_d2u(y) - ((kElmExp2Fix >> i) & 1u) - ((uint64_t)i << 47);
 }
 
 ELM_HOSTDEV static inline float elm_expf(float x) {

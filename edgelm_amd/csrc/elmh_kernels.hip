@@ -257,41 +257,12 @@ __device__ __forceinline__ float item_product(const v4u w0, const v4u w1, float 
   return (float)S * (wsc * xd);
 }
 
-// Sequential block-order fold of one LDS row of products. The next 32 values are read while the
-// current 32 are added, so long rows (448 blocks at K = 14336) keep the add chain fed: the chain
-// (one dependent add per block) is the latency that is left after the last weight has arrived.
+// Four block-order adds into one accumulator (no reassociation).
 __device__ __forceinline__ void add4(float& acc, const float4 v) {
   acc = acc + v.x;
   acc = acc + v.y;
   acc = acc + v.z;
   acc = acc + v.w;
-}
-
-__device__ __forceinline__ float fold_row(const float* row, int nb) {
-  constexpr int D = 8;  // float4 values in flight
-  const float4* pv = reinterpret_cast<const float4*>(row);
-  float acc = 0.f;
-  const int nq = nb >> 2;
-  int q = 0;
-  if (nq >= D) {
-    float4 c[D];
-#pragma unroll
-    for (int i = 0; i < D; ++i) c[i] = pv[i];
-    for (q = D; q + D <= nq; q += D) {
-      float4 n[D];
-#pragma unroll
-      for (int i = 0; i < D; ++i) n[i] = pv[q + i];
-#pragma unroll
-      for (int i = 0; i < D; ++i) add4(acc, c[i]);
-#pragma unroll
-      for (int i = 0; i < D; ++i) c[i] = n[i];
-    }
-#pragma unroll
-    for (int i = 0; i < D; ++i) add4(acc, c[i]);
-  }
-  for (; q < nq; ++q) add4(acc, pv[q]);
-  for (int b = nq * 4; b < nb; ++b) acc = acc + row[b];
-  return acc;
 }
 
 struct GemvLds {
@@ -314,34 +285,105 @@ __device__ __forceinline__ GemvLds gemv_lds(unsigned char* smem, int K, int nb) 
   return L;
 }
 
-// Last phase of both GEMV kernels: lane tid < T*R folds row (tid % R) of token (tid / R), where
-// the workgroup's R rows start at weight row n0, and applies the epilogue.
-template <int WDT, int NT, bool SW>
-__device__ __forceinline__ void gemv_fold(const GemvArgs& a, const GemvLds& L, const GemvTarget& tg, int n0, int R,
-                                          int rows, int tid, float e_res, float e_s, float e_su) {
-  const int ft = tid / R, fr = tid - ft * R;
-  const int fn = n0 + fr;
-  if (tid >= a.T * R || fr >= rows || fn >= tg.N) return;
-  float out = fold_row(L.p + (ft * R + fr) * L.pst, a.nb);
-  out = WDT == WQ8 ? out * e_s : out * 16.0f;
-  if (SW) {
-    float up = fold_row(L.p + ((NT + ft) * R + fr) * L.pst, a.nb);
-    up = WDT == WQ8 ? up * e_su : up * 16.0f;
-    out = silu_exact(out) * up;
-  } else if (tg.res) {
-    out = out + e_res;
+// Block-order fold of one LDS row of nb products into one accumulator. A wave issues one vector
+// instruction every few cycles and the fold runs on few waves, so the code keeps its instruction
+// count low: whole float4 are read eight at a time before the first add, the rest of the row (up
+// to seven float4 and the last nb % 4 values) in one more batch, and every branch depends on nb
+// only (uniform, no lane masking). Reads past the row's last whole float4 are clamped into the row.
+__device__ __forceinline__ float fold_chain(const float* row, int nb) {
+  const float4* p4 = reinterpret_cast<const float4*>(row);
+  const int nq = nb >> 2;
+  float acc = 0.f;
+  int q0 = 0;
+  for (; q0 + 8 <= nq; q0 += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = p4[q0 + i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) add4(acc, v[i]);
   }
-  tg.y[(int64_t)ft * tg.N + fn] = out;
+  const int nr = nq - q0;  // 0 .. 7
+  float4 v[7];
+#pragma unroll
+  for (int i = 0; i < 7; ++i) v[i] = p4[q0 + min(i, max(nr - 1, 0))];
+  const float4 t = p4[(nb - 1) >> 2];  // holds the last nb % 4 values
+#pragma unroll
+  for (int i = 0; i < 7; ++i)
+    if (i < nr) add4(acc, v[i]);
+  const int nt = nb & 3;
+  if (nt > 0) acc = acc + t.x;
+  if (nt > 1) acc = acc + t.y;
+  if (nt > 2) acc = acc + t.z;
+  return acc;
 }
 
-// Epilogue operands (row scale, residual) of a folding lane, loaded early.
+// Value of lane (i + 8) mod 16 within each 16-lane row of the wave (DPP row rotate by 8): swaps
+// the two halves of every row in one VALU instruction.
+__device__ __forceinline__ float row_swap8(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
+}
+
+// Fold lanes: one lane per row chain. Without SwiGLU lane c folds pair c = t * R + r (token t,
+// row r). With SwiGLU every 16-lane row holds 8 pairs, gate chains in lanes 0-7 and the up chains
+// of the same pairs in lanes 8-15, so one row_swap8 brings a row's up sum to its gate lane.
+template <bool SW>
+__device__ __forceinline__ void fold_lane(int tid, int& sel, int& pr) {
+  sel = SW ? (tid >> 3) & 1 : 0;
+  pr = SW ? ((tid >> 4) << 3) | (tid & 7) : tid;
+}
+
+// Threads the fold lanes of T tokens by R rows span.
+template <bool SW>
+__device__ __forceinline__ int fold_lanes(int T, int R) {
+  return SW ? ((T * R + 7) >> 3) << 4 : T * R;
+}
+
+// Last phase of the small GEMV (and of the streaming GEMV without a fold wave): each fold lane
+// sums its chain's row of products (the workgroup's R rows start at weight row n0, of which
+// `rows` are real) and applies the epilogue. e_res and e_s come from chain_epilogue_operands.
+template <int WDT, int NT, bool SW>
+__device__ __forceinline__ void gemv_fold(const GemvArgs& a, const GemvLds& L, const GemvTarget& tg, int n0, int R,
+                                          int rows, int tid, float e_res, float e_s) {
+  if ((tid & ~63) >= fold_lanes<SW>(a.T, R)) return;  // whole waves only: the swap needs every lane
+  int sel, pr;
+  fold_lane<SW>(tid, sel, pr);
+  const int ft = pr / R, fr = pr - ft * R, fn = n0 + fr;
+  const bool live = pr < a.T * R && fr < rows && fn < tg.N;
+  float v = fold_chain(L.p + (live ? (sel * NT + ft) * R + fr : 0) * L.pst, a.nb);
+  v = WDT == WQ8 ? v * e_s : v * 16.0f;
+  if (SW) {
+    const float up = row_swap8(v);
+    if (live && sel == 0) tg.y[(int64_t)ft * tg.N + fn] = silu_exact(v) * up;
+  } else if (live) {
+    tg.y[(int64_t)ft * tg.N + fn] = tg.res ? v + e_res : v;
+  }
+}
+
+// Epilogue operands of a fold lane (gemv_fold's mapping), loaded early: its chain's row scale
+// (q8) and, without SwiGLU, the residual.
 template <int WDT, bool SW>
-__device__ __forceinline__ void gemv_epilogue_operands(const GemvArgs& a, const GemvTarget& tg, int n0, int R, int rows,
-                                                       int tid, float& e_res, float& e_s, float& e_su) {
+__device__ __forceinline__ void chain_epilogue_operands(const GemvArgs& a, const GemvTarget& tg, int n0, int R, int rows,
+                                                        int tid, float& e_res, float& e_s) {
+  e_res = 0.f;
+  e_s = 1.f;
+  int sel, pr;
+  fold_lane<SW>(tid, sel, pr);
+  const int ft = pr / R, fr = pr - ft * R, fn = n0 + fr;
+  if (tid < fold_lanes<SW>(a.T, R) && pr < a.T * R && fr < rows && fn < tg.N) {
+    if (WDT == WQ8) e_s = (sel ? a.tg[1].scales : tg.scales)[fn];
+    if (!SW && tg.res) e_res = tg.res[(int64_t)ft * tg.N + fn];
+  }
+}
+
+// Epilogue operands of a fold-wave lane, which folds both chains of pair `lane` (token
+// lane / R, row lane % R), loaded early.
+template <int WDT, bool SW>
+__device__ __forceinline__ void pair_epilogue_operands(const GemvArgs& a, const GemvTarget& tg, int n0, int R, int rows,
+                                                       int lane, float& e_res, float& e_s, float& e_su) {
   e_res = 0.f;
   e_s = e_su = 1.f;
-  const int ft = tid / R, fr = tid - ft * R, fn = n0 + fr;
-  if (tid < a.T * R && fr < rows && fn < tg.N) {
+  const int ft = lane / R, fr = lane - ft * R, fn = n0 + fr;
+  if (lane < a.T * R && fr < rows && fn < tg.N) {
     if (WDT == WQ8) {
       e_s = tg.scales[fn];
       if (SW) e_su = a.tg[1].scales[fn];
@@ -437,8 +479,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
     }
   }
   // 3. epilogue operands of the folding lanes
-  float e_res, e_s, e_su;
-  gemv_epilogue_operands<WDT, SW>(a, tg, tile * H, H, H, tid, e_res, e_s, e_su);
+  float e_res, e_s;
+  chain_epilogue_operands<WDT, SW>(a, tg, tile * H, H, H, tid, e_res, e_s);
   // 4. quantize: block g = e0 / 32 spread over 4 consecutive lanes
   for (int pass = 0; pass * kSmallMaxAct < nel; ++pass) {
     const int e = pass * kSmallMaxAct + e0;
@@ -504,7 +546,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
             item_product<WDT>(w0, w1, ws, L.q + t * L.kpad + b * kBlock, L.d[t * nb + b], L.s[t * nb + b]);
   }
   __syncthreads();
-  gemv_fold<WDT, NT, SW>(a, L, tg, tile * H, H, H, tid, e_res, e_s, e_su);
+  gemv_fold<WDT, NT, SW>(a, L, tg, tile * H, H, H, tid, e_res, e_s);
 }
 
 // Streaming GEMV: T * K <= kStreamMaxAct activation bytes (staged in LDS).
@@ -604,7 +646,7 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
     const float* const frow_g = L.p + (ft * R + fr) * L.pst;
     const float* const frow_u = L.p + ((NT + ft) * R + fr) * L.pst;
     float e_res, e_s, e_su;
-    gemv_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, lane, e_res, e_s, e_su);
+    pair_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, lane, e_res, e_s, e_su);
     float acc_g = 0.f, acc_u = 0.f;
     int done_g = 0, done_u = 0;
     __syncthreads();  // activation in LDS
@@ -681,8 +723,8 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
   // in flight; the barrier makes every wave's part visible
   wait_vm<2 * D0>();
   __syncthreads();
-  float e_res = 0.f, e_s = 1.f, e_su = 1.f;
-  if (!FW) gemv_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
+  float e_res = 0.f, e_s = 1.f;
+  if (!FW) chain_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, tid, e_res, e_s);
 
   // 4. products into LDS in request order (each waits only for its own loads), one barrier per
   // batch. H is a power of two dividing P, so a thread's row within its tile never changes and
@@ -717,9 +759,9 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
     if (FW) __syncthreads();  // also waits for this wave's product writes
   }
   if (!FW) {
-    // 5. one lane per (token, row) folds its row in block order and applies the epilogue
+    // 5. one lane per row chain folds its row in block order and applies the epilogue
     __syncthreads();
-    gemv_fold<WDT, NT, SW>(a, L, tg, tile0 * H, R, rows, tid, e_res, e_s, e_su);
+    gemv_fold<WDT, NT, SW>(a, L, tg, tile0 * H, R, rows, tid, e_res, e_s);
   }
 }
 
@@ -1585,7 +1627,7 @@ static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
   const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.x ? a.H : a.tpw * a.H, SW ? 2 : 1);
   if (lds > 64 * 1024) return hipErrorInvalidValue;
   if (a.x) {
-    if (!gemv_qin_ok(a.T, a.K) || (a.K & 7)) return hipErrorInvalidValue;
+    if (!gemv_qin_ok(a.T, a.K) || (a.K & 7) || a.T * a.H * (SW ? 2 : 1) > kGemvThreads) return hipErrorInvalidValue;
     gemv_small_kernel<WDT, NT, SW><<<tiles, kGemvThreads, lds, s>>>(a);
     return hipGetLastError();
   }
