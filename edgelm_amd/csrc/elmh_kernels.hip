@@ -3,7 +3,7 @@
 //
 // Numerics follow edgelm's cpu backend on its scalar path bit for bit:
 //  * int8 activations (kernels_ref.cpp:23-37): per row, per 32-block amax/127, IEEE divide,
-//    round half away from zero, clamp +-127;
+//    round half away from zero, clamp +-127 (one division per lane group, elm_quant.h);
 //  * int8 block sums S_b are exact int32 dot products (v_dot4 / MFMA), order-free;
 //  * the f32 fold over blocks is sequential in block order with separate multiply and add
 //    (kernels_cpu.cpp:159-167, 193-204; this file is compiled with -ffp-contract=off and every
@@ -12,6 +12,7 @@
 //    (kernels_cpu.cpp:32-43, 45-71) and per-group order (73-112);
 //  * silu uses an expf identical to the host libm's (elm_expf.h).
 #include "elm_expf.h"
+#include "elm_quant.h"
 #include "elmh_internal.hpp"
 
 namespace elmh {
@@ -25,23 +26,43 @@ __device__ __forceinline__ float silu_exact(float v) { return v / (1.0f + elm_ex
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
-// Quantizes one 32-element block held by 32 consecutive lanes (element = lane & 31). Every lane of
-// the group gets the block scale d and the block sum of q. Same arithmetic as quantize_act_row.
-__device__ __forceinline__ int quant32(float v, float& d, int& sum) {
-  float a = fabsf(v);
+// Cross-lane moves in one VALU instruction (DPP): swap neighbours (quad_perm [1,0,3,2]), swap
+// pairs (quad_perm [2,3,0,1]), mirror each 8-lane half-row (lane i <- 7 - i), rotate each 16-lane
+// row by 8 (lane i <- (i + 8) mod 16).
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppHalfMirror = 0x141, kDppRowRor8 = 0x128;
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+
+// Quantizes one 32-value block held by 8 consecutive lanes (lanes 8k .. 8k+7 of a wave, 4 values
+// each, in order); every lane of the group gets the block scale (returned) and the block sum of q.
+// Same arithmetic as quantize_act_row (kernels_ref.cpp:23-37): the amax is order-free, the
+// rounding of every value that of its division (elm_q8_group). Every lane of the wave must run it.
+__device__ __forceinline__ float quant_block8x4(const float (&v)[4], int (&q)[4], int& sum) {
+  float a = 0.f;
 #pragma unroll
-  for (int off = 16; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
+  for (int i = 0; i < 4; ++i) a = fmaxf(a, fabsf(v[i]));
+  a = fmaxf(a, dpp_f<kDppQuadXor1>(a));
+  a = fmaxf(a, dpp_f<kDppQuadXor2>(a));
+  a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
   const float s = a / 127.0f;
-  const float safe = s == 0.f ? 1.f : s;
-  const float vv = v / safe;
-  const float r = copysignf(floorf(fabsf(vv) + 0.5f), vv);
-  const int q = (int)fminf(127.f, fmaxf(-127.f, r));
-  int sm = q;
-#pragma unroll
-  for (int off = 16; off >= 1; off >>= 1) sm += __shfl_xor(sm, off, 32);
-  d = s;
+  elm_q8_group<4>(v, s == 0.f ? 1.f : s, q);
+  int sm = q[0] + q[1] + q[2] + q[3];
+  sm += dpp_i<kDppQuadXor1>(sm);
+  sm += dpp_i<kDppQuadXor2>(sm);
+  sm += dpp_i<kDppHalfMirror>(sm);
   sum = sm;
-  return q;
+  return s;
+}
+
+__device__ __forceinline__ uint32_t pack_q4(const int (&q)[4]) {
+  return (uint32_t)(q[0] & 0xFF) | (uint32_t)(q[1] & 0xFF) << 8 | (uint32_t)(q[2] & 0xFF) << 16 |
+         (uint32_t)(q[3] & 0xFF) << 24;
 }
 
 // q4 group bytes -> MFMA int8 operand for half h: 16*q of elements h*16 .. h*16+15
@@ -85,20 +106,24 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, const float* __re
 
 // ---------------------------------------------------------------- activation quantization
 
-// Row-major: 8 blocks per 256-thread workgroup (two per wave).
+// Row-major: 32 blocks per 256-thread workgroup, 4 values per thread (8 threads per block).
 __global__ __launch_bounds__(256) void act_quant_rows_kernel(const float* __restrict__ x, int T, int K,
                                                              int8_t* __restrict__ xq, float* __restrict__ xd,
                                                              int32_t* __restrict__ xs) {
   const int nb = K / kBlock;
-  const int g = blockIdx.x * 8 + (threadIdx.x >> 5), l = threadIdx.x & 31;
+  const int g = blockIdx.x * 32 + (threadIdx.x >> 3), l = (threadIdx.x & 7) * 4;
   const bool ok = g < T * nb;
   const int t = ok ? g / nb : 0, b = ok ? g - t * nb : 0;
-  const float v = ok ? x[(int64_t)t * K + b * kBlock + l] : 0.f;
-  float d;
-  int sum;
-  const int q = quant32(v, d, sum);
+  const int64_t e = (int64_t)t * K + b * kBlock + l;
+  // four scalar loads the compiler merges into one 16-byte load (x need only be 4-byte aligned)
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (ok)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = x[e + i];
+  int q[4], sum;
+  const float d = quant_block8x4(v, q, sum);
   if (!ok) return;
-  xq[(int64_t)t * K + b * kBlock + l] = (int8_t)q;
+  *reinterpret_cast<uint32_t*>(xq + e) = pack_q4(q);
   if (l == 0) {
     xd[(int64_t)t * nb + b] = d;
     xs[(int64_t)t * nb + b] = sum;
@@ -109,14 +134,17 @@ __global__ __launch_bounds__(256) void act_quant_rows_kernel(const float* __rest
 // L = h*32 + t%32 the 16 bytes of elements h*16 .. h*16+15 of token t's block b. A thread owns one
 // such half-block: four float4 loads, edgelm's rounding, one 16-byte store.
 
-// edgelm's rounding of v / safe (quantize_act_row, kernels_ref.cpp:23-37)
-__device__ __forceinline__ uint32_t q8_of(float v, float safe) {
-  const float vv = v / safe;
-  const float r = copysignf(floorf(fabsf(vv) + 0.5f), vv);
-  return (uint32_t)(int)fminf(127.f, fmaxf(-127.f, r)) & 0xFFu;
-}
-__device__ __forceinline__ uint32_t q8x4(float4 v, float safe) {
-  return q8_of(v.x, safe) | (q8_of(v.y, safe) << 8) | (q8_of(v.z, safe) << 16) | (q8_of(v.w, safe) << 24);
+// edgelm's rounding of v / safe (quantize_act_row, kernels_ref.cpp:23-37) for 16 values of one
+// block, packed in order (elm_q8_group: one division for the 16)
+__device__ __forceinline__ uint4 q8x16(const float4 (&v)[4], float safe) {
+  const float f[16] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w,
+                       v[2].x, v[2].y, v[2].z, v[2].w, v[3].x, v[3].y, v[3].z, v[3].w};
+  int q[16];
+  elm_q8_group<16>(f, safe, q);
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = pack_q4({q[4 * i], q[4 * i + 1], q[4 * i + 2], q[4 * i + 3]});
+  return make_uint4(w[0], w[1], w[2], w[3]);
 }
 __device__ __forceinline__ float amax4(float4 v, float a) {
   return fmaxf(fmaxf(fmaxf(a, fabsf(v.x)), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
@@ -151,7 +179,7 @@ __global__ __launch_bounds__(256) void act_quant_frag_kernel(const float* __rest
   const float sc = a / 127.0f;
   const float safe = sc == 0.f ? 1.f : sc;
   *reinterpret_cast<uint4*>(xq + ((int64_t)(g * nb + b) * 64 + lane) * 16) =
-      make_uint4(q8x4(v[0], safe), q8x4(v[1], safe), q8x4(v[2], safe), q8x4(v[3], safe));
+      q8x16(v, safe);
   if (h == 0) xd[(int64_t)b * Tpad + t] = sc;
 }
 
@@ -196,15 +224,15 @@ __global__ __launch_bounds__(256) void act_quant_frag_token_kernel(const float* 
     for (int i = 0; i < NR; ++i) {
       const int j = threadIdx.x + 256 * i;
       if (j < hb)
-        *reinterpret_cast<uint4*>(xq + frag_offset(t, j >> 1, j & 1, nb)) =
-            make_uint4(q8x4(v[i][0], safe), q8x4(v[i][1], safe), q8x4(v[i][2], safe), q8x4(v[i][3], safe));
+        *reinterpret_cast<uint4*>(xq + frag_offset(t, j >> 1, j & 1, nb)) = q8x16(v[i], safe);
     }
   } else {
     for (int j = threadIdx.x; j < hb; j += 256) {
       uint4 q = make_uint4(0u, 0u, 0u, 0u);
       if (t < T) {
         const float* p = row + j * 16;
-        q = make_uint4(q8x4(ld4(p, 0), safe), q8x4(ld4(p, 1), safe), q8x4(ld4(p, 2), safe), q8x4(ld4(p, 3), safe));
+        const float4 v4[4] = {ld4(p, 0), ld4(p, 1), ld4(p, 2), ld4(p, 3)};
+        q = q8x16(v4, safe);
       }
       *reinterpret_cast<uint4*>(xq + frag_offset(t, j >> 1, j & 1, nb)) = q;
     }
@@ -320,7 +348,7 @@ __device__ __forceinline__ float fold_chain(const float* row, int nb) {
 // Value of lane (i + 8) mod 16 within each 16-lane row of the wave (DPP row rotate by 8): swaps
 // the two halves of every row in one VALU instruction.
 __device__ __forceinline__ float row_swap8(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
+  return dpp_f<kDppRowRor8>(v);
 }
 
 // Fold lanes: one lane per row chain. Without SwiGLU lane c folds pair c = t * R + r (token t,
@@ -439,15 +467,17 @@ __device__ __forceinline__ GemvTarget gemv_target(const GemvArgs& a, int& wg) {
   return target_at(a, ti);
 }
 
-// Small decode GEMV: x quantized inside the workgroup (8 elements per thread, 4 threads per
-// block), at most two items per thread held in registers before the products (longer tiles loop).
-constexpr int kSmallMaxAct = kGemvThreads * 8;
+// Small decode GEMV: x quantized inside the workgroup (4 values per thread, 8 threads per block,
+// kSmallPass values per pass), at most two items per thread held in registers before the products
+// (longer tiles loop). A workgroup takes up to kSmallMaxAct activation values (T * K).
+constexpr int kSmallPass = kGemvThreads * 4;
+constexpr int kSmallMaxAct = 4 * kSmallPass;
 
 template <int WDT, int NT, bool SW>
 __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int G = WDT == WQ8 ? 32 : 16;
-  const int K = a.K, nb = a.nb, T = a.T, H = a.H, tid = threadIdx.x;
+  const int K = a.K, nb = a.nb, T = a.T, H = a.H, lgH = __builtin_ctz(H), tid = threadIdx.x;
   const GemvLds L = gemv_lds<NT>(smem, K, nb);
   int tile = blockIdx.x;
   const GemvTarget tg = gemv_target<SW>(a, tile);
@@ -457,12 +487,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   const int nel = T * K;
 
   // 1. activation values (first: their wait does not cover the weight loads issued next)
-  const int e0 = tid * 8;
-  float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
-  if (e0 < nel) {
-    x0 = *reinterpret_cast<const float4*>(a.x + e0);
-    x1 = *reinterpret_cast<const float4*>(a.x + e0 + 4);
-  }
+  const int e0 = tid * 4;
+  float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (e0 < nel) x0 = *reinterpret_cast<const float4*>(a.x + e0);
   // 2. weights of this thread's first two items
   v4u w[2][G / 16];
   float wsc[2] = {0.f, 0.f};
@@ -481,38 +508,19 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   // 3. epilogue operands of the folding lanes
   float e_res, e_s;
   chain_epilogue_operands<WDT, SW>(a, tg, tile * H, H, H, tid, e_res, e_s);
-  // 4. quantize: block g = e0 / 32 spread over 4 consecutive lanes
-  for (int pass = 0; pass * kSmallMaxAct < nel; ++pass) {
-    const int e = pass * kSmallMaxAct + e0;
+  // 4. quantize: block g = e0 / 32 spread over 8 consecutive lanes (4 values each)
+  for (int pass = 0; pass * kSmallPass < nel; ++pass) {
+    const int e = pass * kSmallPass + e0;
     if (pass > 0) {
-      x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (e < nel) {
-        x0 = *reinterpret_cast<const float4*>(a.x + e);
-        x1 = *reinterpret_cast<const float4*>(a.x + e + 4);
-      }
+      x0 = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (e < nel) x0 = *reinterpret_cast<const float4*>(a.x + e);
     }
-    const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-    float am = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
-    am = fmaxf(am, __shfl_xor(am, 1, 4));
-    am = fmaxf(am, __shfl_xor(am, 2, 4));
-    const float sc = am / 127.0f;
-    const float safe = sc == 0.f ? 1.f : sc;
-    int qs = 0;
-    uint32_t pk[2] = {0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float vv = v[i] / safe;
-      const int q = (int)fminf(127.f, fmaxf(-127.f, copysignf(floorf(fabsf(vv) + 0.5f), vv)));
-      qs += q;
-      pk[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
-    }
-    qs += __shfl_xor(qs, 1, 4);
-    qs += __shfl_xor(qs, 2, 4);
+    const float v[4] = {x0.x, x0.y, x0.z, x0.w};
+    int qv[4], qs;
+    const float sc = quant_block8x4(v, qv, qs);
     if (e < nel) {
       const int g = e >> 5, t = g / nb, b = g - t * nb;
-      *reinterpret_cast<uint2*>(L.q + t * L.kpad + b * kBlock + (e & 31)) = make_uint2(pk[0], pk[1]);
+      *reinterpret_cast<uint32_t*>(L.q + t * L.kpad + b * kBlock + (e & 31)) = pack_q4(qv);
       if ((e & 31) == 0) {
         L.d[t * nb + b] = sc;
         L.s[t * nb + b] = qs;
@@ -538,7 +546,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
       w1 = G == 32 ? src[1] : w0;
       ws = WDT == WQ4 ? (sel ? ws1 : tg.scales)[gi] : 0.f;
     }
-    const int b = j / H, r = j - b * H;
+    const int b = j >> lgH, r = j & (H - 1);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
       if (t < T)
@@ -1558,7 +1566,7 @@ hipError_t launch_repack(const uint8_t* raw, const float* raw_scales, DevWeight&
 
 hipError_t launch_act_quant_rows(const float* x, int T, int K, int8_t* xq, float* xd, int32_t* xs, hipStream_t s) {
   const int blocks = T * (K / kBlock);
-  act_quant_rows_kernel<<<(blocks + 7) / 8, 256, 0, s>>>(x, T, K, xq, xd, xs);
+  act_quant_rows_kernel<<<(blocks + 31) / 32, 256, 0, s>>>(x, T, K, xq, xd, xs);
   return hipGetLastError();
 }
 
@@ -1595,7 +1603,7 @@ size_t gemv_lds_bytes(int nt, int K, int nb, int H, int nsel) {
   return nt * kpad + (((size_t)nt * nb * 8 + 15) & ~(size_t)15) + (size_t)nsel * nt * H * pst * 4;
 }
 
-bool gemv_qin_ok(int T, int K) { return T * K <= 2 * kSmallMaxAct; }
+bool gemv_qin_ok(int T, int K) { return T * K <= kSmallMaxAct; }
 
 int gemv_stream_ipt(int dtype, int items, int producers) {
   const int per = (items + producers - 1) / producers;
@@ -1627,7 +1635,8 @@ static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
   const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.x ? a.H : a.tpw * a.H, SW ? 2 : 1);
   if (lds > 64 * 1024) return hipErrorInvalidValue;
   if (a.x) {
-    if (!gemv_qin_ok(a.T, a.K) || (a.K & 7) || a.T * a.H * (SW ? 2 : 1) > kGemvThreads) return hipErrorInvalidValue;
+    if (!gemv_qin_ok(a.T, a.K) || (a.K & 31) || (a.H & (a.H - 1)) || a.T * a.H * (SW ? 2 : 1) > kGemvThreads)
+      return hipErrorInvalidValue;
     gemv_small_kernel<WDT, NT, SW><<<tiles, kGemvThreads, lds, s>>>(a);
     return hipGetLastError();
   }

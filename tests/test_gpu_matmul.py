@@ -53,6 +53,40 @@ def test_act_quant_bit_exact(ctx):
     assert d[1, 1] >= 25.0 / 127.0 and d[1, 0] < 0.1  # outlier isolated to its block (test_ops.cpp:205-207)
 
 
+def near_half_activations(r, T, K):
+    """Rows whose values sit within a few ulp of the rounding points (m - 1/2) s of their block
+    (s = amax / 127), where a quotient one ulp off the correctly rounded one would round the
+    other way; one value per block is the block's amax."""
+    nb = K // 32
+    amax = np.exp(r.uniform(-8, 8, (T, nb, 1))).astype(np.float32)
+    s = amax / np.float32(127)
+    m = r.integers(1, 128, (T, nb, 32)).astype(np.float32)
+    base = ((m - np.float32(0.5)) * s).astype(np.float32)
+    off = r.integers(-3, 4, (T, nb, 32)).astype(np.int32)
+    x = (base.view(np.int32) + off).view(np.float32)
+    x = np.minimum(x, amax) * np.where(r.random((T, nb, 32)) < 0.5, -1, 1).astype(np.float32)
+    pos = r.integers(0, 32, (T, nb))
+    np.put_along_axis(x, pos[..., None], amax, axis=2)
+    return x.reshape(T, K).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
+def test_act_quant_near_half_points(ctx, dt):
+    """Every int8 quantizer (row-major, in-workgroup, GEMM fragments) on values at the rounding
+    boundaries: bit-identical to edgelm's per-value division."""
+    r = rng(11)
+    x = near_half_activations(r, 4, 1536)
+    q, d = ctx.quantize_act(x)
+    qo, do = O.quantize_act(x)
+    assert np.array_equal(q, qo) and bits_equal(d, do)
+    for T, K, N in [(1, 576, 1536), (3, 1536, 576), (2, 2048, 256), (64, 576, 256), (130, 576, 256)]:
+        print(f"[gpu] near-half matmul dt={dt} T={T} K={K} N={N}", flush=True)
+        x = near_half_activations(r, T, K)
+        w = weight(r, N, K, dt)
+        got = ctx.matmul(x, [up(ctx, w)])[0]
+        assert bits_equal(got, O.cpu_matmul(x, [w], None, act_quant=True)[0]), f"T={T} K={K}"
+
+
 @pytest.mark.parametrize("dt", [O.Q8, O.Q4])
 def test_block_sums_exact(ctx, dt):
     r = rng(2)
