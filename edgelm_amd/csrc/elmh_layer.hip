@@ -13,34 +13,94 @@
 namespace elmh {
 namespace {
 
+// four floats as one vector value: copies stay register moves (a float4 struct copy between
+// memory spaces can become a memcpy that keeps an array of them out of registers)
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 // ---------------------------------------------------------------- RMSNORM
 //
-// One workgroup per row. The row goes to LDS; lanes 0-3 then run dot_f32_scalar's four strided
-// accumulators s_k = sum of x[i]^2 over i = k (mod 4) in increasing i (the tail past the last
-// multiple of 4 goes into s0), and ss = (s0 + s1) + (s2 + s3); inv = 1 / sqrt(ss / dim + eps);
-// y[i] = (x[i] * inv) * w[i].
+// One workgroup per row: dot_f32_scalar's four strided accumulators s_k = sum of x[i]^2 over
+// i = k (mod 4) in increasing i (the tail past the last multiple of 4 goes into s0), then
+// ss = (s0 + s1) + (s2 + s3); inv = 1 / sqrt(ss / dim + eps); y[i] = (x[i] * inv) * w[i].
+// Every thread squares its float4s (the products are separate roundings in the scalar code too)
+// and writes them to LDS by accumulator: row k holds the terms of s_k in order, zero-padded to a
+// multiple of 32 (adding +0.0 to a sum of squares, which is never -0.0, changes nothing). Lanes
+// 0-3 then run the four sums, reading eight float4 before their 32 dependent adds, and combine
+// them with two DPP steps. x and w stay in registers for the output.
+constexpr int kNormVF = 8;  // float4 of the row per thread: dim <= 8192
+
+__device__ __forceinline__ float4 ld4u(const float* p) {  // 4-byte aligned is enough
+  return make_float4(p[0], p[1], p[2], p[3]);
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                       float* __restrict__ y, int dim, float eps) {
-  extern __shared__ float xs[];
-  __shared__ float part[4];
+  extern __shared__ float sq[];  // [4][rowlen], then the dim % 4 tail squares
+  __shared__ float inv_s;
   const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x, nq = dim >> 2, rowlen = (nq + 31) & ~31, tail = dim & 3;
   const float* xr = x + r * dim;
-  for (int i = threadIdx.x; i < dim; i += 256) xs[i] = xr[i];
-  __syncthreads();
-  if (threadIdx.x < 4) {
-    const int k = threadIdx.x, m4 = dim & ~3;
-    float s = 0.f;
-#pragma unroll 8
-    for (int i = k; i < m4; i += 4) s = s + xs[i] * xs[i];
-    if (k == 0)
-      for (int i = m4; i < dim; ++i) s = s + xs[i] * xs[i];
-    part[k] = s;
+  float4 xv[kNormVF], wv[kNormVF];
+#pragma unroll
+  for (int u = 0; u < kNormVF; ++u) {
+    const int i4 = tid + 256 * u;
+    if (i4 < nq) {
+      xv[u] = ld4u(xr + 4 * i4);
+      wv[u] = ld4u(w + 4 * i4);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kNormVF; ++u) {
+    const int i4 = tid + 256 * u;
+    if (i4 < rowlen) {
+      const bool in = i4 < nq;
+      sq[i4] = in ? xv[u].x * xv[u].x : 0.f;
+      sq[rowlen + i4] = in ? xv[u].y * xv[u].y : 0.f;
+      sq[2 * rowlen + i4] = in ? xv[u].z * xv[u].z : 0.f;
+      sq[3 * rowlen + i4] = in ? xv[u].w * xv[u].w : 0.f;
+    }
+  }
+  if (tid < tail) {
+    const float v = xr[4 * nq + tid];
+    sq[4 * rowlen + tid] = v * v;
   }
   __syncthreads();
-  const float ss = (part[0] + part[1]) + (part[2] + part[3]);
-  const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+  if (tid < 4) {
+    const float4* row = reinterpret_cast<const float4*>(sq + tid * rowlen);
+    float s = 0.f;
+    for (int q0 = 0; q0 < (rowlen >> 2); q0 += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = row[q0 + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        s = s + v[i].x;
+        s = s + v[i].y;
+        s = s + v[i].z;
+        s = s + v[i].w;
+      }
+    }
+    if (tid == 0)
+      for (int t = 0; t < tail; ++t) s = s + sq[4 * rowlen + t];
+    // lanes 0-3 hold s0..s3: lane 0 forms s0 + s1 and lane 2 s2 + s3, then lane 0 their sum
+    const float s01 = s + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s), 0xB1, 0xF, 0xF, false));
+    const float ss = s01 + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s01), 0x4E, 0xF, 0xF, false));
+    if (tid == 0) inv_s = 1.0f / sqrtf(ss / (float)dim + eps);
+  }
+  __syncthreads();
+  const float inv = inv_s;
   float* yr = y + r * dim;
-  for (int i = threadIdx.x; i < dim; i += 256) yr[i] = (xs[i] * inv) * w[i];
+#pragma unroll
+  for (int u = 0; u < kNormVF; ++u) {
+    const int i4 = tid + 256 * u;
+    if (i4 < nq) {
+      yr[4 * i4] = (xv[u].x * inv) * wv[u].x;
+      yr[4 * i4 + 1] = (xv[u].y * inv) * wv[u].y;
+      yr[4 * i4 + 2] = (xv[u].z * inv) * wv[u].z;
+      yr[4 * i4 + 3] = (xv[u].w * inv) * wv[u].w;
+    }
+  }
+  if (tid < tail) yr[4 * nq + tid] = (xr[4 * nq + tid] * inv) * w[4 * nq + tid];
 }
 
 // ---------------------------------------------------------------- attention
@@ -92,21 +152,19 @@ __global__ __launch_bounds__(64) void kv_append_kernel(const float* __restrict__
 //   in flight at once); mx = max sc; e_j = expf(sc[j] - mx); thread 0 sums e_0 + e_1 + ... in
 //   order, inv = 1 / sum; every thread forms p_j = e_j * inv; then lane i of wave 0 runs
 //   o_i = 0, o_i += p_j * v_j[i] in increasing j.
-// The values go through LDS transposed, [dim][position] with a row stride of 4 (mod 8) floats, so
-// that lane i reads four positions of its dim with one conflict-free 16-byte read; they move in
-// chunks of whole positions (a multiple of 4), kAttnVF float4 per thread: the first chunk's loads
-// are issued at the start, after q's, and chunk c + 1 is loaded into registers while wave 0
-// accumulates chunk c.
-// LDS (dynamic): q [hd], scores [n_cap], one transposed value chunk [hd][stride].
+// The values go through LDS as they lie in the cache, rows of hd floats, so that lane i reads
+// v_j[i] of 64 consecutive floats (no bank conflict) and the staging is one 16-byte write per
+// float4. They move in chunks of whole positions (a multiple of 16), kAttnVF float4 per thread; the
+// first chunk's loads are issued at the start, after q's and the key row's, and chunk c + 1 is
+// loaded into registers while wave 0 accumulates chunk c. Every load is unconditional (indices
+// clamped), so waiting for the first ones does not wait for the later ones. Wave 0 reads the
+// values and probabilities of 16 positions before the first of their 16 dependent adds.
+// LDS (dynamic): q [hd], scores [n_cap rounded up to 64], one value chunk [cpos][hd].
 constexpr int kAttnThreads = 256;
 constexpr int kAttnVF = 12;                           // float4 of values per thread per chunk
 constexpr int kAttnChunkF4 = kAttnThreads * kAttnVF;  // 48 KB: 192 positions of head size 64
 
-__device__ __forceinline__ int attn_chunk_pos(int hd) { return (kAttnChunkF4 / (hd / 4)) & ~3; }
-__device__ __host__ __forceinline__ int attn_stride(int cpos) {
-  const int s = (cpos + 3) & ~3;
-  return (s / 4) % 2 ? s : s + 4;
-}
+__device__ __host__ __forceinline__ int attn_chunk_pos(int hd) { return (kAttnChunkF4 / (hd / 4)) & ~15; }
 
 __device__ __forceinline__ float dot_row(const float* __restrict__ q, const float* __restrict__ k, int hd) {
   if (hd == 64) {  // the common head size: all 16 loads issued before the first product
@@ -126,19 +184,22 @@ __device__ __forceinline__ float dot_row(const float* __restrict__ q, const floa
   return dot4(q, k, hd);
 }
 
+// HD: the head size when it is known at compile time (64), else 0 (hd_arg)
+template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ q, float* __restrict__ out,
                                                                  const float* __restrict__ kc,
                                                                  const float* __restrict__ vc, int pos0,
                                                                  const int* __restrict__ pos_dev, int n_heads, int n_kv,
-                                                                 int hd, int max_ctx, int n_cap,
+                                                                 int hd_arg, int max_ctx, int n_cap,
                                                                  const float* __restrict__ rcos,
                                                                  const float* __restrict__ rsin) {
+  const int hd = HD ? HD : hd_arg;
   extern __shared__ float lds[];
   if (pos_dev) pos0 = *pos_dev;
   const int hdp = (hd + 3) & ~3;
   float* qb = lds;
   float* sc = lds + hdp;
-  float* vt = sc + ((n_cap + 3) & ~3);
+  float* vt = sc + ((n_cap + 63) & ~63);
   __shared__ float red[kAttnThreads / 64];
   __shared__ float inv_s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -158,8 +219,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     qa = qs[iq];
   }
   const float* kh = kc + (int64_t)(h / grp) * max_ctx * hd;
-  const float4* vh4 = reinterpret_cast<const float4*>(vc + (int64_t)(h / grp) * max_ctx * hd);
-  const int hd4 = hd / 4, cpos = attn_chunk_pos(hd), cf4 = cpos * hd4, vstride = attn_stride(cpos);
+  const v4f* vh4 = reinterpret_cast<const v4f*>(vc + (int64_t)(h / grp) * max_ctx * hd);
+  const int hd4 = hd / 4, cpos = attn_chunk_pos(hd), cf4 = cpos * hd4;
   const int total4 = n * hd4;  // the values to read, as float4 (hd % 4 == 0)
   // head size 64: this thread's first key row in flight from the start
   float4 kr[16];
@@ -169,12 +230,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     for (int u = 0; u < 16; ++u) kr[u] = k4[u];
   }
   // chunk 0 of the values, also in flight from the start
-  float4 vr[kAttnVF];
+  v4f vr[kAttnVF];
 #pragma unroll
-  for (int u = 0; u < kAttnVF; ++u) {
-    const int f = tid + u * kAttnThreads;
-    vr[u] = f < min(total4, cf4) ? vh4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  for (int u = 0; u < kAttnVF; ++u) vr[u] = vh4[min(tid + u * kAttnThreads, total4 - 1)];
   if (rcos) {
     if (tid < h2) {
       qb[tid] = qa * cr - qb2 * sr;
@@ -210,21 +268,37 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
   if (lane == 0) red[wave] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  for (int j = tid; j < n; j += kAttnThreads) sc[j] = elm_expf(sc[j] - mx);
+  // e_j, and +0.0 in the slots up to the next multiple of 64: adding them changes no sum (a sum
+  // of non-negative terms that starts at +0.0 is never -0.0), and as p_j they scale zero values
+  const int n64 = (n + 63) & ~63;
+  for (int j = tid; j < n64; j += kAttnThreads) sc[j] = j < n ? elm_expf(sc[j] - mx) : 0.f;
+  // chunk 0 of the values into LDS (their loads were issued first thing), zero rows past the
+  // last position
+  v4f* vt4 = reinterpret_cast<v4f*>(vt);
+  auto stage = [&](int f) {
+#pragma unroll
+    for (int u = 0; u < kAttnVF; ++u) {
+      const int rel = tid + u * kAttnThreads;
+      if (rel < cf4) vt4[rel] = f + rel < total4 ? vr[u] : v4f{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  stage(0);
   __syncthreads();
-  if (tid == 0) {  // e_0 + e_1 + ... in order, read 16 bytes at a time
+  if (tid == 0) {  // e_0 + e_1 + ... in order, 64 values read before their adds
     float sum = 0.f;
     const float4* s4 = reinterpret_cast<const float4*>(sc);
-    int j = 0;
-#pragma unroll 8
-    for (; j + 4 <= n; j += 4) {
-      const float4 e = s4[j >> 2];
-      sum = sum + e.x;
-      sum = sum + e.y;
-      sum = sum + e.z;
-      sum = sum + e.w;
+    for (int j0 = 0; j0 < n; j0 += 64) {
+      float4 e[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) e[u] = s4[(j0 >> 2) + u];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        sum = sum + e[u].x;
+        sum = sum + e[u].y;
+        sum = sum + e[u].z;
+        sum = sum + e[u].w;
+      }
     }
-    for (; j < n; ++j) sum = sum + sc[j];
     inv_s = 1.0f / sum;
   }
   __syncthreads();
@@ -234,52 +308,61 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
   }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};  // wave 0: outputs lane, lane + 64, ... (hd <= 256)
   for (int f0 = 0; f0 < total4; f0 += cf4) {
-    // transpose this thread's float4 (position j, dims 4 d .. 4 d + 3) into vt[dim][j - j0]
-#pragma unroll
-    for (int u = 0; u < kAttnVF; ++u) {
-      const int rel = tid + u * kAttnThreads;
-      if (rel < cf4) {
-        const int jj = rel / hd4, d4 = (rel - jj * hd4) * 4;
-        vt[(d4 + 0) * vstride + jj] = vr[u].x;
-        vt[(d4 + 1) * vstride + jj] = vr[u].y;
-        vt[(d4 + 2) * vstride + jj] = vr[u].z;
-        vt[(d4 + 3) * vstride + jj] = vr[u].w;
-      }
-    }
-    __syncthreads();  // the chunk (and, the first time, every p_j) is in LDS
     const int fn = f0 + cf4;
-    if (fn < total4) {
+    if (fn < total4) {  // the next chunk into registers while this one is accumulated
 #pragma unroll
-      for (int u = 0; u < kAttnVF; ++u) {
-        const int rel = tid + u * kAttnThreads;
-        vr[u] = rel < cf4 && fn + rel < total4 ? vh4[fn + rel] : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      for (int u = 0; u < kAttnVF; ++u) vr[u] = vh4[min(fn + tid + u * kAttnThreads, total4 - 1)];
     }
+    __syncthreads();  // this chunk (and, the first time, every p_j) is in LDS
     if (wave == 0) {
+      // positions j0 .. j0 + m - 1, in batches of 16; past the last position p_j and the values
+      // are zero (chunks hold a multiple of 16 positions)
       const int j0 = f0 / hd4, m = min(cpos, n - j0);
-      const float4* p4 = reinterpret_cast<const float4*>(sc + j0);  // j0 is a multiple of 4
+      const float4* p4 = reinterpret_cast<const float4*>(sc + j0);  // j0 is a multiple of 16
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = lane + 64 * r;
         if (i < hd) {
-          const float* vrow = vt + i * vstride;
-          const float4* v4 = reinterpret_cast<const float4*>(vrow);
           float a = acc[r];
-          int jj = 0;
-#pragma unroll 4
-          for (; jj + 4 <= m; jj += 4) {
-            const float4 pv = p4[jj >> 2], vv = v4[jj >> 2];
-            a = a + pv.x * vv.x;
-            a = a + pv.y * vv.y;
-            a = a + pv.z * vv.z;
-            a = a + pv.w * vv.w;
+          // batches of 16 positions; the next batch's reads are issued before this one's adds
+          const int nbat = (m + 15) >> 4;
+          auto load = [&](int bt, float4 (&pv)[4], float (&vv)[16]) {
+            const int jj = min(bt, nbat - 1) * 16;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) pv[u] = p4[(jj >> 2) + u];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) vv[u] = vt[(jj + u) * hd + i];
+          };
+          auto fold = [&](const float4 (&pv)[4], const float (&vv)[16]) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              a = a + pv[u].x * vv[4 * u];
+              a = a + pv[u].y * vv[4 * u + 1];
+              a = a + pv[u].z * vv[4 * u + 2];
+              a = a + pv[u].w * vv[4 * u + 3];
+            }
+          };
+          float4 pa[4], pb[4];
+          float va[16], vb[16];
+          load(0, pa, va);
+          for (int bt = 0; bt < nbat; bt += 2) {
+            load(bt + 1, pb, vb);
+            __builtin_amdgcn_sched_barrier(0);
+            fold(pa, va);
+            if (bt + 1 < nbat) {
+              load(bt + 2, pa, va);
+              __builtin_amdgcn_sched_barrier(0);
+              fold(pb, vb);
+            }
           }
-          for (; jj < m; ++jj) a = a + sc[j0 + jj] * vrow[jj];
           acc[r] = a;
         }
       }
     }
-    __syncthreads();  // wave 0 is done with the chunk before it is overwritten
+    if (fn < total4) {
+      __syncthreads();  // wave 0 is done with this chunk
+      stage(fn);
+    }
   }
   float* o = out + (int64_t)t * qd + h * hd;
   if (wave == 0) {
@@ -402,13 +485,14 @@ hipError_t launch_fill(void* dst, int value, size_t bytes, hipStream_t s) {
 }
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps, hipStream_t s) {
-  rmsnorm_kernel<<<rows, 256, (size_t)dim * sizeof(float), s>>>(x, w, y, dim, eps);
+  if (dim < 1 || dim > 256 * 4 * kNormVF) return hipErrorInvalidValue;
+  const size_t rowlen = ((size_t)(dim >> 2) + 31) & ~(size_t)31;
+  rmsnorm_kernel<<<rows, 256, (4 * rowlen + 4) * sizeof(float), s>>>(x, w, y, dim, eps);
   return hipGetLastError();
 }
 
 size_t attention_lds_bytes(int hd, int n_max) {
-  const int cpos = (kAttnChunkF4 / (hd / 4)) & ~3;
-  return ((size_t)((hd + 3) & ~3) + (size_t)((n_max + 3) & ~3) + (size_t)hd * attn_stride(cpos)) * sizeof(float);
+  return ((size_t)((hd + 3) & ~3) + (size_t)((n_max + 63) & ~63) + (size_t)attn_chunk_pos(hd) * hd) * sizeof(float);
 }
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
@@ -419,8 +503,12 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
   kv_append_kernel<<<T * n_kv, 64, 0, s>>>(k, v, kc, vc, pos0, pos_dev, n_kv, hd, max_ctx, rcos, rsin);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  attention_kernel<<<T * n_heads, kAttnThreads, attention_lds_bytes(hd, n_cap), s>>>(
-      q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin);
+  if (hd == 64)
+    attention_kernel<64><<<T * n_heads, kAttnThreads, attention_lds_bytes(hd, n_cap), s>>>(
+        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin);
+  else
+    attention_kernel<0><<<T * n_heads, kAttnThreads, attention_lds_bytes(hd, n_cap), s>>>(
+        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin);
   return hipGetLastError();
 }
 
