@@ -11,6 +11,7 @@
 //  * f32-activation paths keep the scalar path's four interleaved accumulators
 //    (kernels_cpu.cpp:32-43, 45-71) and per-group order (73-112);
 //  * silu uses an expf identical to the host libm's (elm_expf.h).
+#include "elm_dpp.h"
 #include "elm_expf.h"
 #include "elm_quant.h"
 #include "elmh_internal.hpp"
@@ -25,19 +26,6 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float silu_exact(float v) { return v / (1.0f + elm_expf(-v)); }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
-
-// Cross-lane moves in one VALU instruction (DPP): swap neighbours (quad_perm [1,0,3,2]), swap
-// pairs (quad_perm [2,3,0,1]), mirror each 8-lane half-row (lane i <- 7 - i), rotate each 16-lane
-// row by 8 (lane i <- (i + 8) mod 16).
-constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppHalfMirror = 0x141, kDppRowRor8 = 0x128;
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
-}
 
 // Quantizes one 32-value block held by 8 consecutive lanes (lanes 8k .. 8k+7 of a wave, 4 values
 // each, in order); every lane of the group gets the block scale (returned) and the block sum of q.

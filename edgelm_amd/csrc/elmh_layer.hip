@@ -7,6 +7,7 @@
 //   embed     dequantize_row (model.cpp:192-218) of the token's row, EMBED (backends.cpp, reference)
 #include <hip/hip_runtime.h>
 
+#include "elm_dpp.h"
 #include "elm_expf.h"
 #include "elmh_internal.hpp"
 
@@ -83,8 +84,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     if (tid == 0)
       for (int t = 0; t < tail; ++t) s = s + sq[4 * rowlen + t];
     // lanes 0-3 hold s0..s3: lane 0 forms s0 + s1 and lane 2 s2 + s3, then lane 0 their sum
-    const float s01 = s + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s), 0xB1, 0xF, 0xF, false));
-    const float ss = s01 + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s01), 0x4E, 0xF, 0xF, false));
+    const float s01 = s + dpp_f<kDppQuadXor1>(s);
+    const float ss = s01 + dpp_f<kDppQuadXor2>(s01);
     if (tid == 0) inv_s = 1.0f / sqrtf(ss / (float)dim + eps);
   }
   __syncthreads();
@@ -150,16 +151,18 @@ __global__ __launch_bounds__(64) void kv_append_kernel(const float* __restrict__
 // 0 .. pos0 + t, every float operation in cpu::attention's order:
 //   q rotated into LDS; thread j computes sc[j] = dot_f32(q, k_j) * scale (its key row's loads all
 //   in flight at once); mx = max sc; e_j = expf(sc[j] - mx); thread 0 sums e_0 + e_1 + ... in
-//   order, inv = 1 / sum; every thread forms p_j = e_j * inv; then lane i of wave 0 runs
-//   o_i = 0, o_i += p_j * v_j[i] in increasing j.
-// The values go through LDS as they lie in the cache, rows of hd floats, so that lane i reads
-// v_j[i] of 64 consecutive floats (no bank conflict) and the staging is one 16-byte write per
-// float4. They move in chunks of whole positions (a multiple of 16), kAttnVF float4 per thread; the
-// first chunk's loads are issued at the start, after q's and the key row's, and chunk c + 1 is
-// loaded into registers while wave 0 accumulates chunk c. Every load is unconditional (indices
-// clamped), so waiting for the first ones does not wait for the later ones. Wave 0 reads the
-// values and probabilities of 16 positions before the first of their 16 dependent adds.
-// LDS (dynamic): q [hd], scores [n_cap rounded up to 64], one value chunk [cpos][hd].
+//   order, inv = 1 / sum; p_j = e_j * inv; o_i = 0, o_i += p_j * v_j[i] in increasing j.
+// Only the two sums are chains. The products p_j * v_j[i] are independent roundings: every
+// thread forms them for its float4s of values (each value loaded once, straight from the cache)
+// and writes them to LDS as rows of hd, so that lane i of wave 0 then only adds, reading row j's
+// element i (64 consecutive floats: no bank conflict), 16 positions per batch with the next
+// batch's reads issued before this batch's adds. Values move in chunks of whole positions (a
+// multiple of 16), kAttnVF float4 per thread; the first chunk's loads are issued at the start,
+// after q's and the key row's, and chunk c + 1 is loaded into registers while wave 0 adds chunk
+// c. Every load is unconditional (indices clamped), so waiting for the first ones does not wait
+// for the later ones. Score slots past the last position hold +0.0 and product rows past it are
+// zero: adding them changes no sum (these sums start at +0.0 and are never -0.0).
+// LDS (dynamic): q [hd], scores [n_cap rounded up to 64], one product chunk [cpos][hd].
 constexpr int kAttnThreads = 256;
 constexpr int kAttnVF = 12;                           // float4 of values per thread per chunk
 constexpr int kAttnChunkF4 = kAttnThreads * kAttnVF;  // 48 KB: 192 positions of head size 64
@@ -263,26 +266,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     sc[j] = sj;
     mx = fmaxf(mx, sj);
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  mx = wave_max(mx);
   if (lane == 0) red[wave] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  // e_j, and +0.0 in the slots up to the next multiple of 64: adding them changes no sum (a sum
-  // of non-negative terms that starts at +0.0 is never -0.0), and as p_j they scale zero values
+  // e_j, and +0.0 in the slots up to the next multiple of 64
   const int n64 = (n + 63) & ~63;
   for (int j = tid; j < n64; j += kAttnThreads) sc[j] = j < n ? elm_expf(sc[j] - mx) : 0.f;
-  // chunk 0 of the values into LDS (their loads were issued first thing), zero rows past the
-  // last position
-  v4f* vt4 = reinterpret_cast<v4f*>(vt);
-  auto stage = [&](int f) {
-#pragma unroll
-    for (int u = 0; u < kAttnVF; ++u) {
-      const int rel = tid + u * kAttnThreads;
-      if (rel < cf4) vt4[rel] = f + rel < total4 ? vr[u] : v4f{0.f, 0.f, 0.f, 0.f};
-    }
-  };
-  stage(0);
   __syncthreads();
   if (tid == 0) {  // e_0 + e_1 + ... in order, 64 values read before their adds
     float sum = 0.f;
@@ -302,10 +292,25 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     inv_s = 1.0f / sum;
   }
   __syncthreads();
-  {
-    const float inv = inv_s;
-    for (int j = tid; j < n; j += kAttnThreads) sc[j] = sc[j] * inv;  // p_j
-  }
+  const float inv = inv_s;
+  // The products p_j * v_j[i] of a chunk, p_j = e_j * inv, into LDS as rows of hd (this thread's
+  // float4 of values: position j, dims 4 d .. 4 d + 3); zero rows past the last position.
+  v4f* vt4 = reinterpret_cast<v4f*>(vt);
+  auto products = [&](int f) {
+    float e[kAttnVF];  // every e_j first (slots past the last position read +0.0), then the products
+#pragma unroll
+    for (int u = 0; u < kAttnVF; ++u) e[u] = sc[min((f + tid + u * kAttnThreads) / hd4, n64 - 1)];
+#pragma unroll
+    for (int u = 0; u < kAttnVF; ++u) {
+      const int rel = tid + u * kAttnThreads;
+      if (rel < cf4) {
+        const float pj = e[u] * inv;
+        const v4f pr = v4f{pj * vr[u].x, pj * vr[u].y, pj * vr[u].z, pj * vr[u].w};
+        vt4[rel] = f + rel < total4 ? pr : v4f{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  products(0);
   float acc[4] = {0.f, 0.f, 0.f, 0.f};  // wave 0: outputs lane, lane + 64, ... (hd <= 256)
   for (int f0 = 0; f0 < total4; f0 += cf4) {
     const int fn = f0 + cf4;
@@ -313,46 +318,35 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
 #pragma unroll
       for (int u = 0; u < kAttnVF; ++u) vr[u] = vh4[min(fn + tid + u * kAttnThreads, total4 - 1)];
     }
-    __syncthreads();  // this chunk (and, the first time, every p_j) is in LDS
+    __syncthreads();  // this chunk's products are in LDS
     if (wave == 0) {
-      // positions j0 .. j0 + m - 1, in batches of 16; past the last position p_j and the values
-      // are zero (chunks hold a multiple of 16 positions)
-      const int j0 = f0 / hd4, m = min(cpos, n - j0);
-      const float4* p4 = reinterpret_cast<const float4*>(sc + j0);  // j0 is a multiple of 16
+      // positions j0 .. j0 + m - 1 in batches of 16 (chunks hold a multiple of 16 positions; the
+      // rows past the last position are zero); the next batch's reads go out before this one's adds
+      const int j0 = f0 / hd4, m = min(cpos, n - j0), nbat = (m + 15) >> 4;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = lane + 64 * r;
         if (i < hd) {
           float a = acc[r];
-          // batches of 16 positions; the next batch's reads are issued before this one's adds
-          const int nbat = (m + 15) >> 4;
-          auto load = [&](int bt, float4 (&pv)[4], float (&vv)[16]) {
+          auto load = [&](int bt, float (&vv)[16]) {
             const int jj = min(bt, nbat - 1) * 16;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) pv[u] = p4[(jj >> 2) + u];
 #pragma unroll
             for (int u = 0; u < 16; ++u) vv[u] = vt[(jj + u) * hd + i];
           };
-          auto fold = [&](const float4 (&pv)[4], const float (&vv)[16]) {
+          auto fold = [&](const float (&vv)[16]) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              a = a + pv[u].x * vv[4 * u];
-              a = a + pv[u].y * vv[4 * u + 1];
-              a = a + pv[u].z * vv[4 * u + 2];
-              a = a + pv[u].w * vv[4 * u + 3];
-            }
+            for (int u = 0; u < 16; ++u) a = a + vv[u];
           };
-          float4 pa[4], pb[4];
           float va[16], vb[16];
-          load(0, pa, va);
+          load(0, va);
           for (int bt = 0; bt < nbat; bt += 2) {
-            load(bt + 1, pb, vb);
+            load(bt + 1, vb);
             __builtin_amdgcn_sched_barrier(0);
-            fold(pa, va);
+            fold(va);
             if (bt + 1 < nbat) {
-              load(bt + 2, pa, va);
+              load(bt + 2, va);
               __builtin_amdgcn_sched_barrier(0);
-              fold(pb, vb);
+              fold(vb);
             }
           }
           acc[r] = a;
@@ -361,7 +355,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     }
     if (fn < total4) {
       __syncthreads();  // wave 0 is done with this chunk
-      stage(fn);
+      products(fn);
     }
   }
   float* o = out + (int64_t)t * qd + h * hd;
