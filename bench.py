@@ -200,7 +200,7 @@ def decode_step_bench(ctx, E, steps, warmup, eager=False):
     log(f"decode step {ms_step * 1e3:.1f} us -> {1e3 / ms_step:.1f} tok/s" + (" (eager launches)" if eager else ""))
 
     # per-op kernel time: a graph holding 16 x (the op for all 30 layers, distinct weights),
-    # replayed; time per call (one kernel per call except the LM head's quantize + GEMV)
+    # replayed; time per call (one kernel per call: the GEMV kernels quantize x themselves)
     timer = time_eager if eager else time_graph
     per = {}
     ops = {
@@ -216,7 +216,7 @@ def decode_step_bench(ctx, E, steps, warmup, eager=False):
     hb = q_bytes(1, VOCAB, D) + D * 4 + VOCAB * 4
     ms = timer(ctx, lambda: [head() for _ in range(8)], 10, inner=16) / 8
     per["MATMUL lm_head q8"] = {"us": ms * 1e3, "bytes": hb, "GBs": hb / (ms * 1e-3) / 1e9, "calls_per_step": 1,
-                                "kernels_per_call": 2}
+                                "kernels_per_call": 1}
     for k, v in per.items():
         log(f"  {k:20s} {v['us']:8.2f} us  {v['GBs']:8.1f} GB/s")
     for b in bufs.values():
@@ -256,7 +256,8 @@ def sweep_8b(ctx, E, reps=10, eager=False):
     ms = (time_eager if eager else time_graph)(ctx, sweep, reps)
     gbs = total / (ms * 1e-3) / 1e9
     log(f"8B sweep {ms * 1e3:.1f} us for {total / 1e9:.3f} GB -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of peak)")
-    # each op type alone over the 8 layers (includes its activation quantization launch)
+    # each op type alone over the 8 layers (includes the activation quantization: inside the GEMV
+    # for K = 4096, a separate launch before it for the down GEMV's K = 14336)
     per_op = {}
     ops8 = {
         "MATMUL_N qkv 6144x4096": (lambda l: ctx.matmul_dev(bx.ptr, 1, 4096, [W[f"{l}.q"], W[f"{l}.k"], W[f"{l}.v"]],
@@ -271,7 +272,7 @@ def sweep_8b(ctx, E, reps=10, eager=False):
     for name, (fn, nbytes) in ops8.items():
         ums = timer(ctx, lambda: [fn(l) for l in range(8)], reps, inner=8) / 8
         per_op[name] = {"us": ums * 1e3, "weight_bytes": nbytes, "GBs": nbytes / (ums * 1e-3) / 1e9,
-                        "kernels_per_call": 2}
+                        "kernels_per_call": 2 if name.startswith("MATMUL down") else 1}
         log(f"  8B {name:26s} {ums * 1e3:8.2f} us  {per_op[name]['GBs']:7.0f} GB/s (weights+scales / time, incl. act quant)")
 
     # the down GEMV alone, pre-quantized activation (pure kernel time), all 8 layers
@@ -447,17 +448,26 @@ TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profile
 
 def pmc_workload(ctx, E):
     """The roofline kernels alone, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes: eager launches
-    of the SmolLM2 FFN_SWIGLU GEMV (the headline roofline kernel; 30 distinct layers) and of the 8B
-    down GEMV on a pre-quantized activation (8 distinct layers), 4 rounds each, plus a 64 MiB device
-    copy of known size whose counter readings calibrate the others."""
-    m = Model(ctx, 1234, {f"{l}.{n}": (HID, D) for l in range(L) for n in "gu"}, lambda n: 2)
+    of the SmolLM2 FFN_SWIGLU and MATMUL_ADD down GEMVs (the candidates for the headline roofline
+    kernel; 30 distinct layers each) and of the 8B down GEMV on a pre-quantized activation (8
+    distinct layers), 4 rounds each, plus a 64 MiB device copy of known size whose counter readings
+    calibrate the others."""
+    m = Model(ctx, 1234, {f"{l}.{n}": (HID, D) for l in range(L) for n in "gu"} |
+              {f"{l}.d": (D, HID) for l in range(L)}, lambda n: 2)
     bx = ctx.buffer(14336 * 4)
     bx.upload(np.random.default_rng(5).standard_normal(14336, dtype=np.float32))
     by = ctx.buffer(14336 * 4)
+    bres = ctx.buffer(D * 4)
+    bres.upload(np.random.default_rng(6).standard_normal(D, dtype=np.float32))
     for _ in range(4):
         for l in range(L):
             ctx.swiglu_dev(bx.ptr, 1, D, m.w[f"{l}.g"], m.w[f"{l}.u"], by.ptr, act=E.ACT_INT8)
     ctx.synchronize()
+    for _ in range(4):
+        for l in range(L):
+            ctx.matmul_dev(bx.ptr, 1, HID, [m.w[f"{l}.d"]], [by.ptr], [bres.ptr], act=E.ACT_INT8)
+    ctx.synchronize()
+    bres.free()
     m.free()
     m = Model(ctx, 11, {f"{l}.d": (4096, 14336) for l in range(8)}, lambda n: 2)
     q, d, s = ctx.buffer(14336), ctx.buffer(448 * 4), ctx.buffer(448 * 4)
@@ -544,7 +554,7 @@ def main():
     dom_name, dom = max(((k, v) for k, v in per.items() if v["kernels_per_call"] == 1),
                         key=lambda kv: kv[1]["us"] * kv[1]["calls_per_step"])
     roof = {"kernel": dom_name, "bound": "hbm", "achieved": round(dom["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(dom["GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic("FFN_SWIGLU"),
+            "frac": round(dom["GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_name),
             "algorithmic_bytes_per_launch": dom["bytes"], "avg_launch_us": round(dom["us"], 3),
             "note": "SmolLM2-sized weights are L2/Infinity-Cache resident: latency-bound, see gemv_8b_w4a8 for HBM"}
     if "gemv_8b_w4a8" in extra:

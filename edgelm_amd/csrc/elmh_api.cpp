@@ -149,16 +149,18 @@ int stream_tpw(const DevWeight& w, int T, int tiles_total, int nsel) {
   return tpw;
 }
 
+// x (f32) goes to the small kernel, or with `stream` to the streaming one, which both quantize it
+// per workgroup; otherwise xq / xd / xs hold the pre-quantized activation (streaming kernel).
 int run_gemv_group(elmh_ctx* c, const float* x, const int8_t* xq, const float* xd, const int32_t* xs, int T,
                    int64_t K, const std::vector<int>& idx, elmh_weight* const* w, float* const* y,
-                   const float* const* res) {
+                   const float* const* res, bool stream = false) {
   for (size_t i0 = 0; i0 < idx.size(); i0 += kMaxTargets) {
     GemvArgs a{};
     const size_t n = std::min<size_t>(kMaxTargets, idx.size() - i0);
     const DevWeight& w0 = w[idx[i0]]->w;
     int all_tiles = 0, tiles[kMaxTargets];
     for (size_t j = 0; j < n; ++j) all_tiles += tiles[j] = (int)(w[idx[i0 + j]]->w.rows_pad / w0.H);
-    a.tpw = x ? 1 : stream_tpw(w0, T, all_tiles, 1);
+    a.tpw = x && !stream ? 1 : stream_tpw(w0, T, all_tiles, 1);
     int wgs = 0;
     a.H = w0.H;
     for (size_t j = 0; j < n; ++j) {
@@ -171,6 +173,7 @@ int run_gemv_group(elmh_ctx* c, const float* x, const int8_t* xq, const float* x
     a.n_targets = (int)n;
     a.total_tiles = wgs;
     a.x = x;
+    a.stream = stream;
     a.xq = xq;
     a.xd = xd;
     a.xs = xs;
@@ -300,11 +303,14 @@ int run_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight
   int nt = 4;
   for (int i = 0; i < n; ++i) nt = std::min(nt, gemv_tokens(w[i]->w, 1, qin));
   if (T <= nt) {
-    if (!qin && (rc = quant_rows(c, x, T, K))) return rc;
+    // f32 x to the kernel (each workgroup quantizes it) unless it is too long for the streaming
+    // kernel's registers: then one quantizer launch first
+    const bool xin = qin || stream_qin_ok(T, (int)K);
+    if (!xin && (rc = quant_rows(c, x, T, K))) return rc;
     for (const auto& g : groups)
-      if ((rc = run_gemv_group(c, qin ? x : nullptr, qin ? nullptr : (const int8_t*)c->xq.p,
-                               qin ? nullptr : (const float*)c->xd.p, qin ? nullptr : (const int32_t*)c->xs.p, T, K,
-                               g, w, y, res)))
+      if ((rc = run_gemv_group(c, xin ? x : nullptr, xin ? nullptr : (const int8_t*)c->xq.p,
+                               xin ? nullptr : (const float*)c->xd.p, xin ? nullptr : (const int32_t*)c->xs.p, T, K,
+                               g, w, y, res, !qin)))
         return rc;
     return ELMH_OK;
   }
@@ -358,7 +364,8 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
   const int nt = gemv_tokens(g, 2, qin);
   if (act == ELMH_ACT_INT8 && T <= nt) {
     GemvArgs a{};
-    if (!qin && (rc = quant_rows(c, x, T, K))) return rc;
+    const bool xin = qin || stream_qin_ok(T, (int)K);  // as in run_matmul
+    if (!xin && (rc = quant_rows(c, x, T, K))) return rc;
     const int tiles = (int)(g.rows_pad / g.H);
     a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, tiles};
     a.tg[1] = {u.data, u.scales, y, nullptr, (int)u.rows, tiles};
@@ -366,10 +373,11 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
     a.total_tiles = tiles;
     a.H = g.H;
     a.tpw = 1;
-    a.x = qin ? x : nullptr;
-    a.xq = qin ? nullptr : (const int8_t*)c->xq.p;
-    a.xd = qin ? nullptr : (const float*)c->xd.p;
-    a.xs = qin ? nullptr : (const int32_t*)c->xs.p;
+    a.x = xin ? x : nullptr;
+    a.stream = !qin;
+    a.xq = xin ? nullptr : (const int8_t*)c->xq.p;
+    a.xd = xin ? nullptr : (const float*)c->xd.p;
+    a.xs = xin ? nullptr : (const int32_t*)c->xs.p;
     a.T = T;
     a.K = (int)K;
     a.nb = (int)(K / kBlock);

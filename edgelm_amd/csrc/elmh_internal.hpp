@@ -19,6 +19,16 @@ constexpr int kStreamWavesLong = 7;
 inline int stream_producers(int nb) {
   return 64 * (nb > kStreamFoldWaveBlocks ? kStreamWavesLong : kStreamWavesShort);
 }
+// The streaming GEMV can also take f32 activations and quantize them in each workgroup: every
+// producer thread holds 4 values per pass, at most kStreamQinPasses passes. Only for rows without
+// the fold wave (K <= 8192): every workgroup reads and rounds the whole activation, which at the
+// 8B down GEMV's K = 14336 (57 KB of f32 per workgroup) costs more than a separate quantizer
+// launch whose int8 result the workgroups copy (measured: 16.4 vs 11.6 us per call).
+constexpr int kStreamQinPasses = 8;
+inline bool stream_qin_ok(int T, int K) {
+  return K % kBlock == 0 && K / kBlock <= kStreamFoldWaveBlocks &&
+         T * K <= kStreamQinPasses * 4 * stream_producers(K / kBlock);
+}
 constexpr int kGemmTileN = 128;  // weight rows per GEMM workgroup
 constexpr int kGemmTileT = 128;  // tokens per GEMM workgroup
 constexpr int kPadRows = 64;     // rows_pad is a multiple of this
@@ -64,6 +74,7 @@ struct GemvArgs {
   int H;
   int tpw;            // tiles per workgroup (streaming kernel; tile_start then counts workgroups)
   const float* x;     // f32 [T][K] (quantized inside each workgroup) or null
+  int stream;         // with x: the streaming kernel (else the small one) quantizes it
   const int8_t* xq;   // int8 [T][K] row-major (pre-quantized) when x is null
   const float* xd;    // f32 [T][nb]
   const int32_t* xs;  // int32 [T][nb] block sums of q

@@ -612,7 +612,7 @@ __device__ __forceinline__ float fold_range(float acc, const float* row, int b0,
 // only the last batch's share is left once the last weight has arrived. Without the fold wave
 // (FW false: short rows, where the extra wave costs more than the chain) the producers fold at
 // the end, one lane per (token, row).
-template <int WDT, int NT, bool SW, int IPT, int NPW, int DEPTH, bool FW>
+template <int WDT, int NT, bool SW, int IPT, int NPW, int DEPTH, bool FW, bool QIN>
 __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const GemvArgs a) {
   constexpr int P = 64 * NPW;  // producer threads
   extern __shared__ __align__(16) unsigned char smem[];
@@ -680,9 +680,21 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
   // would put them behind the waits below instead of all in flight at once.
   if (T < 0) tg.y[0] = 0.f;
 
-  // 1. activation (int8 values, block scales and, for q4, block sums) straight into LDS, where
-  // its rows are contiguous (K % 16 == 0): wave w copies chunks w, w + NPW, ... of 1 KB (256 B).
-  {
+  // 1. activation. QIN: the f32 values, four per producer thread per pass (eight 32-blocks per
+  // wave), quantized below once they have landed. Otherwise the pre-quantized int8 values, block
+  // scales and, for q4, block sums straight into LDS, where its rows are contiguous (K % 16 == 0):
+  // wave w copies chunks w, w + NPW, ... of 1 KB (256 B).
+  constexpr int QP = QIN ? kStreamQinPasses : 1;
+  float4 xv[QP];
+  if (QIN) {
+    const int nel = T * K;
+#pragma unroll
+    for (int p = 0; p < QP; ++p) {
+      const float* px = a.x + min((p * P + tid) * 4, nel - 4);  // passes past the end repeat the last float4
+      xv[p] = make_float4(px[0], px[1], px[2], px[3]);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // these loads go out before the weight requests
+  } else {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int nq = T * K, nd = T * nb;
     for (int c = wave; c * 1024 < nq; c += NPW)
@@ -693,7 +705,7 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
         if (WDT == WQ4) dma4(a.xs + c * 64 + lane, (unsigned char*)(L.s + c * 64));
       }
   }
-  asm volatile("" ::: "memory");  // the weight requests below stay behind the activation's
+  if (!QIN) asm volatile("" ::: "memory");  // the weight requests below stay behind the activation's
   // 2. weight items of the first DEPTH batches in flight; batch u + DEPTH is requested once batch
   // u's products are out, so a wave whose requests stall (full memory queues) has already done
   // every product whose data has arrived. Requests past the last item repeat it.
@@ -716,8 +728,31 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
   for (int u = 0; u < D0; ++u) request(u);
   asm volatile("" ::: "memory");  // these loads issued before anything waits
   // 3. the activation has landed once at most this wave's weight loads (two per item) are still
-  // in flight; the barrier makes every wave's part visible
-  wait_vm<2 * D0>();
+  // in flight (QIN: the compiler's wait for each pass's values, loaded first, leaves the weights in
+  // flight); QIN quantizes it into LDS (edgelm's per-block rounding); the barrier makes every
+  // wave's part visible
+  if (QIN) {
+    const int nel = T * K;
+#pragma unroll
+    for (int p = 0; p < QP; ++p) {
+      if (p * P * 4 < nel) {  // whole waves: nel is a multiple of 32
+        const int e = (p * P + tid) * 4;
+        const float v[4] = {xv[p].x, xv[p].y, xv[p].z, xv[p].w};
+        int q[4], sum;
+        const float d = quant_block8x4(v, q, sum);
+        if (e < nel) {
+          const int g = e >> 5, t = g / nb, b = g - t * nb;
+          *reinterpret_cast<uint32_t*>(L.q + t * L.kpad + b * kBlock + (e & 31)) = pack_q4(q);
+          if ((e & 31) == 0) {
+            L.d[t * nb + b] = d;
+            if (WDT == WQ4) L.s[t * nb + b] = sum;
+          }
+        }
+      }
+    }
+  } else {
+    wait_vm<2 * D0>();
+  }
   __syncthreads();
   float e_res = 0.f, e_s = 1.f;
   if (!FW) chain_epilogue_operands<WDT, SW>(a, tg, tile0 * H, R, rows, tid, e_res, e_s);
@@ -1600,15 +1635,15 @@ int gemv_stream_ipt(int dtype, int items, int producers) {
   return per <= 4 ? 4 : per <= 8 ? 8 : 16;
 }
 
-template <int WDT, int NT, bool SW, int NPW, bool FW>
+template <int WDT, int NT, bool SW, int NPW, bool FW, bool QIN>
 static hipError_t stream_launch(const GemvArgs& a, int wgs, size_t lds, int items, hipStream_t s) {
   constexpr int threads = 64 * (NPW + FW);
   switch (gemv_stream_ipt(WDT, items, 64 * NPW)) {
-    case 4: gemv_stream_kernel<WDT, NT, SW, 4, NPW, FW ? 2 : 4, FW><<<wgs, threads, lds, s>>>(a); break;
-    case 8: gemv_stream_kernel<WDT, NT, SW, 8, NPW, FW ? 2 : 4, FW><<<wgs, threads, lds, s>>>(a); break;
+    case 4: gemv_stream_kernel<WDT, NT, SW, 4, NPW, FW ? 2 : 4, FW, QIN><<<wgs, threads, lds, s>>>(a); break;
+    case 8: gemv_stream_kernel<WDT, NT, SW, 8, NPW, FW ? 2 : 4, FW, QIN><<<wgs, threads, lds, s>>>(a); break;
     case 16:
       if (WDT == WQ4) {
-        gemv_stream_kernel<WDT, NT, SW, 16, NPW, FW ? 2 : 4, FW><<<wgs, threads, lds, s>>>(a);
+        gemv_stream_kernel<WDT, NT, SW, 16, NPW, FW ? 2 : 4, FW, QIN><<<wgs, threads, lds, s>>>(a);
         break;
       }
       return hipErrorInvalidValue;
@@ -1617,23 +1652,29 @@ static hipError_t stream_launch(const GemvArgs& a, int wgs, size_t lds, int item
   return hipGetLastError();
 }
 
+template <int WDT, int NT, bool SW, int NPW, bool FW>
+static hipError_t stream_go(const GemvArgs& a, int wgs, size_t lds, int items, hipStream_t s) {
+  if (a.x) return stream_launch<WDT, NT, SW, NPW, FW, true>(a, wgs, lds, items, s);
+  return stream_launch<WDT, NT, SW, NPW, FW, false>(a, wgs, lds, items, s);
+}
+
 template <int WDT, int NT, bool SW>
 static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
   if (a.T > NT) return hipErrorInvalidValue;
-  const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.x ? a.H : a.tpw * a.H, SW ? 2 : 1);
+  const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.x && !a.stream ? a.H : a.tpw * a.H, SW ? 2 : 1);
   if (lds > 64 * 1024) return hipErrorInvalidValue;
-  if (a.x) {
+  if (a.x && !a.stream) {
     if (!gemv_qin_ok(a.T, a.K) || (a.K & 31) || (a.H & (a.H - 1)) || a.T * a.H * (SW ? 2 : 1) > kGemvThreads)
       return hipErrorInvalidValue;
     gemv_small_kernel<WDT, NT, SW><<<tiles, kGemvThreads, lds, s>>>(a);
     return hipGetLastError();
   }
   if (a.tpw < 1 || a.T * a.tpw * a.H > kStreamFoldLanes || a.T * a.K > kStreamMaxAct || (a.K & 15) ||
-      (a.H & (a.H - 1)) || a.H > 64 || a.tpw * a.nb > 4096)
+      (a.H & (a.H - 1)) || a.H > 64 || a.tpw * a.nb > 4096 || (a.x && !stream_qin_ok(a.T, a.K)))
     return hipErrorInvalidValue;
   const int items = (SW ? 2 : 1) * a.tpw * a.H * a.nb;
-  if (a.nb > kStreamFoldWaveBlocks) return stream_launch<WDT, NT, SW, kStreamWavesLong, true>(a, tiles, lds, items, s);
-  return stream_launch<WDT, NT, SW, kStreamWavesShort, false>(a, tiles, lds, items, s);
+  if (a.nb > kStreamFoldWaveBlocks) return stream_go<WDT, NT, SW, kStreamWavesLong, true>(a, tiles, lds, items, s);
+  return stream_go<WDT, NT, SW, kStreamWavesShort, false>(a, tiles, lds, items, s);
 }
 
 template <int WDT, bool SW>
