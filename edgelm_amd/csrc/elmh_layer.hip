@@ -435,29 +435,58 @@ __device__ __forceinline__ ArgBest arg_pick(ArgBest a, ArgBest b) {
 
 // one workgroup of kArgThreads per row
 constexpr int kArgThreads = 1024;
+constexpr int kArgVF = 12;  // float4 per thread per batch: 49,152 logits in one batch
 
 __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __restrict__ x, int64_t n,
                                                              int32_t* __restrict__ out) {
   __shared__ float sv[kArgThreads / 64];
   __shared__ int si[kArgThreads / 64];
   const float* row = x + (int64_t)blockIdx.x * n;
-  ArgBest best{0.f, -1};
-  for (int64_t j = threadIdx.x; j < n; j += kArgThreads) {
-    const float v = row[j];
-    if (v == v || j == 0) best = arg_pick(best, ArgBest{v, (int)j});
+  const int tid = threadIdx.x;
+  // Each thread scans its values in increasing index: the first candidate is its first value that
+  // is not NaN (or index 0 whatever it is), then only a strictly greater value replaces it. That
+  // keeps the first index among equal values, lets a NaN at index 0 stand (nothing compares
+  // greater than it) and skips every later NaN: max_element's answer for the thread's values.
+  float bv = 0.f;
+  int bi = -1;
+  auto scan = [&](float v, int j) {
+    const bool take = bi < 0 ? (v == v || j == 0) : v > bv;
+    bv = take ? v : bv;
+    bi = take ? j : bi;
+  };
+  const int64_t n4 = n >> 2;
+  for (int64_t b0 = 0; b0 < n4; b0 += (int64_t)kArgThreads * kArgVF) {
+    float4 v[kArgVF];  // every load of the batch in flight before the first compare
+#pragma unroll
+    for (int u = 0; u < kArgVF; ++u) {
+      const float* p = row + 4 * min(b0 + tid + (int64_t)u * kArgThreads, n4 - 1);
+      v[u] = make_float4(p[0], p[1], p[2], p[3]);
+    }
+#pragma unroll
+    for (int u = 0; u < kArgVF; ++u) {
+      const int64_t q = b0 + tid + (int64_t)u * kArgThreads;
+      if (q < n4) {
+        scan(v[u].x, (int)(4 * q));
+        scan(v[u].y, (int)(4 * q + 1));
+        scan(v[u].z, (int)(4 * q + 2));
+        scan(v[u].w, (int)(4 * q + 3));
+      }
+    }
   }
+  for (int64_t j = 4 * n4 + tid; j < n; j += kArgThreads) scan(row[j], (int)j);
+  ArgBest best{bv, bi};
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const ArgBest o{__shfl_xor(best.v, off, 64), __shfl_xor(best.i, off, 64)};
     best = arg_pick(best, o);
   }
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0) {
     sv[wave] = best.v;
     si[wave] = best.i;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     ArgBest b{sv[0], si[0]};
     for (int w = 1; w < kArgThreads / 64; ++w) b = arg_pick(b, ArgBest{sv[w], si[w]});
     out[blockIdx.x] = b.i;  // n >= 1 and index 0 is always a candidate, so b.i >= 0
