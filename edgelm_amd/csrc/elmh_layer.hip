@@ -190,12 +190,13 @@ __device__ __forceinline__ float dot_row(const float* __restrict__ q, const floa
 // HD: the head size when it is known at compile time (64), else 0 (hd_arg)
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ q, float* __restrict__ out,
-                                                                 const float* __restrict__ kc,
-                                                                 const float* __restrict__ vc, int pos0,
+                                                                 float* __restrict__ kc, float* __restrict__ vc, int pos0,
                                                                  const int* __restrict__ pos_dev, int n_heads, int n_kv,
                                                                  int hd_arg, int max_ctx, int n_cap,
                                                                  const float* __restrict__ rcos,
-                                                                 const float* __restrict__ rsin) {
+                                                                 const float* __restrict__ rsin,
+                                                                 const float* __restrict__ knew,
+                                                                 const float* __restrict__ vnew) {
   const int hd = HD ? HD : hd_arg;
   extern __shared__ float lds[];
   if (pos_dev) pos0 = *pos_dev;
@@ -203,6 +204,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
   float* qb = lds;
   float* sc = lds + hdp;
   float* vt = sc + ((n_cap + 63) & ~63);
+  float* kn = vt + attn_chunk_pos(hd) * hd;  // fused append: this step's rotated key and value
+  float* vn = kn + hdp;
   __shared__ float red[kAttnThreads / 64];
   __shared__ float inv_s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -221,21 +224,37 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
   } else {
     qa = qs[iq];
   }
-  const float* kh = kc + (int64_t)(h / grp) * max_ctx * hd;
-  const v4f* vh4 = reinterpret_cast<const v4f*>(vc + (int64_t)(h / grp) * max_ctx * hd);
+  const int kvh = h / grp;
+  const float* kh = kc + (int64_t)kvh * max_ctx * hd;
+  const v4f* vh4 = reinterpret_cast<const v4f*>(vc + (int64_t)kvh * max_ctx * hd);
   const int hd4 = hd / 4, cpos = attn_chunk_pos(hd), cf4 = cpos * hd4;
   const int total4 = n * hd4;  // the values to read, as float4 (hd % 4 == 0)
+  // With the append fused (one decode token: knew / vnew given), the last position's key and
+  // value come from knew / vnew through LDS, and the cache reads stop one row earlier (that row is
+  // being written by another workgroup of the kv group).
+  const bool fuse = knew != nullptr;
+  const int nc = fuse ? max(n - 1, 1) : n;  // cache rows read
+  float ka = 0.f, kb = 0.f, va = 0.f, vb = 0.f;
+  if (fuse) {
+    const float* ks = knew + kvh * hd;
+    const float* vs = vnew + kvh * hd;
+    const int ih = tid < h2 ? tid : 0;
+    ka = ks[ih];
+    kb = ks[ih + h2];
+    va = vs[ih];
+    vb = vs[ih + h2];
+  }
   // head size 64: this thread's first key row in flight from the start
   float4 kr[16];
   if (hd == 64) {
-    const float4* k4 = reinterpret_cast<const float4*>(kh + (int64_t)min(tid, n - 1) * hd);
+    const float4* k4 = reinterpret_cast<const float4*>(kh + (int64_t)min(tid, nc - 1) * hd);
 #pragma unroll
     for (int u = 0; u < 16; ++u) kr[u] = k4[u];
   }
   // chunk 0 of the values, also in flight from the start
   v4f vr[kAttnVF];
 #pragma unroll
-  for (int u = 0; u < kAttnVF; ++u) vr[u] = vh4[min(tid + u * kAttnThreads, total4 - 1)];
+  for (int u = 0; u < kAttnVF; ++u) vr[u] = vh4[min(tid + u * kAttnThreads, nc * hd4 - 1)];
   if (rcos) {
     if (tid < h2) {
       qb[tid] = qa * cr - qb2 * sr;
@@ -244,12 +263,31 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
   } else if (tid < hd) {
     qb[tid] = qa;
   }
+  if (fuse && tid < h2) {
+    // step 1 of cpu::attention for this token (kv_append_kernel's arithmetic): rotated key and the
+    // value into LDS, and into the cache by the kv group's first workgroup
+    const float k0 = rcos ? ka * cr - kb * sr : ka, k1 = rcos ? kb * cr + ka * sr : kb;
+    kn[tid] = k0;
+    kn[tid + h2] = k1;
+    vn[tid] = va;
+    vn[tid + h2] = vb;
+    if (h % grp == 0) {
+      float* kd = kc + ((int64_t)kvh * max_ctx + pos) * hd;
+      float* vd = vc + ((int64_t)kvh * max_ctx + pos) * hd;
+      kd[tid] = k0;
+      kd[tid + h2] = k1;
+      vd[tid] = va;
+      vd[tid + h2] = vb;
+    }
+  }
   __syncthreads();
   const float scale = 1.0f / sqrtf((float)hd);
   float mx = -INFINITY;
   for (int j = tid; j < n; j += kAttnThreads) {
     float d;
-    if (hd == 64 && j == tid) {  // the preloaded row: dot_f32_scalar's order
+    if (fuse && j == n - 1) {
+      d = dot4(qb, kn, hd);
+    } else if (hd == 64 && j == tid) {  // the preloaded row: dot_f32_scalar's order
       float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
@@ -305,7 +343,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
       const int rel = tid + u * kAttnThreads;
       if (rel < cf4) {
         const float pj = e[u] * inv;
-        const v4f pr = v4f{pj * vr[u].x, pj * vr[u].y, pj * vr[u].z, pj * vr[u].w};
+        v4f val = vr[u];
+        if (fuse && (f + rel) / hd4 == n - 1) val = reinterpret_cast<const v4f*>(vn)[(f + rel) - (n - 1) * hd4];
+        const v4f pr = v4f{pj * val.x, pj * val.y, pj * val.z, pj * val.w};
         vt4[rel] = f + rel < total4 ? pr : v4f{0.f, 0.f, 0.f, 0.f};
       }
     }
@@ -316,7 +356,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     const int fn = f0 + cf4;
     if (fn < total4) {  // the next chunk into registers while this one is accumulated
 #pragma unroll
-      for (int u = 0; u < kAttnVF; ++u) vr[u] = vh4[min(fn + tid + u * kAttnThreads, total4 - 1)];
+      for (int u = 0; u < kAttnVF; ++u) vr[u] = vh4[min(fn + tid + u * kAttnThreads, nc * hd4 - 1)];
     }
     __syncthreads();  // this chunk's products are in LDS
     if (wave == 0) {
@@ -515,7 +555,8 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, in
 }
 
 size_t attention_lds_bytes(int hd, int n_max) {
-  return ((size_t)((hd + 3) & ~3) + (size_t)((n_max + 63) & ~63) + (size_t)attn_chunk_pos(hd) * hd) * sizeof(float);
+  const size_t hdp = (size_t)((hd + 3) & ~3);
+  return (3 * hdp + (size_t)((n_max + 63) & ~63) + (size_t)attn_chunk_pos(hd) * hd) * sizeof(float);
 }
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
@@ -523,15 +564,21 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
                             const float* rcos, const float* rsin, hipStream_t s) {
   // with the position in device memory the score buffer covers the whole cache
   const int n_cap = pos_dev ? max_ctx : pos0 + T;  // score slots
-  kv_append_kernel<<<T * n_kv, 64, 0, s>>>(k, v, kc, vc, pos0, pos_dev, n_kv, hd, max_ctx, rcos, rsin);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  // one token: the append runs inside the attention kernel; a chunk appends every key first
+  const bool fuse = T == 1;
+  if (!fuse) {
+    kv_append_kernel<<<T * n_kv, 64, 0, s>>>(k, v, kc, vc, pos0, pos_dev, n_kv, hd, max_ctx, rcos, rsin);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const float* kn = fuse ? k : nullptr;
+  const float* vn = fuse ? v : nullptr;
   if (hd == 64)
     attention_kernel<64><<<T * n_heads, kAttnThreads, attention_lds_bytes(hd, n_cap), s>>>(
-        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin);
+        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin, kn, vn);
   else
     attention_kernel<0><<<T * n_heads, kAttnThreads, attention_lds_bytes(hd, n_cap), s>>>(
-        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin);
+        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin, kn, vn);
   return hipGetLastError();
 }
 
