@@ -42,6 +42,8 @@ struct elmh_ctx {
   DevBuf xq, xd, xs;
   // SwiGLU fallback (gate/up of different layouts)
   DevBuf gu;
+  // RMSNORM output when it cannot be fused into the matmul after it
+  DevBuf nrm;
 };
 
 namespace {
@@ -153,7 +155,7 @@ int stream_tpw(const DevWeight& w, int T, int tiles_total, int nsel) {
 // per workgroup; otherwise xq / xd / xs hold the pre-quantized activation (streaming kernel).
 int run_gemv_group(elmh_ctx* c, const float* x, const int8_t* xq, const float* xd, const int32_t* xs, int T,
                    int64_t K, const std::vector<int>& idx, elmh_weight* const* w, float* const* y,
-                   const float* const* res, bool stream = false) {
+                   const float* const* res, bool stream = false, const float* nw = nullptr, float eps = 0.f) {
   for (size_t i0 = 0; i0 < idx.size(); i0 += kMaxTargets) {
     GemvArgs a{};
     const size_t n = std::min<size_t>(kMaxTargets, idx.size() - i0);
@@ -174,6 +176,8 @@ int run_gemv_group(elmh_ctx* c, const float* x, const int8_t* xq, const float* x
     a.total_tiles = wgs;
     a.x = x;
     a.stream = stream;
+    a.nw = nw;
+    a.eps = eps;
     a.xq = xq;
     a.xd = xd;
     a.xs = xs;
@@ -324,7 +328,7 @@ int run_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight
 }
 
 int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight* wg, const elmh_weight* wu, float* y,
-               int act, int mode) {
+               int act, int mode, const float* nw = nullptr, float eps = 0.f) {
   if (!wg || !wu || !y) return fail(c, ELMH_ERR_ARG, "swiglu: null weight or output");
   if (T < 1 || wg->w.cols != K || wu->w.cols != K) return fail(c, ELMH_ERR_ARG, "swiglu: bad shape");
   if (wg->w.rows != wu->w.rows) return fail(c, ELMH_ERR_ARG, "swiglu: gate and up row counts differ");
@@ -362,6 +366,7 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
   }
   const bool qin = use_small_gemv(T, K, g.data_bytes + g.scale_bytes + u.data_bytes + u.scale_bytes);
   const int nt = gemv_tokens(g, 2, qin);
+  if (nw && !(qin && act == ELMH_ACT_INT8 && T <= nt)) return fail(c, ELMH_ERR_UNSUPPORTED, "swiglu: fused rmsnorm off the small path");
   if (act == ELMH_ACT_INT8 && T <= nt) {
     GemvArgs a{};
     const bool xin = qin || stream_qin_ok(T, (int)K);  // as in run_matmul
@@ -375,6 +380,8 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
     a.tpw = 1;
     a.x = xin ? x : nullptr;
     a.stream = !qin;
+    a.nw = nw;  // set only when this small path applies (norm_fusable)
+    a.eps = eps;
     a.xq = xin ? nullptr : (const int8_t*)c->xq.p;
     a.xd = xin ? nullptr : (const float*)c->xd.p;
     a.xs = xin ? nullptr : (const int32_t*)c->xs.p;
@@ -401,6 +408,30 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
   a.nb = (int)(K / kBlock);
   a.fast = mode == ELMH_FAST;
   HIP_OR_FAIL(c, launch_gemm_a8(g.dtype, 1, token, a, tiles, c->stream));
+  return ELMH_OK;
+}
+
+// True if RMSNORM of x can run inside the int8-activation small GEMV that consumes it: the small
+// (workgroup-quantizing) kernel applies to every target at this T and K.
+bool norm_fusable(int T, int64_t K, int n, const elmh_weight* const* w, int nsel, int act) {
+  if (act != ELMH_ACT_INT8 || K % kBlock || K > 2048) return false;
+  size_t bytes = 0;
+  for (int i = 0; i < n; ++i) {
+    if (!a8_applies(w[i]->w)) return false;
+    bytes += w[i]->w.data_bytes + w[i]->w.scale_bytes;
+  }
+  if (!use_small_gemv(T, K, bytes)) return false;
+  for (int i = 0; i < n; ++i)
+    if (T > gemv_tokens(w[i]->w, nsel, true)) return false;
+  return true;
+}
+
+// RMSNORM into the scratch buffer (the path when it cannot be fused)
+int norm_to_scratch(elmh_ctx* c, const float* x, const float* nw, float eps, int T, int64_t K, const float** out) {
+  int rc;
+  if ((rc = ensure(c, c->nrm, (size_t)T * K * sizeof(float)))) return rc;
+  HIP_OR_FAIL(c, launch_rmsnorm(x, nw, (float*)c->nrm.p, T, (int)K, eps, c->stream));
+  *out = (const float*)c->nrm.p;
   return ELMH_OK;
 }
 
@@ -538,6 +569,7 @@ int elmh_reserve(elmh_ctx* c, int max_T, int64_t max_K) {
   if ((rc = ensure(c, c->xq, (size_t)(Tpad * max_K)))) return rc;
   if ((rc = ensure(c, c->xd, (size_t)(Tpad * nb) * sizeof(float)))) return rc;
   if ((rc = ensure(c, c->xs, (size_t)(Tpad * nb) * sizeof(int32_t)))) return rc;
+  if (max_K <= 8192 && (rc = ensure(c, c->nrm, (size_t)max_T * max_K * sizeof(float)))) return rc;
   return ELMH_OK;
 }
 
@@ -553,6 +585,38 @@ int elmh_swiglu_dev(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_we
   if (!c || !x) return fail(c, ELMH_ERR_ARG, "null ctx/x");
   DeviceGuard g(c);
   return run_swiglu(c, x, T, K, wg, wu, y, act, mode);
+}
+
+int elmh_rmsnorm_matmul_dev(elmh_ctx* c, const float* x, const float* norm_w, float eps, int T, int64_t K, int n,
+                            elmh_weight* const* w, float* const* y, const float* const* res, int act, int mode) {
+  if (!c || !x || !norm_w) return fail(c, ELMH_ERR_ARG, "null ctx/x/norm weight");
+  int rc = check_targets(c, T, K, n, w, y);
+  if (rc) return rc;
+  if (K > 8192) return fail(c, ELMH_ERR_ARG, "rmsnorm: dim %lld (1 .. 8192)", (long long)K);
+  DeviceGuard g(c);
+  if (norm_fusable(T, K, n, w, 1, act)) {
+    for (const auto& grp : by_dtype(n, w))
+      if ((rc = run_gemv_group(c, x, nullptr, nullptr, nullptr, T, K, grp, w, y, res, false, norm_w, eps))) return rc;
+    return ELMH_OK;
+  }
+  const float* xn;
+  if ((rc = norm_to_scratch(c, x, norm_w, eps, T, K, &xn))) return rc;
+  return run_matmul(c, xn, T, K, n, w, y, res, act, mode);
+}
+
+int elmh_rmsnorm_swiglu_dev(elmh_ctx* c, const float* x, const float* norm_w, float eps, int T, int64_t K,
+                            const elmh_weight* wg, const elmh_weight* wu, float* y, int act, int mode) {
+  if (!c || !x || !norm_w || !wg || !wu || !y) return fail(c, ELMH_ERR_ARG, "null ctx/x/norm weight/weight/y");
+  if (T < 1 || K < 1 || K > 8192) return fail(c, ELMH_ERR_ARG, "rmsnorm: bad shape T=%d dim=%lld", T, (long long)K);
+  DeviceGuard g(c);
+  const elmh_weight* const ws[2] = {wg, wu};
+  if (wg->w.dtype == wu->w.dtype && wg->w.H == wu->w.H && wg->w.rows == wu->w.rows && wg->w.cols == K &&
+      wu->w.cols == K && norm_fusable(T, K, 2, ws, 2, act))
+    return run_swiglu(c, x, T, K, wg, wu, y, act, mode, norm_w, eps);
+  const float* xn;
+  int rc;
+  if ((rc = norm_to_scratch(c, x, norm_w, eps, T, K, &xn))) return rc;
+  return run_swiglu(c, xn, T, K, wg, wu, y, act, mode);
 }
 
 int elmh_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight* const* w, float* const* y,
@@ -758,7 +822,7 @@ int elmh_embed_dev(elmh_ctx* c, const int32_t* tokens, int T, const elmh_weight*
 
 int elmh_rmsnorm_dev(elmh_ctx* c, const float* x, const float* w, float* y, int rows, int dim, float eps) {
   if (!c || !x || !w || !y) return fail(c, ELMH_ERR_ARG, "null ctx/x/w/y");
-  if (rows < 1 || dim < 1 || dim > 16384) return fail(c, ELMH_ERR_ARG, "rmsnorm: rows %d, dim %d (1 .. 16384)", rows, dim);
+  if (rows < 1 || dim < 1 || dim > 8192) return fail(c, ELMH_ERR_ARG, "rmsnorm: rows %d, dim %d (1 .. 8192)", rows, dim);
   DeviceGuard g(c);
   HIP_OR_FAIL(c, launch_rmsnorm(x, w, y, rows, dim, eps, c->stream));
   return ELMH_OK;

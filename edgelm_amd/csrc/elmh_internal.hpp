@@ -75,6 +75,8 @@ struct GemvArgs {
   int tpw;            // tiles per workgroup (streaming kernel; tile_start then counts workgroups)
   const float* x;     // f32 [T][K] (quantized inside each workgroup) or null
   int stream;         // with x: the streaming kernel (else the small one) quantizes it
+  const float* nw;    // small kernel: x is RMSNORM's input; nw [K] its weight, eps its epsilon
+  float eps;
   const int8_t* xq;   // int8 [T][K] row-major (pre-quantized) when x is null
   const float* xd;    // f32 [T][nb]
   const int32_t* xs;  // int32 [T][nb] block sums of q

@@ -461,7 +461,11 @@ __device__ __forceinline__ GemvTarget gemv_target(const GemvArgs& a, int& wg) {
 constexpr int kSmallPass = kGemvThreads * 4;
 constexpr int kSmallMaxAct = 4 * kSmallPass;
 
-template <int WDT, int NT, bool SW>
+// NORM: x is the un-normalized row and the workgroup applies edgelm's RMSNORM to it first
+// (cpu::rmsnorm, kernels_cpu.cpp:326-335, in the order of rmsnorm_kernel: squares grouped by
+// dot_f32_scalar's four accumulators, four in-order sums, (s0 + s1) + (s2 + s3), then
+// (x * inv) * w), so that RMSNORM and the matmul after it take one launch.
+template <int WDT, int NT, bool SW, bool NORM>
 __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int G = WDT == WQ8 ? 32 : 16;
@@ -474,10 +478,22 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   const int per_sel = H * nb, items = (SW ? 2 : 1) * per_sel;
   const int nel = T * K;
 
-  // 1. activation values (first: their wait does not cover the weight loads issued next)
+  // 1. activation values (first: their wait does not cover the weight loads issued next); with
+  // NORM every pass's values and norm weights (loads past the end repeat the last float4)
   const int e0 = tid * 4;
+  constexpr int XP = NORM ? kSmallMaxAct / kSmallPass : 1;
   float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (e0 < nel) x0 = *reinterpret_cast<const float4*>(a.x + e0);
+  float4 xv[XP], nv[XP];
+  if (NORM) {
+#pragma unroll
+    for (int p = 0; p < XP; ++p) {
+      const int e = min(p * kSmallPass + e0, nel - 4);
+      xv[p] = *reinterpret_cast<const float4*>(a.x + e);
+      nv[p] = *reinterpret_cast<const float4*>(a.nw + (e - e / K * K));
+    }
+  } else if (e0 < nel) {
+    x0 = *reinterpret_cast<const float4*>(a.x + e0);
+  }
   // 2. weights of this thread's first two items
   v4u w[2][G / 16];
   float wsc[2] = {0.f, 0.f};
@@ -496,14 +512,58 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   // 3. epilogue operands of the folding lanes
   float e_res, e_s;
   chain_epilogue_operands<WDT, SW>(a, tg, tile * H, H, H, tid, e_res, e_s);
-  // 4. quantize: block g = e0 / 32 spread over 8 consecutive lanes (4 values each)
-  for (int pass = 0; pass * kSmallPass < nel; ++pass) {
-    const int e = pass * kSmallPass + e0;
-    if (pass > 0) {
-      x0 = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (e < nel) x0 = *reinterpret_cast<const float4*>(a.x + e);
+  if (NORM) {
+    // 3b. RMSNORM of the T rows: squares to LDS as [t][accumulator][rowlen] (zero-padded: adding
+    // +0.0 to a sum of squares changes nothing), lanes 4t .. 4t+3 sum row t's four accumulators,
+    // inv_t = 1 / sqrt(ss / K + eps); then every value becomes (x * inv_t) * w
+    const int K4 = K >> 2, rowlen = (K4 + 31) & ~31;
+    float* sq = L.p + (SW ? 2 : 1) * NT * H * L.pst;
+    float* inv_l = sq + NT * 4 * rowlen;
+#pragma unroll
+    for (int p = 0; p < XP; ++p) {
+      const int e = p * kSmallPass + e0;
+      if (e < nel) {
+        const int t = e / K;
+        float* r = sq + t * 4 * rowlen + ((e - t * K) >> 2);
+        r[0] = xv[p].x * xv[p].x;
+        r[rowlen] = xv[p].y * xv[p].y;
+        r[2 * rowlen] = xv[p].z * xv[p].z;
+        r[3 * rowlen] = xv[p].w * xv[p].w;
+      }
     }
-    const float v[4] = {x0.x, x0.y, x0.z, x0.w};
+    const int padw = rowlen - K4;
+    for (int i = tid; i < T * 4 * padw; i += kGemvThreads) sq[(i / padw) * rowlen + K4 + i % padw] = 0.f;
+    __syncthreads();
+    if (tid < 4 * T) {
+      const float4* row = reinterpret_cast<const float4*>(sq + tid * rowlen);
+      float sacc = 0.f;
+      for (int q0 = 0; q0 < (rowlen >> 2); q0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = row[q0 + i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          sacc = sacc + v[i].x;
+          sacc = sacc + v[i].y;
+          sacc = sacc + v[i].z;
+          sacc = sacc + v[i].w;
+        }
+      }
+      const float s01 = sacc + dpp_f<kDppQuadXor1>(sacc);
+      const float ss = s01 + dpp_f<kDppQuadXor2>(s01);
+      if ((tid & 3) == 0) inv_l[tid >> 2] = 1.0f / sqrtf(ss / (float)K + a.eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < XP; ++p) {
+      const float inv = inv_l[min(p * kSmallPass + e0, nel - 4) / K];
+      xv[p] = make_float4((xv[p].x * inv) * nv[p].x, (xv[p].y * inv) * nv[p].y, (xv[p].z * inv) * nv[p].z,
+                          (xv[p].w * inv) * nv[p].w);
+    }
+  }
+  // 4. quantize: block g = e0 / 32 spread over 8 consecutive lanes (4 values each)
+  auto quantize = [&](int e, const float4 xx) {
+    const float v[4] = {xx.x, xx.y, xx.z, xx.w};
     int qv[4], qs;
     const float sc = quant_block8x4(v, qv, qs);
     if (e < nel) {
@@ -513,6 +573,20 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
         L.d[t * nb + b] = sc;
         L.s[t * nb + b] = qs;
       }
+    }
+  };
+  if (NORM) {
+#pragma unroll
+    for (int p = 0; p < XP; ++p)
+      if (p * kSmallPass < nel) quantize(p * kSmallPass + e0, xv[p]);
+  } else {
+    for (int pass = 0; pass * kSmallPass < nel; ++pass) {
+      const int e = pass * kSmallPass + e0;
+      if (pass > 0) {
+        x0 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (e < nel) x0 = *reinterpret_cast<const float4*>(a.x + e);
+      }
+      quantize(e, x0);
     }
   }
   __syncthreads();
@@ -1666,11 +1740,18 @@ static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
   if (a.x && !a.stream) {
     if (!gemv_qin_ok(a.T, a.K) || (a.K & 31) || (a.H & (a.H - 1)) || a.T * a.H * (SW ? 2 : 1) > kGemvThreads)
       return hipErrorInvalidValue;
-    gemv_small_kernel<WDT, NT, SW><<<tiles, kGemvThreads, lds, s>>>(a);
+    if (a.nw) {
+      const size_t rowlen = ((size_t)(a.K / 4) + 31) & ~(size_t)31;
+      const size_t ldsn = lds + ((size_t)NT * 4 * rowlen + 4) * sizeof(float);
+      if (ldsn > 64 * 1024) return hipErrorInvalidValue;
+      gemv_small_kernel<WDT, NT, SW, true><<<tiles, kGemvThreads, ldsn, s>>>(a);
+    } else {
+      gemv_small_kernel<WDT, NT, SW, false><<<tiles, kGemvThreads, lds, s>>>(a);
+    }
     return hipGetLastError();
   }
   if (a.tpw < 1 || a.T * a.tpw * a.H > kStreamFoldLanes || a.T * a.K > kStreamMaxAct || (a.K & 15) ||
-      (a.H & (a.H - 1)) || a.H > 64 || a.tpw * a.nb > 4096 || (a.x && !stream_qin_ok(a.T, a.K)))
+      (a.H & (a.H - 1)) || a.H > 64 || a.tpw * a.nb > 4096 || (a.x && !stream_qin_ok(a.T, a.K)) || a.nw)
     return hipErrorInvalidValue;
   const int items = (SW ? 2 : 1) * a.tpw * a.H * a.nb;
   if (a.nb > kStreamFoldWaveBlocks) return stream_go<WDT, NT, SW, kStreamWavesLong, true>(a, tiles, lds, items, s);

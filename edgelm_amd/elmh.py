@@ -213,6 +213,20 @@ class Context:
         self._check(lib().elmh_rmsnorm_dev(self.h, C.c_void_p(x_ptr), C.c_void_p(w_ptr), C.c_void_p(y_ptr),
                                            C.c_int(rows), C.c_int(dim), C.c_float(eps)))
 
+    def rmsnorm_matmul_dev(self, x_ptr, nw_ptr, eps, T, K, weights, y_ptrs, res_ptrs=None, act=ACT_INT8, mode=EXACT):
+        n = len(weights)
+        wp = (C.c_void_p * n)(*[w.h.value for w in weights])
+        yp = (C.c_void_p * n)(*y_ptrs)
+        rp = None if res_ptrs is None else (C.c_void_p * n)(*res_ptrs)
+        self._check(lib().elmh_rmsnorm_matmul_dev(self.h, C.c_void_p(x_ptr), C.c_void_p(nw_ptr), C.c_float(eps),
+                                                  C.c_int(T), C.c_int64(K), C.c_int(n), wp, yp, rp, C.c_int(act),
+                                                  C.c_int(mode)))
+
+    def rmsnorm_swiglu_dev(self, x_ptr, nw_ptr, eps, T, K, wg, wu, y_ptr, act=ACT_INT8, mode=EXACT):
+        self._check(lib().elmh_rmsnorm_swiglu_dev(self.h, C.c_void_p(x_ptr), C.c_void_p(nw_ptr), C.c_float(eps),
+                                                  C.c_int(T), C.c_int64(K), wg.h, wu.h, C.c_void_p(y_ptr),
+                                                  C.c_int(act), C.c_int(mode)))
+
     def attention_dev(self, q_ptr, k_ptr, v_ptr, out_ptr, T, pos0, n_heads, n_kv, head_dim, kc_ptr, vc_ptr, max_ctx,
                       cos_ptr=None, sin_ptr=None):
         self._check(lib().elmh_attention_dev(

@@ -110,6 +110,21 @@ class HipBackend : public Backend {
       }
     if (g.output >= 0) host_needed_[g.output] = 1;
     output_ = g.output >= 0 && on_dev_[g.output] ? g.output : -1;
+    // RMSNORM whose output only feeds the matmul right after it, both here: one fused call
+    std::vector<int> readers(nt, 0);
+    for (const Op& op : g.ops)
+      for (int t : op.in) ++readers[t];
+    fuse_norm_.assign(g.ops.size(), 0);
+    for (const Partition& p : parts) {
+      if (p.backend != this) continue;
+      for (int i = p.begin; i + 1 < p.end; ++i) {
+        const Op &a = g.ops[i], &b = g.ops[i + 1];
+        const int t = a.type == OpType::RMSNORM ? a.out[0] : -1;
+        fuse_norm_[i] = t >= 0 && !host_needed_[t] && readers[t] == 1 && !b.in.empty() && b.in[0] == t &&
+                        (b.type == OpType::MATMUL || b.type == OpType::MATMUL_N || b.type == OpType::MATMUL_ADD ||
+                         b.type == OpType::FFN_SWIGLU);
+      }
+    }
     act_.assign(nt, Buf{});
     release_pins();
     pin_.assign(nt, Pin{});
@@ -164,14 +179,23 @@ class HipBackend : public Backend {
   void run(const Op& op, ExecContext& c) override {
     if (!ctx_) throw std::runtime_error("edgelm: hip backend created for planning only");
     if (!prepared_) unprepared(*c.graph);
-    if (&op - c.graph->ops.data() == first_op_) ++epoch_;  // a new forward
+    const int idx = static_cast<int>(&op - c.graph->ops.data());
+    if (idx == first_op_) ++epoch_;  // a new forward
+    // a deferred RMSNORM (fuse_norm_) applies to this op's input inside the matmul call
+    const bool normed = norm_.op == idx - 1 && norm_.op >= 0;
+    if (!normed) norm_.op = -1;
     switch (op.type) {
       case OpType::FFN_SWIGLU: {
         const int T = static_cast<int>(c.rows(op.in[0]));
         const int64_t K = c.tensor(op.in[1]).cols;
-        check(elmh_swiglu_dev(ctx_, in(op.in[0], c), T, K, weight(c.tensor(op.in[1])), weight(c.tensor(op.in[2])),
-                              out(op.out[0], c), act(c), ELMH_EXACT),
-              op);
+        if (normed)
+          check(elmh_rmsnorm_swiglu_dev(ctx_, norm_.x, norm_.w, norm_.eps, T, K, weight(c.tensor(op.in[1])),
+                                        weight(c.tensor(op.in[2])), out(op.out[0], c), act(c), ELMH_EXACT),
+                op);
+        else
+          check(elmh_swiglu_dev(ctx_, in(op.in[0], c), T, K, weight(c.tensor(op.in[1])), weight(c.tensor(op.in[2])),
+                                out(op.out[0], c), act(c), ELMH_EXACT),
+                op);
         break;
       }
       case OpType::MATMUL:
@@ -183,15 +207,20 @@ class HipBackend : public Backend {
         w_.resize(n);
         y_.resize(n);
         r_.assign(n, nullptr);
-        const float* x = in(op.in[0], c);
+        const float* x = normed ? nullptr : in(op.in[0], c);
         for (size_t i = 0; i < n; ++i) {
           w_[i] = weight(c.tensor(op.in[1 + i]));
           y_[i] = out(op.out[i], c);
         }
         if (op.type == OpType::MATMUL_ADD) r_[0] = in(op.in[2], c);
-        check(elmh_matmul_dev(ctx_, x, T, K, static_cast<int>(n), w_.data(), y_.data(),
-                              op.type == OpType::MATMUL_ADD ? r_.data() : nullptr, act(c), ELMH_EXACT),
-              op);
+        const float* const* res = op.type == OpType::MATMUL_ADD ? r_.data() : nullptr;
+        if (normed)
+          check(elmh_rmsnorm_matmul_dev(ctx_, norm_.x, norm_.w, norm_.eps, T, K, static_cast<int>(n), w_.data(),
+                                        y_.data(), res, act(c), ELMH_EXACT),
+                op);
+        else
+          check(elmh_matmul_dev(ctx_, x, T, K, static_cast<int>(n), w_.data(), y_.data(), res, act(c), ELMH_EXACT),
+                op);
         break;
       }
       case OpType::EMBED: {
@@ -206,6 +235,10 @@ class HipBackend : public Backend {
       }
       case OpType::RMSNORM: {
         const int rows = static_cast<int>(c.rows(op.in[0])), dim = static_cast<int>(c.tensor(op.in[0]).cols);
+        if (prepared_ && fuse_norm_[idx] && dim <= kMaxFusedNormDim) {
+          norm_ = {idx, in(op.in[0], c), f32_weight(c.tensor(op.in[1])), op.fattr[0]};
+          return;  // the next op runs it; its output is read by nothing else
+        }
         check(elmh_rmsnorm_dev(ctx_, in(op.in[0], c), f32_weight(c.tensor(op.in[1])), out(op.out[0], c), rows, dim,
                                op.fattr[0]),
               op);
@@ -493,6 +526,14 @@ class HipBackend : public Backend {
   int first_op_ = -1;
   uint64_t epoch_ = 0;
   std::vector<char> on_dev_, host_needed_;
+  std::vector<char> fuse_norm_;  // op index: an RMSNORM that the next op (a matmul) applies
+  struct PendingNorm {
+    int op = -1;
+    const float* x = nullptr;
+    const float* w = nullptr;
+    float eps = 0.f;
+  } norm_;
+  static constexpr int kMaxFusedNormDim = 8192;  // elmh_rmsnorm_matmul_dev's limit
   int output_ = -1;          // graph output when this backend writes it (prepare), else -1
   bool keep_out_ = false;    // keep_output(true): the output is not copied to the host arena
   int32_t* dev_tok_ = nullptr;  // argmax result

@@ -116,8 +116,21 @@ int elmh_gemv_a8_dev(elmh_ctx* ctx, const int8_t* q, const float* d, const int32
  * elmh_upload_weight; token ids must lie in [0, rows) (the caller checks, as edgelm does). */
 int elmh_embed_dev(elmh_ctx* ctx, const int32_t* tokens, int T, const elmh_weight* table, float* y);
 /* RMSNORM (cpu::rmsnorm, kernels_cpu.cpp:326-335): y = x * (1 / sqrt(dot_f32(x, x) / dim + eps)) * w
- * per row, dot_f32 in the four-accumulator order of dot_f32_scalar (kernels_cpu.cpp:30-43). */
+ * per row, dot_f32 in the four-accumulator order of dot_f32_scalar (kernels_cpu.cpp:30-43);
+ * dim <= 8192. */
 int elmh_rmsnorm_dev(elmh_ctx* ctx, const float* x, const float* w, float* y, int rows, int dim, float eps);
+/* RMSNORM followed by the matmul or SwiGLU that consumes it, as one call: the same results as
+ * elmh_rmsnorm_dev into a buffer and then elmh_matmul_dev / elmh_swiglu_dev on it (bit for bit),
+ * for the edgelm op pairs RMSNORM -> MATMUL_N and RMSNORM -> FFN_SWIGLU of a layer
+ * (passes.cpp:72-81,100-104; cpu::rmsnorm kernels_cpu.cpp:326-335). With int8 activations on
+ * rows short enough for the workgroup-quantizing GEMV (T <= 4, K <= 2048) each workgroup
+ * normalizes the rows itself and the normalized activation never goes to memory; otherwise the
+ * normalized rows go to a scratch buffer (reserved by elmh_reserve) first. K <= 8192. */
+int elmh_rmsnorm_matmul_dev(elmh_ctx* ctx, const float* x, const float* norm_w, float eps, int T, int64_t K,
+                            int n_targets, elmh_weight* const* w, float* const* y, const float* const* residual,
+                            int act, int mode);
+int elmh_rmsnorm_swiglu_dev(elmh_ctx* ctx, const float* x, const float* norm_w, float eps, int T, int64_t K,
+                            const elmh_weight* wg, const elmh_weight* wu, float* y, int act, int mode);
 /* ATTENTION (cpu::attention, kernels_cpu.cpp:417-488; AttnArgs, kernels.hpp:28-36): appends this
  * step's keys (rotated when rope_cos/rope_sin, the RopeTable's [pos][head_dim/2] arrays, are given)
  * and values to the cache [n_kv][max_ctx][head_dim] at positions pos0 .. pos0+T-1, then
