@@ -204,8 +204,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
   float* qb = lds;
   float* sc = lds + hdp;
   float* vt = sc + ((n_cap + 63) & ~63);
-  float* kn = vt + attn_chunk_pos(hd) * hd;  // fused append: this step's rotated key and value
-  float* vn = kn + hdp;
+  float* kn = vt + attn_chunk_pos(hd) * hd;  // fused append: this step's rotated key
   __shared__ float red[kAttnThreads / 64];
   __shared__ float inv_s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -229,9 +228,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
   const v4f* vh4 = reinterpret_cast<const v4f*>(vc + (int64_t)kvh * max_ctx * hd);
   const int hd4 = hd / 4, cpos = attn_chunk_pos(hd), cf4 = cpos * hd4;
   const int total4 = n * hd4;  // the values to read, as float4 (hd % 4 == 0)
-  // With the append fused (one decode token: knew / vnew given), the last position's key and
-  // value come from knew / vnew through LDS, and the cache reads stop one row earlier (that row is
-  // being written by another workgroup of the kv group).
+  // With the append fused (one decode token: knew / vnew given), the last position's key comes
+  // from knew (rotated, through LDS) and its value from vnew, and the cache reads stop one row
+  // earlier (that row is being written by another workgroup of the kv group).
   const bool fuse = knew != nullptr;
   const int nc = fuse ? max(n - 1, 1) : n;  // cache rows read
   float ka = 0.f, kb = 0.f, va = 0.f, vb = 0.f;
@@ -242,19 +241,26 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     ka = ks[ih];
     kb = ks[ih + h2];
     va = vs[ih];
-    vb = vs[ih + h2];
+    vb = vs[ih + h2];  // for the cache write
   }
   // head size 64: this thread's first key row in flight from the start
   float4 kr[16];
-  if (hd == 64) {
-    const float4* k4 = reinterpret_cast<const float4*>(kh + (int64_t)min(tid, nc - 1) * hd);
+  if (hd == 64) {  // fused: the last position's row is knew's (rotated below, before its score)
+    const float* krow = fuse && tid == n - 1 ? knew + kvh * hd : kh + (int64_t)min(tid, nc - 1) * hd;
+    const float4* k4 = reinterpret_cast<const float4*>(krow);
 #pragma unroll
     for (int u = 0; u < 16; ++u) kr[u] = k4[u];
   }
-  // chunk 0 of the values, also in flight from the start
+  // chunk 0 of the values, also in flight from the start; with the append fused, the last
+  // position's float4s are read from vnew (one load either way: the address is selected)
+  const v4f* vnb = fuse ? reinterpret_cast<const v4f*>(vnew + kvh * hd) : vh4;
+  auto vsrc = [&](int f) {
+    const int fl = f - (n - 1) * hd4;
+    return fuse && fl >= 0 ? vnb + fl : vh4 + f;
+  };
   v4f vr[kAttnVF];
 #pragma unroll
-  for (int u = 0; u < kAttnVF; ++u) vr[u] = vh4[min(tid + u * kAttnThreads, nc * hd4 - 1)];
+  for (int u = 0; u < kAttnVF; ++u) vr[u] = *vsrc(min(tid + u * kAttnThreads, total4 - 1));
   if (rcos) {
     if (tid < h2) {
       qb[tid] = qa * cr - qb2 * sr;
@@ -264,13 +270,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     qb[tid] = qa;
   }
   if (fuse && tid < h2) {
-    // step 1 of cpu::attention for this token (kv_append_kernel's arithmetic): rotated key and the
-    // value into LDS, and into the cache by the kv group's first workgroup
+    // step 1 of cpu::attention for this token (kv_append_kernel's arithmetic): the rotated key into
+    // LDS, key and value into the cache by the kv group's first workgroup
     const float k0 = rcos ? ka * cr - kb * sr : ka, k1 = rcos ? kb * cr + ka * sr : kb;
     kn[tid] = k0;
     kn[tid + h2] = k1;
-    vn[tid] = va;
-    vn[tid + h2] = vb;
     if (h % grp == 0) {
       float* kd = kc + ((int64_t)kvh * max_ctx + pos) * hd;
       float* vd = vc + ((int64_t)kvh * max_ctx + pos) * hd;
@@ -285,7 +289,20 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
   float mx = -INFINITY;
   for (int j = tid; j < n; j += kAttnThreads) {
     float d;
-    if (fuse && j == n - 1) {
+    if (hd == 64 && fuse && rcos && j == n - 1 && j == tid) {
+      // this step's key, preloaded unrotated: kv_append_kernel's rotation of pairs (i, i + 32)
+      const float4* c4 = reinterpret_cast<const float4*>(rcos + (int64_t)pos * h2);
+      const float4* s4 = reinterpret_cast<const float4*>(rsin + (int64_t)pos * h2);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float4 cc = c4[u], ss = s4[u], ka4 = kr[u], kb4 = kr[u + 8];
+        kr[u] = make_float4(ka4.x * cc.x - kb4.x * ss.x, ka4.y * cc.y - kb4.y * ss.y, ka4.z * cc.z - kb4.z * ss.z,
+                            ka4.w * cc.w - kb4.w * ss.w);
+        kr[u + 8] = make_float4(kb4.x * cc.x + ka4.x * ss.x, kb4.y * cc.y + ka4.y * ss.y, kb4.z * cc.z + ka4.z * ss.z,
+                                kb4.w * cc.w + ka4.w * ss.w);
+      }
+    }
+    if (fuse && j == n - 1 && !(hd == 64 && j == tid)) {  // the step's key from LDS
       d = dot4(qb, kn, hd);
     } else if (hd == 64 && j == tid) {  // the preloaded row: dot_f32_scalar's order
       float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
@@ -343,9 +360,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
       const int rel = tid + u * kAttnThreads;
       if (rel < cf4) {
         const float pj = e[u] * inv;
-        v4f val = vr[u];
-        if (fuse && (f + rel) / hd4 == n - 1) val = reinterpret_cast<const v4f*>(vn)[(f + rel) - (n - 1) * hd4];
-        const v4f pr = v4f{pj * val.x, pj * val.y, pj * val.z, pj * val.w};
+        const v4f pr = v4f{pj * vr[u].x, pj * vr[u].y, pj * vr[u].z, pj * vr[u].w};
         vt4[rel] = f + rel < total4 ? pr : v4f{0.f, 0.f, 0.f, 0.f};
       }
     }
@@ -356,7 +371,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     const int fn = f0 + cf4;
     if (fn < total4) {  // the next chunk into registers while this one is accumulated
 #pragma unroll
-      for (int u = 0; u < kAttnVF; ++u) vr[u] = vh4[min(fn + tid + u * kAttnThreads, nc * hd4 - 1)];
+      for (int u = 0; u < kAttnVF; ++u) vr[u] = *vsrc(min(fn + tid + u * kAttnThreads, total4 - 1));
     }
     __syncthreads();  // this chunk's products are in LDS
     if (wave == 0) {
@@ -556,7 +571,7 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, in
 
 size_t attention_lds_bytes(int hd, int n_max) {
   const size_t hdp = (size_t)((hd + 3) & ~3);
-  return (3 * hdp + (size_t)((n_max + 63) & ~63) + (size_t)attn_chunk_pos(hd) * hd) * sizeof(float);
+  return (2 * hdp + (size_t)((n_max + 63) & ~63) + (size_t)attn_chunk_pos(hd) * hd) * sizeof(float);
 }
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
