@@ -16,6 +16,8 @@
 #include "elm_quant.h"
 #include "elmh_internal.hpp"
 
+#include <cstring>
+
 namespace elmh {
 namespace {
 
@@ -1424,6 +1426,173 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const GemmArgs a) {
   }
 }
 
+// The same per-wave scheme with 16 x 16 tiles (v_mfma_i32_16x16x32_i8: lane l supplies row
+// l % 16 of A and column l % 16 of B, K elements 8 (l / 16) .. + 7 each, and holds
+// D[4 (l / 16) + i][l % 16]). A quarter of the outputs per wave: four times the waves on a
+// problem, and a quarter of the per-block rescale, the serial part of a wave (one dependent
+// convert-multiply-add per output and block). Used when 32 x 32 waves would not fill the chip.
+constexpr int kWave16 = 16;
+
+template <int WDT, bool SW, bool TOK>
+struct Wave16Ops {
+  static constexpr int NSEL = SW ? 2 : 1;
+  static constexpr bool BLOCKX = !TOK;
+  long A;
+  long B[NSEL];
+  float c[NSEL];               // q4: ws / 16 of the lane's row and block
+  float4 xv;                   // block scales of the lane's 4 tokens
+};
+
+__device__ __forceinline__ long q4_operand8(uint2 w, int h) {
+  const int sh = 4 - 4 * h;
+  const uint32_t lo = ((w.x << sh) & 0xF0F0F0F0u) ^ 0x80808080u, hi = ((w.y << sh) & 0xF0F0F0F0u) ^ 0x80808080u;
+  return (long)(((uint64_t)hi << 32) | lo);
+}
+
+template <int WDT, bool SW, bool TOK, bool FAST, int DEPTH = kWaveDepth>
+__global__ __launch_bounds__(256) void gemm_wave16_kernel(const GemmArgs a) {
+  typedef Wave16Ops<WDT, SW, TOK> Ops;
+  constexpr int NSEL = Ops::NSEL;
+  constexpr bool BLOCKX = Ops::BLOCKX;
+  const int lane = threadIdx.x & 63, l16 = lane & 15, c4 = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int nb = a.nb, H = a.H;
+  const int ngroups = (a.T + kWave16 - 1) / kWave16;
+  // wave -> (target, 16-row tile, 16-token group), token group fastest
+  int rt = (int)blockIdx.x * 4 + wave;
+  const int g = rt % ngroups;
+  rt /= ngroups;
+  int ti = 0;
+  const int n = SW ? 1 : a.n_targets;
+  for (; ti < n; ++ti) {
+    const int cnt = (a.tg[ti].N + kWave16 - 1) / kWave16;
+    if (rt < cnt) break;
+    rt -= cnt;
+  }
+  if (ti >= n) return;  // past the last tile (uniform per wave; no barrier below)
+  const GemmTarget tg = SW ? a.tg[0] : gemm_target_at(ti);
+  const int r0 = rt * kWave16, t0 = g * kWave16;
+  const int rows_pad = (tg.N + kPadRows - 1) / kPadRows * kPadRows;
+  const int wrow = min(r0 + l16, rows_pad - 1);
+  const int64_t rbase = (int64_t)(wrow / H) * nb * H + (wrow % H);  // item of (wrow, block 0)
+  const uint8_t* const wd[2] = {tg.data, SW ? a.tg[1].data : tg.data};
+  const float* const wsc[2] = {tg.scales, SW ? a.tg[1].scales : tg.scales};
+  // token t0 + l16 of the 32-token fragment (xq layout: lane h*32 + t%32 holds elements h*16 ..
+  // h*16 + 15 of token t), elements 8 c4 .. 8 c4 + 7
+  const int8_t* const xg = a.xq + (int64_t)(t0 >> 5) * nb * 1024 + ((c4 >> 1) * 32 + (t0 & 31) + l16) * 16 + (c4 & 1) * 8;
+
+  auto load = [&](int blk, Ops& o) {
+    blk = min(blk, nb - 1);
+    o.A = *reinterpret_cast<const long*>(xg + (int64_t)blk * 1024);
+    const int64_t it = rbase + (int64_t)blk * H;
+#pragma unroll
+    for (int s = 0; s < NSEL; ++s) {
+      if (WDT == WQ8) {
+        o.B[s] = *reinterpret_cast<const long*>(wd[s] + it * 32 + c4 * 8);
+        o.c[s] = 1.f;
+      } else {
+        o.B[s] = q4_operand8(*reinterpret_cast<const uint2*>(wd[s] + it * 16 + (c4 & 1) * 8), c4 >> 1);
+        o.c[s] = wsc[s][it];
+      }
+    }
+    if (BLOCKX) o.xv = *reinterpret_cast<const float4*>(a.xd + (int64_t)blk * a.Tpad + t0 + 4 * c4);
+  };
+
+  v4i iacc[NSEL];
+  float facc[NSEL][4];
+  const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < NSEL; ++s) {
+    iacc[s] = zero;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) facc[s][i] = 0.f;
+  }
+  auto rescale = [&](const Ops& o, const v4i (&S)[NSEL]) {
+    const float xv[4] = {o.xv.x, o.xv.y, o.xv.z, o.xv.w};
+#pragma unroll
+    for (int s = 0; s < NSEL; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // q8: p = float(S) * xd; q4 (S = 16 * S_b, c = ws / 16): p = float(S) * (c * xd)
+        const float m = WDT == WQ8 ? xv[BLOCKX ? i : 0] : BLOCKX ? o.c[s] * xv[i] : o.c[s];
+        if (FAST) {
+          facc[s][i] = __builtin_fmaf((float)S[s][i], m, facc[s][i]);
+        } else {
+          facc[s][i] = facc[s][i] + (float)S[s][i] * m;
+        }
+      }
+  };
+
+  Ops ops[DEPTH];
+#pragma unroll
+  for (int k = 0; k < DEPTH; ++k) load(k, ops[k]);
+  for (int b0 = 0; b0 < nb; b0 += DEPTH) {
+    if (TOK && WDT == WQ8) {
+#pragma unroll
+      for (int k = 0; k < DEPTH; ++k) {
+        if (b0 + k < nb)
+#pragma unroll
+          for (int s = 0; s < NSEL; ++s) iacc[s] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ops[k].A, ops[k].B[s], iacc[s], 0, 0, 0);
+        load(b0 + k + DEPTH, ops[k]);  // unconditional (clamped): exact wait counts
+      }
+    } else {
+      v4i S[DEPTH][NSEL];
+#pragma unroll
+      for (int k = 0; k < DEPTH; ++k)
+#pragma unroll
+        for (int s = 0; s < NSEL; ++s) S[k][s] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ops[k].A, ops[k].B[s], zero, 0, 0, 0);
+#pragma unroll
+      for (int k = 0; k < DEPTH; ++k) {
+        if (b0 + k < nb) rescale(ops[k], S[k]);
+        load(b0 + k + DEPTH, ops[k]);
+      }
+    }
+  }
+
+  // epilogue: row r0 + l16, tokens t0 + 4 c4 + i (accumulator i)
+  const int r = r0 + l16;
+  const int rc = min(r, tg.N - 1);
+  const int tv = min(kWave16, a.T - t0);
+  const uint32_t tbytes = (uint32_t)tv * (uint32_t)tg.N * 4u;
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(tg.y + (int64_t)t0 * tg.N, (short)0, (int)tbytes, 0x00020000);
+  float xt[4] = {1.f, 1.f, 1.f, 1.f};
+  if (TOK) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xt[i] = a.xd[min(t0 + 4 * c4 + i, a.Tpad - 1)];
+  }
+  auto value = [&](int s, int i, float ws) {
+    if (WDT == WQ8) return TOK ? ((float)iacc[s][i] * xt[i]) * ws : facc[s][i] * ws;
+    return TOK ? facc[s][i] * xt[i] : facc[s][i];
+  };
+  const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
+  if (SW) {
+    const float wsu = WDT == WQ8 ? a.tg[1].scales[rc] : 1.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int off = r < tg.N ? ((4 * c4 + i) * tg.N + r) * 4 : 0x7FFFFFF0;
+      const float out = silu_exact(value(0, i, ws)) * value(NSEL - 1, i, wsu);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), ry, off, 0, 0);
+    }
+    return;
+  }
+  const bool has_res = tg.res != nullptr;
+  const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(has_res ? tg.res + (int64_t)t0 * tg.N : tg.y), (short)0, has_res ? (int)tbytes : 0, 0x00020000);
+  float res[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int off = r < tg.N ? ((4 * c4 + i) * tg.N + r) * 4 : 0x7FFFFFF0;
+    res[i] = has_res ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, off, 0, 0)) : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int off = r < tg.N ? ((4 * c4 + i) * tg.N + r) * 4 : 0x7FFFFFF0;
+    float out = value(0, i, ws);
+    if (has_res) out = out + res[i];
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), ry, off, 0, 0);
+  }
+}
+
 // ---------------------------------------------------------------- f32-activation paths
 
 // T == 1 (kernels_cpu.cpp:366-368, 397-399 with dot_row): one lane per weight row.
@@ -1793,6 +1962,18 @@ static void gemm_wave_launch(const GemmArgs& a, hipStream_t s) {
 }
 
 template <int WDT, bool SW, bool TOK>
+static void gemm_wave16_launch(const GemmArgs& a, hipStream_t s) {
+  int rows = 0;
+  for (int i = 0; i < (SW ? 1 : a.n_targets); ++i) rows += (a.tg[i].N + kWave16 - 1) / kWave16;
+  const int waves = rows * ((a.T + kWave16 - 1) / kWave16);
+  const dim3 grid((waves + 3) / 4);
+  if (a.fast && !(TOK && WDT == WQ8))
+    gemm_wave16_kernel<WDT, SW, TOK, true><<<grid, 256, 0, s>>>(a);
+  else
+    gemm_wave16_kernel<WDT, SW, TOK, false><<<grid, 256, 0, s>>>(a);
+}
+
+template <int WDT, bool SW, bool TOK>
 static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
   if (a.Tpad % kGemmTileT || a.T < 1 || a.T > a.Tpad || tiles < 1 ||
       tiles != (SW ? a.tg[0].ntiles : a.tile_start[a.n_targets]))
@@ -1818,9 +1999,17 @@ static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
     small = ev[0] == '6' ? true : ev[0] == '1' ? false : small;
     wave = false;
   }
-  if (const char* ev = getenv("ELMH_GEMM_KERNEL")) wave = ev[0] == 'w' ? true : ev[0] == 'r' ? false : wave;
+  // 16 x 16 waves unless 32 x 32 waves already fill the chip
+  bool wave32 = false;
+  if (const char* ev = getenv("ELMH_GEMM_KERNEL")) {
+    wave = ev[0] == 'w' ? true : ev[0] == 'r' ? false : wave;
+    wave32 = std::strcmp(ev, "wave32") == 0;
+  }
   if (wave) {
-    gemm_wave_launch<WDT, SW, TOK>(a, s);
+    if (wave32)
+      gemm_wave_launch<WDT, SW, TOK>(a, s);
+    else
+      gemm_wave16_launch<WDT, SW, TOK>(a, s);
     return hipGetLastError();
   }
   if (small)

@@ -360,11 +360,11 @@ def test_gemm_token_tiles(ctx, dt, tile, monkeypatch):
         d.free()
 
 
-@pytest.mark.parametrize("kernel", ["wave", "ring"])
+@pytest.mark.parametrize("kernel", ["wave", "wave32", "ring"])
 @pytest.mark.parametrize("dt", [O.Q8, O.Q4])
 def test_gemm_kernels_small_and_ragged(ctx, dt, kernel, monkeypatch):
-    """Both GEMM kernels forced (ELMH_GEMM_KERNEL): the one-wave-per-32x32-tile kernel that small
-    problems select, and the LDS-ring kernel. Ragged rows and tokens (partial 32-row and 32-token
+    """Every GEMM kernel forced (ELMH_GEMM_KERNEL): one wave per 16x16 tile (what small problems
+    select), one wave per 32x32 tile, and the LDS-ring kernel. Ragged rows and tokens (partial
     tiles), MATMUL_N with a residual, FFN_SWIGLU, per-block exact and fast, per-token, and an odd
     block count."""
     monkeypatch.setenv("ELMH_GEMM_KERNEL", kernel)
