@@ -421,6 +421,135 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
   }
 }
 
+// Prefill (T > 1, head size 64): one workgroup per (head, kAttnQ consecutive query tokens), wave w
+// for query t0 + w. Keys and values are read once for the group's queries instead of once per
+// query, and the per-query chains (the sum of the exponentials, lane 0; the 64 output sums, one
+// per lane) run in the four waves at once. Same float operations in the same order as
+// attention_kernel (cpu::attention): scores by dot_f32_scalar's order, max, expf(s - max), the sum
+// in increasing position, p_j = e_j * inv, o_i += p_j * v_j[i] in increasing position.
+// LDS (dynamic): q [kAttnQ][64], scores [kAttnQ][n_cap rounded up to 64], values [kAttnPVPos][64].
+constexpr int kAttnQ = 4;
+constexpr int kAttnPVPos = 96;  // value rows per chunk (24 KB)
+
+__global__ __launch_bounds__(256) void attention_prefill_kernel(const float* __restrict__ q, float* __restrict__ out,
+                                                                const float* __restrict__ kc,
+                                                                const float* __restrict__ vc, int pos0, int T,
+                                                                int n_heads, int n_kv, int max_ctx, int n_cap,
+                                                                const float* __restrict__ rcos,
+                                                                const float* __restrict__ rsin) {
+  constexpr int hd = 64, h2 = 32, hd4 = 16;
+  extern __shared__ float lds[];
+  const int scs = (n_cap + 63) & ~63;  // score row stride
+  float* qb = lds;                     // [kAttnQ][64]
+  float* sc = qb + kAttnQ * hd;        // [kAttnQ][scs]
+  float* vt = sc + kAttnQ * scs;       // [kAttnPVPos][64]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int ngr = (T + kAttnQ - 1) / kAttnQ;
+  const int h = blockIdx.x / ngr, t0 = (blockIdx.x - h * ngr) * kAttnQ;
+  const int nq = min(kAttnQ, T - t0);               // queries in this group
+  const int tw = t0 + min(w, nq - 1), posw = pos0 + tw, nw = posw + 1;  // this wave's query
+  const int nmax = pos0 + t0 + nq;                  // positions of the group's last query
+  const int qd = n_heads * hd, grp = n_heads / n_kv, kvh = h / grp;
+  const float* kh = kc + (int64_t)kvh * max_ctx * hd;
+  const float4* vh4 = reinterpret_cast<const float4*>(vc + (int64_t)kvh * max_ctx * hd);
+  // 1. q of the wave's query, rotated, into LDS
+  {
+    const float* qs = q + (int64_t)tw * qd + h * hd;
+    if (rcos) {
+      if (lane < h2) {
+        const float a = qs[lane], b = qs[lane + h2];
+        const float c = rcos[(int64_t)posw * h2 + lane], sn = rsin[(int64_t)posw * h2 + lane];
+        qb[w * hd + lane] = a * c - b * sn;
+        qb[w * hd + lane + h2] = b * c + a * sn;
+      }
+    } else {
+      qb[w * hd + lane] = qs[lane];
+    }
+  }
+  __syncthreads();
+  // 2. scores: thread j takes positions j, j + 256, ...: one key row, the group's dot products
+  const float scale = 1.0f / sqrtf((float)hd);
+  for (int j = tid; j < nmax; j += 256) {
+    float4 kr[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) kr[u] = reinterpret_cast<const float4*>(kh + (int64_t)j * hd)[u];
+#pragma unroll
+    for (int qi = 0; qi < kAttnQ; ++qi) {
+      if (qi < nq && j <= pos0 + t0 + qi) {
+        const float* qq = qb + qi * hd;
+        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          s0 = s0 + qq[4 * u] * kr[u].x;
+          s1 = s1 + qq[4 * u + 1] * kr[u].y;
+          s2 = s2 + qq[4 * u + 2] * kr[u].z;
+          s3 = s3 + qq[4 * u + 3] * kr[u].w;
+        }
+        sc[qi * scs + j] = ((s0 + s1) + (s2 + s3)) * scale;
+      }
+    }
+  }
+  __syncthreads();
+  // 3. per wave (query): max, exponentials (+0.0 past the last position, to a multiple of 64),
+  // the in-order sum by lane 0, p_j = e_j * inv
+  float* sw = sc + w * scs;
+  float mx = -INFINITY;
+  for (int j = lane; j < nw; j += 64) mx = fmaxf(mx, sw[j]);
+  mx = wave_max(mx);
+  const int n64 = (nw + 63) & ~63;
+  for (int j = lane; j < n64; j += 64) sw[j] = j < nw ? elm_expf(sw[j] - mx) : 0.f;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  float sum = 0.f;
+  if (lane == 0) {
+    const float4* s4 = reinterpret_cast<const float4*>(sw);
+    for (int j0 = 0; j0 < nw; j0 += 64) {
+      float4 e[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) e[u] = s4[(j0 >> 2) + u];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        sum = sum + e[u].x;
+        sum = sum + e[u].y;
+        sum = sum + e[u].z;
+        sum = sum + e[u].w;
+      }
+    }
+  }
+  const float inv = 1.0f / __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sum)));
+  __builtin_amdgcn_wave_barrier();
+  for (int j = lane; j < nw; j += 64) sw[j] = sw[j] * inv;
+  // 4. values by chunks of whole positions into LDS (rows of 64; zero rows past the group's last
+  // position), then each wave adds p_j * v_j[lane] for its own positions in increasing j
+  float acc = 0.f;
+  float4* vt4 = reinterpret_cast<float4*>(vt);
+  for (int j0 = 0; j0 < nmax; j0 += kAttnPVPos) {
+    __syncthreads();  // every p_j written (first chunk); the previous chunk consumed
+    const int rows = min(kAttnPVPos, nmax - j0);
+    for (int f = tid; f < kAttnPVPos * hd4; f += 256)
+      vt4[f] = f < rows * hd4 ? vh4[(int64_t)j0 * hd4 + f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    __syncthreads();
+    const int m = min(rows, nw - j0);  // this query's positions in the chunk
+    auto batch = [&](int jj, int lim) {  // positions jj .. jj + 15, those below lim added
+      float4 pv[4];
+      float vv[16];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pv[u] = reinterpret_cast<const float4*>(sw + j0 + jj)[u];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) vv[u] = vt[(jj + u) * hd + lane];
+      const float pf[16] = {pv[0].x, pv[0].y, pv[0].z, pv[0].w, pv[1].x, pv[1].y, pv[1].z, pv[1].w,
+                            pv[2].x, pv[2].y, pv[2].z, pv[2].w, pv[3].x, pv[3].y, pv[3].z, pv[3].w};
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (u < lim) acc = acc + pf[u] * vv[u];
+    };
+    int jj = 0;
+    for (; jj + 16 <= m; jj += 16) batch(jj, 16);
+    if (jj < m) batch(jj, m - jj);  // the last, partial batch
+  }
+  if (w < nq) out[(int64_t)tw * qd + h * hd + lane] = acc;
+}
+
 // ---------------------------------------------------------------- EMBED
 
 // y[t][k] = dequantize_row(table, tokens[t])[k] read from the repacked weight layout:
@@ -588,6 +717,13 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
   }
   const float* kn = fuse ? k : nullptr;
   const float* vn = fuse ? v : nullptr;
+  const size_t lds_pf = ((size_t)kAttnQ * hd + (size_t)kAttnQ * ((n_cap + 63) & ~63) + (size_t)kAttnPVPos * hd) * 4;
+  if (!fuse && hd == 64 && lds_pf <= 64 * 1024) {
+    const int ngr = (T + kAttnQ - 1) / kAttnQ;
+    attention_prefill_kernel<<<n_heads * ngr, 256, lds_pf, s>>>(q, out, kc, vc, pos0, T, n_heads, n_kv, max_ctx, n_cap,
+                                                                rcos, rsin);
+    return hipGetLastError();
+  }
   if (hd == 64)
     attention_kernel<64><<<T * n_heads, kAttnThreads, attention_lds_bytes(hd, n_cap), s>>>(
         q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin, kn, vn);
