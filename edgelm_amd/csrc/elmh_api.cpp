@@ -259,6 +259,18 @@ int quant_frag(elmh_ctx* c, const float* x, int T, int64_t K, int token_mode, in
   return ELMH_OK;
 }
 
+// RMSNORM and the block-scale fragment quantization in one launch (K <= 2048)
+int quant_frag_norm(elmh_ctx* c, const float* x, const float* nw, float eps, int T, int64_t K, int* Tpad_out) {
+  const int Tpad = (int)round_up(T, kGemmTileT);
+  const int64_t nb = K / kBlock;
+  int rc;
+  if ((rc = ensure(c, c->xq, (size_t)Tpad * K))) return rc;
+  if ((rc = ensure(c, c->xd, (size_t)Tpad * nb * sizeof(float)))) return rc;
+  HIP_OR_FAIL(c, launch_rmsnorm_quant_frag(x, nw, eps, T, Tpad, (int)K, (int8_t*)c->xq.p, (float*)c->xd.p, c->stream));
+  *Tpad_out = Tpad;
+  return ELMH_OK;
+}
+
 int quant_rows(elmh_ctx* c, const float* x, int T, int64_t K) {
   const int64_t nb = K / kBlock;
   int rc;
@@ -366,7 +378,8 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
   }
   const bool qin = use_small_gemv(T, K, g.data_bytes + g.scale_bytes + u.data_bytes + u.scale_bytes);
   const int nt = gemv_tokens(g, 2, qin);
-  if (nw && !(qin && act == ELMH_ACT_INT8 && T <= nt)) return fail(c, ELMH_ERR_UNSUPPORTED, "swiglu: fused rmsnorm off the small path");
+  if (nw && !(act == ELMH_ACT_INT8 && (T <= nt ? qin : K <= 2048)))
+    return fail(c, ELMH_ERR_UNSUPPORTED, "swiglu: fused rmsnorm off the small GEMV and block-scale GEMM paths");
   if (act == ELMH_ACT_INT8 && T <= nt) {
     GemvArgs a{};
     const bool xin = qin || stream_qin_ok(T, (int)K);  // as in run_matmul
@@ -393,7 +406,7 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
   }
   const int token = act == ELMH_ACT_INT8_TOKEN;
   int Tpad;
-  if ((rc = quant_frag(c, x, T, K, token, &Tpad))) return rc;
+  if ((rc = nw ? quant_frag_norm(c, x, nw, eps, T, K, &Tpad) : quant_frag(c, x, T, K, token, &Tpad))) return rc;
   GemmArgs a{};
   const int tiles = (int)((g.rows_pad + kGemmTileN - 1) / kGemmTileN);
   a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, tiles};
@@ -424,6 +437,21 @@ bool norm_fusable(int T, int64_t K, int n, const elmh_weight* const* w, int nsel
   for (int i = 0; i < n; ++i)
     if (T > gemv_tokens(w[i]->w, nsel, true)) return false;
   return true;
+}
+
+// True if the int8-activation (block scales) call takes the GEMM at this T (more tokens than the
+// GEMV takes) and K fits the fused RMSNORM + fragment quantizer.
+bool norm_gemm(int T, int64_t K, int n, const elmh_weight* const* w, int nsel, int act) {
+  if (act != ELMH_ACT_INT8 || K % kBlock || K > 2048) return false;
+  size_t bytes = 0;
+  for (int i = 0; i < n; ++i) {
+    if (!a8_applies(w[i]->w)) return false;
+    bytes += w[i]->w.data_bytes + w[i]->w.scale_bytes;
+  }
+  const bool qin = use_small_gemv(T, K, bytes);
+  int nt = 4;
+  for (int i = 0; i < n; ++i) nt = std::min(nt, gemv_tokens(w[i]->w, nsel, qin));
+  return T > nt;
 }
 
 // RMSNORM into the scratch buffer (the path when it cannot be fused)
@@ -599,6 +627,15 @@ int elmh_rmsnorm_matmul_dev(elmh_ctx* c, const float* x, const float* norm_w, fl
       if ((rc = run_gemv_group(c, x, nullptr, nullptr, nullptr, T, K, grp, w, y, res, false, norm_w, eps))) return rc;
     return ELMH_OK;
   }
+  if (norm_gemm(T, K, n, w, 1, act)) {  // the block-scale GEMM: RMSNORM inside its quantizer launch
+    int Tpad;
+    if ((rc = quant_frag_norm(c, x, norm_w, eps, T, K, &Tpad))) return rc;
+    for (const auto& grp : by_dtype(n, w))
+      if ((rc = run_gemm_group(c, (const int8_t*)c->xq.p, (const float*)c->xd.p, T, Tpad, K, grp, w, y, res, 0,
+                               mode == ELMH_FAST)))
+        return rc;
+    return ELMH_OK;
+  }
   const float* xn;
   if ((rc = norm_to_scratch(c, x, norm_w, eps, T, K, &xn))) return rc;
   return run_matmul(c, xn, T, K, n, w, y, res, act, mode);
@@ -611,7 +648,7 @@ int elmh_rmsnorm_swiglu_dev(elmh_ctx* c, const float* x, const float* norm_w, fl
   DeviceGuard g(c);
   const elmh_weight* const ws[2] = {wg, wu};
   if (wg->w.dtype == wu->w.dtype && wg->w.H == wu->w.H && wg->w.rows == wu->w.rows && wg->w.cols == K &&
-      wu->w.cols == K && norm_fusable(T, K, 2, ws, 2, act))
+      wu->w.cols == K && (norm_fusable(T, K, 2, ws, 2, act) || norm_gemm(T, K, 2, ws, 2, act)))
     return run_swiglu(c, x, T, K, wg, wu, y, act, mode, norm_w, eps);
   const float* xn;
   int rc;

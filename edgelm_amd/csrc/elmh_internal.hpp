@@ -120,6 +120,8 @@ hipError_t launch_act_quant_rows(const float* x, int T, int K, int8_t* xq, float
 // Fragment-major activation quantization for the MFMA GEMM: xq [Tpad/32][nb][1024], xd [nb][Tpad]
 // (rows t >= T are written as zeros).
 hipError_t launch_act_quant_frag(const float* x, int T, int Tpad, int K, int8_t* xq, float* xd, hipStream_t s);
+hipError_t launch_rmsnorm_quant_frag(const float* x, const float* nw, float eps, int T, int Tpad, int K, int8_t* xq,
+                                     float* xd, hipStream_t s);
 // Per-token scale (extension): xq fragment-major as above, xd [Tpad].
 hipError_t launch_act_quant_frag_token(const float* x, int T, int Tpad, int K, int8_t* xq, float* xd, hipStream_t s);
 

@@ -173,6 +173,88 @@ __global__ __launch_bounds__(256) void act_quant_frag_kernel(const float* __rest
   if (h == 0) xd[(int64_t)b * Tpad + t] = sc;
 }
 
+// RMSNORM and the GEMM's per-block activation quantization in one pass (the input of a layer's
+// QKV and gate/up GEMMs): kNqTok rows per workgroup, each normalized in rmsnorm_kernel's order
+// (squares grouped by dot_f32_scalar's accumulators in LDS, four in-order sums, (s0 + s1) +
+// (s2 + s3), then (x * inv) * w), then quantized into fragments exactly as act_quant_frag_kernel
+// does. Tokens at or past T give zero fragments and scales. K <= 2048.
+constexpr int kNqTok = 4;
+constexpr int kNqVF = 8;  // float4 of x per thread
+
+__global__ __launch_bounds__(256) void rmsnorm_quant_frag_kernel(const float* __restrict__ x, const float* __restrict__ nw,
+                                                                 float eps, int T, int Tpad, int K,
+                                                                 int8_t* __restrict__ xq, float* __restrict__ xd) {
+  extern __shared__ __align__(16) float nq_lds[];
+  __shared__ float inv_l[kNqTok];
+  const int K4 = K >> 2, rowlen = (K4 + 31) & ~31, nb = K / kBlock;
+  float* sq = nq_lds;                    // [kNqTok][4][rowlen]
+  float* yb = sq + kNqTok * 4 * rowlen;  // [kNqTok][K] normalized rows
+  const int t0 = blockIdx.x * kNqTok, tid = threadIdx.x, nf = kNqTok * K4;
+  float4 xv[kNqVF];
+#pragma unroll
+  for (int u = 0; u < kNqVF; ++u) {
+    const int f = tid + 256 * u;
+    const int r = f / K4, k4 = f - r * K4, t = t0 + r;
+    xv[u] = f < nf && t < T ? ld4(x + (int64_t)t * K + 4 * k4, 0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (f < nf) {
+      float* q = sq + r * 4 * rowlen + k4;
+      q[0] = xv[u].x * xv[u].x;
+      q[rowlen] = xv[u].y * xv[u].y;
+      q[2 * rowlen] = xv[u].z * xv[u].z;
+      q[3 * rowlen] = xv[u].w * xv[u].w;
+    }
+  }
+  const int padw = rowlen - K4;
+  for (int i = tid; i < kNqTok * 4 * padw; i += 256) sq[(i / padw) * rowlen + K4 + i % padw] = 0.f;
+  __syncthreads();
+  if (tid < 4 * kNqTok) {
+    const float4* row = reinterpret_cast<const float4*>(sq + tid * rowlen);
+    float sacc = 0.f;
+    for (int q0 = 0; q0 < (rowlen >> 2); q0 += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = row[q0 + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        sacc = sacc + v[i].x;
+        sacc = sacc + v[i].y;
+        sacc = sacc + v[i].z;
+        sacc = sacc + v[i].w;
+      }
+    }
+    const float s01 = sacc + dpp_f<kDppQuadXor1>(sacc);
+    const float ss = s01 + dpp_f<kDppQuadXor2>(s01);
+    if ((tid & 3) == 0) inv_l[tid >> 2] = 1.0f / sqrtf(ss / (float)K + eps);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kNqVF; ++u) {
+    const int f = tid + 256 * u;
+    if (f < nf) {
+      const int r = f / K4, k4 = f - r * K4;
+      const float inv = inv_l[r];
+      const float4 w4 = ld4(nw + 4 * k4, 0);
+      *reinterpret_cast<float4*>(yb + r * K + 4 * k4) =
+          make_float4((xv[u].x * inv) * w4.x, (xv[u].y * inv) * w4.y, (xv[u].z * inv) * w4.z, (xv[u].w * inv) * w4.w);
+    }
+  }
+  __syncthreads();
+  // items (row, block, half): the two halves of a block sit in neighbouring lanes
+  const int items = kNqTok * nb * 2;
+  for (int it = tid; it < items; it += 256) {
+    const int r = it / (2 * nb), rem = it - r * 2 * nb, b = rem >> 1, h = rem & 1, t = t0 + r;
+    const float* src = yb + r * K + b * kBlock + h * 16;
+    const float4 v[4] = {ld4(src, 0), ld4(src, 1), ld4(src, 2), ld4(src, 3)};
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a = amax4(v[i], a);
+    a = fmaxf(a, dpp_f<kDppQuadXor1>(a));
+    const float sc = a / 127.0f;
+    *reinterpret_cast<uint4*>(xq + frag_offset(t, b, h, nb)) = q8x16(v, sc == 0.f ? 1.f : sc);
+    if (h == 0) xd[(int64_t)b * Tpad + t] = sc;
+  }
+}
+
 // Per-token scale (extension): one workgroup per token row. NPER > 0: a thread keeps its NPER
 // half-blocks (j = tid + 256 i) in registers between the row amax and the rounding (K <= NPER * 4096);
 // NPER == 0 reads the row twice, the second time from cache.
@@ -1839,6 +1921,15 @@ hipError_t launch_act_quant_rows(const float* x, int T, int K, int8_t* xq, float
 hipError_t launch_act_quant_frag(const float* x, int T, int Tpad, int K, int8_t* xq, float* xd, hipStream_t s) {
   const dim3 grid(Tpad / 32, (K / kBlock + 3) / 4);
   act_quant_frag_kernel<<<grid, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_quant_frag(const float* x, const float* nw, float eps, int T, int Tpad, int K, int8_t* xq,
+                                     float* xd, hipStream_t s) {
+  if (K % kBlock || K > 2048 || Tpad % kNqTok) return hipErrorInvalidValue;
+  const size_t rowlen = ((size_t)(K / 4) + 31) & ~(size_t)31;
+  const size_t lds = ((size_t)kNqTok * 4 * rowlen + (size_t)kNqTok * K) * sizeof(float);
+  rmsnorm_quant_frag_kernel<<<Tpad / kNqTok, 256, lds, s>>>(x, nw, eps, T, Tpad, K, xq, xd);
   return hipGetLastError();
 }
 

@@ -436,10 +436,12 @@ def test_dev_pointer_unaligned_input(ctx):
 @pytest.mark.parametrize("dt", [O.Q8, O.Q4])
 def test_rmsnorm_fused_into_matmul(ctx, dt):
     """elmh_rmsnorm_matmul_dev / elmh_rmsnorm_swiglu_dev: bit-identical to RMSNORM then the matmul
-    (edgelm's cpu::rmsnorm and cpu backend matmul, through the oracle), both where each workgroup
-    normalizes the rows itself (T <= 4, K <= 2048) and where the rows go through scratch first."""
+    (edgelm's cpu::rmsnorm and cpu backend matmul, through the oracle) on every path: each GEMV
+    workgroup normalizing its rows (T <= 4, K <= 2048), the GEMM's quantizer normalizing them
+    (T > 4, K <= 2048, ragged token counts), and the rows going through scratch first."""
     r = rng(21)
-    for T, K, N in [(1, 576, 960), (2, 576, 64), (4, 1536, 576), (3, 2048, 96), (5, 576, 64), (1, 4096, 64)]:
+    for T, K, N in [(1, 576, 960), (2, 576, 64), (4, 1536, 576), (3, 2048, 96), (5, 576, 64), (1, 4096, 64),
+                    (33, 576, 96), (130, 1536, 64), (64, 2048, 32), (9, 4096, 64)]:
         print(f"[gpu] rmsnorm+matmul dt={dt} T={T} K={K} N={N}", flush=True)
         x = r.normal(0, 2, (T, K)).astype(np.float32)
         nw = r.normal(1, 0.2, K).astype(np.float32)
