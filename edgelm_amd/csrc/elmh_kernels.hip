@@ -1531,7 +1531,9 @@ __device__ __forceinline__ long q4_operand8(uint2 w, int h) {
   return (long)(((uint64_t)hi << 32) | lo);
 }
 
-template <int WDT, bool SW, bool TOK, bool FAST, int DEPTH = kWaveDepth>
+constexpr int kWave16Depth = 8;  // blocks in flight per wave (its operands are small)
+
+template <int WDT, bool SW, bool TOK, bool FAST, int DEPTH = kWave16Depth>
 __global__ __launch_bounds__(256) void gemm_wave16_kernel(const GemmArgs a) {
   typedef Wave16Ops<WDT, SW, TOK> Ops;
   constexpr int NSEL = Ops::NSEL;
