@@ -177,9 +177,11 @@ __global__ __launch_bounds__(256) void act_quant_frag_kernel(const float* __rest
 // QKV and gate/up GEMMs): kNqTok rows per workgroup, each normalized in rmsnorm_kernel's order
 // (squares grouped by dot_f32_scalar's accumulators in LDS, four in-order sums, (s0 + s1) +
 // (s2 + s3), then (x * inv) * w), then quantized into fragments exactly as act_quant_frag_kernel
-// does. Tokens at or past T give zero fragments and scales. K <= 2048.
+// does. A thread owns up to kNqItems half-blocks (row, block, half) and loads their x and norm
+// weights at the start, so the normalized values never leave its registers; the two halves of a
+// block sit in neighbouring lanes. Tokens at or past T give zero fragments and scales. K <= 2048.
 constexpr int kNqTok = 4;
-constexpr int kNqVF = 8;  // float4 of x per thread
+constexpr int kNqItems = 2;  // kNqTok * (2048 / 32) * 2 half-blocks over 256 threads
 
 __global__ __launch_bounds__(256) void rmsnorm_quant_frag_kernel(const float* __restrict__ x, const float* __restrict__ nw,
                                                                  float eps, int T, int Tpad, int K,
@@ -187,21 +189,29 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_frag_kernel(const float* __
   extern __shared__ __align__(16) float nq_lds[];
   __shared__ float inv_l[kNqTok];
   const int K4 = K >> 2, rowlen = (K4 + 31) & ~31, nb = K / kBlock;
-  float* sq = nq_lds;                    // [kNqTok][4][rowlen]
-  float* yb = sq + kNqTok * 4 * rowlen;  // [kNqTok][K] normalized rows
-  const int t0 = blockIdx.x * kNqTok, tid = threadIdx.x, nf = kNqTok * K4;
-  float4 xv[kNqVF];
+  float* sq = nq_lds;  // [kNqTok][4][rowlen]
+  const int t0 = blockIdx.x * kNqTok, tid = threadIdx.x, items = kNqTok * nb * 2;
+  float4 xv[kNqItems][4], wv[kNqItems][4];
 #pragma unroll
-  for (int u = 0; u < kNqVF; ++u) {
-    const int f = tid + 256 * u;
-    const int r = f / K4, k4 = f - r * K4, t = t0 + r;
-    xv[u] = f < nf && t < T ? ld4(x + (int64_t)t * K + 4 * k4, 0) : make_float4(0.f, 0.f, 0.f, 0.f);
-    if (f < nf) {
-      float* q = sq + r * 4 * rowlen + k4;
-      q[0] = xv[u].x * xv[u].x;
-      q[rowlen] = xv[u].y * xv[u].y;
-      q[2 * rowlen] = xv[u].z * xv[u].z;
-      q[3 * rowlen] = xv[u].w * xv[u].w;
+  for (int i = 0; i < kNqItems; ++i) {
+    const int it = tid + 256 * i;
+    const int r = it / (2 * nb), rem = it - r * 2 * nb, t = t0 + r;
+    const int e0 = (rem >> 1) * kBlock + (rem & 1) * 16;  // first element of the half-block
+    const bool in = it < items, ld = in && t < T;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xv[i][j] = ld ? ld4(x + (int64_t)t * K + e0, j) : make_float4(0.f, 0.f, 0.f, 0.f);
+      wv[i][j] = in ? ld4(nw + e0, j) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (in) {
+      float* q = sq + r * 4 * rowlen + (e0 >> 2);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        q[j] = xv[i][j].x * xv[i][j].x;
+        q[rowlen + j] = xv[i][j].y * xv[i][j].y;
+        q[2 * rowlen + j] = xv[i][j].z * xv[i][j].z;
+        q[3 * rowlen + j] = xv[i][j].w * xv[i][j].w;
+      }
     }
   }
   const int padw = rowlen - K4;
@@ -228,30 +238,24 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_frag_kernel(const float* __
   }
   __syncthreads();
 #pragma unroll
-  for (int u = 0; u < kNqVF; ++u) {
-    const int f = tid + 256 * u;
-    if (f < nf) {
-      const int r = f / K4, k4 = f - r * K4;
+  for (int i = 0; i < kNqItems; ++i) {
+    const int it = tid + 256 * i;
+    if (it < items) {  // items is even: both lanes of a block pair take this branch
+      const int r = it / (2 * nb), rem = it - r * 2 * nb, b = rem >> 1, h = rem & 1, t = t0 + r;
       const float inv = inv_l[r];
-      const float4 w4 = ld4(nw + 4 * k4, 0);
-      *reinterpret_cast<float4*>(yb + r * K + 4 * k4) =
-          make_float4((xv[u].x * inv) * w4.x, (xv[u].y * inv) * w4.y, (xv[u].z * inv) * w4.z, (xv[u].w * inv) * w4.w);
-    }
-  }
-  __syncthreads();
-  // items (row, block, half): the two halves of a block sit in neighbouring lanes
-  const int items = kNqTok * nb * 2;
-  for (int it = tid; it < items; it += 256) {
-    const int r = it / (2 * nb), rem = it - r * 2 * nb, b = rem >> 1, h = rem & 1, t = t0 + r;
-    const float* src = yb + r * K + b * kBlock + h * 16;
-    const float4 v[4] = {ld4(src, 0), ld4(src, 1), ld4(src, 2), ld4(src, 3)};
-    float a = 0.f;
+      float4 v[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a = amax4(v[i], a);
-    a = fmaxf(a, dpp_f<kDppQuadXor1>(a));
-    const float sc = a / 127.0f;
-    *reinterpret_cast<uint4*>(xq + frag_offset(t, b, h, nb)) = q8x16(v, sc == 0.f ? 1.f : sc);
-    if (h == 0) xd[(int64_t)b * Tpad + t] = sc;
+      for (int j = 0; j < 4; ++j)
+        v[j] = make_float4((xv[i][j].x * inv) * wv[i][j].x, (xv[i][j].y * inv) * wv[i][j].y,
+                           (xv[i][j].z * inv) * wv[i][j].z, (xv[i][j].w * inv) * wv[i][j].w);
+      float a = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a = amax4(v[j], a);
+      a = fmaxf(a, dpp_f<kDppQuadXor1>(a));
+      const float sc = a / 127.0f;
+      *reinterpret_cast<uint4*>(xq + frag_offset(t, b, h, nb)) = q8x16(v, sc == 0.f ? 1.f : sc);
+      if (h == 0) xd[(int64_t)b * Tpad + t] = sc;
+    }
   }
 }
 
@@ -1930,7 +1934,7 @@ hipError_t launch_rmsnorm_quant_frag(const float* x, const float* nw, float eps,
                                      float* xd, hipStream_t s) {
   if (K % kBlock || K > 2048 || Tpad % kNqTok) return hipErrorInvalidValue;
   const size_t rowlen = ((size_t)(K / 4) + 31) & ~(size_t)31;
-  const size_t lds = ((size_t)kNqTok * 4 * rowlen + (size_t)kNqTok * K) * sizeof(float);
+  const size_t lds = (size_t)kNqTok * 4 * rowlen * sizeof(float);
   rmsnorm_quant_frag_kernel<<<Tpad / kNqTok, 256, lds, s>>>(x, nw, eps, T, Tpad, K, xq, xd);
   return hipGetLastError();
 }
