@@ -44,3 +44,10 @@ ELM_HOSTDEV static inline void elm_q8_group(const float* v, float safe, int* q) 
 #pragma unroll
   for (int i = 0; i < N; ++i) q[i] = elm_q8_round(t[i]);
 }
+
+// Byte offset of the 16 elements h*16 .. h*16+15 of token t's block b in the block-scale GEMM's
+// activation fragments: the 1 KB fragment of (32-token group, block b) holds them for lane
+// h*32 + t%32; nb = blocks per token row.
+ELM_HOSTDEV static inline long long elm_frag_offset(int t, int b, int h, int nb) {
+  return ((((long long)(t >> 5) * nb + b) * 64) + h * 32 + (t & 31)) * 16;
+}

@@ -441,8 +441,10 @@ bool norm_fusable(int T, int64_t K, int n, const elmh_weight* const* w, int nsel
 
 // True if the int8-activation (block scales) call takes the GEMM at this T (more tokens than the
 // GEMV takes) and K fits the fused RMSNORM + fragment quantizer.
-bool norm_gemm(int T, int64_t K, int n, const elmh_weight* const* w, int nsel, int act) {
-  if (act != ELMH_ACT_INT8 || K % kBlock || K > 2048) return false;
+// run_matmul / run_swiglu take the block-scale GEMM (fragments from act_quant_frag_kernel) for
+// these targets: int8 block activations and too many tokens for the GEMV
+bool block_gemm(int T, int64_t K, int n, const elmh_weight* const* w, int nsel, int act) {
+  if (act != ELMH_ACT_INT8 || K % kBlock) return false;
   size_t bytes = 0;
   for (int i = 0; i < n; ++i) {
     if (!a8_applies(w[i]->w)) return false;
@@ -452,6 +454,10 @@ bool norm_gemm(int T, int64_t K, int n, const elmh_weight* const* w, int nsel, i
   int nt = 4;
   for (int i = 0; i < n; ++i) nt = std::min(nt, gemv_tokens(w[i]->w, nsel, qin));
   return T > nt;
+}
+
+bool norm_gemm(int T, int64_t K, int n, const elmh_weight* const* w, int nsel, int act) {
+  return K <= 2048 && block_gemm(T, K, n, w, nsel, act);
 }
 
 // RMSNORM into the scratch buffer (the path when it cannot be fused)
@@ -466,6 +472,20 @@ int norm_to_scratch(elmh_ctx* c, const float* x, const float* nw, float eps, int
 struct DeviceGuard {
   explicit DeviceGuard(elmh_ctx* c) { (void)hipSetDevice(c->device); }
 };
+
+int check_attention(elmh_ctx* c, const float* q, const float* k, const float* v, const float* out, int T, int pos0,
+                    int n_heads, int n_kv, int head_dim, const float* k_cache, const float* v_cache, int max_ctx,
+                    const float* rope_cos, const float* rope_sin) {
+  if (!c || !q || !k || !v || !out || !k_cache || !v_cache) return fail(c, ELMH_ERR_ARG, "attention: null pointer");
+  if (T < 1 || pos0 < 0 || (int64_t)pos0 + T > max_ctx)
+    return fail(c, ELMH_ERR_ARG, "attention: context overflow (pos0 %d + T %d > max_ctx %d)", pos0, T, max_ctx);
+  if (n_heads < 1 || n_kv < 1 || n_heads % n_kv || head_dim < 4 || head_dim % 4 || head_dim > 256)
+    return fail(c, ELMH_ERR_ARG, "attention: heads %d / kv heads %d / head_dim %d", n_heads, n_kv, head_dim);
+  if (!rope_cos != !rope_sin) return fail(c, ELMH_ERR_ARG, "attention: rope_cos and rope_sin go together");
+  if (attention_lds_bytes(head_dim, pos0 + T) > 65536)
+    return fail(c, ELMH_ERR_UNSUPPORTED, "attention: %d positions exceed the kernel's LDS", pos0 + T);
+  return ELMH_OK;
+}
 
 }  // namespace
 
@@ -865,17 +885,45 @@ int elmh_rmsnorm_dev(elmh_ctx* c, const float* x, const float* w, float* y, int 
   return ELMH_OK;
 }
 
+int elmh_attention_matmul_dev(elmh_ctx* c, const float* q, const float* k, const float* v, float* out, int T,
+                              int pos0, int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache,
+                              int max_ctx, const float* rope_cos, const float* rope_sin, elmh_weight* w, float* y,
+                              const float* res, int act, int mode) {
+  int rc = check_attention(c, q, k, v, out, T, pos0, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx, rope_cos,
+                           rope_sin);
+  if (rc) return rc;
+  const int64_t K = (int64_t)n_heads * head_dim;
+  elmh_weight* const ws[1] = {w};
+  float* const ys[1] = {y};
+  const float* const rs[1] = {res};
+  if ((rc = check_targets(c, T, K, 1, ws, ys))) return rc;
+  if (act < ELMH_ACT_F32 || act > ELMH_ACT_INT8_TOKEN) return fail(c, ELMH_ERR_ARG, "bad act mode %d", act);
+  DeviceGuard g(c);
+  int8_t* xq = nullptr;
+  float* xd = nullptr;
+  const int Tpad = (int)round_up(T, kGemmTileT);
+  if (T > 1 && head_dim == 64 && block_gemm(T, K, 1, ws, 1, act)) {
+    // the GEMM's activation fragments come out of the attention kernel
+    if ((rc = ensure(c, c->xq, (size_t)Tpad * K))) return rc;
+    if ((rc = ensure(c, c->xd, (size_t)Tpad * (K / kBlock) * sizeof(float)))) return rc;
+    xq = (int8_t*)c->xq.p;
+    xd = (float*)c->xd.p;
+  }
+  bool quantized = false;
+  HIP_OR_FAIL(c, launch_attention(q, k, v, out, T, pos0, nullptr, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx,
+                                  rope_cos, rope_sin, c->stream, xq, xd, Tpad, &quantized));
+  if (!quantized) return run_matmul(c, out, T, K, 1, ws, ys, res ? rs : nullptr, act, mode);
+  for (const auto& grp : by_dtype(1, ws))
+    if ((rc = run_gemm_group(c, xq, xd, T, Tpad, K, grp, ws, ys, res ? rs : nullptr, 0, mode == ELMH_FAST))) return rc;
+  return ELMH_OK;
+}
+
 int elmh_attention_dev(elmh_ctx* c, const float* q, const float* k, const float* v, float* out, int T, int pos0,
                        int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache, int max_ctx,
                        const float* rope_cos, const float* rope_sin) {
-  if (!c || !q || !k || !v || !out || !k_cache || !v_cache) return fail(c, ELMH_ERR_ARG, "attention: null pointer");
-  if (T < 1 || pos0 < 0 || (int64_t)pos0 + T > max_ctx)
-    return fail(c, ELMH_ERR_ARG, "attention: context overflow (pos0 %d + T %d > max_ctx %d)", pos0, T, max_ctx);
-  if (n_heads < 1 || n_kv < 1 || n_heads % n_kv || head_dim < 4 || head_dim % 4 || head_dim > 256)
-    return fail(c, ELMH_ERR_ARG, "attention: heads %d / kv heads %d / head_dim %d", n_heads, n_kv, head_dim);
-  if (!rope_cos != !rope_sin) return fail(c, ELMH_ERR_ARG, "attention: rope_cos and rope_sin go together");
-  if (attention_lds_bytes(head_dim, pos0 + T) > 65536)
-    return fail(c, ELMH_ERR_UNSUPPORTED, "attention: %d positions exceed the kernel's LDS", pos0 + T);
+  const int rc = check_attention(c, q, k, v, out, T, pos0, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx,
+                                 rope_cos, rope_sin);
+  if (rc) return rc;
   DeviceGuard g(c);
   HIP_OR_FAIL(c, launch_attention(q, k, v, out, T, pos0, nullptr, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx,
                                   rope_cos, rope_sin, c->stream));

@@ -139,10 +139,15 @@ hipError_t launch_silu_mul(const float* g, const float* u, float* y, int64_t n, 
 // The non-matmul ops of a layer (elmh_layer.hip), same float order as edgelm's cpu backend.
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps, hipStream_t s);
 size_t attention_lds_bytes(int hd, int n_max);
-// pos_dev (if not null): pos0 read from device memory (T must be 1; LDS sized for max_ctx)
+// pos_dev (if not null): pos0 read from device memory (T must be 1; LDS sized for max_ctx).
+// xq, xd, Tpad, quantized (all given): where the chunk kernel (T > 1, head size 64) runs, it also
+// writes its output as the block-scale GEMM's activation fragments (xq, Tpad * n_heads * hd bytes)
+// and scales (xd, 2 * n_heads * Tpad floats; tokens T .. Tpad-1 left as they were) and sets
+// *quantized; otherwise *quantized is false and xq, xd are untouched.
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
                             const int* pos_dev, int n_heads, int n_kv, int hd, float* kc, float* vc, int max_ctx,
-                            const float* rcos, const float* rsin, hipStream_t s);
+                            const float* rcos, const float* rsin, hipStream_t s, int8_t* xq = nullptr,
+                            float* xd = nullptr, int Tpad = 0, bool* quantized = nullptr);
 hipError_t launch_embed(const int32_t* tok, int T, const DevWeight& w, float* y, hipStream_t s);
 // dst[0, bytes) = value (a kernel: capturable in a HIP graph, unlike hipMemsetAsync)
 hipError_t launch_fill(void* dst, int value, size_t bytes, hipStream_t s);

@@ -144,9 +144,7 @@ __device__ __forceinline__ float amax4(float4 v, float a) {
 __device__ __forceinline__ float4 ld4(const float* p, int i) {
   return make_float4(p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]);
 }
-__device__ __forceinline__ int64_t frag_offset(int t, int b, int h, int nb) {
-  return ((((int64_t)(t >> 5) * nb + b) * 64) + h * 32 + (t & 31)) * 16;
-}
+__device__ __forceinline__ int64_t frag_offset(int t, int b, int h, int nb) { return elm_frag_offset(t, b, h, nb); }
 
 // Per-32-block scales. Workgroup = (32-token group g, blocks 4 y .. 4 y + 3); wave w takes block
 // b = 4 y + w and lane L = h*32 + t%32 the 16 elements of half h of token t's block b, so each wave

@@ -9,6 +9,7 @@
 
 #include "elm_dpp.h"
 #include "elm_expf.h"
+#include "elm_quant.h"
 #include "elmh_internal.hpp"
 
 namespace elmh {
@@ -436,7 +437,9 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(const float* __r
                                                                 const float* __restrict__ vc, int pos0, int T,
                                                                 int n_heads, int n_kv, int max_ctx, int n_cap,
                                                                 const float* __restrict__ rcos,
-                                                                const float* __restrict__ rsin) {
+                                                                const float* __restrict__ rsin,
+                                                                int8_t* __restrict__ xq, float* __restrict__ xd,
+                                                                int Tpad) {
   constexpr int hd = 64, h2 = 32, hd4 = 16;
   extern __shared__ float lds[];
   const int scs = (n_cap + 63) & ~63;  // score row stride
@@ -547,7 +550,22 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(const float* __r
     for (; jj + 16 <= m; jj += 16) batch(jj, 16);
     if (jj < m) batch(jj, m - jj);  // the last, partial batch
   }
-  if (w < nq) out[(int64_t)tw * qd + h * hd + lane] = acc;
+  if (w < nq) {
+    out[(int64_t)tw * qd + h * hd + lane] = acc;
+    if (xq) {
+      // the next GEMM's activation fragments: lanes 0-31 hold block 2h of token tw, lanes 32-63
+      // block 2h + 1; scale = amax / 127 and edgelm's rounding, as act_quant_frag_kernel
+      float a = fmaxf(0.f, fabsf(acc));
+#pragma unroll
+      for (int m = 1; m < 32; m <<= 1) a = fmaxf(a, __shfl_xor(a, m, 64));
+      const float scl = a / 127.0f;
+      int qv;
+      elm_q8_group<1>(&acc, scl == 0.f ? 1.f : scl, &qv);
+      const int b = 2 * h + (lane >> 5), e = lane & 31;
+      xq[elm_frag_offset(tw, b, e >> 4, 2 * n_heads) + (e & 15)] = (int8_t)qv;
+      if (e == 0) xd[(int64_t)b * Tpad + tw] = scl;
+    }
+  }
 }
 
 // ---------------------------------------------------------------- EMBED
@@ -705,7 +723,9 @@ size_t attention_lds_bytes(int hd, int n_max) {
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
                             const int* pos_dev, int n_heads, int n_kv, int hd, float* kc, float* vc, int max_ctx,
-                            const float* rcos, const float* rsin, hipStream_t s) {
+                            const float* rcos, const float* rsin, hipStream_t s, int8_t* xq, float* xd, int Tpad,
+                            bool* quantized) {
+  if (quantized) *quantized = false;
   // with the position in device memory the score buffer covers the whole cache
   const int n_cap = pos_dev ? max_ctx : pos0 + T;  // score slots
   // one token: the append runs inside the attention kernel; a chunk appends every key first
@@ -720,9 +740,13 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
   const size_t lds_pf = ((size_t)kAttnQ * hd + (size_t)kAttnQ * ((n_cap + 63) & ~63) + (size_t)kAttnPVPos * hd) * 4;
   if (!fuse && hd == 64 && lds_pf <= 64 * 1024) {
     const int ngr = (T + kAttnQ - 1) / kAttnQ;
+    const bool quant = xq && xd && quantized;
     attention_prefill_kernel<<<n_heads * ngr, 256, lds_pf, s>>>(q, out, kc, vc, pos0, T, n_heads, n_kv, max_ctx, n_cap,
-                                                                rcos, rsin);
-    return hipGetLastError();
+                                                                rcos, rsin, quant ? xq : nullptr,
+                                                                quant ? xd : nullptr, Tpad);
+    const hipError_t e = hipGetLastError();
+    if (e == hipSuccess && quant) *quantized = true;
+    return e;
   }
   if (hd == 64)
     attention_kernel<64><<<T * n_heads, kAttnThreads, attention_lds_bytes(hd, n_cap), s>>>(

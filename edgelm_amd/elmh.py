@@ -234,6 +234,14 @@ class Context:
             C.c_int(pos0), C.c_int(n_heads), C.c_int(n_kv), C.c_int(head_dim), C.c_void_p(kc_ptr), C.c_void_p(vc_ptr),
             C.c_int(max_ctx), C.c_void_p(cos_ptr), C.c_void_p(sin_ptr)))
 
+    def attention_matmul_dev(self, q_ptr, k_ptr, v_ptr, out_ptr, T, pos0, n_heads, n_kv, head_dim, kc_ptr, vc_ptr,
+                             max_ctx, cos_ptr, sin_ptr, weight, y_ptr, res_ptr=None, act=ACT_INT8, mode=EXACT):
+        self._check(lib().elmh_attention_matmul_dev(
+            self.h, C.c_void_p(q_ptr), C.c_void_p(k_ptr), C.c_void_p(v_ptr), C.c_void_p(out_ptr), C.c_int(T),
+            C.c_int(pos0), C.c_int(n_heads), C.c_int(n_kv), C.c_int(head_dim), C.c_void_p(kc_ptr), C.c_void_p(vc_ptr),
+            C.c_int(max_ctx), C.c_void_p(cos_ptr), C.c_void_p(sin_ptr), weight.h, C.c_void_p(y_ptr),
+            C.c_void_p(res_ptr), C.c_int(act), C.c_int(mode)))
+
     def argmax_dev(self, x_ptr, rows, n, out_ptr):
         self._check(lib().elmh_argmax_dev(self.h, C.c_void_p(x_ptr), C.c_int(rows), C.c_int64(n), C.c_void_p(out_ptr)))
 

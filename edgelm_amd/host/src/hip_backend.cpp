@@ -115,6 +115,7 @@ class HipBackend : public Backend {
     for (const Op& op : g.ops)
       for (int t : op.in) ++readers[t];
     fuse_norm_.assign(g.ops.size(), 0);
+    fuse_attn_.assign(g.ops.size(), 0);
     for (const Partition& p : parts) {
       if (p.backend != this) continue;
       for (int i = p.begin; i + 1 < p.end; ++i) {
@@ -123,6 +124,11 @@ class HipBackend : public Backend {
         fuse_norm_[i] = t >= 0 && !host_needed_[t] && readers[t] == 1 && !b.in.empty() && b.in[0] == t &&
                         (b.type == OpType::MATMUL || b.type == OpType::MATMUL_N || b.type == OpType::MATMUL_ADD ||
                          b.type == OpType::FFN_SWIGLU);
+        // ATTENTION whose output the next op (the o projection) multiplies: one call, which still
+        // writes the attention output for later device readers (none on the host: its copy-back
+        // would run before the deferred kernel)
+        fuse_attn_[i] = a.type == OpType::ATTENTION && !host_needed_[a.out[0]] && !b.in.empty() &&
+                        b.in[0] == a.out[0] && (b.type == OpType::MATMUL || b.type == OpType::MATMUL_ADD);
       }
     }
     act_.assign(nt, Buf{});
@@ -184,6 +190,9 @@ class HipBackend : public Backend {
     // a deferred RMSNORM (fuse_norm_) applies to this op's input inside the matmul call
     const bool normed = norm_.op == idx - 1 && norm_.op >= 0;
     if (!normed) norm_.op = -1;
+    // a deferred ATTENTION (fuse_attn_) runs inside this matmul's call
+    const bool attended = attn_.op == idx - 1 && attn_.op >= 0;
+    if (!attended) attn_.op = -1;
     switch (op.type) {
       case OpType::FFN_SWIGLU: {
         const int T = static_cast<int>(c.rows(op.in[0]));
@@ -218,7 +227,15 @@ class HipBackend : public Backend {
           check(elmh_rmsnorm_matmul_dev(ctx_, norm_.x, norm_.w, norm_.eps, T, K, static_cast<int>(n), w_.data(),
                                         y_.data(), res, act(c), ELMH_EXACT),
                 op);
-        else
+        else if (attended) {
+          const PendingAttention& a = attn_;
+          EDGELM_CHECK(n == 1 && a.out == x && a.T == T && static_cast<int64_t>(a.nh) * a.hd == K,
+                       "attention + matmul: operands do not match");
+          check(elmh_attention_matmul_dev(ctx_, a.q, a.k, a.v, a.out, T, a.pos0, a.nh, a.nkv, a.hd, a.kc, a.vc, a.mc,
+                                          a.rc, a.rs, w_[0], y_[0], r_[0], act(c), ELMH_EXACT),
+                op);
+          attn_.op = -1;
+        } else
           check(elmh_matmul_dev(ctx_, x, T, K, static_cast<int>(n), w_.data(), y_.data(), res, act(c), ELMH_EXACT),
                 op);
         break;
@@ -509,6 +526,11 @@ class HipBackend : public Backend {
     const float* q = in(op.in[0], c);
     const float* k = in(op.in[1], c);
     const float* v = in(op.in[2], c);
+    const int idx = static_cast<int>(&op - c.graph->ops.data());
+    if (prepared_ && fuse_attn_[idx] && !capturing_ && T > 1) {
+      attn_ = {idx, q, k, v, out(op.out[0], c), T, c.pos0, nh, nkv, hd, l.k, l.v, mc, rc, rs};
+      return;  // the next op (the o projection) runs it
+    }
     if (capturing_)  // the replayed step reads its position from device memory
       check(elmh_attention_step_dev(ctx_, q, k, v, out(op.out[0], c), pos_dev_, nh, nkv, hd, l.k, l.v, mc, rc, rs), op);
     else
@@ -534,6 +556,16 @@ class HipBackend : public Backend {
     float eps = 0.f;
   } norm_;
   static constexpr int kMaxFusedNormDim = 8192;  // elmh_rmsnorm_matmul_dev's limit
+  std::vector<char> fuse_attn_;  // op index: an ATTENTION that the next op (a matmul) runs
+  struct PendingAttention {
+    int op = -1;
+    const float *q = nullptr, *k = nullptr, *v = nullptr;
+    float* out = nullptr;
+    int T = 0, pos0 = 0, nh = 0, nkv = 0, hd = 0;
+    float *kc = nullptr, *vc = nullptr;
+    int mc = 0;
+    const float *rc = nullptr, *rs = nullptr;
+  } attn_;
   int output_ = -1;          // graph output when this backend writes it (prepare), else -1
   bool keep_out_ = false;    // keep_output(true): the output is not copied to the host arena
   int32_t* dev_tok_ = nullptr;  // argmax result

@@ -124,8 +124,10 @@ int elmh_rmsnorm_dev(elmh_ctx* ctx, const float* x, const float* w, float* y, in
  * for the edgelm op pairs RMSNORM -> MATMUL_N and RMSNORM -> FFN_SWIGLU of a layer
  * (passes.cpp:72-81,100-104; cpu::rmsnorm kernels_cpu.cpp:326-335). With int8 activations on
  * rows short enough for the workgroup-quantizing GEMV (T <= 4, K <= 2048) each workgroup
- * normalizes the rows itself and the normalized activation never goes to memory; otherwise the
- * normalized rows go to a scratch buffer (reserved by elmh_reserve) first. K <= 8192. */
+ * normalizes the rows itself and the normalized activation never goes to memory; on the
+ * block-scale GEMM path (K <= 2048) one launch normalizes and quantizes the rows into the GEMM's
+ * operand; otherwise the normalized rows go to a scratch buffer (reserved by elmh_reserve)
+ * first. K <= 8192. */
 int elmh_rmsnorm_matmul_dev(elmh_ctx* ctx, const float* x, const float* norm_w, float eps, int T, int64_t K,
                             int n_targets, elmh_weight* const* w, float* const* y, const float* const* residual,
                             int act, int mode);
@@ -139,6 +141,17 @@ int elmh_rmsnorm_swiglu_dev(elmh_ctx* ctx, const float* x, const float* norm_w, 
 int elmh_attention_dev(elmh_ctx* ctx, const float* q, const float* k, const float* v, float* out, int T, int pos0,
                        int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache, int max_ctx,
                        const float* rope_cos, const float* rope_sin);
+/* ATTENTION followed by the MATMUL or MATMUL_ADD that consumes its output (a layer's o projection,
+ * MATMUL_ADD after fuse_residual, passes.cpp:88-110; cpu::attention kernels_cpu.cpp:417-488), as
+ * one call: the same results as elmh_attention_dev into out and then elmh_matmul_dev(out, T,
+ * n_heads*head_dim, one target w -> y, residual res or NULL), bit for bit; out is written as
+ * well. Where the chunk attention kernel (T > 1, head_dim 64) and the block-scale GEMM (int8
+ * activations, too many rows for the GEMV) both apply, the attention kernel also writes its
+ * output as the GEMM's quantized operand, so no quantizer launch runs in between. */
+int elmh_attention_matmul_dev(elmh_ctx* ctx, const float* q, const float* k, const float* v, float* out, int T,
+                              int pos0, int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache,
+                              int max_ctx, const float* rope_cos, const float* rope_sin, elmh_weight* w, float* y,
+                              const float* res, int act, int mode);
 /* One decode token (T = 1) of elmh_attention_dev with its position pos0 read from device memory
  * (*pos_dev, in [0, max_ctx)), so that a decode step captured in a HIP graph replays at every
  * position. No counterpart in edgelm: it serves callers that replay graphs (this build's hip

@@ -74,6 +74,50 @@ def test_attention_bit_exact(ctx, shape, rope):
         b.free()
 
 
+FUSED_ATTN = [(9, 3, 64, 300, (128, 1, 33, 7, 3)), (4, 4, 32, 64, (17, 5))]
+
+
+@pytest.mark.parametrize("shape", FUSED_ATTN, ids=[f"{s[0]}x{s[1]}x{s[2]}" for s in FUSED_ATTN])
+@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
+def test_attention_fused_into_matmul(ctx, shape, dt):
+    """elmh_attention_matmul_dev: out and the KV caches as ATTENTION, and y bit-identical to the o
+    projection (MATMUL_ADD with the residual, then plain MATMUL) on edgelm's cpu backend over the
+    attention's output, for a session's calls: chunks where the attention kernel writes the GEMM's
+    quantized operand (T = 128, then T = 33 over the rows the first call left past T), a decode
+    token and short chunks on the GEMV, and head size 32, which never fuses."""
+    nh, nkv, hd, mc, steps = shape
+    r = np.random.default_rng(nh + hd + dt)
+    tab = O.rope_table(hd, mc, 100000.0)
+    kc = np.zeros((nkv, mc, hd), np.float32)
+    vc = np.zeros_like(kc)
+    bkc, bvc, bcos, bsin = dev(ctx, kc), dev(ctx, vc), dev(ctx, tab[0]), dev(ctx, tab[1])
+    D, N = nh * hd, 96
+    w = O.make_weight(r.normal(0, 0.05, (N, D)).astype(np.float32), dt)
+    dw = ctx.upload(w.dtype, w.rows, w.cols, w.data, w.scales)
+    pos = 0
+    for i, T in enumerate(steps):
+        print(f"[gpu] attention+matmul {shape[:4]} dt={dt} pos0={pos} T={T}", flush=True)
+        q = r.normal(0, 1, (T, D)).astype(np.float32)
+        k = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+        v = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+        res = r.normal(0, 1, (T, N)).astype(np.float32) if i % 2 == 0 else None
+        bq, bk, bv, bo, by = dev(ctx, q), dev(ctx, k), dev(ctx, v), ctx.buffer(q.nbytes), ctx.buffer(T * N * 4)
+        bres = dev(ctx, res) if res is not None else None
+        ctx.attention_matmul_dev(bq.ptr, bk.ptr, bv.ptr, bo.ptr, T, pos, nh, nkv, hd, bkc.ptr, bvc.ptr, mc,
+                                 bcos.ptr, bsin.ptr, dw, by.ptr, bres.ptr if bres else None)
+        att = O.attention(q, k, v, pos, nh, nkv, kc, vc, tab)
+        assert bits_equal(bo.download(q.shape, np.float32), att), f"pos0={pos} T={T}"
+        want = O.cpu_matmul(att, [w], [res], act_quant=True)[0]
+        assert bits_equal(by.download((T, N), np.float32), want), f"pos0={pos} T={T}"
+        for b in (bq, bk, bv, bo, by) + ((bres,) if bres else ()):
+            b.free()
+        pos += T
+    assert bits_equal(bkc.download(kc.shape, np.float32), kc)
+    assert bits_equal(bvc.download(vc.shape, np.float32), vc)
+    for b in (bkc, bvc, bcos, bsin, dw):
+        b.free()
+
+
 def test_attention_rejects_bad_shapes(ctx):
     from edgelm_amd import elmh as E
     b = ctx.buffer(4096)
