@@ -131,6 +131,25 @@ def test_attention_rejects_bad_shapes(ctx):
     b.free()
 
 
+def test_attention_matmul_rejects_bad_arguments(ctx):
+    """elmh_attention_matmul_dev checks the attention's arguments as elmh_attention_dev does, and
+    the weight against the attention's output width (n_heads * head_dim), before any launch."""
+    from edgelm_amd import elmh as E
+    b = ctx.buffer(1 << 16)
+    r = np.random.default_rng(5)
+    w = O.make_weight(r.normal(0, 0.05, (32, 9 * 64)).astype(np.float32), O.Q8)
+    dw = ctx.upload(w.dtype, w.rows, w.cols, w.data, w.scales)
+    for T, pos0, nh, act in [(8, 0, 8, E.ACT_INT8),    # weight width 576 != 8 * 64
+                             (4, 10, 9, E.ACT_INT8),   # pos0 + T > max_ctx
+                             (8, 0, 9, 7)]:            # no such activation mode
+        with pytest.raises(E.ElmhError) as e:
+            ctx.attention_matmul_dev(b.ptr, b.ptr, b.ptr, b.ptr, T, pos0, nh, 1 if nh == 8 else 3, 64, b.ptr, b.ptr,
+                                     12, None, None, dw, b.ptr, None, act=act)
+        assert e.value.code == E.ERR_ARG, e.value
+    b.free()
+    dw.free()
+
+
 @pytest.mark.parametrize("dt", [O.Q8, O.Q4])
 def test_embed_bit_exact(ctx, dt):
     r = np.random.default_rng(30 + dt)
