@@ -39,7 +39,7 @@ enum WDType { WQ8 = 1, WQ4 = 2 };
 //   data:   [rows_pad/H][nb][H][G] bytes, G = 32 (q8: int8 row segment of one 32-block)
 //                                       G = 16 (q4: the group's 16 bytes exactly as exported)
 //   scales: q8 -> [rows_pad] f32 (per row)
-//           q4 -> [rows_pad/H][nb][H] f32 holding ws/16 (exact: power-of-two scaling)
+//           q4 -> [rows_pad/H][nb][H] f32, the group scales as exported
 // A (row n, block b) item sits at index ((n/H)*nb + b)*H + n%H, so a run of H rows of one
 // block is contiguous and one H-row tile of all blocks is one contiguous chunk.
 struct DevWeight {

@@ -86,7 +86,7 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, const float* __re
       }
     } else {
       for (int j = 0; j < 16; ++j) o[j] = n < rows ? raw[n * (cols / 2) + b * 16 + j] : 0x88;  // 0x88: q = 0
-      out_scales[dst] = n < rows ? raw_scales[n * nb + b] * 0.0625f : 0.f;
+      out_scales[dst] = n < rows ? raw_scales[n * nb + b] : 0.f;
     }
   }
   if (dtype == WQ8)
@@ -318,8 +318,8 @@ __global__ __launch_bounds__(256) void act_quant_frag_token_kernel(const float* 
 //
 // A workgroup owns one H-row tile of the weight (for SwiGLU the gate and up tiles together): one
 // contiguous chunk of the repacked layout. Every (row, block) item's product
-//   q8: p = float(S_b) * xd_b        q4: p/16 = float(S_b) * ((ws_b/16) * xd_b)
-// goes to LDS (each multiply rounds exactly as on the CPU; /16 is exact); then one lane per
+//   q8: p = float(S_b) * xd_b        q4: p = float(S_b) * (ws_b * xd_b)
+// goes to LDS (each multiply rounds exactly as on the CPU); then one lane per
 // (token, row) folds its products in block order with plain adds and applies the epilogue.
 // Consecutive lanes take consecutive items, so every weight load instruction reads one
 // contiguous run. Every dispatch starts with cold instruction caches, so the kernels are kept
@@ -452,7 +452,7 @@ __device__ __forceinline__ void gemv_fold(const GemvArgs& a, const GemvLds& L, c
   const int ft = pr / R, fr = pr - ft * R, fn = n0 + fr;
   const bool live = pr < a.T * R && fr < rows && fn < tg.N;
   float v = fold_chain(L.p + (live ? (sel * NT + ft) * R + fr : 0) * L.pst, a.nb);
-  v = WDT == WQ8 ? v * e_s : v * 16.0f;
+  if (WDT == WQ8) v = v * e_s;
   if (SW) {
     const float up = row_swap8(v);
     if (live && sel == 0) tg.y[(int64_t)ft * tg.N + fn] = silu_exact(v) * up;
@@ -823,9 +823,9 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
     if (!folder) return;
     const int fn = tile0 * H + fr;
     if (fn >= tg.N) return;
-    float out = WDT == WQ8 ? acc_g * e_s : acc_g * 16.0f;
+    float out = WDT == WQ8 ? acc_g * e_s : acc_g;
     if (SW) {
-      const float up = WDT == WQ8 ? acc_u * e_su : acc_u * 16.0f;
+      const float up = WDT == WQ8 ? acc_u * e_su : acc_u;
       out = silu_exact(out) * up;
     } else if (tg.res) {
       out = out + e_res;
@@ -1132,7 +1132,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
             const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[mt], B[nt], zero, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-              // q8: p = float(S) * xd; q4 (S = 16 * S_b, c = ws / 16): p = float(S) * (c * xd)
+              // q8: p = float(S) * xd; q4 (S = 16 * S_b, c = ws): p = float(S) * (c * xd) = 16 * edgelm's product
+              // (c * xd rounds as on the CPU; 16 times a product or a sum of multiples of 2^-149 is exact, so
+              // the q4 fold stays 16 times edgelm's, subnormal range included, up to 2^124 in magnitude, and
+              // one multiply by 1/16 before the store restores it)
               const float m = WDT == WQ8 ? xv[i] : BLOCKX ? c[nt] * xv[i] : c[nt];
               if (FAST) {
                 facc[s][mt][nt][i] = __builtin_fmaf((float)S[i], m, facc[s][mt][nt][i]);
@@ -1247,8 +1250,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
             g = TOK ? ((float)iacc[0][mt][nt][i] * xt[i]) * ws : facc[0][mt][nt][i] * ws;
             u = TOK ? ((float)iacc[NSEL - 1][mt][nt][i] * xt[i]) * wsu : facc[NSEL - 1][mt][nt][i] * wsu;
           } else {
-            g = TOK ? facc[0][mt][nt][i] * xt[i] : facc[0][mt][nt][i];
-            u = TOK ? facc[NSEL - 1][mt][nt][i] * xt[i] : facc[NSEL - 1][mt][nt][i];
+            g = TOK ? (facc[0][mt][nt][i] * 0.0625f) * xt[i] : facc[0][mt][nt][i] * 0.0625f;
+            u = TOK ? (facc[NSEL - 1][mt][nt][i] * 0.0625f) * xt[i] : facc[NSEL - 1][mt][nt][i] * 0.0625f;
           }
           ep[i * 64 + lane] = g;
           ep[1024 + i * 64 + lane] = u;
@@ -1297,7 +1300,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
           if (WDT == WQ8) {
             out = TOK ? ((float)iacc[0][mt][nt][i] * xt[i]) * ws : facc[0][mt][nt][i] * ws;
           } else {
-            out = TOK ? facc[0][mt][nt][i] * xt[i] : facc[0][mt][nt][i];
+            out = TOK ? (facc[0][mt][nt][i] * 0.0625f) * xt[i] : facc[0][mt][nt][i] * 0.0625f;
           }
           if (RES) out = out + res[i];
           __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), ry, off, 0, 0);
@@ -1329,7 +1332,7 @@ struct WaveOps {
   static constexpr bool BLOCKX = !TOK;
   v4i A;
   v4i B[NSEL];
-  float c[NSEL];                // q4: ws / 16 of the lane's row and block
+  float c[NSEL];                // q4: ws of the lane's row and block
   float xv[BLOCKX ? 16 : 1];    // block scales of the lane's 16 tokens
 };
 
@@ -1413,7 +1416,7 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const GemmArgs a) {
     for (int s = 0; s < NSEL; ++s)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        // q8: p = float(S) * xd; q4 (S = 16 * S_b, c = ws / 16): p = float(S) * (c * xd)
+        // q8: p = float(S) * xd; q4 (S = 16 * S_b, c = ws): p = float(S) * (c * xd) = 16 * edgelm's product
         const float m = WDT == WQ8 ? o.xv[BLOCKX ? i : 0] : BLOCKX ? o.c[s] * o.xv[i] : o.c[s];
         if (FAST) {
           facc[s][i] = __builtin_fmaf((float)S[s][i], m, facc[s][i]);
@@ -1467,7 +1470,7 @@ __global__ __launch_bounds__(256) void gemm_wave_kernel(const GemmArgs a) {
   }
   auto value = [&](int s, int i, float ws) {
     if (WDT == WQ8) return TOK ? ((float)iacc[s][i] * xt[i]) * ws : facc[s][i] * ws;
-    return TOK ? facc[s][i] * xt[i] : facc[s][i];
+    return TOK ? (facc[s][i] * 0.0625f) * xt[i] : facc[s][i] * 0.0625f;
   };
   if (SW) {
     // gate and up through this wave's LDS slice, so that silu (an expf) is emitted once in a loop
@@ -1523,7 +1526,7 @@ struct Wave16Ops {
   static constexpr bool BLOCKX = !TOK;
   long A;
   long B[NSEL];
-  float c[NSEL];               // q4: ws / 16 of the lane's row and block
+  float c[NSEL];               // q4: ws of the lane's row and block
   float4 xv;                   // block scales of the lane's 4 tokens
 };
 
@@ -1599,7 +1602,7 @@ __global__ __launch_bounds__(256) void gemm_wave16_kernel(const GemmArgs a) {
     for (int s = 0; s < NSEL; ++s)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        // q8: p = float(S) * xd; q4 (S = 16 * S_b, c = ws / 16): p = float(S) * (c * xd)
+        // q8: p = float(S) * xd; q4 (S = 16 * S_b, c = ws): p = float(S) * (c * xd) = 16 * edgelm's product
         const float m = WDT == WQ8 ? xv[BLOCKX ? i : 0] : BLOCKX ? o.c[s] * xv[i] : o.c[s];
         if (FAST) {
           facc[s][i] = __builtin_fmaf((float)S[s][i], m, facc[s][i]);
@@ -1648,7 +1651,7 @@ __global__ __launch_bounds__(256) void gemm_wave16_kernel(const GemmArgs a) {
   }
   auto value = [&](int s, int i, float ws) {
     if (WDT == WQ8) return TOK ? ((float)iacc[s][i] * xt[i]) * ws : facc[s][i] * ws;
-    return TOK ? facc[s][i] * xt[i] : facc[s][i];
+    return TOK ? (facc[s][i] * 0.0625f) * xt[i] : facc[s][i] * 0.0625f;
   };
   const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
   if (SW) {
@@ -1719,7 +1722,7 @@ __device__ __forceinline__ float dot_row_f32(const uint8_t* __restrict__ data, c
         g0 = g0 + sx[g * 32 + i] * (float)((int)(byte & 0x0F) - 8);
         g1 = g1 + sx[g * 32 + 16 + i] * (float)((int)(byte >> 4) - 8);
       }
-      s = s + (g0 + g1) * (scales[item] * 16.0f);
+      s = s + (g0 + g1) * scales[item];
     }
     return s;
   }
@@ -1773,7 +1776,7 @@ __device__ __forceinline__ float4 deq4(const uint8_t* __restrict__ data, const f
     const int e = i & 31;  // 4 consecutive elements of one half of the group
     const uint32_t w = *reinterpret_cast<const uint32_t*>(data + item * 16 + (e & 15));
     const int sh = e >= 16 ? 4 : 0;
-    const float s = scales[item] * 16.0f;
+    const float s = scales[item];
     r.x = (float)((int)((w >> sh) & 0x0F) - 8) * s;
     r.y = (float)((int)((w >> (8 + sh)) & 0x0F) - 8) * s;
     r.z = (float)((int)((w >> (16 + sh)) & 0x0F) - 8) * s;
@@ -1790,7 +1793,7 @@ __device__ __forceinline__ float deq1(const uint8_t* __restrict__ data, const fl
   if (WDT == WQ8) return (float)*reinterpret_cast<const int8_t*>(data + item * 32 + (i & 31)) * scales[n];
   const int e = i & 31;
   const uint8_t byte = data[item * 16 + (e & 15)];
-  return (float)((int)(e >= 16 ? byte >> 4 : byte & 0x0F) - 8) * (scales[item] * 16.0f);
+  return (float)((int)(e >= 16 ? byte >> 4 : byte & 0x0F) - 8) * scales[item];
 }
 
 template <int WDT, bool SW>

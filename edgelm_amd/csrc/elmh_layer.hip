@@ -571,7 +571,7 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(const float* __r
 // ---------------------------------------------------------------- EMBED
 
 // y[t][k] = dequantize_row(table, tokens[t])[k] read from the repacked weight layout:
-//   q8: float(q) * s_row;  q4: float(nibble - 8) * s_group, s_group = (stored s/16) * 16
+//   q8: float(q) * s_row;  q4: float(nibble - 8) * s_group
 __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tok, int64_t total,
                                                     const uint8_t* __restrict__ data,
                                                     const float* __restrict__ scales, int dtype, int64_t cols,
@@ -587,7 +587,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ 
     } else {
       const uint8_t byte = data[it * 16 + (j & 15)];
       const int nib = j < 16 ? (byte & 0x0F) : (byte >> 4);
-      v = (float)(nib - 8) * (scales[it] * 16.0f);
+      v = (float)(nib - 8) * scales[it];
     }
     y[idx] = v;
   }

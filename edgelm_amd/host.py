@@ -30,8 +30,10 @@ def quantize_q8(w, threads=0):
     n, k = w.shape
     q = np.empty((n, k), np.int8)
     s = np.empty(n, np.float32)
-    lib().elm_quantize_q8(C.c_void_p(w.ctypes.data), C.c_int64(n), C.c_int64(k), C.c_void_p(q.ctypes.data),
-                          C.c_void_p(s.ctypes.data), C.c_int(_threads(threads)))
+    rc = lib().elm_quantize_q8(C.c_void_p(w.ctypes.data), C.c_int64(n), C.c_int64(k), C.c_void_p(q.ctypes.data),
+                               C.c_void_p(s.ctypes.data), C.c_int(_threads(threads)))
+    if rc != 0:
+        raise ValueError(f"elm_quantize_q8 refused shape {w.shape}")
     return q, s
 
 
@@ -39,12 +41,12 @@ def quantize_q4(w, threads=0):
     """edgelm quantize_q4: u8 [N,K/2] (16 bytes per 32-group) + f32 scale per (row, group)."""
     w = np.ascontiguousarray(w, dtype=np.float32)
     n, k = w.shape
-    if k % 32:
-        raise ValueError("q4 needs K % 32 == 0")
-    q = np.empty((n, k // 2), np.uint8)
-    s = np.empty((n, k // 32), np.float32)
-    lib().elm_quantize_q4(C.c_void_p(w.ctypes.data), C.c_int64(n), C.c_int64(k), C.c_void_p(q.ctypes.data),
-                          C.c_void_p(s.ctypes.data), C.c_int(_threads(threads)))
+    q = np.empty((n, max(k, 0) // 2), np.uint8)
+    s = np.empty((n, max(k, 0) // 32), np.float32)
+    rc = lib().elm_quantize_q4(C.c_void_p(w.ctypes.data), C.c_int64(n), C.c_int64(k), C.c_void_p(q.ctypes.data),
+                               C.c_void_p(s.ctypes.data), C.c_int(_threads(threads)))
+    if rc != 0:
+        raise ValueError(f"elm_quantize_q4 refused shape {w.shape} (K must be a positive multiple of 32)")
     return q, s
 
 

@@ -153,6 +153,11 @@ class HipBackend : public Backend {
     }
     step_checks(p, c);
     upload_step_inputs(p, c);
+    if (sg.exec && sg.scratch_gen != elmh_scratch_generation(ctx_)) {
+      // the library's scratch moved since the capture (a larger op ran in between): capture again
+      elmh_graph_destroy(ctx_, sg.exec);
+      sg.exec = nullptr;
+    }
     if (!sg.exec) {
       capturing_ = true;
       const uint64_t gen = buffer_gen_;
@@ -172,6 +177,7 @@ class HipBackend : public Backend {
       capturing_ = false;
       if (rc != ELMH_OK) throw std::runtime_error(std::string("edgelm: hip graph capture: ") + elmh_last_error(ctx_));
       if (gen != buffer_gen_) throw std::runtime_error("edgelm: hip graph capture: a buffer moved while capturing");
+      sg.scratch_gen = elmh_scratch_generation(ctx_);
     }
     if (elmh_graph_launch(ctx_, sg.exec) != ELMH_OK)
       throw std::runtime_error(std::string("edgelm: hip graph launch: ") + elmh_last_error(ctx_));
@@ -380,6 +386,7 @@ class HipBackend : public Backend {
   struct StepGraph {
     int warm = 0;
     void* exec = nullptr;
+    uint64_t scratch_gen = 0;  // elmh_scratch_generation at capture
   };
 
   void drop_graphs() {

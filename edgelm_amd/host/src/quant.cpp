@@ -59,11 +59,16 @@ void split_rows(int64_t n, int threads, F&& f) {
 
 }  // namespace
 
-extern "C" void elm_quantize_q8(const float* w, int64_t n, int64_t k, int8_t* out, float* scales, int threads) {
+extern "C" int elm_quantize_q8(const float* w, int64_t n, int64_t k, int8_t* out, float* scales, int threads) {
+  if (n < 0 || k < 1 || (n && (!w || !out || !scales))) return -1;
   split_rows(n, threads, [&](int64_t a, int64_t b) { q8_rows(w, a, b, k, out, scales); });
+  return 0;
 }
 
-extern "C" void elm_quantize_q4(const float* w, int64_t n, int64_t k, uint8_t* out, float* scales, int threads) {
-  if (k % 32) return;
+// edgelm's quantize_q4 refuses K % 32 != 0 through EDGELM_CHECK (model.cpp:165-167); so does this one,
+// before writing anything.
+extern "C" int elm_quantize_q4(const float* w, int64_t n, int64_t k, uint8_t* out, float* scales, int threads) {
+  if (n < 0 || k < 32 || k % 32 || (n && (!w || !out || !scales))) return -1;
   split_rows(n, threads, [&](int64_t a, int64_t b) { q4_rows(w, a, b, k, out, scales); });
+  return 0;
 }

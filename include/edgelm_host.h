@@ -11,9 +11,11 @@ extern "C" {
 #endif
 
 /* Load-time quantizers, bit-identical to edgelm's quantize_q8 (model.cpp:150-163) and
- * quantize_q4 (model.cpp:165-190); rows are split over `threads` host threads. */
-void elm_quantize_q8(const float* w, int64_t n, int64_t k, int8_t* out, float* scales, int threads);
-void elm_quantize_q4(const float* w, int64_t n, int64_t k, uint8_t* out, float* scales, int threads);
+ * quantize_q4 (model.cpp:165-190); rows are split over `threads` host threads. Return 0, or -1
+ * without writing anything for a bad shape (q4: K not a positive multiple of 32, as edgelm's
+ * EDGELM_CHECK refuses) or a null pointer. */
+int elm_quantize_q8(const float* w, int64_t n, int64_t k, int8_t* out, float* scales, int threads);
+int elm_quantize_q4(const float* w, int64_t n, int64_t k, uint8_t* out, float* scales, int threads);
 
 /* ---- models and sessions (edgelm's Model / Session, reference runtime.hpp:17-67) ----
  * Every call returns 0 / a handle on success; on failure -1 / NULL and elm_last_error() says why. */

@@ -95,6 +95,11 @@ int elmh_swiglu(elmh_ctx* ctx, const float* x, int T, int64_t K, const elmh_weig
 /* ---- device-resident variants: same semantics, device pointers, asynchronous on the context
  * stream (no host synchronization; capturable in a HIP graph once scratch is reserved). */
 int elmh_reserve(elmh_ctx* ctx, int max_T, int64_t max_K);
+/* Counter of the context's scratch reallocations. A *_dev call whose shape needs more scratch than is
+ * reserved reallocates it (outside capture) and bumps the counter; a HIP graph captured while the
+ * counter had another value holds freed addresses and must be captured again before it is launched.
+ * No counterpart in edgelm: for callers that replay graphs (this build's hip backend). */
+uint64_t elmh_scratch_generation(const elmh_ctx* ctx);
 int elmh_matmul_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, int n_targets, elmh_weight* const* w,
                     float* const* y, const float* const* residual, int act, int mode);
 int elmh_swiglu_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, const elmh_weight* wg,

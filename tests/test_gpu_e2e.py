@@ -137,3 +137,26 @@ def test_generate_device_argmax_matches_edgelm(tiny, smollm, backends):
         got = s.generate(prompt, gen)["tokens"].tolist()
         s.close()
         assert got == ref_greedy(path, prompt, gen, batch, True, mc)
+
+
+@pytest.mark.parametrize("dt", ["q8", "q4"])
+def test_decode_graphs_survive_larger_forwards(tiny, dt):
+    """Decode steps replay captured graphs; a later, larger forward grows device buffers and the library's
+    scratch, after which the next decode step must capture again (elmh_scratch_generation) instead of
+    replaying addresses that were freed. Short prompt, decodes, a longer chunk, decodes, a reset and a
+    still longer chunk: logits bit-identical to edgelm's session at every step."""
+    m = host.Model(tiny[dt])
+    ids = np.random.default_rng(17).integers(0, 320, 64).astype(np.int32)
+    mine = host.Session(m, "hip,cpu", threads=4, max_ctx=64, max_batch=48, all_logits=True, act_quant=True)
+    ref = O.RefSession(tiny[dt], "cpu", threads=4, max_ctx=64, max_batch=48, all_logits=True, act_quant=True)
+    plan = [("prefill", ids[:3])] + [("decode", ids[3 + i:4 + i]) for i in range(4)] + [("chunk", ids[7:37])] + \
+           [("decode", ids[37 + i:38 + i]) for i in range(5)] + [("reset", None), ("chunk", ids[:48])] + \
+           [("decode", ids[48 + i:49 + i]) for i in range(4)]
+    for step, (what, toks) in enumerate(plan):
+        if what == "reset":
+            mine.reset(), ref.reset()
+            continue
+        print(f"[gpu] graph regrowth {dt} step {step}: {what} of {len(toks)}", flush=True)
+        a, b = mine.forward(toks), ref.forward(toks)
+        assert bits_equal(a, b), f"step {step} ({what}): max diff {np.abs(a - b).max()}"
+    mine.close(), ref.close()

@@ -190,3 +190,145 @@ def test_device_expf_matches_libm_exhaustively(tmp_path):
                     str(exe), "-lm"], check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
     assert out.returncode == 0 and out.stdout.strip() == "0", out.stdout
+
+
+@needs_ref
+def test_act_quant_applies_against_reference_build():
+    """act_quant_applies (kernels.hpp:46-48): with K % 32 != 0, or f32 weights, int8 activations do not apply and
+    edgelm's cpu and reference backends take the f32 path; the oracle must agree with edgelm's build there."""
+    r = np.random.default_rng(12)
+    pool = O.RefPool(2, 9, 200)
+    try:
+        for k, dt in [(40, O.Q8), (72, O.Q8), (200, O.Q8), (64, O.F32), (96, O.F32)]:
+            n = 37
+            W = O.make_weight(r.normal(0, 0.05, (n, k)).astype(np.float32), dt)
+            Wu = O.make_weight(r.normal(0, 0.05, (n, k)).astype(np.float32), dt)
+            for T in (1, 9):
+                x = r.normal(0, 1, (T, k)).astype(np.float32)
+                res = r.normal(0, 1, (T, n)).astype(np.float32)
+                a8 = O.cpu_matmul(x, [W], [res], True)[0]
+                assert bits_equal(a8, O.rq_cpu_matmul(pool, x, [W], [res], True)[0]), (k, dt, T)
+                assert bits_equal(a8, O.cpu_matmul(x, [W], [res], False)[0]), (k, dt, T)
+                assert bits_equal(O.ref_matmul(x, W, res, True), O.rq_ref_matmul(x, W, res, True)), (k, dt, T)
+                assert bits_equal(O.cpu_swiglu(x, W, Wu, True), O.rq_cpu_swiglu(pool, x, W, Wu, True)), (k, dt, T)
+    finally:
+        pool.close()
+
+
+# ---- the per-token activation mode (an extension: edgelm has no such mode, so nothing of edgelm's pins it
+# directly; these checks tie it to the pinned per-block quantizer and matmul, and to integer brute force) ----
+
+def _rows_with_shared_block_max(r, T, K):
+    """Rows where every 32-block holds the row's largest magnitude (both signs occur), so the per-block
+    scales all equal the per-row one."""
+    x = r.normal(0, 1, (T, K)).astype(np.float32)
+    amax = np.float32(5.0) + np.abs(x).max()
+    for t in range(T):
+        for b in range(K // 32):
+            x[t, b * 32 + r.integers(0, 32)] = amax if (t + b) % 2 else -amax
+    return x
+
+
+def test_token_quantizer_equals_block_quantizer_when_block_maxima_agree():
+    r = np.random.default_rng(21)
+    x = _rows_with_shared_block_max(r, 6, 256)
+    q, d = O.quantize_act_token(x)
+    qb, db = O.quantize_act(x)
+    assert np.array_equal(q, qb) and np.all(db == d[:, None])
+    if O.ref_available():
+        qr, dr = O.rq_quantize_act(x)
+        assert np.array_equal(q, qr) and np.all(dr == d[:, None])
+
+
+def test_token_quantizer_closed_forms():
+    r = np.random.default_rng(22)
+    x = r.normal(0, 1, (7, 160)).astype(np.float32)
+    x[2] = 0.0
+    x[3, 17] = -40.0  # an outlier sets the whole row's scale
+    q, d = O.quantize_act_token(x)
+    assert d[2] == 0 and np.all(q[2] == 0)
+    nz = d > 0
+    assert np.all(d == (np.abs(x).max(axis=1) / np.float32(127)).astype(np.float32))
+    assert np.all(np.abs(q[nz].astype(np.int32)).max(axis=1) == 127)
+    err = np.abs(q.astype(np.float64) * d[:, None].astype(np.float64) - x)
+    assert np.all(err <= d[:, None] * 0.5 * (1 + 1e-6))
+    assert q[3, 17] == -127 and np.abs(q[3]).astype(np.int32).sum() < np.abs(q[4]).astype(np.int32).sum()
+
+
+def _int_weights(W):
+    if W.dtype == O.Q8:
+        return W.data.astype(np.int64)
+    p = W.data.reshape(W.rows, W.cols // 32, 16).astype(np.int64)
+    return np.concatenate([(p & 15) - 8, (p >> 4) - 8], axis=2).reshape(W.rows, W.cols)
+
+
+def test_token_matmul_integer_sums_brute_force():
+    """q8: one int32 sum over all of K (numpy int64 brute force), then (float(S) * d) * ws;
+    q4: int32 sums per 32-group, folded in group order as float(S_g) * ws_g, then * d."""
+    r = np.random.default_rng(23)
+    for dt in (O.Q8, O.Q4):
+        n, k, T = 53, 224, 5
+        W = O.make_weight(r.normal(0, 0.05, (n, k)).astype(np.float32), dt)
+        x = r.normal(0, 1, (T, k)).astype(np.float32)
+        res = r.normal(0, 1, (T, n)).astype(np.float32)
+        xq, d = O.quantize_act_token(x)
+        wq = _int_weights(W)
+        if dt == O.Q8:
+            S = xq.astype(np.int64) @ wq.T
+            assert np.abs(S).max() < 2 ** 24
+            want = (S.astype(np.float32) * d[:, None]) * W.scales[None, :]
+        else:
+            Sg = np.einsum("tgi,ngi->tng", xq.astype(np.int64).reshape(T, k // 32, 32), wq.reshape(n, k // 32, 32))
+            acc = np.zeros((T, n), np.float32)
+            for g in range(k // 32):
+                acc = acc + Sg[:, :, g].astype(np.float32) * W.scales[None, :, g]
+            want = acc * d[:, None]
+        assert bits_equal(O.matmul_a8_token(x, W), want), dt
+        assert bits_equal(O.matmul_a8_token(x, W, res), res + want), dt
+
+
+def test_token_matmul_equals_edgelm_where_the_modes_coincide():
+    """With a single nonzero 32-block per row the per-block fold has one term, and with a power-of-two scale
+    (block max 127 * 2^-3) every rescale is exact: the per-token result then equals edgelm's per-block
+    cpu::matmul bit for bit."""
+    r = np.random.default_rng(24)
+    for dt in (O.Q8, O.Q4):
+        n, k, T = 41, 192, 4
+        W = O.make_weight(r.normal(0, 0.05, (n, k)).astype(np.float32), dt)
+        x = np.zeros((T, k), np.float32)
+        for t in range(T):
+            b = (2 * t + 1) % (k // 32)
+            blk = r.normal(0, 0.03, 32).astype(np.float32)
+            blk[r.integers(0, 32)] = np.float32(127 * 0.125) * (1 if t % 2 else -1)
+            x[t, b * 32:(b + 1) * 32] = blk
+        _, d = O.quantize_act_token(x)
+        assert np.all(d == np.float32(0.125))
+        want = O.cpu_matmul(x, [W], None, act_quant=True)[0]
+        assert bits_equal(O.matmul_a8_token(x, W), want), dt
+
+
+@needs_ref
+def test_oracle_tiny_magnitudes_against_reference_build():
+    """Scales and activation blocks near and below the normal range: the oracle keeps edgelm's float order there
+    too (q4: float(S) * (ws * xd) per block, subnormal products included)."""
+    r = np.random.default_rng(13)
+    pool = O.RefPool(2, 40, 576)
+    try:
+        for dt in (O.Q8, O.Q4):
+            w = r.normal(0, 0.05, (40, 576)).astype(np.float32)
+            w[1] *= np.float32(1e-30)
+            w[2] *= np.float32(1e-36)
+            w[3] = np.float32(3e-39) * np.sign(w[3])
+            W = O.make_weight(w, dt)
+            Wu = O.make_weight(r.normal(0, 0.05, (40, 576)).astype(np.float32), dt)
+            for T in (1, 5, 33):
+                x = r.normal(0, 1, (T, 576)).astype(np.float32)
+                x[:, 32:64] *= np.float32(1e-33)
+                x[:, 96:128] *= np.float32(1e-38)
+                x[:, 160:192] = np.float32(2e-42)
+                res = r.normal(0, 1e-30, (T, 40)).astype(np.float32)
+                for aq in (False, True):
+                    assert bits_equal(O.cpu_matmul(x, [W], [res], aq)[0], O.rq_cpu_matmul(pool, x, [W], [res], aq)[0])
+                    assert bits_equal(O.cpu_swiglu(x, W, Wu, aq), O.rq_cpu_swiglu(pool, x, W, Wu, aq))
+    finally:
+        pool.close()
