@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -29,6 +30,15 @@ struct DevBuf {
 
 thread_local std::string g_last_error;
 
+// Scratch of elmh_matmul_noalloc_dev: a fixed device array, one copy per GPU the library runs on,
+// held until the process ends. In host code `scratch` names a host-side stand-in, never a device
+// address: elmh_create looks up each device's copy with hipGetSymbolAddress (that device current)
+// and every host use goes through the pointer kept in g_noalloc_ptr.
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::mutex g_noalloc_mu;
+std::vector<unsigned char*> g_noalloc_ptr;  // per device id
+
 }  // namespace
 
 struct elmh_ctx {
@@ -46,6 +56,8 @@ struct elmh_ctx {
   DevBuf nrm;
   // bumped whenever a scratch buffer above moves (a graph captured before then holds stale addresses)
   uint64_t scratch_gen = 0;
+  // this device's copy of the no-allocation scratch array
+  unsigned char* noalloc = nullptr;
 };
 
 namespace {
@@ -248,39 +260,75 @@ int run_f32_group(elmh_ctx* c, const float* x, int T, int64_t K, const std::vect
   return ELMH_OK;
 }
 
-int quant_frag(elmh_ctx* c, const float* x, int T, int64_t K, int token_mode, int* Tpad_out) {
+// Where one call's quantized activation lives: the context's buffers (grown on demand), or with
+// `fixed` set a region of fixed size carved into the same three parts (the no-allocation entry point).
+struct Scratch {
+  unsigned char* fixed = nullptr;
+  size_t fixed_bytes = 0;
+};
+struct ActBufs {
+  int8_t* q = nullptr;  // int8 values (row-major or GEMM fragments)
+  float* d = nullptr;   // scales
+  int32_t* s = nullptr; // block sums of q (row-major GEMV path only)
+};
+
+int act_buffers(elmh_ctx* c, const Scratch& sc, size_t q_bytes, size_t d_bytes, size_t s_bytes, ActBufs* out) {
+  if (sc.fixed) {
+    const size_t d_off = (size_t)round_up((int64_t)q_bytes, 256), s_off = (size_t)round_up((int64_t)(d_off + d_bytes), 256);
+    const size_t need = s_off + s_bytes;
+    if (need > sc.fixed_bytes)
+      return fail(c, ELMH_ERR_ARG, "the activation needs %zu bytes of scratch; the no-allocation entry point has %zu",
+                  need, sc.fixed_bytes);
+    out->q = (int8_t*)sc.fixed;
+    out->d = (float*)(sc.fixed + d_off);
+    out->s = s_bytes ? (int32_t*)(sc.fixed + s_off) : nullptr;
+    return ELMH_OK;
+  }
+  int rc;
+  if ((rc = ensure(c, c->xq, q_bytes))) return rc;
+  if ((rc = ensure(c, c->xd, d_bytes))) return rc;
+  if (s_bytes && (rc = ensure(c, c->xs, s_bytes))) return rc;
+  out->q = (int8_t*)c->xq.p;
+  out->d = (float*)c->xd.p;
+  out->s = s_bytes ? (int32_t*)c->xs.p : nullptr;
+  return ELMH_OK;
+}
+
+// x quantized into the GEMM's fragments: every one of the Tpad token slots is written (zeros past T),
+// so nothing left in the buffer by an earlier call is read
+int quant_frag(elmh_ctx* c, const Scratch& sc, const float* x, int T, int64_t K, int token_mode, int* Tpad_out,
+               ActBufs* a) {
   const int Tpad = (int)round_up(T, kGemmTileT);
   const int64_t nb = K / kBlock;
   int rc;
-  if ((rc = ensure(c, c->xq, (size_t)Tpad * K))) return rc;
-  if ((rc = ensure(c, c->xd, (size_t)Tpad * nb * sizeof(float)))) return rc;
+  if ((rc = act_buffers(c, sc, (size_t)Tpad * K, (size_t)Tpad * (token_mode ? 1 : nb) * sizeof(float), 0, a)))
+    return rc;
   if (token_mode)
-    HIP_OR_FAIL(c, launch_act_quant_frag_token(x, T, Tpad, (int)K, (int8_t*)c->xq.p, (float*)c->xd.p, c->stream));
+    HIP_OR_FAIL(c, launch_act_quant_frag_token(x, T, Tpad, (int)K, a->q, a->d, c->stream));
   else
-    HIP_OR_FAIL(c, launch_act_quant_frag(x, T, Tpad, (int)K, (int8_t*)c->xq.p, (float*)c->xd.p, c->stream));
+    HIP_OR_FAIL(c, launch_act_quant_frag(x, T, Tpad, (int)K, a->q, a->d, c->stream));
   *Tpad_out = Tpad;
   return ELMH_OK;
 }
 
 // RMSNORM and the block-scale fragment quantization in one launch (K <= 2048)
-int quant_frag_norm(elmh_ctx* c, const float* x, const float* nw, float eps, int T, int64_t K, int* Tpad_out) {
+int quant_frag_norm(elmh_ctx* c, const float* x, const float* nw, float eps, int T, int64_t K, int* Tpad_out,
+                    ActBufs* a) {
   const int Tpad = (int)round_up(T, kGemmTileT);
   const int64_t nb = K / kBlock;
   int rc;
-  if ((rc = ensure(c, c->xq, (size_t)Tpad * K))) return rc;
-  if ((rc = ensure(c, c->xd, (size_t)Tpad * nb * sizeof(float)))) return rc;
-  HIP_OR_FAIL(c, launch_rmsnorm_quant_frag(x, nw, eps, T, Tpad, (int)K, (int8_t*)c->xq.p, (float*)c->xd.p, c->stream));
+  if ((rc = act_buffers(c, Scratch{}, (size_t)Tpad * K, (size_t)Tpad * nb * sizeof(float), 0, a))) return rc;
+  HIP_OR_FAIL(c, launch_rmsnorm_quant_frag(x, nw, eps, T, Tpad, (int)K, a->q, a->d, c->stream));
   *Tpad_out = Tpad;
   return ELMH_OK;
 }
 
-int quant_rows(elmh_ctx* c, const float* x, int T, int64_t K) {
+int quant_rows(elmh_ctx* c, const Scratch& sc, const float* x, int T, int64_t K, ActBufs* a) {
   const int64_t nb = K / kBlock;
   int rc;
-  if ((rc = ensure(c, c->xq, (size_t)T * K))) return rc;
-  if ((rc = ensure(c, c->xd, (size_t)T * nb * sizeof(float)))) return rc;
-  if ((rc = ensure(c, c->xs, (size_t)T * nb * sizeof(int32_t)))) return rc;
-  HIP_OR_FAIL(c, launch_act_quant_rows(x, T, (int)K, (int8_t*)c->xq.p, (float*)c->xd.p, (int32_t*)c->xs.p, c->stream));
+  if ((rc = act_buffers(c, sc, (size_t)T * K, (size_t)T * nb * sizeof(float), (size_t)T * nb * sizeof(int32_t), a)))
+    return rc;
+  HIP_OR_FAIL(c, launch_act_quant_rows(x, T, (int)K, a->q, a->d, a->s, c->stream));
   return ELMH_OK;
 }
 
@@ -295,7 +343,7 @@ std::vector<std::vector<int>> by_dtype(int n, elmh_weight* const* w) {
 }
 
 int run_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight* const* w, float* const* y,
-               const float* const* res, int act, int mode) {
+               const float* const* res, int act, int mode, const Scratch& sc = Scratch{}) {
   int rc = check_targets(c, T, K, n, w, y);
   if (rc) return rc;
   if (act < ELMH_ACT_F32 || act > ELMH_ACT_INT8_TOKEN) return fail(c, ELMH_ERR_ARG, "bad act mode %d", act);
@@ -309,10 +357,10 @@ int run_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight
   }
   if (act == ELMH_ACT_INT8_TOKEN) {
     int Tpad;
-    if ((rc = quant_frag(c, x, T, K, 1, &Tpad))) return rc;
+    ActBufs ab;
+    if ((rc = quant_frag(c, sc, x, T, K, 1, &Tpad, &ab))) return rc;
     for (const auto& g : groups)
-      if ((rc = run_gemm_group(c, (const int8_t*)c->xq.p, (const float*)c->xd.p, T, Tpad, K, g, w, y, res, 1,
-                               mode == ELMH_FAST)))
+      if ((rc = run_gemm_group(c, ab.q, ab.d, T, Tpad, K, g, w, y, res, 1, mode == ELMH_FAST)))
         return rc;
     return ELMH_OK;
   }
@@ -325,19 +373,18 @@ int run_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight
     // f32 x to the kernel (each workgroup quantizes it) unless it is too long for the streaming
     // kernel's registers: then one quantizer launch first
     const bool xin = qin || stream_qin_ok(T, (int)K);
-    if (!xin && (rc = quant_rows(c, x, T, K))) return rc;
+    ActBufs ab;
+    if (!xin && (rc = quant_rows(c, sc, x, T, K, &ab))) return rc;
     for (const auto& g : groups)
-      if ((rc = run_gemv_group(c, xin ? x : nullptr, xin ? nullptr : (const int8_t*)c->xq.p,
-                               xin ? nullptr : (const float*)c->xd.p, xin ? nullptr : (const int32_t*)c->xs.p, T, K,
-                               g, w, y, res, !qin)))
+      if ((rc = run_gemv_group(c, xin ? x : nullptr, ab.q, ab.d, ab.s, T, K, g, w, y, res, !qin)))
         return rc;
     return ELMH_OK;
   }
   int Tpad;
-  if ((rc = quant_frag(c, x, T, K, 0, &Tpad))) return rc;
+  ActBufs ab;
+  if ((rc = quant_frag(c, sc, x, T, K, 0, &Tpad, &ab))) return rc;
   for (const auto& g : groups)
-    if ((rc = run_gemm_group(c, (const int8_t*)c->xq.p, (const float*)c->xd.p, T, Tpad, K, g, w, y, res, 0,
-                             mode == ELMH_FAST)))
+    if ((rc = run_gemm_group(c, ab.q, ab.d, T, Tpad, K, g, w, y, res, 0, mode == ELMH_FAST)))
       return rc;
   return ELMH_OK;
 }
@@ -386,7 +433,8 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
   if (act == ELMH_ACT_INT8 && T <= nt) {
     GemvArgs a{};
     const bool xin = qin || stream_qin_ok(T, (int)K);  // as in run_matmul
-    if (!xin && (rc = quant_rows(c, x, T, K))) return rc;
+    ActBufs ab;
+    if (!xin && (rc = quant_rows(c, Scratch{}, x, T, K, &ab))) return rc;
     const int tiles = (int)(g.rows_pad / g.H);
     a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, tiles};
     a.tg[1] = {u.data, u.scales, y, nullptr, (int)u.rows, tiles};
@@ -398,9 +446,9 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
     a.stream = !qin;
     a.nw = nw;  // set only when this small path applies (norm_fusable)
     a.eps = eps;
-    a.xq = xin ? nullptr : (const int8_t*)c->xq.p;
-    a.xd = xin ? nullptr : (const float*)c->xd.p;
-    a.xs = xin ? nullptr : (const int32_t*)c->xs.p;
+    a.xq = ab.q;
+    a.xd = ab.d;
+    a.xs = ab.s;
     a.T = T;
     a.K = (int)K;
     a.nb = (int)(K / kBlock);
@@ -409,15 +457,17 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
   }
   const int token = act == ELMH_ACT_INT8_TOKEN;
   int Tpad;
-  if ((rc = nw ? quant_frag_norm(c, x, nw, eps, T, K, &Tpad) : quant_frag(c, x, T, K, token, &Tpad))) return rc;
+  ActBufs ab;
+  if ((rc = nw ? quant_frag_norm(c, x, nw, eps, T, K, &Tpad, &ab) : quant_frag(c, Scratch{}, x, T, K, token, &Tpad, &ab)))
+    return rc;
   GemmArgs a{};
   const int tiles = (int)((g.rows_pad + kGemmTileN - 1) / kGemmTileN);
   a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, tiles};
   a.tg[1] = {u.data, u.scales, y, nullptr, (int)u.rows, tiles};
   a.n_targets = 2;
   a.H = g.H;
-  a.xq = (const int8_t*)c->xq.p;
-  a.xd = (const float*)c->xd.p;
+  a.xq = ab.q;
+  a.xd = ab.d;
   a.T = T;
   a.Tpad = Tpad;
   a.K = (int)K;
@@ -521,6 +571,22 @@ int elmh_create(int device, elmh_ctx** out) {
     delete c;
     return fail(nullptr, ELMH_ERR_HIP, "stream creation failed");
   }
+  {
+    // once per device, with the device current: the device address of its copy of `scratch`
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if ((size_t)device >= g_noalloc_ptr.size()) g_noalloc_ptr.resize((size_t)device + 1, nullptr);
+    if (!g_noalloc_ptr[device]) {
+      void* p = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return fail(nullptr, ELMH_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+      }
+      g_noalloc_ptr[device] = static_cast<unsigned char*>(p);
+    }
+    c->noalloc = g_noalloc_ptr[device];
+  }
   *out = c;
   return ELMH_OK;
 }
@@ -529,7 +595,7 @@ void elmh_destroy(elmh_ctx* c) {
   if (!c) return;
   DeviceGuard g(c);
   (void)hipStreamSynchronize(c->stream);
-  for (DevBuf* b : {&c->x, &c->y, &c->res, &c->xq, &c->xd, &c->xs, &c->gu})
+  for (DevBuf* b : {&c->x, &c->y, &c->res, &c->xq, &c->xd, &c->xs, &c->gu, &c->nrm})
     if (b->p) (void)hipFree(b->p);
   (void)hipStreamDestroy(c->stream);
   delete c;
@@ -624,6 +690,14 @@ int elmh_matmul_dev(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_w
   return run_matmul(c, x, T, K, n, w, y, res, act, mode);
 }
 
+int elmh_matmul_noalloc_dev(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight* const* w,
+                            float* const* y, const float* const* res, int act, int mode) {
+  if (!c || !x) return fail(c, ELMH_ERR_ARG, "null ctx/x");
+  if (!c->noalloc) return fail(c, ELMH_ERR_HIP, "no-allocation scratch missing on device %d", c->device);
+  DeviceGuard g(c);
+  return run_matmul(c, x, T, K, n, w, y, res, act, mode, Scratch{c->noalloc, kNoAllocScratchBytes});
+}
+
 int elmh_swiglu_dev(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight* wg, const elmh_weight* wu,
                     float* y, int act, int mode) {
   if (!c || !x) return fail(c, ELMH_ERR_ARG, "null ctx/x");
@@ -645,10 +719,10 @@ int elmh_rmsnorm_matmul_dev(elmh_ctx* c, const float* x, const float* norm_w, fl
   }
   if (norm_gemm(T, K, n, w, 1, act)) {  // the block-scale GEMM: RMSNORM inside its quantizer launch
     int Tpad;
-    if ((rc = quant_frag_norm(c, x, norm_w, eps, T, K, &Tpad))) return rc;
+    ActBufs ab;
+    if ((rc = quant_frag_norm(c, x, norm_w, eps, T, K, &Tpad, &ab))) return rc;
     for (const auto& grp : by_dtype(n, w))
-      if ((rc = run_gemm_group(c, (const int8_t*)c->xq.p, (const float*)c->xd.p, T, Tpad, K, grp, w, y, res, 0,
-                               mode == ELMH_FAST)))
+      if ((rc = run_gemm_group(c, ab.q, ab.d, T, Tpad, K, grp, w, y, res, 0, mode == ELMH_FAST)))
         return rc;
     return ELMH_OK;
   }
@@ -752,9 +826,10 @@ int elmh_quantize_act(elmh_ctx* c, const float* x, int T, int64_t K, int8_t* q, 
   const int64_t nb = K / kBlock;
   if ((rc = ensure(c, c->x, (size_t)T * K * sizeof(float)))) return rc;
   HIP_OR_FAIL(c, hipMemcpyAsync(c->x.p, x, (size_t)T * K * sizeof(float), hipMemcpyHostToDevice, c->stream));
-  if ((rc = quant_rows(c, (const float*)c->x.p, T, K))) return rc;
-  HIP_OR_FAIL(c, hipMemcpyAsync(q, c->xq.p, (size_t)T * K, hipMemcpyDeviceToHost, c->stream));
-  HIP_OR_FAIL(c, hipMemcpyAsync(d, c->xd.p, (size_t)T * nb * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+  ActBufs ab;
+  if ((rc = quant_rows(c, Scratch{}, (const float*)c->x.p, T, K, &ab))) return rc;
+  HIP_OR_FAIL(c, hipMemcpyAsync(q, ab.q, (size_t)T * K, hipMemcpyDeviceToHost, c->stream));
+  HIP_OR_FAIL(c, hipMemcpyAsync(d, ab.d, (size_t)T * nb * sizeof(float), hipMemcpyDeviceToHost, c->stream));
   HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
   return ELMH_OK;
 }
@@ -900,10 +975,11 @@ int elmh_attention_matmul_dev(elmh_ctx* c, const float* q, const float* k, const
   const int Tpad = (int)round_up(T, kGemmTileT);
   if (T > 1 && head_dim == 64 && block_gemm(T, K, 1, ws, 1, act)) {
     // the GEMM's activation fragments come out of the attention kernel
-    if ((rc = ensure(c, c->xq, (size_t)Tpad * K))) return rc;
-    if ((rc = ensure(c, c->xd, (size_t)Tpad * (K / kBlock) * sizeof(float)))) return rc;
-    xq = (int8_t*)c->xq.p;
-    xd = (float*)c->xd.p;
+    ActBufs ab;
+    if ((rc = act_buffers(c, Scratch{}, (size_t)Tpad * K, (size_t)Tpad * (K / kBlock) * sizeof(float), 0, &ab)))
+      return rc;
+    xq = ab.q;
+    xd = ab.d;
   }
   bool quantized = false;
   HIP_OR_FAIL(c, launch_attention(q, k, v, out, T, pos0, nullptr, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx,

@@ -189,6 +189,15 @@ class Context:
         self._check(lib().elmh_matmul_dev(self.h, C.c_void_p(x_ptr), C.c_int(T), C.c_int64(K), C.c_int(n), wp, yp, rp,
                                           C.c_int(act), C.c_int(mode)))
 
+    def matmul_noalloc_dev(self, x_ptr, T, K, weights, y_ptrs, res_ptrs=None, act=ACT_INT8, mode=EXACT):
+        """elmh_matmul_noalloc_dev: matmul_dev with the activation in the library's fixed scratch array."""
+        n = len(weights)
+        wp = (C.c_void_p * n)(*[w.h.value for w in weights])
+        yp = (C.c_void_p * n)(*y_ptrs)
+        rp = None if res_ptrs is None else (C.c_void_p * n)(*res_ptrs)
+        self._check(lib().elmh_matmul_noalloc_dev(self.h, C.c_void_p(x_ptr), C.c_int(T), C.c_int64(K), C.c_int(n), wp,
+                                                  yp, rp, C.c_int(act), C.c_int(mode)))
+
     def swiglu_dev(self, x_ptr, T, K, wg, wu, y_ptr, act=ACT_INT8, mode=EXACT):
         self._check(lib().elmh_swiglu_dev(self.h, C.c_void_p(x_ptr), C.c_int(T), C.c_int64(K), wg.h, wu.h,
                                           C.c_void_p(y_ptr), C.c_int(act), C.c_int(mode)))

@@ -104,6 +104,17 @@ int elmh_matmul_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, int n_targe
                     float* const* y, const float* const* residual, int act, int mode);
 int elmh_swiglu_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, const elmh_weight* wg,
                     const elmh_weight* wu, float* y, int act, int mode);
+/* elmh_matmul_dev with no device allocation. No counterpart in edgelm: it is for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that must not call hipMalloc). The same kernels
+ * and the same results, bit for bit; the quantized activation goes to a fixed 8 MiB device array of the
+ * library (one per GPU, held until the process ends) instead of context scratch, so nothing is
+ * allocated or freed. Limit: the quantized activation must fit the array; int8 activations with more
+ * tokens than the GEMV takes need round_up(T, 128) * K bytes plus the scales, e.g. T <= 512 at
+ * K <= 14336; larger calls fail with ELMH_ERR_ARG before anything runs. Every call on one GPU shares that
+ * GPU's array (each call writes all of it that it reads): calls that overlap on one GPU (two contexts,
+ * or two streams, in flight at once) race. */
+int elmh_matmul_noalloc_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, int n_targets, elmh_weight* const* w,
+                            float* const* y, const float* const* residual, int act, int mode);
 
 /* ---- pre-quantized activations (the ActBuf of kernels.hpp:39-44, row-major) ----
  * elmh_quantize_act_dev writes q [T, K] int8, d [T, K/32] f32 and s [T, K/32] int32 block
