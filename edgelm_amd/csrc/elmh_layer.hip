@@ -129,7 +129,7 @@ __global__ __launch_bounds__(64) void kv_append_kernel(const float* __restrict__
                                                        float* __restrict__ kc, float* __restrict__ vc, int pos0,
                                                        const int* __restrict__ pos_dev, int n_kv, int hd, int max_ctx,
                                                        const float* __restrict__ rcos, const float* __restrict__ rsin) {
-  if (pos_dev) pos0 = *pos_dev;
+  if (pos_dev) pos0 = min(max(*pos_dev, 0), max_ctx - 1);  // the caller keeps it in range; stay in bounds anyway
   const int t = blockIdx.x / n_kv, h = blockIdx.x - t * n_kv, pos = pos0 + t, h2 = hd / 2;
   const float* ks = k + ((int64_t)t * n_kv + h) * hd;
   const float* vs = v + ((int64_t)t * n_kv + h) * hd;
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
                                                                  const float* __restrict__ vnew) {
   const int hd = HD ? HD : hd_arg;
   extern __shared__ float lds[];
-  if (pos_dev) pos0 = *pos_dev;
+  if (pos_dev) pos0 = min(max(*pos_dev, 0), max_ctx - 1);  // the caller keeps it in range; stay in bounds anyway
   const int hdp = (hd + 3) & ~3;
   float* qb = lds;
   float* sc = lds + hdp;
@@ -575,10 +575,11 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(const float* __r
 __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tok, int64_t total,
                                                     const uint8_t* __restrict__ data,
                                                     const float* __restrict__ scales, int dtype, int64_t cols,
-                                                    int64_t nb, int H, float* __restrict__ y) {
+                                                    int64_t nb, int H, int64_t rows, float* __restrict__ y) {
   for (int64_t idx = blockIdx.x * 256ll + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
     const int64_t t = idx / cols, k = idx - t * cols;
-    const int64_t row = tok[t], b = k >> 5;
+    // ids are the caller's to check (edgelm checks them on the host); clamping keeps a bad id in bounds
+    const int64_t row = min(max((int64_t)tok[t], (int64_t)0), rows - 1), b = k >> 5;
     const int j = (int)(k & 31);
     const int64_t it = item_index(row, b, nb, H);
     float v;
@@ -761,7 +762,7 @@ hipError_t launch_embed(const int32_t* tok, int T, const DevWeight& w, float* y,
   const int64_t total = (int64_t)T * w.cols;
   const int64_t blocks = (total + 255) / 256;
   embed_kernel<<<(unsigned)(blocks < 4096 ? blocks : 4096), 256, 0, s>>>(tok, total, w.data, w.scales, w.dtype, w.cols,
-                                                                         w.nb, w.H, y);
+                                                                         w.nb, w.H, w.rows, y);
   return hipGetLastError();
 }
 

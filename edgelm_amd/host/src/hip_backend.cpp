@@ -192,7 +192,9 @@ class HipBackend : public Backend {
     if (!ctx_) throw std::runtime_error("edgelm: hip backend created for planning only");
     if (!prepared_) unprepared(*c.graph);
     const int idx = static_cast<int>(&op - c.graph->ops.data());
-    if (idx == first_op_) ++epoch_;  // a new forward
+    // a new upload epoch before any input is read (a fresh buffer has epoch 0, so it is uploaded): once per
+    // forward with prepare(), and for every op without it (no residency: every op uploads its inputs)
+    if (idx == first_op_ || !prepared_) ++epoch_;
     // a deferred RMSNORM (fuse_norm_) applies to this op's input inside the matmul call
     const bool normed = norm_.op == idx - 1 && norm_.op >= 0;
     if (!normed) norm_.op = -1;
@@ -281,7 +283,6 @@ class HipBackend : public Backend {
     for (int t : op.out)
       if (to_host(t)) download(t, c);
     flush();
-    if (!prepared_) ++epoch_;  // no residency: every op uploads its inputs afresh
   }
 
   // greedy sampling: the logits stay in HBM and only the token id crosses to the host

@@ -7,6 +7,9 @@ Two libraries, both built by ``oracle/Makefile`` (called from ``__graft_entry__.
 * ``_ref/libedgelm_ref.so`` — edgelm's own C++ compiled from its sources (plus the
   ``ref_shim.cpp`` C wrappers). Present only where it was built; the built file travels with
   the tree.
+* ``_ref/libedgelm_ref_hip.so`` — the same, with the ``hip`` delegate registered in edgelm's
+  ``make_backend`` at link time (``ref_hip_registration.cpp``): edgelm's own Session, partitioner
+  and backends driving the delegate, for the boundary tests.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import
 this package, and only as the checker or the CPU baseline. The product (``edgelm_amd``)
@@ -20,6 +23,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libedgelm_ref.so")
+REF_HIP_SO = os.path.join(HERE, "_ref", "libedgelm_ref_hip.so")
 
 F32, Q8, Q4 = 0, 1, 2
 
@@ -38,6 +42,7 @@ class _OrcWeight(C.Structure):
 
 _orc = None
 _ref = None
+_ref_hip = None
 
 
 def orc():
@@ -58,22 +63,50 @@ def ref_available():
     return os.path.exists(REF_SO)
 
 
+def _type_ref(lib):
+    lib.eref_pool_create.restype = C.c_void_p
+    lib.eref_pool_create.argtypes = [C.c_int, C.c_int, C.c_int64]
+    lib.eref_pool_destroy.argtypes = [C.c_void_p]
+    lib.eref_session_create.restype = C.c_void_p
+    lib.eref_session_create.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+    for f in ("eref_session_destroy", "eref_session_reset", "eref_session_vocab"):
+        getattr(lib, f).argtypes = [C.c_void_p]
+    lib.eref_last_error.restype = C.c_char_p
+    lib.eref_argmax.restype = C.c_int32
+    return lib
+
+
 def ref():
     global _ref
     if _ref is None:
         if not ref_available():
             raise RuntimeError(f"reference build missing: {REF_SO}")
-        _ref = C.CDLL(REF_SO)
-        _ref.eref_pool_create.restype = C.c_void_p
-        _ref.eref_pool_create.argtypes = [C.c_int, C.c_int, C.c_int64]
-        _ref.eref_pool_destroy.argtypes = [C.c_void_p]
-        _ref.eref_session_create.restype = C.c_void_p
-        _ref.eref_session_create.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
-        for f in ("eref_session_destroy", "eref_session_reset", "eref_session_vocab"):
-            getattr(_ref, f).argtypes = [C.c_void_p]
-        _ref.eref_last_error.restype = C.c_char_p
-        _ref.eref_argmax.restype = C.c_int32
+        _ref = _type_ref(C.CDLL(REF_SO))
     return _ref
+
+
+def ref_hip_available():
+    return os.path.exists(REF_HIP_SO)
+
+
+def ref_hip():
+    """edgelm's own runtime with the hip delegate registered (loads libelmh.so, which needs no GPU to load)."""
+    global _ref_hip
+    if _ref_hip is None:
+        if not ref_hip_available():
+            raise RuntimeError(f"reference build with the hip backend missing: {REF_HIP_SO}")
+        _ref_hip = _type_ref(C.CDLL(REF_HIP_SO))
+        _ref_hip.erefhip_partition.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.c_char_p, C.c_int]
+    return _ref_hip
+
+
+def ref_hip_partition(path, backends, fuse=True):
+    """edgelm's partition_graph over the model with the delegate's claims (planning only, no device)."""
+    buf = C.create_string_buffer(4096)
+    n = ref_hip().erefhip_partition(path.encode(), backends.encode(), int(fuse), buf, 4096)
+    if n < 0:
+        raise RuntimeError("erefhip_partition failed")
+    return n, buf.value.decode()
 
 
 class Weight:
@@ -378,12 +411,15 @@ class RefSession:
     """edgelm's own Session over an .elm file (loader, fusion passes, partitioner, backends)."""
 
     def __init__(self, path, backends="cpu", threads=1, max_ctx=256, max_batch=128, all_logits=False,
-                 act_quant=False):
-        self.h = ref().eref_session_create(path.encode(), backends.encode(), threads, max_ctx, max_batch,
-                                           int(all_logits), int(act_quant))
+                 act_quant=False, fuse=True, with_hip=False):
+        """with_hip: edgelm's runtime built with the hip delegate registered (libedgelm_ref_hip.so), so
+        backends may name "hip" / "hip-matmul" next to edgelm's own "cpu", "matmul-only", "reference"."""
+        self.lib = ref_hip() if with_hip else ref()
+        self.h = self.lib.eref_session_create(path.encode(), backends.encode(), threads, max_ctx, max_batch,
+                                              int(all_logits), int(act_quant), int(fuse))
         if not self.h:
-            raise RuntimeError(ref().eref_last_error().decode())
-        self.vocab = ref().eref_session_vocab(C.c_void_p(self.h))
+            raise RuntimeError(self.lib.eref_last_error().decode())
+        self.vocab = self.lib.eref_session_vocab(C.c_void_p(self.h))
         self.all_logits = all_logits
 
     def forward(self, tokens):
@@ -391,21 +427,21 @@ class RefSession:
         n = len(tokens)
         rows = n if self.all_logits else 1
         out = np.empty((rows, self.vocab), np.float32)
-        if ref().eref_session_forward(C.c_void_p(self.h), _ptr(tokens), C.c_int(n), _ptr(out)):
-            raise RuntimeError(ref().eref_last_error().decode())
+        if self.lib.eref_session_forward(C.c_void_p(self.h), _ptr(tokens), C.c_int(n), _ptr(out)):
+            raise RuntimeError(self.lib.eref_last_error().decode())
         return out
 
     def reset(self):
-        ref().eref_session_reset(C.c_void_p(self.h))
+        self.lib.eref_session_reset(C.c_void_p(self.h))
 
     def describe(self):
         buf = C.create_string_buffer(4096)
-        nops = ref().eref_session_describe(C.c_void_p(self.h), buf, 4096)
+        nops = self.lib.eref_session_describe(C.c_void_p(self.h), buf, 4096)
         return nops, buf.value.decode()
 
     def close(self):
         if self.h:
-            ref().eref_session_destroy(C.c_void_p(self.h))
+            self.lib.eref_session_destroy(C.c_void_p(self.h))
             self.h = None
 
     def __del__(self):

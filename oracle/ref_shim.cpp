@@ -120,7 +120,7 @@ struct RefRun {
 
 // Loads an .elm file and builds a Session. backends: comma-separated preference list.
 void* eref_session_create(const char* path, const char* backends, int threads, int max_ctx, int max_batch,
-                          int all_logits, int act_quant) {
+                          int all_logits, int act_quant, int fuse) {
   try {
     auto r = std::make_unique<RefRun>();
     r->model = Model::load(path);
@@ -140,6 +140,7 @@ void* eref_session_create(const char* path, const char* backends, int threads, i
     o.max_batch = max_batch;
     o.all_logits = all_logits != 0;
     o.act_quant = act_quant != 0;
+    o.fuse = fuse != 0;
     r->session = std::make_unique<Session>(r->model, o);
     return r.release();
   } catch (const std::exception& e) {
