@@ -322,13 +322,13 @@ def e2e_bench(path_dir, P=128, G=64, reps=3, cpu_reference=True):
     build's Session, backends "hip,cpu" (whole model on the GPU) and "hip-matmul,cpu" (matmuls on the
     GPU); edgelm's bench protocol (main.cpp:173-233): LCG prompt, warm-up rep, then the median of
     `reps` reps of prefill + argmax (TTFT) + G greedy decodes."""
-    from edgelm_amd import elm_format as F
+    from edgelm_amd import synth as S
     from edgelm_amd import host
     path = os.path.join(path_dir, "smollm2-135m-random.q4.elm")
     t0 = time.time()
-    F.write_elm(path, F.SMOLLM2_135M, F.random_weights(F.SMOLLM2_135M, 20260101), "q4", embed_dtype="q8")
+    S.write_model(path, S.SMOLLM2_135M, "q4", embed_dtype="q8", seed=20260101)
     log(f"e2e model written in {time.time() - t0:.1f}s ({os.path.getsize(path) / 1e6:.1f} MB)")
-    prompt = F.lcg_prompt(P, 49152)
+    prompt = S.lcg_prompt(P, 49152)
     threads = min(8, os.cpu_count() or 1)
     m = host.Model(path)
     med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731

@@ -82,6 +82,17 @@ def _setup():
     return L
 
 
+def partition_counts(desc):
+    """{backend: (ops, partitions)} from the first line of describe_partitions
+    ("<n> partitions | <backend>: <ops> ops in <parts> | ...")."""
+    out = {}
+    for part in desc.splitlines()[0].split(" | ")[1:]:
+        name, rest = part.split(": ")
+        w = rest.split()
+        out[name] = (int(w[0]), int(w[3]))
+    return out
+
+
 class Model:
     """An .elm file loaded (memory-mapped) by the host library."""
 
@@ -114,6 +125,35 @@ class Model:
         if n < 0:
             raise RuntimeError(_err())
         return n, buf.value.decode()
+
+    def convert(self, dtype, threads=0):
+        """Model::convert_weights: f32 weight matrices to "q8" or "q4" in memory (edgelm model.cpp:220-251)."""
+        L = _setup()
+        L.elm_model_convert.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        if L.elm_model_convert(self.h, {"f32": 0, "q8": 1, "q4": 2}[dtype], _threads(threads)):
+            raise RuntimeError(_err())
+        self.cfg["dtype"] = {"f32": 0, "q8": 1, "q4": 2}[dtype] if dtype != "f32" else self.cfg["dtype"]
+
+    def prefault(self):
+        L = _setup()
+        L.elm_model_prefault.argtypes = [C.c_void_p]
+        if L.elm_model_prefault(self.h):
+            raise RuntimeError(_err())
+
+    def weight(self, name):
+        """(dtype, data, scales) of weight `name` as stored (after any conversion)."""
+        L = _setup()
+        L.elm_model_weight.argtypes = [C.c_void_p, C.c_char_p, C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.c_void_p,
+                                       C.c_void_p]
+        rows, cols = C.c_int64(), C.c_int64()
+        dt = L.elm_model_weight(self.h, name.encode(), C.byref(rows), C.byref(cols), None, None)
+        if dt < 0:
+            raise KeyError(name)
+        r, c = rows.value, cols.value
+        data = np.empty((r, c) if dt != 2 else (r, c // 2), {0: np.float32, 1: np.int8, 2: np.uint8}[dt])
+        scales = None if dt == 0 else np.empty(r if dt == 1 else (r, c // 32), np.float32)
+        L.elm_model_weight(self.h, name.encode(), None, None, data.ctypes.data, None if scales is None else scales.ctypes.data)
+        return dt, data, scales
 
     def close(self):
         if self.h:

@@ -1,6 +1,9 @@
-// .elm model loader (format of the reference's tools/elm.py:1-9, 207-276; C++ loader model.cpp:67-148):
-// the file is memory-mapped and weight tensors point into the mapping.
+// A model as the runtime sees it: the config, the (unfused) graph and the weight arrays of an .elm
+// container (the file format of edgelm's exporter, tools/elm.py:207-276; edgelm's Model is
+// include/edgelm/model.hpp:29-53). Weights point into a read-only mapping of the file, or into
+// buffers the model owns after convert_weights().
 #pragma once
+#include <cstdint>
 #include <memory>
 #include <string>
 #include <vector>
@@ -17,18 +20,29 @@ struct Config {
   bool tied = false;
 };
 
-class Mapping;
+class FileMap;
 
 class Model {
  public:
   static Model load(const std::string& path);
-  size_t weight_bytes() const;
+
+  // Quantize every f32 weight matrix (more than one row) to q8 or q4 in memory, as edgelm's
+  // Model::convert_weights does at load for `--dtype` (model.cpp:220-251, main.cpp:53-60): the same
+  // quantizers, byte for byte; norm vectors stay f32. F32 keeps an f32 file as it is and refuses a
+  // quantized one. Runs the rows over `threads` host threads.
+  void convert_weights(DType target, int threads = 1);
+  // Read every page of the mapping once, so the first forward does not take the page faults
+  // (edgelm's Model::prefault, model.cpp:260-266).
+  void prefault() const;
+  size_t weight_bytes() const;  // data + scales of every weight
+  size_t file_bytes() const;
 
   Config cfg;
   Graph graph;
 
  private:
-  std::shared_ptr<Mapping> map_;
+  std::shared_ptr<const FileMap> file_;
+  std::vector<std::shared_ptr<std::vector<uint8_t>>> converted_;  // arrays made by convert_weights
 };
 
 // edgelm's quantizers (model.cpp:150-190) and row dequantization (model.cpp:192-218).

@@ -1,7 +1,7 @@
-// Session (reference include/edgelm/runtime.hpp:17-67): a fused, partitioned, memory-planned
-// instance of a model's graph with a preallocated KV cache; forward() runs T tokens through the
-// partitions in op order. The MATMUL family goes to the `hip` backend; the remaining ops run on the
-// host ("cpu" / "reference" backends of this build, which carry no quantized-matmul code at all).
+// The runtime around the delegate: graph rewrites, the activation arena planner and the Session
+// (edgelm's interfaces: passes.hpp:12-38, runtime.hpp:17-67). The MATMUL family goes to the `hip`
+// backend; the remaining ops run on the host ("cpu" / "reference" backends of this build, which carry
+// no quantized-matmul code at all).
 #pragma once
 #include <memory>
 #include <string>
@@ -12,7 +12,7 @@
 
 namespace edgelm {
 
-// Graph passes (reference passes.hpp:12-38).
+// Fusion rewrites (edgelm's passes.hpp:12-38); each returns how many fused ops it made.
 int fuse_swiglu(Graph& g);
 int fuse_shared_input(Graph& g);
 int fuse_residual(Graph& g);
@@ -75,7 +75,7 @@ class Session {
   std::vector<Partition> parts_;
   std::unique_ptr<ThreadPool> pool_;
   std::vector<uint8_t> arena_;
-  std::vector<float> kcache_, vcache_;
+  std::vector<float> kv_;  // per layer: keys [n_kv][max_ctx][head_dim], then values
   RopeTable rope_;
   ExecContext ctx_;
   int pos_ = 0;

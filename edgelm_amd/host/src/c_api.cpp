@@ -8,6 +8,10 @@
 
 using namespace edgelm;
 
+namespace edgelm {
+void write_random_model(const std::string& path, const elm_model_spec& spec);  // elm_synth.cpp
+}
+
 struct elm_model {
   Model m;
 };
@@ -69,6 +73,46 @@ elm_model* elm_model_load(const char* path) {
 }
 
 void elm_model_free(elm_model* m) { delete m; }
+
+int elm_model_convert(elm_model* m, int dtype, int threads) {
+  return guard([&] {
+    if (!m) throw std::runtime_error("edgelm: null model");
+    if (dtype < 0 || dtype > 2) throw std::runtime_error("edgelm: convert to f32 (0), q8 (1) or q4 (2)");
+    m->m.convert_weights(static_cast<DType>(dtype), threads);
+    return 0;
+  });
+}
+
+int elm_model_prefault(const elm_model* m) {
+  return guard([&] {
+    if (!m) throw std::runtime_error("edgelm: null model");
+    m->m.prefault();
+    return 0;
+  });
+}
+
+int elm_model_weight(const elm_model* m, const char* name, int64_t* rows, int64_t* cols, void* data, float* scales) {
+  return guard([&] {
+    if (!m || !name) throw std::runtime_error("edgelm: null argument");
+    for (const Tensor& t : m->m.graph.tensors) {
+      if (!t.is_weight() || t.name != name) continue;
+      if (rows) *rows = t.rows;
+      if (cols) *cols = t.cols;
+      if (data) std::memcpy(data, t.data, t.data_bytes);
+      if (scales && t.scales) std::memcpy(scales, t.scales, t.scale_bytes);
+      return static_cast<int>(t.dtype);
+    }
+    return -1;
+  });
+}
+
+int elm_write_random_model(const char* path, const elm_model_spec* spec) {
+  return guard([&] {
+    if (!path || !spec) throw std::runtime_error("edgelm: null argument");
+    write_random_model(path, *spec);
+    return 0;
+  });
+}
 
 int elm_model_config(const elm_model* m, int* o) {
   if (!m || !o) return -1;

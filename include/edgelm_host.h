@@ -17,6 +17,22 @@ extern "C" {
 int elm_quantize_q8(const float* w, int64_t n, int64_t k, int8_t* out, float* scales, int threads);
 int elm_quantize_q4(const float* w, int64_t n, int64_t k, uint8_t* out, float* scales, int threads);
 
+/* ---- synthetic models: a seeded random-init Llama-shaped model written as an .elm file (the
+ * unfused graph edgelm's exporter emits, tools/elm.py:105-161; edgelm's loader reads it). Weight
+ * matrices are N(0, sd), the embedding N(0, embed_sd), norm vectors 1 + N(0, norm_sd); each row comes
+ * from its own splitmix64 stream of (seed, tensor, row), so the file does not depend on `threads`. */
+typedef struct {
+  int32_t vocab, dim, hidden, n_layers, n_heads, n_kv_heads, head_dim, max_seq;
+  float rope_theta, norm_eps;
+  int32_t bos, eos, tied;
+  int32_t weight_dtype; /* every weight matrix: 0 f32, 1 q8, 2 q4 */
+  int32_t embed_dtype;  /* the embedding (and tied LM head); -1: weight_dtype */
+  uint64_t seed;
+  float sd, embed_sd, norm_sd;
+  int32_t threads;
+} elm_model_spec;
+int elm_write_random_model(const char* path, const elm_model_spec* spec);
+
 /* ---- models and sessions (edgelm's Model / Session, reference runtime.hpp:17-67) ----
  * Every call returns 0 / a handle on success; on failure -1 / NULL and elm_last_error() says why. */
 typedef struct elm_model elm_model;
@@ -26,6 +42,14 @@ const char* elm_last_error(void);
 
 elm_model* elm_model_load(const char* path);
 void elm_model_free(elm_model* m);
+/* Model::convert_weights (edgelm model.cpp:220-251): quantize the f32 weight matrices to dtype 1 (q8)
+ * or 2 (q4) in memory, byte-identical to edgelm's; 0 keeps an f32 model. */
+int elm_model_convert(elm_model* m, int dtype, int threads);
+/* Model::prefault: touch every page of the mapping. */
+int elm_model_prefault(const elm_model* m);
+/* Copies weight `name`'s data and scales (either may be NULL) and returns its dtype, or -1 if there is
+ * no such weight; rows/cols get its shape. For tests of the loader and of convert_weights. */
+int elm_model_weight(const elm_model* m, const char* name, int64_t* rows, int64_t* cols, void* data, float* scales);
 /* vocab, dim, hidden, n_layers, n_heads, n_kv_heads, head_dim, max_seq, weight dtype, tied */
 int elm_model_config(const elm_model* m, int* out10);
 /* Fusion statistics of the model's graph: swiglu, shared_input, residual, rope, ops_before, ops_after. */

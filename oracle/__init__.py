@@ -100,6 +100,33 @@ def ref_hip():
     return _ref_hip
 
 
+def partition_counts(desc):
+    """{backend: (ops, partitions)} from edgelm's describe_partitions (backends.cpp:184-201):
+    "<n> partitions: <backend> <ops> ops in <parts>; ..."."""
+    head = desc.splitlines()[0].split(":", 1)[1]
+    out = {}
+    for part in head.split(";"):
+        w = part.split()
+        if len(w) >= 5:
+            out[w[0]] = (int(w[1]), int(w[4]))
+    return out
+
+
+def ref_convert_weight(path, dtype, name, data_cap=1 << 26, scale_cap=1 << 24):
+    """edgelm's Model::load + convert_weights(dtype: 1 q8, 2 q4) on the file, then weight `name` as edgelm
+    holds it: (dtype, data bytes, scale bytes)."""
+    lib = ref()
+    lib.eref_convert_weight.argtypes = [C.c_char_p, C.c_int, C.c_char_p, C.c_void_p, C.POINTER(C.c_int64), C.c_void_p,
+                                        C.POINTER(C.c_int64)]
+    data, scales = np.empty(data_cap, np.uint8), np.empty(scale_cap, np.uint8)
+    nd, ns = C.c_int64(data_cap), C.c_int64(scale_cap)
+    dt = lib.eref_convert_weight(path.encode(), dtype, name.encode(), data.ctypes.data, C.byref(nd), scales.ctypes.data,
+                                 C.byref(ns))
+    if dt < 0:
+        raise RuntimeError(lib.eref_last_error().decode())
+    return dt, data[:nd.value].copy(), scales[:ns.value].copy()
+
+
 def ref_hip_partition(path, backends, fuse=True):
     """edgelm's partition_graph over the model with the delegate's claims (planning only, no device)."""
     buf = C.create_string_buffer(4096)

@@ -169,6 +169,33 @@ int eref_session_forward(void* h, const int32_t* tokens, int n, float* out) {
 
 int32_t eref_argmax(const float* logits, int n) { return argmax(logits, n); }
 
+// edgelm's Model::load then convert_weights(dtype) (model.cpp:220-251); copies weight `name` into data /
+// scales (capacities in, sizes out) and returns its dtype, or -1.
+int eref_convert_weight(const char* path, int dtype, const char* name, void* data, int64_t* data_bytes, void* scales,
+                        int64_t* scale_bytes) {
+  try {
+    Model m = Model::load(path);
+    m.convert_weights(static_cast<DType>(dtype));
+    for (const Tensor& t : m.graph.tensors) {
+      if (!t.is_weight() || t.name != name) continue;
+      if (static_cast<int64_t>(t.data_bytes) > *data_bytes || static_cast<int64_t>(t.scale_bytes) > *scale_bytes) {
+        g_err = "buffer too small";
+        return -1;
+      }
+      std::memcpy(data, t.data, t.data_bytes);
+      if (t.scale_bytes) std::memcpy(scales, t.scales, t.scale_bytes);
+      *data_bytes = static_cast<int64_t>(t.data_bytes);
+      *scale_bytes = static_cast<int64_t>(t.scale_bytes);
+      return static_cast<int>(t.dtype);
+    }
+    g_err = std::string("no weight ") + name;
+    return -1;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
 // describe_partitions of the session's graph (for partition-count parity tests)
 int eref_session_describe(void* h, char* buf, int cap) {
   RefRun* r = static_cast<RefRun*>(h);

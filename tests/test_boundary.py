@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from edgelm_amd import elm_format as F
+from edgelm_amd import synth as S
 from edgelm_amd import host
 
 needs_ref_hip = pytest.mark.skipif(not O.ref_hip_available(), reason="oracle/_ref not built (no /root/reference here)")
@@ -20,24 +20,16 @@ needs_ref_hip = pytest.mark.skipif(not O.ref_hip_available(), reason="oracle/_re
 @pytest.fixture(scope="module")
 def tiny(tmp_path_factory):
     d = tmp_path_factory.mktemp("tiny_boundary")
-    W = F.random_weights(F.TINY, 4321, sd=0.15, embed_sd=0.5)
+    TINY_SEED = 4321
     paths = {}
     for dt in ("q8", "q4"):
         p = str(d / f"tiny.{dt}.elm")
-        F.write_elm(p, F.TINY, W, dt)
+        S.write_model(p, S.TINY, dt, seed=TINY_SEED, sd=0.15, embed_sd=0.5)
         paths[dt] = p
     return paths
 
 
-def counts(desc):
-    """{backend: (ops, partitions)} from the first line of describe_partitions."""
-    head = desc.splitlines()[0].split(":", 1)[1]
-    out = {}
-    for part in head.split(";"):
-        w = part.split()
-        if len(w) >= 5:
-            out[w[0]] = (int(w[1]), int(w[4]))
-    return out
+counts = O.partition_counts  # edgelm's describe_partitions format
 
 
 @needs_ref_hip
@@ -81,7 +73,7 @@ def test_edgelm_and_this_runtime_partition_alike(tiny, backends):
             n_ref, d_ref = O.ref_hip_partition(tiny[dt], backends, fuse)
             m = host.Model(tiny[dt])
             n_mine, d_mine = m.partition(backends, fuse)
-            assert n_ref == n_mine and counts(d_ref) == counts(d_mine), (d_ref, d_mine)
+            assert n_ref == n_mine and counts(d_ref) == host.partition_counts(d_mine), (d_ref, d_mine)
 
 
 @needs_ref_hip

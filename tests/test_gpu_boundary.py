@@ -13,7 +13,7 @@ import pytest
 
 import oracle as O
 from conftest import bits_equal
-from edgelm_amd import elm_format as F
+from edgelm_amd import synth as S
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not O.ref_hip_available(), reason="needs oracle/_ref (edgelm's own build)")]
@@ -22,11 +22,11 @@ pytestmark = [pytest.mark.gpu,
 @pytest.fixture(scope="module")
 def tiny(tmp_path_factory):
     d = tmp_path_factory.mktemp("tiny_gpu_boundary")
-    W = F.random_weights(F.TINY, 4321, sd=0.15, embed_sd=0.5)
+    TINY_SEED = 4321
     paths = {}
     for dt in ("q8", "q4"):
         p = str(d / f"tiny.{dt}.elm")
-        F.write_elm(p, F.TINY, W, dt)
+        S.write_model(p, S.TINY, dt, seed=TINY_SEED, sd=0.15, embed_sd=0.5)
         paths[dt] = p
     return paths
 
@@ -66,8 +66,8 @@ def test_edgelm_session_smollm2_shape(tmp_path):
     SmolLM2-135M-shaped random model (q4 + q8 embedding, int8 activations), delegate un-hooked."""
     p = str(tmp_path / "smollm2.q4.elm")
     print("[gpu] writing SmolLM2-135M-shaped random q4 model", flush=True)
-    F.write_elm(p, F.SMOLLM2_135M, F.random_weights(F.SMOLLM2_135M, 20260101), "q4", embed_dtype="q8")
-    prompt = F.lcg_prompt(128, 49152)
+    S.write_model(p, S.SMOLLM2_135M, "q4", embed_dtype="q8", seed=20260101)
+    prompt = S.lcg_prompt(128, 49152)
     for backends in ("hip,cpu", "hip-matmul,cpu"):
         mine = O.RefSession(p, backends, threads=8, max_ctx=160, max_batch=128, act_quant=True, with_hip=True)
         ref = O.RefSession(p, "cpu", threads=16, max_ctx=160, max_batch=128, act_quant=True)

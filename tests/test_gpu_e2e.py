@@ -11,7 +11,7 @@ import pytest
 
 import oracle as O
 from conftest import bits_equal, rel_err
-from edgelm_amd import elm_format as F
+from edgelm_amd import synth as S
 from edgelm_amd import host
 
 pytestmark = [pytest.mark.gpu,
@@ -21,11 +21,11 @@ pytestmark = [pytest.mark.gpu,
 @pytest.fixture(scope="module")
 def tiny(tmp_path_factory):
     d = tmp_path_factory.mktemp("tiny")
-    W = F.random_weights(F.TINY, 1234, sd=0.15, embed_sd=0.5)
+    TINY_SEED = 1234
     paths = {}
     for dt in ("q8", "q4"):
         p = str(d / f"tiny.{dt}.elm")
-        F.write_elm(p, F.TINY, W, dt)
+        S.write_model(p, S.TINY, dt, seed=TINY_SEED, sd=0.15, embed_sd=0.5)
         paths[dt] = p
     return paths
 
@@ -84,13 +84,13 @@ def smollm(tmp_path_factory):
     d = tmp_path_factory.mktemp("smollm")
     p = str(d / "smollm2-135m-random.q4.elm")
     print("[gpu] writing SmolLM2-135M-shaped random q4 model (q8 embedding)", flush=True)
-    F.write_elm(p, F.SMOLLM2_135M, F.random_weights(F.SMOLLM2_135M, 20260101), "q4", embed_dtype="q8")
+    S.write_model(p, S.SMOLLM2_135M, "q4", embed_dtype="q8", seed=20260101)
     return p
 
 
 def test_smollm2_greedy_bit_identical_to_edgelm(smollm):
     """configs[3] protocol: 128-token LCG prompt, then greedy decode (16 steps here), act int8."""
-    prompt = F.lcg_prompt(128, 49152)
+    prompt = S.lcg_prompt(128, 49152)
     m = host.Model(smollm)
     mine = host.Session(m, "hip,cpu", threads=8, max_ctx=160, max_batch=128, act_quant=True)
     ref = O.RefSession(smollm, "cpu", threads=16, max_ctx=160, max_batch=128, act_quant=True)
@@ -129,7 +129,7 @@ def test_generate_device_argmax_matches_edgelm(tiny, smollm, backends):
     the host): the same tokens as edgelm's session and argmax, with a chunked prefill (7-token
     chunks) on the tiny model and the configs[3] protocol on the SmolLM2-shaped model."""
     cases = [(tiny["q4"], np.random.default_rng(9).integers(0, 320, 20).astype(np.int32), 8, 7, 64),
-             (smollm, F.lcg_prompt(128, 49152), 12, 128, 160)]
+             (smollm, S.lcg_prompt(128, 49152), 12, 128, 160)]
     for path, prompt, gen, batch, mc in cases:
         print(f"[gpu] generate {backends} {path.split('/')[-1]} batch={batch}", flush=True)
         m = host.Model(path)

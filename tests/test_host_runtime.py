@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from edgelm_amd import elm_format as F
+from edgelm_amd import synth as S
 from edgelm_amd import host
 
 needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (no /root/reference here)")
@@ -16,11 +16,11 @@ needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not bu
 @pytest.fixture(scope="module")
 def tiny(tmp_path_factory):
     d = tmp_path_factory.mktemp("tiny")
-    W = F.random_weights(F.TINY, 1234, sd=0.15, embed_sd=0.5)
+    TINY_SEED = 1234
     paths = {}
     for dt in ("f32", "q8", "q4"):
         p = str(d / f"tiny.{dt}.elm")
-        F.write_elm(p, F.TINY, W, dt)
+        S.write_model(p, S.TINY, dt, seed=TINY_SEED, sd=0.15, embed_sd=0.5)
         paths[dt] = p
     return paths
 
@@ -64,16 +64,44 @@ def test_partitioner_hip_claims(tiny):
         m = host.Model(tiny[dt])
         # hip-matmul: exactly the quantized matmuls (per layer 4, plus the LM head)
         n, desc = m.partition("hip-matmul,cpu")
-        assert "hip-matmul 9 ops" in desc and "cpu 7 ops" in desc and "reference 2 ops" in desc
+        c = host.partition_counts(desc)
+        assert c["hip-matmul"][0] == 9 and c["cpu"][0] == 7 and c["reference"][0] == 2, desc
         n2, desc2 = m.partition("hip-matmul")  # no cpu: the reference backend takes the rest
-        assert "hip-matmul 9 ops" in desc2 and "reference 9 ops" in desc2
+        c2 = host.partition_counts(desc2)
+        assert c2["hip-matmul"][0] == 9 and c2["reference"][0] == 9, desc2
         # hip: the whole quantized model (EMBED, RMSNORM, ATTENTION, LAST_ROWS too) in one partition
         n3, desc3 = m.partition("hip,cpu")
-        assert n3 == 1 and "hip 18 ops in 1" in desc3
+        assert n3 == 1 and host.partition_counts(desc3) == {"hip": (18, 1)}, desc3
     # f32 weights: not claimed, and no host backend of this build runs a matmul -> loud failure
     m = host.Model(tiny["f32"])
-    with pytest.raises(RuntimeError, match="no backend supports"):
+    with pytest.raises(RuntimeError, match="no backend claims"):
         m.partition("hip,cpu")
+
+
+@needs_ref
+@pytest.mark.parametrize("dtype", ["q8", "q4"])
+def test_convert_weights_equals_edgelm(tiny, dtype):
+    """Model::convert_weights (load-time quantization of an f32 file, edgelm model.cpp:220-251, main.cpp:53-60)
+    byte for byte against edgelm's own on the same file: every weight matrix converted, norm vectors kept f32;
+    the converted model then partitions onto the delegate like a quantized file."""
+    m = host.Model(tiny["f32"])
+    m.convert(dtype, threads=3)
+    code = {"q8": 1, "q4": 2}[dtype]
+    names = ["model.embed_tokens.weight", "model.layers.0.self_attn.q_proj.weight", "model.layers.1.mlp.down_proj.weight",
+             "model.layers.1.mlp.gate_proj.weight", "model.norm.weight", "model.layers.0.input_layernorm.weight"]
+    for name in names:
+        dt, data, scales = m.weight(name)
+        rdt, rdata, rscales = O.ref_convert_weight(tiny["f32"], code, name)
+        assert dt == rdt, name
+        assert np.array_equal(data.view(np.uint8).ravel(), rdata), name
+        if scales is None:
+            assert dt == 0 and rscales.size == 0, name
+        else:
+            assert np.array_equal(scales.view(np.uint8).ravel(), rscales), name
+    n, desc = m.partition("hip,cpu")
+    assert n == 1 and host.partition_counts(desc) == {"hip": (18, 1)}, desc
+    with pytest.raises(RuntimeError):
+        m.convert("f32")  # a quantized model cannot go back
 
 
 def test_session_without_gpu_fails_loudly(tiny):
@@ -87,7 +115,7 @@ def test_session_without_gpu_fails_loudly(tiny):
 
 def test_lcg_prompt_matches_edgelm_bench():
     # main.cpp:178-184 with vocab 49152 (lo = 1000): first ids recomputed with Python integers
-    p = F.lcg_prompt(4, 49152)
+    p = S.lcg_prompt(4, 49152)
     x, want = 12345, []
     for _ in range(4):
         x = (x * 6364136223846793005 + 1442695040888963407) % 2 ** 64
