@@ -1,17 +1,16 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X quantized-matmul delegate (one GPU).
 
-Headline workload: one SmolLM2-135M-shaped decode step of the hot
-path, W4A8 — per token 30 x [MATMUL_N q/k/v 576+192+192 x 576, MATMUL_ADD o 576 x 576 + residual,
-FFN_SWIGLU 2 x 1536 x 576, MATMUL_ADD down 576 x 1536 + residual] + the q8 LM head 49152 x 576,
-q4 group-32 weights quantized from N(0, 0.02) with edgelm's quantizer, int8 activations
-quantized per 32-block in-kernel, every input resident in HBM, one HIP graph per step.
-A "step" is one token; value = decode tok/s of that step.
+Headline workload: a random-init SmolLM2-135M-shaped model (30 layers, q4 group-32
+weights with a q8 embedding, int8 activations) through this build's Session with the `hip` delegate running
+the whole model on the GPU; edgelm's bench protocol: a 128-token LCG prompt, then greedy decode. A "step" is
+one decode token; value = decode tok/s over exactly --steps timed steps after --warmup untimed ones.
 
-Also reported (extra keys): per-kernel event timings and HBM roofline, the 8B-shaped W4A8 decode
-sweep (configs[4]: 8 Llama-3-8B layers round-robin, > 256 MB Infinity Cache), the int8 GEMM at
-T=128 / 512, and the CPU baseline: edgelm's own cpu backend (compiled from the reference sources
-into oracle/_ref) on this host's cores over a bounded sample of the same decode step.
+Also reported (extra keys): TTFT and cold TTFT, the matmul-only flavour, per-kernel event timings and the HBM
+roofline of the step's dominant kernel, the decode matmul chain alone, the 8B-shaped W4A8 decode
+sweep (configs[4]: 8 Llama-3-8B layers round-robin, > 256 MB Infinity Cache), the int8 GEMMs at T=128 / 512
+(configs[2], configs[4]), and the CPU baseline: edgelm's own Session (compiled from the reference sources into
+oracle/_ref) on this host's cores, same model file and protocol.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -317,130 +316,118 @@ def gemm_bench(ctx, E, T, shapes, dt=1, act=None, reps=10, eager=False):
     return out
 
 
-def e2e_bench(path_dir, P=128, G=64, reps=3, cpu_reference=True):
-    """random-init SmolLM2-135M (q4 g32 + q8 embedding, int8 activations) through this
-    build's Session, backends "hip,cpu" (whole model on the GPU) and "hip-matmul,cpu" (matmuls on the
-    GPU); edgelm's bench protocol (main.cpp:173-233): LCG prompt, warm-up rep, then the median of
-    `reps` reps of prefill + argmax (TTFT) + G greedy decodes."""
+E2E_SD, E2E_EMBED_SD = 0.05, 0.5  # weight scales of the e2e model: greedy tokens differ step to step
+
+
+def write_e2e_model(path):
+    from edgelm_amd import synth as S
+    t0 = time.time()
+    S.write_model(path, S.SMOLLM2_135M, "q4", embed_dtype="q8", seed=20260101, sd=E2E_SD, embed_sd=E2E_EMBED_SD)
+    log(f"e2e model written in {time.time() - t0:.1f}s ({os.path.getsize(path) / 1e6:.1f} MB)")
+
+
+def e2e_headline(path, steps, warmup, P=128):
+    """the random-init SmolLM2-135M-shaped model (q4 g32 + q8 embedding, int8 activations) through
+    this build's Session with backends "hip,cpu" (the whole model on the GPU, decode steps replayed as HIP
+    graphs, greedy argmax on the device): edgelm's bench protocol (main.cpp:173-233) with the LCG prompt of P
+    tokens; after a warm-up rep, one timed rep: TTFT of the prompt, `warmup` untimed decode steps, then exactly
+    `steps` timed greedy decode steps (each ends with its token id on the host)."""
     from edgelm_amd import synth as S
     from edgelm_amd import host
-    path = os.path.join(path_dir, "smollm2-135m-random.q4.elm")
-    t0 = time.time()
-    S.write_model(path, S.SMOLLM2_135M, "q4", embed_dtype="q8", seed=20260101)
-    log(f"e2e model written in {time.time() - t0:.1f}s ({os.path.getsize(path) / 1e6:.1f} MB)")
     prompt = S.lcg_prompt(P, 49152)
     threads = min(8, os.cpu_count() or 1)
+    t0 = time.perf_counter()
     m = host.Model(path)
-    med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731
-
-    def session_bench(backends):
-        s = host.Session(m, backends, threads=threads, max_ctx=P + G + 8, max_batch=P, act_quant=True)
-        runs = [s.generate(prompt, G) for _ in range(reps + 1)][1:]
-        s.close()
-        r = {"prefill_tok_s": med([P / (x["prefill_ms"] / 1e3) for x in runs]), "ttft_ms": med([x["ttft_ms"] for x in runs]),
-             "decode_tok_s": med([G / (x["decode_ms"] / 1e3) for x in runs]), "backends": backends}
-        log(f"e2e {backends}: prefill {r['prefill_tok_s']:.1f} tok/s, TTFT {r['ttft_ms']:.2f} ms, "
-            f"decode {r['decode_tok_s']:.1f} tok/s")
-        return r, runs
-
-    # the whole model on the GPU (activations and KV cache resident in HBM)
-    out, runs = session_bench("hip,cpu")
-    out.update({"prompt": P, "gen": G, "host_threads": threads,
-                "greedy_tokens_head": [int(t) for t in runs[0]["tokens"][:8]]})
-    # matmuls only on the GPU, the rest on the host cores (activations cross PCIe around every matmul)
-    out["matmul_only"], runs_mm = session_bench("hip-matmul,cpu")
-    out["matmul_only"]["greedy_tokens_match"] = bool(np.array_equal(runs_mm[0]["tokens"], runs[0]["tokens"]))
-    if cpu_reference:
-        import oracle as O
-        if O.ref_available():
-            ct = min(16, os.cpu_count() or 1)
-            r = O.RefSession(path, "cpu", threads=ct, max_ctx=P + G + 8, max_batch=P, act_quant=True)
-            def gen_ref():
-                r.reset()
-                t0 = time.perf_counter()
-                lg = r.forward(prompt)
-                t1 = time.perf_counter()
-                tok = int(np.argmax(lg[-1]))
-                t2 = time.perf_counter()
-                toks = [tok]
-                for _ in range(G):
-                    tok = int(np.argmax(r.forward(np.array([tok], np.int32))[-1]))
-                    toks.append(tok)
-                t3 = time.perf_counter()
-                return (t1 - t0) * 1e3, (t2 - t0) * 1e3, (t3 - t2) * 1e3, toks
-            gen_ref()
-            pm, tm, dm, toks = gen_ref()
-            out["cpu_reference"] = {"prefill_tok_s": P / (pm / 1e3), "ttft_ms": tm, "decode_tok_s": G / (dm / 1e3),
-                                    "threads": ct, "kind": "reference",
-                                    "greedy_tokens_match": toks == [int(t) for t in runs[0]["tokens"]]}
-            r.close()
-            log(f"e2e cpu (edgelm cpu backend, {ct} threads): prefill {out['cpu_reference']['prefill_tok_s']:.1f} tok/s, "
-                f"decode {out['cpu_reference']['decode_tok_s']:.1f} tok/s, tokens match: "
-                f"{out['cpu_reference']['greedy_tokens_match']}")
-    os.remove(path)
-    return out
+    m.prefault()
+    s = host.Session(m, "hip,cpu", threads=threads, max_ctx=P + warmup + steps + 8, max_batch=P, act_quant=True)
+    cold = s.bench(prompt, 0, 1)  # first use: weight upload and repack, buffers, graph capture on later steps
+    cold_ms = (time.perf_counter() - t0) * 1e3 - cold["decode_ms"]
+    s.bench(prompt, 2, 4)  # warm-up rep
+    r = s.bench(prompt, warmup, steps)
+    s.close()
+    out = {"decode_tok_s": steps / (r["decode_ms"] / 1e3), "ms_per_step": r["decode_ms"] / steps,
+           "ttft_ms": r["ttft_ms"], "prefill_tok_s": P / (r["ttft_ms"] / 1e3), "prompt": P, "steps": steps,
+           "warmup": warmup, "backends": "hip,cpu", "host_threads": threads,
+           "cold_ttft_ms": cold_ms, "cold_ttft_note": "model load + prefault + session creation + first prompt "
+                                                      "(weight upload and repack included) to the first token",
+           "greedy_tokens": [int(t) for t in r["tokens"]]}
+    log(f"e2e hip,cpu: decode {out['decode_tok_s']:.1f} tok/s ({out['ms_per_step'] * 1e3:.0f} us/token), "
+        f"TTFT {out['ttft_ms']:.2f} ms, prefill {out['prefill_tok_s']:.0f} tok/s, cold TTFT {cold_ms:.0f} ms")
+    # the matmul-only flavour (configs[3] as BASELINE words it: MATMUL* on the GPU, the rest on the host)
+    s = host.Session(m, "hip-matmul,cpu", threads=threads, max_ctx=P + warmup + steps + 8, max_batch=P, act_quant=True)
+    s.bench(prompt, 2, 4)
+    rm = s.bench(prompt, warmup, steps)
+    s.close()
+    out["matmul_only"] = {"decode_tok_s": steps / (rm["decode_ms"] / 1e3), "ttft_ms": rm["ttft_ms"],
+                          "backends": "hip-matmul,cpu",
+                          "greedy_tokens_match": bool(np.array_equal(rm["tokens"], r["tokens"]))}
+    log(f"e2e hip-matmul,cpu: decode {out['matmul_only']['decode_tok_s']:.1f} tok/s, TTFT {rm['ttft_ms']:.2f} ms, "
+        f"tokens match: {out['matmul_only']['greedy_tokens_match']}")
+    m.close()
+    return out, r["tokens"]
 
 
-def cpu_baseline(budget_s=12.0):
-    """edgelm's own cpu backend (oracle/_ref) on this host: the same W4A8 decode-step matmuls."""
+def host_cpu():
+    """CPU model, logical CPUs the process may use, and physical cores of the host."""
+    model, cores = "unknown", set()
+    try:
+        phys = core = None
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+            elif not k and phys is not None:
+                cores.add((phys, core))
+                phys = core = None
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"model": model, "usable_logical_cpus": usable, "physical_cores": len(cores) or None}
+
+
+def cpu_baseline(path, tokens_gpu, steps, warmup, P=128, budget_s=15.0):
+    """edgelm's own Session (compiled from the reference sources into oracle/_ref; cpu backend, its x86 scalar
+    path since this host has no NEON, act int8) on the same model file and protocol as the headline, timed
+    inside C (eref_session_bench). Bounded: repeated timed reps for about budget_s seconds at 16 threads
+    (this box's CPU share), then one rep each at 1 and 4 threads (4 is edgelm's CLI default)."""
     import oracle as O
-    from edgelm_amd import host
-    threads = min(16, os.cpu_count() or 1)
-    if O.ref_available():
-        kind = "reference"
-    else:
-        kind = "port"
-    r = np.random.default_rng(1234)
-    layers = 4  # bounded sample: 4 of the 30 layers per timed pass, scaled to a full token
-    ws = {}
-    for name, (n, k) in [("q", (D, D)), ("k", (KV, D)), ("v", (KV, D)), ("o", (D, D)), ("g", (HID, D)),
-                         ("u", (HID, D)), ("d", (D, HID))]:
-        for l in range(layers):
-            f = r.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
-            q, s = host.quantize_q4(f)
-            ws[f"{l}.{name}"] = O.Weight(2, n, k, q, s)
-    f = r.standard_normal((VOCAB, D), dtype=np.float32) * np.float32(0.02)
-    q, s = host.quantize_q8(f)
-    head = O.Weight(1, VOCAB, D, q, s)
-    x = r.standard_normal((1, D)).astype(np.float32)
-    res = r.standard_normal((1, D)).astype(np.float32)
-    hx = r.standard_normal((1, HID)).astype(np.float32)
-
-    if kind == "reference":
-        pool = O.RefPool(threads, 1, HID)
-        mm = lambda xx, wl, rl: O.rq_cpu_matmul(pool, xx, wl, rl, True)  # noqa: E731
-        sw = lambda xx, g, u: O.rq_cpu_swiglu(pool, xx, g, u, True)  # noqa: E731
-    else:
-        threads = 1
-        mm = lambda xx, wl, rl: O.cpu_matmul(xx, wl, rl, True)  # noqa: E731
-        sw = lambda xx, g, u: O.cpu_swiglu(xx, g, u, True)  # noqa: E731
-
-    def layer_pass():
-        for l in range(layers):
-            mm(x, [ws[f"{l}.q"], ws[f"{l}.k"], ws[f"{l}.v"]], None)
-            mm(x, [ws[f"{l}.o"]], [res])
-            sw(x, ws[f"{l}.g"], ws[f"{l}.u"])
-            mm(hx, [ws[f"{l}.d"]], [res])
-
-    layer_pass()
-    mm(x, [head], None)
-    t_layers, n_layers, t_head, n_head = 0.0, 0, 0.0, 0
-    t_end = time.time() + budget_s
-    while time.time() < t_end:
-        t0 = time.perf_counter()
-        layer_pass()
-        t_layers += time.perf_counter() - t0
-        n_layers += layers
-        t0 = time.perf_counter()
-        mm(x, [head], None)
-        t_head += time.perf_counter() - t0
-        n_head += 1
-    per_token = t_layers / n_layers * L + t_head / n_head
-    if kind == "reference":
-        pool.close()
-    return {"value": 1.0 / per_token, "unit": "tok/s", "cores": threads, "kind": kind,
-            "sample": f"{n_layers} layer-passes + {n_head} LM heads of the same W4A8 decode-step matmuls "
-                      f"(edgelm cpu backend, scalar x86 path, act int8), scaled to 30 layers + head"}
+    from edgelm_amd import synth as S
+    if not O.ref_available():
+        log("cpu baseline skipped: oracle/_ref not built")
+        return None, None
+    prompt = S.lcg_prompt(P, 49152)
+    ct = min(16, os.cpu_count() or 1)
+    r = O.RefSession(path, "cpu", threads=ct, max_ctx=P + warmup + steps + 8, max_batch=P, act_quant=True)
+    r.bench(prompt, 2, 4)
+    reps, t_end = [], time.time() + budget_s
+    while time.time() < t_end or not reps:
+        reps.append(r.bench(prompt, warmup, steps))
+    r.close()
+    dec = sorted(steps / (x["decode_ms"] / 1e3) for x in reps)
+    med = dec[len(dec) // 2]
+    match = bool(np.array_equal(reps[0]["tokens"], tokens_gpu))
+    log(f"cpu baseline (edgelm session, {ct} threads): decode {med:.1f} tok/s over {len(reps)} reps, "
+        f"TTFT {reps[0]['ttft_ms']:.0f} ms, greedy tokens match the GPU's: {match}")
+    by_threads = {}
+    for th in (1, 4):
+        r = O.RefSession(path, "cpu", threads=th, max_ctx=P + warmup + steps + 8, max_batch=P, act_quant=True)
+        x = r.bench(prompt, 2, min(steps, 32))
+        by_threads[str(th)] = {"decode_tok_s": min(steps, 32) / (x["decode_ms"] / 1e3), "ttft_ms": x["ttft_ms"]}
+        r.close()
+    cpu = host_cpu()
+    base = {"value": med, "unit": "tok/s", "cores": ct, "kind": "reference",
+            "sample": f"{len(reps)} timed reps of the headline protocol ({P}-token prompt, {warmup} untimed + {steps} "
+                      f"timed greedy decode steps) on edgelm's own Session, cpu backend, act int8, {ct} threads, "
+                      f"~{budget_s:.0f} s",
+            "cpu_model": cpu["model"], "usable_logical_cpus": cpu["usable_logical_cpus"],
+            "physical_cores": cpu["physical_cores"], "path": "x86 scalar (EDGELM_NEON=0)"}
+    extra = {"ttft_ms": reps[0]["ttft_ms"], "greedy_tokens_match_gpu": match, "by_threads": by_threads}
+    return base, extra
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
@@ -502,12 +489,12 @@ def measured_traffic(kernel):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=128, help="timed greedy decode steps (tokens)")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed greedy decode steps before them")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-8b", action="store_true", help="skip the 8B-shaped sweep")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMMs")
-    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end SmolLM2 session")
+    ap.add_argument("--no-chain", action="store_true", help="skip the decode matmul chain and its per-op timers")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the roofline kernels and a calibration copy (for rocprofv3 counter passes)")
     ap.add_argument("--eager", action="store_true",
@@ -521,64 +508,89 @@ def main():
         print(f"bench.py measures one GPU only (this delegate has no multi-GPU path); got --gpus {args.gpus}, "
               f"WORLD_SIZE {world}", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        sys.exit(2)
 
     from edgelm_amd import elmh as E
-    ctx = E.Context(0)
-    log(f"device {ctx.arch}")
     if args.pmc_workload:
+        ctx = E.Context(0)
         pmc_workload(ctx, E)
         ctx.close()
         return
-    ms_step, per = decode_step_bench(ctx, E, args.steps, args.warmup, args.eager)
+
+    import tempfile
     extra = {}
-    if not args.no_8b:
-        extra["gemv_8b_w4a8"] = sweep_8b(ctx, E, eager=args.eager)
-    if not args.no_gemm:
-        sm = [(D + 2 * KV, D), (HID, D), (D, HID), (VOCAB, D)]
-        b8 = [(4096, 4096), (14336, 4096), (4096, 14336)]
-        # W8A8, int8 per-channel weights, per-token int8 activations (ELMH_ACT_INT8_TOKEN)
-        extra["gemm_w8a8_token_T128"] = gemm_bench(ctx, E, 128, sm, act=E.ACT_INT8_TOKEN, eager=args.eager)
-        extra["gemm_w8a8_token_T512_8b"] = gemm_bench(ctx, E, 512, b8, act=E.ACT_INT8_TOKEN, eager=args.eager)
-        # edgelm's parity mode: per-32-block activation scales, block-order f32 rescale (VALU-bound)
-        extra["gemm_w8a8_T128"] = gemm_bench(ctx, E, 128, sm, eager=args.eager)
-        extra["gemm_w8a8_T512_8b"] = gemm_bench(ctx, E, 512, b8, eager=args.eager)
-        # W4A8 prefill (the e2e model's layers), parity mode
-        extra["gemm_w4a8_T512_8b"] = gemm_bench(ctx, E, 512, b8, dt=2, eager=args.eager)
-    if not args.no_e2e:
-        import tempfile
-        ctx.close()  # the session opens its own context
-        with tempfile.TemporaryDirectory() as d:
-            extra["e2e_smollm2_w4a8"] = e2e_bench(d, cpu_reference=not args.no_cpu)
+    with tempfile.TemporaryDirectory() as tmp:
+        model_path = os.path.join(tmp, "smollm2-135m-random.q4.elm")
+        write_e2e_model(model_path)
+        head, tokens = e2e_headline(model_path, args.steps, args.warmup)
+
         ctx = E.Context(0)
-    # dominant kernel of the headline step: largest total time per step (one kernel per call)
-    dom_name, dom = max(((k, v) for k, v in per.items() if v["kernels_per_call"] == 1),
-                        key=lambda kv: kv[1]["us"] * kv[1]["calls_per_step"])
-    roof = {"kernel": dom_name, "bound": "hbm", "achieved": round(dom["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(dom["GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_name),
-            "algorithmic_bytes_per_launch": dom["bytes"], "avg_launch_us": round(dom["us"], 3),
-            "note": "SmolLM2-sized weights are L2/Infinity-Cache resident: latency-bound, see gemv_8b_w4a8 for HBM"}
-    if "gemv_8b_w4a8" in extra:
-        g8 = extra["gemv_8b_w4a8"]
-        extra["roofline_8b_down_gemv"] = {
-            "kernel": "gemv_stream_kernel (8B down 4096x14336, W4A8, T=1)", "bound": "hbm",
-            "achieved": round(g8["down_gemv_GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(g8["down_gemv_GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic("8B down GEMV"),
-            "algorithmic_bytes_per_launch": g8["down_gemv_bytes"], "avg_launch_us": round(g8["down_gemv_us"], 3)}
-    cpu = None
-    if not args.no_cpu:
-        log("CPU baseline (edgelm cpu backend on host cores)")
-        cpu = cpu_baseline()
-        log(f"CPU baseline {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
-    ctx.close()
+        log(f"device {ctx.arch}")
+        per = None
+        if not args.no_chain:
+            ms_chain, per = decode_step_bench(ctx, E, 200, 20, args.eager)
+            extra["decode_matmul_chain"] = {"us_per_token": ms_chain * 1e3, "tok_s": 1e3 / ms_chain,
+                                            "what": "the 121 matmul-family calls of a decode step alone (configs[1] "
+                                                    "shapes, W4A8, device-resident, one HIP graph per step)",
+                                            "per_op": per}
+        if not args.no_8b:
+            extra["gemv_8b_w4a8"] = sweep_8b(ctx, E, eager=args.eager)
+        if not args.no_gemm:
+            sm = [(D + 2 * KV, D), (HID, D), (D, HID), (VOCAB, D)]
+            b8 = [(4096, 4096), (14336, 4096), (4096, 14336)]
+            # W8A8, int8 per-channel weights, per-token int8 activations (ELMH_ACT_INT8_TOKEN)
+            extra["gemm_w8a8_token_T128"] = gemm_bench(ctx, E, 128, sm, act=E.ACT_INT8_TOKEN, eager=args.eager)
+            extra["gemm_w8a8_token_T512_8b"] = gemm_bench(ctx, E, 512, b8, act=E.ACT_INT8_TOKEN, eager=args.eager)
+            # edgelm's parity mode: per-32-block activation scales, block-order f32 rescale (VALU-bound)
+            extra["gemm_w8a8_T128"] = gemm_bench(ctx, E, 128, sm, eager=args.eager)
+            extra["gemm_w8a8_T512_8b"] = gemm_bench(ctx, E, 512, b8, eager=args.eager)
+            # W4A8 prefill (the e2e model's layers), parity mode
+            extra["gemm_w4a8_T512_8b"] = gemm_bench(ctx, E, 512, b8, dt=2, eager=args.eager)
+        ctx.close()
+
+        roof = None
+        if per:
+            # dominant kernel of the headline decode step: gemv_small_kernel<q4, 1 token, no SwiGLU, no norm> runs the
+            # o projection and the down projection of every layer (the largest share of the step's GPU time in
+            # the kernel trace); its per-launch time comes from HIP events around graph replays on the library's
+            # stream, and its algorithmic bytes are the down projection's (the larger of its two calls)
+            dom_name = "MATMUL_ADD down"
+            dom = per[dom_name]
+            roof = {"kernel": "gemv_small_kernel<2, 1, false, false> (" + dom_name + " 576x1536 q4 + residual, T=1)",
+                    "bound": "hbm", "achieved": round(dom["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(dom["GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_name),
+                    "algorithmic_bytes_per_launch": dom["bytes"], "avg_launch_us": round(dom["us"], 3),
+                    "note": "SmolLM2-sized weights stay in L2 / Infinity Cache and each call is a few microseconds: "
+                            "latency-bound; roofline_8b_down_gemv is the HBM-bound kernel (configs[4])"}
+        if "gemv_8b_w4a8" in extra:
+            g8 = extra["gemv_8b_w4a8"]
+            extra["roofline_8b_down_gemv"] = {
+                "kernel": "gemv_stream_kernel (8B down 4096x14336, W4A8, T=1)", "bound": "hbm",
+                "achieved": round(g8["down_gemv_GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(g8["down_gemv_GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic("8B down GEMV"),
+                "algorithmic_bytes_per_launch": g8["down_gemv_bytes"], "avg_launch_us": round(g8["down_gemv_us"], 3)}
+        cpu = None
+        if not args.no_cpu:
+            cpu, cpu_extra = cpu_baseline(model_path, tokens, args.steps, args.warmup)
+            if cpu_extra:
+                head["cpu_reference"] = cpu_extra
+                head["greedy_tokens_match_edgelm"] = cpu_extra["greedy_tokens_match_gpu"]
+
     line = {
-        "metric": METRIC, "value": round(1e3 / ms_step, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8 (W4A8: q4 g32 weights x per-32-block int8 activations, int32 acc, f32 rescale)",
-        "data": "synthetic (random-init N(0,0.02) weights quantized with edgelm's quantizers; N(0,1) activations)",
-        "config": {"workload": "configs[1]: SmolLM2-135M-shaped W4A8 decode step (30 layers + q8 LM head), T=1, "
-                               "device-resident, one HIP graph per token", "parallelism": "single GPU",
-                   "timing": "eager launches (kernel-trace mode; step rate host-bound)" if args.eager else "HIP graph"},
-        "roofline": roof, "cpu_baseline": cpu, "per_kernel": per, **extra,
+        "metric": METRIC, "value": round(head["decode_tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(head["ms_per_step"], 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 (W4A8: q4 g32 weights x per-32-block int8 activations, int32 acc, f32 rescale)",
+        "data": f"synthetic (random-init SmolLM2-135M-shaped model, weights N(0,{E2E_SD}), embedding "
+                f"N(0,{E2E_EMBED_SD}), quantized with edgelm's quantizers; LCG prompt of edgelm's bench)",
+        "config": {"workload": "configs[3]: end-to-end SmolLM2-135M-shaped decode (30 layers, q4 g32 + q8 embedding, "
+                               "int8 activations), backends hip,cpu, 128-token prompt then greedy decode; a step is one "
+                               "token", "parallelism": "single GPU",
+                   "timing": "eager launches (kernel-trace mode; step rate host-bound)" if args.eager else
+                             "host clock around exactly `steps` greedy steps, each ending with its token on the host"},
+        "roofline": roof, "cpu_baseline": cpu, "e2e_smollm2_w4a8": head, **extra,
     }
     print(json.dumps(line))
 

@@ -195,6 +195,20 @@ class Session:
         n = _setup().elm_session_describe(self.h, buf, 4096)
         return n, buf.value.decode()
 
+    def bench(self, prompt, warmup, steps):
+        """bench.py's protocol (elm_session_bench): TTFT of the prompt, `warmup` untimed greedy decode steps,
+        then `steps` timed ones."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        L = _setup()
+        L.elm_session_bench.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double),
+                                        C.POINTER(C.c_double), C.c_void_p]
+        tt, dm = C.c_double(), C.c_double()
+        toks = np.empty(1 + warmup + steps, np.int32)
+        if L.elm_session_bench(self.h, prompt.ctypes.data, len(prompt), warmup, steps, C.byref(tt), C.byref(dm),
+                               toks.ctypes.data):
+            raise RuntimeError(_err())
+        return dict(ttft_ms=tt.value, decode_ms=dm.value, tokens=toks)
+
     def generate(self, prompt, gen):
         """edgelm's bench protocol: prefill, argmax (TTFT), `gen` greedy decode steps."""
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)

@@ -216,6 +216,33 @@ int elm_session_describe(const elm_session* s, char* buf, int cap) {
   return static_cast<int>(s->s->graph().ops.size());
 }
 
+int elm_session_bench(elm_session* s, const int32_t* prompt, int n_prompt, int warmup, int steps, double* ttft_ms,
+                      double* decode_ms, int32_t* tokens_out) {
+  return guard([&] {
+    if (!s || !prompt || n_prompt < 1 || warmup < 0 || steps < 1) throw std::runtime_error("edgelm: bad bench arguments");
+    Session& ss = *s->s;
+    ss.reset();
+    const auto t0 = std::chrono::steady_clock::now();
+    int32_t tok = ss.greedy_prefill(std::vector<int32_t>(prompt, prompt + n_prompt));
+    const auto t1 = std::chrono::steady_clock::now();
+    if (tokens_out) tokens_out[0] = tok;
+    for (int i = 0; i < warmup; ++i) {
+      tok = ss.greedy(&tok, 1);
+      if (tokens_out) tokens_out[1 + i] = tok;
+    }
+    // every greedy step ends with its token id on the host, so the clock brackets finished work
+    const auto t2 = std::chrono::steady_clock::now();
+    for (int i = 0; i < steps; ++i) {
+      tok = ss.greedy(&tok, 1);
+      if (tokens_out) tokens_out[1 + warmup + i] = tok;
+    }
+    const auto t3 = std::chrono::steady_clock::now();
+    *ttft_ms = ms_between(t0, t1);
+    *decode_ms = ms_between(t2, t3);
+    return 0;
+  });
+}
+
 int elm_session_generate(elm_session* s, const int32_t* prompt, int n_prompt, int gen, double* prefill_ms,
                          double* ttft_ms, double* decode_ms, int32_t* tokens_out) {
   return guard([&] {

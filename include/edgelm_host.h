@@ -77,6 +77,11 @@ int elm_session_describe(const elm_session* s, char* buf, int cap);
  * generated token ids (first one from the prefill). Each argmax is taken where the logits are
  * (Session::greedy: on the device when a hip backend writes them), so the first one is part of the
  * prefill's last step and prefill ms equals TTFT ms. */
+/* bench.py's protocol on one session: reset, prefill the prompt and take its greedy token (TTFT), run
+ * `warmup` untimed greedy decode steps, then time exactly `steps` more (decode_ms). Every step ends when
+ * its token id is on the host. tokens_out (optional) gets the 1 + warmup + steps greedy tokens. */
+int elm_session_bench(elm_session* s, const int32_t* prompt, int n_prompt, int warmup, int steps, double* ttft_ms,
+                      double* decode_ms, int32_t* tokens_out);
 int elm_session_generate(elm_session* s, const int32_t* prompt, int n_prompt, int gen, double* prefill_ms,
                          double* ttft_ms, double* decode_ms, int32_t* tokens_out);
 

@@ -461,6 +461,18 @@ class RefSession:
     def reset(self):
         self.lib.eref_session_reset(C.c_void_p(self.h))
 
+    def bench(self, prompt, warmup, steps):
+        """bench.py's protocol on edgelm's Session, timed in C (eref_session_bench)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        tt, dm = C.c_double(), C.c_double()
+        toks = np.empty(1 + warmup + steps, np.int32)
+        self.lib.eref_session_bench.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                                C.POINTER(C.c_double), C.POINTER(C.c_double), C.c_void_p]
+        if self.lib.eref_session_bench(C.c_void_p(self.h), _ptr(prompt), len(prompt), warmup, steps, C.byref(tt),
+                                       C.byref(dm), _ptr(toks)):
+            raise RuntimeError(self.lib.eref_last_error().decode())
+        return dict(ttft_ms=tt.value, decode_ms=dm.value, tokens=toks)
+
     def describe(self):
         buf = C.create_string_buffer(4096)
         nops = self.lib.eref_session_describe(C.c_void_p(self.h), buf, 4096)

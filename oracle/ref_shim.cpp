@@ -2,6 +2,7 @@
 // reference sources by oracle/Makefile into oracle/_ref/libedgelm_ref.so). Used to pin the C
 // oracle, to generate fixtures, and as bench.py's cpu_baseline ("kind": "reference"). The
 // product never links or loads it.
+#include <chrono>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -168,6 +169,42 @@ int eref_session_forward(void* h, const int32_t* tokens, int n, float* out) {
 }
 
 int32_t eref_argmax(const float* logits, int n) { return argmax(logits, n); }
+
+// The bench protocol of bench.py on edgelm's own Session, timed here in C: reset, prefill (edgelm's
+// Session::prefill in max_batch chunks) and argmax of the last logits row (TTFT), `warmup` untimed
+// greedy decode steps, then `steps` timed ones (edgelm's argmax, tokenizer.cpp:187-189).
+int eref_session_bench(void* h, const int32_t* prompt, int n_prompt, int warmup, int steps, double* ttft_ms,
+                       double* decode_ms, int32_t* tokens_out) {
+  try {
+    RefRun* r = static_cast<RefRun*>(h);
+    Session& s = *r->session;
+    const int V = r->model.cfg.vocab;
+    auto last_row = [&](const float* lg, int n) { return s.options().all_logits ? lg + static_cast<size_t>(n - 1) * V : lg; };
+    s.reset();
+    const auto t0 = std::chrono::steady_clock::now();
+    const float* lg = s.prefill(std::vector<int32_t>(prompt, prompt + n_prompt));
+    const int mb = s.options().max_batch, tail = n_prompt % mb ? n_prompt % mb : mb;
+    int32_t tok = argmax(last_row(lg, tail), V);
+    const auto t1 = std::chrono::steady_clock::now();
+    if (tokens_out) tokens_out[0] = tok;
+    for (int i = 0; i < warmup; ++i) {
+      tok = argmax(last_row(s.decode(tok), 1), V);
+      if (tokens_out) tokens_out[1 + i] = tok;
+    }
+    const auto t2 = std::chrono::steady_clock::now();
+    for (int i = 0; i < steps; ++i) {
+      tok = argmax(last_row(s.decode(tok), 1), V);
+      if (tokens_out) tokens_out[1 + warmup + i] = tok;
+    }
+    const auto t3 = std::chrono::steady_clock::now();
+    *ttft_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    *decode_ms = std::chrono::duration<double, std::milli>(t3 - t2).count();
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return 1;
+  }
+}
 
 // edgelm's Model::load then convert_weights(dtype) (model.cpp:220-251); copies weight `name` into data /
 // scales (capacities in, sizes out) and returns its dtype, or -1.

@@ -66,7 +66,7 @@ def test_edgelm_session_smollm2_shape(tmp_path):
     SmolLM2-135M-shaped random model (q4 + q8 embedding, int8 activations), delegate un-hooked."""
     p = str(tmp_path / "smollm2.q4.elm")
     print("[gpu] writing SmolLM2-135M-shaped random q4 model", flush=True)
-    S.write_model(p, S.SMOLLM2_135M, "q4", embed_dtype="q8", seed=20260101)
+    S.write_model(p, S.SMOLLM2_135M, "q4", embed_dtype="q8", seed=20260101, sd=0.05, embed_sd=0.5)
     prompt = S.lcg_prompt(128, 49152)
     for backends in ("hip,cpu", "hip-matmul,cpu"):
         mine = O.RefSession(p, backends, threads=8, max_ctx=160, max_batch=128, act_quant=True, with_hip=True)

@@ -84,7 +84,7 @@ def smollm(tmp_path_factory):
     d = tmp_path_factory.mktemp("smollm")
     p = str(d / "smollm2-135m-random.q4.elm")
     print("[gpu] writing SmolLM2-135M-shaped random q4 model (q8 embedding)", flush=True)
-    S.write_model(p, S.SMOLLM2_135M, "q4", embed_dtype="q8", seed=20260101)
+    S.write_model(p, S.SMOLLM2_135M, "q4", embed_dtype="q8", seed=20260101, sd=0.05, embed_sd=0.5)
     return p
 
 
