@@ -535,7 +535,7 @@ int check_attention(elmh_ctx* c, const float* q, const float* k, const float* v,
   if (n_heads < 1 || n_kv < 1 || n_heads % n_kv || head_dim < 4 || head_dim % 4 || head_dim > 256)
     return fail(c, ELMH_ERR_ARG, "attention: heads %d / kv heads %d / head_dim %d", n_heads, n_kv, head_dim);
   if (!rope_cos != !rope_sin) return fail(c, ELMH_ERR_ARG, "attention: rope_cos and rope_sin go together");
-  if (attention_lds_bytes(head_dim, pos0 + T) > 65536)
+  if (attention_lds_bytes(head_dim, pos0 + T) > kMaxAttnLds)
     return fail(c, ELMH_ERR_UNSUPPORTED, "attention: %d positions exceed the kernel's LDS", pos0 + T);
   return ELMH_OK;
 }
@@ -1002,6 +1002,11 @@ int elmh_attention_dev(elmh_ctx* c, const float* q, const float* k, const float*
   return ELMH_OK;
 }
 
+int elmh_attention_step_supported(int head_dim, int max_ctx) {
+  return head_dim >= 4 && head_dim % 4 == 0 && head_dim <= 256 && max_ctx >= 1 &&
+         attention_lds_bytes(head_dim, max_ctx) <= kMaxAttnLds;
+}
+
 int elmh_attention_step_dev(elmh_ctx* c, const float* q, const float* k, const float* v, float* out,
                             const int32_t* pos_dev, int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache,
                             int max_ctx, const float* rope_cos, const float* rope_sin) {
@@ -1011,7 +1016,7 @@ int elmh_attention_step_dev(elmh_ctx* c, const float* q, const float* k, const f
     return fail(c, ELMH_ERR_ARG, "attention_step: heads %d / kv heads %d / head_dim %d / max_ctx %d", n_heads, n_kv,
                 head_dim, max_ctx);
   if (!rope_cos != !rope_sin) return fail(c, ELMH_ERR_ARG, "attention_step: rope_cos and rope_sin go together");
-  if (attention_lds_bytes(head_dim, max_ctx) > 65536)
+  if (!elmh_attention_step_supported(head_dim, max_ctx))
     return fail(c, ELMH_ERR_UNSUPPORTED, "attention_step: max_ctx %d exceeds the kernel's LDS", max_ctx);
   DeviceGuard g(c);
   HIP_OR_FAIL(c, launch_attention(q, k, v, out, 1, 0, pos_dev, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx,

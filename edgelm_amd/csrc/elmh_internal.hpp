@@ -138,6 +138,11 @@ hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_grou
 hipError_t launch_silu_mul(const float* g, const float* u, float* y, int64_t n, hipStream_t s);
 // The non-matmul ops of a layer (elmh_layer.hip), same float order as edgelm's cpu backend.
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps, hipStream_t s);
+// LDS a workgroup may allocate on gfx950 (160 KB per CU; kernels that use more than 64 KB raise their
+// dynamic-LDS limit with hipFuncSetAttribute before the first launch)
+constexpr size_t kMaxLds = 160 * 1024;
+// dynamic LDS the attention kernels may take (their static LDS is a few words; this leaves 1 KB for it)
+constexpr size_t kMaxAttnLds = kMaxLds - 1024;
 size_t attention_lds_bytes(int hd, int n_max);
 // pos_dev (if not null): pos0 read from device memory (T must be 1; LDS sized for max_ctx).
 // xq, xd, Tpad, quantized (all given): where the chunk kernel (T > 1, head size 64) runs, it also

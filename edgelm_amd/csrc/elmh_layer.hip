@@ -165,8 +165,8 @@ __global__ __launch_bounds__(64) void kv_append_kernel(const float* __restrict__
 // zero: adding them changes no sum (these sums start at +0.0 and are never -0.0).
 // LDS (dynamic): q [hd], scores [n_cap rounded up to 64], one product chunk [cpos][hd].
 constexpr int kAttnThreads = 256;
-constexpr int kAttnVF = 12;                           // float4 of values per thread per chunk
-constexpr int kAttnChunkF4 = kAttnThreads * kAttnVF;  // 48 KB: 192 positions of head size 64
+constexpr int kAttnVF = 20;                           // float4 of values per thread per chunk
+constexpr int kAttnChunkF4 = kAttnThreads * kAttnVF;  // 80 KB: 320 positions of head size 64
 
 __device__ __host__ __forceinline__ int attn_chunk_pos(int hd) { return (kAttnChunkF4 / (hd / 4)) & ~15; }
 
@@ -353,13 +353,15 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
   // float4 of values: position j, dims 4 d .. 4 d + 3); zero rows past the last position.
   v4f* vt4 = reinterpret_cast<v4f*>(vt);
   auto products = [&](int f) {
+    // only the rows the accumulation reads: this chunk's positions, zero-padded to a multiple of 16
+    const int lim = min(cf4, ((min(cpos, n - f / hd4) + 15) & ~15) * hd4);
     float e[kAttnVF];  // every e_j first (slots past the last position read +0.0), then the products
 #pragma unroll
     for (int u = 0; u < kAttnVF; ++u) e[u] = sc[min((f + tid + u * kAttnThreads) / hd4, n64 - 1)];
 #pragma unroll
     for (int u = 0; u < kAttnVF; ++u) {
       const int rel = tid + u * kAttnThreads;
-      if (rel < cf4) {
+      if (rel < lim) {
         const float pj = e[u] * inv;
         const v4f pr = v4f{pj * vr[u].x, pj * vr[u].y, pj * vr[u].z, pj * vr[u].w};
         vt4[rel] = f + rel < total4 ? pr : v4f{0.f, 0.f, 0.f, 0.f};
@@ -722,6 +724,18 @@ size_t attention_lds_bytes(int hd, int n_max) {
   return (2 * hdp + (size_t)((n_max + 63) & ~63) + (size_t)attn_chunk_pos(hd) * hd) * sizeof(float);
 }
 
+// the attention kernels keep a whole score row (and a chunk of values) in LDS: allow them up to kMaxAttnLds
+bool raise_lds_limit() {
+  const void* kernels[] = {(const void*)attention_kernel<64>, (const void*)attention_kernel<0>,
+                           (const void*)attention_prefill_kernel};
+  for (const void* k : kernels) {
+    hipFuncAttributes fa;
+    if (hipFuncGetAttributes(&fa, k) != hipSuccess || fa.sharedSizeBytes + kMaxAttnLds > kMaxLds) return false;
+    if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxAttnLds) != hipSuccess) return false;
+  }
+  return true;
+}
+
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
                             const int* pos_dev, int n_heads, int n_kv, int hd, float* kc, float* vc, int max_ctx,
                             const float* rcos, const float* rsin, hipStream_t s, int8_t* xq, float* xd, int Tpad,
@@ -739,7 +753,9 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
   const float* kn = fuse ? k : nullptr;
   const float* vn = fuse ? v : nullptr;
   const size_t lds_pf = ((size_t)kAttnQ * hd + (size_t)kAttnQ * ((n_cap + 63) & ~63) + (size_t)kAttnPVPos * hd) * 4;
-  if (!fuse && hd == 64 && lds_pf <= 64 * 1024) {
+  static const bool lds_ok = raise_lds_limit();  // once per process (the attribute holds for the kernel)
+  if (!lds_ok) return hipErrorInvalidValue;
+  if (!fuse && hd == 64 && lds_pf <= kMaxAttnLds) {
     const int ngr = (T + kAttnQ - 1) / kAttnQ;
     const bool quant = xq && xd && quantized;
     attention_prefill_kernel<<<n_heads * ngr, 256, lds_pf, s>>>(q, out, kc, vc, pos0, T, n_heads, n_kv, max_ctx, n_cap,

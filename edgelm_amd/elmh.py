@@ -243,6 +243,13 @@ class Context:
             C.c_int(pos0), C.c_int(n_heads), C.c_int(n_kv), C.c_int(head_dim), C.c_void_p(kc_ptr), C.c_void_p(vc_ptr),
             C.c_int(max_ctx), C.c_void_p(cos_ptr), C.c_void_p(sin_ptr)))
 
+    def attention_step_dev(self, q_ptr, k_ptr, v_ptr, out_ptr, pos_ptr, n_heads, n_kv, head_dim, kc_ptr, vc_ptr, max_ctx,
+                           cos_ptr=None, sin_ptr=None):
+        self._check(lib().elmh_attention_step_dev(
+            self.h, C.c_void_p(q_ptr), C.c_void_p(k_ptr), C.c_void_p(v_ptr), C.c_void_p(out_ptr), C.c_void_p(pos_ptr),
+            C.c_int(n_heads), C.c_int(n_kv), C.c_int(head_dim), C.c_void_p(kc_ptr), C.c_void_p(vc_ptr), C.c_int(max_ctx),
+            C.c_void_p(cos_ptr), C.c_void_p(sin_ptr)))
+
     def attention_matmul_dev(self, q_ptr, k_ptr, v_ptr, out_ptr, T, pos0, n_heads, n_kv, head_dim, kc_ptr, vc_ptr,
                              max_ctx, cos_ptr, sin_ptr, weight, y_ptr, res_ptr=None, act=ACT_INT8, mode=EXACT):
         self._check(lib().elmh_attention_matmul_dev(

@@ -23,6 +23,7 @@
 //
 // keep_output() and argmax_output() (the greedy-sampling hooks) leave the logits in HBM and hand
 // the host only the argmax of their last row.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -146,6 +147,17 @@ class HipBackend : public Backend {
     if (!graphs_on_ || !ctx_ || !prepared_ || c.T != 1 || c.L != 1 || p.end - p.begin < kMinGraphOps) return false;
     const Graph& g = *c.graph;
     StepGraph& sg = graphs_[p.begin];
+    if (sg.warm == 0) {
+      // a captured step reads its position from device memory and sizes attention's score row for the
+      // whole cache; past the kernel's limit the partition runs op by op, sized by the position in use
+      for (int i = p.begin; i < p.end; ++i) {
+        const Op& op = g.ops[i];
+        if (op.type != OpType::ATTENTION || op.iattr[0] < 0 || op.iattr[0] >= static_cast<int>(c.kv.size())) continue;
+        const int hd = static_cast<int>(c.tensor(op.in[0]).cols) / std::max(op.iattr[1], 1);
+        if (!elmh_attention_step_supported(hd, c.kv[op.iattr[0]].max_ctx)) sg.eager = true;
+      }
+    }
+    if (sg.eager) return false;
     if (!sg.exec && sg.warm == 0) {  // warm-up: allocations and uploads happen op by op
       for (int i = p.begin; i < p.end; ++i) run(g.ops[i], c);
       sg.warm = 1;
@@ -388,6 +400,7 @@ class HipBackend : public Backend {
     int warm = 0;
     void* exec = nullptr;
     uint64_t scratch_gen = 0;  // elmh_scratch_generation at capture
+    bool eager = false;        // never captured: an attention op's cache is past the step kernel's limit
   };
 
   void drop_graphs() {

@@ -176,6 +176,12 @@ int elmh_attention_step_dev(elmh_ctx* ctx, const float* q, const float* k, const
                             const int32_t* pos_dev, int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache,
                             int max_ctx, const float* rope_cos, const float* rope_sin);
 
+/* 1 if elmh_attention_step_dev runs this head size with a cache of max_ctx positions, else 0 (its score
+ * row spans the whole cache: about 20K positions at head size 64). elmh_attention_dev takes up to the
+ * same number of positions in use. No counterpart in edgelm (whose attention has no such limit); a
+ * caller that replays graphs runs longer contexts step by step with elmh_attention_dev. */
+int elmh_attention_step_supported(int head_dim, int max_ctx);
+
 /* Greedy sampling: argmax (tokenizer.cpp:187-189, std::max_element) of each row of x [rows, n]
  * (device pointers) into out [rows] (device int32): the first index of the largest value under
  * IEEE <, so NaNs after index 0 are never chosen and a NaN at index 0 is. Lets a caller take the

@@ -51,3 +51,12 @@ def test_hip_backend_compiles_against_edgelm_headers():
     p = subprocess.run([cxx, "-std=c++17", "-fsyntax-only", "-Wall", "-Wextra", "-Werror",
                         "-I/root/reference/include", f"-I{INCLUDE}", src], capture_output=True, text=True)
     assert p.returncode == 0, p.stderr
+
+
+def test_attention_step_limit_is_a_pure_query():
+    """elmh_attention_step_supported needs no device: the step kernel's whole-cache score row fits gfx950's LDS
+    up to about 20K positions at head size 64."""
+    from edgelm_amd import elmh as E
+    f = E.lib().elmh_attention_step_supported
+    assert f(64, 2048) == 1 and f(64, 16384) == 1 and f(64, 20000) == 1
+    assert f(64, 40000) == 0 and f(62, 128) == 0 and f(64, 0) == 0

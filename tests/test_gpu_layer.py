@@ -74,6 +74,43 @@ def test_attention_bit_exact(ctx, shape, rope):
         b.free()
 
 
+@pytest.mark.parametrize("rope", [False, True])
+def test_attention_long_cache_decode_steps(ctx, rope):
+    """Decode steps with the position read from device memory (the form a captured graph replays) over a
+    cache of 16,384 positions, whose score row the step kernel keeps whole in LDS (more than 64 KB: the
+    kernel's LDS limit is raised to gfx950's 160 KB), at positions around the 320-position value chunks."""
+    nh, nkv, hd, mc = 9, 3, 64, 16384
+    r = np.random.default_rng(77 + int(rope))
+    tab = O.rope_table(hd, mc, 100000.0) if rope else None
+    kc = np.zeros((nkv, mc, hd), np.float32)
+    vc = np.zeros_like(kc)
+    bkc, bvc = dev(ctx, kc), dev(ctx, vc)
+    bcos, bsin = (dev(ctx, tab[0]), dev(ctx, tab[1])) if rope else (None, None)
+    bpos = ctx.buffer(4)
+    pos = 0
+    for T, step in [(318, False), (1, True), (1, True), (1, True), (318, False), (1, True), (1, True)]:
+        print(f"[gpu] long-cache attention rope={rope} pos0={pos} T={T} step={step}", flush=True)
+        q = r.normal(0, 1, (T, nh * hd)).astype(np.float32)
+        k = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+        v = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+        bq, bk, bv, bo = dev(ctx, q), dev(ctx, k), dev(ctx, v), ctx.buffer(q.nbytes)
+        if step:
+            bpos.upload(np.array([pos], np.int32))
+            ctx.attention_step_dev(bq.ptr, bk.ptr, bv.ptr, bo.ptr, bpos.ptr, nh, nkv, hd, bkc.ptr, bvc.ptr, mc,
+                                   bcos.ptr if rope else None, bsin.ptr if rope else None)
+        else:
+            ctx.attention_dev(bq.ptr, bk.ptr, bv.ptr, bo.ptr, T, pos, nh, nkv, hd, bkc.ptr, bvc.ptr, mc,
+                              bcos.ptr if rope else None, bsin.ptr if rope else None)
+        want = O.attention(q, k, v, pos, nh, nkv, kc, vc, tab)
+        assert bits_equal(bo.download(q.shape, np.float32), want), f"pos0={pos} T={T}"
+        for b in (bq, bk, bv, bo):
+            b.free()
+        pos += T
+    assert bits_equal(bkc.download(kc.shape, np.float32), kc)
+    for b in [bkc, bvc, bpos] + ([bcos, bsin] if rope else []):
+        b.free()
+
+
 FUSED_ATTN = [(9, 3, 64, 300, (128, 1, 33, 7, 3)), (4, 4, 32, 64, (17, 5))]
 
 
