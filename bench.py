@@ -475,6 +475,27 @@ def pmc_workload(ctx, E):
     log("pmc workload done")
 
 
+def pmc_gemm_workload(ctx, E):
+    """The configs[4] T = 512 prefill GEMMs alone (q8 weights; per-token scale, then edgelm's per-block scales),
+    four eager launches per shape, for rocprofv3 --pmc passes (MFMA busy cycles, LDS bank conflicts, VALU and
+    MFMA instruction counts)."""
+    b8 = [(4096, 4096), (14336, 4096), (4096, 14336)]
+    m = Model(ctx, 5, {f"{i}": sh for i, sh in enumerate(b8)}, lambda n: 1)
+    bx = ctx.buffer(512 * 14336 * 4)
+    bx.upload(np.random.default_rng(3).standard_normal(512 * 14336, dtype=np.float32))
+    by = ctx.buffer(512 * 14336 * 4)
+    ctx.reserve(512, 14336)
+    for act in (E.ACT_INT8_TOKEN, E.ACT_INT8):
+        for i, (n, k) in enumerate(b8):
+            for _ in range(4):
+                ctx.matmul_dev(bx.ptr, 512, k, [m.w[f"{i}"]], [by.ptr], act=act)
+            ctx.synchronize()
+    bx.free()
+    by.free()
+    m.free()
+    log("pmc gemm workload done")
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary, or None."""
     try:
@@ -497,6 +518,8 @@ def main():
     ap.add_argument("--no-chain", action="store_true", help="skip the decode matmul chain and its per-op timers")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the roofline kernels and a calibration copy (for rocprofv3 counter passes)")
+    ap.add_argument("--pmc-gemm", action="store_true",
+                    help="run only the T = 512 prefill GEMMs (for rocprofv3 counter passes)")
     ap.add_argument("--eager", action="store_true",
                     help="no HIP graphs, in the benchmarks or the e2e sessions (for kernel tracing): the step "
                          "rate becomes host-bound, per-kernel event timings are unchanged")
@@ -513,9 +536,9 @@ def main():
         sys.exit(2)
 
     from edgelm_amd import elmh as E
-    if args.pmc_workload:
+    if args.pmc_workload or args.pmc_gemm:
         ctx = E.Context(0)
-        pmc_workload(ctx, E)
+        (pmc_workload if args.pmc_workload else pmc_gemm_workload)(ctx, E)
         ctx.close()
         return
 
