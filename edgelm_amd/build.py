@@ -1,8 +1,8 @@
 """In-tree build of the native libraries (no JIT cache, no pip install).
 
 * ``edgelm_amd/lib/libelmh.so`` — the HIP kernels for gfx950 plus the C ABI of ``include/elmh.h``.
-* ``edgelm_amd/lib/libedgelm_host.so`` — the C++17 host runtime (edgelm's Backend / partitioner /
-  Session restated, with the ``hip`` backend that calls libelmh), linked against libelmh.
+* ``edgelm_amd/lib/libedgelm_host.so`` — the C++17 host runtime (edgelm's Backend / partitioner / Session
+  interfaces, implemented here, with the ``hip`` backend that calls libelmh), linked against libelmh.
 
 Run ``python -m edgelm_amd.build`` (or ``__graft_entry__.build()``). Always recompiles.
 """
