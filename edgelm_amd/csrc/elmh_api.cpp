@@ -118,6 +118,44 @@ int choose_H(int dtype, int64_t K) {
   return 4;
 }
 
+// The repacked layout of a q8 / q4 weight (DevWeight): tile height, blocks, padded rows and bytes.
+struct Layout {
+  int H = 0;
+  int64_t nb = 0, rows_pad = 0;
+  size_t data_bytes = 0, scale_bytes = 0;
+};
+Layout layout_of(int dtype, int64_t rows, int64_t cols) {
+  Layout L;
+  L.nb = (cols + kBlock - 1) / kBlock;
+  L.H = choose_H(dtype, cols);
+  L.rows_pad = round_up(rows, kPadRows);
+  L.data_bytes = (size_t)(L.rows_pad * L.nb * (dtype == ELMH_Q8 ? 32 : 16));
+  L.scale_bytes = (size_t)(dtype == ELMH_Q8 ? L.rows_pad : L.rows_pad * L.nb) * sizeof(float);
+  return L;
+}
+int check_weight(elmh_ctx* c, int dtype, int64_t rows, int64_t cols) {
+  if (dtype != ELMH_Q8 && dtype != ELMH_Q4)
+    return fail(c, ELMH_ERR_UNSUPPORTED, "dtype %d: only q8 (1) and q4 (2) weights are uploaded", dtype);
+  if (rows < 1 || cols < 1) return fail(c, ELMH_ERR_ARG, "bad weight %lldx%lld", (long long)rows, (long long)cols);
+  if (rows > (1ll << 30) || cols > (1ll << 24)) return fail(c, ELMH_ERR_UNSUPPORTED, "weight too large");
+  if (dtype == ELMH_Q4 && cols % kBlock) return fail(c, ELMH_ERR_ARG, "q4 needs K %% 32 == 0, got K=%lld", (long long)cols);
+  return ELMH_OK;
+}
+
+DevWeight new_weight(int dtype, int64_t rows, int64_t cols) {
+  const Layout L = layout_of(dtype, rows, cols);
+  DevWeight w;
+  w.dtype = dtype;
+  w.rows = rows;
+  w.cols = cols;
+  w.nb = L.nb;
+  w.H = L.H;
+  w.rows_pad = L.rows_pad;
+  w.data_bytes = L.data_bytes;
+  w.scale_bytes = L.scale_bytes;
+  return w;
+}
+
 // Small-matrix decode path (workgroups quantize x themselves) vs the streaming path: short rows and
 // at most ~4 MB of weights per launch.
 bool use_small_gemv(int T, int64_t K, size_t bytes = 0) {
@@ -609,22 +647,11 @@ int elmh_upload_weight(elmh_ctx* c, int dtype, int64_t rows, int64_t cols, const
                        elmh_weight** out) {
   if (!c || !out) return fail(c, ELMH_ERR_ARG, "null ctx/out");
   *out = nullptr;
-  if (dtype != ELMH_Q8 && dtype != ELMH_Q4)
-    return fail(c, ELMH_ERR_UNSUPPORTED, "dtype %d: only q8 (1) and q4 (2) weights are uploaded", dtype);
-  if (rows < 1 || cols < 1 || !data || !scales) return fail(c, ELMH_ERR_ARG, "bad weight %lldx%lld", (long long)rows, (long long)cols);
-  if (rows > (1ll << 30) || cols > (1ll << 24)) return fail(c, ELMH_ERR_UNSUPPORTED, "weight too large");
-  if (dtype == ELMH_Q4 && cols % kBlock) return fail(c, ELMH_ERR_ARG, "q4 needs K %% 32 == 0, got K=%lld", (long long)cols);
+  int rc = check_weight(c, dtype, rows, cols);
+  if (rc) return rc;
+  if (!data || !scales) return fail(c, ELMH_ERR_ARG, "null weight data/scales");
   DeviceGuard guard(c);
-  DevWeight w;
-  w.dtype = dtype;
-  w.rows = rows;
-  w.cols = cols;
-  w.nb = (cols + kBlock - 1) / kBlock;
-  w.H = choose_H(dtype, cols);
-  w.rows_pad = round_up(rows, kPadRows);
-  const int G = dtype == ELMH_Q8 ? 32 : 16;
-  w.data_bytes = (size_t)(w.rows_pad * w.nb * G);
-  w.scale_bytes = (size_t)(dtype == ELMH_Q8 ? w.rows_pad : w.rows_pad * w.nb) * sizeof(float);
+  DevWeight w = new_weight(dtype, rows, cols);
   const size_t raw_bytes = (size_t)(dtype == ELMH_Q8 ? rows * cols : rows * (cols / 2));
   const size_t raw_sbytes = (size_t)(dtype == ELMH_Q8 ? rows : rows * w.nb) * sizeof(float);
   void *raw = nullptr, *raw_s = nullptr;
@@ -667,6 +694,84 @@ int elmh_free_weight(elmh_ctx* c, elmh_weight* w) {
 }
 
 size_t elmh_weight_bytes(const elmh_weight* w) { return w ? w->w.data_bytes + w->w.scale_bytes : 0; }
+
+int elmh_weight_layout(int dtype, int64_t rows, int64_t cols, int* H, size_t* data_bytes, size_t* scale_bytes) {
+  int rc = check_weight(nullptr, dtype, rows, cols);
+  if (rc) return rc;
+  const Layout L = layout_of(dtype, rows, cols);
+  if (H) *H = L.H;
+  if (data_bytes) *data_bytes = L.data_bytes;
+  if (scale_bytes) *scale_bytes = L.scale_bytes;
+  return ELMH_OK;
+}
+
+// repack_kernel's permutation on the host: item (row n, block b) at item_index(n, b, nb, H), q8 rows
+// zero-padded past K and past the last row, q4 padding rows 0x88 (q = 0) with scale 0.
+int elmh_repack_host(int dtype, int64_t rows, int64_t cols, const void* data, const float* scales, void* out_data,
+                     float* out_scales) {
+  int rc = check_weight(nullptr, dtype, rows, cols);
+  if (rc) return rc;
+  if (!data || !scales || !out_data || !out_scales) return fail(nullptr, ELMH_ERR_ARG, "repack: null pointer");
+  const Layout L = layout_of(dtype, rows, cols);
+  const uint8_t* raw = static_cast<const uint8_t*>(data);
+  uint8_t* out = static_cast<uint8_t*>(out_data);
+  const int G = dtype == ELMH_Q8 ? 32 : 16;
+  for (int64_t n = 0; n < L.rows_pad; ++n) {
+    const bool real = n < rows;
+    if (dtype == ELMH_Q8) out_scales[n] = real ? scales[n] : 0.f;
+    for (int64_t b = 0; b < L.nb; ++b) {
+      const int64_t dst = item_index(n, b, L.nb, L.H);
+      uint8_t* o = out + dst * G;
+      if (dtype == ELMH_Q8) {
+        const int64_t k0 = b * kBlock, nk = real ? std::min<int64_t>(kBlock, cols - k0) : 0;
+        if (nk > 0) std::memcpy(o, raw + n * cols + k0, (size_t)nk);
+        std::memset(o + std::max<int64_t>(nk, 0), 0, (size_t)(kBlock - std::max<int64_t>(nk, 0)));
+      } else {
+        if (real)
+          std::memcpy(o, raw + n * (cols / 2) + b * 16, 16);
+        else
+          std::memset(o, 0x88, 16);
+        out_scales[dst] = real ? scales[n * L.nb + b] : 0.f;
+      }
+    }
+  }
+  return ELMH_OK;
+}
+
+int elmh_upload_weight_image(elmh_ctx* c, int dtype, int64_t rows, int64_t cols, const void* data, const float* scales,
+                             elmh_weight** out) {
+  if (!c || !out) return fail(c, ELMH_ERR_ARG, "null ctx/out");
+  *out = nullptr;
+  int rc = check_weight(c, dtype, rows, cols);
+  if (rc) return rc;
+  if (!data || !scales) return fail(c, ELMH_ERR_ARG, "null weight image");
+  DeviceGuard guard(c);
+  DevWeight w = new_weight(dtype, rows, cols);
+  if (hipMalloc((void**)&w.data, w.data_bytes) != hipSuccess || hipMalloc((void**)&w.scales, w.scale_bytes) != hipSuccess) {
+    if (w.data) (void)hipFree(w.data);
+    if (w.scales) (void)hipFree(w.scales);
+    return fail(c, ELMH_ERR_OOM, "hipMalloc failed for a %lldx%lld weight", (long long)rows, (long long)cols);
+  }
+  hipError_t e = hipMemcpyAsync(w.data, data, w.data_bytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(w.scales, scales, w.scale_bytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(w.data);
+    (void)hipFree(w.scales);
+    return fail(c, ELMH_ERR_HIP, "weight image upload: %s", hipGetErrorString(e));
+  }
+  *out = new elmh_weight{w};
+  return ELMH_OK;
+}
+
+int elmh_download_weight_image(elmh_ctx* c, const elmh_weight* w, void* data, float* scales) {
+  if (!c || !w || !data || !scales) return fail(c, ELMH_ERR_ARG, "null ctx/weight/output");
+  DeviceGuard guard(c);
+  HIP_OR_FAIL(c, hipMemcpyAsync(data, w->w.data, w->w.data_bytes, hipMemcpyDeviceToHost, c->stream));
+  HIP_OR_FAIL(c, hipMemcpyAsync(scales, w->w.scales, w->w.scale_bytes, hipMemcpyDeviceToHost, c->stream));
+  HIP_OR_FAIL(c, hipStreamSynchronize(c->stream));
+  return ELMH_OK;
+}
 
 uint64_t elmh_scratch_generation(const elmh_ctx* c) { return c ? c->scratch_gen : 0; }
 

@@ -56,6 +56,26 @@ def device_count():
     return n.value
 
 
+def weight_layout(dtype, rows, cols):
+    """(H, data bytes, scale bytes) of a weight's repacked HBM layout (pure host call, no GPU)."""
+    H, db, sb = C.c_int(), C.c_size_t(), C.c_size_t()
+    rc = lib().elmh_weight_layout(C.c_int(dtype), C.c_int64(rows), C.c_int64(cols), C.byref(H), C.byref(db), C.byref(sb))
+    if rc:
+        raise ElmhError(rc, lib().elmh_last_error(None).decode())
+    return H.value, db.value, sb.value
+
+
+def repack_host(dtype, rows, cols, data, scales):
+    """edgelm's export layout -> the repacked HBM layout, on the CPU: (data bytes, scales) as numpy arrays."""
+    _, db, sb = weight_layout(dtype, rows, cols)
+    data, scales = np.ascontiguousarray(data), np.ascontiguousarray(scales, dtype=np.float32)
+    out, out_s = np.empty(db, np.uint8), np.empty(sb // 4, np.float32)
+    rc = lib().elmh_repack_host(C.c_int(dtype), C.c_int64(rows), C.c_int64(cols), _p(data), _p(scales), _p(out), _p(out_s))
+    if rc:
+        raise ElmhError(rc, lib().elmh_last_error(None).decode())
+    return out, out_s
+
+
 class DevWeight:
     """A weight resident in HBM (repacked). ``free()`` or context teardown releases it."""
 
@@ -139,6 +159,22 @@ class Context:
         return DevWeight(self, h, dtype, rows, cols)
 
     # ---- host-pointer ops (synchronous)
+    def upload_image(self, dtype, rows, cols, data, scales):
+        """A weight already in the repacked layout (repack_host's output)."""
+        data = np.ascontiguousarray(data)
+        scales = np.ascontiguousarray(scales, dtype=np.float32)
+        h = C.c_void_p()
+        self._check(lib().elmh_upload_weight_image(self.h, C.c_int(dtype), C.c_int64(rows), C.c_int64(cols), _p(data),
+                                                   _p(scales), C.byref(h)))
+        return DevWeight(self, h, dtype, rows, cols)
+
+    def download_image(self, w):
+        """(data bytes, scales) of a weight's repacked layout in HBM."""
+        _, db, sb = weight_layout(w.dtype, w.rows, w.cols)
+        out, out_s = np.empty(db, np.uint8), np.empty(sb // 4, np.float32)
+        self._check(lib().elmh_download_weight_image(self.h, w.h, _p(out), _p(out_s)))
+        return out, out_s
+
     def matmul(self, x, weights, residuals=None, act=ACT_INT8, mode=EXACT):
         x = np.ascontiguousarray(x, dtype=np.float32)
         T, K = x.shape

@@ -140,6 +140,25 @@ class Model:
         if L.elm_model_prefault(self.h):
             raise RuntimeError(_err())
 
+    def write_device_image(self, path, threads=0):
+        """Every q8 / q4 weight in the hip delegate's HBM layout, cached in one file; returns the count."""
+        L = _setup()
+        L.elm_model_write_device_image.argtypes = [C.c_void_p, C.c_char_p, C.c_int]
+        n = L.elm_model_write_device_image(self.h, os.fsencode(path), _threads(threads))
+        if n < 0:
+            raise RuntimeError(_err())
+        return n
+
+    def attach_device_image(self, path):
+        """Sessions made afterwards upload the weights from the image at `path`; False if it is missing or
+        was written for other weights."""
+        L = _setup()
+        L.elm_model_attach_device_image.argtypes = [C.c_void_p, C.c_char_p]
+        r = L.elm_model_attach_device_image(self.h, os.fsencode(path))
+        if r < 0:
+            raise RuntimeError(_err())
+        return r == 1
+
     def weight(self, name):
         """(dtype, data, scales) of weight `name` as stored (after any conversion)."""
         L = _setup()

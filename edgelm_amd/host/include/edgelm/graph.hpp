@@ -40,8 +40,14 @@ struct Tensor {
   const float* scales = nullptr;  // q8: [rows]; q4: [rows * cols / 32]
   size_t data_bytes = 0, scale_bytes = 0;
   int group = 0;
+  // Not in edgelm's Tensor: the weight in a device's repacked layout, from a device image attached to
+  // the model (Model::attach_device_image), or null. Code that must also compile against edgelm's
+  // header tests EDGELM_TENSOR_DEVICE_IMAGE.
+  const void* image = nullptr;
+  const float* image_scales = nullptr;
   bool is_weight() const { return kind == TensorKind::Weight; }
 };
+#define EDGELM_TENSOR_DEVICE_IMAGE 1
 
 struct Op {
   OpType type = OpType::COUNT;

@@ -37,11 +37,21 @@ class Model {
   size_t weight_bytes() const;  // data + scales of every weight
   size_t file_bytes() const;
 
+  // Device image: every q8 / q4 weight in the repacked layout the hip delegate keeps in HBM
+  // (elmh_repack_host), in one file, so that a later session uploads each weight as it will lie in
+  // HBM. The image records a digest of the model (its config, tensor table and weight contents);
+  // attach_device_image maps an image and points the weights at it, or returns false (and changes
+  // nothing) when the file is missing or was written for other weights. Returns the weights written.
+  int write_device_image(const std::string& path, int threads = 1) const;
+  bool attach_device_image(const std::string& path);
+  uint64_t digest() const;
+
   Config cfg;
   Graph graph;
 
  private:
   std::shared_ptr<const FileMap> file_;
+  std::shared_ptr<const FileMap> image_;  // an attached device image
   std::vector<std::shared_ptr<std::vector<uint8_t>>> converted_;  // arrays made by convert_weights
 };
 

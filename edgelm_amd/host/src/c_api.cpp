@@ -91,6 +91,20 @@ int elm_model_prefault(const elm_model* m) {
   });
 }
 
+int elm_model_write_device_image(const elm_model* m, const char* path, int threads) {
+  return guard([&] {
+    if (!m || !path) throw std::runtime_error("edgelm: null argument");
+    return m->m.write_device_image(path, threads);
+  });
+}
+
+int elm_model_attach_device_image(elm_model* m, const char* path) {
+  return guard([&] {
+    if (!m || !path) throw std::runtime_error("edgelm: null argument");
+    return m->m.attach_device_image(path) ? 1 : 0;
+  });
+}
+
 int elm_model_weight(const elm_model* m, const char* name, int64_t* rows, int64_t* cols, void* data, float* scales) {
   return guard([&] {
     if (!m || !name) throw std::runtime_error("edgelm: null argument");

@@ -10,46 +10,14 @@
 //   weight blob      the arrays, each 64-byte aligned, at offsets relative to the blob start
 #include "edgelm/elm_container.hpp"
 
-#include <fcntl.h>
-#include <sys/mman.h>
-#include <sys/stat.h>
-#include <unistd.h>
-
 #include <cstring>
 #include <stdexcept>
 
+#include "edgelm/file_map.hpp"
 #include "edgelm/model.hpp"
 #include "edgelm_host.h"
 
 namespace edgelm {
-
-// A read-only private mapping of a whole file.
-class FileMap {
- public:
-  explicit FileMap(const std::string& path) {
-    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
-    if (fd < 0) throw std::runtime_error("edgelm: cannot open model file " + path);
-    struct stat st {};
-    const bool sized = ::fstat(fd, &st) == 0 && st.st_size > 0;
-    if (sized) {
-      len_ = static_cast<size_t>(st.st_size);
-      void* p = ::mmap(nullptr, len_, PROT_READ, MAP_PRIVATE, fd, 0);
-      base_ = p == MAP_FAILED ? nullptr : static_cast<const uint8_t*>(p);
-    }
-    ::close(fd);
-    if (!base_) throw std::runtime_error("edgelm: cannot map model file " + path + (sized ? "" : " (empty)"));
-  }
-  ~FileMap() { ::munmap(const_cast<uint8_t*>(base_), len_); }
-  FileMap(const FileMap&) = delete;
-  FileMap& operator=(const FileMap&) = delete;
-  const uint8_t* base() const { return base_; }
-  size_t size() const { return len_; }
-
- private:
-  const uint8_t* base_ = nullptr;
-  size_t len_ = 0;
-};
-
 namespace {
 
 [[noreturn]] void corrupt(const std::string& what) { throw std::runtime_error("edgelm: malformed .elm file: " + what); }

@@ -497,7 +497,15 @@ class HipBackend : public Backend {
     auto it = weights_.find(&t);
     if (it != weights_.end()) return it->second;
     elmh_weight* w = nullptr;
-    if (elmh_upload_weight(ctx_, static_cast<int>(t.dtype), t.rows, t.cols, t.data, t.scales, &w) != ELMH_OK)
+    const int dt = static_cast<int>(t.dtype);
+#ifdef EDGELM_TENSOR_DEVICE_IMAGE
+    // the weight already in the device layout (a device image attached to the model)
+    const int rc = t.image ? elmh_upload_weight_image(ctx_, dt, t.rows, t.cols, t.image, t.image_scales, &w)
+                           : elmh_upload_weight(ctx_, dt, t.rows, t.cols, t.data, t.scales, &w);
+#else
+    const int rc = elmh_upload_weight(ctx_, dt, t.rows, t.cols, t.data, t.scales, &w);
+#endif
+    if (rc != ELMH_OK)
       throw std::runtime_error(std::string("edgelm: hip upload of ") + t.name + ": " + elmh_last_error(ctx_));
     weights_.emplace(&t, w);
     return w;

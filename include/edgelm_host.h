@@ -47,6 +47,12 @@ void elm_model_free(elm_model* m);
 int elm_model_convert(elm_model* m, int dtype, int threads);
 /* Model::prefault: touch every page of the mapping. */
 int elm_model_prefault(const elm_model* m);
+/* Device image (the cached repacked layout of the load path): elm_model_write_device_image writes every
+ * q8 / q4 weight in the hip delegate's HBM layout to `path` and returns how many it wrote;
+ * elm_model_attach_device_image maps such a file and returns 1, so that sessions made afterwards upload
+ * the weights from it, or 0 (nothing changed) when the file is missing or belongs to other weights. */
+int elm_model_write_device_image(const elm_model* m, const char* path, int threads);
+int elm_model_attach_device_image(elm_model* m, const char* path);
 /* Copies weight `name`'s data and scales (either may be NULL) and returns its dtype, or -1 if there is
  * no such weight; rows/cols get its shape. For tests of the loader and of convert_weights. */
 int elm_model_weight(const elm_model* m, const char* name, int64_t* rows, int64_t* cols, void* data, float* scales);

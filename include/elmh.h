@@ -80,6 +80,21 @@ int elmh_free_weight(elmh_ctx* ctx, elmh_weight* w);
 /* Device bytes held by the weight (data + scales, after padding). */
 size_t elmh_weight_bytes(const elmh_weight* w);
 
+/* ---- device images of weights (the cached repacked layout of the load path, model.cpp:94-116) ----
+ * The layout a weight has in HBM: row tiles of H rows, [rows_pad/H][nb][H] items of 32 (q8) or 16 (q4)
+ * bytes, scales q8 [rows_pad], q4 [rows_pad/H][nb][H]; rows_pad = rows rounded up to 64. H depends on
+ * dtype and cols only. elmh_weight_layout gives H and the byte counts; elmh_repack_host builds the
+ * layout from edgelm's export layout on the CPU (the same bytes the upload's device repack writes);
+ * elmh_upload_weight_image uploads a weight already in that layout (no repack launch, no staging of
+ * the export layout); elmh_download_weight_image copies one back. No counterpart in edgelm: they let
+ * a host cache the repacked weights on disk next to the .elm file. */
+int elmh_weight_layout(int dtype, int64_t rows, int64_t cols, int* H, size_t* data_bytes, size_t* scale_bytes);
+int elmh_repack_host(int dtype, int64_t rows, int64_t cols, const void* data, const float* scales, void* out_data,
+                     float* out_scales);
+int elmh_upload_weight_image(elmh_ctx* ctx, int dtype, int64_t rows, int64_t cols, const void* data,
+                             const float* scales, elmh_weight** out);
+int elmh_download_weight_image(elmh_ctx* ctx, const elmh_weight* w, void* data, float* scales);
+
 /* ---- MATMUL / MATMUL_N / MATMUL_ADD (cpu::matmul, kernels_cpu.cpp:339-377) ----
  * For each target i: y[i][T, N_i] = (residual[i] ? residual[i] : 0) + x[T, K] . W_i^T.
  * x is quantized once for all targets (int8 modes). residual may be NULL, or residual[i]
