@@ -58,6 +58,8 @@ struct elmh_ctx {
   uint64_t scratch_gen = 0;
   // this device's copy of the no-allocation scratch array
   unsigned char* noalloc = nullptr;
+  // whether the last elmh_attention_matmul_dev call had the attention kernel write the GEMM's operand
+  int attn_fused = 0;
 };
 
 namespace {
@@ -1087,13 +1089,17 @@ int elmh_attention_matmul_dev(elmh_ctx* c, const float* q, const float* k, const
     xd = ab.d;
   }
   bool quantized = false;
+  c->attn_fused = 0;
   HIP_OR_FAIL(c, launch_attention(q, k, v, out, T, pos0, nullptr, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx,
                                   rope_cos, rope_sin, c->stream, xq, xd, Tpad, &quantized));
+  c->attn_fused = quantized ? 1 : 0;
   if (!quantized) return run_matmul(c, out, T, K, 1, ws, ys, res ? rs : nullptr, act, mode);
   for (const auto& grp : by_dtype(1, ws))
     if ((rc = run_gemm_group(c, xq, xd, T, Tpad, K, grp, ws, ys, res ? rs : nullptr, 0, mode == ELMH_FAST))) return rc;
   return ELMH_OK;
 }
+
+int elmh_attention_matmul_fused(const elmh_ctx* c) { return c ? c->attn_fused : 0; }
 
 int elmh_attention_dev(elmh_ctx* c, const float* q, const float* k, const float* v, float* out, int T, int pos0,
                        int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache, int max_ctx,

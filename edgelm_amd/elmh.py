@@ -294,6 +294,10 @@ class Context:
             C.c_int(max_ctx), C.c_void_p(cos_ptr), C.c_void_p(sin_ptr), weight.h, C.c_void_p(y_ptr),
             C.c_void_p(res_ptr), C.c_int(act), C.c_int(mode)))
 
+    def attention_matmul_fused(self):
+        """True if the last attention_matmul_dev call had the attention kernel write the GEMM's operand."""
+        return bool(lib().elmh_attention_matmul_fused(self.h))
+
     def argmax_dev(self, x_ptr, rows, n, out_ptr):
         self._check(lib().elmh_argmax_dev(self.h, C.c_void_p(x_ptr), C.c_int(rows), C.c_int64(n), C.c_void_p(out_ptr)))
 

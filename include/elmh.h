@@ -178,7 +178,12 @@ int elmh_attention_dev(elmh_ctx* ctx, const float* q, const float* k, const floa
  * n_heads*head_dim, one target w -> y, residual res or NULL), bit for bit; out is written as
  * well. Where the chunk attention kernel (T > 1, head_dim 64) and the block-scale GEMM (int8
  * activations, too many rows for the GEMV) both apply, the attention kernel also writes its
- * output as the GEMM's quantized operand, so no quantizer launch runs in between. */
+ * output as the GEMM's quantized operand, so no quantizer launch runs in between. The GEMM then
+ * also multiplies the token slots T .. round_up(T, 128) - 1 of that operand, which hold whatever an
+ * earlier call left there: their results are never stored, and every stored output depends only on
+ * its own token's slot. elmh_attention_matmul_fused(ctx) returns 1 if the last call took that path,
+ * else 0 (no counterpart in edgelm: it lets a test tell the two paths apart). */
+int elmh_attention_matmul_fused(const elmh_ctx* ctx);
 int elmh_attention_matmul_dev(elmh_ctx* ctx, const float* q, const float* k, const float* v, float* out, int T,
                               int pos0, int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache,
                               int max_ctx, const float* rope_cos, const float* rope_sin, elmh_weight* w, float* y,

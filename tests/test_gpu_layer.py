@@ -120,8 +120,9 @@ def test_attention_fused_into_matmul(ctx, shape, dt):
     """elmh_attention_matmul_dev: out and the KV caches as ATTENTION, and y bit-identical to the o
     projection (MATMUL_ADD with the residual, then plain MATMUL) on edgelm's cpu backend over the
     attention's output, for a session's calls: chunks where the attention kernel writes the GEMM's
-    quantized operand (T = 128, then T = 33 over the rows the first call left past T), a decode
-    token and short chunks on the GEMV, and head size 32, which never fuses."""
+    quantized operand (T = 128, then T = 33 and 7 over the token slots the first call left past T), a
+    decode token and a short chunk on the GEMV, and head size 32, which never fuses; each call's path
+    is asserted through elmh_attention_matmul_fused."""
     nh, nkv, hd, mc, steps = shape
     r = np.random.default_rng(nh + hd + dt)
     tab = O.rope_table(hd, mc, 100000.0)
@@ -142,6 +143,10 @@ def test_attention_fused_into_matmul(ctx, shape, dt):
         bres = dev(ctx, res) if res is not None else None
         ctx.attention_matmul_dev(bq.ptr, bk.ptr, bv.ptr, bo.ptr, T, pos, nh, nkv, hd, bkc.ptr, bvc.ptr, mc,
                                  bcos.ptr, bsin.ptr, dw, by.ptr, bres.ptr if bres else None)
+        # the path taken: the attention kernel writes the GEMM's operand for chunks of head size 64 that
+        # go to the block-scale GEMM (more than 4 tokens at these shapes: T = 128, 33, 7); decode tokens
+        # and chunks of up to 4 tokens use the GEMV, head size 32 the separate quantizer
+        assert ctx.attention_matmul_fused() == (hd == 64 and T > 4), f"pos0={pos} T={T}"
         att = O.attention(q, k, v, pos, nh, nkv, kc, vc, tab)
         assert bits_equal(bo.download(q.shape, np.float32), att), f"pos0={pos} T={T}"
         want = O.cpu_matmul(att, [w], [res], act_quant=True)[0]
