@@ -612,6 +612,23 @@ __device__ __forceinline__ void dma4(const void* src, unsigned char* dst) {
   const unsigned m0 = (unsigned)(size_t)(LdsBytes)dst;
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory");
 }
+// The same from a wave-uniform base (scalar registers) plus a 32-bit byte offset per lane: a loop
+// that walks the base keeps the per-lane address arithmetic out of its body. The base must be the
+// same in every lane; it is read from the first active one.
+__device__ __forceinline__ uint64_t uniform_addr(const void* p) {
+  const uint64_t v = (uint64_t)(size_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (uint64_t)hi << 32 | lo;
+}
+// dst: the LDS byte address (wave-uniform) the lanes' data go to.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t off, unsigned dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(dst);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(uniform_addr(base)), "s"(m0) : "memory");
+}
+__device__ __forceinline__ void dma4s(const void* base, uint32_t off, unsigned dst) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(dst);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(uniform_addr(base)), "s"(m0) : "memory");
+}
 
 // s_waitcnt vmcnt(N) only (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4] << 14)
 template <int N>
@@ -937,26 +954,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
   const int dhalf = (lane & 1) ^ ((drow >> 3) & 1);  // q8: the half that lane fills
   const int wrow = min(r0 + drow, rows_pad - 1);
   const int64_t rbase = (int64_t)(wrow / H) * nb * H + (wrow % H);  // item of (wrow, block 0)
-  const int8_t* const xg = a.xq + (int64_t)((t0 >> 5) + (MT == 2 ? wave : wave >> 1)) * nb * 1024 +
-                           (MT == 2 ? lane * 16 : (wave & 1) * 512 + l32 * 16);
+  // this lane's byte offsets at block 0 (the host keeps both arrays below 2 GB); a block adds a
+  // uniform stride to the scalar base: 1 KB of activation, H items of weight, Tpad scales
+  const uint32_t xoff = (uint32_t)(((int64_t)((t0 >> 5) + (MT == 2 ? wave : wave >> 1)) * nb * 1024) +
+                                   (MT == 2 ? lane * 16 : (wave & 1) * 512 + l32 * 16));
+  const uint32_t woff = (uint32_t)(WDT == WQ8 ? rbase * 32 + dhalf * 16 : rbase * 16);
+  const uint32_t soff = (uint32_t)(rbase * 4);
+  const uint32_t doff = (uint32_t)((t0 + wave * (TT / 4) + lane) * 4);
+  constexpr uint32_t G = WDT == WQ8 ? 32 : 16;
+  const uint32_t wstride = (uint32_t)H * G, sstride = (uint32_t)H * 4, dstride = (uint32_t)a.Tpad * 4;
+  const unsigned ring_lds = (unsigned)(size_t)(LdsBytes)ring;
   auto issue = [&](int blk, int slot) {
-    blk = min(blk, nb - 1);
-    unsigned char* sb = ring + slot * R::SLOT;
-    if (MT == 2 || lane < 32) dma16(xg + (int64_t)blk * 1024, sb + wave * (MT == 2 ? 1024 : 512));
-    const int64_t it = rbase + (int64_t)blk * H;
+    const uint32_t ub = (uint32_t)min(blk, nb - 1);
+    const unsigned sb = ring_lds + (unsigned)slot * R::SLOT;
+    if (MT == 2 || lane < 32) dma16s(a.xq + ub * 1024u, xoff, sb + wave * (MT == 2 ? 1024 : 512));
 #pragma unroll
     for (int sl = 0; sl < NSEL; ++sl) {
-      unsigned char* wb = sb + R::ACT + sl * R::WSEL;
-      if (WDT == WQ8) {
-        dma16(wdata(sl) + it * 32 + dhalf * 16, wb + wave * 1024);
-      } else if (wave < 2) {
-        dma16(wdata(sl) + it * 16, wb + wave * 1024);
+      const unsigned wb = sb + R::ACT + sl * R::WSEL;
+      if (WDT == WQ8 || wave < 2) {
+        dma16s(wdata(sl) + ub * wstride, woff, wb + wave * 1024);
       } else {
-        dma4(wscal(sl) + it, wb + 2048 + (wave - 2) * 256);
+        dma4s((const unsigned char*)wscal(sl) + ub * sstride, soff, wb + 2048 + (wave - 2) * 256);
       }
     }
     if (BLOCKX && lane < TT / 4)
-      dma4(a.xd + (int64_t)blk * a.Tpad + t0 + wave * (TT / 4) + lane, sb + R::ACT + NSEL * R::WSEL + wave * TT);
+      dma4s((const unsigned char*)a.xd + ub * dstride, doff, sb + R::ACT + NSEL * R::WSEL + wave * TT);
   };
 
   v16i iacc[NSEL][MT][2];
@@ -1080,15 +1102,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
         }
       }
       __builtin_amdgcn_sched_barrier(0);  // every fragment read of the group ahead of its MFMAs
+      if (b + KB <= nb) {
 #pragma unroll
-      for (int k = 0; k < KB; ++k) {
-        const bool ok = b + k < nb;  // uniform; a block past the last adds zero
+        for (int k = 0; k < KB; ++k)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const v4i a4 = ok ? A[k][mt] : v4i{0, 0, 0, 0};
+          for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
-            iacc[0][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, B[k][nt], iacc[0][mt][nt], 0, 0, 0);
+            for (int nt = 0; nt < 2; ++nt)
+              iacc[0][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[k][mt], B[k][nt], iacc[0][mt][nt], 0, 0, 0);
+      } else {  // the last group: a block past the last (its slot repeats the last) adds zero
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+          const bool ok = b + k < nb;  // uniform
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const v4i a4 = ok ? A[k][mt] : v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+              iacc[0][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, B[k][nt], iacc[0][mt][nt], 0, 0, 0);
+          }
         }
       }
       cs = cs + KB < D ? cs + KB : cs + KB - D;
@@ -2004,6 +2036,11 @@ static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
   return hipGetLastError();
 }
 hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs& a, int total_tiles, hipStream_t s) {
+  // the ring GEMM addresses its DMA sources as a scalar base plus a 32-bit lane offset
+  const int64_t G = dtype == WQ8 ? 32 : 16, lim = int64_t(1) << 31;
+  if ((int64_t)a.Tpad * a.K >= lim) return hipErrorInvalidValue;
+  for (int i = 0; i < (swiglu ? 2 : a.n_targets); ++i)
+    if ((a.tg[i].N + kPadRows - 1) / kPadRows * (int64_t)kPadRows * a.nb * G >= lim) return hipErrorInvalidValue;
   if (dtype == WQ8) {
     if (token_mode) return swiglu ? gemm_go<WQ8, true, true>(a, total_tiles, s) : gemm_go<WQ8, false, true>(a, total_tiles, s);
     return swiglu ? gemm_go<WQ8, true, false>(a, total_tiles, s) : gemm_go<WQ8, false, false>(a, total_tiles, s);
