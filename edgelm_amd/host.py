@@ -214,6 +214,25 @@ class Session:
         n = _setup().elm_session_describe(self.h, buf, 4096)
         return n, buf.value.decode()
 
+    def greedy(self, tokens):
+        """Session::greedy: forward the tokens, then the argmax of the last logits row."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        nxt = C.c_int32()
+        L = _setup()
+        L.elm_session_greedy.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.POINTER(C.c_int32)]
+        if L.elm_session_greedy(self.h, tokens.ctypes.data, len(tokens), C.byref(nxt)):
+            raise RuntimeError(_err())
+        return nxt.value
+
+    def greedy_steps(self, first, n):
+        """Session::greedy_steps: n greedy decode steps from token `first`; the n tokens."""
+        out = np.empty(n, np.int32)
+        L = _setup()
+        L.elm_session_greedy_steps.argtypes = [C.c_void_p, C.c_int32, C.c_int, C.c_void_p]
+        if L.elm_session_greedy_steps(self.h, int(first), n, out.ctypes.data):
+            raise RuntimeError(_err())
+        return out
+
     def bench(self, prompt, warmup, steps):
         """bench.py's protocol (elm_session_bench): TTFT of the prompt, `warmup` untimed greedy decode steps,
         then `steps` timed ones."""

@@ -70,6 +70,13 @@ class Backend {
   // Optional: the argmax (edgelm's argmax, tokenizer.cpp:187-189) of the graph output's last row,
   // taken where the output lives; false if this backend cannot.
   virtual bool argmax_output(const ExecContext&, int32_t*) { return false; }
+  // Optional (default: false = not handled), for greedy decoding when this backend runs the whole
+  // graph as one partition and keeps its output: n decode steps at positions ctx.pos0 .. + n - 1,
+  // the first from token `first` and each later one from the argmax of the step before, fed back
+  // where the logits are, so the steps can be queued back to back; out[i] is step i's argmax.
+  virtual bool greedy_steps(const Partition&, ExecContext&, int32_t /*first*/, int /*n*/, int32_t* /*out*/) {
+    return false;
+  }
 };
 
 std::unique_ptr<Backend> make_reference_backend();

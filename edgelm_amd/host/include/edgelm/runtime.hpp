@@ -57,6 +57,11 @@ class Session {
   // then stay there), else on the host arena's copy as edgelm's bench does (main.cpp:199-213).
   int32_t greedy(const int32_t* tokens, int n);
   int32_t greedy_prefill(const std::vector<int32_t>& tokens);
+  // n greedy decode steps, the first from token `first`, each later one from the token the step
+  // before chose: the same tokens as n calls of greedy(&tok, 1). A backend that runs the whole graph
+  // and keeps the logits may queue the steps back to back (greedy_steps hook); tokens (may be null)
+  // gets all n, and the last one is returned.
+  int32_t greedy_steps(int32_t first, int n, int32_t* tokens);
   void reset() { pos_ = 0; }
   int pos() const { return pos_; }
 

@@ -230,6 +230,22 @@ int elm_session_describe(const elm_session* s, char* buf, int cap) {
   return static_cast<int>(s->s->graph().ops.size());
 }
 
+int elm_session_greedy(elm_session* s, const int32_t* tokens, int n, int32_t* next) {
+  return guard([&] {
+    if (!s || !tokens || n < 1 || !next) throw std::runtime_error("edgelm: bad greedy arguments");
+    *next = s->s->greedy(tokens, n);
+    return 0;
+  });
+}
+
+int elm_session_greedy_steps(elm_session* s, int32_t first, int n, int32_t* tokens) {
+  return guard([&] {
+    if (!s || n < 1 || !tokens) throw std::runtime_error("edgelm: bad greedy_steps arguments");
+    s->s->greedy_steps(first, n, tokens);
+    return 0;
+  });
+}
+
 int elm_session_bench(elm_session* s, const int32_t* prompt, int n_prompt, int warmup, int steps, double* ttft_ms,
                       double* decode_ms, int32_t* tokens_out) {
   return guard([&] {
@@ -240,16 +256,10 @@ int elm_session_bench(elm_session* s, const int32_t* prompt, int n_prompt, int w
     int32_t tok = ss.greedy_prefill(std::vector<int32_t>(prompt, prompt + n_prompt));
     const auto t1 = std::chrono::steady_clock::now();
     if (tokens_out) tokens_out[0] = tok;
-    for (int i = 0; i < warmup; ++i) {
-      tok = ss.greedy(&tok, 1);
-      if (tokens_out) tokens_out[1 + i] = tok;
-    }
-    // every greedy step ends with its token id on the host, so the clock brackets finished work
+    if (warmup > 0) tok = ss.greedy_steps(tok, warmup, tokens_out ? tokens_out + 1 : nullptr);
+    // greedy_steps returns with every step's token id on the host, so the clock brackets finished work
     const auto t2 = std::chrono::steady_clock::now();
-    for (int i = 0; i < steps; ++i) {
-      tok = ss.greedy(&tok, 1);
-      if (tokens_out) tokens_out[1 + warmup + i] = tok;
-    }
+    tok = ss.greedy_steps(tok, steps, tokens_out ? tokens_out + 1 + warmup : nullptr);
     const auto t3 = std::chrono::steady_clock::now();
     *ttft_ms = ms_between(t0, t1);
     *decode_ms = ms_between(t2, t3);
@@ -269,10 +279,7 @@ int elm_session_generate(elm_session* s, const int32_t* prompt, int n_prompt, in
     const auto t1 = std::chrono::steady_clock::now();
     const auto t2 = t1;
     if (tokens_out) tokens_out[0] = tok;
-    for (int i = 0; i < gen; ++i) {
-      tok = ss.greedy(&tok, 1);
-      if (tokens_out) tokens_out[i + 1] = tok;
-    }
+    if (gen > 0) tok = ss.greedy_steps(tok, gen, tokens_out ? tokens_out + 1 : nullptr);
     const auto t3 = std::chrono::steady_clock::now();
     *prefill_ms = ms_between(t0, t1);
     *ttft_ms = ms_between(t0, t2);

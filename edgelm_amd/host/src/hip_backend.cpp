@@ -314,7 +314,88 @@ class HipBackend : public Backend {
     return true;
   }
 
+  // Greedy decode steps queued back to back: once the step graph is captured, each step's argmax is
+  // written straight into the token-id buffer the next step's EMBED reads, the position goes up from
+  // a pinned slot, and the token ids come back asynchronously; the host waits once per kStepRing
+  // steps (to reuse the position slots) and at the end. Until the graph exists, steps run one by one
+  // with their token on the host.
+  bool greedy_steps(const Partition& p, ExecContext& c, int32_t first, int n, int32_t* out) {  // overrides where Backend declares it
+    const Graph& g = *c.graph;
+    if (!graphs_on_ || !ctx_ || !prepared_ || !keep_out_ || output_ < 0 || g.input < 0 || c.L != 1 || n < 1 ||
+        p.begin != 0 || p.end != static_cast<int>(g.ops.size()))
+      return false;
+    for (size_t t = 0; t < host_needed_.size(); ++t)
+      if (host_needed_[t] && static_cast<int>(t) != output_) return false;  // another reader of an activation
+    const int pos0 = c.pos0;
+    int32_t tok = first;
+    int i = 0;
+    auto ready = [&]() {
+      auto it = graphs_.find(p.begin);
+      return it != graphs_.end() && it->second.exec && !it->second.eager &&
+             it->second.scratch_gen == elmh_scratch_generation(ctx_);
+    };
+    for (; i < n && !ready(); ++i) {  // one by one: warm-up, capture
+      std::memcpy(c.f(g.input), &tok, sizeof tok);
+      c.T = 1;
+      c.pos0 = pos0 + i;
+      if (!run_partition(p, c))
+        for (int k = p.begin; k < p.end; ++k) run(g.ops[k], c);
+      if (!argmax_output(c, &tok)) throw std::runtime_error("edgelm: hip greedy: the logits are not on the device");
+      out[i] = tok;
+    }
+    if (i == n) return true;
+    StepGraph& sg = graphs_[p.begin];
+    const size_t need = kStepRing + 1 + static_cast<size_t>(n);
+    if (step_pin_cap_ < need) {
+      wait_all();
+      elmh_host_free(ctx_, step_pin_);
+      step_pin_ = nullptr;
+      step_pin_cap_ = 0;
+      if (elmh_host_alloc(ctx_, need * sizeof(int32_t), reinterpret_cast<void**>(&step_pin_)) != ELMH_OK)
+        throw std::runtime_error(std::string("edgelm: hip pinned staging: ") + elmh_last_error(ctx_));
+      step_pin_cap_ = need;
+    }
+    int32_t* const pos_ring = step_pin_;                 // [kStepRing] positions
+    int32_t* const toks = step_pin_ + kStepRing + 1;      // [n] token ids, step_pin_[kStepRing]: the first
+    int32_t* const d_tok = static_cast<int32_t*>(act_[g.input].p);  // the EMBED's token ids
+    const int64_t V = c.tensor(output_).cols;
+    const float* const logits = static_cast<const float*>(act_[output_].p);
+    auto ok = [&](int rc) {
+      if (rc != ELMH_OK) throw std::runtime_error(std::string("edgelm: hip greedy steps: ") + elmh_last_error(ctx_));
+    };
+    wait_all();  // earlier copies out of the staging buffers are done
+    const int i0 = i;
+    step_pin_[kStepRing] = tok;
+    ok(elmh_memcpy_h2d_async(ctx_, d_tok, step_pin_ + kStepRing, sizeof(int32_t)));
+    for (int s = 0; i < n; ++i, ++s) {
+      c.pos0 = pos0 + i;
+      for (int k = p.begin; k < p.end; ++k) {  // run()'s position checks for a replayed step
+        const Op& op = g.ops[k];
+        if (op.type == OpType::ATTENTION) {
+          EDGELM_CHECK(c.pos0 + 1 <= c.kv[op.iattr[0]].max_ctx, "context overflow");
+          EDGELM_CHECK(!op.iattr[3] || c.pos0 + 1 <= rope_pos_, "position beyond rope table");
+        }
+      }
+      if (s == kStepRing) {  // every slot has been copied from: reuse them
+        ok(elmh_synchronize(ctx_));
+        s = 0;
+      }
+      pos_ring[s] = c.pos0;
+      ok(elmh_memcpy_h2d_async(ctx_, pos_dev_, pos_ring + s, sizeof(int32_t)));
+      ok(elmh_graph_launch(ctx_, sg.exec));
+      ok(elmh_argmax_dev(ctx_, logits, 1, V, d_tok));  // the next step's token, where its EMBED reads it
+      ok(elmh_memcpy_d2h_async(ctx_, toks + i, d_tok, sizeof(int32_t)));
+    }
+    ok(elmh_synchronize(ctx_));
+    std::memcpy(out + i0, toks + i0, sizeof(int32_t) * static_cast<size_t>(n - i0));
+    return true;
+  }
+
  private:
+  static constexpr int kStepRing = 64;
+  int32_t* step_pin_ = nullptr;  // pinned: kStepRing positions, the first token, then the token ids
+  size_t step_pin_cap_ = 0;
+
   bool to_host(int t) const { return host_needed_[t] && !(keep_out_ && t == output_); }
 
   // Host <-> device transfers of activations go through pinned staging buffers, one per tensor, as
@@ -383,6 +464,9 @@ class HipBackend : public Backend {
     pin_.clear();
     elmh_host_free(ctx_, pin_pos_.p);
     pin_pos_ = Pin{};
+    elmh_host_free(ctx_, step_pin_);
+    step_pin_ = nullptr;
+    step_pin_cap_ = 0;
   }
   struct Buf {
     void* p = nullptr;

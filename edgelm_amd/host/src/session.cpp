@@ -108,6 +108,31 @@ int32_t Session::greedy(const int32_t* tokens, int n) {
   return argmax(logits + static_cast<size_t>(ctx_.L - 1) * static_cast<size_t>(vocab), static_cast<int>(vocab));
 }
 
+int32_t Session::greedy_steps(int32_t first, int n, int32_t* tokens) {
+  if (n < 1) throw std::runtime_error("edgelm: greedy_steps takes n >= 1");
+  if (pos_ + n > opt_.max_ctx) throw std::runtime_error("edgelm: the context is full");
+  std::vector<int32_t> own;
+  if (!tokens) own.resize(static_cast<size_t>(n));
+  int32_t* out = tokens ? tokens : own.data();
+  Backend* b = output_backend_;
+  if (parts_.size() == 1 && parts_[0].backend == b && b->keep_output(true)) {
+    struct Release {
+      Backend* b;
+      ~Release() { b->keep_output(false); }
+    } release{b};
+    ctx_.T = 1;
+    ctx_.L = 1;
+    ctx_.pos0 = pos_;
+    if (b->greedy_steps(parts_[0], ctx_, first, n, out)) {
+      pos_ += n;
+      return out[n - 1];
+    }
+  }
+  int32_t tok = first;
+  for (int i = 0; i < n; ++i) out[i] = tok = greedy(&tok, 1);
+  return tok;
+}
+
 int32_t Session::greedy_prefill(const std::vector<int32_t>& tokens) {
   if (tokens.empty()) throw std::runtime_error("edgelm: prefill of an empty prompt");
   const size_t chunk = static_cast<size_t>(opt_.max_batch), tail = (tokens.size() - 1) / chunk * chunk;

@@ -83,9 +83,15 @@ int elm_session_describe(const elm_session* s, char* buf, int cap);
  * generated token ids (first one from the prefill). Each argmax is taken where the logits are
  * (Session::greedy: on the device when a hip backend writes them), so the first one is part of the
  * prefill's last step and prefill ms equals TTFT ms. */
+/* Session::greedy: forward n tokens and take the argmax of the last logits row (where the logits are). */
+int elm_session_greedy(elm_session* s, const int32_t* tokens, int n, int32_t* next);
+/* Session::greedy_steps: n greedy decode steps from token `first` (the same tokens as n greedy calls,
+ * fed back on the device where the hip backend runs the whole graph); tokens gets all n. */
+int elm_session_greedy_steps(elm_session* s, int32_t first, int n, int32_t* tokens);
 /* bench.py's protocol on one session: reset, prefill the prompt and take its greedy token (TTFT), run
- * `warmup` untimed greedy decode steps, then time exactly `steps` more (decode_ms). Every step ends when
- * its token id is on the host. tokens_out (optional) gets the 1 + warmup + steps greedy tokens. */
+ * `warmup` untimed greedy decode steps, then time exactly `steps` more (decode_ms), both through
+ * Session::greedy_steps: the clock stops once every step's token id is on the host. tokens_out
+ * (optional) gets the 1 + warmup + steps greedy tokens. */
 int elm_session_bench(elm_session* s, const int32_t* prompt, int n_prompt, int warmup, int steps, double* ttft_ms,
                       double* decode_ms, int32_t* tokens_out);
 int elm_session_generate(elm_session* s, const int32_t* prompt, int n_prompt, int gen, double* prefill_ms,

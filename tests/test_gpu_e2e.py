@@ -160,3 +160,30 @@ def test_decode_graphs_survive_larger_forwards(tiny, dt):
         a, b = mine.forward(toks), ref.forward(toks)
         assert bits_equal(a, b), f"step {step} ({what}): max diff {np.abs(a - b).max()}"
     mine.close(), ref.close()
+
+
+@pytest.mark.parametrize("backends", ["hip,cpu", "hip-matmul,cpu"])
+def test_greedy_steps_match_edgelm(smollm, backends):
+    """Session::greedy_steps: with "hip,cpu" the steps are queued back to back, each one's token fed to the
+    next on the device (more steps than the backend's ring of position slots); "hip-matmul,cpu" takes the
+    one-by-one path. The tokens are edgelm's (its own session and argmax), and the session carries on
+    exactly where they leave it: the next forward's logits are bit-identical to edgelm's."""
+    prompt = S.lcg_prompt(128, 49152)
+    n = 100
+    m = host.Model(smollm)
+    s = host.Session(m, backends, threads=8, max_ctx=240, max_batch=128, act_quant=True)
+    ref = O.RefSession(smollm, "cpu", threads=16, max_ctx=240, max_batch=128, act_quant=True)
+    print(f"[gpu] greedy_steps {backends} n={n}", flush=True)
+    first = s.greedy(prompt)
+    lg = ref.forward(prompt)
+    want = [int(O.rq_argmax(lg[-1])[0])]
+    assert first == want[0]
+    got = s.greedy_steps(first, n).tolist()
+    for _ in range(n):
+        want.append(int(O.rq_argmax(ref.forward(np.array([want[-1]], np.int32))[-1])[0]))
+    assert got == want[1:]
+    assert s.pos() == 128 + n
+    a = s.forward(np.array([got[-1]], np.int32))
+    b = ref.forward(np.array([want[-1]], np.int32))
+    assert bits_equal(a, b)
+    s.close(), ref.close()
