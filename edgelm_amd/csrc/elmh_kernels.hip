@@ -902,15 +902,18 @@ struct GemmRing {
   static constexpr int WSEL = WDT == WQ8 ? kGemmTileN * 32 : kGemmTileN * 20;  // q8 [2][128][16]; q4 [128][16] + [128] f32
   static constexpr int XD = BLOCKX ? TT * 4 : 0;
   static constexpr int SLOT = ACT + NSEL * WSEL + XD;
-  static constexpr int D = (76 * 1024) / SLOT < 4 ? 4 : (76 * 1024) / SLOT;  // ring depth
+  // ring depth: whole block groups in the per-token q8 loop (KB below), one block otherwise
+  static constexpr int KBQ = TOK && WDT == WQ8 && !SW && KBO == 0 ? (MT == 1 ? 4 : 2) : (KBO ? KBO : 1);
+  static constexpr int D0 = (76 * 1024) / SLOT < 4 ? 4 : (76 * 1024) / SLOT;
+  static constexpr int D = KBQ > 1 ? D0 / KBQ * KBQ : D0;
   static constexpr int P = 1 + NSEL + (BLOCKX ? 1 : 0);                        // DMA instructions per wave per slot
   // blocks per barrier: the per-token q8 loop is a few MFMAs per block, so its barrier, fragment
-  // reads and DMA issues are grouped over KB blocks (the ring then runs D - 2 KB blocks ahead)
+  // reads and DMA issues are grouped over KB blocks, and the ring holds whole groups
   static constexpr int KB = KBO ? KBO : TOK && WDT == WQ8 && !SW ? (MT == 1 ? 4 : 2) : 1;
-  static_assert(D >= 2 * KB + 1, "ring too shallow for the block group");
+  static_assert(D >= 2 * KB + 1 || (KB > 1 && D >= 3 * KB), "ring too shallow for the block group");
   static constexpr int EP = SW ? 4 * 2 * 32 * 32 * 4 : 16;                     // SwiGLU epilogue: gate and up per wave
   static constexpr int BYTES = D * SLOT > EP ? D * SLOT : EP;
-  static_assert((D - 2 * KB) * P < 64, "vmcnt range");
+  static_assert((D - KB) * P < 64, "vmcnt range");
 };
 
 template <int WDT, bool SW, bool TOK, bool FAST, int MT, int KBO = 0>
@@ -1073,58 +1076,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
       is = is + 1 == D ? 0 : is + 1;
     }
   } else {
-    // per-token q8: block j lives in slot j % D; a group computes blocks b .. b + KB - 1 after
-    // refilling the slots the previous group read. Fragments of the whole group are read before
-    // its MFMAs; blocks past the last (their slots repeat it) are read but add zero.
+    // per-token q8, software-pipelined over groups of KB blocks (block j in slot j % D; D is a
+    // multiple of KB). Step g multiplies group g from registers while it reads group g + 1's
+    // fragments and refills group g's slots with group g + D / KB, interleaved so that the DMA
+    // issue, the LDS reads and the MFMAs of one wave overlap. Group g was read into registers in
+    // step g - 1, before the barrier at the top of step g, so its slots are free; group g + 1 has
+    // landed once at most D - 2 KB blocks are in flight. Blocks past the last (their slots repeat it)
+    // are read but add zero.
     constexpr int KB = R::KB;
+    static_assert(D % KB == 0, "the ring holds whole groups");
+    auto read_group = [&](v4i (&A)[KB][MT], v4i (&B)[KB][2], int blk0, int k) {
+      const unsigned char* sb = ring + ((blk0 % D) + k) * R::SLOT;
 #pragma unroll
-    for (int i = 0; i < D - KB; ++i) issue(i, i);
-    int cs = 0, is = D - KB;
-    for (int b = 0; b < nb; b += KB) {
-      wait_vm<(D - 2 * KB) * R::P>();  // this wave's parts of blocks b .. b + KB - 1 have landed
-      lds_barrier();                   // every wave's have; every wave is done with the last group
+      for (int mt = 0; mt < MT; ++mt) A[k][mt] = *reinterpret_cast<const v4i*>(sb + ((wt * MT + mt) * 64 + lane) * 16);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int rl = wr * 64 + nt * 32 + l32;
+        B[k][nt] = *reinterpret_cast<const v4i*>(sb + R::ACT + (2 * rl + (h ^ ((rl >> 3) & 1))) * 16);
+      }
+    };
+    auto step = [&](v4i (&A)[KB][MT], v4i (&B)[KB][2], v4i (&A2)[KB][MT], v4i (&B2)[KB][2], int b) {
+      wait_vm<(D - 2 * KB) * R::P>();  // group b + KB has landed (this wave's part)
+      lds_barrier();                   // every wave's part; every wave holds group b in registers
+      const bool full = b + KB <= nb;  // uniform
 #pragma unroll
       for (int k = 0; k < KB; ++k) {
-        issue(b + D - KB + k, is);
-        is = is + 1 == D ? 0 : is + 1;
-      }
-      v4i A[KB][MT], B[KB][2];
+        const bool ok = full || b + k < nb;
 #pragma unroll
-      for (int k = 0; k < KB; ++k) {
-        const int sl = cs + k < D ? cs + k : cs + k - D;
-        const unsigned char* sb = ring + sl * R::SLOT;
+        for (int mt = 0; mt < MT; ++mt) {
+          const v4i a4 = ok ? A[k][mt] : v4i{0, 0, 0, 0};
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) A[k][mt] = *reinterpret_cast<const v4i*>(sb + ((wt * MT + mt) * 64 + lane) * 16);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const int rl = wr * 64 + nt * 32 + l32;
-          B[k][nt] = *reinterpret_cast<const v4i*>(sb + R::ACT + (2 * rl + (h ^ ((rl >> 3) & 1))) * 16);
+          for (int nt = 0; nt < 2; ++nt)
+            iacc[0][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, B[k][nt], iacc[0][mt][nt], 0, 0, 0);
         }
+        read_group(A2, B2, b + KB, k);
+        issue(b + D + k, (b % D) + k);
+        __builtin_amdgcn_sched_barrier(0);  // keep the MFMAs, reads and DMA of block k together
       }
-      __builtin_amdgcn_sched_barrier(0);  // every fragment read of the group ahead of its MFMAs
-      if (b + KB <= nb) {
+    };
 #pragma unroll
-        for (int k = 0; k < KB; ++k)
+    for (int i = 0; i < D; ++i) issue(i, i);
+    wait_vm<(D - KB) * R::P>();  // group 0 has landed
+    lds_barrier();
+    v4i A0[KB][MT], B0[KB][2], A1[KB][MT], B1[KB][2];
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-              iacc[0][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[k][mt], B[k][nt], iacc[0][mt][nt], 0, 0, 0);
-      } else {  // the last group: a block past the last (its slot repeats the last) adds zero
-#pragma unroll
-        for (int k = 0; k < KB; ++k) {
-          const bool ok = b + k < nb;  // uniform
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const v4i a4 = ok ? A[k][mt] : v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-              iacc[0][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, B[k][nt], iacc[0][mt][nt], 0, 0, 0);
-          }
-        }
-      }
-      cs = cs + KB < D ? cs + KB : cs + KB - D;
+    for (int k = 0; k < KB; ++k) read_group(A0, B0, 0, k);
+    int b = 0;
+    for (; b + KB < nb; b += 2 * KB) {
+      step(A0, B0, A1, B1, b);
+      step(A1, B1, A0, B0, b + KB);
     }
+    if (b < nb) step(A0, B0, A1, B1, b);
   }
   wait_vm<0>();  // the repeated last-block issues have landed before the ring is reused or freed
   lds_barrier();
