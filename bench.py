@@ -331,7 +331,9 @@ def e2e_headline(path, steps, warmup, P=128):
     this build's Session with backends "hip,cpu" (the whole model on the GPU, decode steps replayed as HIP
     graphs, greedy argmax on the device): edgelm's bench protocol (main.cpp:173-233) with the LCG prompt of P
     tokens; after a warm-up rep, one timed rep: TTFT of the prompt, `warmup` untimed decode steps, then exactly
-    `steps` timed greedy decode steps (each ends with its token id on the host)."""
+    `steps` timed greedy decode steps queued back to back (Session::greedy_steps: each step's token id goes
+    from the device argmax into the next step on the device and is copied back asynchronously; the clock stops
+    once every token id is on the host)."""
     from edgelm_amd import synth as S
     from edgelm_amd import host
     prompt = S.lcg_prompt(P, 49152)
@@ -633,7 +635,8 @@ def main():
                                "int8 activations), backends hip,cpu, 128-token prompt then greedy decode; a step is one "
                                "token", "parallelism": "single GPU",
                    "timing": "eager launches (kernel-trace mode; step rate host-bound)" if args.eager else
-                             "host clock around exactly `steps` greedy steps, each ending with its token on the host"},
+                             "host clock around exactly `steps` greedy steps queued back to back; stops once every "
+                             "step's token id is on the host"},
         "roofline": roof, "cpu_baseline": cpu, "e2e_smollm2_w4a8": head, **extra,
     }
     print(json.dumps(line))

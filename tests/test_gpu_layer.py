@@ -111,6 +111,50 @@ def test_attention_long_cache_decode_steps(ctx, rope):
         b.free()
 
 
+@pytest.mark.parametrize("rope", [False, True])
+def test_attention_decode_steps_across_row_chunks(ctx, rope):
+    """Decode steps (position in device memory) of the head-size-64 decode kernel, which moves the cached
+    rows into LDS 256 at a time: the first position, positions on both sides of 256 and 512 cached rows
+    (one and several chunks of keys and values) and the cache's last position. Rows past the step's
+    position hold NaN: the kernel reads such rows ahead and must never use them."""
+    nh, nkv, hd, mc = 9, 3, 64, 1100
+    r = np.random.default_rng(91 + int(rope))
+    tab = O.rope_table(hd, mc, 100000.0) if rope else None
+    kc = np.full((nkv, mc, hd), np.nan, np.float32)
+    vc = np.full_like(kc, np.nan)
+    bkc, bvc = dev(ctx, kc), dev(ctx, vc)
+    bcos, bsin = (dev(ctx, tab[0]), dev(ctx, tab[1])) if rope else (None, None)
+    bpos = ctx.buffer(4)
+    pos = 0
+    plan = [(1, True), (1, True), (253, False)] + [(1, True)] * 5 + [(250, False)] + [(1, True)] * 4 + \
+           [(585, False), (1, True)]
+    for T, step in plan:
+        print(f"[gpu] chunked decode attention rope={rope} pos0={pos} T={T} step={step}", flush=True)
+        q = r.normal(0, 1, (T, nh * hd)).astype(np.float32)
+        k = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+        v = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+        bq, bk, bv, bo = dev(ctx, q), dev(ctx, k), dev(ctx, v), ctx.buffer(q.nbytes)
+        if step:
+            bpos.upload(np.array([pos], np.int32))
+            ctx.attention_step_dev(bq.ptr, bk.ptr, bv.ptr, bo.ptr, bpos.ptr, nh, nkv, hd, bkc.ptr, bvc.ptr, mc,
+                                   bcos.ptr if rope else None, bsin.ptr if rope else None)
+        else:
+            ctx.attention_dev(bq.ptr, bk.ptr, bv.ptr, bo.ptr, T, pos, nh, nkv, hd, bkc.ptr, bvc.ptr, mc,
+                              bcos.ptr if rope else None, bsin.ptr if rope else None)
+        want = O.attention(q, k, v, pos, nh, nkv, kc, vc, tab)
+        got = bo.download(q.shape, np.float32)
+        assert not np.isnan(got).any(), f"pos0={pos} T={T}"
+        assert bits_equal(got, want), f"pos0={pos} T={T}"
+        for b in (bq, bk, bv, bo):
+            b.free()
+        pos += T
+    assert pos == mc
+    assert bits_equal(bkc.download(kc.shape, np.float32), kc)
+    assert bits_equal(bvc.download(vc.shape, np.float32), vc)
+    for b in [bkc, bvc, bpos] + ([bcos, bsin] if rope else []):
+        b.free()
+
+
 FUSED_ATTN = [(9, 3, 64, 300, (128, 1, 33, 7, 3)), (4, 4, 32, 64, (17, 5))]
 
 
