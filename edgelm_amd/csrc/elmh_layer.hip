@@ -809,6 +809,181 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(const float* __r
   }
 }
 
+// Prefill (T > 1, head size 64) with the cached rows moved into LDS by DMA, as the decode kernel
+// does: one 256-thread workgroup per (head, kAttnQ consecutive query tokens), wave w for query
+// t0 + w; the same float operations in the same order as attention_prefill_kernel. Keys and
+// values of positions [0, nmax) (nmax: the group's last query's positions) go to LDS kPfRows rows
+// at a time: thread j scores row j against the group's queries; then each wave takes its own
+// query's max, exponentials, in-order sum (ordered_sum256) and p_j = e_j * inv, and adds
+// p_j * v_j[lane] over the value rows in increasing j. Longer prompts pass through the buffers a
+// chunk at a time (keys through the key buffer; values alternating, the next chunk in flight).
+// LDS (dynamic): keys [kPfRows][64] (chunk u of row r in slot u ^ (r & 15)), values [kPfRows][64],
+// scores [kAttnQ][n_cap rounded up to 256], q [kAttnQ][64].
+constexpr int kPfRows = 128;
+
+__global__ __launch_bounds__(256) void attention_prefill64_kernel(
+    const float* __restrict__ q, float* __restrict__ out, const float* __restrict__ kc, const float* __restrict__ vc,
+    int pos0, int T, int n_heads, int n_kv, int max_ctx, int n_cap, const float* __restrict__ rcos,
+    const float* __restrict__ rsin, int8_t* __restrict__ xq, float* __restrict__ xd, int Tpad) {
+  constexpr int HD = 64, H2 = 32, R = kPfRows, ROWB = HD * 4;
+  extern __shared__ __align__(16) float lds[];
+  const int scs = (n_cap + 255) & ~255;  // score row stride
+  float* const kb = lds;                 // [R][64]
+  float* const vb = kb + R * HD;         // [R][64]
+  float* const sc = vb + R * HD;         // [kAttnQ][scs]
+  float* const qb = sc + kAttnQ * scs;   // [kAttnQ][64]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int ngr = (T + kAttnQ - 1) / kAttnQ;
+  const int h = blockIdx.x / ngr, t0 = (blockIdx.x - h * ngr) * kAttnQ;
+  const int nq = min(kAttnQ, T - t0);                                   // queries in this group
+  const int tw = t0 + min(w, nq - 1), posw = pos0 + tw, nw = posw + 1;  // this wave's query
+  const int nmax = pos0 + t0 + nq;                                      // the group's positions
+  const int qd = n_heads * HD, grp = n_heads / n_kv, kvh = h / grp;
+  const float* const kh = kc + (int64_t)kvh * max_ctx * HD;
+  const float* const vh = vc + (int64_t)kvh * max_ctx * HD;
+  const unsigned kb_lds = (unsigned)(size_t)(LdsBytes)(unsigned char*)kb;
+  const unsigned vb_lds = (unsigned)(size_t)(LdsBytes)(unsigned char*)vb;
+  // rows [c0, c0 + rows) of a cache into a buffer: wave w moves 1 KB pieces w, w + 4, ... (4 rows
+  // each, lane -> row lane / 16, slot lane % 16); the last piece repeats the last row
+  auto dma_rows = [&](const float* base, int c0, int rows, unsigned dst, bool swz) {
+    for (int pc = w; 4 * pc < rows; pc += 4) {
+      const int r = 4 * pc + (lane >> 4), s = lane & 15;
+      dma16s(base, (uint32_t)((c0 + min(r, rows - 1)) * ROWB + ((swz ? s ^ (r & 15) : s) << 4)), dst + pc * 1024);
+    }
+  };
+  dma_rows(kh, 0, min(R, nmax), kb_lds, true);
+  // q of the wave's query, rotated, into LDS
+  {
+    const float* const qs = q + (int64_t)tw * qd + h * HD;
+    const int ih = lane & (H2 - 1);
+    const float a = qs[ih], b = qs[ih + H2];
+    float c = 0.f, sn = 0.f;
+    if (rcos) {
+      c = rcos[(int64_t)posw * H2 + ih];
+      sn = rsin[(int64_t)posw * H2 + ih];
+    }
+    wait_vm<0>();  // the keys, q, cos / sin
+    if (lane < H2) {
+      qb[w * HD + lane] = rcos ? a * c - b * sn : a;
+      qb[w * HD + lane + H2] = rcos ? b * c + a * sn : b;
+    }
+  }
+  dma_rows(vh, 0, min(R, nmax), vb_lds, false);
+  lds_barrier();  // keys (every wave waited for its own) and the queries in LDS
+
+  // scores: thread j takes row j of each chunk of R positions, against every query of the group
+  // that sees it
+  const float scale = 1.0f / sqrtf((float)HD);
+  for (int c0 = 0; c0 < nmax; c0 += R) {
+    if (c0 > 0) {  // the next key chunk, once every thread has scored the previous one
+      __syncthreads();
+      dma_rows(kh, c0, min(R, nmax - c0), kb_lds, true);
+      wait_vm<0>();
+      lds_barrier();
+    }
+    const int j = c0 + tid;
+    if (tid < R && j < nmax) {
+      const float* const row = kb + tid * HD;
+      const int sw = tid & 15;
+      float4 kv[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) kv[u] = *reinterpret_cast<const float4*>(row + ((u ^ sw) << 2));
+#pragma unroll
+      for (int qi = 0; qi < kAttnQ; ++qi) {
+        if (qi < nq && j <= pos0 + t0 + qi) {
+          const float* const qq = qb + qi * HD;
+          float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+          for (int u = 0; u < 16; ++u) {
+            s0 = s0 + qq[4 * u] * kv[u].x;
+            s1 = s1 + qq[4 * u + 1] * kv[u].y;
+            s2 = s2 + qq[4 * u + 2] * kv[u].z;
+            s3 = s3 + qq[4 * u + 3] * kv[u].w;
+          }
+          sc[qi * scs + j] = ((s0 + s1) + (s2 + s3)) * scale;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // per wave (query): max, exponentials (+0.0 past the last position, to a multiple of 16), the
+  // in-order sum, p_j = e_j * inv
+  float* const sw = sc + w * scs;
+  float mx = -INFINITY;
+  for (int j = lane; j < nw; j += 64) mx = fmaxf(mx, sw[j]);
+  mx = wave_max(mx);
+  const int n16 = (nw + 15) & ~15;
+  for (int j = lane; j < n16; j += 64) sw[j] = j < nw ? elm_expf(sw[j] - mx) : 0.f;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  float sum = 0.f;
+  for (int g0 = 0; g0 < n16; g0 += 256) sum = ordered_sum256(sw + g0, min(16, (n16 - g0) >> 4), sum);
+  const float inv = 1.0f / sum;
+  __builtin_amdgcn_wave_barrier();
+  for (int j = lane; j < n16; j += 64) sw[j] = sw[j] * inv;
+  wait_vm<0>();  // this wave's value rows
+  __syncthreads();  // every value row in LDS; every wave's p_j written
+
+  // o_i = 0, o_i += p_j * v_j[i] in increasing j (lane i), value chunks of R rows alternating
+  // between the two buffers, the next chunk in flight while the waves add the current one
+  float acc = 0.f;
+  for (int c0 = 0, ci = 0; c0 < nmax; c0 += R, ++ci) {
+    const float* const cur = (ci & 1) ? kb : vb;
+    const int nx = c0 + R;
+    if (nx < nmax) dma_rows(vh, nx, min(R, nmax - nx), (ci & 1) ? vb_lds : kb_lds, false);
+    const int m = min(R, nw - c0), nbt = max(m, 0) >> 4;  // this query's positions in the chunk
+    const float* const pj = sw + c0;
+    const float* const vcol = cur + lane;
+    float pa[16], xa[16], pb[16], xb[16];
+    auto load = [&](int bt, float (&pv)[16], float (&x)[16]) {
+      const int j0 = min(bt, nbt - 1) * 16;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        pv[u] = pj[j0 + u];
+        x[u] = vcol[(j0 + u) * HD];
+      }
+    };
+    auto fold = [&](const float (&pv)[16], const float (&x)[16]) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc = acc + pv[u] * x[u];
+    };
+    if (nbt > 0) {
+      load(0, pa, xa);
+      for (int bt = 0; bt < nbt; bt += 2) {
+        load(bt + 1, pb, xb);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(pa, xa);
+        if (bt + 1 < nbt) {
+          load(bt + 2, pa, xa);
+          __builtin_amdgcn_sched_barrier(0);
+          fold(pb, xb);
+        }
+      }
+    }
+    for (int j = nbt * 16; j < m; ++j) acc = acc + pj[j] * vcol[j * HD];
+    if (nx < nmax) {
+      wait_vm<0>();
+      __syncthreads();  // every wave is done with this chunk; the next one has landed
+    }
+  }
+  if (w < nq) {
+    out[(int64_t)tw * qd + h * HD + lane] = acc;
+    if (xq) {
+      // the next GEMM's activation fragments: lanes 0-31 hold block 2h of token tw, lanes 32-63
+      // block 2h + 1; scale = amax / 127 and edgelm's rounding, as act_quant_frag_kernel
+      float a = fmaxf(0.f, fabsf(acc));
+#pragma unroll
+      for (int k = 1; k < 32; k <<= 1) a = fmaxf(a, __shfl_xor(a, k, 64));
+      const float scl = a / 127.0f;
+      int qv;
+      elm_q8_group<1>(&acc, scl == 0.f ? 1.f : scl, &qv);
+      const int b = 2 * h + (lane >> 5), e = lane & 31;
+      xq[elm_frag_offset(tw, b, e >> 4, 2 * n_heads) + (e & 15)] = (int8_t)qv;
+      if (e == 0) xd[(int64_t)b * Tpad + tw] = scl;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- EMBED
 
 // y[t][k] = dequantize_row(table, tokens[t])[k] read from the repacked weight layout:
@@ -971,7 +1146,8 @@ size_t attention_lds_bytes(int hd, int n_max) {
 // the attention kernels keep a whole score row (and a chunk of values) in LDS: allow them up to kMaxAttnLds
 bool raise_lds_limit() {
   const void* kernels[] = {(const void*)attention_kernel<64>, (const void*)attention_kernel<0>,
-                           (const void*)attention_prefill_kernel, (const void*)attention_decode64_kernel};
+                           (const void*)attention_prefill_kernel, (const void*)attention_decode64_kernel,
+                           (const void*)attention_prefill64_kernel};
   for (const void* k : kernels) {
     hipFuncAttributes fa;
     if (hipFuncGetAttributes(&fa, k) != hipSuccess || fa.sharedSizeBytes + kMaxAttnLds > kMaxLds) return false;
@@ -997,8 +1173,19 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
   const float* kn = fuse ? k : nullptr;
   const float* vn = fuse ? v : nullptr;
   const size_t lds_pf = ((size_t)kAttnQ * hd + (size_t)kAttnQ * ((n_cap + 63) & ~63) + (size_t)kAttnPVPos * hd) * 4;
+  const size_t lds_pf64 = ((size_t)2 * kPfRows * 64 + (size_t)kAttnQ * ((n_cap + 255) & ~255) + (size_t)kAttnQ * 64) * 4;
   static const bool lds_ok = raise_lds_limit();  // once per process (the attribute holds for the kernel)
   if (!lds_ok) return hipErrorInvalidValue;
+  if (!fuse && hd == 64 && lds_pf64 <= kMaxAttnLds) {
+    const int ngr = (T + kAttnQ - 1) / kAttnQ;
+    const bool quant = xq && xd && quantized;
+    attention_prefill64_kernel<<<n_heads * ngr, 256, lds_pf64, s>>>(q, out, kc, vc, pos0, T, n_heads, n_kv, max_ctx,
+                                                                    n_cap, rcos, rsin, quant ? xq : nullptr,
+                                                                    quant ? xd : nullptr, Tpad);
+    const hipError_t e = hipGetLastError();
+    if (e == hipSuccess && quant) *quantized = true;
+    return e;
+  }
   if (!fuse && hd == 64 && lds_pf <= kMaxAttnLds) {
     const int ngr = (T + kAttnQ - 1) / kAttnQ;
     const bool quant = xq && xd && quantized;
