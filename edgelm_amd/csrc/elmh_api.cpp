@@ -60,6 +60,8 @@ struct elmh_ctx {
   unsigned char* noalloc = nullptr;
   // whether the last elmh_attention_matmul_dev call had the attention kernel write the GEMM's operand
   int attn_fused = 0;
+  // the one-row argmax's per-workgroup posts and counter (the counter zero between launches)
+  void* argmax_scratch = nullptr;
 };
 
 namespace {
@@ -566,6 +568,8 @@ struct DeviceGuard {
   explicit DeviceGuard(elmh_ctx* c) { (void)hipSetDevice(c->device); }
 };
 
+constexpr int kArgStepMaxN = 64 * 4096;  // launch_argmax_parts: 64 workgroups of 4096 values
+
 int check_attention(elmh_ctx* c, const float* q, const float* k, const float* v, const float* out, int T, int pos0,
                     int n_heads, int n_kv, int head_dim, const float* k_cache, const float* v_cache, int max_ctx,
                     const float* rope_cos, const float* rope_sin) {
@@ -627,6 +631,13 @@ int elmh_create(int device, elmh_ctx** out) {
     }
     c->noalloc = g_noalloc_ptr[device];
   }
+  if (hipMalloc(&c->argmax_scratch, argmax_parts_scratch_bytes()) != hipSuccess ||
+      hipMemset(c->argmax_scratch, 0, argmax_parts_scratch_bytes()) != hipSuccess) {
+    if (c->argmax_scratch) (void)hipFree(c->argmax_scratch);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return fail(nullptr, ELMH_ERR_HIP, "argmax scratch allocation failed on device %d", device);
+  }
   *out = c;
   return ELMH_OK;
 }
@@ -637,6 +648,7 @@ void elmh_destroy(elmh_ctx* c) {
   (void)hipStreamSynchronize(c->stream);
   for (DevBuf* b : {&c->x, &c->y, &c->res, &c->xq, &c->xd, &c->xs, &c->gu, &c->nrm})
     if (b->p) (void)hipFree(b->p);
+  if (c->argmax_scratch) (void)hipFree(c->argmax_scratch);
   (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -1043,7 +1055,22 @@ int elmh_argmax_dev(elmh_ctx* c, const float* x, int rows, int64_t n, int32_t* o
   if (rows < 1 || n < 1) return fail(c, ELMH_ERR_ARG, "argmax: rows and n must be >= 1 (rows=%d n=%lld)", rows, (long long)n);
   if (n > INT32_MAX) return fail(c, ELMH_ERR_ARG, "argmax: n=%lld exceeds int32 indices", (long long)n);
   DeviceGuard g(c);
-  HIP_OR_FAIL(c, launch_argmax(x, rows, n, out, c->stream));
+  if (rows == 1 && n <= kArgStepMaxN)  // one row (a decode step's logits): over several workgroups
+    HIP_OR_FAIL(c, launch_argmax_parts(x, n, out, nullptr, nullptr, 0, c->argmax_scratch, c->stream));
+  else
+    HIP_OR_FAIL(c, launch_argmax(x, rows, n, out, c->stream));
+  return ELMH_OK;
+}
+
+int elmh_argmax_step_dev(elmh_ctx* c, const float* x, int64_t n, int32_t* out, int32_t* pos_dev, int32_t* ring,
+                         int ring_len) {
+  if (!c || !x || !out || !pos_dev || !ring) return fail(c, ELMH_ERR_ARG, "argmax_step: null pointer");
+  if (n < 1 || n > kArgStepMaxN)
+    return fail(c, ELMH_ERR_ARG, "argmax_step: n=%lld outside 1 .. %d", (long long)n, kArgStepMaxN);
+  if (ring_len < 1 || (ring_len & (ring_len - 1)))
+    return fail(c, ELMH_ERR_ARG, "argmax_step: ring_len %d is not a power of two", ring_len);
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, launch_argmax_parts(x, n, out, pos_dev, ring, ring_len - 1, c->argmax_scratch, c->stream));
   return ELMH_OK;
 }
 

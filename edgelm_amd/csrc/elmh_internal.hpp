@@ -157,6 +157,12 @@ hipError_t launch_embed(const int32_t* tok, int T, const DevWeight& w, float* y,
 // dst[0, bytes) = value (a kernel: capturable in a HIP graph, unlike hipMemsetAsync)
 hipError_t launch_fill(void* dst, int value, size_t bytes, hipStream_t s);
 hipError_t launch_argmax(const float* x, int rows, int64_t n, int32_t* out, hipStream_t s);
+// one row's argmax over several workgroups (n <= 64 * 4096); with pos: ring[*pos & ring_mask] =
+// the index, then *pos + 1. scratch: argmax_parts_scratch_bytes(), its last word zero before the
+// first launch (each launch leaves it zero)
+size_t argmax_parts_scratch_bytes();
+hipError_t launch_argmax_parts(const float* x, int64_t n, int32_t* out, int32_t* pos, int32_t* ring, int ring_mask,
+                               void* scratch, hipStream_t s);
 // Test hook: S[t][n][b] for pre-quantized row-major activations.
 hipError_t launch_block_sums(const DevWeight& w, const int8_t* xq, int T, int32_t* S, hipStream_t s);
 

@@ -1112,6 +1112,114 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __rest
   }
 }
 
+// The argmax of one row over kArgPartMax workgroups at most: workgroup b scans the slice
+// [b S, (b + 1) S) by argmax_kernel's rule (the first candidate: the slice's first value that is
+// not NaN, or index 0; then only a strictly greater value) and posts its best; the last workgroup
+// to post (a device-scope counter) merges the posts with arg_pick, which no order of merging
+// changes, writes the index and clears the counter for the next launch. With `pos` given it also
+// feeds a greedy decode step on the device: ring[*pos & ring_mask] = index, then *pos + 1.
+namespace {
+
+constexpr int kArgPartThreads = 256;
+constexpr int kArgPartMax = 64;
+constexpr int kArgPartVF = 4;  // float4 per thread: slices of 4096 values
+
+__global__ __launch_bounds__(kArgPartThreads) void argmax_parts_kernel(const float* __restrict__ x, int n, int slice,
+                                                                       float* __restrict__ post_v,
+                                                                       int* __restrict__ post_i,
+                                                                       unsigned* __restrict__ counter,
+                                                                       int32_t* __restrict__ out, int32_t* __restrict__ pos,
+                                                                       int32_t* __restrict__ ring, int ring_mask) {
+  __shared__ float sv[kArgPartThreads / 64];
+  __shared__ int si[kArgPartThreads / 64];
+  __shared__ bool last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j0 = blockIdx.x * slice, j1 = min(n, j0 + slice);
+  float bv = 0.f;
+  int bi = -1;
+  auto scan = [&](float v, int j) {
+    const bool take = bi < 0 ? (v == v || j == 0) : v > bv;
+    bv = take ? v : bv;
+    bi = take ? j : bi;
+  };
+  // thread t takes float4 t, t + 256, ... of the slice (slices start on a multiple of 4), in
+  // increasing index; every load out before the first compare
+  const int q0 = j0 >> 2, nq = (j1 - j0) >> 2;
+  if (nq > 0) {  // loads past the slice's last float4 repeat it
+    float4 v[kArgPartVF];
+#pragma unroll
+    for (int u = 0; u < kArgPartVF; ++u) {
+      const float* p = x + 4 * (q0 + min(tid + u * kArgPartThreads, nq - 1));
+      v[u] = make_float4(p[0], p[1], p[2], p[3]);
+    }
+#pragma unroll
+    for (int u = 0; u < kArgPartVF; ++u) {
+      const int q = tid + u * kArgPartThreads;
+      if (q < nq) {
+        const int j = 4 * (q0 + q);
+        scan(v[u].x, j);
+        scan(v[u].y, j + 1);
+        scan(v[u].z, j + 2);
+        scan(v[u].w, j + 3);
+      }
+    }
+  }
+  for (int j = j0 + 4 * nq + tid; j < j1; j += kArgPartThreads) scan(x[j], j);  // the row's tail
+  ArgBest best{bv, bi};
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) best = arg_pick(best, ArgBest{__shfl_xor(best.v, off, 64), __shfl_xor(best.i, off, 64)});
+  if (lane == 0) {
+    sv[wave] = best.v;
+    si[wave] = best.i;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    ArgBest b{sv[0], si[0]};
+    for (int w = 1; w < kArgPartThreads / 64; ++w) b = arg_pick(b, ArgBest{sv[w], si[w]});
+    post_v[blockIdx.x] = b.v;
+    post_i[blockIdx.x] = b.i;
+    __threadfence();  // the post is visible device-wide before the count says so
+    last = atomicAdd(counter, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();  // every other workgroup's post, as counted
+  ArgBest b{0.f, -1};
+  if (tid < (int)gridDim.x) b = ArgBest{post_v[tid], post_i[tid]};
+  if (wave == 0) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) b = arg_pick(b, ArgBest{__shfl_xor(b.v, off, 64), __shfl_xor(b.i, off, 64)});
+    if (lane == 0) {
+      out[0] = b.i;  // n >= 1 and index 0 is always a candidate, so b.i >= 0
+      if (pos) {
+        const int p = pos[0];
+        ring[p & ring_mask] = b.i;
+        pos[0] = p + 1;
+      }
+      counter[0] = 0u;
+    }
+  }
+}
+
+}  // namespace
+
+size_t argmax_parts_scratch_bytes() { return kArgPartMax * (sizeof(float) + sizeof(int)) + sizeof(unsigned); }
+
+hipError_t launch_argmax_parts(const float* x, int64_t n, int32_t* out, int32_t* pos, int32_t* ring, int ring_mask,
+                               void* scratch, hipStream_t s) {
+  // slices of kArgPartThreads * kArgPartVF * 4 values at most, a multiple of 4, at most kArgPartMax of them
+  const int64_t per = (int64_t)kArgPartThreads * kArgPartVF * 4;
+  const int64_t parts = (n + per - 1) / per;
+  if (n < 1 || parts > kArgPartMax) return hipErrorInvalidValue;
+  const int slice = (int)((((n + parts - 1) / parts) + 3) & ~(int64_t)3);
+  float* post_v = static_cast<float*>(scratch);
+  int* post_i = reinterpret_cast<int*>(post_v + kArgPartMax);
+  unsigned* counter = reinterpret_cast<unsigned*>(post_i + kArgPartMax);
+  argmax_parts_kernel<<<(unsigned)((n + slice - 1) / slice), kArgPartThreads, 0, s>>>(
+      x, (int)n, slice, post_v, post_i, counter, out, pos, ring, ring_mask);
+  return hipGetLastError();
+}
+
 hipError_t launch_argmax(const float* x, int rows, int64_t n, int32_t* out, hipStream_t s) {
   argmax_kernel<<<rows, kArgThreads, 0, s>>>(x, n, out);
   return hipGetLastError();

@@ -301,6 +301,11 @@ class Context:
     def argmax_dev(self, x_ptr, rows, n, out_ptr):
         self._check(lib().elmh_argmax_dev(self.h, C.c_void_p(x_ptr), C.c_int(rows), C.c_int64(n), C.c_void_p(out_ptr)))
 
+    def argmax_step_dev(self, x_ptr, n, out_ptr, pos_ptr, ring_ptr, ring_len):
+        """elmh_argmax_step_dev: *out = argmax(x[:n]); ring[*pos % ring_len] = *out; *pos += 1 (device pointers)."""
+        self._check(lib().elmh_argmax_step_dev(self.h, C.c_void_p(x_ptr), C.c_int64(n), C.c_void_p(out_ptr),
+                                               C.c_void_p(pos_ptr), C.c_void_p(ring_ptr), C.c_int(ring_len)))
+
     def memcpy_d2d(self, dst_ptr, src_ptr, nbytes):
         self._check(lib().elmh_memcpy_d2d(self.h, C.c_void_p(dst_ptr), C.c_void_p(src_ptr), C.c_size_t(nbytes)))
 

@@ -64,6 +64,7 @@ class HipBackend : public Backend {
     elmh_free(ctx_, rope_cos_);
     elmh_free(ctx_, rope_sin_);
     elmh_free(ctx_, dev_tok_);
+    elmh_free(ctx_, step_ring_);
     release_pins();
     elmh_destroy(ctx_);
   }
@@ -314,11 +315,11 @@ class HipBackend : public Backend {
     return true;
   }
 
-  // Greedy decode steps queued back to back: once the step graph is captured, each step's argmax is
-  // written straight into the token-id buffer the next step's EMBED reads, the position goes up from
-  // a pinned slot, and the token ids come back asynchronously; the host waits once per kStepRing
-  // steps (to reuse the position slots) and at the end. Until the graph exists, steps run one by one
-  // with their token on the host.
+  // Greedy decode steps queued back to back: once the step graph is captured, each step is the
+  // graph's launch and one argmax launch, which writes the token id straight into the buffer the
+  // next step's EMBED reads, bumps the device position the next step's attention reads and keeps
+  // the id in a device ring; the host copies the ring back and waits once per kStepRing steps and
+  // at the end. Until the graph exists, steps run one by one with their token on the host.
   bool greedy_steps(const Partition& p, ExecContext& c, int32_t first, int n, int32_t* out) {  // overrides where Backend declares it
     const Graph& g = *c.graph;
     if (!graphs_on_ || !ctx_ || !prepared_ || !keep_out_ || output_ < 0 || g.input < 0 || c.L != 1 || n < 1 ||
@@ -345,7 +346,8 @@ class HipBackend : public Backend {
     }
     if (i == n) return true;
     StepGraph& sg = graphs_[p.begin];
-    const size_t need = kStepRing + 1 + static_cast<size_t>(n);
+    // pinned staging: the ring's copy [kStepRing], then the first replayed step's token and position
+    const size_t need = kStepRing + 2;
     if (step_pin_cap_ < need) {
       wait_all();
       elmh_host_free(ctx_, step_pin_);
@@ -355,19 +357,23 @@ class HipBackend : public Backend {
         throw std::runtime_error(std::string("edgelm: hip pinned staging: ") + elmh_last_error(ctx_));
       step_pin_cap_ = need;
     }
-    int32_t* const pos_ring = step_pin_;                 // [kStepRing] positions
-    int32_t* const toks = step_pin_ + kStepRing + 1;      // [n] token ids, step_pin_[kStepRing]: the first
+    if (!step_ring_ && elmh_malloc(ctx_, kStepRing * sizeof(int32_t), reinterpret_cast<void**>(&step_ring_)) != ELMH_OK)
+      throw std::runtime_error(std::string("edgelm: hip: ") + elmh_last_error(ctx_));
     int32_t* const d_tok = static_cast<int32_t*>(act_[g.input].p);  // the EMBED's token ids
     const int64_t V = c.tensor(output_).cols;
     const float* const logits = static_cast<const float*>(act_[output_].p);
     auto ok = [&](int rc) {
       if (rc != ELMH_OK) throw std::runtime_error(std::string("edgelm: hip greedy steps: ") + elmh_last_error(ctx_));
     };
-    wait_all();  // earlier copies out of the staging buffers are done
-    const int i0 = i;
+    wait_all();  // earlier copies out of the staging buffer are done
+    // the device carries the steps from here: each step's argmax writes the next step's token id
+    // where its EMBED reads it, bumps the position its attention reads, and leaves the id in a ring
+    // slot (position mod kStepRing) that the host collects every kStepRing steps
     step_pin_[kStepRing] = tok;
+    step_pin_[kStepRing + 1] = pos0 + i;
     ok(elmh_memcpy_h2d_async(ctx_, d_tok, step_pin_ + kStepRing, sizeof(int32_t)));
-    for (int s = 0; i < n; ++i, ++s) {
+    ok(elmh_memcpy_h2d_async(ctx_, pos_dev_, step_pin_ + kStepRing + 1, sizeof(int32_t)));
+    for (int done = i; i < n; ++i) {
       c.pos0 = pos0 + i;
       for (int k = p.begin; k < p.end; ++k) {  // run()'s position checks for a replayed step
         const Op& op = g.ops[k];
@@ -376,25 +382,23 @@ class HipBackend : public Backend {
           EDGELM_CHECK(!op.iattr[3] || c.pos0 + 1 <= rope_pos_, "position beyond rope table");
         }
       }
-      if (s == kStepRing) {  // every slot has been copied from: reuse them
-        ok(elmh_synchronize(ctx_));
-        s = 0;
-      }
-      pos_ring[s] = c.pos0;
-      ok(elmh_memcpy_h2d_async(ctx_, pos_dev_, pos_ring + s, sizeof(int32_t)));
       ok(elmh_graph_launch(ctx_, sg.exec));
-      ok(elmh_argmax_dev(ctx_, logits, 1, V, d_tok));  // the next step's token, where its EMBED reads it
-      ok(elmh_memcpy_d2h_async(ctx_, toks + i, d_tok, sizeof(int32_t)));
+      ok(elmh_argmax_step_dev(ctx_, logits, V, d_tok, pos_dev_, step_ring_, kStepRing));
+      if (i + 1 - done == kStepRing || i + 1 == n) {  // the ring holds every step since `done`
+        ok(elmh_memcpy_d2h_async(ctx_, step_pin_, step_ring_, kStepRing * sizeof(int32_t)));
+        ok(elmh_synchronize(ctx_));
+        for (int k = done; k <= i; ++k) out[k] = step_pin_[(pos0 + k) & (kStepRing - 1)];
+        done = i + 1;
+      }
     }
-    ok(elmh_synchronize(ctx_));
-    std::memcpy(out + i0, toks + i0, sizeof(int32_t) * static_cast<size_t>(n - i0));
     return true;
   }
 
  private:
-  static constexpr int kStepRing = 64;
-  int32_t* step_pin_ = nullptr;  // pinned: kStepRing positions, the first token, then the token ids
+  static constexpr int kStepRing = 64;  // a power of two
+  int32_t* step_pin_ = nullptr;  // pinned: the ring's copy, the first replayed step's token and position
   size_t step_pin_cap_ = 0;
+  int32_t* step_ring_ = nullptr;  // device: greedy steps' token ids by position mod kStepRing
 
   bool to_host(int t) const { return host_needed_[t] && !(keep_out_ && t == output_); }
 

@@ -208,6 +208,15 @@ int elmh_attention_step_supported(int head_dim, int max_ctx);
  * next token without copying the logits off the device. n >= 1. */
 int elmh_argmax_dev(elmh_ctx* ctx, const float* x, int rows, int64_t n, int32_t* out);
 
+/* One greedy decode step's tail on the device: *out = the argmax of the row x [n] (as
+ * elmh_argmax_dev), then ring[*pos_dev & (ring_len - 1)] = that index and *pos_dev += 1, so that the
+ * next step (its EMBED reading *out, its attention reading *pos_dev) follows with no host copy and the
+ * host collects the token ids from ring later. ring_len is a power of two; n <= 262144. No counterpart
+ * in edgelm: it is the device side of this build's greedy-steps hook (Session::greedy_steps). Calls on
+ * one context run in stream order (they share a small counter in the context). */
+int elmh_argmax_step_dev(elmh_ctx* ctx, const float* x, int64_t n, int32_t* out, int32_t* pos_dev, int32_t* ring,
+                         int ring_len);
+
 /* ---- test hooks ----
  * quantize_act_row on the device (host pointers; q [T,K], d [T,K/32]). */
 int elmh_quantize_act(elmh_ctx* ctx, const float* x, int T, int64_t K, int8_t* q, float* d);

@@ -7,6 +7,7 @@ import pytest
 
 import oracle as O
 from conftest import bits_equal
+from edgelm_amd import elmh as E
 
 pytestmark = pytest.mark.gpu
 
@@ -269,6 +270,37 @@ def test_fill_and_copy(ctx):
     c.free()
 
 
+def test_argmax_step_feeds_the_next_step(ctx):
+    """elmh_argmax_step_dev: the argmax into the next step's token slot, into the ring slot of the step's
+    position (mod the ring length), and the device position one up, call after call."""
+    r = np.random.default_rng(33)
+    ring_len, V = 8, 49152
+    bx, bo, bpos, bring = ctx.buffer(V * 4), ctx.buffer(4), ctx.buffer(4), ctx.buffer(ring_len * 4)
+    bring.upload(np.full(ring_len, -1, np.int32))
+    pos = 13
+    bpos.upload(np.array([pos], np.int32))
+    want = {}
+    for step in range(11):
+        x = r.normal(0, 1, V).astype(np.float32)
+        bx.upload(x)
+        print(f"[gpu] argmax step pos={pos}", flush=True)
+        ctx.argmax_step_dev(bx.ptr, V, bo.ptr, bpos.ptr, bring.ptr, ring_len)
+        tok = int(O.argmax(x)[0])
+        assert int(bo.download((1,), np.int32)[0]) == tok
+        want[pos % ring_len] = tok
+        pos += 1
+        assert int(bpos.download((1,), np.int32)[0]) == pos
+    ring = bring.download((ring_len,), np.int32)
+    for slot, tok in want.items():
+        assert ring[slot] == tok
+    with pytest.raises(E.ElmhError):
+        ctx.argmax_step_dev(bx.ptr, V, bo.ptr, bpos.ptr, bring.ptr, 6)  # not a power of two
+    with pytest.raises(E.ElmhError):
+        ctx.argmax_step_dev(bx.ptr, 64 * 4096 + 1, bo.ptr, bpos.ptr, bring.ptr, ring_len)
+    for b in (bx, bo, bpos, bring):
+        b.free()
+
+
 def test_argmax_matches_edgelm(ctx):
     """Greedy sampling on the device (argmax, tokenizer.cpp:187-189) against the oracle's
     restatement of std::max_element: ties, signed zeros, NaNs at and after index 0, and row lengths
@@ -281,6 +313,25 @@ def test_argmax_matches_edgelm(ctx):
         bx, bo = dev(ctx, x), ctx.buffer(4)
         ctx.argmax_dev(bx.ptr, 1, x.size, bo.ptr)
         assert int(bo.download((1,), np.int32)[0]) == int(O.argmax(x)[0])
+        bx.free()
+        bo.free()
+    # one row is split into workgroup slices of up to 4096 values: ties, NaNs and maxima across slices
+    x = r.normal(0, 1, 9000).astype(np.float32)
+    x[[5, 4096 + 7]] = 9.0  # a tie across slices: the first wins
+    y = r.normal(0, 1, 9000).astype(np.float32)
+    y[4100:8192] = np.nan  # a whole slice of NaNs posts no candidate
+    y[8500] = 20.0
+    z = r.normal(0, 1, 12289).astype(np.float32)
+    z[0] = np.nan  # NaN at index 0 stands against a larger value in a later slice
+    z[12288] = 99.0
+    u = r.normal(0, 1, 262144).astype(np.float32)  # 64 slices, the maximum in the last value
+    u[-1] = 50.0
+    for x in (x, y, z, u, r.normal(0, 1, 4097).astype(np.float32), r.normal(0, 1, 49151).astype(np.float32)):
+        print(f"[gpu] argmax across slices n={x.size}", flush=True)
+        bx, bo = dev(ctx, x), ctx.buffer(4)
+        for _ in range(2):  # the second launch finds the counter the first one left zero
+            ctx.argmax_dev(bx.ptr, 1, x.size, bo.ptr)
+            assert int(bo.download((1,), np.int32)[0]) == int(O.argmax(x)[0])
         bx.free()
         bo.free()
     x = r.normal(0, 1, (6, 49152)).astype(np.float32)
