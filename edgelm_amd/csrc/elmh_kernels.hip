@@ -1409,6 +1409,57 @@ __device__ __forceinline__ long q4_operand8(uint2 w, int h) {
   return (long)(((uint64_t)hi << 32) | lo);
 }
 
+// The epilogue of a 16 x 16 wave tile (gemm_wave16_kernel, gemm_lds16_kernel): row r0 + l16,
+// tokens t0 + 4 c4 + i (accumulator i); the row (and token) rescale, then SwiGLU or the residual,
+// stores bounded by T and N.
+template <int WDT, bool SW, bool TOK>
+__device__ __forceinline__ void wave16_store(const GemmArgs& a, const GemmTarget& tg, int r0, int t0, int lane,
+                                             const v4i (&iacc)[SW ? 2 : 1], const float (&facc)[SW ? 2 : 1][4]) {
+  constexpr int NSEL = SW ? 2 : 1;
+  const int l16 = lane & 15, c4 = lane >> 4;
+  const int r = r0 + l16;
+  const int rc = min(r, tg.N - 1);
+  const int tv = min(kWave16, a.T - t0);
+  const uint32_t tbytes = (uint32_t)tv * (uint32_t)tg.N * 4u;
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(tg.y + (int64_t)t0 * tg.N, (short)0, (int)tbytes, 0x00020000);
+  float xt[4] = {1.f, 1.f, 1.f, 1.f};
+  if (TOK) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xt[i] = a.xd[min(t0 + 4 * c4 + i, a.Tpad - 1)];
+  }
+  auto value = [&](int s, int i, float ws) {
+    if (WDT == WQ8) return TOK ? ((float)iacc[s][i] * xt[i]) * ws : facc[s][i] * ws;
+    return TOK ? (facc[s][i] * 0.0625f) * xt[i] : facc[s][i] * 0.0625f;
+  };
+  const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
+  if (SW) {
+    const float wsu = WDT == WQ8 ? a.tg[1].scales[rc] : 1.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int off = r < tg.N ? ((4 * c4 + i) * tg.N + r) * 4 : 0x7FFFFFF0;
+      const float out = silu_exact(value(0, i, ws)) * value(NSEL - 1, i, wsu);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), ry, off, 0, 0);
+    }
+    return;
+  }
+  const bool has_res = tg.res != nullptr;
+  const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(has_res ? tg.res + (int64_t)t0 * tg.N : tg.y), (short)0, has_res ? (int)tbytes : 0, 0x00020000);
+  float res[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int off = r < tg.N ? ((4 * c4 + i) * tg.N + r) * 4 : 0x7FFFFFF0;
+    res[i] = has_res ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, off, 0, 0)) : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int off = r < tg.N ? ((4 * c4 + i) * tg.N + r) * 4 : 0x7FFFFFF0;
+    float out = value(0, i, ws);
+    if (has_res) out = out + res[i];
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), ry, off, 0, 0);
+  }
+}
+
 constexpr int kWave16Depth = 8;  // blocks in flight per wave (its operands are small)
 
 template <int WDT, bool SW, bool TOK, bool FAST, int DEPTH = kWave16Depth>
@@ -1511,48 +1562,191 @@ __global__ __launch_bounds__(256) void gemm_wave16_kernel(const GemmArgs a) {
     }
   }
 
-  // epilogue: row r0 + l16, tokens t0 + 4 c4 + i (accumulator i)
-  const int r = r0 + l16;
-  const int rc = min(r, tg.N - 1);
-  const int tv = min(kWave16, a.T - t0);
-  const uint32_t tbytes = (uint32_t)tv * (uint32_t)tg.N * 4u;
-  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(tg.y + (int64_t)t0 * tg.N, (short)0, (int)tbytes, 0x00020000);
-  float xt[4] = {1.f, 1.f, 1.f, 1.f};
-  if (TOK) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) xt[i] = a.xd[min(t0 + 4 * c4 + i, a.Tpad - 1)];
+  wave16_store<WDT, SW, TOK>(a, tg, r0, t0, lane, iacc, facc);
+}
+
+// Small GEMMs (K <= 1536: the prefill of a small model): gemm_wave16_kernel's waves and arithmetic
+// (the same bits), with a workgroup's operands (one 16-row tile, 64 tokens: four waves of 16
+// tokens) moved into LDS by DMA in one go, 1 KB per instruction, every request out before the
+// first wait: the activation fragments of the 64 tokens (two 32-token groups, contiguous in xq),
+// their block scales, the 16 rows' weight items and their q4 scales. gemm_wave16_kernel loads each
+// wave's operands from L2 eight blocks ahead, and its loop is bound by that latency (~150 ns per
+// 32-block with the operands in the Infinity Cache, measured at T = 128, K = 1536); here the loop
+// reads LDS. LDS: A [2][nb][1024] | XD [nb][64] f32 (token mode: [64]) | B[s] [nb][16][G] | BS[s]
+// (q4) [nb][16] f32, each region with room for kLds16Ahead more blocks and rounded up to 1 KB
+// (gemm_lds16_bytes).
+__host__ __device__ constexpr int lds16_region_bytes(int bytes) { return (bytes + 1023) / 1024 * 1024; }
+constexpr int kLds16MaxBlocks = 48;  // K <= 1536
+constexpr int kLds16Ahead = 3;       // blocks read ahead; every region has room for them past nb
+template <int WDT, bool SW, bool TOK>
+__host__ __device__ inline int gemm_lds16_bytes(int nb) {
+  constexpr int G = WDT == WQ8 ? 32 : 16, NSEL = SW ? 2 : 1, P = kLds16Ahead;
+  const int xd = TOK ? 1024 : lds16_region_bytes((nb + P) * 64 * 4);
+  const int bw = lds16_region_bytes((nb + P) * 16 * G), bs = WDT == WQ4 ? lds16_region_bytes((nb + P) * 16 * 4) : 0;
+  return (2 * nb + P) * 1024 + xd + NSEL * (bw + bs);
+}
+
+template <int WDT, bool SW, bool TOK, bool FAST>
+__global__ __launch_bounds__(256) void gemm_lds16_kernel(const GemmArgs a) {
+  typedef Wave16Ops<WDT, SW, TOK> Ops;
+  constexpr int NSEL = Ops::NSEL, G = WDT == WQ8 ? 32 : 16;
+  constexpr bool BLOCKX = Ops::BLOCKX;
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int lane = threadIdx.x & 63, l16 = lane & 15, c4 = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int nb = a.nb, H = a.H;
+  // workgroup -> (target, 16-row tile, 64-token chunk), chunk fastest
+  const int nchunk = (a.T + 63) / 64;
+  int rt = (int)blockIdx.x;
+  const int ch = rt % nchunk;
+  rt /= nchunk;
+  int ti = 0;
+  const int n = SW ? 1 : a.n_targets;
+  for (; ti < n; ++ti) {
+    const int cnt = (a.tg[ti].N + kWave16 - 1) / kWave16;
+    if (rt < cnt) break;
+    rt -= cnt;
   }
-  auto value = [&](int s, int i, float ws) {
-    if (WDT == WQ8) return TOK ? ((float)iacc[s][i] * xt[i]) * ws : facc[s][i] * ws;
-    return TOK ? (facc[s][i] * 0.0625f) * xt[i] : facc[s][i] * 0.0625f;
-  };
-  const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
-  if (SW) {
-    const float wsu = WDT == WQ8 ? a.tg[1].scales[rc] : 1.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int off = r < tg.N ? ((4 * c4 + i) * tg.N + r) * 4 : 0x7FFFFFF0;
-      const float out = silu_exact(value(0, i, ws)) * value(NSEL - 1, i, wsu);
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), ry, off, 0, 0);
+  if (ti >= n) return;  // past the last tile (uniform per workgroup; no barrier below)
+  const GemmTarget tg = SW ? a.tg[0] : gemm_target_at(ti);
+  const int r0 = rt * kWave16, tc = ch * 64;
+  const uint8_t* const wd[2] = {tg.data, SW ? a.tg[1].data : tg.data};
+  const float* const wsc[2] = {tg.scales, SW ? a.tg[1].scales : tg.scales};
+  constexpr int P = kLds16Ahead;
+  const int xd_bytes = TOK ? 1024 : lds16_region_bytes((nb + P) * 64 * 4);
+  const int bw_bytes = lds16_region_bytes((nb + P) * 16 * G);
+  const int bs_bytes = WDT == WQ4 ? lds16_region_bytes((nb + P) * 16 * 4) : 0;
+  unsigned char* const A = lds;
+  unsigned char* const XD = A + (2 * nb + P) * 1024;
+  unsigned char* const BW = XD + xd_bytes;             // [s] at BW + s * bw_bytes
+  unsigned char* const BS = BW + NSEL * bw_bytes;      // [s] at BS + s * bs_bytes
+  const unsigned base = (unsigned)(size_t)(LdsBytes)lds;
+  const unsigned xd_lds = base + (2 * nb + P) * 1024, bw_lds = xd_lds + xd_bytes, bs_lds = bw_lds + NSEL * bw_bytes;
+
+  // 1. every operand of the workgroup into LDS; instruction j of a region fills its KB j, and wave w
+  // issues j = w, w + 4, ... Chunks past a region's end repeat its last one (into the padding).
+  {
+    // activation fragments: the two 32-token groups are contiguous in xq ([Tpad/32][nb][1 KB])
+    const int8_t* const xs = a.xq + (int64_t)(tc >> 5) * nb * 1024;
+    for (int j = wave; j < 2 * nb; j += 4) dma16s(xs, (uint32_t)(j * 1024 + lane * 16), base + j * 1024);
+    if (BLOCKX) {  // XD[b][t]: lane -> block 4 j + lane / 16, tokens 4 (lane % 16) ..
+      for (int j = wave; 4 * j < nb; j += 4) {
+        const int b = min(4 * j + (lane >> 4), nb - 1);
+        dma16s(a.xd, (uint32_t)(((int64_t)b * a.Tpad + tc + 4 * l16) * 4), xd_lds + j * 1024);
+      }
+    } else if (wave == 0) {  // XD[t]
+      dma16s(a.xd, (uint32_t)((tc + 4 * l16) * 4), xd_lds);
     }
-    return;
-  }
-  const bool has_res = tg.res != nullptr;
-  const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(has_res ? tg.res + (int64_t)t0 * tg.N : tg.y), (short)0, has_res ? (int)tbytes : 0, 0x00020000);
-  float res[4];
+    // weight item (row, b) sits at ((row / H) nb + b) H + row % H (H a power of two; the launch
+    // keeps byte offsets below 2^31)
+    const int lgH = __builtin_ctz(H);
+    auto item = [&](int row, int b) { return (((row >> lgH) * nb + b) << lgH) + (row & (H - 1)); };
+    constexpr int CPB = G;  // 16-byte chunks per block of the 16 rows: 16 rows x G / 16
+    const int nw = nb * CPB;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int off = r < tg.N ? ((4 * c4 + i) * tg.N + r) * 4 : 0x7FFFFFF0;
-    res[i] = has_res ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, off, 0, 0)) : 0.f;
+    for (int s = 0; s < NSEL; ++s) {
+      for (int j = wave; 64 * j < nw; j += 4) {
+        const int c = min(64 * j + lane, nw - 1), b = c / CPB, w = c - b * CPB;
+        const int row = WDT == WQ8 ? w >> 1 : w, half = WDT == WQ8 ? (w & 1) : 0;
+        dma16s(wd[s], (uint32_t)(item(r0 + row, b) * G + half * 16), bw_lds + s * bw_bytes + j * 1024);
+      }
+      if (WDT == WQ4) {  // BS[b][row]: 4 rows per chunk, consecutive items (H >= 4, r0 % 4 == 0)
+        const int ns = nb * 4;
+        for (int j = wave; 64 * j < ns; j += 4) {
+          const int c = min(64 * j + lane, ns - 1), b = c >> 2, q = c & 3;
+          dma16s(wsc[s], (uint32_t)(item(r0 + 4 * q, b) * 4), bs_lds + s * bs_bytes + j * 1024);
+        }
+      }
+    }
+    wait_vm<0>();
+    __syncthreads();
   }
+
+  // 2. the wave's 16 tokens against the 16 rows, block by block from LDS, D blocks read ahead
+  const int tw = wave * kWave16, t0 = tc + tw;
+  const unsigned char* const xa = A + (tw >> 5) * nb * 1024 + ((c4 >> 1) * 32 + (tw & 31) + l16) * 16 + (c4 & 1) * 8;
+  auto load = [&](int blk, Ops& o) {
+    // blocks nb .. nb + P - 1 (read ahead, never used) lie in the regions' padding
+    o.A = *reinterpret_cast<const long*>(xa + blk * 1024);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int off = r < tg.N ? ((4 * c4 + i) * tg.N + r) * 4 : 0x7FFFFFF0;
-    float out = value(0, i, ws);
-    if (has_res) out = out + res[i];
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), ry, off, 0, 0);
+    for (int s = 0; s < NSEL; ++s) {
+      const unsigned char* const bw = BW + s * bw_bytes + (blk * 16 + l16) * G;
+      if (WDT == WQ8) {
+        o.B[s] = *reinterpret_cast<const long*>(bw + c4 * 8);
+        o.c[s] = 1.f;
+      } else {
+        o.B[s] = q4_operand8(*reinterpret_cast<const uint2*>(bw + (c4 & 1) * 8), c4 >> 1);
+        o.c[s] = reinterpret_cast<const float*>(BS + s * bs_bytes)[blk * 16 + l16];
+      }
+    }
+    if (BLOCKX) o.xv = *reinterpret_cast<const float4*>(XD + (blk * 64 + tw + 4 * c4) * 4);
+  };
+  v4i iacc[NSEL];
+  float facc[NSEL][4];
+  const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < NSEL; ++s) {
+    iacc[s] = zero;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) facc[s][i] = 0.f;
   }
+  auto rescale = [&](const Ops& o, const v4i (&S)[NSEL]) {
+    const float xv[4] = {o.xv.x, o.xv.y, o.xv.z, o.xv.w};
+#pragma unroll
+    for (int s = 0; s < NSEL; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float m = WDT == WQ8 ? xv[BLOCKX ? i : 0] : BLOCKX ? o.c[s] * xv[i] : o.c[s];
+        if (FAST) {
+          facc[s][i] = __builtin_fmaf((float)S[s][i], m, facc[s][i]);
+        } else {
+          facc[s][i] = facc[s][i] + (float)S[s][i] * m;
+        }
+      }
+  };
+  // Straight-line code over the blocks (at most kLds16MaxBlocks): block k + 3's operands are read
+  // and block k + 1's MFMA issued before block k's products are rescaled and added, every read
+  // unconditional once its step is reached (the empty asm keeps the compiler from sinking it past
+  // the exits), so the operands of an MFMA were requested two steps before. (In a loop the
+  // compiler's wait-count pass made every iteration wait for all reads at its head.)
+  Ops ops[4];
+  v4i S[2][NSEL];
+  load(0, ops[0]);
+  load(1, ops[1]);
+  load(2, ops[2]);
+  asm volatile("" ::: "memory");
+  if (!(TOK && WDT == WQ8)) {
+#pragma unroll
+    for (int s = 0; s < NSEL; ++s) S[0][s] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ops[0].A, ops[0].B[s], zero, 0, 0, 0);
+  }
+#define ELM_L16_STEP(k)                                                                                   \
+  if (nb <= (k)) goto done;                                                                              \
+  if ((k) + 3 < kLds16MaxBlocks) {                                                                       \
+    load((k) + 3, ops[((k) + 3) % 4]);                                                                   \
+    asm volatile("" ::: "memory");                                                                       \
+    __builtin_amdgcn_sched_barrier(0);                                                                   \
+  }                                                                                                      \
+  if (TOK && WDT == WQ8) {                                                                               \
+    _Pragma("unroll") for (int s = 0; s < NSEL; ++s) iacc[s] =                                           \
+        __builtin_amdgcn_mfma_i32_16x16x32_i8(ops[(k) % 4].A, ops[(k) % 4].B[s], iacc[s], 0, 0, 0);       \
+  } else {                                                                                               \
+    if ((k) + 1 < kLds16MaxBlocks) {                                                                     \
+      _Pragma("unroll") for (int s = 0; s < NSEL; ++s) S[((k) + 1) % 2][s] =                             \
+          __builtin_amdgcn_mfma_i32_16x16x32_i8(ops[((k) + 1) % 4].A, ops[((k) + 1) % 4].B[s], zero, 0, 0, 0); \
+    }                                                                                                    \
+    rescale(ops[(k) % 4], S[(k) % 2]);                                                                   \
+  }
+  ELM_L16_STEP(0) ELM_L16_STEP(1) ELM_L16_STEP(2) ELM_L16_STEP(3) ELM_L16_STEP(4) ELM_L16_STEP(5)
+  ELM_L16_STEP(6) ELM_L16_STEP(7) ELM_L16_STEP(8) ELM_L16_STEP(9) ELM_L16_STEP(10) ELM_L16_STEP(11)
+  ELM_L16_STEP(12) ELM_L16_STEP(13) ELM_L16_STEP(14) ELM_L16_STEP(15) ELM_L16_STEP(16) ELM_L16_STEP(17)
+  ELM_L16_STEP(18) ELM_L16_STEP(19) ELM_L16_STEP(20) ELM_L16_STEP(21) ELM_L16_STEP(22) ELM_L16_STEP(23)
+  ELM_L16_STEP(24) ELM_L16_STEP(25) ELM_L16_STEP(26) ELM_L16_STEP(27) ELM_L16_STEP(28) ELM_L16_STEP(29)
+  ELM_L16_STEP(30) ELM_L16_STEP(31) ELM_L16_STEP(32) ELM_L16_STEP(33) ELM_L16_STEP(34) ELM_L16_STEP(35)
+  ELM_L16_STEP(36) ELM_L16_STEP(37) ELM_L16_STEP(38) ELM_L16_STEP(39) ELM_L16_STEP(40) ELM_L16_STEP(41)
+  ELM_L16_STEP(42) ELM_L16_STEP(43) ELM_L16_STEP(44) ELM_L16_STEP(45) ELM_L16_STEP(46) ELM_L16_STEP(47)
+#undef ELM_L16_STEP
+done:
+  if (t0 < a.T) wave16_store<WDT, SW, TOK>(a, tg, r0, t0, lane, iacc, facc);
 }
 
 // ---------------------------------------------------------------- f32-activation paths
@@ -1944,6 +2138,29 @@ static void gemm_wave16_launch(const GemmArgs& a, hipStream_t s) {
     gemm_wave16_kernel<WDT, SW, TOK, false><<<grid, 256, 0, s>>>(a);
 }
 
+// gemm_lds16_kernel when its LDS fits (K <= 1536 or so); false otherwise
+template <int WDT, bool SW, bool TOK>
+static bool gemm_lds16_launch(const GemmArgs& a, hipStream_t s) {
+  const int bytes = gemm_lds16_bytes<WDT, SW, TOK>(a.nb);
+  if (a.nb > kLds16MaxBlocks || bytes > (int)kMaxLds - 1024 || a.H < 4 || (a.H & (a.H - 1))) return false;
+  const void* k = a.fast && !(TOK && WDT == WQ8) ? (const void*)gemm_lds16_kernel<WDT, SW, TOK, true>
+                                                  : (const void*)gemm_lds16_kernel<WDT, SW, TOK, false>;
+  static bool raised[2] = {false, false};  // the LDS limit, once per kernel
+  const int which = a.fast && !(TOK && WDT == WQ8) ? 1 : 0;
+  if (!raised[which]) {
+    if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds - 1024) != hipSuccess) return false;
+    raised[which] = true;
+  }
+  int rows = 0;
+  for (int i = 0; i < (SW ? 1 : a.n_targets); ++i) rows += (a.tg[i].N + kWave16 - 1) / kWave16;
+  const dim3 grid(rows * ((a.T + 63) / 64));
+  if (which)
+    gemm_lds16_kernel<WDT, SW, TOK, true><<<grid, 256, bytes, s>>>(a);
+  else
+    gemm_lds16_kernel<WDT, SW, TOK, false><<<grid, 256, bytes, s>>>(a);
+  return true;
+}
+
 template <int WDT, bool SW, bool TOK>
 static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
   if (a.Tpad % kGemmTileT || a.T < 1 || a.T > a.Tpad || tiles < 1 ||
@@ -1970,16 +2187,19 @@ static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
     small = ev[0] == '6' ? true : ev[0] == '1' ? false : small;
     wave = false;
   }
-  // 16 x 16 waves unless 32 x 32 waves already fill the chip
-  bool wave32 = false;
+  // 16 x 16 waves with their operands staged in LDS (gemm_lds16_kernel) where they fit, else
+  // loaded from L2 (gemm_wave16_kernel); ELMH_GEMM_KERNEL = lds16, wave (16 x 16 from L2), wave32
+  // or ring forces a kernel
+  bool wave32 = false, lds16 = true;
   if (const char* ev = getenv("ELMH_GEMM_KERNEL")) {
-    wave = ev[0] == 'w' ? true : ev[0] == 'r' ? false : wave;
+    wave = ev[0] == 'w' || ev[0] == 'l' ? true : ev[0] == 'r' ? false : wave;
     wave32 = std::strcmp(ev, "wave32") == 0;
+    lds16 = ev[0] == 'l';
   }
   if (wave) {
     if (wave32)
       gemm_wave_launch<WDT, SW, TOK>(a, s);
-    else
+    else if (!lds16 || !gemm_lds16_launch<WDT, SW, TOK>(a, s))
       gemm_wave16_launch<WDT, SW, TOK>(a, s);
     return hipGetLastError();
   }

@@ -360,13 +360,14 @@ def test_gemm_token_tiles(ctx, dt, tile, monkeypatch):
         d.free()
 
 
-@pytest.mark.parametrize("kernel", ["wave", "wave32", "ring"])
+@pytest.mark.parametrize("kernel", ["lds16", "wave", "wave32", "ring"])
 @pytest.mark.parametrize("dt", [O.Q8, O.Q4])
 def test_gemm_kernels_small_and_ragged(ctx, dt, kernel, monkeypatch):
-    """Every GEMM kernel forced (ELMH_GEMM_KERNEL): one wave per 16x16 tile (what small problems
-    select), one wave per 32x32 tile, and the LDS-ring kernel. Ragged rows and tokens (partial
-    tiles), MATMUL_N with a residual, FFN_SWIGLU, per-block exact and fast, per-token, and an odd
-    block count."""
+    """Every GEMM kernel forced (ELMH_GEMM_KERNEL): one wave per 16x16 tile with the workgroup's
+    operands staged in LDS (what small problems select; at K = 1568 the q8 SwiGLU's operands do not
+    fit and it falls back to the next), the same loading from L2, one wave per 32x32 tile, and the
+    LDS-ring kernel. Ragged rows and tokens (partial tiles), MATMUL_N with a residual, FFN_SWIGLU,
+    per-block exact and fast, per-token, and an odd block count."""
     monkeypatch.setenv("ELMH_GEMM_KERNEL", kernel)
     r = rng(700 + dt)
     for n, n2, k in [(300, 40, 576), (70, 33, 1568)]:
