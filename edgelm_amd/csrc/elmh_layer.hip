@@ -495,6 +495,58 @@ done:
   return acc;
 }
 
+// acc + p_0 v_0 + p_1 v_1 + ... + p_k v_k in order, k < 16 nbt (nbt <= NB): each product rounded,
+// then added (cpu::attention's o_i += p_j * v_j[i] without contraction), p_j = pj[j] and
+// v_j = vcol[64 j]; the reads stay below 16 NB values of each. Straight-line code over batches of
+// 16, as ordered_sum256: batch b + 2 is read and batch b + 1's products are formed while batch b's
+// products are added, so the dependent adds alternate with independent multiplies (the empty asm
+// keeps each product in its step instead of sunk to the step that adds it).
+template <int NB>
+__device__ __forceinline__ float ordered_dot_col(const float* __restrict__ pj, const float* __restrict__ vcol, int nbt,
+                                                 float acc) {
+  float pv[3][16], xv[3][16], pr[2][16];
+#define ELM_DOT_LOAD(bt)                                                                           \
+  _Pragma("unroll") for (int u = 0; u < 16; ++u) {                                                 \
+    pv[(bt) % 3][u] = pj[16 * (bt) + u];                                                           \
+    xv[(bt) % 3][u] = vcol[64 * (16 * (bt) + u)];                                                  \
+  }                                                                                                \
+  asm volatile("" ::: "memory");
+#define ELM_DOT_STEP(bt)                                                                           \
+  if (nbt <= (bt)) goto done;                                                                      \
+  if ((bt) + 2 < NB) { ELM_DOT_LOAD((bt) + 2) }                                                    \
+  _Pragma("unroll") for (int u = 0; u < 16; ++u) {                                                 \
+    if ((bt) + 1 < NB) {                                                                           \
+      pr[((bt) + 1) % 2][u] = pv[((bt) + 1) % 3][u] * xv[((bt) + 1) % 3][u];                       \
+      asm volatile("" : "+v"(pr[((bt) + 1) % 2][u]));                                              \
+    }                                                                                              \
+    acc = acc + pr[(bt) % 2][u];                                                                   \
+  }
+  ELM_DOT_LOAD(0)
+  if (NB > 1) { ELM_DOT_LOAD(1) }
+#pragma unroll
+  for (int u = 0; u < 16; ++u) pr[0][u] = pv[0][u] * xv[0][u];
+  ELM_DOT_STEP(0)
+  if (NB > 1) { ELM_DOT_STEP(1) }
+  if (NB > 2) { ELM_DOT_STEP(2) }
+  if (NB > 3) { ELM_DOT_STEP(3) }
+  if (NB > 4) { ELM_DOT_STEP(4) }
+  if (NB > 5) { ELM_DOT_STEP(5) }
+  if (NB > 6) { ELM_DOT_STEP(6) }
+  if (NB > 7) { ELM_DOT_STEP(7) }
+  if (NB > 8) { ELM_DOT_STEP(8) }
+  if (NB > 9) { ELM_DOT_STEP(9) }
+  if (NB > 10) { ELM_DOT_STEP(10) }
+  if (NB > 11) { ELM_DOT_STEP(11) }
+  if (NB > 12) { ELM_DOT_STEP(12) }
+  if (NB > 13) { ELM_DOT_STEP(13) }
+  if (NB > 14) { ELM_DOT_STEP(14) }
+  if (NB > 15) { ELM_DOT_STEP(15) }
+#undef ELM_DOT_STEP
+#undef ELM_DOT_LOAD
+done:
+  return acc;
+}
+
 __global__ __launch_bounds__(256) void attention_decode64_kernel(
     const float* __restrict__ q, float* __restrict__ out, float* __restrict__ kc, float* __restrict__ vc, int pos0,
     const int* __restrict__ pos_dev, int n_heads, int n_kv, int max_ctx, int n_cap, const float* __restrict__ rcos,
@@ -622,37 +674,11 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
         dma16s(vh, (uint32_t)((nx + min(r, rows - 1)) * ROWB + ((lane & 15) << 4)), dst + pc * 1024);
       }
     }
-    if (wave == 0) {
-      // 16 positions per batch, the next batch's reads out before this one's products and adds
+    if (wave == 0) {  // 16 positions per batch (C / 16 at most), then the rest one by one
       const int m = min(C, nc - c0), nbt = m >> 4;
       const float* const pj = sc + c0;
       const float* const vcol = cur + lane;
-      float pa[16], xa[16], pb[16], xb[16];
-      auto load = [&](int bt, float (&p)[16], float (&x)[16]) {
-        const int j0 = min(bt, nbt - 1) * 16;
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-          p[u] = pj[j0 + u];
-          x[u] = vcol[(j0 + u) * HD];
-        }
-      };
-      auto fold = [&](const float (&p)[16], const float (&x)[16]) {
-#pragma unroll
-        for (int u = 0; u < 16; ++u) acc = acc + p[u] * x[u];
-      };
-      if (nbt > 0) {
-        load(0, pa, xa);
-        for (int bt = 0; bt < nbt; bt += 2) {
-          load(bt + 1, pb, xb);
-          __builtin_amdgcn_sched_barrier(0);
-          fold(pa, xa);
-          if (bt + 1 < nbt) {
-            load(bt + 2, pa, xa);
-            __builtin_amdgcn_sched_barrier(0);
-            fold(pb, xb);
-          }
-        }
-      }
+      acc = ordered_dot_col<kDecRows / 16>(pj, vcol, nbt, acc);
       for (int j = nbt * 16; j < m; ++j) acc = acc + pj[j] * vcol[j * HD];
     }
     if (nx < nc) {
@@ -934,32 +960,7 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
     const int m = min(R, nw - c0), nbt = max(m, 0) >> 4;  // this query's positions in the chunk
     const float* const pj = sw + c0;
     const float* const vcol = cur + lane;
-    float pa[16], xa[16], pb[16], xb[16];
-    auto load = [&](int bt, float (&pv)[16], float (&x)[16]) {
-      const int j0 = min(bt, nbt - 1) * 16;
-#pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        pv[u] = pj[j0 + u];
-        x[u] = vcol[(j0 + u) * HD];
-      }
-    };
-    auto fold = [&](const float (&pv)[16], const float (&x)[16]) {
-#pragma unroll
-      for (int u = 0; u < 16; ++u) acc = acc + pv[u] * x[u];
-    };
-    if (nbt > 0) {
-      load(0, pa, xa);
-      for (int bt = 0; bt < nbt; bt += 2) {
-        load(bt + 1, pb, xb);
-        __builtin_amdgcn_sched_barrier(0);
-        fold(pa, xa);
-        if (bt + 1 < nbt) {
-          load(bt + 2, pa, xa);
-          __builtin_amdgcn_sched_barrier(0);
-          fold(pb, xb);
-        }
-      }
-    }
+    acc = ordered_dot_col<R / 16>(pj, vcol, nbt, acc);
     for (int j = nbt * 16; j < m; ++j) acc = acc + pj[j] * vcol[j * HD];
     if (nx < nmax) {
       wait_vm<0>();
