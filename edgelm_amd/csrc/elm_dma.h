@@ -48,9 +48,12 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// workgroup barrier that orders LDS accesses in the compiler's view without waiting for loads
+// workgroup barrier for LDS data: this wave's LDS accesses complete (lgkmcnt(0)) before it, and
+// the compiler keeps memory accesses on their side of it, but loads from memory (vmcnt) and
+// copies into LDS stay in flight
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt 63 and expcnt 7: no wait
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }

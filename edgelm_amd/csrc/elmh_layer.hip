@@ -897,9 +897,11 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
   dma_rows(vh, 0, min(R, nmax), vb_lds, false);
   lds_barrier();  // keys (every wave waited for its own) and the queries in LDS
 
-  // scores: thread j takes row j of each chunk of R positions, against every query of the group
-  // that sees it
+  // scores: thread (j, g) takes row j of each chunk of R positions against queries 2 g and 2 g + 1
+  // of the group (those that see it)
+  static_assert(R == 128 && kAttnQ == 4, "two threads per key row, two queries each");
   const float scale = 1.0f / sqrtf((float)HD);
+  const int srow = tid & (R - 1), sq0 = 2 * (tid >> 7);
   for (int c0 = 0; c0 < nmax; c0 += R) {
     if (c0 > 0) {  // the next key chunk, once every thread has scored the previous one
       __syncthreads();
@@ -907,15 +909,15 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
       wait_vm<0>();
       lds_barrier();
     }
-    const int j = c0 + tid;
-    if (tid < R && j < nmax) {
-      const float* const row = kb + tid * HD;
-      const int sw = tid & 15;
+    const int j = c0 + srow;
+    if (j < nmax && j <= pos0 + t0 + min(sq0 + 1, nq - 1)) {
+      const float* const row = kb + srow * HD;
+      const int sw = srow & 15;
       float4 kv[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) kv[u] = *reinterpret_cast<const float4*>(row + ((u ^ sw) << 2));
 #pragma unroll
-      for (int qi = 0; qi < kAttnQ; ++qi) {
+      for (int qi = sq0; qi < sq0 + 2; ++qi) {
         if (qi < nq && j <= pos0 + t0 + qi) {
           const float* const qq = qb + qi * HD;
           float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
