@@ -16,11 +16,11 @@ typedef __attribute__((address_space(3))) unsigned char* LdsBytes;
 // streaming GEMV, the GEMM and the decode attention) make no other use of it (their code
 // references M0 only inside these statements), so the write disturbs nothing.
 __device__ __forceinline__ void dma16(const void* src, unsigned char* dst) {
-  const unsigned m0 = (unsigned)(size_t)(LdsBytes)dst;
+  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(LdsBytes)dst);
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
 }
 __device__ __forceinline__ void dma4(const void* src, unsigned char* dst) {
-  const unsigned m0 = (unsigned)(size_t)(LdsBytes)dst;
+  const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(LdsBytes)dst);
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory");
 }
 // The same from a wave-uniform base (scalar registers) plus a 32-bit byte offset per lane: a loop

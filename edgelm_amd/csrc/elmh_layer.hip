@@ -843,14 +843,20 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(const float* __r
 // query's max, exponentials, in-order sum (ordered_sum256) and p_j = e_j * inv, and adds
 // p_j * v_j[lane] over the value rows in increasing j. Longer prompts pass through the buffers a
 // chunk at a time (keys through the key buffer; values alternating, the next chunk in flight).
+// Step 1 of cpu::attention (the append) is part of the kernel: rows from pos0 on come from the
+// step's own keys and values (knew, vnew: [T][n_kv][64]) instead of the cache, the keys rotated in
+// LDS once they have landed (kv_append_kernel's arithmetic), and the workgroups of each kv group's
+// first head write their query tokens' rotated keys and values to the cache (nothing in this
+// launch reads them there).
 // LDS (dynamic): keys [kPfRows][64] (chunk u of row r in slot u ^ (r & 15)), values [kPfRows][64],
 // scores [kAttnQ][n_cap rounded up to 256], q [kAttnQ][64].
 constexpr int kPfRows = 128;
 
 __global__ __launch_bounds__(256) void attention_prefill64_kernel(
-    const float* __restrict__ q, float* __restrict__ out, const float* __restrict__ kc, const float* __restrict__ vc,
-    int pos0, int T, int n_heads, int n_kv, int max_ctx, int n_cap, const float* __restrict__ rcos,
-    const float* __restrict__ rsin, int8_t* __restrict__ xq, float* __restrict__ xd, int Tpad) {
+    const float* __restrict__ q, float* __restrict__ out, float* __restrict__ kc, float* __restrict__ vc, int pos0,
+    int T, int n_heads, int n_kv, int max_ctx, int n_cap, const float* __restrict__ rcos, const float* __restrict__ rsin,
+    int8_t* __restrict__ xq, float* __restrict__ xd, int Tpad, const float* __restrict__ knew,
+    const float* __restrict__ vnew) {
   constexpr int HD = 64, H2 = 32, R = kPfRows, ROWB = HD * 4;
   extern __shared__ __align__(16) float lds[];
   const int scs = (n_cap + 255) & ~255;  // score row stride
@@ -865,19 +871,64 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
   const int tw = t0 + min(w, nq - 1), posw = pos0 + tw, nw = posw + 1;  // this wave's query
   const int nmax = pos0 + t0 + nq;                                      // the group's positions
   const int qd = n_heads * HD, grp = n_heads / n_kv, kvh = h / grp;
-  const float* const kh = kc + (int64_t)kvh * max_ctx * HD;
-  const float* const vh = vc + (int64_t)kvh * max_ctx * HD;
-  const unsigned kb_lds = (unsigned)(size_t)(LdsBytes)(unsigned char*)kb;
-  const unsigned vb_lds = (unsigned)(size_t)(LdsBytes)(unsigned char*)vb;
-  // rows [c0, c0 + rows) of a cache into a buffer: wave w moves 1 KB pieces w, w + 4, ... (4 rows
-  // each, lane -> row lane / 16, slot lane % 16); the last piece repeats the last row
-  auto dma_rows = [&](const float* base, int c0, int rows, unsigned dst, bool swz) {
+  float* const kh = kc + (int64_t)kvh * max_ctx * HD;
+  float* const vh = vc + (int64_t)kvh * max_ctx * HD;
+  const bool fresh = knew != nullptr;  // rows from pos0 on: the step's keys and values, not the cache
+  // rows [c0, c0 + rows) of a cache (or, from pos0 on, of the step's rows of kv head kvh) into a
+  // buffer: wave w moves 1 KB pieces w, w + 4, ... (4 rows each, lane -> row lane / 16, slot
+  // lane % 16); the last piece repeats the last row
+  auto dma_rows = [&](const float* cache, const float* step, int c0, int rows, float* dst, bool swz) {
     for (int pc = w; 4 * pc < rows; pc += 4) {
-      const int r = 4 * pc + (lane >> 4), s = lane & 15;
-      dma16s(base, (uint32_t)((c0 + min(r, rows - 1)) * ROWB + ((swz ? s ^ (r & 15) : s) << 4)), dst + pc * 1024);
+      const int r = 4 * pc + (lane >> 4), s = lane & 15, p = c0 + min(r, rows - 1);
+      const int ch = (swz ? s ^ (r & 15) : s) * 4;
+      const float* const src = fresh && p >= pos0 ? step + ((int64_t)(p - pos0) * n_kv + kvh) * HD + ch
+                                                  : cache + (int64_t)p * HD + ch;
+      dma16(src, reinterpret_cast<unsigned char*>(dst) + pc * 1024);
     }
   };
-  dma_rows(kh, 0, min(R, nmax), kb_lds, true);
+  // the step's key rows of [c0, c0 + rows) rotated in place, pairs (i, i + 32): thread task
+  // (row r, chunk pair u, u + 8), tasks tid, tid + 256, ...; cos / sin of the first chunk's tasks
+  // are loaded at the start (cpre)
+  constexpr int kRotTasks = R * 8 / 256;
+  float4 cpre[kRotTasks][2];
+  auto rotate_rows = [&](int c0, int rows, bool pre) {
+#pragma unroll
+    for (int m = 0; m < kRotTasks; ++m) {
+      const int task = tid + 256 * m, r = task >> 3, u = task & 7, p = c0 + r;
+      if (r < rows && p >= pos0) {
+        float* const row = kb + r * HD;
+        float4* const lo = reinterpret_cast<float4*>(row + ((u ^ (r & 15)) << 2));
+        float4* const hi = reinterpret_cast<float4*>(row + (((u + 8) ^ (r & 15)) << 2));
+        const float4 c = pre ? cpre[m][0] : *reinterpret_cast<const float4*>(rcos + (int64_t)p * H2 + 4 * u);
+        const float4 sn = pre ? cpre[m][1] : *reinterpret_cast<const float4*>(rsin + (int64_t)p * H2 + 4 * u);
+        const float4 a = *lo, b = *hi;
+        *lo = make_float4(a.x * c.x - b.x * sn.x, a.y * c.y - b.y * sn.y, a.z * c.z - b.z * sn.z, a.w * c.w - b.w * sn.w);
+        *hi = make_float4(b.x * c.x + a.x * sn.x, b.y * c.y + a.y * sn.y, b.z * c.z + a.z * sn.z, b.w * c.w + a.w * sn.w);
+      }
+    }
+  };
+  dma_rows(kh, knew, 0, min(R, nmax), kb, true);
+  if (fresh && rcos) {
+#pragma unroll
+    for (int m = 0; m < kRotTasks; ++m) {
+      const int task = tid + 256 * m, p = min(task >> 3, nmax - 1), u = task & 7;
+      cpre[m][0] = *reinterpret_cast<const float4*>(rcos + (int64_t)p * H2 + 4 * u);
+      cpre[m][1] = *reinterpret_cast<const float4*>(rsin + (int64_t)p * H2 + 4 * u);
+    }
+  }
+  // the append: token t0 + w's key element `lane`, rotated, and its value (kv group's first head)
+  const bool writer = fresh && h % grp == 0 && w < nq;
+  float ak = 0.f, ap = 0.f, ac = 1.f, as = 0.f, av = 0.f;
+  if (writer) {
+    const float* const ks = knew + ((int64_t)(t0 + w) * n_kv + kvh) * HD;
+    ak = ks[lane];
+    ap = ks[lane ^ H2];
+    av = vnew[((int64_t)(t0 + w) * n_kv + kvh) * HD + lane];
+    if (rcos) {
+      ac = rcos[(int64_t)(pos0 + t0 + w) * H2 + (lane & (H2 - 1))];
+      as = rsin[(int64_t)(pos0 + t0 + w) * H2 + (lane & (H2 - 1))];
+    }
+  }
   // q of the wave's query, rotated, into LDS
   {
     const float* const qs = q + (int64_t)tw * qd + h * HD;
@@ -894,8 +945,18 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
       qb[w * HD + lane + H2] = rcos ? b * c + a * sn : b;
     }
   }
-  dma_rows(vh, 0, min(R, nmax), vb_lds, false);
+  dma_rows(vh, vnew, 0, min(R, nmax), vb, false);
   lds_barrier();  // keys (every wave waited for its own) and the queries in LDS
+  if (fresh && rcos) {
+    rotate_rows(0, min(R, nmax), true);
+    lds_barrier();
+  }
+  if (writer) {  // kv_append_kernel's arithmetic
+    const int p = pos0 + t0 + w;
+    const float kr = !rcos ? ak : lane < H2 ? ak * ac - ap * as : ak * ac + ap * as;
+    kh[(int64_t)p * HD + lane] = kr;
+    vh[(int64_t)p * HD + lane] = av;
+  }
 
   // scores: thread (j, g) takes row j of each chunk of R positions against queries 2 g and 2 g + 1
   // of the group (those that see it)
@@ -905,9 +966,13 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
   for (int c0 = 0; c0 < nmax; c0 += R) {
     if (c0 > 0) {  // the next key chunk, once every thread has scored the previous one
       __syncthreads();
-      dma_rows(kh, c0, min(R, nmax - c0), kb_lds, true);
+      dma_rows(kh, knew, c0, min(R, nmax - c0), kb, true);
       wait_vm<0>();
       lds_barrier();
+      if (fresh && rcos && c0 + R > pos0) {
+        rotate_rows(c0, min(R, nmax - c0), false);
+        lds_barrier();
+      }
     }
     const int j = c0 + srow;
     if (j < nmax && j <= pos0 + t0 + min(sq0 + 1, nq - 1)) {
@@ -958,7 +1023,7 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
   for (int c0 = 0, ci = 0; c0 < nmax; c0 += R, ++ci) {
     const float* const cur = (ci & 1) ? kb : vb;
     const int nx = c0 + R;
-    if (nx < nmax) dma_rows(vh, nx, min(R, nmax - nx), (ci & 1) ? vb_lds : kb_lds, false);
+    if (nx < nmax) dma_rows(vh, vnew, nx, min(R, nmax - nx), (ci & 1) ? vb : kb, false);
     const int m = min(R, nw - c0), nbt = max(m, 0) >> 4;  // this query's positions in the chunk
     const float* const pj = sw + c0;
     const float* const vcol = cur + lane;
@@ -1274,25 +1339,27 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
   if (quantized) *quantized = false;
   // with the position in device memory the score buffer covers the whole cache
   const int n_cap = pos_dev ? max_ctx : pos0 + T;  // score slots
-  // one token: the append runs inside the attention kernel; a chunk appends every key first
+  // one token, and chunks on the head-size-64 prefill kernel: the append runs inside the attention
+  // kernel; other chunks append every key first
   const bool fuse = T == 1;
-  if (!fuse) {
+  const size_t lds_pf = ((size_t)kAttnQ * hd + (size_t)kAttnQ * ((n_cap + 63) & ~63) + (size_t)kAttnPVPos * hd) * 4;
+  const size_t lds_pf64 = ((size_t)2 * kPfRows * 64 + (size_t)kAttnQ * ((n_cap + 255) & ~255) + (size_t)kAttnQ * 64) * 4;
+  const bool pf64 = !fuse && hd == 64 && lds_pf64 <= kMaxAttnLds && !pos_dev;
+  if (!fuse && !pf64) {
     kv_append_kernel<<<T * n_kv, 64, 0, s>>>(k, v, kc, vc, pos0, pos_dev, n_kv, hd, max_ctx, rcos, rsin);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   const float* kn = fuse ? k : nullptr;
   const float* vn = fuse ? v : nullptr;
-  const size_t lds_pf = ((size_t)kAttnQ * hd + (size_t)kAttnQ * ((n_cap + 63) & ~63) + (size_t)kAttnPVPos * hd) * 4;
-  const size_t lds_pf64 = ((size_t)2 * kPfRows * 64 + (size_t)kAttnQ * ((n_cap + 255) & ~255) + (size_t)kAttnQ * 64) * 4;
   static const bool lds_ok = raise_lds_limit();  // once per process (the attribute holds for the kernel)
   if (!lds_ok) return hipErrorInvalidValue;
-  if (!fuse && hd == 64 && lds_pf64 <= kMaxAttnLds) {
+  if (pf64) {
     const int ngr = (T + kAttnQ - 1) / kAttnQ;
     const bool quant = xq && xd && quantized;
     attention_prefill64_kernel<<<n_heads * ngr, 256, lds_pf64, s>>>(q, out, kc, vc, pos0, T, n_heads, n_kv, max_ctx,
                                                                     n_cap, rcos, rsin, quant ? xq : nullptr,
-                                                                    quant ? xd : nullptr, Tpad);
+                                                                    quant ? xd : nullptr, Tpad, k, v);
     const hipError_t e = hipGetLastError();
     if (e == hipSuccess && quant) *quantized = true;
     return e;
