@@ -20,7 +20,7 @@ inline int stream_producers(int nb) {
   return 64 * (nb > kStreamFoldWaveBlocks ? kStreamWavesLong : kStreamWavesShort);
 }
 // The streaming GEMV can also take f32 activations and quantize them in each workgroup: every
-// producer thread holds 4 values per pass, at most kStreamQinPasses passes. Only for rows without
+// producer thread holds up to 4 * kStreamQinPasses values (passes of 16). Only for rows without
 // the fold wave (K <= 8192): every workgroup reads and rounds the whole activation, which at the
 // 8B down GEMV's K = 14336 (57 KB of f32 per workgroup) costs more than a separate quantizer
 // launch whose int8 result the workgroups copy (measured: 16.4 vs 11.6 us per call).

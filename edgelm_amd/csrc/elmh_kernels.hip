@@ -700,15 +700,21 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
   // wave), quantized below once they have landed. Otherwise the pre-quantized int8 values, block
   // scales and, for q4, block sums straight into LDS, where its rows are contiguous (K % 16 == 0):
   // wave w copies chunks w, w + NPW, ... of 1 KB (256 B).
-  constexpr int QP = QIN ? kStreamQinPasses : 1;
-  float4 xv[QP];
+  // QIN: 16 consecutive values per thread and pass (half a 32-block; the pair of lanes 2k, 2k + 1
+  // holds one block), so each lane's share of the block's scale and reciprocal divisions covers 16
+  // values (with 4 per lane, eight lanes per block, they were most of every workgroup's quantization
+  // time)
+  constexpr int QV = 16, QP = QIN ? kStreamQinPasses * 4 / QV : 1;
+  float4 xv[QP][QV / 4];
   if (QIN) {
     const int nel = T * K;
 #pragma unroll
-    for (int p = 0; p < QP; ++p) {
-      const float* px = a.x + min((p * P + tid) * 4, nel - 4);  // passes past the end repeat the last float4
-      xv[p] = make_float4(px[0], px[1], px[2], px[3]);
-    }
+    for (int p = 0; p < QP; ++p)
+#pragma unroll
+      for (int i = 0; i < QV / 4; ++i) {
+        const float* px = a.x + min((p * P + tid) * QV + 4 * i, nel - 4);  // past the end: the last float4 again
+        xv[p][i] = make_float4(px[0], px[1], px[2], px[3]);
+      }
     __builtin_amdgcn_sched_barrier(0);  // these loads go out before the weight requests
   } else {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -751,17 +757,40 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
     const int nel = T * K;
 #pragma unroll
     for (int p = 0; p < QP; ++p) {
-      if (p * P * 4 < nel) {  // whole waves: nel is a multiple of 32
-        const int e = (p * P + tid) * 4;
-        const float v[4] = {xv[p].x, xv[p].y, xv[p].z, xv[p].w};
-        int q[4], sum;
-        const float d = quant_block8x4(v, q, sum);
-        if (e < nel) {
+      if (p * P * QV < nel) {  // uniform; every lane runs the pass (the pair exchange below)
+        const int e = (p * P + tid) * QV;
+        float v[QV];
+#pragma unroll
+        for (int i = 0; i < QV / 4; ++i) {
+          v[4 * i] = xv[p][i].x;
+          v[4 * i + 1] = xv[p][i].y;
+          v[4 * i + 2] = xv[p][i].z;
+          v[4 * i + 3] = xv[p][i].w;
+        }
+        // quantize_act_row's block (kernels_ref.cpp:23-37): amax over both lanes, s = amax / 127,
+        // every value's rounding that of its division (elm_q8_group), the block sum of q
+        float am = 0.f;
+#pragma unroll
+        for (int i = 0; i < QV; ++i) am = fmaxf(am, fabsf(v[i]));
+        am = fmaxf(am, dpp_f<kDppQuadXor1>(am));
+        const float d = am / 127.0f;
+        int q[QV];
+        elm_q8_group<QV>(v, d == 0.f ? 1.f : d, q);
+        int sm = 0;
+#pragma unroll
+        for (int i = 0; i < QV; ++i) sm += q[i];
+        sm += dpp_i<kDppQuadXor1>(sm);
+        if (e < nel) {  // nel is a multiple of 32: both lanes of a block, or neither
           const int g = e >> 5, t = g / nb, b = g - t * nb;
-          *reinterpret_cast<uint32_t*>(L.q + t * L.kpad + b * kBlock + (e & 31)) = pack_q4(q);
+          uint4 pk;
+          pk.x = pack_q4({q[0], q[1], q[2], q[3]});
+          pk.y = pack_q4({q[4], q[5], q[6], q[7]});
+          pk.z = pack_q4({q[8], q[9], q[10], q[11]});
+          pk.w = pack_q4({q[12], q[13], q[14], q[15]});
+          *reinterpret_cast<uint4*>(L.q + t * L.kpad + b * kBlock + (e & 31)) = pk;
           if ((e & 31) == 0) {
             L.d[t * nb + b] = d;
-            if (WDT == WQ4) L.s[t * nb + b] = sum;
+            if (WDT == WQ4) L.s[t * nb + b] = sm;
           }
         }
       }
