@@ -1849,6 +1849,62 @@ __global__ __launch_bounds__(256) void gemv_f32act_kernel(const F32Args a) {
   tg.y[n] = out;
 }
 
+// T == 1, q4, one workgroup per H-row tile (of the target, or of gate and up with SW): dot_q4's
+// operations (kernels_cpu.cpp:397-399) spread over the groups instead of one lane walking the row.
+// Every (selection, row, group) item is (g0 + g1) * ws_g, g0 / g1 the in-order 16-term sums of the
+// group's low / high nibbles against x, and goes to LDS; then one lane per row adds its row's items
+// in group order (s = s + p_g from s = 0, as dot_q4 does) and applies the epilogue.
+template <bool SW>
+__global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
+  extern __shared__ __align__(16) float f32q4_lds[];
+  constexpr int NSEL = SW ? 2 : 1;
+  const int K = a.K, nb = a.nb, H = a.H, lgH = __builtin_ctz(H), pst = nb + 1;
+  float* const sx = f32q4_lds;                // [K]
+  float* const P = f32q4_lds + ((K + 3) & ~3);  // [NSEL][H][nb + 1]
+  for (int i = threadIdx.x; i < K; i += 256) sx[i] = a.x[i];
+  int ti = 0, tile = blockIdx.x;
+  if (!SW) {
+    while (ti + 1 < a.n_targets && tile >= a.tile_start[ti + 1]) ++ti;
+    tile -= a.tile_start[ti];
+  }
+  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  __syncthreads();
+  const int per_sel = H * nb, items = NSEL * per_sel;
+  for (int it = threadIdx.x; it < items; it += 256) {
+    const int sel = SW && it >= per_sel ? 1 : 0, j = it - sel * per_sel, g = j >> lgH, r = j & (H - 1);
+    const int64_t item = ((int64_t)tile * nb + g) * H + r;  // rows past N: the padding's items
+    const uint4 wq = *reinterpret_cast<const uint4*>((sel ? a.tg[1].data : tg.data) + item * 16);
+    const float ws = (sel ? a.tg[1].scales : tg.scales)[item];
+    const uint32_t wd[4] = {wq.x, wq.y, wq.z, wq.w};
+    const float* const xs = sx + g * 32;
+    float g0 = 0.f, g1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t byte = (wd[i >> 2] >> (8 * (i & 3))) & 0xFF;
+      g0 = g0 + xs[i] * (float)((int)(byte & 0x0F) - 8);
+      g1 = g1 + xs[16 + i] * (float)((int)(byte >> 4) - 8);
+    }
+    P[(sel * H + r) * pst + g] = (g0 + g1) * ws;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < H) {
+    const int r = threadIdx.x, n = tile * H + r;
+    if (n < tg.N) {
+      const float* const pr = P + r * pst;
+      float s = 0.f;
+      for (int g = 0; g < nb; ++g) s = s + pr[g];
+      if (SW) {
+        const float* const pu = P + (H + r) * pst;
+        float u = 0.f;
+        for (int g = 0; g < nb; ++g) u = u + pu[g];
+        tg.y[n] = silu_exact(s) * u;
+      } else {
+        tg.y[n] = (tg.res ? tg.res[n] : 0.f) + s;
+      }
+    }
+  }
+}
+
 // T > 1 (kernels_cpu.cpp:369-371, 401-403): the weight tile is dequantized (float(q) * s, one
 // rounding) and dotted in four interleaved chains (dot_f32_scalar); y = (res or 0) + dot.
 // One lane per weight row, four tokens per lane; x staged through LDS in chunks.
@@ -2253,6 +2309,29 @@ hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs&
 }
 
 hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_groups, hipStream_t s) {
+  if (a.T == 1 && dtype == WQ4 && a.H >= 1 && !(a.H & (a.H - 1)) && a.K == a.nb * kBlock) {
+    // one workgroup per H-row tile; the tile starts counted in tiles here
+    F32Args b = a;
+    const int nsel = swiglu ? 2 : 1, n = swiglu ? 1 : a.n_targets;
+    int tiles = 0;
+    for (int i = 0; i < n; ++i) {
+      b.tile_start[i] = tiles;
+      tiles += (a.tg[i].N + a.H - 1) / a.H;
+    }
+    b.tile_start[n] = tiles;
+    const size_t lds = ((size_t)((a.K + 3) & ~3) + (size_t)nsel * a.H * (a.nb + 1)) * 4;
+    if (lds > kMaxLds - 1024 || tiles < 1) return hipErrorInvalidValue;
+    static bool raised[2] = {false, false};  // the LDS limit, once per kernel
+    if (lds > 64 * 1024 && !raised[nsel - 1]) {
+      const void* k = swiglu ? (const void*)gemv_f32act_q4_kernel<true> : (const void*)gemv_f32act_q4_kernel<false>;
+      const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds - 1024);
+      if (e != hipSuccess) return e;
+      raised[nsel - 1] = true;
+    }
+    if (swiglu) gemv_f32act_q4_kernel<true><<<tiles, 256, lds, s>>>(b);
+    else gemv_f32act_q4_kernel<false><<<tiles, 256, lds, s>>>(b);
+    return hipGetLastError();
+  }
   if (a.T == 1) {
     const size_t lds = (size_t)((a.K + 3) & ~3) * 4;
     if (lds > 64 * 1024) return hipErrorInvalidValue;

@@ -162,7 +162,8 @@ def test_matmul_n_mixed_targets(ctx):
 @pytest.mark.parametrize("dt", [O.Q8, O.Q4])
 def test_matmul_f32act_exact(ctx, dt):
     r = rng(4 + dt)
-    shapes = [(48, 64), (37, 96), (130, 160), (960, 576)] + ([(37, 50), (20, 7)] if dt == O.Q8 else [])
+    shapes = [(48, 64), (37, 96), (130, 160), (960, 576)] + ([(37, 50), (20, 7)] if dt == O.Q8 else
+                                                              [(576, 1536), (70, 4096)])
     for n, k in shapes:
         w = weight(r, n, k, dt)
         dw = up(ctx, w)
@@ -181,6 +182,13 @@ def test_matmul_f32act_exact(ctx, dt):
                 assert bits_equal(got2, got)
             sg = ctx.swiglu(x, dw, du, act=E.ACT_F32)
             assert bits_equal(sg, O.cpu_swiglu(x, w, wu, act_quant=False))
+            # MATMUL_N: targets of different row counts in one launch
+            w2 = weight(r, n // 2 + 3, k, dt)
+            dw2 = up(ctx, w2)
+            got = ctx.matmul(x, [dw, dw2], [res, None], act=E.ACT_F32)
+            want = O.cpu_matmul(x, [w, w2], [res, None], act_quant=False)
+            assert bits_equal(got[0], want[0]) and bits_equal(got[1], want[1])
+            dw2.free()
 
 
 @pytest.mark.parametrize("dt", [O.Q8, O.Q4])
