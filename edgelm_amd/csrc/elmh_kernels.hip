@@ -1905,6 +1905,53 @@ __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
   }
 }
 
+// T == 1, q8: dot_q8's four chains (kernels_cpu.cpp:366-368: chain c takes i = c mod 4 in order,
+// the K mod 4 tail goes to chain 0) are independent, so four lanes take one row, a chain each,
+// and 64 rows share a workgroup; the lanes of a row read the same 16 weight bytes and each uses
+// its own four. ((s0 + s1) + (s2 + s3)) * ws is formed across the row's lanes.
+template <bool SW>
+__global__ __launch_bounds__(256) void gemv_f32act_q8_kernel(const F32Args a) {
+  extern __shared__ __align__(16) float f32q8_lds[];
+  const int K = a.K, K4 = K & ~3, H = a.H;
+  for (int i = threadIdx.x; i < K; i += 256) f32q8_lds[i] = a.x[i];
+  int ti = 0, grp = blockIdx.x;
+  if (!SW) {
+    while (ti + 1 < a.n_targets && grp >= a.tile_start[ti + 1]) ++ti;
+    grp -= a.tile_start[ti];
+  }
+  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  __syncthreads();
+  const int c = threadIdx.x & 3, n = grp * 64 + (threadIdx.x >> 2);  // rows past N: padding (rows_pad % 64 == 0)
+  const int64_t nbase = (int64_t)(n / H) * a.nb * H + (n % H);
+  float dots[SW ? 2 : 1];
+#pragma unroll
+  for (int sel = 0; sel < (SW ? 2 : 1); ++sel) {
+    const uint8_t* __restrict__ data = sel ? a.tg[1].data : tg.data;
+    float sc = 0.f;
+    int i = 0;
+    for (; i + 16 <= K4; i += 16) {
+      const uint4 w = *reinterpret_cast<const uint4*>(data + (nbase + (int64_t)(i >> 5) * H) * 32 + (i & 31));
+      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        sc = sc + f32q8_lds[i + 4 * j + c] * (float)(int8_t)((wd[j] >> (8 * c)) & 0xFF);
+    }
+    for (; i < K4; i += 4) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(data + (nbase + (int64_t)(i >> 5) * H) * 32 + (i & 31));
+      sc = sc + f32q8_lds[i + c] * (float)(int8_t)((w >> (8 * c)) & 0xFF);
+    }
+    if (c == 0)
+      for (; i < K; ++i)
+        sc = sc + f32q8_lds[i] * (float)*reinterpret_cast<const int8_t*>(data + (nbase + (int64_t)(i >> 5) * H) * 32 + (i & 31));
+    const float pair = sc + __shfl_xor(sc, 1);  // lane 0: s0 + s1, lane 2: s2 + s3
+    dots[sel] = (pair + __shfl_xor(pair, 2)) * (sel ? a.tg[1].scales : tg.scales)[n];
+  }
+  if (c == 0 && n < tg.N) {
+    if (SW) tg.y[n] = silu_exact(dots[0]) * dots[SW ? 1 : 0];
+    else tg.y[n] = (tg.res ? tg.res[n] : 0.f) + dots[0];
+  }
+}
+
 // T > 1 (kernels_cpu.cpp:369-371, 401-403): the weight tile is dequantized (float(q) * s, one
 // rounding) and dotted in four interleaved chains (dot_f32_scalar); y = (res or 0) + dot.
 // One lane per weight row, four tokens per lane; x staged through LDS in chunks.
@@ -2336,8 +2383,18 @@ hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_grou
     const size_t lds = (size_t)((a.K + 3) & ~3) * 4;
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     if (dtype == WQ8) {
-      if (swiglu) gemv_f32act_kernel<WQ8, true><<<total_groups, 256, lds, s>>>(a);
-      else gemv_f32act_kernel<WQ8, false><<<total_groups, 256, lds, s>>>(a);
+      // four lanes per row, 64 rows per workgroup; the group starts counted in 64-row groups here
+      F32Args b = a;
+      const int n = swiglu ? 1 : a.n_targets;
+      int groups = 0;
+      for (int i = 0; i < n; ++i) {
+        b.tile_start[i] = groups;
+        groups += (a.tg[i].N + 63) / 64;
+      }
+      b.tile_start[n] = groups;
+      if (groups < 1) return hipErrorInvalidValue;
+      if (swiglu) gemv_f32act_q8_kernel<true><<<groups, 256, lds, s>>>(b);
+      else gemv_f32act_q8_kernel<false><<<groups, 256, lds, s>>>(b);
     } else {
       if (swiglu) gemv_f32act_kernel<WQ4, true><<<total_groups, 256, lds, s>>>(a);
       else gemv_f32act_kernel<WQ4, false><<<total_groups, 256, lds, s>>>(a);
