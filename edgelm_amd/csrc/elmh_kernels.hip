@@ -1953,10 +1953,14 @@ __global__ __launch_bounds__(256) void gemv_f32act_q8_kernel(const F32Args a) {
 }
 
 // T > 1 (kernels_cpu.cpp:369-371, 401-403): the weight tile is dequantized (float(q) * s, one
-// rounding) and dotted in four interleaved chains (dot_f32_scalar); y = (res or 0) + dot.
-// One lane per weight row, four tokens per lane; x staged through LDS in chunks.
+// rounding) and dotted in dot_f32_scalar's four chains (chain c takes i = c mod 4 in order, the
+// K mod 4 tail goes to chain 0); y = (res or 0) + dot. The chains are independent, so four lanes
+// take one (row, 4 tokens) tile, a chain each: a workgroup is 64 rows x 4 tokens. x is staged
+// through LDS by chain ([token][chain][k / 4], so a lane reads four of its chain's values at
+// once), and the row's four lanes read the same 16 weight bytes, each using its own four.
 constexpr int kF32TT = 4;
-constexpr int kF32Chunk = 1024;
+constexpr int kF32Chunk = 2048;
+constexpr int kF32ChainStride = kF32Chunk / 4 + 4;  // floats; the +4 spreads the staging writes over banks
 
 template <int WDT>
 __device__ __forceinline__ float4 deq4(const uint8_t* __restrict__ data, const float* __restrict__ scales,
@@ -1995,84 +1999,111 @@ __device__ __forceinline__ float deq1(const uint8_t* __restrict__ data, const fl
   return (float)((int)(e >= 16 ? byte >> 4 : byte & 0x0F) - 8) * scales[item];
 }
 
+// four consecutive weights of chain c starting at element i (i % 16 == 0): elements i + c + 4m
+template <int WDT>
+__device__ __forceinline__ float4 deq_chain(const uint8_t* __restrict__ data, const float* __restrict__ scales,
+                                            int64_t nbase, int H, int i, int n, int c) {
+  const int64_t item = nbase + (int64_t)(i >> 5) * H;
+  float4 r;
+  if (WDT == WQ8) {
+    const uint4 w = *reinterpret_cast<const uint4*>(data + item * 32 + (i & 31));
+    const float s = scales[n];
+    r.x = (float)(int8_t)((w.x >> (8 * c)) & 0xFF) * s;
+    r.y = (float)(int8_t)((w.y >> (8 * c)) & 0xFF) * s;
+    r.z = (float)(int8_t)((w.z >> (8 * c)) & 0xFF) * s;
+    r.w = (float)(int8_t)((w.w >> (8 * c)) & 0xFF) * s;
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4*>(data + item * 16);  // the group: byte m holds m, m + 16
+    const int sh = 8 * c + ((i & 31) >= 16 ? 4 : 0);
+    const float s = scales[item];
+    r.x = (float)((int)((w.x >> sh) & 0x0F) - 8) * s;
+    r.y = (float)((int)((w.y >> sh) & 0x0F) - 8) * s;
+    r.z = (float)((int)((w.z >> sh) & 0x0F) - 8) * s;
+    r.w = (float)((int)((w.w >> sh) & 0x0F) - 8) * s;
+  }
+  return r;
+}
+
 template <int WDT, bool SW>
 __global__ __launch_bounds__(256) void gemm_f32act_kernel(const F32Args a) {
-  __shared__ __align__(16) float sx[kF32TT][kF32Chunk];
-  int ti = 0, grp = blockIdx.x;
+  __shared__ __align__(16) float sxp[kF32TT][4][kF32ChainStride];
+  int ti = 0, grp = blockIdx.y;
   if (!SW) {
-    while (ti + 1 < a.n_targets && (int)blockIdx.x >= a.tile_start[ti + 1]) ++ti;
-    grp = blockIdx.x - a.tile_start[ti];
+    while (ti + 1 < a.n_targets && grp >= a.tile_start[ti + 1]) ++ti;
+    grp -= a.tile_start[ti];
   }
   const GemvTarget& tg = a.tg[SW ? 0 : ti];
-  const int K = a.K, H = a.H, nb = a.nb, T = a.T;
-  const int t0 = blockIdx.y * kF32TT;
-  const int n = grp * 256 + threadIdx.x;
-  const bool live = n < tg.N;
-  const int nn = live ? n : 0;
-  const int64_t nbase = (int64_t)(nn / H) * nb * H + (nn % H);
-  float s[kF32TT][4], su[kF32TT][4];
+  const int K = a.K, K4 = K & ~3, H = a.H, nb = a.nb, T = a.T;
+  const int t0 = blockIdx.x * kF32TT, c = threadIdx.x & 3;
+  const int n = grp * 64 + (threadIdx.x >> 2);  // rows past N: padding (rows_pad % 64 == 0)
+  const int64_t nbase = (int64_t)(n / H) * nb * H + (n % H);
+  float s[kF32TT], su[kF32TT];
 #pragma unroll
-  for (int t = 0; t < kF32TT; ++t)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      s[t][c] = 0.f;
-      su[t][c] = 0.f;
-    }
-  const int kmain = K & ~3;
-  for (int k0 = 0; k0 < K; k0 += kF32Chunk) {
-    const int klen = min(kF32Chunk, K - k0);
+  for (int t = 0; t < kF32TT; ++t) s[t] = su[t] = 0.f;
+  for (int k0 = 0; k0 < K4; k0 += kF32Chunk) {
+    const int klen = min(kF32Chunk, K4 - k0);
     __syncthreads();
     for (int i = threadIdx.x; i < kF32TT * kF32Chunk; i += 256) {
       const int t = i / kF32Chunk, k = i - t * kF32Chunk;
-      sx[t][k] = (t0 + t < T && k < klen) ? a.x[(int64_t)(t0 + t) * K + k0 + k] : 0.f;
+      if (k < klen) sxp[t][k & 3][k >> 2] = t0 + t < T ? a.x[(int64_t)(t0 + t) * K + k0 + k] : 0.f;
     }
     __syncthreads();
-    if (!live) continue;
-    const int kend = min(k0 + klen, kmain);
-    for (int i = k0; i < kend; i += 4) {
-      const float4 w = deq4<WDT>(tg.data, tg.scales, nbase, H, i, nn);
+    int i = k0;
+    for (; i + 16 <= k0 + klen; i += 16) {
+      const float4 w = deq_chain<WDT>(tg.data, tg.scales, nbase, H, i, n, c);
       float4 wu = w;
-      if (SW) wu = deq4<WDT>(a.tg[1].data, a.tg[1].scales, nbase, H, i, nn);
+      if (SW) wu = deq_chain<WDT>(a.tg[1].data, a.tg[1].scales, nbase, H, i, n, c);
 #pragma unroll
       for (int t = 0; t < kF32TT; ++t) {
-        const float4 xv = *reinterpret_cast<const float4*>(&sx[t][i - k0]);
-        s[t][0] = s[t][0] + xv.x * w.x;
-        s[t][1] = s[t][1] + xv.y * w.y;
-        s[t][2] = s[t][2] + xv.z * w.z;
-        s[t][3] = s[t][3] + xv.w * w.w;
+        const float4 xv = *reinterpret_cast<const float4*>(&sxp[t][c][(i - k0) >> 2]);
+        s[t] = s[t] + xv.x * w.x;
+        s[t] = s[t] + xv.y * w.y;
+        s[t] = s[t] + xv.z * w.z;
+        s[t] = s[t] + xv.w * w.w;
         if (SW) {
-          su[t][0] = su[t][0] + xv.x * wu.x;
-          su[t][1] = su[t][1] + xv.y * wu.y;
-          su[t][2] = su[t][2] + xv.z * wu.z;
-          su[t][3] = su[t][3] + xv.w * wu.w;
+          su[t] = su[t] + xv.x * wu.x;
+          su[t] = su[t] + xv.y * wu.y;
+          su[t] = su[t] + xv.z * wu.z;
+          su[t] = su[t] + xv.w * wu.w;
         }
       }
     }
-    for (int i = max(k0, kmain); i < k0 + klen; ++i) {  // tail (K % 4) into the first chain
-      const float w = deq1<WDT>(tg.data, tg.scales, nbase, H, i, nn);
-      const float wu = SW ? deq1<WDT>(a.tg[1].data, a.tg[1].scales, nbase, H, i, nn) : w;
+    for (; i < k0 + klen; i += 4) {  // the last chunk's steps past its last 16-element run
+      const float w = deq1<WDT>(tg.data, tg.scales, nbase, H, i + c, n);
+      const float wu = SW ? deq1<WDT>(a.tg[1].data, a.tg[1].scales, nbase, H, i + c, n) : w;
 #pragma unroll
       for (int t = 0; t < kF32TT; ++t) {
-        s[t][0] = s[t][0] + sx[t][i - k0] * w;
-        if (SW) su[t][0] = su[t][0] + sx[t][i - k0] * wu;
+        const float xv = sxp[t][c][(i - k0) >> 2];
+        s[t] = s[t] + xv * w;
+        if (SW) su[t] = su[t] + xv * wu;
       }
     }
   }
-  if (!live) return;
+  if (c == 0)
+    for (int i = K4; i < K; ++i) {  // tail (K % 4) into the first chain
+      const float w = deq1<WDT>(tg.data, tg.scales, nbase, H, i, n);
+      const float wu = SW ? deq1<WDT>(a.tg[1].data, a.tg[1].scales, nbase, H, i, n) : w;
+#pragma unroll
+      for (int t = 0; t < kF32TT; ++t) {
+        const float xv = t0 + t < T ? a.x[(int64_t)(t0 + t) * K + i] : 0.f;
+        s[t] = s[t] + xv * w;
+        if (SW) su[t] = su[t] + xv * wu;
+      }
+    }
 #pragma unroll
   for (int t = 0; t < kF32TT; ++t) {
-    const int tt = t0 + t;
-    if (tt >= T) break;
-    const float dot = (s[t][0] + s[t][1]) + (s[t][2] + s[t][3]);
+    const float p = s[t] + __shfl_xor(s[t], 1);  // lane 0: s0 + s1, lane 2: s2 + s3
+    const float dot = p + __shfl_xor(p, 2);
     float out;
     if (SW) {
+      const float pu = su[t] + __shfl_xor(su[t], 1);
       const float g = 0.f + dot;
-      const float u = 0.f + ((su[t][0] + su[t][1]) + (su[t][2] + su[t][3]));
+      const float u = 0.f + (pu + __shfl_xor(pu, 2));
       out = silu_exact(g) * u;
     } else {
-      out = (tg.res ? tg.res[(int64_t)tt * tg.N + n] : 0.f) + dot;
+      out = (t0 + t < T && tg.res ? tg.res[(int64_t)(t0 + t) * tg.N + n] : 0.f) + dot;
     }
-    tg.y[(int64_t)tt * tg.N + n] = out;
+    if (c == 0 && n < tg.N && t0 + t < T) tg.y[(int64_t)(t0 + t) * tg.N + n] = out;
   }
 }
 
@@ -2400,13 +2431,23 @@ hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_grou
       else gemv_f32act_kernel<WQ4, false><<<total_groups, 256, lds, s>>>(a);
     }
   } else {
-    dim3 grid(total_groups, (a.T + kF32TT - 1) / kF32TT);
+    // grid x: 4-token tiles (consecutive workgroups share their weight rows), y: 64-row groups
+    F32Args b = a;
+    const int n = swiglu ? 1 : a.n_targets;
+    int groups = 0;
+    for (int i = 0; i < n; ++i) {
+      b.tile_start[i] = groups;
+      groups += (a.tg[i].N + 63) / 64;
+    }
+    b.tile_start[n] = groups;
+    if (groups < 1 || groups > 65535) return hipErrorInvalidValue;
+    const dim3 grid((a.T + kF32TT - 1) / kF32TT, groups);
     if (dtype == WQ8) {
-      if (swiglu) gemm_f32act_kernel<WQ8, true><<<grid, 256, 0, s>>>(a);
-      else gemm_f32act_kernel<WQ8, false><<<grid, 256, 0, s>>>(a);
+      if (swiglu) gemm_f32act_kernel<WQ8, true><<<grid, 256, 0, s>>>(b);
+      else gemm_f32act_kernel<WQ8, false><<<grid, 256, 0, s>>>(b);
     } else {
-      if (swiglu) gemm_f32act_kernel<WQ4, true><<<grid, 256, 0, s>>>(a);
-      else gemm_f32act_kernel<WQ4, false><<<grid, 256, 0, s>>>(a);
+      if (swiglu) gemm_f32act_kernel<WQ4, true><<<grid, 256, 0, s>>>(b);
+      else gemm_f32act_kernel<WQ4, false><<<grid, 256, 0, s>>>(b);
     }
   }
   return hipGetLastError();
