@@ -1955,10 +1955,12 @@ __global__ __launch_bounds__(256) void gemv_f32act_q8_kernel(const F32Args a) {
 // T > 1 (kernels_cpu.cpp:369-371, 401-403): the weight tile is dequantized (float(q) * s, one
 // rounding) and dotted in dot_f32_scalar's four chains (chain c takes i = c mod 4 in order, the
 // K mod 4 tail goes to chain 0); y = (res or 0) + dot. The chains are independent, so four lanes
-// take one (row, 4 tokens) tile, a chain each: a workgroup is 64 rows x 4 tokens. x is staged
+// take one (row, kF32TT tokens) tile, a chain each: a workgroup is 64 rows x kF32TT tokens (2
+// tokens measured faster than 4 or 8 at the 135M model's 128-token prefill, which has too few
+// (row, token) pairs to fill the chip with more tokens per lane). x is staged
 // through LDS by chain ([token][chain][k / 4], so a lane reads four of its chain's values at
 // once), and the row's four lanes read the same 16 weight bytes, each using its own four.
-constexpr int kF32TT = 4;
+constexpr int kF32TT = 2;
 constexpr int kF32Chunk = 2048;
 constexpr int kF32ChainStride = kF32Chunk / 4 + 4;  // floats; the +4 spreads the staging writes over banks
 
@@ -2431,7 +2433,7 @@ hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_grou
       else gemv_f32act_kernel<WQ4, false><<<total_groups, 256, lds, s>>>(a);
     }
   } else {
-    // grid x: 4-token tiles (consecutive workgroups share their weight rows), y: 64-row groups
+    // grid x: kF32TT-token tiles (consecutive workgroups share their weight rows), y: 64-row groups
     F32Args b = a;
     const int n = swiglu ? 1 : a.n_targets;
     int groups = 0;
