@@ -277,7 +277,7 @@ int run_gemm_group(elmh_ctx* c, const int8_t* xq, const float* xd, int T, int Tp
 }
 
 int run_f32_group(elmh_ctx* c, const float* x, int T, int64_t K, const std::vector<int>& idx, elmh_weight* const* w,
-                  float* const* y, const float* const* res) {
+                  float* const* y, const float* const* res, const float* nw = nullptr, float eps = 0.f) {
   for (size_t i0 = 0; i0 < idx.size(); i0 += kMaxTargets) {
     F32Args a{};
     const size_t n = std::min<size_t>(kMaxTargets, idx.size() - i0);
@@ -297,6 +297,8 @@ int run_f32_group(elmh_ctx* c, const float* x, int T, int64_t K, const std::vect
     a.T = T;
     a.K = (int)K;
     a.nb = (int)w0.nb;
+    a.nw = nw;  // set only when f32_norm_fusable holds
+    a.eps = eps;
     HIP_OR_FAIL(c, launch_f32act(w0.dtype, 0, a, groups, c->stream));
   }
   return ELMH_OK;
@@ -465,6 +467,8 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
     a.T = T;
     a.K = (int)K;
     a.nb = (int)g.nb;
+    a.nw = nw;  // set only when f32_norm_fusable holds
+    a.eps = eps;
     HIP_OR_FAIL(c, launch_f32act(g.dtype, 1, a, groups, c->stream));
     return ELMH_OK;
   }
@@ -549,6 +553,17 @@ bool block_gemm(int T, int64_t K, int n, const elmh_weight* const* w, int nsel, 
   int nt = 4;
   for (int i = 0; i < n; ++i) nt = std::min(nt, gemv_tokens(w[i]->w, nsel, qin));
   return T > nt;
+}
+
+// True if RMSNORM of x can run inside the f32-activation GEMV that consumes it (one token, q4
+// targets of the group-parallel q4 GEMV's layout)
+bool f32_norm_fusable(int T, int64_t K, int n, const elmh_weight* const* w, int nsel, int act) {
+  if (act != ELMH_ACT_F32 || K > 8192) return false;
+  for (int i = 0; i < n; ++i)
+    if (w[i]->w.dtype != WQ4 || w[i]->w.H != w[0]->w.H ||
+        !f32act_norm_ok(T, (int)K, (int)w[i]->w.nb, w[i]->w.H, nsel))
+      return false;
+  return true;
 }
 
 bool norm_gemm(int T, int64_t K, int n, const elmh_weight* const* w, int nsel, int act) {
@@ -836,6 +851,11 @@ int elmh_rmsnorm_matmul_dev(elmh_ctx* c, const float* x, const float* norm_w, fl
       if ((rc = run_gemv_group(c, x, nullptr, nullptr, nullptr, T, K, grp, w, y, res, false, norm_w, eps))) return rc;
     return ELMH_OK;
   }
+  if (f32_norm_fusable(T, K, n, w, 1, act)) {
+    for (const auto& grp : by_dtype(n, w))
+      if ((rc = run_f32_group(c, x, T, K, grp, w, y, res, norm_w, eps))) return rc;
+    return ELMH_OK;
+  }
   if (norm_gemm(T, K, n, w, 1, act)) {  // the block-scale GEMM: RMSNORM inside its quantizer launch
     int Tpad;
     ActBufs ab;
@@ -857,7 +877,8 @@ int elmh_rmsnorm_swiglu_dev(elmh_ctx* c, const float* x, const float* norm_w, fl
   DeviceGuard g(c);
   const elmh_weight* const ws[2] = {wg, wu};
   if (wg->w.dtype == wu->w.dtype && wg->w.H == wu->w.H && wg->w.rows == wu->w.rows && wg->w.cols == K &&
-      wu->w.cols == K && (norm_fusable(T, K, 2, ws, 2, act) || norm_gemm(T, K, 2, ws, 2, act)))
+      wu->w.cols == K &&
+      (norm_fusable(T, K, 2, ws, 2, act) || norm_gemm(T, K, 2, ws, 2, act) || f32_norm_fusable(T, K, 2, ws, 2, act)))
     return run_swiglu(c, x, T, K, wg, wu, y, act, mode, norm_w, eps);
   const float* xn;
   int rc;

@@ -1854,14 +1854,52 @@ __global__ __launch_bounds__(256) void gemv_f32act_kernel(const F32Args a) {
 // Every (selection, row, group) item is (g0 + g1) * ws_g, g0 / g1 the in-order 16-term sums of the
 // group's low / high nibbles against x, and goes to LDS; then one lane per row adds its row's items
 // in group order (s = s + p_g from s = 0, as dot_q4 does) and applies the epilogue.
+// With a.nw, x is first RMSNORM'd in the workgroup in rmsnorm_kernel's float order (four strided
+// sums of squares, (s0 + s1) + (s2 + s3), inv = 1 / sqrt(ss / K + eps), (x * inv) * w), so that
+// RMSNORM and the matmul after it take one launch.
 template <bool SW>
 __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
   extern __shared__ __align__(16) float f32q4_lds[];
+  __shared__ float inv_s;
   constexpr int NSEL = SW ? 2 : 1;
   const int K = a.K, nb = a.nb, H = a.H, lgH = __builtin_ctz(H), pst = nb + 1;
   float* const sx = f32q4_lds;                // [K]
   float* const P = f32q4_lds + ((K + 3) & ~3);  // [NSEL][H][nb + 1]
   for (int i = threadIdx.x; i < K; i += 256) sx[i] = a.x[i];
+  if (a.nw) {
+    // squares as [accumulator][rowlen] (zero-padded: adding +0.0 to a sum of squares changes
+    // nothing); K % 4 == 0 here (K = 32 nb)
+    float* const sq = f32q4_lds + ((((K + 3) & ~3) + NSEL * H * pst + 3) & ~3);
+    const int K4 = K >> 2, rowlen = (K4 + 31) & ~31;
+    for (int i = threadIdx.x; i < 4 * rowlen; i += 256) {
+      const int c = i / rowlen, j = i - c * rowlen;
+      const float v = j < K4 ? a.x[4 * j + c] : 0.f;
+      sq[i] = v * v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 4) {
+      const float4* row = reinterpret_cast<const float4*>(sq + threadIdx.x * rowlen);
+      float s = 0.f;
+      for (int q0 = 0; q0 < (rowlen >> 2); q0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = row[q0 + i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          s = s + v[i].x;
+          s = s + v[i].y;
+          s = s + v[i].z;
+          s = s + v[i].w;
+        }
+      }
+      const float s01 = s + dpp_f<kDppQuadXor1>(s);  // lane 0: s0 + s1, lane 2: s2 + s3
+      const float ss = s01 + dpp_f<kDppQuadXor2>(s01);
+      if (threadIdx.x == 0) inv_s = 1.0f / sqrtf(ss / (float)K + a.eps);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    for (int i = threadIdx.x; i < K; i += 256) sx[i] = (sx[i] * inv) * a.nw[i];
+  }
   int ti = 0, tile = blockIdx.x;
   if (!SW) {
     while (ti + 1 < a.n_targets && tile >= a.tile_start[ti + 1]) ++ti;
@@ -2388,19 +2426,31 @@ hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs&
   return swiglu ? gemm_go<WQ4, true, false>(a, total_tiles, s) : gemm_go<WQ4, false, false>(a, total_tiles, s);
 }
 
+// LDS of gemv_f32act_q4_kernel: x, the (selection, row, group) products and, with RMSNORM, the squares
+static size_t f32q4_lds_bytes(int K, int nb, int H, int nsel, bool norm) {
+  const size_t base = ((size_t)((K + 3) & ~3) + (size_t)nsel * H * (nb + 1) + 3) & ~(size_t)3;
+  return (base + (norm ? 4 * (size_t)(((K >> 2) + 31) & ~31) : 0)) * sizeof(float);
+}
+
+bool f32act_norm_ok(int T, int K, int nb, int H, int nsel) {
+  return T == 1 && H >= 1 && !(H & (H - 1)) && K == nb * kBlock &&
+         f32q4_lds_bytes(K, nb, H, nsel, true) <= kMaxLds - 1024;
+}
+
 hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_groups, hipStream_t s) {
-  if (a.T == 1 && dtype == WQ4 && a.H >= 1 && !(a.H & (a.H - 1)) && a.K == a.nb * kBlock) {
+  const int nsel = swiglu ? 2 : 1;
+  if (a.T == 1 && dtype == WQ4 && f32act_norm_ok(a.T, a.K, a.nb, a.H, nsel)) {
     // one workgroup per H-row tile; the tile starts counted in tiles here
     F32Args b = a;
-    const int nsel = swiglu ? 2 : 1, n = swiglu ? 1 : a.n_targets;
+    const int n = swiglu ? 1 : a.n_targets;
     int tiles = 0;
     for (int i = 0; i < n; ++i) {
       b.tile_start[i] = tiles;
       tiles += (a.tg[i].N + a.H - 1) / a.H;
     }
     b.tile_start[n] = tiles;
-    const size_t lds = ((size_t)((a.K + 3) & ~3) + (size_t)nsel * a.H * (a.nb + 1)) * 4;
-    if (lds > kMaxLds - 1024 || tiles < 1) return hipErrorInvalidValue;
+    const size_t lds = f32q4_lds_bytes(a.K, a.nb, a.H, nsel, a.nw != nullptr);
+    if (tiles < 1) return hipErrorInvalidValue;
     static bool raised[2] = {false, false};  // the LDS limit, once per kernel
     if (lds > 64 * 1024 && !raised[nsel - 1]) {
       const void* k = swiglu ? (const void*)gemv_f32act_q4_kernel<true> : (const void*)gemv_f32act_q4_kernel<false>;
@@ -2412,6 +2462,7 @@ hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_grou
     else gemv_f32act_q4_kernel<false><<<tiles, 256, lds, s>>>(b);
     return hipGetLastError();
   }
+  if (a.nw) return hipErrorInvalidValue;  // RMSNORM is applied by the q4 GEMV above only
   if (a.T == 1) {
     const size_t lds = (size_t)((a.K + 3) & ~3) * 4;
     if (lds > 64 * 1024) return hipErrorInvalidValue;

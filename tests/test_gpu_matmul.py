@@ -476,6 +476,40 @@ def test_rmsnorm_fused_block_gemm_wide_values(ctx, dt):
 
 
 @pytest.mark.parametrize("dt", [O.Q8, O.Q4])
+def test_rmsnorm_fused_f32act(ctx, dt):
+    """f32 activations: at one token the q4 GEMV's workgroups normalize x themselves (q8, and q4
+    at T > 1, go through scratch); values spread over 24 binades so that the sum of squares'
+    order shows. Bit-identical to edgelm's cpu::rmsnorm then the cpu backend's f32-activation
+    matmul / SwiGLU (through the oracle)."""
+    r = rng(25)
+    for T, K, N in [(1, 576, 960), (1, 32, 40), (1, 1536, 576), (1, 4096, 130), (1, 8192, 48), (2, 576, 64),
+                    (3, 64, 96)]:
+        print(f"[gpu] rmsnorm f32act dt={dt} T={T} K={K} N={N}", flush=True)
+        x = (r.normal(0, 1, (T, K)) * np.exp2(r.integers(-12, 12, (T, K)))).astype(np.float32)
+        nw = r.normal(1, 0.3, K).astype(np.float32)
+        res = r.normal(0, 1, (T, N)).astype(np.float32)
+        w, w2 = weight(r, N, K, dt), weight(r, N // 2 + 3, K, dt)
+        xn = O.rmsnorm(x, nw, 1e-5)
+        bx, bnw, bres = ctx.buffer(x.nbytes), ctx.buffer(nw.nbytes), ctx.buffer(res.nbytes)
+        bx.upload(x)
+        bnw.upload(nw)
+        bres.upload(res)
+        by, by2 = ctx.buffer(T * N * 4), ctx.buffer(T * (N // 2 + 3) * 4)
+        dw, dw2 = up(ctx, w), up(ctx, w2)
+        ctx.rmsnorm_matmul_dev(bx.ptr, bnw.ptr, 1e-5, T, K, [dw, dw2], [by.ptr, by2.ptr], [bres.ptr, 0],
+                               act=E.ACT_F32)
+        want = O.cpu_matmul(xn, [w, w2], [res, None], act_quant=False)
+        assert bits_equal(by.download((T, N), np.float32), want[0]), f"T={T} K={K}"
+        assert bits_equal(by2.download((T, N // 2 + 3), np.float32), want[1]), f"T={T} K={K}"
+        wg, wu = weight(r, N, K, dt), weight(r, N, K, dt)
+        dg, du = up(ctx, wg), up(ctx, wu)
+        ctx.rmsnorm_swiglu_dev(bx.ptr, bnw.ptr, 1e-5, T, K, dg, du, by.ptr, act=E.ACT_F32)
+        assert bits_equal(by.download((T, N), np.float32), O.cpu_swiglu(xn, wg, wu, act_quant=False)), f"T={T} K={K}"
+        for b in (bx, bnw, bres, by, by2, dw, dw2, dg, du):
+            b.free()
+
+
+@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
 def test_rmsnorm_fused_into_matmul(ctx, dt):
     """elmh_rmsnorm_matmul_dev / elmh_rmsnorm_swiglu_dev: bit-identical to RMSNORM then the matmul
     (edgelm's cpu::rmsnorm and cpu backend matmul, through the oracle) on every path: each GEMV
