@@ -1865,6 +1865,29 @@ __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
   const int K = a.K, nb = a.nb, H = a.H, lgH = __builtin_ctz(H), pst = nb + 1;
   float* const sx = f32q4_lds;                // [K]
   float* const P = f32q4_lds + ((K + 3) & ~3);  // [NSEL][H][nb + 1]
+  int ti = 0, tile = blockIdx.x;
+  if (!SW) {
+    while (ti + 1 < a.n_targets && tile >= a.tile_start[ti + 1]) ++ti;
+    tile -= a.tile_start[ti];
+  }
+  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  const int per_sel = H * nb, items = NSEL * per_sel;
+  // the first item's weights go out before x is staged, so that the two loads overlap
+  const auto item_of = [&](int it, int& sel, int& g, int& r) -> int64_t {
+    sel = SW && it >= per_sel ? 1 : 0;
+    const int j = it - sel * per_sel;
+    g = j >> lgH;
+    r = j & (H - 1);
+    return ((int64_t)tile * nb + g) * H + r;  // rows past N: the padding's items
+  };
+  uint4 wq0 = make_uint4(0, 0, 0, 0);
+  float ws0 = 0.f;
+  if ((int)threadIdx.x < items) {
+    int sel, g, r;
+    const int64_t item = item_of(threadIdx.x, sel, g, r);
+    wq0 = *reinterpret_cast<const uint4*>((sel ? a.tg[1].data : tg.data) + item * 16);
+    ws0 = (sel ? a.tg[1].scales : tg.scales)[item];
+  }
   for (int i = threadIdx.x; i < K; i += 256) sx[i] = a.x[i];
   if (a.nw) {
     // squares as [accumulator][rowlen] (zero-padded: adding +0.0 to a sum of squares changes
@@ -1900,19 +1923,16 @@ __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
     const float inv = inv_s;
     for (int i = threadIdx.x; i < K; i += 256) sx[i] = (sx[i] * inv) * a.nw[i];
   }
-  int ti = 0, tile = blockIdx.x;
-  if (!SW) {
-    while (ti + 1 < a.n_targets && tile >= a.tile_start[ti + 1]) ++ti;
-    tile -= a.tile_start[ti];
-  }
-  const GemvTarget& tg = a.tg[SW ? 0 : ti];
   __syncthreads();
-  const int per_sel = H * nb, items = NSEL * per_sel;
   for (int it = threadIdx.x; it < items; it += 256) {
-    const int sel = SW && it >= per_sel ? 1 : 0, j = it - sel * per_sel, g = j >> lgH, r = j & (H - 1);
-    const int64_t item = ((int64_t)tile * nb + g) * H + r;  // rows past N: the padding's items
-    const uint4 wq = *reinterpret_cast<const uint4*>((sel ? a.tg[1].data : tg.data) + item * 16);
-    const float ws = (sel ? a.tg[1].scales : tg.scales)[item];
+    int sel, g, r;
+    const int64_t item = item_of(it, sel, g, r);
+    uint4 wq = wq0;
+    float ws = ws0;
+    if (it != (int)threadIdx.x) {
+      wq = *reinterpret_cast<const uint4*>((sel ? a.tg[1].data : tg.data) + item * 16);
+      ws = (sel ? a.tg[1].scales : tg.scales)[item];
+    }
     const uint32_t wd[4] = {wq.x, wq.y, wq.z, wq.w};
     const float* const xs = sx + g * 32;
     float g0 = 0.f, g1 = 0.f;
