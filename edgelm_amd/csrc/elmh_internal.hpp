@@ -112,6 +112,7 @@ struct F32Args {
   int T, K, nb;
   const float* nw;  // T == 1, q4: x is RMSNORM's input, nw [K] its weight, eps its epsilon (else null)
   float eps;
+  int rt;           // set by launch_f32act: rows per workgroup of the group-parallel q4 GEMV (divides H)
 };
 
 // ---------------------------------------------------------------- launchers (elmh_kernels.hip)

@@ -1862,23 +1862,24 @@ __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
   extern __shared__ __align__(16) float f32q4_lds[];
   __shared__ float inv_s;
   constexpr int NSEL = SW ? 2 : 1;
-  const int K = a.K, nb = a.nb, H = a.H, lgH = __builtin_ctz(H), pst = nb + 1;
+  const int K = a.K, nb = a.nb, H = a.H, RT = a.rt, lgRT = __builtin_ctz(RT), pst = nb + 1;
   float* const sx = f32q4_lds;                // [K]
-  float* const P = f32q4_lds + ((K + 3) & ~3);  // [NSEL][H][nb + 1]
+  float* const P = f32q4_lds + ((K + 3) & ~3);  // [NSEL][RT][nb + 1]
   int ti = 0, tile = blockIdx.x;
   if (!SW) {
     while (ti + 1 < a.n_targets && tile >= a.tile_start[ti + 1]) ++ti;
     tile -= a.tile_start[ti];
   }
   const GemvTarget& tg = a.tg[SW ? 0 : ti];
-  const int per_sel = H * nb, items = NSEL * per_sel;
+  const int per_sel = RT * nb, items = NSEL * per_sel, n0 = tile * RT;
+  const int64_t ibase = (int64_t)(n0 / H) * nb * H + n0 % H;  // item (row n0, group 0)
   // the first item's weights go out before x is staged, so that the two loads overlap
   const auto item_of = [&](int it, int& sel, int& g, int& r) -> int64_t {
     sel = SW && it >= per_sel ? 1 : 0;
     const int j = it - sel * per_sel;
-    g = j >> lgH;
-    r = j & (H - 1);
-    return ((int64_t)tile * nb + g) * H + r;  // rows past N: the padding's items
+    g = j >> lgRT;
+    r = j & (RT - 1);
+    return ibase + (int64_t)g * H + r;  // rows past N: the padding's items
   };
   uint4 wq0 = make_uint4(0, 0, 0, 0);
   float ws0 = 0.f;
@@ -1892,7 +1893,7 @@ __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
   if (a.nw) {
     // squares as [accumulator][rowlen] (zero-padded: adding +0.0 to a sum of squares changes
     // nothing); K % 4 == 0 here (K = 32 nb)
-    float* const sq = f32q4_lds + ((((K + 3) & ~3) + NSEL * H * pst + 3) & ~3);
+    float* const sq = f32q4_lds + ((((K + 3) & ~3) + NSEL * RT * pst + 3) & ~3);
     const int K4 = K >> 2, rowlen = (K4 + 31) & ~31;
     for (int i = threadIdx.x; i < 4 * rowlen; i += 256) {
       const int c = i / rowlen, j = i - c * rowlen;
@@ -1942,17 +1943,17 @@ __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
       g0 = g0 + xs[i] * (float)((int)(byte & 0x0F) - 8);
       g1 = g1 + xs[16 + i] * (float)((int)(byte >> 4) - 8);
     }
-    P[(sel * H + r) * pst + g] = (g0 + g1) * ws;
+    P[(sel * RT + r) * pst + g] = (g0 + g1) * ws;
   }
   __syncthreads();
-  if ((int)threadIdx.x < H) {
-    const int r = threadIdx.x, n = tile * H + r;
+  if ((int)threadIdx.x < RT) {
+    const int r = threadIdx.x, n = n0 + r;
     if (n < tg.N) {
       const float* const pr = P + r * pst;
       float s = 0.f;
       for (int g = 0; g < nb; ++g) s = s + pr[g];
       if (SW) {
-        const float* const pu = P + (H + r) * pst;
+        const float* const pu = P + (RT + r) * pst;
         float u = 0.f;
         for (int g = 0; g < nb; ++g) u = u + pu[g];
         tg.y[n] = silu_exact(s) * u;
@@ -2460,16 +2461,24 @@ bool f32act_norm_ok(int T, int K, int nb, int H, int nsel) {
 hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_groups, hipStream_t s) {
   const int nsel = swiglu ? 2 : 1;
   if (a.T == 1 && dtype == WQ4 && f32act_norm_ok(a.T, a.K, a.nb, a.H, nsel)) {
-    // one workgroup per H-row tile; the tile starts counted in tiles here
+    // one workgroup per tile of rt rows (rt divides H); the tile starts counted in tiles here.
+    // rt: the most rows whose items take one pass of the workgroup's threads, raised while that
+    // makes more than 1024 workgroups (each one stages all of x)
     F32Args b = a;
     const int n = swiglu ? 1 : a.n_targets;
+    int rows = 0;
+    for (int i = 0; i < n; ++i) rows += a.tg[i].N;
+    int rt = a.H;
+    while (rt > 1 && nsel * rt * a.nb > 256) rt >>= 1;
+    while (rt < a.H && (rows + rt - 1) / rt > 1024) rt <<= 1;
+    b.rt = rt;
     int tiles = 0;
     for (int i = 0; i < n; ++i) {
       b.tile_start[i] = tiles;
-      tiles += (a.tg[i].N + a.H - 1) / a.H;
+      tiles += (a.tg[i].N + rt - 1) / rt;
     }
     b.tile_start[n] = tiles;
-    const size_t lds = f32q4_lds_bytes(a.K, a.nb, a.H, nsel, a.nw != nullptr);
+    const size_t lds = f32q4_lds_bytes(a.K, a.nb, rt, nsel, a.nw != nullptr);
     if (tiles < 1) return hipErrorInvalidValue;
     static bool raised[2] = {false, false};  // the LDS limit, once per kernel
     if (lds > 64 * 1024 && !raised[nsel - 1]) {
