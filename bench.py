@@ -386,6 +386,16 @@ def e2e_headline(path, steps, warmup, P=128):
                           "greedy_tokens_match": bool(np.array_equal(rm["tokens"], r["tokens"]))}
     log(f"e2e hip-matmul,cpu: decode {out['matmul_only']['decode_tok_s']:.1f} tok/s, TTFT {rm['ttft_ms']:.2f} ms, "
         f"tokens match: {out['matmul_only']['greedy_tokens_match']}")
+    # edgelm's f32-activation mode (act_quant off: the f32 x dequantized-weight dot products), whole model
+    # on the GPU as above; its tokens follow other numerics than the int8 run's, so they are not compared
+    s = host.Session(m, "hip,cpu", threads=threads, max_ctx=P + warmup + steps + 8, max_batch=P, act_quant=False)
+    s.bench(prompt, 2, 4)
+    rf = s.bench(prompt, warmup, steps)
+    s.close()
+    out["f32_activations"] = {"decode_tok_s": steps / (rf["decode_ms"] / 1e3), "ttft_ms": rf["ttft_ms"],
+                              "backends": "hip,cpu", "act_quant": False}
+    log(f"e2e hip,cpu f32 activations: decode {out['f32_activations']['decode_tok_s']:.1f} tok/s, "
+        f"TTFT {rf['ttft_ms']:.2f} ms")
     m.close()
     return out, r["tokens"]
 
