@@ -2060,30 +2060,37 @@ __device__ __forceinline__ float deq1(const uint8_t* __restrict__ data, const fl
   return (float)((int)(e >= 16 ? byte >> 4 : byte & 0x0F) - 8) * scales[item];
 }
 
-// four consecutive weights of chain c starting at element i (i % 16 == 0): elements i + c + 4m
+// The 16 weight bytes that hold elements i .. i + 15 of row n (i % 16 == 0) and their scale
+struct WChunk {
+  uint4 q;
+  float s;
+};
 template <int WDT>
-__device__ __forceinline__ float4 deq_chain(const uint8_t* __restrict__ data, const float* __restrict__ scales,
-                                            int64_t nbase, int H, int i, int n, int c) {
+__device__ __forceinline__ WChunk load_chunk(const uint8_t* __restrict__ data, const float* __restrict__ scales,
+                                             int64_t nbase, int H, int i, int n) {
   const int64_t item = nbase + (int64_t)(i >> 5) * H;
+  if (WDT == WQ8) return {*reinterpret_cast<const uint4*>(data + item * 32 + (i & 31)), scales[n]};
+  return {*reinterpret_cast<const uint4*>(data + item * 16), scales[item]};  // the group: byte m holds m, m + 16
+}
+// chain c's four dequantized weights of the chunk: elements i + c + 4m, m = 0 .. 3
+template <int WDT>
+__device__ __forceinline__ float4 chunk_chain(const WChunk& w, int i, int c) {
   float4 r;
   if (WDT == WQ8) {
-    const uint4 w = *reinterpret_cast<const uint4*>(data + item * 32 + (i & 31));
-    const float s = scales[n];
-    r.x = (float)(int8_t)((w.x >> (8 * c)) & 0xFF) * s;
-    r.y = (float)(int8_t)((w.y >> (8 * c)) & 0xFF) * s;
-    r.z = (float)(int8_t)((w.z >> (8 * c)) & 0xFF) * s;
-    r.w = (float)(int8_t)((w.w >> (8 * c)) & 0xFF) * s;
+    r.x = (float)(int8_t)((w.q.x >> (8 * c)) & 0xFF) * w.s;
+    r.y = (float)(int8_t)((w.q.y >> (8 * c)) & 0xFF) * w.s;
+    r.z = (float)(int8_t)((w.q.z >> (8 * c)) & 0xFF) * w.s;
+    r.w = (float)(int8_t)((w.q.w >> (8 * c)) & 0xFF) * w.s;
   } else {
-    const uint4 w = *reinterpret_cast<const uint4*>(data + item * 16);  // the group: byte m holds m, m + 16
     const int sh = 8 * c + ((i & 31) >= 16 ? 4 : 0);
-    const float s = scales[item];
-    r.x = (float)((int)((w.x >> sh) & 0x0F) - 8) * s;
-    r.y = (float)((int)((w.y >> sh) & 0x0F) - 8) * s;
-    r.z = (float)((int)((w.z >> sh) & 0x0F) - 8) * s;
-    r.w = (float)((int)((w.w >> sh) & 0x0F) - 8) * s;
+    r.x = (float)((int)((w.q.x >> sh) & 0x0F) - 8) * w.s;
+    r.y = (float)((int)((w.q.y >> sh) & 0x0F) - 8) * w.s;
+    r.z = (float)((int)((w.q.z >> sh) & 0x0F) - 8) * w.s;
+    r.w = (float)((int)((w.q.w >> sh) & 0x0F) - 8) * w.s;
   }
   return r;
 }
+constexpr int kF32Ahead = 4;  // 16-element steps whose weights are in flight
 
 template <int WDT, bool SW>
 __global__ __launch_bounds__(256) void gemm_f32act_kernel(const F32Args a) {
@@ -2109,26 +2116,44 @@ __global__ __launch_bounds__(256) void gemm_f32act_kernel(const F32Args a) {
       if (k < klen) sxp[t][k & 3][k >> 2] = t0 + t < T ? a.x[(int64_t)(t0 + t) * K + k0 + k] : 0.f;
     }
     __syncthreads();
-    int i = k0;
-    for (; i + 16 <= k0 + klen; i += 16) {
-      const float4 w = deq_chain<WDT>(tg.data, tg.scales, nbase, H, i, n, c);
-      float4 wu = w;
-      if (SW) wu = deq_chain<WDT>(a.tg[1].data, a.tg[1].scales, nbase, H, i, n, c);
+    // the chunk's 16-element steps; each step's weights are loaded kF32Ahead steps before it
+    const int nst = klen >> 4;
+    WChunk wr[kF32Ahead], ur[kF32Ahead];
 #pragma unroll
-      for (int t = 0; t < kF32TT; ++t) {
-        const float4 xv = *reinterpret_cast<const float4*>(&sxp[t][c][(i - k0) >> 2]);
-        s[t] = s[t] + xv.x * w.x;
-        s[t] = s[t] + xv.y * w.y;
-        s[t] = s[t] + xv.z * w.z;
-        s[t] = s[t] + xv.w * w.w;
-        if (SW) {
-          su[t] = su[t] + xv.x * wu.x;
-          su[t] = su[t] + xv.y * wu.y;
-          su[t] = su[t] + xv.z * wu.z;
-          su[t] = su[t] + xv.w * wu.w;
+    for (int u = 0; u < kF32Ahead; ++u)
+      if (u < nst) {
+        wr[u] = load_chunk<WDT>(tg.data, tg.scales, nbase, H, k0 + 16 * u, n);
+        if (SW) ur[u] = load_chunk<WDT>(a.tg[1].data, a.tg[1].scales, nbase, H, k0 + 16 * u, n);
+      }
+    for (int s0 = 0; s0 < nst; s0 += kF32Ahead) {
+#pragma unroll
+      for (int u = 0; u < kF32Ahead; ++u) {
+        const int st = s0 + u, ii = k0 + 16 * st;
+        if (st < nst) {
+          const float4 w = chunk_chain<WDT>(wr[u], ii, c);
+          const float4 wu = SW ? chunk_chain<WDT>(ur[u], ii, c) : w;
+          if (st + kF32Ahead < nst) {
+            wr[u] = load_chunk<WDT>(tg.data, tg.scales, nbase, H, ii + 16 * kF32Ahead, n);
+            if (SW) ur[u] = load_chunk<WDT>(a.tg[1].data, a.tg[1].scales, nbase, H, ii + 16 * kF32Ahead, n);
+          }
+#pragma unroll
+          for (int t = 0; t < kF32TT; ++t) {
+            const float4 xv = *reinterpret_cast<const float4*>(&sxp[t][c][(ii - k0) >> 2]);
+            s[t] = s[t] + xv.x * w.x;
+            s[t] = s[t] + xv.y * w.y;
+            s[t] = s[t] + xv.z * w.z;
+            s[t] = s[t] + xv.w * w.w;
+            if (SW) {
+              su[t] = su[t] + xv.x * wu.x;
+              su[t] = su[t] + xv.y * wu.y;
+              su[t] = su[t] + xv.z * wu.z;
+              su[t] = su[t] + xv.w * wu.w;
+            }
+          }
         }
       }
     }
+    int i = k0 + 16 * nst;
     for (; i < k0 + klen; i += 4) {  // the last chunk's steps past its last 16-element run
       const float w = deq1<WDT>(tg.data, tg.scales, nbase, H, i + c, n);
       const float wu = SW ? deq1<WDT>(a.tg[1].data, a.tg[1].scales, nbase, H, i + c, n) : w;
