@@ -299,7 +299,7 @@ int run_f32_group(elmh_ctx* c, const float* x, int T, int64_t K, const std::vect
     a.nb = (int)w0.nb;
     a.nw = nw;  // set only when f32_norm_fusable holds
     a.eps = eps;
-    HIP_OR_FAIL(c, launch_f32act(w0.dtype, 0, a, groups, c->stream));
+    HIP_OR_FAIL(c, launch_f32act(w0.dtype, 0, a, c->stream));
   }
   return ELMH_OK;
 }
@@ -469,7 +469,7 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
     a.nb = (int)g.nb;
     a.nw = nw;  // set only when f32_norm_fusable holds
     a.eps = eps;
-    HIP_OR_FAIL(c, launch_f32act(g.dtype, 1, a, groups, c->stream));
+    HIP_OR_FAIL(c, launch_f32act(g.dtype, 1, a, c->stream));
     return ELMH_OK;
   }
   const bool qin = use_small_gemv(T, K, g.data_bytes + g.scale_bytes + u.data_bytes + u.scale_bytes);

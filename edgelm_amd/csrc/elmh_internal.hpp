@@ -105,7 +105,7 @@ struct GemmArgs {
 
 struct F32Args {
   GemvTarget tg[kMaxTargets];
-  int tile_start[kMaxTargets + 1];  // in units of 256-row groups (gemv) / 64-row groups (gemm)
+  int tile_start[kMaxTargets + 1];  // set by launch_f32act (in its kernel's row tiles)
   int n_targets;
   int H;
   const float* x;  // [T][K]
@@ -137,7 +137,7 @@ int gemv_stream_ipt(int dtype, int items, int producers);
 size_t gemv_lds_bytes(int nt, int K, int nb, int H, int nsel);
 hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_tiles, hipStream_t s);
 hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs& a, int total_tiles, hipStream_t s);
-hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_groups, hipStream_t s);
+hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, hipStream_t s);
 // True if the f32-activation GEMV that launch_f32act runs for this call can apply RMSNORM to x
 // itself (a.nw): one token, q4 targets whose layout the group-parallel q4 GEMV takes.
 bool f32act_norm_ok(int T, int K, int nb, int H, int nsel);

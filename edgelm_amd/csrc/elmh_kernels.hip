@@ -1780,75 +1780,6 @@ done:
 
 // ---------------------------------------------------------------- f32-activation paths
 
-// T == 1 (kernels_cpu.cpp:366-368, 397-399 with dot_row): one lane per weight row.
-//   q8: ((s0 + s1) + (s2 + s3)) * ws, chains over i mod 4, tail into s0 (dot_q8)
-//   q4: s += (g0 + g1) * ws_g per group, g0/g1 sequential over 16 elements (dot_q4)
-template <int WDT>
-__device__ __forceinline__ float dot_row_f32(const uint8_t* __restrict__ data, const float* __restrict__ scales,
-                                             int n, int H, int nb, int K, const float* __restrict__ sx) {
-  const int64_t nbase = (int64_t)(n / H) * nb * H + (n % H);
-  if (WDT == WQ8) {
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-    int i = 0;
-    for (; i + 4 <= K; i += 4) {
-      const int b = i >> 5;
-      const uint32_t w = *reinterpret_cast<const uint32_t*>(data + (nbase + (int64_t)b * H) * 32 + (i & 31));
-      const float4 xv = *reinterpret_cast<const float4*>(sx + i);
-      s0 = s0 + xv.x * (float)(int8_t)(w & 0xFF);
-      s1 = s1 + xv.y * (float)(int8_t)((w >> 8) & 0xFF);
-      s2 = s2 + xv.z * (float)(int8_t)((w >> 16) & 0xFF);
-      s3 = s3 + xv.w * (float)(int8_t)(w >> 24);
-    }
-    for (; i < K; ++i) {
-      const int b = i >> 5;
-      const int8_t w = *reinterpret_cast<const int8_t*>(data + (nbase + (int64_t)b * H) * 32 + (i & 31));
-      s0 = s0 + sx[i] * (float)w;
-    }
-    return ((s0 + s1) + (s2 + s3)) * scales[n];
-  } else {
-    float s = 0.f;
-    for (int g = 0; g < nb; ++g) {
-      const int64_t item = nbase + (int64_t)g * H;
-      const uint4 wq = *reinterpret_cast<const uint4*>(data + item * 16);
-      const uint32_t wd[4] = {wq.x, wq.y, wq.z, wq.w};
-      float g0 = 0.f, g1 = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint32_t byte = (wd[i >> 2] >> (8 * (i & 3))) & 0xFF;
-        g0 = g0 + sx[g * 32 + i] * (float)((int)(byte & 0x0F) - 8);
-        g1 = g1 + sx[g * 32 + 16 + i] * (float)((int)(byte >> 4) - 8);
-      }
-      s = s + (g0 + g1) * scales[item];
-    }
-    return s;
-  }
-}
-
-template <int WDT, bool SW>
-__global__ __launch_bounds__(256) void gemv_f32act_kernel(const F32Args a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  float* sx = reinterpret_cast<float*>(smem);
-  const int K = a.K;
-  for (int i = threadIdx.x; i < K; i += 256) sx[i] = a.x[i];
-  __syncthreads();
-  int ti = 0, grp = blockIdx.x;
-  if (!SW) {
-    while (ti + 1 < a.n_targets && (int)blockIdx.x >= a.tile_start[ti + 1]) ++ti;
-    grp = blockIdx.x - a.tile_start[ti];
-  }
-  const GemvTarget& tg = a.tg[SW ? 0 : ti];
-  const int n = grp * 256 + threadIdx.x;
-  if (n >= tg.N) return;
-  float out = dot_row_f32<WDT>(tg.data, tg.scales, n, a.H, a.nb, K, sx);
-  if (SW) {
-    const float up = dot_row_f32<WDT>(a.tg[1].data, a.tg[1].scales, n, a.H, a.nb, K, sx);
-    out = silu_exact(out) * up;
-  } else {
-    out = (tg.res ? tg.res[n] : 0.f) + out;
-  }
-  tg.y[n] = out;
-}
-
 // T == 1, q4, one workgroup per H-row tile (of the target, or of gate and up with SW): dot_q4's
 // operations (kernels_cpu.cpp:397-399) spread over the groups instead of one lane walking the row.
 // Every (selection, row, group) item is (g0 + g1) * ws_g, g0 / g1 the in-order 16-term sums of the
@@ -2022,32 +1953,6 @@ __global__ __launch_bounds__(256) void gemv_f32act_q8_kernel(const F32Args a) {
 constexpr int kF32TT = 2;
 constexpr int kF32Chunk = 2048;
 constexpr int kF32ChainStride = kF32Chunk / 4 + 4;  // floats; the +4 spreads the staging writes over banks
-
-template <int WDT>
-__device__ __forceinline__ float4 deq4(const uint8_t* __restrict__ data, const float* __restrict__ scales,
-                                       int64_t nbase, int H, int i, int n) {
-  const int b = i >> 5;
-  const int64_t item = nbase + (int64_t)b * H;
-  float4 r;
-  if (WDT == WQ8) {
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(data + item * 32 + (i & 31));
-    const float s = scales[n];
-    r.x = (float)(int8_t)(w & 0xFF) * s;
-    r.y = (float)(int8_t)((w >> 8) & 0xFF) * s;
-    r.z = (float)(int8_t)((w >> 16) & 0xFF) * s;
-    r.w = (float)(int8_t)(w >> 24) * s;
-  } else {
-    const int e = i & 31;  // 4 consecutive elements of one half of the group
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(data + item * 16 + (e & 15));
-    const int sh = e >= 16 ? 4 : 0;
-    const float s = scales[item];
-    r.x = (float)((int)((w >> sh) & 0x0F) - 8) * s;
-    r.y = (float)((int)((w >> (8 + sh)) & 0x0F) - 8) * s;
-    r.z = (float)((int)((w >> (16 + sh)) & 0x0F) - 8) * s;
-    r.w = (float)((int)((w >> (24 + sh)) & 0x0F) - 8) * s;
-  }
-  return r;
-}
 
 template <int WDT>
 __device__ __forceinline__ float deq1(const uint8_t* __restrict__ data, const float* __restrict__ scales,
@@ -2483,7 +2388,7 @@ bool f32act_norm_ok(int T, int K, int nb, int H, int nsel) {
          f32q4_lds_bytes(K, nb, H, nsel, true) <= kMaxLds - 1024;
 }
 
-hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_groups, hipStream_t s) {
+hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, hipStream_t s) {
   const int nsel = swiglu ? 2 : 1;
   if (a.T == 1 && dtype == WQ4 && f32act_norm_ok(a.T, a.K, a.nb, a.H, nsel)) {
     // one workgroup per tile of rt rows (rt divides H); the tile starts counted in tiles here.
@@ -2518,25 +2423,22 @@ hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, int total_grou
   }
   if (a.nw) return hipErrorInvalidValue;  // RMSNORM is applied by the q4 GEMV above only
   if (a.T == 1) {
+    // q4 always takes the GEMV above (K = 32 nb, H a power of two) unless its LDS would not fit
+    if (dtype != WQ8) return hipErrorInvalidValue;
     const size_t lds = (size_t)((a.K + 3) & ~3) * 4;
     if (lds > 64 * 1024) return hipErrorInvalidValue;
-    if (dtype == WQ8) {
-      // four lanes per row, 64 rows per workgroup; the group starts counted in 64-row groups here
-      F32Args b = a;
-      const int n = swiglu ? 1 : a.n_targets;
-      int groups = 0;
-      for (int i = 0; i < n; ++i) {
-        b.tile_start[i] = groups;
-        groups += (a.tg[i].N + 63) / 64;
-      }
-      b.tile_start[n] = groups;
-      if (groups < 1) return hipErrorInvalidValue;
-      if (swiglu) gemv_f32act_q8_kernel<true><<<groups, 256, lds, s>>>(b);
-      else gemv_f32act_q8_kernel<false><<<groups, 256, lds, s>>>(b);
-    } else {
-      if (swiglu) gemv_f32act_kernel<WQ4, true><<<total_groups, 256, lds, s>>>(a);
-      else gemv_f32act_kernel<WQ4, false><<<total_groups, 256, lds, s>>>(a);
+    // four lanes per row, 64 rows per workgroup; the group starts counted in 64-row groups here
+    F32Args b = a;
+    const int n = swiglu ? 1 : a.n_targets;
+    int groups = 0;
+    for (int i = 0; i < n; ++i) {
+      b.tile_start[i] = groups;
+      groups += (a.tg[i].N + 63) / 64;
     }
+    b.tile_start[n] = groups;
+    if (groups < 1) return hipErrorInvalidValue;
+    if (swiglu) gemv_f32act_q8_kernel<true><<<groups, 256, lds, s>>>(b);
+    else gemv_f32act_q8_kernel<false><<<groups, 256, lds, s>>>(b);
   } else {
     // grid x: kF32TT-token tiles (consecutive workgroups share their weight rows), y: 64-row groups
     F32Args b = a;
