@@ -1895,50 +1895,154 @@ __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
   }
 }
 
-// T == 1, q8: dot_q8's four chains (kernels_cpu.cpp:366-368: chain c takes i = c mod 4 in order,
-// the K mod 4 tail goes to chain 0) are independent, so four lanes take one row, a chain each,
-// and 64 rows share a workgroup; the lanes of a row read the same 16 weight bytes and each uses
-// its own four. ((s0 + s1) + (s2 + s3)) * ws is formed across the row's lanes.
+// The same with the workgroup's rows first copied into LDS (global_load_lds, all in flight at
+// once; one wait): row r of selection sel is its K bytes (32 nb, the layout's block padding
+// included) plus one 16-byte pad at LDS byte ((sel * 16 + r) * (2 nb + 1)) * 16, so the 16 rows'
+// reads of one step fall on different banks. x follows in LDS. Used while that fits 64 KB.
+constexpr int kQ8F32LdsRows = 16;
+__host__ __device__ inline int q8f32_chunks(int nb, int nsel) { return nsel * kQ8F32LdsRows * (2 * nb + 1); }
 template <bool SW>
-__global__ __launch_bounds__(256) void gemv_f32act_q8_kernel(const F32Args a) {
-  extern __shared__ __align__(16) float f32q8_lds[];
-  const int K = a.K, K4 = K & ~3, H = a.H;
-  for (int i = threadIdx.x; i < K; i += 256) f32q8_lds[i] = a.x[i];
+__global__ __launch_bounds__(64) void gemv_f32act_q8_lds_kernel(const F32Args a) {
+  extern __shared__ __align__(16) unsigned char q8l_lds[];
+  constexpr int NSEL = SW ? 2 : 1;
+  const int K = a.K, K4 = K & ~3, H = a.H, nb = a.nb, cpr = 2 * nb + 1, lane = threadIdx.x;
   int ti = 0, grp = blockIdx.x;
   if (!SW) {
     while (ti + 1 < a.n_targets && grp >= a.tile_start[ti + 1]) ++ti;
     grp -= a.tile_start[ti];
   }
   const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  const int n0 = grp * kQ8F32LdsRows;  // rows past N: padding (rows_pad % 64 == 0)
+  const int nch = q8f32_chunks(nb, NSEL);
+  unsigned char* const wl = q8l_lds;
+  float* const sx = reinterpret_cast<float*>(q8l_lds + ((nch + 63) & ~63) * 16);
+  for (int q0 = 0; q0 < nch; q0 += 64) {
+    const int q = min(q0 + lane, nch - 1), sel = q / (kQ8F32LdsRows * cpr), rem = q - sel * kQ8F32LdsRows * cpr;
+    const int r = rem / cpr, k = min(rem - r * cpr, 2 * nb - 1);  // the pad slot repeats the last chunk
+    const int n = n0 + r;
+    const int64_t item = (int64_t)(n / H) * nb * H + (int64_t)(k >> 1) * H + (n % H);
+    dma16((SW && sel ? a.tg[1].data : tg.data) + item * 32 + (k & 1) * 16, wl + q0 * 16);
+  }
+  for (int i = lane; i < K; i += 64) sx[i] = a.x[i];
+  wait_vm<0>();
   __syncthreads();
-  const int c = threadIdx.x & 3, n = grp * 64 + (threadIdx.x >> 2);  // rows past N: padding (rows_pad % 64 == 0)
-  const int64_t nbase = (int64_t)(n / H) * a.nb * H + (n % H);
-  float dots[SW ? 2 : 1];
+  const int c = lane & 3, r = lane >> 2, n = n0 + r;
+  const unsigned char* const rg = wl + r * cpr * 16;
+  const unsigned char* const ru = wl + (kQ8F32LdsRows + r) * cpr * 16;
+  float sg = 0.f, su = 0.f;
+  int i = 0;
+  for (; i + 16 <= K4; i += 16) {
+    const uint4 w = *reinterpret_cast<const uint4*>(rg + i);
+    const uint4 wu = SW ? *reinterpret_cast<const uint4*>(ru + i) : w;
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w}, ud[4] = {wu.x, wu.y, wu.z, wu.w};
 #pragma unroll
-  for (int sel = 0; sel < (SW ? 2 : 1); ++sel) {
-    const uint8_t* __restrict__ data = sel ? a.tg[1].data : tg.data;
-    float sc = 0.f;
-    int i = 0;
-    for (; i + 16 <= K4; i += 16) {
-      const uint4 w = *reinterpret_cast<const uint4*>(data + (nbase + (int64_t)(i >> 5) * H) * 32 + (i & 31));
-      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        sc = sc + f32q8_lds[i + 4 * j + c] * (float)(int8_t)((wd[j] >> (8 * c)) & 0xFF);
+    for (int j = 0; j < 4; ++j) {
+      const float xv = sx[i + 4 * j + c];
+      sg = sg + xv * (float)(int8_t)((wd[j] >> (8 * c)) & 0xFF);
+      if (SW) su = su + xv * (float)(int8_t)((ud[j] >> (8 * c)) & 0xFF);
     }
-    for (; i < K4; i += 4) {
-      const uint32_t w = *reinterpret_cast<const uint32_t*>(data + (nbase + (int64_t)(i >> 5) * H) * 32 + (i & 31));
-      sc = sc + f32q8_lds[i + c] * (float)(int8_t)((w >> (8 * c)) & 0xFF);
+  }
+  for (; i < K4; i += 4) {
+    const float xv = sx[i + c];
+    sg = sg + xv * (float)(int8_t)rg[i + c];
+    if (SW) su = su + xv * (float)(int8_t)ru[i + c];
+  }
+  if (c == 0)
+    for (; i < K; ++i) {  // the K mod 4 tail into chain 0
+      sg = sg + sx[i] * (float)(int8_t)rg[i];
+      if (SW) su = su + sx[i] * (float)(int8_t)ru[i];
     }
-    if (c == 0)
-      for (; i < K; ++i)
-        sc = sc + f32q8_lds[i] * (float)*reinterpret_cast<const int8_t*>(data + (nbase + (int64_t)(i >> 5) * H) * 32 + (i & 31));
-    const float pair = sc + __shfl_xor(sc, 1);  // lane 0: s0 + s1, lane 2: s2 + s3
-    dots[sel] = (pair + __shfl_xor(pair, 2)) * (sel ? a.tg[1].scales : tg.scales)[n];
+  const float pg = sg + __shfl_xor(sg, 1);  // lane 0: s0 + s1, lane 2: s2 + s3
+  const float g = (pg + __shfl_xor(pg, 2)) * tg.scales[n];
+  float up = 0.f;
+  if (SW) {
+    const float pu = su + __shfl_xor(su, 1);
+    up = (pu + __shfl_xor(pu, 2)) * a.tg[1].scales[n];
   }
   if (c == 0 && n < tg.N) {
-    if (SW) tg.y[n] = silu_exact(dots[0]) * dots[SW ? 1 : 0];
-    else tg.y[n] = (tg.res ? tg.res[n] : 0.f) + dots[0];
+    if (SW) tg.y[n] = silu_exact(g) * up;
+    else tg.y[n] = (tg.res ? tg.res[n] : 0.f) + g;
+  }
+}
+
+// T == 1, q8: dot_q8's four chains (kernels_cpu.cpp:366-368: chain c takes i = c mod 4 in order,
+// the K mod 4 tail goes to chain 0) are independent, so four lanes take one row, a chain each,
+// and 16 rows share a one-wave workgroup; the lanes of a row read the same 16 weight bytes and each uses
+// its own four. ((s0 + s1) + (s2 + s3)) * ws is formed across the row's lanes.
+constexpr int kQ8F32Rows = 16;  // rows per workgroup: one wave, four lanes per row
+constexpr int kQ8F32Ahead = 8;  // 16-element steps whose weights are in flight
+
+template <bool SW>
+__global__ __launch_bounds__(64) void gemv_f32act_q8_kernel(const F32Args a) {
+  extern __shared__ __align__(16) float f32q8_lds[];
+  const int K = a.K, K4 = K & ~3, H = a.H;
+  int ti = 0, grp = blockIdx.x;
+  if (!SW) {
+    while (ti + 1 < a.n_targets && grp >= a.tile_start[ti + 1]) ++ti;
+    grp -= a.tile_start[ti];
+  }
+  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  // rows past N: padding (rows_pad % 64 == 0)
+  const int c = threadIdx.x & 3, n = grp * kQ8F32Rows + (threadIdx.x >> 2);
+  const int64_t nbase = (int64_t)(n / H) * a.nb * H + (n % H);
+  const uint8_t* const dg = tg.data;
+  const uint8_t* const du = SW ? a.tg[1].data : tg.data;
+  const auto at = [&](const uint8_t* d, int i) { return d + (nbase + (int64_t)(i >> 5) * H) * 32 + (i & 31); };
+  // the first steps' weights go out before x is staged; each step's weights are loaded
+  // kQ8F32Ahead steps before it (gate and up chains side by side with SW)
+  const int nst = K4 >> 4;
+  uint4 wr[kQ8F32Ahead], ur[kQ8F32Ahead];
+#pragma unroll
+  for (int u = 0; u < kQ8F32Ahead; ++u)
+    if (u < nst) {
+      wr[u] = *reinterpret_cast<const uint4*>(at(dg, 16 * u));
+      if (SW) ur[u] = *reinterpret_cast<const uint4*>(at(du, 16 * u));
+    }
+  for (int i = threadIdx.x; i < K; i += 64) f32q8_lds[i] = a.x[i];
+  __syncthreads();
+  float sg = 0.f, su = 0.f;
+  for (int s0 = 0; s0 < nst; s0 += kQ8F32Ahead) {
+#pragma unroll
+    for (int u = 0; u < kQ8F32Ahead; ++u) {
+      const int st = s0 + u, i = 16 * st;
+      if (st < nst) {
+        const uint4 w = wr[u];
+        const uint4 wu = SW ? ur[u] : w;
+        if (st + kQ8F32Ahead < nst) {
+          wr[u] = *reinterpret_cast<const uint4*>(at(dg, i + 16 * kQ8F32Ahead));
+          if (SW) ur[u] = *reinterpret_cast<const uint4*>(at(du, i + 16 * kQ8F32Ahead));
+        }
+        const uint32_t wd[4] = {w.x, w.y, w.z, w.w}, ud[4] = {wu.x, wu.y, wu.z, wu.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float xv = f32q8_lds[i + 4 * j + c];
+          sg = sg + xv * (float)(int8_t)((wd[j] >> (8 * c)) & 0xFF);
+          if (SW) su = su + xv * (float)(int8_t)((ud[j] >> (8 * c)) & 0xFF);
+        }
+      }
+    }
+  }
+  int i = 16 * nst;
+  for (; i < K4; i += 4) {
+    const float xv = f32q8_lds[i + c];
+    sg = sg + xv * (float)(int8_t)((*reinterpret_cast<const uint32_t*>(at(dg, i)) >> (8 * c)) & 0xFF);
+    if (SW) su = su + xv * (float)(int8_t)((*reinterpret_cast<const uint32_t*>(at(du, i)) >> (8 * c)) & 0xFF);
+  }
+  if (c == 0)
+    for (; i < K; ++i) {  // the K mod 4 tail into chain 0
+      sg = sg + f32q8_lds[i] * (float)*reinterpret_cast<const int8_t*>(at(dg, i));
+      if (SW) su = su + f32q8_lds[i] * (float)*reinterpret_cast<const int8_t*>(at(du, i));
+    }
+  const float pg = sg + __shfl_xor(sg, 1);  // lane 0: s0 + s1, lane 2: s2 + s3
+  const float g = (pg + __shfl_xor(pg, 2)) * tg.scales[n];
+  float up = 0.f;
+  if (SW) {
+    const float pu = su + __shfl_xor(su, 1);
+    up = (pu + __shfl_xor(pu, 2)) * a.tg[1].scales[n];
+  }
+  if (c == 0 && n < tg.N) {
+    if (SW) tg.y[n] = silu_exact(g) * up;
+    else tg.y[n] = (tg.res ? tg.res[n] : 0.f) + g;
   }
 }
 
@@ -2427,18 +2531,26 @@ hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, hipStream_t s)
     if (dtype != WQ8) return hipErrorInvalidValue;
     const size_t lds = (size_t)((a.K + 3) & ~3) * 4;
     if (lds > 64 * 1024) return hipErrorInvalidValue;
-    // four lanes per row, 64 rows per workgroup; the group starts counted in 64-row groups here
+    // four lanes per row, kQ8F32Rows rows per workgroup; the group starts counted in those here
     F32Args b = a;
     const int n = swiglu ? 1 : a.n_targets;
     int groups = 0;
     for (int i = 0; i < n; ++i) {
       b.tile_start[i] = groups;
-      groups += (a.tg[i].N + 63) / 64;
+      groups += (a.tg[i].N + kQ8F32Rows - 1) / kQ8F32Rows;
     }
     b.tile_start[n] = groups;
     if (groups < 1) return hipErrorInvalidValue;
-    if (swiglu) gemv_f32act_q8_kernel<true><<<groups, 256, lds, s>>>(b);
-    else gemv_f32act_q8_kernel<false><<<groups, 256, lds, s>>>(b);
+    static_assert(kQ8F32Rows == kQ8F32LdsRows, "one grid for both q8 GEMVs");
+    const size_t lds_w = (size_t)((q8f32_chunks(a.nb, nsel) + 63) & ~63) * 16 + lds;
+    if (lds_w <= 64 * 1024) {
+      if (swiglu) gemv_f32act_q8_lds_kernel<true><<<groups, 64, lds_w, s>>>(b);
+      else gemv_f32act_q8_lds_kernel<false><<<groups, 64, lds_w, s>>>(b);
+    } else if (swiglu) {
+      gemv_f32act_q8_kernel<true><<<groups, 64, lds, s>>>(b);
+    } else {
+      gemv_f32act_q8_kernel<false><<<groups, 64, lds, s>>>(b);
+    }
   } else {
     // grid x: kF32TT-token tiles (consecutive workgroups share their weight rows), y: 64-row groups
     F32Args b = a;
