@@ -1895,6 +1895,88 @@ __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
   }
 }
 
+// T == 1, q8, rows of up to 2048 values: the products x_i * w_i (each rounded, as dot_q8 forms
+// them) are independent, so all 256 threads form them into LDS by chain ([sel][row][chain][K / 4],
+// rows padded by 4 floats against bank conflicts); then lane 4r + c of wave 0 adds chain c of row
+// r in order (the K mod 4 tail into chain 0) and ((s0 + s1) + (s2 + s3)) * ws follows. The
+// dependent adds are all that stays on one lane. Eight rows per workgroup.
+constexpr int kQ8PRows = 8;
+__host__ __device__ inline int q8p_stride(int K) { return ((((K & ~3) >> 2) + 63) & ~63) + 4; }
+template <bool SW>
+__global__ __launch_bounds__(256) void gemv_f32act_q8_prod_kernel(const F32Args a) {
+  extern __shared__ __align__(16) float q8p_lds[];
+  constexpr int NSEL = SW ? 2 : 1;
+  const int K = a.K, K4 = K & ~3, Lq = K4 >> 2, Lr = q8p_stride(K), H = a.H, nb = a.nb, tid = threadIdx.x;
+  int ti = 0, grp = blockIdx.x;
+  if (!SW) {
+    while (ti + 1 < a.n_targets && grp >= a.tile_start[ti + 1]) ++ti;
+    grp -= a.tile_start[ti];
+  }
+  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  const int n0 = grp * kQ8PRows;  // rows past N: padding (rows_pad % 64 == 0)
+  float* const sx = q8p_lds;
+  float* const P = q8p_lds + ((K + 3) & ~3);  // [NSEL][kQ8PRows][4][Lr]
+  for (int i = tid; i < K; i += 256) sx[i] = a.x[i];
+  __syncthreads();
+  for (int it = tid; it < NSEL * kQ8PRows * Lq; it += 256) {
+    const int sr = it / Lq, q = it - sr * Lq, sel = sr / kQ8PRows, r = sr - sel * kQ8PRows, n = n0 + r;
+    const int64_t item = (int64_t)(n / H) * nb * H + (int64_t)(q >> 3) * H + (n % H);
+    const uint32_t w = *reinterpret_cast<const uint32_t*>((SW && sel ? a.tg[1].data : tg.data) + item * 32 + ((4 * q) & 31));
+    float* const pr = P + (size_t)sr * 4 * Lr + q;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) pr[cc * Lr] = sx[4 * q + cc] * (float)(int8_t)((w >> (8 * cc)) & 0xFF);
+  }
+  __syncthreads();
+  if (tid >= 4 * kQ8PRows) return;
+  const int r = tid >> 2, c = tid & 3, n = n0 + r;
+  const float* const rg = P + (size_t)(r * 4 + c) * Lr;
+  const float* const ru = P + (size_t)((kQ8PRows + r) * 4 + c) * Lr;
+  float sg = 0.f, su = 0.f;
+  int j = 0;
+  for (; j + 32 <= Lq; j += 32) {
+    float4 vg[8], vu[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      vg[u] = *reinterpret_cast<const float4*>(rg + j + 4 * u);
+      if (SW) vu[u] = *reinterpret_cast<const float4*>(ru + j + 4 * u);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      sg = sg + vg[u].x;
+      sg = sg + vg[u].y;
+      sg = sg + vg[u].z;
+      sg = sg + vg[u].w;
+      if (SW) {
+        su = su + vu[u].x;
+        su = su + vu[u].y;
+        su = su + vu[u].z;
+        su = su + vu[u].w;
+      }
+    }
+  }
+  for (; j < Lq; ++j) {
+    sg = sg + rg[j];
+    if (SW) su = su + ru[j];
+  }
+  if (c == 0)
+    for (int i = K4; i < K; ++i) {  // the K mod 4 tail into chain 0
+      const int64_t item = (int64_t)(n / H) * nb * H + (int64_t)(i >> 5) * H + (n % H);
+      sg = sg + sx[i] * (float)*reinterpret_cast<const int8_t*>(tg.data + item * 32 + (i & 31));
+      if (SW) su = su + sx[i] * (float)*reinterpret_cast<const int8_t*>(a.tg[1].data + item * 32 + (i & 31));
+    }
+  const float pg = sg + __shfl_xor(sg, 1);  // lane 4r: s0 + s1, lane 4r + 2: s2 + s3
+  const float g = (pg + __shfl_xor(pg, 2)) * tg.scales[n];
+  float up = 0.f;
+  if (SW) {
+    const float pu = su + __shfl_xor(su, 1);
+    up = (pu + __shfl_xor(pu, 2)) * a.tg[1].scales[n];
+  }
+  if (c == 0 && n < tg.N) {
+    if (SW) tg.y[n] = silu_exact(g) * up;
+    else tg.y[n] = (tg.res ? tg.res[n] : 0.f) + g;
+  }
+}
+
 // The same with the workgroup's rows first copied into LDS (global_load_lds, all in flight at
 // once; one wait): row r of selection sel is its K bytes (32 nb, the layout's block padding
 // included) plus one 16-byte pad at LDS byte ((sel * 16 + r) * (2 nb + 1)) * 16, so the 16 rows'
@@ -2531,9 +2613,23 @@ hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, hipStream_t s)
     if (dtype != WQ8) return hipErrorInvalidValue;
     const size_t lds = (size_t)((a.K + 3) & ~3) * 4;
     if (lds > 64 * 1024) return hipErrorInvalidValue;
+    const int n = swiglu ? 1 : a.n_targets;
+    const size_t lds_p = ((size_t)((a.K + 3) & ~3) + (size_t)nsel * kQ8PRows * 4 * q8p_stride(a.K)) * 4;
+    if (lds_p <= 64 * 1024) {  // products in LDS; group starts counted in kQ8PRows-row groups here
+      F32Args b = a;
+      int groups = 0;
+      for (int i = 0; i < n; ++i) {
+        b.tile_start[i] = groups;
+        groups += (a.tg[i].N + kQ8PRows - 1) / kQ8PRows;
+      }
+      b.tile_start[n] = groups;
+      if (groups < 1) return hipErrorInvalidValue;
+      if (swiglu) gemv_f32act_q8_prod_kernel<true><<<groups, 256, lds_p, s>>>(b);
+      else gemv_f32act_q8_prod_kernel<false><<<groups, 256, lds_p, s>>>(b);
+      return hipGetLastError();
+    }
     // four lanes per row, kQ8F32Rows rows per workgroup; the group starts counted in those here
     F32Args b = a;
-    const int n = swiglu ? 1 : a.n_targets;
     int groups = 0;
     for (int i = 0; i < n; ++i) {
       b.tile_start[i] = groups;
