@@ -2614,8 +2614,12 @@ hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, hipStream_t s)
     const size_t lds = (size_t)((a.K + 3) & ~3) * 4;
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     const int n = swiglu ? 1 : a.n_targets;
+    int rows = 0;
+    for (int i = 0; i < n; ++i) rows += a.tg[i].N;
     const size_t lds_p = ((size_t)((a.K + 3) & ~3) + (size_t)nsel * kQ8PRows * 4 * q8p_stride(a.K)) * 4;
-    if (lds_p <= 64 * 1024) {  // products in LDS; group starts counted in kQ8PRows-row groups here
+    // products in LDS while the chains are the bottleneck (a layer's few rows); with many rows (an
+    // LM head) the chip is full either way and the four-lane kernels below do less work per row
+    if (lds_p <= 64 * 1024 && rows <= 8192) {  // group starts counted in kQ8PRows-row groups here
       F32Args b = a;
       int groups = 0;
       for (int i = 0; i < n; ++i) {

@@ -162,7 +162,7 @@ def test_matmul_n_mixed_targets(ctx):
 @pytest.mark.parametrize("dt", [O.Q8, O.Q4])
 def test_matmul_f32act_exact(ctx, dt):
     r = rng(4 + dt)
-    shapes = [(48, 64), (37, 96), (130, 160), (960, 576)] + ([(37, 50), (20, 7)] if dt == O.Q8 else
+    shapes = [(48, 64), (37, 96), (130, 160), (960, 576)] + ([(37, 50), (20, 7), (8200, 64)] if dt == O.Q8 else
                                                               [(576, 1536), (70, 4096)])
     for n, k in shapes:
         w = weight(r, n, k, dt)
