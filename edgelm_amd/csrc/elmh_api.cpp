@@ -559,9 +559,11 @@ bool block_gemm(int T, int64_t K, int n, const elmh_weight* const* w, int nsel, 
 // targets of the group-parallel q4 GEMV's layout)
 bool f32_norm_fusable(int T, int64_t K, int n, const elmh_weight* const* w, int nsel, int act) {
   if (act != ELMH_ACT_F32 || K > 8192) return false;
+  int64_t rows = 0;  // launch_f32act's output rows: SwiGLU's gate rows, else every target's
+  for (int i = 0; i < (nsel == 2 ? 1 : n); ++i) rows += w[i]->w.rows;
   for (int i = 0; i < n; ++i)
     if (w[i]->w.dtype != WQ4 || w[i]->w.H != w[0]->w.H ||
-        !f32act_norm_ok(T, (int)K, (int)w[i]->w.nb, w[i]->w.H, nsel))
+        !f32act_q4_ok(T, (int)K, (int)w[i]->w.nb, w[i]->w.H, nsel, (int)std::min<int64_t>(rows, 1 << 30), true))
       return false;
   return true;
 }

@@ -138,9 +138,10 @@ size_t gemv_lds_bytes(int nt, int K, int nb, int H, int nsel);
 hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_tiles, hipStream_t s);
 hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs& a, int total_tiles, hipStream_t s);
 hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, hipStream_t s);
-// True if the f32-activation GEMV that launch_f32act runs for this call can apply RMSNORM to x
-// itself (a.nw): one token, q4 targets whose layout the group-parallel q4 GEMV takes.
-bool f32act_norm_ok(int T, int K, int nb, int H, int nsel);
+// True if launch_f32act runs the group-parallel q4 GEMV for this call (one token, q4 targets of tile
+// height H, `rows` output rows, nsel = 2 for SwiGLU): its LDS, sized for the tile height the launch
+// picks and, with norm (RMSNORM applied to x inside, a.nw), for the squares, fits a workgroup.
+bool f32act_q4_ok(int T, int K, int nb, int H, int nsel, int rows, bool norm);
 hipError_t launch_silu_mul(const float* g, const float* u, float* y, int64_t n, hipStream_t s);
 // The non-matmul ops of a layer (elmh_layer.hip), same float order as edgelm's cpu backend.
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps, hipStream_t s);

@@ -1895,7 +1895,9 @@ __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
   }
 }
 
-// T == 1, q8, rows of up to 2048 values: the products x_i * w_i (each rounded, as dot_q8 forms
+// T == 1, q8, rows whose products fit the launch's 64 KB of LDS (x plus [sel][8 rows][4 chains][stride]
+// floats: K up to 1792 for one output, up to 768 for SwiGLU; longer rows take the four-lane kernels
+// below): the products x_i * w_i (each rounded, as dot_q8 forms
 // them) are independent, so all 256 threads form them into LDS by chain ([sel][row][chain][K / 4],
 // rows padded by 4 floats against bank conflicts); then lane 4r + c of wave 0 adds chain c of row
 // r in order (the K mod 4 tail into chain 0) and ((s0 + s1) + (s2 + s3)) * ws follows. The
@@ -2569,24 +2571,30 @@ static size_t f32q4_lds_bytes(int K, int nb, int H, int nsel, bool norm) {
   return (base + (norm ? 4 * (size_t)(((K >> 2) + 31) & ~31) : 0)) * sizeof(float);
 }
 
-bool f32act_norm_ok(int T, int K, int nb, int H, int nsel) {
+// Rows per workgroup of gemv_f32act_q4_kernel (a divisor of H): the most rows whose (selection, row,
+// group) items take one pass of the 256 threads, raised while that makes more than 1024 workgroups
+// (each one stages all of x). rows: the output rows of the call.
+static int f32q4_tile_rows(int H, int nb, int nsel, int rows) {
+  int rt = H;
+  while (rt > 1 && nsel * rt * nb > 256) rt >>= 1;
+  while (rt < H && (rows + rt - 1) / rt > 1024) rt <<= 1;
+  return rt;
+}
+
+bool f32act_q4_ok(int T, int K, int nb, int H, int nsel, int rows, bool norm) {
   return T == 1 && H >= 1 && !(H & (H - 1)) && K == nb * kBlock &&
-         f32q4_lds_bytes(K, nb, H, nsel, true) <= kMaxLds - 1024;
+         f32q4_lds_bytes(K, nb, f32q4_tile_rows(H, nb, nsel, rows), nsel, norm) <= kMaxLds - 1024;
 }
 
 hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, hipStream_t s) {
   const int nsel = swiglu ? 2 : 1;
-  if (a.T == 1 && dtype == WQ4 && f32act_norm_ok(a.T, a.K, a.nb, a.H, nsel)) {
-    // one workgroup per tile of rt rows (rt divides H); the tile starts counted in tiles here.
-    // rt: the most rows whose items take one pass of the workgroup's threads, raised while that
-    // makes more than 1024 workgroups (each one stages all of x)
+  const int n = swiglu ? 1 : a.n_targets;
+  int rows = 0;
+  for (int i = 0; i < n; ++i) rows += a.tg[i].N;
+  if (a.T == 1 && dtype == WQ4 && f32act_q4_ok(a.T, a.K, a.nb, a.H, nsel, rows, a.nw != nullptr)) {
+    // one workgroup per tile of rt rows; the tile starts counted in tiles here
     F32Args b = a;
-    const int n = swiglu ? 1 : a.n_targets;
-    int rows = 0;
-    for (int i = 0; i < n; ++i) rows += a.tg[i].N;
-    int rt = a.H;
-    while (rt > 1 && nsel * rt * a.nb > 256) rt >>= 1;
-    while (rt < a.H && (rows + rt - 1) / rt > 1024) rt <<= 1;
+    const int rt = f32q4_tile_rows(a.H, a.nb, nsel, rows);
     b.rt = rt;
     int tiles = 0;
     for (int i = 0; i < n; ++i) {
@@ -2613,9 +2621,6 @@ hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, hipStream_t s)
     if (dtype != WQ8) return hipErrorInvalidValue;
     const size_t lds = (size_t)((a.K + 3) & ~3) * 4;
     if (lds > 64 * 1024) return hipErrorInvalidValue;
-    const int n = swiglu ? 1 : a.n_targets;
-    int rows = 0;
-    for (int i = 0; i < n; ++i) rows += a.tg[i].N;
     const size_t lds_p = ((size_t)((a.K + 3) & ~3) + (size_t)nsel * kQ8PRows * 4 * q8p_stride(a.K)) * 4;
     // products in LDS while the chains are the bottleneck (a layer's few rows); with many rows (an
     // LM head) the chip is full either way and the four-lane kernels below do less work per row
@@ -2654,7 +2659,6 @@ hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, hipStream_t s)
   } else {
     // grid x: kF32TT-token tiles (consecutive workgroups share their weight rows), y: 64-row groups
     F32Args b = a;
-    const int n = swiglu ? 1 : a.n_targets;
     int groups = 0;
     for (int i = 0; i < n; ++i) {
       b.tile_start[i] = groups;

@@ -57,13 +57,18 @@ struct AttnArgs {
 };
 
 namespace host {
-float dot_f32(const float* a, const float* b, int64_t k);  // four interleaved accumulators
+// Which of edgelm's two host backends an op reproduces. They round alike except in how a dot product
+// or sum of squares accumulates (one running sum, or four over the index mod 4) and in the softmax
+// weight of a position (e / sum, or e * (1 / sum)).
+enum class Flavor { Reference, Cpu };
+
 void embed(const int32_t* tokens, int T, const Tensor& table, float* y);
-void rmsnorm_ref(const float* x, const float* w, float* y, int rows, int dim, float eps);
-void rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps, ThreadPool* pool);
+// Reference runs serially; Cpu splits rows over `pool` (when non-null).
+void rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps, Flavor f, ThreadPool* pool);
 void rope(const float* x, float* y, int T, int n_heads, int head_dim, int pos0, const RopeTable& rt);
-void attention_ref(const AttnArgs& a);
-void attention(const AttnArgs& a, ThreadPool* pool);
+// Appends the step's keys and values to the cache, then one output row per (token, head); Cpu splits
+// the rows over `pool` (when non-null).
+void attention(const AttnArgs& a, Flavor f, ThreadPool* pool);
 void add(const float* a, const float* b, float* y, int64_t n);
 void silu(const float* x, float* y, int64_t n);
 void mul(const float* a, const float* b, float* y, int64_t n);

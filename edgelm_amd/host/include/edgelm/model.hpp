@@ -39,7 +39,8 @@ class Model {
 
   // Device image: every q8 / q4 weight in the repacked layout the hip delegate keeps in HBM
   // (elmh_repack_host), in one file, so that a later session uploads each weight as it will lie in
-  // HBM. The image records a digest of the model (its config, tensor table and weight contents);
+  // HBM. The image records a digest of the model (its config, tensor table and every byte of every
+  // weight's data and scales);
   // attach_device_image maps an image and points the weights at it, or returns false (and changes
   // nothing) when the file is missing or was written for other weights. Returns the weights written.
   int write_device_image(const std::string& path, int threads = 1) const;

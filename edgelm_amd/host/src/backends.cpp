@@ -76,10 +76,10 @@ class HostReference final : public Backend {
         host::embed(reinterpret_cast<const int32_t*>(c.f(op.in[0])), c.T, c.tensor(op.in[1]), c.f(op.out[0]));
         break;
       case OpType::RMSNORM:
-        host::rmsnorm_ref(c.f(op.in[0]), norm_weight(c, op), c.f(op.out[0]), static_cast<int>(c.rows(op.in[0])),
-                          static_cast<int>(c.tensor(op.in[0]).cols), op.fattr[0]);
+        host::rmsnorm(c.f(op.in[0]), norm_weight(c, op), c.f(op.out[0]), static_cast<int>(c.rows(op.in[0])),
+                      static_cast<int>(c.tensor(op.in[0]).cols), op.fattr[0], host::Flavor::Reference, nullptr);
         break;
-      case OpType::ATTENTION: host::attention_ref(attention_operands(op, c)); break;
+      case OpType::ATTENTION: host::attention(attention_operands(op, c), host::Flavor::Reference, nullptr); break;
       case OpType::LAST_ROWS: {
         const int64_t cols = c.tensor(op.in[0]).cols, keep = c.rows(op.out[0]), skip = c.rows(op.in[0]) - keep;
         if (skip < 0) throw std::runtime_error("edgelm: LAST_ROWS keeps more rows than it has");
@@ -103,9 +103,9 @@ class HostCpu final : public Backend {
     if (run_elementwise(op, c)) return;
     if (op.type == OpType::RMSNORM)
       host::rmsnorm(c.f(op.in[0]), norm_weight(c, op), c.f(op.out[0]), static_cast<int>(c.rows(op.in[0])),
-                    static_cast<int>(c.tensor(op.in[0]).cols), op.fattr[0], c.pool);
+                    static_cast<int>(c.tensor(op.in[0]).cols), op.fattr[0], host::Flavor::Cpu, c.pool);
     else if (op.type == OpType::ATTENTION)
-      host::attention(attention_operands(op, c), c.pool);
+      host::attention(attention_operands(op, c), host::Flavor::Cpu, c.pool);
     else
       unhandled(name(), op);
   }

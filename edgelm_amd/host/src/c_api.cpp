@@ -289,3 +289,59 @@ int elm_session_generate(elm_session* s, const int32_t* prompt, int n_prompt, in
 }
 
 }  // extern "C"
+
+// ---- the host ops alone (test hooks): flavor 0 = edgelm's reference backend, 1 = its cpu backend
+#include "edgelm/host_ops.hpp"
+
+namespace {
+host::Flavor flavor_of(int f) { return f ? host::Flavor::Cpu : host::Flavor::Reference; }
+}  // namespace
+
+extern "C" int elm_host_rope_table(int head_dim, int max_pos, float theta, float* cos_out, float* sin_out) {
+  return guard([&] {
+    const RopeTable rt(head_dim, max_pos, theta);
+    std::memcpy(cos_out, rt.cos.data(), rt.cos.size() * sizeof(float));
+    std::memcpy(sin_out, rt.sin.data(), rt.sin.size() * sizeof(float));
+    return 0;
+  });
+}
+
+extern "C" int elm_host_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps, int flavor,
+                                int threads) {
+  return guard([&] {
+    ThreadPool pool(threads);
+    host::rmsnorm(x, w, y, rows, dim, eps, flavor_of(flavor), threads > 1 ? &pool : nullptr);
+    return 0;
+  });
+}
+
+extern "C" int elm_host_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
+                                  int n_heads, int n_kv, int head_dim, float* kc, float* vc, int max_ctx, int rope,
+                                  float theta, int flavor, int threads) {
+  return guard([&] {
+    const RopeTable rt(head_dim, max_ctx, theta);
+    AttnArgs a{q, k, v, out, T, pos0, n_heads, n_kv, head_dim, KVLayer{kc, vc, max_ctx}, rope ? &rt : nullptr};
+    ThreadPool pool(threads);
+    host::attention(a, flavor_of(flavor), threads > 1 ? &pool : nullptr);
+    return 0;
+  });
+}
+
+extern "C" int elm_host_rope(const float* x, float* y, int T, int n_heads, int head_dim, int pos0, int max_pos,
+                             float theta) {
+  return guard([&] {
+    const RopeTable rt(head_dim, max_pos, theta);
+    host::rope(x, y, T, n_heads, head_dim, pos0, rt);
+    return 0;
+  });
+}
+
+// op: 0 add, 1 mul, 2 silu (b unused)
+extern "C" int elm_host_elementwise(int op, const float* a, const float* b, float* y, int64_t n) {
+  return guard([&] {
+    if (op == 0) host::add(a, b, y, n);
+    else if (op == 1) host::mul(a, b, y, n);
+    else host::silu(a, y, n);
+    return 0;
+  });
+}

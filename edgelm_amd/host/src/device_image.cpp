@@ -9,8 +9,9 @@
 //                       data and scales are
 //   arrays              each 256-byte aligned
 //
-// The digest covers the config, the tensor table, every weight's scales and a sample of every
-// weight's data (one 64-byte chunk in 64), so an image written for other weights is refused.
+// The digest covers the config, the tensor table and every byte of every weight's data and scales
+// (hashed in parallel, each 8-byte word through a full 64-bit finalizer so that any changed bit moves
+// the whole hash), so an image written for other weights is refused.
 #include <algorithm>
 #include <atomic>
 #include <cstdio>
@@ -52,17 +53,31 @@ static_assert(sizeof(ImageEntry) == 192, "image entry is 192 bytes");
 
 uint64_t align_up(uint64_t v) { return (v + kImageAlign - 1) / kImageAlign * kImageAlign; }
 
-// 64-bit FNV-1a over bytes, eight at a time where they line up.
+// 64-bit hash of byte strings fed in order. Each 8-byte word goes through murmur3's fmix64 finalizer
+// before it is folded in, so a change in any bit of any word changes every bit of the result with
+// probability 1/2; four lanes take the words in turn so the folds do not form one dependent chain.
 class Digest {
  public:
+  static uint64_t fmix(uint64_t x) {
+    x ^= x >> 33;
+    x *= 0xff51afd7ed558ccdull;
+    x ^= x >> 33;
+    x *= 0xc4ceb9fe1a85ec53ull;
+    return x ^ (x >> 33);
+  }
   void bytes(const void* p, size_t n) {
     const uint8_t* b = static_cast<const uint8_t*>(p);
-    for (; n >= 8; n -= 8, b += 8) {
-      uint64_t w;
-      std::memcpy(&w, b, 8);
-      h_ = (h_ ^ w) * 0x100000001b3ull;
-    }
-    for (; n > 0; --n, ++b) h_ = (h_ ^ *b) * 0x100000001b3ull;
+    uint64_t lane[4] = {h_, h_ ^ 0x9e3779b97f4a7c15ull, h_ ^ 0xbf58476d1ce4e5b9ull, h_ ^ 0x94d049bb133111ebull};
+    size_t i = 0;
+    for (; i + 32 <= n; i += 32)
+      for (int l = 0; l < 4; ++l) {
+        uint64_t w;
+        std::memcpy(&w, b + i + 8 * l, 8);
+        lane[l] = (lane[l] ^ fmix(w)) * 0x100000001b3ull;
+      }
+    uint64_t tail = n;  // the length, then the bytes past the last whole 32
+    for (; i < n; ++i) tail = (tail ^ b[i]) * 0x100000001b3ull;
+    h_ = fmix(fmix(fmix(fmix(lane[0]) ^ lane[1]) ^ lane[2]) ^ lane[3]) ^ fmix(tail);
   }
   template <class Pod>
   void pod(const Pod& v) {
@@ -74,6 +89,32 @@ class Digest {
   uint64_t h_ = 0xcbf29ce484222325ull;
 };
 
+// Digest of one array: 1 MiB pieces hashed on `threads` host threads, their hashes folded in order.
+uint64_t digest_array(const void* p, size_t n, int threads) {
+  constexpr size_t kPiece = size_t(1) << 20;
+  const size_t pieces = (n + kPiece - 1) / kPiece;
+  std::vector<uint64_t> part(pieces);
+  std::atomic<size_t> next{0};
+  auto work = [&] {
+    for (size_t i; (i = next.fetch_add(1)) < pieces;) {
+      Digest d;
+      d.bytes(static_cast<const uint8_t*>(p) + i * kPiece, std::min(kPiece, n - i * kPiece));
+      part[i] = d.value();
+    }
+  };
+  std::vector<std::thread> pool;
+  for (int k = 1; k < std::min<int>(threads, static_cast<int>(pieces)); ++k) pool.emplace_back(work);
+  work();
+  for (std::thread& th : pool) th.join();
+  Digest all;
+  all.pod(n);
+  if (!part.empty()) all.bytes(part.data(), part.size() * sizeof(uint64_t));
+  return all.value();
+}
+
+// Host threads for hashing a model's weights.
+int digest_threads() { return static_cast<int>(std::clamp(std::thread::hardware_concurrency(), 1u, 8u)); }
+
 // The weights an image holds: q8 / q4 weights whose layout libelmh accepts.
 bool imageable(const Tensor& t) {
   if (!t.is_weight() || (t.dtype != DType::Q8 && t.dtype != DType::Q4) || !t.data || !t.scales) return false;
@@ -84,6 +125,7 @@ bool imageable(const Tensor& t) {
 }  // namespace
 
 uint64_t Model::digest() const {
+  const int threads = digest_threads();
   Digest d;
   d.pod(cfg.vocab), d.pod(cfg.dim), d.pod(cfg.hidden), d.pod(cfg.n_layers), d.pod(cfg.n_heads);
   d.pod(cfg.n_kv_heads), d.pod(cfg.head_dim), d.pod(cfg.max_seq), d.pod(cfg.rope_theta), d.pod(cfg.norm_eps);
@@ -91,9 +133,8 @@ uint64_t Model::digest() const {
     d.bytes(t.name.data(), t.name.size());
     d.pod(t.kind), d.pod(t.dtype), d.pod(t.rows), d.pod(t.cols), d.pod(t.data_bytes), d.pod(t.scale_bytes);
     if (!t.is_weight()) continue;
-    if (t.scales) d.bytes(t.scales, t.scale_bytes);
-    const uint8_t* p = static_cast<const uint8_t*>(t.data);
-    for (size_t off = 0; p && off < t.data_bytes; off += 64 * 64) d.bytes(p + off, std::min<size_t>(64, t.data_bytes - off));
+    if (t.scales) d.pod(digest_array(t.scales, t.scale_bytes, threads));
+    if (t.data) d.pod(digest_array(t.data, t.data_bytes, threads));
   }
   return d.value();
 }
@@ -192,9 +233,11 @@ bool Model::attach_device_image(const std::string& path) {
   if (map->size() < sizeof(ImageHeader)) return false;
   ImageHeader h;
   std::memcpy(&h, map->base(), sizeof h);
+  // range checks as `offset <= size && length <= size - offset`, which cannot wrap
+  auto fits = [&](uint64_t off, uint64_t len) { return off <= map->size() && len <= map->size() - off; };
   if (std::memcmp(h.magic, kImageMagic, sizeof kImageMagic) != 0 || h.version != kImageVersion ||
       h.file_bytes != map->size() || h.table_offset != sizeof(ImageHeader) ||
-      h.table_offset + uint64_t(h.n_entries) * sizeof(ImageEntry) > map->size() || h.digest != digest())
+      !fits(h.table_offset, uint64_t(h.n_entries) * sizeof(ImageEntry)) || h.digest != digest())
     return false;
   std::unordered_map<std::string, Tensor*> by_name;
   for (Tensor& t : graph.tensors)
@@ -211,8 +254,8 @@ bool Model::attach_device_image(const std::string& path) {
     elmh_weight_layout(static_cast<int>(t.dtype), t.rows, t.cols, &H, &db, &sb);
     if (e->dtype != static_cast<uint32_t>(t.dtype) || e->rows != t.rows || e->cols != t.cols ||
         e->H != static_cast<uint32_t>(H) || e->data_bytes != db || e->scale_bytes != sb ||
-        e->data_offset % kImageAlign || e->scale_offset % kImageAlign || e->data_offset + db > map->size() ||
-        e->scale_offset + sb > map->size())
+        e->data_offset % kImageAlign || e->scale_offset % kImageAlign || !fits(e->data_offset, db) ||
+        !fits(e->scale_offset, sb))
       return false;
     hits.emplace_back(it->second, e);
   }

@@ -6,7 +6,8 @@
 //                    the model config and flags
 //   graph section    per tensor: u16 name length, name, TensorRecord; then per op: OpRecord, the
 //                    int32 input and output tensor ids, OpAttrs, u16 name length, name
-//   tokenizer        edgelm's vocabulary and merges (bounds-checked, not used: this build runs ids)
+//   tokenizer        edgelm's vocabulary and merges (only its extent is checked against the file:
+//                    this build runs token ids and never parses the section)
 //   weight blob      the arrays, each 64-byte aligned, at offsets relative to the blob start
 #include "edgelm/elm_container.hpp"
 
@@ -92,6 +93,13 @@ Model Model::load(const std::string& path) {
 
   const uint8_t* blob = file->base() + h.blob.off;
   SectionReader r(file->base() + h.graph.off, h.graph.len, "graph");
+  // every tensor record takes at least its name length and TensorRecord, every op record at least its
+  // OpRecord, OpAttrs and name length: counts the section cannot hold are refused before any allocation
+  const uint64_t min_tensor = sizeof(uint16_t) + sizeof(TensorRecord);
+  const uint64_t min_op = sizeof(OpRecord) + sizeof(OpAttrs) + sizeof(uint16_t);
+  if (h.n_tensors > h.graph.len / min_tensor || h.n_ops > (h.graph.len - h.n_tensors * min_tensor) / min_op)
+    corrupt(std::to_string(h.n_tensors) + " tensors and " + std::to_string(h.n_ops) + " ops cannot fit a graph section of " +
+            std::to_string(h.graph.len) + " bytes");
   m.graph.tensors.resize(h.n_tensors);
   for (Tensor& t : m.graph.tensors) {
     t.name = r.name();

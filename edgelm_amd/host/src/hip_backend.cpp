@@ -345,6 +345,11 @@ class HipBackend : public Backend {
       out[i] = tok;
     }
     if (i == n) return true;
+    // the replayed steps' token ids come from the device argmax (in range by construction); the first
+    // one may still be the caller's, so it gets run()'s check here
+    for (int k = p.begin; k < p.end; ++k)
+      if (g.ops[k].type == OpType::EMBED)
+        EDGELM_CHECK(tok >= 0 && tok < c.tensor(g.ops[k].in[1]).rows, "token id out of range");
     StepGraph& sg = graphs_[p.begin];
     // pinned staging: the ring's copy [kStepRing], then the first replayed step's token and position
     const size_t need = kStepRing + 2;

@@ -79,206 +79,202 @@ void ThreadPool::parallel_for(int64_t n, const std::function<void(int64_t, int64
 }
 
 // ------------------------------------------------------------------ ops
+//
+// The float arithmetic below is edgelm's, operation for operation, so that sessions mixing these
+// host ops with the hip backend are bit-identical to edgelm's. The two edgelm host backends differ in
+// two accumulation choices only, named here as a Flavor:
+//   * a dot product or sum of squares: one running sum (reference backend, kernels_ref.cpp:41-57,
+//     100-141) or four running sums over the element index mod 4, the tail added to the first, and
+//     the four combined as (0 + 1) + (2 + 3) (cpu backend, kernels_cpu.cpp:32-43, 326-335, 417-488);
+//   * the softmax weight of a position: e / sum (reference) or e * (1 / sum) (cpu).
+// Every other rounding (RoPE's rotation, the exponentials and their sum in position order, the value
+// accumulation o += p * v in position order, y = (x * inv) * w) is shared.
+
+namespace {
+
+// theta^(-2i / head_dim) for each rotated pair i, in double (kernels_ref.cpp:11-21).
+std::vector<double> inverse_frequencies(int head_dim, float theta) {
+  std::vector<double> f(static_cast<size_t>(head_dim / 2));
+  for (size_t i = 0; i < f.size(); ++i) f[i] = std::pow(static_cast<double>(theta), -2.0 * static_cast<int>(i) / head_dim);
+  return f;
+}
+
+}  // namespace
 
 RopeTable::RopeTable(int head_dim, int max_pos_, float theta) : half(head_dim / 2), max_pos(max_pos_) {
-  cos.resize(static_cast<size_t>(max_pos) * half);
-  sin.resize(cos.size());
+  const std::vector<double> freq = inverse_frequencies(head_dim, theta);
+  const size_t n = static_cast<size_t>(max_pos) * half;
+  cos.assign(n, 0.f);
+  sin.assign(n, 0.f);
+  size_t at = 0;
   for (int p = 0; p < max_pos; ++p)
-    for (int i = 0; i < half; ++i) {
-      const double ang = p * std::pow(static_cast<double>(theta), -2.0 * i / head_dim);  // in double
-      cos[static_cast<size_t>(p) * half + i] = static_cast<float>(std::cos(ang));
-      sin[static_cast<size_t>(p) * half + i] = static_cast<float>(std::sin(ang));
+    for (double f : freq) {
+      const double angle = p * f;
+      cos[at] = static_cast<float>(std::cos(angle));
+      sin[at] = static_cast<float>(std::sin(angle));
+      ++at;
     }
 }
 
 namespace host {
+namespace {
 
-float dot_f32(const float* a, const float* b, int64_t k) {
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  int64_t i = 0;
-  for (; i + 4 <= k; i += 4) {
-    s0 += a[i] * b[i];
-    s1 += a[i + 1] * b[i + 1];
-    s2 += a[i + 2] * b[i + 2];
-    s3 += a[i + 3] * b[i + 3];
-  }
-  for (; i < k; ++i) s0 += a[i] * b[i];
-  return (s0 + s1) + (s2 + s3);
+float sum_products_serial(const float* a, const float* b, int64_t n) {
+  float acc = 0.f;
+  for (int64_t i = 0; i < n; ++i) acc += a[i] * b[i];
+  return acc;
 }
+
+float sum_products_four(const float* a, const float* b, int64_t n) {
+  float part[4] = {0.f, 0.f, 0.f, 0.f};
+  const int64_t whole = n - n % 4;
+  for (int64_t base = 0; base < whole; base += 4)
+    for (int lane = 0; lane < 4; ++lane) part[lane] += a[base + lane] * b[base + lane];
+  for (int64_t i = whole; i < n; ++i) part[0] += a[i] * b[i];
+  return (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+inline float sum_products(Flavor f, const float* a, const float* b, int64_t n) {
+  return f == Flavor::Cpu ? sum_products_four(a, b, n) : sum_products_serial(a, b, n);
+}
+
+// The RoPE angles of one position: pair i of a head vector, (lo, hi) = (x[i], x[i + half]), becomes
+// (lo·c − hi·s, hi·c + lo·s), each product rounded on its own. src may equal dst.
+struct Rotation {
+  const float* c;
+  const float* s;
+  int half;
+  void apply(const float* src, float* dst) const {
+    for (int i = 0; i < half; ++i) {
+      const float lo = src[i], hi = src[i + half];
+      const float lo_c = lo * c[i], hi_s = hi * s[i], hi_c = hi * c[i], lo_s = lo * s[i];
+      dst[i] = lo_c - hi_s;
+      dst[i + half] = hi_c + lo_s;
+    }
+  }
+};
+
+Rotation rotation_at(const RopeTable& rt, int pos) {
+  const size_t at = static_cast<size_t>(pos) * rt.half;
+  return Rotation{rt.cos.data() + at, rt.sin.data() + at, rt.half};
+}
+
+// One layer's KV cache seen as rows of head_dim floats: [kv head][position][head_dim].
+struct CacheRows {
+  const KVLayer& kv;
+  int head_dim;
+  float* key(int kv_head, int pos) const { return kv.k + (static_cast<int64_t>(kv_head) * kv.max_ctx + pos) * head_dim; }
+  float* value(int kv_head, int pos) const { return kv.v + (static_cast<int64_t>(kv_head) * kv.max_ctx + pos) * head_dim; }
+};
+
+// The step's keys (rotated when RoPE is fused) and values go into the cache at positions pos0 .. pos0+T-1
+// before any query of the step reads it.
+void store_step(const AttnArgs& a, const CacheRows& cache) {
+  const int64_t width = static_cast<int64_t>(a.n_kv) * a.head_dim;
+  for (int t = 0; t < a.T; ++t) {
+    const int pos = a.pos0 + t;
+    for (int g = 0; g < a.n_kv; ++g) {
+      const int64_t from = t * width + static_cast<int64_t>(g) * a.head_dim;
+      if (a.rope) rotation_at(*a.rope, pos).apply(a.k + from, cache.key(g, pos));
+      else std::copy_n(a.k + from, a.head_dim, cache.key(g, pos));
+      std::copy_n(a.v + from, a.head_dim, cache.value(g, pos));
+    }
+  }
+}
+
+// Output row of query token t, head h: softmax over positions 0..pos0+t of q·k / sqrt(head_dim), then
+// the weighted sum of the value rows. `work` holds head_dim + (pos0 + T) floats.
+void attend(const AttnArgs& a, const CacheRows& cache, Flavor f, int t, int h, float* work) {
+  const int hd = a.head_dim, pos = a.pos0 + t, visible = pos + 1, group = h / (a.n_heads / a.n_kv);
+  const int64_t row = (static_cast<int64_t>(t) * a.n_heads + h) * hd;
+  const float* q = a.q + row;
+  float* rotated = work;
+  float* weight = work + hd;
+  if (a.rope) {
+    rotation_at(*a.rope, pos).apply(q, rotated);
+    q = rotated;
+  }
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+  float peak = -INFINITY;
+  for (int j = 0; j < visible; ++j) {
+    weight[j] = sum_products(f, q, cache.key(group, j), hd) * scale;
+    peak = std::max(peak, weight[j]);
+  }
+  float total = 0.f;
+  for (int j = 0; j < visible; ++j) {
+    weight[j] = std::exp(weight[j] - peak);
+    total += weight[j];
+  }
+  const float inv_total = 1.0f / total;
+  float* out = a.out + row;
+  std::fill_n(out, hd, 0.f);
+  for (int j = 0; j < visible; ++j) {
+    const float p = f == Flavor::Cpu ? weight[j] * inv_total : weight[j] / total;
+    const float* v = cache.value(group, j);
+    for (int i = 0; i < hd; ++i) out[i] += p * v[i];
+  }
+}
+
+}  // namespace
 
 void embed(const int32_t* tokens, int T, const Tensor& table, float* y) {
   for (int t = 0; t < T; ++t) {
-    EDGELM_CHECK(tokens[t] >= 0 && tokens[t] < table.rows, "token id out of range");
-    dequantize_row(table, tokens[t], y + static_cast<int64_t>(t) * table.cols);
+    const int32_t id = tokens[t];
+    EDGELM_CHECK(id >= 0 && id < table.rows, "token id out of range");
+    dequantize_row(table, id, y + static_cast<int64_t>(t) * table.cols);
   }
 }
 
-void rmsnorm_ref(const float* x, const float* w, float* y, int rows, int dim, float eps) {
-  for (int r = 0; r < rows; ++r) {
-    const float* xr = x + static_cast<int64_t>(r) * dim;
-    float ss = 0.f;
-    for (int i = 0; i < dim; ++i) ss += xr[i] * xr[i];
-    const float inv = 1.0f / std::sqrt(ss / dim + eps);
-    for (int i = 0; i < dim; ++i) y[static_cast<int64_t>(r) * dim + i] = xr[i] * inv * w[i];
-  }
-}
-
-void rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps, ThreadPool* pool) {
-  auto body = [&](int64_t b, int64_t e) {
-    for (int64_t r = b; r < e; ++r) {
-      const float* xr = x + r * dim;
-      float* yr = y + r * dim;
-      const float inv = 1.0f / std::sqrt(dot_f32(xr, xr, dim) / dim + eps);
-      for (int i = 0; i < dim; ++i) yr[i] = xr[i] * inv * w[i];
+void rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps, Flavor f, ThreadPool* pool) {
+  auto normalize = [&](int64_t first, int64_t last) {
+    for (int64_t r = first; r < last; ++r) {
+      const float* in = x + r * dim;
+      float* out = y + r * dim;
+      const float squares = sum_products(f, in, in, dim);
+      const float inv = 1.0f / std::sqrt(squares / dim + eps);
+      for (int i = 0; i < dim; ++i) out[i] = in[i] * inv * w[i];
     }
   };
-  if (pool && rows > 8) pool->parallel_for(rows, body);
-  else body(0, rows);
+  if (pool && f == Flavor::Cpu && rows > 8) pool->parallel_for(rows, normalize);
+  else normalize(0, rows);
 }
 
 void rope(const float* x, float* y, int T, int n_heads, int hd, int pos0, const RopeTable& rt) {
-  const int h2 = hd / 2;
   for (int t = 0; t < T; ++t) {
     EDGELM_CHECK(pos0 + t < rt.max_pos, "position beyond rope table");
-    const float* c = &rt.cos[static_cast<size_t>(pos0 + t) * h2];
-    const float* s = &rt.sin[static_cast<size_t>(pos0 + t) * h2];
+    const Rotation r = rotation_at(rt, pos0 + t);
     for (int h = 0; h < n_heads; ++h) {
-      const float* xi = x + (static_cast<int64_t>(t) * n_heads + h) * hd;
-      float* yo = y + (static_cast<int64_t>(t) * n_heads + h) * hd;
-      for (int i = 0; i < h2; ++i) {
-        const float a = xi[i], b = xi[i + h2];
-        yo[i] = a * c[i] - b * s[i];
-        yo[i + h2] = b * c[i] + a * s[i];
-      }
+      const int64_t at = (static_cast<int64_t>(t) * n_heads + h) * hd;
+      r.apply(x + at, y + at);
     }
   }
 }
 
-namespace {
-// Appends this step's keys (rotated when the rope is fused) and values to the cache.
-void append_kv(const AttnArgs& a) {
-  const int hd = a.head_dim, h2 = hd / 2, kvd = a.n_kv * hd;
-  const int64_t mc = a.cache.max_ctx;
-  for (int t = 0; t < a.T; ++t) {
-    const int pos = a.pos0 + t;
-    for (int h = 0; h < a.n_kv; ++h) {
-      const float* ks = a.k + static_cast<int64_t>(t) * kvd + h * hd;
-      float* kd = a.cache.k + (h * mc + pos) * hd;
-      if (a.rope) {
-        const float* c = &a.rope->cos[static_cast<size_t>(pos) * h2];
-        const float* s = &a.rope->sin[static_cast<size_t>(pos) * h2];
-        for (int i = 0; i < h2; ++i) {
-          kd[i] = ks[i] * c[i] - ks[i + h2] * s[i];
-          kd[i + h2] = ks[i + h2] * c[i] + ks[i] * s[i];
-        }
-      } else {
-        std::memcpy(kd, ks, sizeof(float) * hd);
-      }
-      std::memcpy(a.cache.v + (h * mc + pos) * hd, a.v + static_cast<int64_t>(t) * kvd + h * hd, sizeof(float) * hd);
-    }
-  }
-}
-}  // namespace
-
-// edgelm's cpu attention (kernels_cpu.cpp:417-488, scalar path): one item per (token, head).
-void attention(const AttnArgs& a, ThreadPool* pool) {
-  const int hd = a.head_dim, h2 = hd / 2, qd = a.n_heads * hd, grp = a.n_heads / a.n_kv;
-  const int64_t mc = a.cache.max_ctx;
-  EDGELM_CHECK(a.pos0 + a.T <= mc, "context overflow");
-  append_kv(a);
-  const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
-  auto body = [&](int64_t b, int64_t e) {
-    std::vector<float> qbuf(static_cast<size_t>(hd)), sc(static_cast<size_t>(a.pos0 + a.T));
-    for (int64_t idx = b; idx < e; ++idx) {
-      const int t = static_cast<int>(idx / a.n_heads), h = static_cast<int>(idx % a.n_heads);
-      const int pos = a.pos0 + t;
-      const float* q = a.q + static_cast<int64_t>(t) * qd + h * hd;
-      if (a.rope) {
-        const float* c = &a.rope->cos[static_cast<size_t>(pos) * h2];
-        const float* s = &a.rope->sin[static_cast<size_t>(pos) * h2];
-        for (int i = 0; i < h2; ++i) {
-          qbuf[i] = q[i] * c[i] - q[i + h2] * s[i];
-          qbuf[i + h2] = q[i + h2] * c[i] + q[i] * s[i];
-        }
-        q = qbuf.data();
-      }
-      const float* kc = a.cache.k + (h / grp) * mc * hd;
-      const float* vc = a.cache.v + (h / grp) * mc * hd;
-      const int n = pos + 1;
-      float mx = -INFINITY;
-      for (int j = 0; j < n; ++j) {
-        sc[j] = dot_f32(q, kc + static_cast<int64_t>(j) * hd, hd) * scale;
-        mx = std::max(mx, sc[j]);
-      }
-      float sum = 0.f;
-      for (int j = 0; j < n; ++j) sum += (sc[j] = std::exp(sc[j] - mx));
-      const float inv = 1.0f / sum;
-      float* o = a.out + static_cast<int64_t>(t) * qd + h * hd;
-      std::fill(o, o + hd, 0.f);
-      for (int j = 0; j < n; ++j) {
-        const float p = sc[j] * inv;
-        const float* vj = vc + static_cast<int64_t>(j) * hd;
-        for (int i = 0; i < hd; ++i) o[i] += p * vj[i];
-      }
-    }
-  };
-  const int64_t items = static_cast<int64_t>(a.T) * a.n_heads;
-  if (pool) pool->parallel_for(items, body);
-  else body(0, items);
-}
-
-// edgelm's reference attention (kernels_ref.cpp:100-141).
-void attention_ref(const AttnArgs& a) {
-  const int hd = a.head_dim, kvd = a.n_kv * hd, qd = a.n_heads * hd, grp = a.n_heads / a.n_kv;
+void attention(const AttnArgs& a, Flavor f, ThreadPool* pool) {
   EDGELM_CHECK(a.pos0 + a.T <= a.cache.max_ctx, "context overflow");
-  std::vector<float> kr(static_cast<size_t>(a.T) * kvd), qr(static_cast<size_t>(a.T) * qd);
-  const float* k = a.k;
-  const float* q = a.q;
-  if (a.rope) {
-    rope(a.k, kr.data(), a.T, a.n_kv, hd, a.pos0, *a.rope);
-    rope(a.q, qr.data(), a.T, a.n_heads, hd, a.pos0, *a.rope);
-    k = kr.data();
-    q = qr.data();
-  }
-  for (int t = 0; t < a.T; ++t)
-    for (int h = 0; h < a.n_kv; ++h)
-      for (int i = 0; i < hd; ++i) {
-        const size_t dst = (static_cast<size_t>(h) * a.cache.max_ctx + a.pos0 + t) * hd + i;
-        a.cache.k[dst] = k[static_cast<size_t>(t) * kvd + h * hd + i];
-        a.cache.v[dst] = a.v[static_cast<size_t>(t) * kvd + h * hd + i];
-      }
-  const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
-  std::vector<float> sc(static_cast<size_t>(a.pos0 + a.T));
-  for (int t = 0; t < a.T; ++t)
-    for (int h = 0; h < a.n_heads; ++h) {
-      const float* qv = q + static_cast<size_t>(t) * qd + h * hd;
-      const float* kc = a.cache.k + static_cast<size_t>(h / grp) * a.cache.max_ctx * hd;
-      const float* vc = a.cache.v + static_cast<size_t>(h / grp) * a.cache.max_ctx * hd;
-      const int n = a.pos0 + t + 1;
-      float mx = -INFINITY;
-      for (int j = 0; j < n; ++j) {
-        float d = 0.f;
-        for (int i = 0; i < hd; ++i) d += qv[i] * kc[static_cast<size_t>(j) * hd + i];
-        sc[j] = d * scale;
-        mx = std::max(mx, sc[j]);
-      }
-      float sum = 0.f;
-      for (int j = 0; j < n; ++j) sum += (sc[j] = std::exp(sc[j] - mx));
-      float* o = a.out + static_cast<size_t>(t) * qd + h * hd;
-      for (int i = 0; i < hd; ++i) o[i] = 0.f;
-      for (int j = 0; j < n; ++j)
-        for (int i = 0; i < hd; ++i) o[i] += sc[j] / sum * vc[static_cast<size_t>(j) * hd + i];
-    }
+  if (a.rope && f == Flavor::Reference)  // the reference backend rotates through its rope op
+    EDGELM_CHECK(a.pos0 + a.T <= a.rope->max_pos, "position beyond rope table");
+  const CacheRows cache{a.cache, a.head_dim};
+  store_step(a, cache);
+  const size_t work = static_cast<size_t>(a.head_dim) + static_cast<size_t>(a.pos0 + a.T);
+  auto items = [&](int64_t first, int64_t last) {
+    std::vector<float> scratch(work);
+    for (int64_t i = first; i < last; ++i)
+      attend(a, cache, f, static_cast<int>(i / a.n_heads), static_cast<int>(i % a.n_heads), scratch.data());
+  };
+  const int64_t n = static_cast<int64_t>(a.T) * a.n_heads;
+  if (pool && f == Flavor::Cpu) pool->parallel_for(n, items);
+  else items(0, n);
 }
 
 void add(const float* a, const float* b, float* y, int64_t n) {
-  for (int64_t i = 0; i < n; ++i) y[i] = a[i] + b[i];
-}
-void silu(const float* x, float* y, int64_t n) {
-  for (int64_t i = 0; i < n; ++i) y[i] = x[i] / (1.0f + std::exp(-x[i]));
+  std::transform(a, a + n, b, y, [](float u, float v) { return u + v; });
 }
 void mul(const float* a, const float* b, float* y, int64_t n) {
-  for (int64_t i = 0; i < n; ++i) y[i] = a[i] * b[i];
+  std::transform(a, a + n, b, y, [](float u, float v) { return u * v; });
+}
+void silu(const float* x, float* y, int64_t n) {
+  std::transform(x, x + n, y, [](float v) { return v / (1.0f + std::exp(-v)); });
 }
 
 }  // namespace host

@@ -1,4 +1,5 @@
-// Load-time weight quantizers (edgelm model.cpp:150-190), split over host threads by rows.
+// Load-time weight quantizers, byte-identical to edgelm's quantize_q8 / quantize_q4 (model.cpp:150-190),
+// with the rows split over host threads.
 #include <algorithm>
 #include <cmath>
 #include <thread>
@@ -8,39 +9,52 @@
 
 namespace {
 
-inline float round_away(float v) { return std::copysign(std::floor(std::fabs(v) + 0.5f), v); }  // model.cpp:63
+// Nearest integer, halves away from zero (edgelm's round_away, model.cpp:63), clamped to [lo, hi] as
+// min(hi, max(lo, r)).
+inline float level(float v, float lo, float hi) {
+  const float r = std::copysign(std::floor(std::fabs(v) + 0.5f), v);
+  return std::min(hi, std::max(lo, r));
+}
 
+// What a row or group is divided by: its scale, or 1 when the scale is 0 (all-zero data).
+inline float divisor(float scale) { return scale == 0.f ? 1.f : scale; }
+
+// q8 (model.cpp:150-163): one scale per row, the row's largest magnitude / 127; levels in [-127, 127].
 void q8_rows(const float* w, int64_t r0, int64_t r1, int64_t k, int8_t* out, float* scales) {
   for (int64_t r = r0; r < r1; ++r) {
-    const float* row = w + r * k;
+    const float* src = w + r * k;
     float amax = 0.f;
-    for (int64_t i = 0; i < k; ++i) amax = std::max(amax, std::fabs(row[i]));
-    const float s = amax / 127.0f;
-    const float safe = s == 0.f ? 1.f : s;
-    scales[r] = s;
-    for (int64_t i = 0; i < k; ++i)
-      out[r * k + i] = static_cast<int8_t>(std::min(127.f, std::max(-127.f, round_away(row[i] / safe))));
+    for (int64_t i = 0; i < k; ++i) amax = std::max(amax, std::fabs(src[i]));
+    scales[r] = amax / 127.0f;
+    const float div = divisor(scales[r]);
+    std::transform(src, src + k, out + r * k,
+                   [div](float v) { return static_cast<int8_t>(level(v / div, -127.f, 127.f)); });
   }
 }
 
+// Index of the first element of largest magnitude in x[0, n) (numpy argmax's tie rule).
+int first_peak(const float* x, int n) {
+  int best = 0;
+  for (int i = 1; i < n; ++i)
+    if (std::fabs(x[i]) > std::fabs(x[best])) best = i;
+  return best;
+}
+
+// q4 (model.cpp:165-190): per 32-element group, scale = (signed element of largest magnitude) / -8, levels
+// in [-8, 7] stored as level + 8; byte j of the group's 16 holds element j in its low nibble and element
+// j + 16 in its high nibble.
 void q4_rows(const float* w, int64_t r0, int64_t r1, int64_t k, uint8_t* out, float* scales) {
-  constexpr int G = 32;
+  constexpr int G = 32, H = G / 2;
+  const int64_t groups = k / G;
   for (int64_t r = r0; r < r1; ++r)
-    for (int64_t g = 0; g < k / G; ++g) {
-      const float* x = w + r * k + g * G;
-      int best = 0;  // first element of largest magnitude
-      float amax = std::fabs(x[0]);
-      for (int i = 1; i < G; ++i)
-        if (std::fabs(x[i]) > amax) {
-          amax = std::fabs(x[i]);
-          best = i;
-        }
-      const float d = x[best] / -8.0f;
-      const float safe = d == 0.f ? 1.f : d;
-      scales[r * (k / G) + g] = d;
-      uint8_t* o = out + r * (k / 2) + g * (G / 2);
-      auto q = [&](float v) { return static_cast<uint8_t>(std::min(7.f, std::max(-8.f, round_away(v / safe))) + 8); };
-      for (int i = 0; i < G / 2; ++i) o[i] = static_cast<uint8_t>(q(x[i]) | (q(x[i + G / 2]) << 4));
+    for (int64_t g = 0; g < groups; ++g) {
+      const float* src = w + r * k + g * G;
+      const float d = src[first_peak(src, G)] / -8.0f;
+      scales[r * groups + g] = d;
+      const float div = divisor(d);
+      auto nibble = [div](float v) { return static_cast<uint8_t>(level(v / div, -8.f, 7.f) + 8); };
+      uint8_t* dst = out + r * (k / 2) + g * H;
+      for (int j = 0; j < H; ++j) dst[j] = static_cast<uint8_t>(nibble(src[j]) | (nibble(src[j + H]) << 4));
     }
 }
 

@@ -97,6 +97,20 @@ int elm_session_bench(elm_session* s, const int32_t* prompt, int n_prompt, int w
 int elm_session_generate(elm_session* s, const int32_t* prompt, int n_prompt, int gen, double* prefill_ms,
                          double* ttft_ms, double* decode_ms, int32_t* tokens_out);
 
+/* ---- test hooks: the host ops a partition leaves on the CPU, alone. flavor 0 reproduces edgelm's
+ * reference backend (kernels_ref.cpp:11-21,41-57,82-151), 1 its cpu backend's x86 scalar path
+ * (kernels_cpu.cpp:326-335,413-492); threads > 1 splits the cpu flavor's rows / (token, head) items
+ * over a pool. The caches are [n_kv][max_ctx][head_dim]; the RoPE table covers max_ctx positions.
+ * Return 0, or -1 with elm_last_error() (context overflow, position beyond the table). */
+int elm_host_rope_table(int head_dim, int max_pos, float theta, float* cos_out, float* sin_out);
+int elm_host_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps, int flavor, int threads);
+int elm_host_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0, int n_heads,
+                       int n_kv, int head_dim, float* kc, float* vc, int max_ctx, int rope, float theta, int flavor,
+                       int threads);
+int elm_host_rope(const float* x, float* y, int T, int n_heads, int head_dim, int pos0, int max_pos, float theta);
+/* op: 0 add, 1 mul, 2 silu (b unused) */
+int elm_host_elementwise(int op, const float* a, const float* b, float* y, int64_t n);
+
 #ifdef __cplusplus
 }
 #endif

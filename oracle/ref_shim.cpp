@@ -275,3 +275,63 @@ void eref_attention(const float* q, const float* k, const float* v, float* out, 
   cpu::attention(a, nullptr, &sp);
 }
 }  // extern "C"
+
+// edgelm's reference-backend ops (kernels_ref.cpp:41-57,82-151), serial.
+extern "C" {
+void eref_ref_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps) {
+  ref::rmsnorm(x, w, y, rows, dim, eps);
+}
+void eref_ref_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0, int n_heads,
+                        int n_kv, int hd, float* kc, float* vc, int max_ctx, int rope, float theta) {
+  RopeTable rt(hd, max_ctx, theta);
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.T = T;
+  a.pos0 = pos0;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv;
+  a.head_dim = hd;
+  a.cache.k = kc;
+  a.cache.v = vc;
+  a.cache.max_ctx = max_ctx;
+  a.rope = rope ? &rt : nullptr;
+  ref::attention(a);
+}
+void eref_ref_rope(const float* x, float* y, int T, int n_heads, int hd, int pos0, int max_pos, float theta) {
+  RopeTable rt(hd, max_pos, theta);
+  ref::rope(x, y, T, n_heads, hd, pos0, rt);
+}
+void eref_ref_elementwise(int op, const float* a, const float* b, float* y, int64_t n) {
+  if (op == 0) ref::add(a, b, y, n);
+  else if (op == 1) ref::mul(a, b, y, n);
+  else ref::silu(a, y, n);
+}
+// cpu::attention over a pool of `threads` (scratch per thread as the cpu backend sizes it)
+void eref_cpu_attention_pool(const float* q, const float* k, const float* v, float* out, int T, int pos0, int n_heads,
+                             int n_kv, int hd, float* kc, float* vc, int max_ctx, int rope, float theta, int threads) {
+  RopeTable rt(hd, max_ctx, theta);
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.T = T;
+  a.pos0 = pos0;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv;
+  a.head_dim = hd;
+  a.cache.k = kc;
+  a.cache.v = vc;
+  a.cache.max_ctx = max_ctx;
+  a.rope = rope ? &rt : nullptr;
+  ThreadPool pool(threads);
+  std::vector<std::vector<float>> bufs;
+  std::vector<float*> ptrs;
+  for (int i = 0; i < pool.size(); ++i) bufs.emplace_back(cpu::scratch_floats(T, hd, max_ctx, hd));
+  for (auto& b : bufs) ptrs.push_back(b.data());
+  cpu::attention(a, &pool, ptrs.data());
+}
+}  // extern "C"

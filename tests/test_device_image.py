@@ -117,3 +117,32 @@ def test_attach_refuses_other_weights_and_broken_files(models):
     assert not m.attach_device_image(bad)                  # not an image
     assert m.attach_device_image(img)
     other.close(), m.close()
+
+
+@pytest.mark.parametrize("offset,bit", [(100, 0x80), (1031, 0x01), (3000, 0x10)])
+def test_attach_refuses_a_one_byte_edit_anywhere(models, offset, bit):
+    """A model re-exported to the same path with one weight byte changed (away from any 64-byte sample the
+    digest once took, in a high or a low bit of its word) must not attach the image of the old weights."""
+    d, paths = models
+    img = str(d / f"edit{offset}.img")
+    host.Model(paths["a"]).write_device_image(img)
+    m = host.Model(paths["a"])
+    _, data, _ = m.weight("model.layers.0.mlp.down_proj.weight")
+    m.close()
+    with open(paths["a"], "rb") as f:
+        blob = bytearray(f.read())
+    raw = data.view(np.uint8).ravel()
+    assert raw.size > offset + 64
+    at = blob.find(bytes(raw[:256]))
+    assert at > 0 and blob.find(bytes(raw[:256]), at + 1) < 0  # the weight's bytes sit once in the file
+    edited = str(d / f"edit{offset}.elm")
+    blob[at + offset] ^= bit
+    with open(edited, "wb") as f:
+        f.write(blob)
+    e = host.Model(edited)
+    assert not e.attach_device_image(img)
+    assert e.weight("model.layers.0.mlp.down_proj.weight")[1].view(np.uint8).ravel()[offset] == raw[offset] ^ bit
+    e.close()
+    same = host.Model(paths["a"])
+    assert same.attach_device_image(img)
+    same.close()

@@ -186,4 +186,9 @@ def test_greedy_steps_match_edgelm(smollm, backends):
     a = s.forward(np.array([got[-1]], np.int32))
     b = ref.forward(np.array([want[-1]], np.int32))
     assert bits_equal(a, b)
+    # a first token outside the vocabulary is refused as edgelm's Session refuses it, also when the step
+    # graph is already captured (the replayed steps skip run()'s host checks)
+    for bad in (49152, -1):
+        with pytest.raises(RuntimeError, match="token id out of range"):
+            s.greedy_steps(bad, 3)
     s.close(), ref.close()

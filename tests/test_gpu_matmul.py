@@ -333,6 +333,16 @@ def test_matmul_f32act_long_rows(ctx, dt):
             got = ctx.matmul(x, [dw], [res], act=E.ACT_F32)[0]
             assert bits_equal(got, O.cpu_matmul(x, [w], [res], act_quant=False)[0]), f"T={T}"
         dw.free()
+    # SwiGLU at K from 16288 to 16384 (H = 8 for q4): the group-parallel q4 GEMV takes one-row tiles there,
+    # and its LDS check must size them, not the layout's 8-row tiles, at one token as at several
+    for k in (16288, 16384):
+        wg, wu = weight(r, 40, k, dt), weight(r, 40, k, dt)
+        dg, du = up(ctx, wg), up(ctx, wu)
+        for T in [1, 3]:
+            print(f"[gpu] swiglu f32act long dt={dt} 40x{k} T={T}", flush=True)
+            x = r.normal(0, 1, (T, k)).astype(np.float32)
+            assert bits_equal(ctx.swiglu(x, dg, du, act=E.ACT_F32), O.cpu_swiglu(x, wg, wu, act_quant=False)), f"T={T}"
+        dg.free(), du.free()
 
 
 @pytest.mark.parametrize("tile", ["64", "128"])

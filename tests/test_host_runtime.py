@@ -37,6 +37,17 @@ def test_loader_config_and_graph(tiny):
         f.write(b"definitely not an elm file" + b"." * 200)
     with pytest.raises(RuntimeError):
         host.Model(bad)
+    # record counts the graph section cannot hold (u32 n_tensors at byte 8, n_ops at byte 12) are refused as
+    # a malformed file before anything is allocated for them
+    with open(tiny["q8"], "rb") as f:
+        blob = bytearray(f.read())
+    for at in (8, 12):
+        huge = bytearray(blob)
+        huge[at:at + 4] = (0xFFFFFFFF).to_bytes(4, "little")
+        with open(bad, "wb") as f:
+            f.write(huge)
+        with pytest.raises(RuntimeError, match="malformed .elm file"):
+            host.Model(bad)
 
 
 def test_fusion_and_planner(tiny):
