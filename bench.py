@@ -316,6 +316,204 @@ def gemm_bench(ctx, E, T, shapes, dt=1, act=None, reps=10, eager=False):
     return out
 
 
+class HostWeight:
+    """One weight quantized on the host with edgelm's quantizers (the product's host.quantize_*), kept in the
+    export layout so the same bytes feed the GPU upload and edgelm's cpu backend."""
+
+    def __init__(self, seed, n, k, dtype):
+        from edgelm_amd import host
+        f = randn(seed, n, k)
+        self.dtype, self.rows, self.cols = dtype, n, k
+        self.data, self.scales = host.quantize_q4(f) if dtype == 2 else host.quantize_q8(f)
+
+    def rows_sample(self, m):
+        """The first m rows (the CPU baseline's bounded sample: edgelm's work per row is the same for every row)."""
+        h = HostWeight.__new__(HostWeight)
+        h.dtype, h.rows, h.cols = self.dtype, m, self.cols
+        h.data = np.ascontiguousarray(self.data[:m])
+        h.scales = np.ascontiguousarray(self.scales[:m])
+        return h
+
+
+def measured_ceilings(ctx, E, reps=10):
+    """Read and copy bandwidth this GPU reaches, for the roofline next to the nominal 8 TB/s: elmh_read_sweep_dev
+    over 4 GiB (far past the 256 MB Infinity Cache: HBM) and over 128 MiB read again and again (past the 8 x 4 MB
+    of L2, inside the Infinity Cache), and a 2 GiB device-to-device copy (read + write bytes)."""
+    sinkn = E.Context.read_sweep_sink_bytes()
+    sink = ctx.buffer(sinkn)
+    out = {}
+    for name, n, inner in (("hbm_read_GBs", 4 << 30, 1), ("infinity_cache_read_GBs", 128 << 20, 16)):
+        b = ctx.buffer(n)
+        ctx.memset_dev(b.ptr, 1, n)
+        ms = time_graph(ctx, lambda: ctx.read_sweep_dev(b.ptr, n, sink.ptr), reps, inner=inner)
+        out[name] = n / (ms * 1e-3) / 1e9
+        out[name.replace("_GBs", "_bytes")] = n
+        b.free()
+    n = 2 << 30
+    src, dst = ctx.buffer(n), ctx.buffer(n)
+    ctx.memset_dev(src.ptr, 1, n)
+    ms = time_eager(ctx, lambda: ctx.memcpy_d2d(dst.ptr, src.ptr, n), reps)
+    out["hbm_copy_GBs"] = 2 * n / (ms * 1e-3) / 1e9
+    out["hbm_copy_bytes"] = n
+    for b in (src, dst, sink):
+        b.free()
+    log("measured ceilings: HBM read {hbm_read_GBs:.0f} GB/s, Infinity Cache read {infinity_cache_read_GBs:.0f} GB/s, "
+        "HBM copy {hbm_copy_GBs:.0f} GB/s (read + write)".format(**out))
+    return out
+
+
+def cpu_op_baseline(op, T, threads_list=(1, 4, 16), macs_per_thread=30e6, budget_s=0.3):
+    """CPU-baseline leg for one op: edgelm's own cpu::matmul / cpu::swiglu (oracle/_ref, compiled from the
+    reference sources; its ThreadPool, x86 scalar path) on the op's host weights and a seeded x, timed in C.
+    A call is bounded to about macs_per_thread multiply-adds per thread: bigger ops run on the first rows of
+    each weight (edgelm's cost per row is the same for every row) and their time is scaled to the whole op;
+    `sample` says which."""
+    import oracle as O
+    if not O.ref_available():
+        return None
+    ws, kind = op["weights"], op["kind"]
+    K = ws[0].cols
+    full = sum(w.rows for w in (ws[:1] if kind == "swiglu" else ws)) * (2 if kind == "swiglu" else 1) * T * K
+    x = np.random.default_rng(3).standard_normal((T, K), dtype=np.float32)
+    out = {}
+    for th in threads_list:
+        # at least two of edgelm's 16-row blocks per thread, so the sample keeps every thread busy
+        f = min(1.0, macs_per_thread * th / full)
+        sw = [w if f >= 1.0 else w.rows_sample(min(w.rows, max(32 * th, int(round(w.rows * f / 16)) * 16))) for w in ws]
+        done = sum(w.rows for w in (sw[:1] if kind == "swiglu" else sw)) * (2 if kind == "swiglu" else 1) * T * K
+        res = None
+        if op.get("residual"):
+            res = [np.random.default_rng(4).standard_normal((T, w.rows), dtype=np.float32) for w in sw]
+        med, reps = O.rq_time_cpu_op(th, x, sw, res, act_quant=op["act"] != "f32", swiglu=kind == "swiglu",
+                                     budget_s=budget_s)
+        us = med * 1e3 * full / done
+        out[str(th)] = {"us": us, "reps": reps,
+                        "sample": "whole op" if done == full else f"first {sw[0].rows} of {ws[0].rows} rows "
+                                                                  f"per weight, time scaled by {full / done:.2f}"}
+    return out
+
+
+def pair_rates(entry, nbytes=None, ops=None, ceil=None):
+    """Adds GB/s (nbytes) or TOP/s (ops) and roofline fractions to a {gpu_us, cpu: {threads: {us}}} entry."""
+    def rate(us):
+        return (nbytes / (us * 1e-6) / 1e9) if nbytes else (ops / (us * 1e-6) / 1e12)
+    g = entry["gpu_us"]
+    if nbytes:
+        entry.update(unit="GB/s", algorithmic_bytes=nbytes, gpu_GBs=rate(g), gpu_frac_hbm_peak=rate(g) / HBM_PEAK_GBS)
+        if ceil:
+            entry["gpu_frac_hbm_read_measured"] = rate(g) / ceil["hbm_read_GBs"]
+            entry["gpu_frac_infinity_cache_read_measured"] = rate(g) / ceil["infinity_cache_read_GBs"]
+    else:
+        entry.update(unit="TOP/s", int_ops=ops, gpu_TOPs=rate(g), gpu_frac_int8_peak=rate(g) / INT8_PEAK_TOPS)
+    for v in (entry.get("cpu") or {}).values():
+        v["GBs" if nbytes else "TOPs"] = rate(v["us"])
+    if entry.get("cpu"):
+        best = min(v["us"] for v in entry["cpu"].values())
+        entry["gpu_speedup_vs_best_cpu"] = best / g
+    return entry
+
+
+def config_pairs(ctx, E, per_decode, per_8b, ceil, cpu=True, reps=10):
+    """Every BASELINE config on the GPU beside edgelm's cpu backend at 1 / 4 / 16 threads, same inputs:
+    configs[0] (q8 GEMV 960x576, f32 activations), configs[1] (the SmolLM2 W4A8 decode ops: GPU times from the
+    decode chain), configs[2] (the SmolLM2 ops at T = 32 / 128 / 512, W8A8 in edgelm's per-block mode, epilogues
+    fused), configs[4] (the 8B W4A8 ops at T = 1: GPU times from the 8-layer sweep; and at T = 512)."""
+    out = {}
+    copies = 30  # T = 1 ops cycle through 30 distinct weights, as a decode step's 30 layers do
+
+    def gpu_time(fn, T, inner):
+        return time_graph(ctx, fn, reps, inner=inner) * 1e3
+
+    # configs[0]
+    w0 = [HostWeight(700 + i, 960, 576, 1) for i in range(copies)]
+    d0 = [ctx.upload(1, 960, 576, w.data, w.scales) for w in w0]
+    bx = ctx.buffer(512 * 14336 * 4)  # x of every op below: at most T = 512 rows of K = 14336
+    bx.upload(np.random.default_rng(3).standard_normal(512 * 14336, dtype=np.float32))
+    ctx.reserve(512, 14336)
+    y0 = ctx.buffer(960 * 4)
+    us = time_graph(ctx, lambda: [ctx.matmul_dev(bx.ptr, 1, 576, [d], [y0.ptr], act=E.ACT_F32) for d in d0],
+                    reps, inner=4) * 1e3 / copies
+    y0.free()
+    e = {"op": "MATMUL q8 960x576 (fused QKV rows as one weight), f32 activations, T=1", "gpu_us": us,
+         "cpu": cpu_op_baseline({"weights": w0[:1], "kind": "matmul", "act": "f32"}, 1) if cpu else None}
+    out["configs[0] q8 GEMV 960x576 f32-act"] = pair_rates(e, nbytes=q_bytes(1, 960, 576) + 576 * 4 + 960 * 4,
+                                                         ceil=ceil)
+    for d in d0:
+        d.free()
+    cpu_us = " / ".join("%.1f" % v["us"] for v in e["cpu"].values()) if e["cpu"] else ""
+    log(f"  configs[0] q8 GEMV f32-act 960x576: GPU {us:.2f} us" + (f", CPU 1/4/16 threads {cpu_us} us" if cpu_us else ""))
+
+    # configs[1] (GPU per-op times from the decode chain, 30 distinct layers)
+    sm = {"MATMUL_N qkv": ([(D, D), (KV, D), (KV, D)], "matmul", False), "FFN_SWIGLU": ([(HID, D), (HID, D)], "swiglu", False),
+          "MATMUL_ADD down": ([(D, HID)], "matmul", True), "MATMUL lm_head q8": ([(VOCAB, D)], "matmul", False)}
+    if per_decode:
+        for name, (shapes, kind, resid) in sm.items():
+            dt = 1 if "lm_head" in name else 2
+            ws = [HostWeight(800 + i, n, k, dt) for i, (n, k) in enumerate(shapes)]
+            p = per_decode[name]
+            e = {"op": f"{name} W4A8 T=1" if dt == 2 else f"{name} W8A8 T=1", "gpu_us": p["us"],
+                 "cpu": cpu_op_baseline({"weights": ws, "kind": kind, "act": "int8", "residual": resid}, 1)
+                 if cpu else None}
+            out[f"configs[1] {name}"] = pair_rates(e, nbytes=p["bytes"], ceil=ceil)
+
+    def fused_op(T, K, shapes, kind, resid, dws):
+        """The op's call and its int ops; every output buffer (and the residual) at exactly its size."""
+        outs = [ctx.buffer(T * n * 4) for n, _ in shapes[:1 if kind == "swiglu" else len(shapes)]]
+        rb = ctx.buffer(T * shapes[0][0] * 4) if resid else None
+        if rb:
+            rb.upload(np.random.default_rng(4).standard_normal(T * shapes[0][0], dtype=np.float32))
+        if kind == "swiglu":
+            fn = lambda: ctx.swiglu_dev(bx.ptr, T, K, dws[0], dws[1], outs[0].ptr, act=E.ACT_INT8)
+            ops = 2 * T * K * shapes[0][0] * 2
+        else:
+            fn = lambda: ctx.matmul_dev(bx.ptr, T, K, dws, [o.ptr for o in outs], [rb.ptr] if rb else None,
+                                        act=E.ACT_INT8)
+            ops = 2 * T * K * sum(n for n, _ in shapes)
+        assert T * K * 4 <= bx.nbytes
+        return fn, ops, outs + ([rb] if rb else [])
+
+    # configs[2]: W8A8 (edgelm's per-block mode), T = 32 / 128 / 512, epilogues fused
+    for T in (32, 128, 512):
+        for name, (shapes, kind, resid) in sm.items():
+            ws = [HostWeight(900 + i, n, k, 1) for i, (n, k) in enumerate(shapes)]
+            dws = [ctx.upload(1, w.rows, w.cols, w.data, w.scales) for w in ws]
+            fn, ops, bufs = fused_op(T, shapes[0][1], shapes, kind, resid, dws)
+            log(f"  configs[2] {name} T={T} on the GPU")
+            us = gpu_time(fn, T, 16 if T < 512 else 4)
+            e = {"op": f"{name} W8A8 (per-32-block activation scales) T={T}", "gpu_us": us,
+                 "cpu": cpu_op_baseline({"weights": ws, "kind": kind, "act": "int8", "residual": resid}, T)
+                 if cpu else None}
+            out[f"configs[2] {name} T={T}"] = pair_rates(e, ops=ops)
+            for d in dws + bufs:
+                d.free()
+        log(f"  configs[2] T={T}: " + ", ".join(f"{n} {out[f'configs[2] {n} T={T}']['gpu_us']:.1f} us" for n in sm))
+
+    # configs[4]: 8B W4A8 at T = 1 (GPU per-op times from the sweep) and T = 512
+    b8 = {"MATMUL_N qkv 6144x4096": ([(4096, 4096), (1024, 4096), (1024, 4096)], "matmul"),
+          "FFN_SWIGLU 2x14336x4096": ([(14336, 4096), (14336, 4096)], "swiglu"),
+          "MATMUL down 4096x14336": ([(4096, 14336)], "matmul")}
+    for name, (shapes, kind) in b8.items():
+        ws = [HostWeight(950 + i, n, k, 2) for i, (n, k) in enumerate(shapes)]
+        if per_8b:
+            p = per_8b[name]
+            e = {"op": f"{name} W4A8 T=1 (8 distinct layers round-robin on the GPU)", "gpu_us": p["us"],
+                 "cpu": cpu_op_baseline({"weights": ws, "kind": kind, "act": "int8"}, 1) if cpu else None}
+            out[f"configs[4] {name} T=1"] = pair_rates(e, nbytes=p["weight_bytes"], ceil=ceil)
+        dws = [ctx.upload(2, w.rows, w.cols, w.data, w.scales) for w in ws]
+        T = 512
+        fn, ops, bufs = fused_op(T, shapes[0][1], shapes, kind, False, dws)
+        log(f"  configs[4] {name} T=512 on the GPU")
+        us = gpu_time(fn, T, 2)
+        e = {"op": f"{name} W4A8 (per-32-block activation scales) T=512", "gpu_us": us,
+             "cpu": cpu_op_baseline({"weights": ws, "kind": kind, "act": "int8"}, T) if cpu else None}
+        out[f"configs[4] {name} T=512"] = pair_rates(e, ops=ops)
+        log(f"  configs[4] {name} T=512: GPU {us:.1f} us")
+        for d in dws + bufs:
+            d.free()
+    bx.free()
+    return out
+
+
 E2E_SD, E2E_EMBED_SD = 0.05, 0.5  # weight scales of the e2e model: greedy tokens differ step to step
 
 
@@ -549,6 +747,8 @@ def main():
     ap.add_argument("--no-8b", action="store_true", help="skip the 8B-shaped sweep")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMMs")
     ap.add_argument("--no-chain", action="store_true", help="skip the decode matmul chain and its per-op timers")
+    ap.add_argument("--no-pairs", action="store_true",
+                    help="skip the per-config GPU / CPU pairs (configs[0], [1], [2], [4] beside edgelm's cpu backend)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the roofline kernels and a calibration copy (for rocprofv3 counter passes)")
     ap.add_argument("--pmc-gemm", action="store_true",
@@ -584,6 +784,8 @@ def main():
 
         ctx = E.Context(0)
         log(f"device {ctx.arch}")
+        ceil = measured_ceilings(ctx, E)
+        extra["measured_ceilings"] = ceil
         per = None
         if not args.no_chain:
             ms_chain, per = decode_step_bench(ctx, E, 200, 20, args.eager)
@@ -596,14 +798,18 @@ def main():
         if not args.no_gemm:
             sm = [(D + 2 * KV, D), (HID, D), (D, HID), (VOCAB, D)]
             b8 = [(4096, 4096), (14336, 4096), (4096, 14336)]
-            # W8A8, int8 per-channel weights, per-token int8 activations (ELMH_ACT_INT8_TOKEN)
+            # BASELINE configs[2] read literally: W8A8, int8 per-channel weights, one int8 scale per token
+            # (ELMH_ACT_INT8_TOKEN, an extension: edgelm's mode is per 32-block, timed in configs[2] below)
             extra["gemm_w8a8_token_T128"] = gemm_bench(ctx, E, 128, sm, act=E.ACT_INT8_TOKEN, eager=args.eager)
             extra["gemm_w8a8_token_T512_8b"] = gemm_bench(ctx, E, 512, b8, act=E.ACT_INT8_TOKEN, eager=args.eager)
             # edgelm's parity mode: per-32-block activation scales, block-order f32 rescale (VALU-bound)
-            extra["gemm_w8a8_T128"] = gemm_bench(ctx, E, 128, sm, eager=args.eager)
             extra["gemm_w8a8_T512_8b"] = gemm_bench(ctx, E, 512, b8, eager=args.eager)
             # W4A8 prefill (the e2e model's layers), parity mode
             extra["gemm_w4a8_T512_8b"] = gemm_bench(ctx, E, 512, b8, dt=2, eager=args.eager)
+        if not args.no_pairs:
+            log("per-config GPU / CPU pairs")
+            extra["config_pairs"] = config_pairs(ctx, E, per, extra.get("gemv_8b_w4a8", {}).get("per_op"), ceil,
+                                                 cpu=not args.no_cpu)
         ctx.close()
 
         roof = None
@@ -618,6 +824,10 @@ def main():
                     "bound": "hbm", "achieved": round(dom["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(dom["GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_name),
                     "algorithmic_bytes_per_launch": dom["bytes"], "avg_launch_us": round(dom["us"], 3),
+                    "peak_hbm_read_measured": round(ceil["hbm_read_GBs"], 1),
+                    "frac_hbm_read_measured": round(dom["GBs"] / ceil["hbm_read_GBs"], 4),
+                    "peak_infinity_cache_read_measured": round(ceil["infinity_cache_read_GBs"], 1),
+                    "frac_infinity_cache_read_measured": round(dom["GBs"] / ceil["infinity_cache_read_GBs"], 4),
                     "note": "SmolLM2-sized weights stay in L2 / Infinity Cache and each call is a few microseconds: "
                             "latency-bound; roofline_8b_down_gemv is the HBM-bound kernel (configs[4])"}
         if "gemv_8b_w4a8" in extra:
@@ -626,7 +836,10 @@ def main():
                 "kernel": "gemv_stream_kernel (8B down 4096x14336, W4A8, T=1)", "bound": "hbm",
                 "achieved": round(g8["down_gemv_GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(g8["down_gemv_GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic("8B down GEMV"),
-                "algorithmic_bytes_per_launch": g8["down_gemv_bytes"], "avg_launch_us": round(g8["down_gemv_us"], 3)}
+                "algorithmic_bytes_per_launch": g8["down_gemv_bytes"], "avg_launch_us": round(g8["down_gemv_us"], 3),
+                "peak_hbm_read_measured": round(ceil["hbm_read_GBs"], 1),
+                "frac_hbm_read_measured": round(g8["down_gemv_GBs"] / ceil["hbm_read_GBs"], 4),
+                "sweep_frac_hbm_read_measured": round(g8["GBs"] / ceil["hbm_read_GBs"], 4)}
         cpu = None
         if not args.no_cpu:
             cpu, cpu_extra = cpu_baseline(model_path, tokens, args.steps, args.warmup)

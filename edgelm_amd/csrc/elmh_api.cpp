@@ -54,6 +54,8 @@ struct elmh_ctx {
   DevBuf gu;
   // RMSNORM output when it cannot be fused into the matmul after it
   DevBuf nrm;
+  // attention score rows longer than LDS holds
+  DevBuf asc;
   // bumped whenever a scratch buffer above moves (a graph captured before then holds stale addresses)
   uint64_t scratch_gen = 0;
   // this device's copy of the no-allocation scratch array
@@ -596,8 +598,16 @@ int check_attention(elmh_ctx* c, const float* q, const float* k, const float* v,
   if (n_heads < 1 || n_kv < 1 || n_heads % n_kv || head_dim < 4 || head_dim % 4 || head_dim > 256)
     return fail(c, ELMH_ERR_ARG, "attention: heads %d / kv heads %d / head_dim %d", n_heads, n_kv, head_dim);
   if (!rope_cos != !rope_sin) return fail(c, ELMH_ERR_ARG, "attention: rope_cos and rope_sin go together");
-  if (attention_lds_bytes(head_dim, pos0 + T) > kMaxAttnLds)
-    return fail(c, ELMH_ERR_UNSUPPORTED, "attention: %d positions exceed the kernel's LDS", pos0 + T);
+  return ELMH_OK;
+}
+
+// The global score rows of an attention call whose rows do not fit LDS (null when they do).
+int attention_scores(elmh_ctx* c, int T, int pos0, bool pos_dev, int n_heads, int head_dim, int max_ctx, float** out) {
+  const size_t bytes = attention_global_score_bytes(T, pos0, pos_dev, n_heads, head_dim, max_ctx);
+  *out = nullptr;
+  if (!bytes) return ELMH_OK;
+  if (const int rc = ensure(c, c->asc, bytes)) return rc;
+  *out = static_cast<float*>(c->asc.p);
   return ELMH_OK;
 }
 
@@ -663,7 +673,7 @@ void elmh_destroy(elmh_ctx* c) {
   if (!c) return;
   DeviceGuard g(c);
   (void)hipStreamSynchronize(c->stream);
-  for (DevBuf* b : {&c->x, &c->y, &c->res, &c->xq, &c->xd, &c->xs, &c->gu, &c->nrm})
+  for (DevBuf* b : {&c->x, &c->y, &c->res, &c->xq, &c->xd, &c->xs, &c->gu, &c->nrm, &c->asc})
     if (b->p) (void)hipFree(b->p);
   if (c->argmax_scratch) (void)hipFree(c->argmax_scratch);
   (void)hipStreamDestroy(c->stream);
@@ -1065,6 +1075,18 @@ int elmh_memset_dev(elmh_ctx* c, void* dst, int value, size_t bytes) {
   return ELMH_OK;
 }
 
+size_t elmh_read_sweep_sink_bytes(void) { return read_sweep_sink_bytes(); }
+
+int elmh_read_sweep_dev(elmh_ctx* c, const void* src, size_t bytes, void* sink) {
+  if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
+  if (!src || !sink) return fail(c, ELMH_ERR_ARG, "null src/sink");
+  if (bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16)
+    return fail(c, ELMH_ERR_ARG, "read sweep: src and bytes must be 16-byte aligned (bytes=%zu)", bytes);
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, launch_read_sweep(src, bytes, sink, c->stream));
+  return ELMH_OK;
+}
+
 int elmh_memcpy_d2d(elmh_ctx* c, void* dst, const void* src, size_t bytes) {
   if (!c) return fail(c, ELMH_ERR_ARG, "null ctx");
   if (bytes && (!dst || !src)) return fail(c, ELMH_ERR_ARG, "null dst/src");
@@ -1140,8 +1162,10 @@ int elmh_attention_matmul_dev(elmh_ctx* c, const float* q, const float* k, const
   }
   bool quantized = false;
   c->attn_fused = 0;
+  float* gsc = nullptr;
+  if ((rc = attention_scores(c, T, pos0, false, n_heads, head_dim, max_ctx, &gsc))) return rc;
   HIP_OR_FAIL(c, launch_attention(q, k, v, out, T, pos0, nullptr, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx,
-                                  rope_cos, rope_sin, c->stream, xq, xd, Tpad, &quantized));
+                                  rope_cos, rope_sin, c->stream, xq, xd, Tpad, &quantized, gsc));
   c->attn_fused = quantized ? 1 : 0;
   if (!quantized) return run_matmul(c, out, T, K, 1, ws, ys, res ? rs : nullptr, act, mode);
   for (const auto& grp : by_dtype(1, ws))
@@ -1158,14 +1182,15 @@ int elmh_attention_dev(elmh_ctx* c, const float* q, const float* k, const float*
                                  rope_cos, rope_sin);
   if (rc) return rc;
   DeviceGuard g(c);
+  float* gsc = nullptr;
+  if (const int r2 = attention_scores(c, T, pos0, false, n_heads, head_dim, max_ctx, &gsc)) return r2;
   HIP_OR_FAIL(c, launch_attention(q, k, v, out, T, pos0, nullptr, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx,
-                                  rope_cos, rope_sin, c->stream));
+                                  rope_cos, rope_sin, c->stream, nullptr, nullptr, 0, nullptr, gsc));
   return ELMH_OK;
 }
 
 int elmh_attention_step_supported(int head_dim, int max_ctx) {
-  return head_dim >= 4 && head_dim % 4 == 0 && head_dim <= 256 && max_ctx >= 1 &&
-         attention_lds_bytes(head_dim, max_ctx) <= kMaxAttnLds;
+  return head_dim >= 4 && head_dim % 4 == 0 && head_dim <= 256 && max_ctx >= 1;
 }
 
 int elmh_attention_step_dev(elmh_ctx* c, const float* q, const float* k, const float* v, float* out,
@@ -1177,11 +1202,11 @@ int elmh_attention_step_dev(elmh_ctx* c, const float* q, const float* k, const f
     return fail(c, ELMH_ERR_ARG, "attention_step: heads %d / kv heads %d / head_dim %d / max_ctx %d", n_heads, n_kv,
                 head_dim, max_ctx);
   if (!rope_cos != !rope_sin) return fail(c, ELMH_ERR_ARG, "attention_step: rope_cos and rope_sin go together");
-  if (!elmh_attention_step_supported(head_dim, max_ctx))
-    return fail(c, ELMH_ERR_UNSUPPORTED, "attention_step: max_ctx %d exceeds the kernel's LDS", max_ctx);
   DeviceGuard g(c);
+  float* gsc = nullptr;
+  if (const int rc = attention_scores(c, 1, 0, true, n_heads, head_dim, max_ctx, &gsc)) return rc;
   HIP_OR_FAIL(c, launch_attention(q, k, v, out, 1, 0, pos_dev, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx,
-                                  rope_cos, rope_sin, c->stream));
+                                  rope_cos, rope_sin, c->stream, nullptr, nullptr, 0, nullptr, gsc));
   return ELMH_OK;
 }
 

@@ -151,18 +151,27 @@ constexpr size_t kMaxLds = 160 * 1024;
 // dynamic LDS the attention kernels may take (their static LDS is a few words; this leaves 1 KB for it)
 constexpr size_t kMaxAttnLds = kMaxLds - 1024;
 size_t attention_lds_bytes(int hd, int n_max);
+// Bytes of global score rows launch_attention needs for this call (0: the rows fit LDS). pos_dev: the
+// position comes from device memory (rows sized for max_ctx).
+size_t attention_global_score_bytes(int T, int pos0, bool pos_dev, int n_heads, int hd, int max_ctx);
 // pos_dev (if not null): pos0 read from device memory (T must be 1; LDS sized for max_ctx).
 // xq, xd, Tpad, quantized (all given): where the chunk kernel (T > 1, head size 64) runs, it also
 // writes its output as the block-scale GEMM's activation fragments (xq, Tpad * n_heads * hd bytes)
 // and scales (xd, 2 * n_heads * Tpad floats; tokens T .. Tpad-1 left as they were) and sets
 // *quantized; otherwise *quantized is false and xq, xd are untouched.
+// gscores: attention_global_score_bytes() of device memory where that is not 0 (score rows longer than
+// LDS holds); without it such a call fails with hipErrorInvalidValue.
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
                             const int* pos_dev, int n_heads, int n_kv, int hd, float* kc, float* vc, int max_ctx,
                             const float* rcos, const float* rsin, hipStream_t s, int8_t* xq = nullptr,
-                            float* xd = nullptr, int Tpad = 0, bool* quantized = nullptr);
+                            float* xd = nullptr, int Tpad = 0, bool* quantized = nullptr, float* gscores = nullptr);
 hipError_t launch_embed(const int32_t* tok, int T, const DevWeight& w, float* y, hipStream_t s);
 // dst[0, bytes) = value (a kernel: capturable in a HIP graph, unlike hipMemsetAsync)
 hipError_t launch_fill(void* dst, int value, size_t bytes, hipStream_t s);
+// measurement: every 16-byte word of src[0, bytes) read once (bytes and src 16-byte aligned), folded
+// into sink (read_sweep_sink_bytes())
+size_t read_sweep_sink_bytes();
+hipError_t launch_read_sweep(const void* src, size_t bytes, void* sink, hipStream_t s);
 hipError_t launch_argmax(const float* x, int rows, int64_t n, int32_t* out, hipStream_t s);
 // one row's argmax over several workgroups (n <= 64 * 4096); with pos: ring[*pos & ring_mask] =
 // the index, then *pos + 1. scratch: argmax_parts_scratch_bytes(), its last word zero before the

@@ -165,6 +165,10 @@ __global__ __launch_bounds__(64) void kv_append_kernel(const float* __restrict__
 // for the later ones. Score slots past the last position hold +0.0 and product rows past it are
 // zero: adding them changes no sum (these sums start at +0.0 and are never -0.0).
 // LDS (dynamic): q [hd], scores [n_cap rounded up to 64], one product chunk [cpos][hd].
+// GS (global scores): for score rows longer than LDS holds, the row lives in gsc (one row of n_cap
+// rounded up to 64 floats per workgroup) and LDS keeps q and the product chunk only; the in-order sum
+// of the exponentials then passes them through the product region a chunk at a time. Same float
+// operations in the same order.
 constexpr int kAttnThreads = 256;
 constexpr int kAttnVF = 20;                           // float4 of values per thread per chunk
 constexpr int kAttnChunkF4 = kAttnThreads * kAttnVF;  // 80 KB: 320 positions of head size 64
@@ -189,8 +193,8 @@ __device__ __forceinline__ float dot_row(const float* __restrict__ q, const floa
   return dot4(q, k, hd);
 }
 
-// HD: the head size when it is known at compile time (64), else 0 (hd_arg)
-template <int HD>
+// HD: the head size when it is known at compile time (64), else 0 (hd_arg). GS: scores in gsc.
+template <int HD, bool GS>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ q, float* __restrict__ out,
                                                                  float* __restrict__ kc, float* __restrict__ vc, int pos0,
                                                                  const int* __restrict__ pos_dev, int n_heads, int n_kv,
@@ -198,14 +202,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
                                                                  const float* __restrict__ rcos,
                                                                  const float* __restrict__ rsin,
                                                                  const float* __restrict__ knew,
-                                                                 const float* __restrict__ vnew) {
+                                                                 const float* __restrict__ vnew,
+                                                                 float* __restrict__ gsc) {
   const int hd = HD ? HD : hd_arg;
   extern __shared__ float lds[];
   if (pos_dev) pos0 = min(max(*pos_dev, 0), max_ctx - 1);  // the caller keeps it in range; stay in bounds anyway
   const int hdp = (hd + 3) & ~3;
+  const int row = (n_cap + 63) & ~63;  // score slots
   float* qb = lds;
-  float* sc = lds + hdp;
-  float* vt = sc + ((n_cap + 63) & ~63);
+  float* sc = GS ? gsc + (int64_t)blockIdx.x * row : lds + hdp;
+  float* vt = GS ? lds + hdp : sc + row;
   float* kn = vt + attn_chunk_pos(hd) * hd;  // fused append: this step's rotated key
   __shared__ float red[kAttnThreads / 64];
   __shared__ float inv_s;
@@ -331,10 +337,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
   const int n64 = (n + 63) & ~63;
   for (int j = tid; j < n64; j += kAttnThreads) sc[j] = j < n ? elm_expf(sc[j] - mx) : 0.f;
   __syncthreads();
-  if (tid == 0) {  // e_0 + e_1 + ... in order, 64 values read before their adds
-    float sum = 0.f;
-    const float4* s4 = reinterpret_cast<const float4*>(sc);
-    for (int j0 = 0; j0 < n; j0 += 64) {
+  // e_0 + e_1 + ... in order by thread 0, 64 values read from LDS before their adds
+  auto add_in_order = [](float sum, const float* e_lds, int count) {
+    const float4* s4 = reinterpret_cast<const float4*>(e_lds);
+    for (int j0 = 0; j0 < count; j0 += 64) {
       float4 e[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) e[u] = s4[(j0 >> 2) + u];
@@ -346,7 +352,23 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
         sum = sum + e[u].w;
       }
     }
-    inv_s = 1.0f / sum;
+    return sum;
+  };
+  if (GS) {
+    // the row passes through the product region (a multiple of 64 floats) a chunk at a time
+    const int ch = attn_chunk_pos(hd) * hd;
+    float sum = 0.f;
+    for (int c0 = 0; c0 < n; c0 += ch) {
+      const int m = min(ch, n64 - c0);
+      for (int i = 4 * tid; i < m; i += 4 * kAttnThreads)
+        *reinterpret_cast<float4*>(vt + i) = *reinterpret_cast<const float4*>(sc + c0 + i);
+      __syncthreads();
+      if (tid == 0) sum = add_in_order(sum, vt, min(ch, n - c0));
+      __syncthreads();
+    }
+    if (tid == 0) inv_s = 1.0f / sum;
+  } else if (tid == 0) {
+    inv_s = 1.0f / add_in_order(0.f, sc, n);
   }
   __syncthreads();
   const float inv = inv_s;
@@ -1095,6 +1117,33 @@ __global__ __launch_bounds__(256) void fill_kernel(uint8_t* __restrict__ dst, si
   if (i0 < bytes - tail) dst[tail + i0] = (uint8_t)v4;
 }
 
+// ---------------------------------------------------------------- read-bandwidth ceiling
+
+// Reads every 16-byte word of src[0, n16) once (grid-stride, kReadSweepUnroll loads in flight per
+// thread) and folds them by XOR; each wave stores its fold to sink[block * 4 + wave], so no load
+// can be dropped. A measured ceiling for the GEMVs' read streams.
+constexpr int kReadSweepBlocks = 2048, kReadSweepUnroll = 8;
+__global__ __launch_bounds__(256) void read_sweep_kernel(const uint4* __restrict__ src, size_t n16,
+                                                         uint32_t* __restrict__ sink) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  size_t i = blockIdx.x * (size_t)256 + threadIdx.x;
+  uint32_t acc = 0;
+  for (; i + (kReadSweepUnroll - 1) * stride < n16; i += kReadSweepUnroll * stride) {
+    uint4 v[kReadSweepUnroll];
+#pragma unroll
+    for (int u = 0; u < kReadSweepUnroll; ++u) v[u] = src[i + u * stride];
+#pragma unroll
+    for (int u = 0; u < kReadSweepUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (; i < n16; i += stride) {
+    const uint4 v = src[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, off, 64);
+  if ((threadIdx.x & 63) == 0) sink[blockIdx.x * 4 + (threadIdx.x >> 6)] = acc;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- greedy sampling
@@ -1302,6 +1351,15 @@ hipError_t launch_fill(void* dst, int value, size_t bytes, hipStream_t s) {
   return hipGetLastError();
 }
 
+size_t read_sweep_sink_bytes() { return (size_t)kReadSweepBlocks * 4 * sizeof(uint32_t); }
+
+hipError_t launch_read_sweep(const void* src, size_t bytes, void* sink, hipStream_t s) {
+  if (bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16) return hipErrorInvalidValue;
+  read_sweep_kernel<<<kReadSweepBlocks, 256, 0, s>>>(static_cast<const uint4*>(src), bytes / 16,
+                                                     static_cast<uint32_t*>(sink));
+  return hipGetLastError();
+}
+
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int dim, float eps, hipStream_t s) {
   if (dim < 1 || dim > 256 * 4 * kNormVF) return hipErrorInvalidValue;
   const size_t rowlen = ((size_t)(dim >> 2) + 31) & ~(size_t)31;
@@ -1319,9 +1377,21 @@ size_t attention_lds_bytes(int hd, int n_max) {
   return (2 * hdp + (size_t)((n_max + 63) & ~63) + (size_t)attn_chunk_pos(hd) * hd) * sizeof(float);
 }
 
+// attention_kernel with its score rows in global memory (GS): LDS holds q, the fused key and a chunk
+static size_t attention_gs_lds_bytes(int hd) {
+  return (2 * (size_t)((hd + 3) & ~3) + (size_t)attn_chunk_pos(hd) * hd) * sizeof(float);
+}
+
+size_t attention_global_score_bytes(int T, int pos0, bool pos_dev, int n_heads, int hd, int max_ctx) {
+  const int n_cap = pos_dev ? max_ctx : pos0 + T;
+  if (attention_lds_bytes(hd, n_cap) <= kMaxAttnLds) return 0;
+  return (size_t)T * n_heads * (size_t)((n_cap + 63) & ~63) * sizeof(float);
+}
+
 // the attention kernels keep a whole score row (and a chunk of values) in LDS: allow them up to kMaxAttnLds
 bool raise_lds_limit() {
-  const void* kernels[] = {(const void*)attention_kernel<64>, (const void*)attention_kernel<0>,
+  const void* kernels[] = {(const void*)attention_kernel<64, false>, (const void*)attention_kernel<0, false>,
+                           (const void*)attention_kernel<64, true>, (const void*)attention_kernel<0, true>,
                            (const void*)attention_prefill_kernel, (const void*)attention_decode64_kernel,
                            (const void*)attention_prefill64_kernel};
   for (const void* k : kernels) {
@@ -1335,7 +1405,7 @@ bool raise_lds_limit() {
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
                             const int* pos_dev, int n_heads, int n_kv, int hd, float* kc, float* vc, int max_ctx,
                             const float* rcos, const float* rsin, hipStream_t s, int8_t* xq, float* xd, int Tpad,
-                            bool* quantized) {
+                            bool* quantized, float* gscores) {
   if (quantized) *quantized = false;
   // with the position in device memory the score buffer covers the whole cache
   const int n_cap = pos_dev ? max_ctx : pos0 + T;  // score slots
@@ -1374,15 +1444,24 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
     if (e == hipSuccess && quant) *quantized = true;
     return e;
   }
+  const bool in_lds = attention_lds_bytes(hd, n_cap) <= kMaxAttnLds;
+  if (!in_lds && !gscores) return hipErrorInvalidValue;  // a score row past LDS needs the global rows
+  const size_t lds_gs = attention_gs_lds_bytes(hd), lds = attention_lds_bytes(hd, n_cap);
   if (fuse && hd == 64 && attention_decode_lds_bytes(n_cap) <= kMaxAttnLds)
     attention_decode64_kernel<<<n_heads, 256, attention_decode_lds_bytes(n_cap), s>>>(
         q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, max_ctx, n_cap, rcos, rsin, k, v);
+  else if (hd == 64 && in_lds)
+    attention_kernel<64, false><<<T * n_heads, kAttnThreads, lds, s>>>(
+        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin, kn, vn, nullptr);
   else if (hd == 64)
-    attention_kernel<64><<<T * n_heads, kAttnThreads, attention_lds_bytes(hd, n_cap), s>>>(
-        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin, kn, vn);
+    attention_kernel<64, true><<<T * n_heads, kAttnThreads, lds_gs, s>>>(
+        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin, kn, vn, gscores);
+  else if (in_lds)
+    attention_kernel<0, false><<<T * n_heads, kAttnThreads, lds, s>>>(
+        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin, kn, vn, nullptr);
   else
-    attention_kernel<0><<<T * n_heads, kAttnThreads, attention_lds_bytes(hd, n_cap), s>>>(
-        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin, kn, vn);
+    attention_kernel<0, true><<<T * n_heads, kAttnThreads, lds_gs, s>>>(
+        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin, kn, vn, gscores);
   return hipGetLastError();
 }
 

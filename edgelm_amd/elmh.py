@@ -312,6 +312,15 @@ class Context:
     def memset_dev(self, dst_ptr, value, nbytes):
         self._check(lib().elmh_memset_dev(self.h, C.c_void_p(dst_ptr), C.c_int(value), C.c_size_t(nbytes)))
 
+    def read_sweep_dev(self, src_ptr, nbytes, sink_ptr):
+        """elmh_read_sweep_dev: every 16-byte word of src read once (a read-bandwidth ceiling)."""
+        self._check(lib().elmh_read_sweep_dev(self.h, C.c_void_p(src_ptr), C.c_size_t(nbytes), C.c_void_p(sink_ptr)))
+
+    @staticmethod
+    def read_sweep_sink_bytes():
+        lib().elmh_read_sweep_sink_bytes.restype = C.c_size_t
+        return int(lib().elmh_read_sweep_sink_bytes())
+
     def buffer(self, nbytes):
         return DevBuffer(self, nbytes)
 

@@ -196,10 +196,12 @@ int elmh_attention_step_dev(elmh_ctx* ctx, const float* q, const float* k, const
                             const int32_t* pos_dev, int n_heads, int n_kv, int head_dim, float* k_cache, float* v_cache,
                             int max_ctx, const float* rope_cos, const float* rope_sin);
 
-/* 1 if elmh_attention_step_dev runs this head size with a cache of max_ctx positions, else 0 (its score
- * row spans the whole cache: about 20K positions at head size 64). elmh_attention_dev takes up to the
- * same number of positions in use. No counterpart in edgelm (whose attention has no such limit); a
- * caller that replays graphs runs longer contexts step by step with elmh_attention_dev. */
+/* 1 if elmh_attention_step_dev runs this head size with a cache of max_ctx positions, else 0. Every
+ * context length runs, as in edgelm's attention: score rows longer than a workgroup's LDS holds (about
+ * 20K positions at head size 64) live in a device buffer the context allocates on the first such call
+ * (T * n_heads rows of the positions in use, or of max_ctx for elmh_attention_step_dev), with the same
+ * float operations in the same order; a graph captured before that buffer grows must be captured again
+ * (elmh_scratch_generation). No counterpart in edgelm. */
 int elmh_attention_step_supported(int head_dim, int max_ctx);
 
 /* Greedy sampling: argmax (tokenizer.cpp:187-189, std::max_element) of each row of x [rows, n]
@@ -245,6 +247,13 @@ int elmh_memset_dev(elmh_ctx* ctx, void* dst, int value, size_t bytes);
 int elmh_memcpy_d2d(elmh_ctx* ctx, void* dst, const void* src, size_t bytes);
 int elmh_synchronize(elmh_ctx* ctx);
 void* elmh_stream(elmh_ctx* ctx); /* the context's hipStream_t */
+/* Measurement hook, no counterpart in edgelm: reads every 16-byte word of src[0, bytes) once (src and
+ * bytes 16-byte aligned) and folds them into sink (elmh_read_sweep_sink_bytes() of device memory),
+ * asynchronously on the context stream. Timed over a buffer far larger than the 256 MB Infinity
+ * Cache it is the read ceiling of HBM; repeated over a buffer that stays in that cache (larger than
+ * the L2s), the cache's; the benchmark reports the GEMVs against both. */
+size_t elmh_read_sweep_sink_bytes(void);
+int elmh_read_sweep_dev(elmh_ctx* ctx, const void* src, size_t bytes, void* sink);
 /* Events on the context stream: record, then elapsed milliseconds between two records. */
 int elmh_event_create(elmh_ctx* ctx, void** ev);
 int elmh_event_destroy(elmh_ctx* ctx, void* ev);

@@ -434,6 +434,33 @@ def rq_cpu_swiglu(pool, x, wg, wu, act_quant=False, out=None):
     return y
 
 
+def rq_time_cpu_op(threads, x, weights, residuals=None, act_quant=True, swiglu=False, warm=1, min_reps=3,
+                   max_reps=200, budget_s=0.3):
+    """edgelm's cpu::matmul over `weights` (MATMUL / MATMUL_N / MATMUL_ADD), or cpu::swiglu of weights[0]
+    (gate) and weights[1] (up), on edgelm's ThreadPool of `threads`, timed in C (eref_time_cpu_op): `warm`
+    untimed calls, then calls for `budget_s` seconds (min_reps .. max_reps); (median ms per call, calls)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    n = len(weights)
+    dt = (C.c_int * n)(*[w.dtype for w in weights])
+    rows = (C.c_int64 * n)(*[w.rows for w in weights])
+    data = (C.c_void_p * n)(*[w.data.ctypes.data for w in weights])
+    sc = (C.c_void_p * n)(*[None if w.scales is None else w.scales.ctypes.data for w in weights])
+    ys = [np.empty((T, w.rows), np.float32) for w in weights]
+    yp = (C.c_void_p * n)(*[y.ctypes.data for y in ys])
+    rp = None
+    if residuals is not None:
+        rp = (C.c_void_p * n)(*[None if r is None else r.ctypes.data for r in residuals])
+    med, reps = C.c_double(), C.c_int()
+    rc = ref().eref_time_cpu_op(C.c_int(1 if swiglu else 0), C.c_int(threads), _ptr(x), C.c_int(T), C.c_int(n), dt,
+                                rows, _I64(weights[0].cols), data, sc, yp, rp, C.c_int(int(act_quant)), C.c_int(warm),
+                                C.c_int(min_reps), C.c_int(max_reps), C.c_double(budget_s), C.byref(med),
+                                C.byref(reps))
+    if rc:
+        raise RuntimeError(ref().eref_last_error().decode())
+    return med.value, reps.value
+
+
 class RefSession:
     """edgelm's own Session over an .elm file (loader, fusion passes, partitioner, backends)."""
 

@@ -2,6 +2,7 @@
 // reference sources by oracle/Makefile into oracle/_ref/libedgelm_ref.so). Used to pin the C
 // oracle, to generate fixtures, and as bench.py's cpu_baseline ("kind": "reference"). The
 // product never links or loads it.
+#include <algorithm>
 #include <chrono>
 #include <cstring>
 #include <memory>
@@ -335,3 +336,47 @@ void eref_cpu_attention_pool(const float* q, const float* k, const float* v, flo
   cpu::attention(a, &pool, ptrs.data());
 }
 }  // extern "C"
+
+// ---- CPU baseline of the matmul family: edgelm's cpu::matmul / cpu::swiglu (kernels_cpu.cpp:339-411) on its
+// own ThreadPool (thread_pool.cpp:31-63, dynamic chunking), timed here in C as edgelm's bench times a
+// step (main.cpp:199-217): `warm` untimed calls, then calls until `budget_s` seconds have passed (at least
+// `min_reps`, at most `max_reps`); the median call time goes to *median_ms, the count to *reps.
+// op 0: MATMUL / MATMUL_N / MATMUL_ADD over n targets (residual may be null); op 1: FFN_SWIGLU of targets
+// 0 (gate) and 1 (up) into y[0].
+extern "C" int eref_time_cpu_op(int op, int threads, const float* x, int T, int n, const int* dtypes,
+                                const int64_t* rows, int64_t cols, const void* const* data,
+                                const float* const* scales, float* const* y, const float* const* residual,
+                                int act_quant, int warm, int min_reps, int max_reps, double budget_s,
+                                double* median_ms, int* reps) {
+  try {
+    Pool p(threads, T, cols);
+    std::vector<Tensor> ts;
+    for (int i = 0; i < n; ++i) ts.push_back(make_tensor(dtypes[i], rows[i], cols, data[i], scales[i]));
+    std::vector<MatmulTarget> tg;
+    for (int i = 0; i < n; ++i) tg.push_back({&ts[i], y[i], residual ? residual[i] : nullptr});
+    std::vector<int8_t> q(static_cast<size_t>(T) * cols);
+    std::vector<float> d(static_cast<size_t>(T) * (cols / kActBlock + 1));
+    ActBuf aq{q.data(), d.data()};
+    const ActBuf* a = act_quant ? &aq : nullptr;
+    auto call = [&] {
+      if (op == 1) cpu::swiglu(x, T, ts[0], ts[1], y[0], &p.pool, p.ptrs.data(), a);
+      else cpu::matmul(x, T, tg, &p.pool, p.ptrs.data(), a);
+    };
+    for (int i = 0; i < warm; ++i) call();
+    std::vector<double> ms;
+    const auto t_end = std::chrono::steady_clock::now() + std::chrono::duration<double>(budget_s);
+    while (static_cast<int>(ms.size()) < max_reps &&
+           (static_cast<int>(ms.size()) < min_reps || std::chrono::steady_clock::now() < t_end)) {
+      const auto t0 = std::chrono::steady_clock::now();
+      call();
+      ms.push_back(std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count());
+    }
+    std::sort(ms.begin(), ms.end());
+    *median_ms = ms[ms.size() / 2];
+    *reps = static_cast<int>(ms.size());
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return 1;
+  }
+}

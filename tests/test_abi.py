@@ -53,10 +53,10 @@ def test_hip_backend_compiles_against_edgelm_headers():
     assert p.returncode == 0, p.stderr
 
 
-def test_attention_step_limit_is_a_pure_query():
-    """elmh_attention_step_supported needs no device: the step kernel's whole-cache score row fits gfx950's LDS
-    up to about 20K positions at head size 64."""
+def test_attention_step_support_is_a_pure_query():
+    """elmh_attention_step_supported needs no device: every cache length runs (score rows past LDS live in a
+    device buffer); only head sizes the kernels do not take and empty caches are refused."""
     from edgelm_amd import elmh as E
     f = E.lib().elmh_attention_step_supported
-    assert f(64, 2048) == 1 and f(64, 16384) == 1 and f(64, 20000) == 1
-    assert f(64, 40000) == 0 and f(62, 128) == 0 and f(64, 0) == 0
+    assert f(64, 2048) == 1 and f(64, 16384) == 1 and f(64, 20000) == 1 and f(64, 40000) == 1 and f(64, 1 << 20) == 1
+    assert f(62, 128) == 0 and f(64, 0) == 0 and f(260, 128) == 0

@@ -75,6 +75,54 @@ def test_attention_bit_exact(ctx, shape, rope):
         b.free()
 
 
+# (n_heads, n_kv, head_dim, max_ctx, cached positions): score rows past what LDS holds (about 20K positions at
+# head size 64, fewer at 20), through the head-size-64 and the generic instantiation
+LONG_SHAPES = [(9, 3, 64, 33024, 32760), (6, 2, 20, 40000, 39950)]
+
+
+@pytest.mark.parametrize("shape", LONG_SHAPES, ids=[f"{s[0]}x{s[1]}x{s[2]}" for s in LONG_SHAPES])
+def test_attention_past_lds_score_rows(ctx, shape):
+    """Contexts longer than a workgroup's LDS can hold a score row of: a chunk of prompt tokens, a decode
+    step, and decode steps with the position read from device memory (the graph-replayed form, its rows
+    sized for the whole cache), each bit-identical to edgelm's cpu attention (the oracle), KV caches
+    included. The rows live in a device buffer; the in-order sum of the exponentials crosses chunk
+    boundaries of the LDS staging."""
+    nh, nkv, hd, mc, p0 = shape
+    r = np.random.default_rng(hd + mc)
+    tab = O.rope_table(hd, mc, 100000.0)
+    kc = r.normal(0, 1, (nkv, mc, hd)).astype(np.float32)
+    vc = r.normal(0, 1, (nkv, mc, hd)).astype(np.float32)
+    kc[:, p0:] = np.nan  # never read before the step that writes them
+    vc[:, p0:] = np.nan
+    bkc, bvc = dev(ctx, kc), dev(ctx, vc)
+    bcos, bsin = dev(ctx, tab[0]), dev(ctx, tab[1])
+    bpos = ctx.buffer(4)
+    pos = p0
+    for T, step in [(5, False), (1, False), (1, True), (1, True)]:
+        print(f"[gpu] attention past LDS {shape} pos0={pos} T={T} step={step}", flush=True)
+        q = r.normal(0, 1, (T, nh * hd)).astype(np.float32)
+        k = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+        v = r.normal(0, 1, (T, nkv * hd)).astype(np.float32)
+        bq, bk, bv, bo = dev(ctx, q), dev(ctx, k), dev(ctx, v), ctx.buffer(q.nbytes)
+        if step:
+            bpos.upload(np.array([pos], np.int32))
+            ctx.attention_step_dev(bq.ptr, bk.ptr, bv.ptr, bo.ptr, bpos.ptr, nh, nkv, hd, bkc.ptr, bvc.ptr, mc,
+                                   bcos.ptr, bsin.ptr)
+        else:
+            ctx.attention_dev(bq.ptr, bk.ptr, bv.ptr, bo.ptr, T, pos, nh, nkv, hd, bkc.ptr, bvc.ptr, mc, bcos.ptr,
+                              bsin.ptr)
+        want = O.attention(q, k, v, pos, nh, nkv, kc, vc, tab)
+        assert bits_equal(bo.download(q.shape, np.float32), want), f"pos0={pos} T={T}"
+        for b in (bq, bk, bv, bo):
+            b.free()
+        pos += T
+    assert bits_equal(bkc.download(kc.shape, np.float32), kc)
+    assert bits_equal(bvc.download(vc.shape, np.float32), vc)
+    assert E.lib().elmh_attention_step_supported(hd, mc) == 1
+    for b in (bkc, bvc, bcos, bsin, bpos):
+        b.free()
+
+
 @pytest.mark.parametrize("rope", [False, True])
 def test_attention_long_cache_decode_steps(ctx, rope):
     """Decode steps with the position read from device memory (the form a captured graph replays) over a
@@ -268,6 +316,30 @@ def test_fill_and_copy(ctx):
     assert np.array_equal(c.download((1031,), np.uint8), want)
     b.free()
     c.free()
+
+
+def test_read_sweep_reads_every_word(ctx):
+    """elmh_read_sweep_dev (the benchmark's read ceiling) folds every 16-byte word of its source by XOR, one
+    fold per wave: the XOR of all the folds is the XOR of all the source's 32-bit words, for sizes around
+    the kernel's unrolled-loop and grid boundaries; unaligned sizes are refused."""
+    nsink = E.Context.read_sweep_sink_bytes()
+    sink = ctx.buffer(nsink)
+    r = np.random.default_rng(11)
+    for n16 in (1, 255, 2048 * 256, 2048 * 256 * 8 - 1, 2048 * 256 * 8 + 17, 3 * 2048 * 256 * 8 + 5):
+        print(f"[gpu] read sweep {n16 * 16} bytes", flush=True)
+        words = r.integers(0, 2 ** 32, n16 * 4, dtype=np.uint32)
+        src = ctx.buffer(n16 * 16)
+        src.upload(words)
+        ctx.memset_dev(sink.ptr, 0, nsink)
+        ctx.read_sweep_dev(src.ptr, n16 * 16, sink.ptr)
+        folds = sink.download((nsink // 4,), np.uint32)
+        assert np.bitwise_xor.reduce(folds) == np.bitwise_xor.reduce(words)
+        src.free()
+    src = ctx.buffer(64)
+    with pytest.raises(E.ElmhError):
+        ctx.read_sweep_dev(src.ptr, 40, sink.ptr)
+    src.free()
+    sink.free()
 
 
 def test_argmax_step_feeds_the_next_step(ctx):
