@@ -362,6 +362,25 @@ def measured_ceilings(ctx, E, reps=10):
     return out
 
 
+def rescale_ceiling(ctx, E, iters=20000, cus=256):
+    """The per-32-block exact rescale's ceiling (SURVEY's per-block epilogue question), measured without memory
+    traffic by elmh_rescale_ceiling_dev: int8 MFMA blocks alone, then with the q8 and the q4 rescale of every
+    block's 32 x 32 int32 sums, at 1, 2 and 4 four-wave workgroups per CU (1, 2, 4 waves per SIMD); int ops /
+    time as a fraction of the int8 peak."""
+    out = {}
+    for wpc in (1, 2, 4):
+        blocks = cus * wpc
+        sink = ctx.buffer(blocks * 1024)
+        for mode, name in ((0, "mfma_only"), (1, "q8_exact_rescale"), (2, "q4_exact_rescale")):
+            ms = time_eager(ctx, lambda: ctx.rescale_ceiling_dev(mode, blocks, iters, sink.ptr, sink.nbytes), 5)
+            tops = blocks * 4 * iters * 2 * 65536 / (ms * 1e-3) / 1e12
+            out.setdefault(name, {})[f"{wpc}_workgroups_per_cu"] = {"TOPs": tops, "frac_int8_peak": tops / INT8_PEAK_TOPS}
+        sink.free()
+    log("rescale ceiling (fraction of int8 peak, 1 / 2 / 4 workgroups per CU): " + "; ".join(
+        f"{k} " + " / ".join("%.3f" % v["frac_int8_peak"] for v in d.values()) for k, d in out.items()))
+    return out
+
+
 def cpu_op_baseline(op, T, threads_list=(1, 4, 16), macs_per_thread=30e6, budget_s=0.3):
     """CPU-baseline leg for one op: edgelm's own cpu::matmul / cpu::swiglu (oracle/_ref, compiled from the
     reference sources; its ThreadPool, x86 scalar path) on the op's host weights and a seeded x, timed in C.
@@ -806,6 +825,8 @@ def main():
             extra["gemm_w8a8_T512_8b"] = gemm_bench(ctx, E, 512, b8, eager=args.eager)
             # W4A8 prefill (the e2e model's layers), parity mode
             extra["gemm_w4a8_T512_8b"] = gemm_bench(ctx, E, 512, b8, dt=2, eager=args.eager)
+        if not args.no_gemm:
+            extra["gemm_rescale_ceiling"] = rescale_ceiling(ctx, E)
         if not args.no_pairs:
             log("per-config GPU / CPU pairs")
             extra["config_pairs"] = config_pairs(ctx, E, per, extra.get("gemv_8b_w4a8", {}).get("per_op"), ceil,

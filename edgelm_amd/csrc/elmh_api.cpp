@@ -1075,6 +1075,17 @@ int elmh_memset_dev(elmh_ctx* c, void* dst, int value, size_t bytes) {
   return ELMH_OK;
 }
 
+int elmh_rescale_ceiling_dev(elmh_ctx* c, int mode, int blocks, int iters, float* sink, size_t sink_bytes) {
+  if (!c || !sink) return fail(c, ELMH_ERR_ARG, "null ctx/sink");
+  if (mode < 0 || mode > 2 || blocks < 1 || blocks > 65536 || iters < 1)
+    return fail(c, ELMH_ERR_ARG, "rescale ceiling: mode %d, %d workgroups, %d blocks", mode, blocks, iters);
+  if (sink_bytes < (size_t)blocks * 256 * sizeof(float))
+    return fail(c, ELMH_ERR_ARG, "rescale ceiling: sink of %zu bytes for %d workgroups", sink_bytes, blocks);
+  DeviceGuard g(c);
+  HIP_OR_FAIL(c, launch_rescale_ceiling(mode, blocks, iters, sink, c->stream));
+  return ELMH_OK;
+}
+
 size_t elmh_read_sweep_sink_bytes(void) { return read_sweep_sink_bytes(); }
 
 int elmh_read_sweep_dev(elmh_ctx* c, const void* src, size_t bytes, void* sink) {

@@ -179,6 +179,9 @@ hipError_t launch_argmax(const float* x, int rows, int64_t n, int32_t* out, hipS
 size_t argmax_parts_scratch_bytes();
 hipError_t launch_argmax_parts(const float* x, int64_t n, int32_t* out, int32_t* pos, int32_t* ring, int ring_mask,
                                void* scratch, hipStream_t s);
+// Measurement: `blocks` 256-thread workgroups of the rescale-ceiling kernel (mode 0 MFMA only, 1 q8 exact
+// rescale, 2 q4 exact rescale), `iters` blocks per wave; sink: blocks * 256 floats.
+hipError_t launch_rescale_ceiling(int mode, int blocks, int iters, float* sink, hipStream_t s);
 // Test hook: S[t][n][b] for pre-quantized row-major activations.
 hipError_t launch_block_sums(const DevWeight& w, const int8_t* xq, int T, int32_t* S, hipStream_t s);
 

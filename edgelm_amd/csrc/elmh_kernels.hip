@@ -2683,6 +2683,62 @@ hipError_t launch_silu_mul(const float* g, const float* u, float* y, int64_t n, 
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- rescale ceiling (measurement)
+
+// The per-32-block exact rescale's ceiling on the matrix and vector pipes alone, with no memory
+// traffic: each wave runs `iters` steps of two v_mfma_i32_32x32x32_i8 (one 32-deep block of two 32 x 32
+// output tiles, as a wave of the ring GEMM does per block; operands in registers, made opaque to the
+// compiler each step) and, by MODE, the rescale of the 2 x 16 int32 sums per lane that the per-block
+// GEMM does: 0 none (the sums accumulate in the MFMA: the per-token form), 1 q8
+// (acc = acc + float(S) * xd, multiply and add rounded separately), 2 q4 (acc = acc + float(S) * (c * xd),
+// c the block's weight scale, new every block). Each thread writes one value to sink so that nothing is
+// dropped.
+template <int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void rescale_ceiling_kernel(int iters,
+                                                                                           float* __restrict__ sink) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  v4i A = {lane, 3 * lane + 1, 5 * lane + 2, 7 * lane + 3};
+  v4i B0 = {lane ^ 5, lane + 9, 2 * lane + 7, lane * 11}, B1 = {lane + 1, lane ^ 3, 3 * lane, lane * 13};
+  v16i zero;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) zero[i] = 0;
+  float xv[16], f0[16], f1[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    xv[i] = 1.0f / (float)(lane + i + 1);
+    f0[i] = f1[i] = 0.f;
+  }
+  float c0 = 0.25f + 0.001f * (float)lane, c1 = 0.5f - 0.001f * (float)lane;
+  v16i acc0 = zero, acc1 = zero;
+  for (int k = 0; k < iters; ++k) {
+    asm volatile("" : "+v"(A), "+v"(B0), "+v"(B1));  // new operands every block, as far as the compiler knows
+    if (MODE == 0) {
+      acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B1, acc1, 0, 0, 0);
+    } else {
+      const v16i S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B0, zero, 0, 0, 0);
+      const v16i S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B1, zero, 0, 0, 0);
+      if (MODE == 2) asm volatile("" : "+v"(c0), "+v"(c1));  // the block's weight scales
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        f0[i] = f0[i] + (float)S0[i] * (MODE == 1 ? xv[i] : c0 * xv[i]);
+        f1[i] = f1[i] + (float)S1[i] * (MODE == 1 ? xv[i] : c1 * xv[i]);
+      }
+    }
+  }
+  float out = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) out = out + (MODE == 0 ? (float)(acc0[i] ^ acc1[i]) : f0[i] + f1[i]);
+  sink[(size_t)blockIdx.x * blockDim.x + tid] = out;
+}
+
+hipError_t launch_rescale_ceiling(int mode, int blocks, int iters, float* sink, hipStream_t s) {
+  if (mode == 0) rescale_ceiling_kernel<0><<<blocks, 256, 0, s>>>(iters, sink);
+  else if (mode == 1) rescale_ceiling_kernel<1><<<blocks, 256, 0, s>>>(iters, sink);
+  else rescale_ceiling_kernel<2><<<blocks, 256, 0, s>>>(iters, sink);
+  return hipGetLastError();
+}
+
 hipError_t launch_block_sums(const DevWeight& w, const int8_t* xq, int T, int32_t* S, hipStream_t s) {
   block_sums_kernel<<<grid_for((int64_t)T * w.rows * w.nb, 256), 256, 0, s>>>(w.data, w.dtype, w.rows, (int)w.nb, w.H,
                                                                               xq, T, S);

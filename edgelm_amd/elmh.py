@@ -316,6 +316,11 @@ class Context:
         """elmh_read_sweep_dev: every 16-byte word of src read once (a read-bandwidth ceiling)."""
         self._check(lib().elmh_read_sweep_dev(self.h, C.c_void_p(src_ptr), C.c_size_t(nbytes), C.c_void_p(sink_ptr)))
 
+    def rescale_ceiling_dev(self, mode, blocks, iters, sink_ptr, sink_bytes):
+        """elmh_rescale_ceiling_dev: MFMA blocks with the per-block rescale of mode 0 / 1 (q8) / 2 (q4)."""
+        self._check(lib().elmh_rescale_ceiling_dev(self.h, C.c_int(mode), C.c_int(blocks), C.c_int(iters),
+                                                   C.c_void_p(sink_ptr), C.c_size_t(sink_bytes)))
+
     @staticmethod
     def read_sweep_sink_bytes():
         lib().elmh_read_sweep_sink_bytes.restype = C.c_size_t

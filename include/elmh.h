@@ -254,6 +254,15 @@ void* elmh_stream(elmh_ctx* ctx); /* the context's hipStream_t */
  * the L2s), the cache's; the benchmark reports the GEMVs against both. */
 size_t elmh_read_sweep_sink_bytes(void);
 int elmh_read_sweep_dev(elmh_ctx* ctx, const void* src, size_t bytes, void* sink);
+/* Measurement hook, no counterpart in edgelm: the ceiling that edgelm's per-32-block activation scales
+ * (kernels_cpu.cpp:159-167, 193-204: one f32 rescale of every block's int32 sum, multiply and add rounded
+ * separately) put on an int8 MFMA GEMM, measured without memory traffic. `blocks` workgroups of four
+ * waves each run `iters` 32-deep blocks: two v_mfma_i32_32x32x32_i8 per block (two 32 x 32 output tiles,
+ * as a wave of the ring GEMM) and, by mode, no rescale (0: the sums accumulate in the MFMA, the per-token
+ * form), the q8 rescale (1) or the q4 rescale (2) of the block's sums. Each thread writes one float to
+ * sink (at least blocks * 1 KiB).
+ * Asynchronous on the context stream. */
+int elmh_rescale_ceiling_dev(elmh_ctx* ctx, int mode, int blocks, int iters, float* sink, size_t sink_bytes);
 /* Events on the context stream: record, then elapsed milliseconds between two records. */
 int elmh_event_create(elmh_ctx* ctx, void** ev);
 int elmh_event_destroy(elmh_ctx* ctx, void* ev);

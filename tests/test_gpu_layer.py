@@ -342,6 +342,24 @@ def test_read_sweep_reads_every_word(ctx):
     sink.free()
 
 
+def test_rescale_ceiling_runs_every_mode(ctx):
+    """elmh_rescale_ceiling_dev (the benchmark's per-block rescale ceiling) runs each mode to completion, writes
+    one finite value per thread, the same on a second run, and refuses a sink too small for its grid."""
+    blocks, iters = 8, 64
+    sink = ctx.buffer(blocks * 1024)
+    for mode in (0, 1, 2):
+        print(f"[gpu] rescale ceiling mode {mode}", flush=True)
+        runs = []
+        for _ in range(2):
+            ctx.memset_dev(sink.ptr, 0xFF, sink.nbytes)
+            ctx.rescale_ceiling_dev(mode, blocks, iters, sink.ptr, sink.nbytes)
+            runs.append(sink.download((blocks * 256,), np.float32))
+        assert np.all(np.isfinite(runs[0])) and np.array_equal(runs[0].view(np.int32), runs[1].view(np.int32))
+    with pytest.raises(E.ElmhError):
+        ctx.rescale_ceiling_dev(1, blocks + 1, iters, sink.ptr, sink.nbytes)
+    sink.free()
+
+
 def test_argmax_step_feeds_the_next_step(ctx):
     """elmh_argmax_step_dev: the argmax into the next step's token slot, into the ring slot of the step's
     position (mod the ring length), and the device position one up, call after call."""
