@@ -857,6 +857,13 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
 // earlier. Issues past the last block repeat the last block, which keeps the count fixed.
 // Workgroups are numbered so that each XCD (workgroup index mod 8) takes a contiguous range of
 // (row tile, token tile) pairs, token tile fastest: an XCD's L2 keeps its own weight rows.
+//
+// WV = 8 (block-scale modes without SwiGLU, for grids of fewer than two workgroups per CU): eight
+// waves, two per SIMD. Waves 0-3 keep the roles above, DMA included (the same P instructions per
+// slot, the same wait counts); waves 4-7 issue no DMA. Each of the eight computes one of the two
+// 32-row MFMA tiles that a wave of the four-wave form computes (wave w: tile w >> 2 of the part of
+// wave w & 3), so a block's VALU rescale on one wave of a SIMD can run while the other wave of the
+// SIMD waits on its MFMA or its LDS reads. Same arithmetic, same order, same bits.
 
 static_assert(kGemmTileT == 128 && kGemmTileN == 128, "GEMM tile: the token padding covers both tile heights");
 
@@ -897,17 +904,23 @@ struct GemmRing {
   static_assert((D - KB) * P < 64, "vmcnt range");
 };
 
-template <int WDT, bool SW, bool TOK, bool FAST, int MT, int KBO = 0>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT == 2 ? 1 : 2))) void gemm_a8_kernel(
+template <int WDT, bool SW, bool TOK, bool FAST, int MT, int KBO = 0, int WV = 4>
+__global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && MT == 2 ? 1 : 2))) void gemm_a8_kernel(
     const GemmArgs a) {
   typedef GemmRing<WDT, SW, TOK, MT, KBO> R;
   constexpr int TT = R::TT, NSEL = R::NSEL, D = R::D;
   constexpr bool BLOCKX = R::BLOCKX;
+  static_assert(WV == 4 || (WV == 8 && BLOCKX && !SW && R::KB == 1), "eight waves: block-scale modes without SwiGLU");
+  constexpr int NTW = WV == 8 ? 1 : 2;  // 32-row MFMA tiles per wave
   __shared__ __align__(16) unsigned char ring[R::BYTES];
   __shared__ __align__(16) float Lxdt[TOK ? TT : 4];
 
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wt = wave >> 1, wr = wave & 1;
+  // wave: 0 .. WV - 1; role: the four-wave form's wave whose part this wave shares (DMA by waves 0-3
+  // only); nt0: the first of this wave's 32-row tiles within that part
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), role = wave & 3, wt = role >> 1, wr = role & 1;
+  const int nt0 = WV == 8 ? wave >> 2 : 0;
+  const bool dma_wave = WV == 4 || wave < 4;
   const int nb = a.nb, H = a.H;
   // workgroup -> (row tile, token tile)
   const int n = pin_sgpr(a.n_targets);
@@ -934,45 +947,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
   // of row r, so that wave w's lanes read rows 32 w .. 32 w + 31 as consecutive 16-byte chunks of
   // the repacked layout, and 16 lanes reading one half of 16 rows touch every LDS bank once.
   // q4 weights: lane row (w & 1) * 64 + lane, data (w < 2) or scale.
-  const int drow = WDT == WQ8 ? wave * 32 + (lane >> 1) : (wave & 1) * 64 + lane;
+  const int drow = WDT == WQ8 ? role * 32 + (lane >> 1) : (role & 1) * 64 + lane;
   const int dhalf = (lane & 1) ^ ((drow >> 3) & 1);  // q8: the half that lane fills
   const int wrow = min(r0 + drow, rows_pad - 1);
   const int64_t rbase = (int64_t)(wrow / H) * nb * H + (wrow % H);  // item of (wrow, block 0)
   // this lane's byte offsets at block 0 (the host keeps both arrays below 2 GB); a block adds a
   // uniform stride to the scalar base: 1 KB of activation, H items of weight, Tpad scales
-  const uint32_t xoff = (uint32_t)(((int64_t)((t0 >> 5) + (MT == 2 ? wave : wave >> 1)) * nb * 1024) +
-                                   (MT == 2 ? lane * 16 : (wave & 1) * 512 + l32 * 16));
+  const uint32_t xoff = (uint32_t)(((int64_t)((t0 >> 5) + (MT == 2 ? role : role >> 1)) * nb * 1024) +
+                                   (MT == 2 ? lane * 16 : (role & 1) * 512 + l32 * 16));
   const uint32_t woff = (uint32_t)(WDT == WQ8 ? rbase * 32 + dhalf * 16 : rbase * 16);
   const uint32_t soff = (uint32_t)(rbase * 4);
-  const uint32_t doff = (uint32_t)((t0 + wave * (TT / 4) + lane) * 4);
+  const uint32_t doff = (uint32_t)((t0 + role * (TT / 4) + lane) * 4);
   constexpr uint32_t G = WDT == WQ8 ? 32 : 16;
   const uint32_t wstride = (uint32_t)H * G, sstride = (uint32_t)H * 4, dstride = (uint32_t)a.Tpad * 4;
   const unsigned ring_lds = (unsigned)(size_t)(LdsBytes)ring;
   auto issue = [&](int blk, int slot) {
+    if (!dma_wave) return;  // uniform per wave: waves 4-7 of the eight-wave form copy nothing
     const uint32_t ub = (uint32_t)min(blk, nb - 1);
     const unsigned sb = ring_lds + (unsigned)slot * R::SLOT;
-    if (MT == 2 || lane < 32) dma16s(a.xq + ub * 1024u, xoff, sb + wave * (MT == 2 ? 1024 : 512));
+    if (MT == 2 || lane < 32) dma16s(a.xq + ub * 1024u, xoff, sb + role * (MT == 2 ? 1024 : 512));
 #pragma unroll
     for (int sl = 0; sl < NSEL; ++sl) {
       const unsigned wb = sb + R::ACT + sl * R::WSEL;
-      if (WDT == WQ8 || wave < 2) {
-        dma16s(wdata(sl) + ub * wstride, woff, wb + wave * 1024);
+      if (WDT == WQ8 || role < 2) {
+        dma16s(wdata(sl) + ub * wstride, woff, wb + role * 1024);
       } else {
-        dma4s((const unsigned char*)wscal(sl) + ub * sstride, soff, wb + 2048 + (wave - 2) * 256);
+        dma4s((const unsigned char*)wscal(sl) + ub * sstride, soff, wb + 2048 + (role - 2) * 256);
       }
     }
     if (BLOCKX && lane < TT / 4)
-      dma4s((const unsigned char*)a.xd + ub * dstride, doff, sb + R::ACT + NSEL * R::WSEL + wave * TT);
+      dma4s((const unsigned char*)a.xd + ub * dstride, doff, sb + R::ACT + NSEL * R::WSEL + role * TT);
   };
 
-  v16i iacc[NSEL][MT][2];
-  float facc[NSEL][MT][2][16];
+  v16i iacc[NSEL][MT][NTW];
+  float facc[NSEL][MT][NTW][16];
 #pragma unroll
   for (int s = 0; s < NSEL; ++s)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           iacc[s][mt][nt][i] = 0;
@@ -982,7 +996,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
 #pragma unroll
   for (int i = 0; i < 16; ++i) zero[i] = 0;
 
-  // one 32-block from a slot: MT x 2 MFMAs per wave (per weight selection)
+  // one 32-block from a slot: MT x NTW MFMAs per wave (per weight selection)
   auto block = [&](int slot) {
     const unsigned char* sb = ring + slot * R::SLOT;
     v4i A[MT];
@@ -991,11 +1005,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
 #pragma unroll
     for (int s = 0; s < NSEL; ++s) {
       const unsigned char* wb = sb + R::ACT + s * R::WSEL;
-      v4i B[2];
-      float c[2] = {1.f, 1.f};
+      v4i B[NTW];
+      float c[NTW];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int rl = wr * 64 + nt * 32 + l32;
+      for (int nt = 0; nt < NTW; ++nt) {
+        const int rl = wr * 64 + (nt0 + nt) * 32 + l32;
+        c[nt] = 1.f;
         if (WDT == WQ8) {
           B[nt] = *reinterpret_cast<const v4i*>(wb + (2 * rl + (h ^ ((rl >> 3) & 1))) * 16);
         } else {
@@ -1018,7 +1033,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
           }
         }
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NTW; ++nt) {
           if (TOK && WDT == WQ8) {
             iacc[s][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[mt], B[nt], iacc[s][mt][nt], 0, 0, 0);
           } else {
@@ -1131,13 +1146,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
       xt[4 * g + 3] = x4.w;
     }
   };
-  if (SW) {
+  if constexpr (SW) {
     // gate and up of each 32x32 tile go through this wave's LDS slice, so that silu (an expf)
     // is emitted once in a loop rather than once per accumulator
     float* const ep = reinterpret_cast<float*>(ring) + wave * (2 * 32 * 32);
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int r = r0 + wr * 64 + nt * 32 + l32;
+    for (int nt = 0; nt < NTW; ++nt) {
+      const int r = r0 + wr * 64 + (nt0 + nt) * 32 + l32;
       const int rc = min(r, tg.N - 1);
       const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
       const float wsu = WDT == WQ8 ? a.tg[1].scales[rc] : 1.f;
@@ -1176,8 +1191,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SW && MT ==
   auto store_tiles = [&](auto res_tag) {
     constexpr bool RES = decltype(res_tag)::value;
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int r = r0 + wr * 64 + nt * 32 + l32;
+    for (int nt = 0; nt < NTW; ++nt) {
+      const int r = r0 + wr * 64 + (nt0 + nt) * 32 + l32;
       const int rc = min(r, tg.N - 1);
       const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f;
 #pragma unroll
@@ -2447,13 +2462,26 @@ hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_ti
   return swiglu ? gemv_nt<WQ4, true>(a, total_tiles, s) : gemv_nt<WQ4, false>(a, total_tiles, s);
 }
 
-template <int WDT, bool SW, bool TOK, int MT>
+template <int WDT, bool SW, bool TOK, int MT, int WV = 4>
 static void gemm_launch(const GemmArgs& a, dim3 grid, hipStream_t s) {
   // the per-token q8 accumulation is all-integer: FAST changes nothing there
   if (a.fast && !(TOK && WDT == WQ8))
-    gemm_a8_kernel<WDT, SW, TOK, true, MT><<<grid, 256, 0, s>>>(a);
+    gemm_a8_kernel<WDT, SW, TOK, true, MT, 0, WV><<<grid, 64 * WV, 0, s>>>(a);
   else
-    gemm_a8_kernel<WDT, SW, TOK, false, MT><<<grid, 256, 0, s>>>(a);
+    gemm_a8_kernel<WDT, SW, TOK, false, MT, 0, WV><<<grid, 64 * WV, 0, s>>>(a);
+}
+
+// The ring GEMM with four or eight waves (eight: block-scale modes without SwiGLU, where the grid
+// gives fewer than two workgroups per CU; ELMH_GEMM_WAVES=4 or 8 forces one, same bits).
+template <int WDT, bool SW, bool TOK, int MT>
+static void gemm_launch_waves(const GemmArgs& a, int wgs, int cus, hipStream_t s) {
+  const dim3 grid((wgs + 7) / 8 * 8);
+  if constexpr (!TOK && !SW) {
+    bool eight = wgs < 2 * cus;
+    if (const char* ev = getenv("ELMH_GEMM_WAVES")) eight = ev[0] == '8' ? true : ev[0] == '4' ? false : eight;
+    if (eight) return gemm_launch<WDT, SW, TOK, MT, 8>(a, grid, s);
+  }
+  gemm_launch<WDT, SW, TOK, MT>(a, grid, s);
 }
 
 template <int WDT, bool SW, bool TOK>
@@ -2546,9 +2574,9 @@ static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
     return hipGetLastError();
   }
   if (small)
-    gemm_launch<WDT, SW, TOK, 1>(a, dim3((t64 + 7) / 8 * 8), s);
+    gemm_launch_waves<WDT, SW, TOK, 1>(a, t64, cus, s);
   else
-    gemm_launch<WDT, SW, TOK, 2>(a, dim3((t128 + 7) / 8 * 8), s);
+    gemm_launch_waves<WDT, SW, TOK, 2>(a, t128, cus, s);
   return hipGetLastError();
 }
 hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs& a, int total_tiles, hipStream_t s) {

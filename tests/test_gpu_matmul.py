@@ -6,6 +6,8 @@ Bars (mirroring edgelm's own tests, tests/test_ops.cpp:119-240):
   * vs the reference backend (ref::matmul / ref::swiglu): rel_err < 1e-5 (test_ops.cpp:228,232);
   * ELMH_FAST GEMM: rel_err < 1e-5 against the exact result.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -351,7 +353,14 @@ def test_gemm_token_tiles(ctx, dt, tile, monkeypatch):
     """Both GEMM tile heights (64 and 128 tokens, picked by shape unless ELMH_GEMM_TOKEN_TILE forces
     one) over several token tiles with a ragged last one and a partial last row tile: per-block
     int8 (exact, fast, residual), per-token int8 (block groups with a partial last group: K = 576
-    is 18 blocks), MATMUL_N and FFN_SWIGLU."""
+    is 18 blocks), MATMUL_N and FFN_SWIGLU. The tile height is forced with four and with eight waves
+    per workgroup (ELMH_GEMM_WAVES; eight serve the block-scale modes without SwiGLU)."""
+    for waves in ("8", "4"):
+        monkeypatch.setenv("ELMH_GEMM_WAVES", waves)
+        check_token_tiles(ctx, dt, tile, monkeypatch)
+
+
+def check_token_tiles(ctx, dt, tile, monkeypatch):
     monkeypatch.setenv("ELMH_GEMM_TOKEN_TILE", tile)
     r = rng(500 + dt)
     n, k = 300, 576
@@ -359,7 +368,7 @@ def test_gemm_token_tiles(ctx, dt, tile, monkeypatch):
     wg, wu = weight(r, n, k, dt), weight(r, n, k, dt)
     dw, dw2, dg, du = up(ctx, w), up(ctx, w2), up(ctx, wg), up(ctx, wu)
     for T in [65, 130, 257, 512]:
-        print(f"[gpu] gemm tile={tile} dt={dt} T={T}", flush=True)
+        print(f"[gpu] gemm tile={tile} waves={os.environ.get('ELMH_GEMM_WAVES')} dt={dt} T={T}", flush=True)
         x = r.normal(0, 1, (T, k)).astype(np.float32)
         res = r.normal(0, 1, (T, n)).astype(np.float32)
         got = ctx.matmul(x, [dw, dw2], [res, None], act=E.ACT_INT8, mode=E.EXACT)
