@@ -459,10 +459,27 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f);
   float4 xv[XP], nv[XP];
   if (NORM) {
+    // a.pre_p (one token): element n of x is the small GEMV epilogue of products row n (the o
+    // projection's, formed by the attention kernel): fold in block order, x row scale (q8), + residual
+    const bool pre = a.pre_p != nullptr;
 #pragma unroll
     for (int p = 0; p < XP; ++p) {
       const int e = min(p * kSmallPass + e0, nel - 4);
-      xv[p] = *reinterpret_cast<const float4*>(a.x + e);
+      if (pre) {
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p * kSmallPass + e0 < nel) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float f = fold_chain(a.pre_p + (int64_t)(e + i) * a.pre_stride, a.pre_nb);
+            if (a.pre_ws) f = f * a.pre_ws[e + i];
+            v[i] = a.pre_res ? f + a.pre_res[e + i] : f;
+          }
+          if (blockIdx.x == 0) *reinterpret_cast<float4*>(a.pre_out + e) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+        xv[p] = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+        xv[p] = *reinterpret_cast<const float4*>(a.x + e);
+      }
       nv[p] = *reinterpret_cast<const float4*>(a.nw + (e - e / K * K));
     }
   } else if (e0 < nel) {
@@ -2472,12 +2489,14 @@ static void gemm_launch(const GemmArgs& a, dim3 grid, hipStream_t s) {
 }
 
 // The ring GEMM with four or eight waves (eight: block-scale modes without SwiGLU, where the grid
-// gives fewer than two workgroups per CU; ELMH_GEMM_WAVES=4 or 8 forces one, same bits).
+// gives at most one workgroup per CU, so that four waves would leave one wave per SIMD; measured at
+// T = 512: q8 4096 x 4096 59.2 -> 48.3 us, 4096 x 14336 173.4 -> 133.4 us, while 14336 x 4096 with
+// 448 workgroups went from 98.8 to 103.7 us; ELMH_GEMM_WAVES=4 or 8 forces one, same bits).
 template <int WDT, bool SW, bool TOK, int MT>
 static void gemm_launch_waves(const GemmArgs& a, int wgs, int cus, hipStream_t s) {
   const dim3 grid((wgs + 7) / 8 * 8);
   if constexpr (!TOK && !SW) {
-    bool eight = wgs < 2 * cus;
+    bool eight = wgs <= cus;
     if (const char* ev = getenv("ELMH_GEMM_WAVES")) eight = ev[0] == '8' ? true : ev[0] == '4' ? false : eight;
     if (eight) return gemm_launch<WDT, SW, TOK, MT, 8>(a, grid, s);
   }
