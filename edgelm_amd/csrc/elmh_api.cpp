@@ -619,8 +619,8 @@ bool oproj_pair_ok(int head_dim, int n_heads, int max_ctx, const elmh_weight* wo
                    const elmh_weight* wu, int act) {
   if (!wo || !wg || !wu || act != ELMH_ACT_INT8 || head_dim != 64 || n_heads < 1 || max_ctx < 1) return false;
   const DevWeight& o = wo->w;
-  if (!a8_applies(o) || o.cols != (int64_t)n_heads * 64 || o.nb != 2 * n_heads || o.rows < 4 || o.rows % 4 ||
-      o.rows > 8192 || !attention_oproj_ok(max_ctx))
+  if (!a8_applies(o) || o.cols != (int64_t)n_heads * 64 || o.nb != 2 * n_heads || o.nb > 20 || o.rows < 4 ||
+      o.rows % 4 || o.rows > 1024 || !attention_oproj_ok(max_ctx))
     return false;
   const int64_t K = o.rows;
   const elmh_weight* const ws[2] = {wg, wu};

@@ -92,7 +92,7 @@ struct GemvArgs {
   const float* xd;    // f32 [T][nb]
   const int32_t* xs;  // int32 [T][nb] block sums of q
   int T, K, nb;
-  // small kernel with nw, T = 1: x is not read; element n of x is the fold of the products
+  // small kernel with nw, T = 1, K <= 1024: x is not read; element n of x is the fold of the products
   // pre_p[n * pre_stride + 0 .. pre_nb - 1] in block order, times pre_ws[n] (q8 rows; null for q4),
   // plus pre_res[n] (null: none), exactly the small GEMV's epilogue; workgroup 0 writes it to pre_out
   const float* pre_p;

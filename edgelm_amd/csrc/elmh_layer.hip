@@ -474,7 +474,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
 // of each thread have their weights requested once the keys have landed, to arrive during the
 // scores and the sums.
 constexpr int kDecRows = 256;  // C: rows per LDS buffer, one per thread
-constexpr int kOprojPre = 4;   // weight items per thread requested early
+constexpr int kOprojPre = 5;   // weight items per thread requested early (SmolLM2: 1152 items)
 
 // item (row n, block b) of a repacked weight: its index in the [rows_pad / H][nb][H] layout
 __device__ __forceinline__ int64_t oproj_item(const OprojArgs& op, int n, int b) {

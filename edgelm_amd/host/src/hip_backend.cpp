@@ -21,6 +21,11 @@
 // position, launches the graph, and copies back what the host reads (the logits). A buffer that
 // has to grow (a longer prefill) drops the graphs. EDGELM_HIP_GRAPHS=0 turns graphs off.
 //
+// A decode step's ATTENTION -> o projection -> RMSNORM -> FFN_SWIGLU runs as two calls: the attention
+// workgroups also form the o projection's per-block products, and the RMSNORM + FFN_SWIGLU call folds
+// them with the residual (writing the o projection's output for its later readers), so the o
+// projection takes no launch of its own. EDGELM_HIP_OPROJ=0 runs it on its own (same bits).
+//
 // keep_output() and argmax_output() (the greedy-sampling hooks) leave the logits in HBM and hand
 // the host only the argmax of their last row.
 #include <algorithm>
@@ -46,6 +51,8 @@ class HipBackend : public Backend {
   HipBackend(int device, bool layer_ops) : layer_ops_(layer_ops) {
     const char* g = std::getenv("EDGELM_HIP_GRAPHS");
     graphs_on_ = !(g && g[0] == '0');
+    const char* op = std::getenv("EDGELM_HIP_OPROJ");  // 0: the decode step's o projection runs on its own
+    oproj_on_ = !(op && op[0] == '0');
     if (device < 0) return;
     if (elmh_create(device, &ctx_) != ELMH_OK)
       throw std::runtime_error(std::string("edgelm: hip backend unavailable: ") + elmh_last_error(nullptr));
@@ -680,7 +687,7 @@ class HipBackend : public Backend {
     const float* k = in(op.in[1], c);
     const float* v = in(op.in[2], c);
     const int idx = static_cast<int>(&op - c.graph->ops.data());
-    if (prepared_ && fuse_oproj_[idx] && T == 1 && c.act_quant) {
+    if (prepared_ && oproj_on_ && fuse_oproj_[idx] && T == 1 && c.act_quant) {
       const Graph& g = *c.graph;
       elmh_weight* wo = weight(c.tensor(g.ops[idx + 1].in[1]));
       elmh_weight* wg = weight(c.tensor(g.ops[idx + 3].in[1]));
@@ -711,6 +718,7 @@ class HipBackend : public Backend {
 
   bool layer_ops_;
   bool graphs_on_ = true;
+  bool oproj_on_ = true;
   bool capturing_ = false;
   uint64_t buffer_gen_ = 0;
   std::map<int, StepGraph> graphs_;  // by the partition's first op
