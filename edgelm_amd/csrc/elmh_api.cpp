@@ -436,7 +436,7 @@ int run_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight
 }
 
 int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight* wg, const elmh_weight* wu, float* y,
-               int act, int mode, const float* nw = nullptr, float eps = 0.f, const GemvArgs* pre = nullptr) {
+               int act, int mode, const float* nw = nullptr, float eps = 0.f) {
   if (!wg || !wu || !y) return fail(c, ELMH_ERR_ARG, "swiglu: null weight or output");
   if (T < 1 || wg->w.cols != K || wu->w.cols != K) return fail(c, ELMH_ERR_ARG, "swiglu: bad shape");
   if (wg->w.rows != wu->w.rows) return fail(c, ELMH_ERR_ARG, "swiglu: gate and up row counts differ");
@@ -500,18 +500,9 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
     a.T = T;
     a.K = (int)K;
     a.nb = (int)(K / kBlock);
-    if (pre) {  // x is the fold of products (elmh_oproj_rmsnorm_swiglu_dev checked this path applies)
-      a.pre_p = pre->pre_p;
-      a.pre_ws = pre->pre_ws;
-      a.pre_res = pre->pre_res;
-      a.pre_out = pre->pre_out;
-      a.pre_stride = pre->pre_stride;
-      a.pre_nb = pre->pre_nb;
-    }
     HIP_OR_FAIL(c, launch_gemv_a8(g.dtype, 1, a, tiles, c->stream));
     return ELMH_OK;
   }
-  if (pre) return fail(c, ELMH_ERR_UNSUPPORTED, "swiglu: product fold off the small GEMV path");
   const int token = act == ELMH_ACT_INT8_TOKEN;
   int Tpad;
   ActBufs ab;
@@ -608,24 +599,6 @@ int check_attention(elmh_ctx* c, const float* q, const float* k, const float* v,
     return fail(c, ELMH_ERR_ARG, "attention: heads %d / kv heads %d / head_dim %d", n_heads, n_kv, head_dim);
   if (!rope_cos != !rope_sin) return fail(c, ELMH_ERR_ARG, "attention: rope_cos and rope_sin go together");
   return ELMH_OK;
-}
-
-// Row stride (floats) of the o projection's products: nb rounded up to whole float4 (fold_chain's reads).
-int oproj_pstride(const DevWeight& w) { return (int)((w.nb + 3) & ~3); }
-
-// Whether a decode step's attention may form the o projection's products (elmh_attention_oproj_dev)
-// for the RMSNORM + FFN_SWIGLU call that folds them (elmh_oproj_rmsnorm_swiglu_dev).
-bool oproj_pair_ok(int head_dim, int n_heads, int max_ctx, const elmh_weight* wo, const elmh_weight* wg,
-                   const elmh_weight* wu, int act) {
-  if (!wo || !wg || !wu || act != ELMH_ACT_INT8 || head_dim != 64 || n_heads < 1 || max_ctx < 1) return false;
-  const DevWeight& o = wo->w;
-  if (!a8_applies(o) || o.cols != (int64_t)n_heads * 64 || o.nb != 2 * n_heads || o.nb > 20 || o.rows < 4 ||
-      o.rows % 4 || o.rows > 1024 || !attention_oproj_ok(max_ctx))
-    return false;
-  const int64_t K = o.rows;
-  const elmh_weight* const ws[2] = {wg, wu};
-  return wg->w.dtype == wu->w.dtype && wg->w.H == wu->w.H && wg->w.rows == wu->w.rows && wg->w.cols == K &&
-         wu->w.cols == K && norm_fusable(1, K, 2, ws, 2, act);
 }
 
 // The global score rows of an attention call whose rows do not fit LDS (null when they do).
@@ -1225,56 +1198,6 @@ int elmh_attention_dev(elmh_ctx* c, const float* q, const float* k, const float*
   HIP_OR_FAIL(c, launch_attention(q, k, v, out, T, pos0, nullptr, n_heads, n_kv, head_dim, k_cache, v_cache, max_ctx,
                                   rope_cos, rope_sin, c->stream, nullptr, nullptr, 0, nullptr, gsc));
   return ELMH_OK;
-}
-
-int elmh_attention_oproj_supported(int head_dim, int n_heads, int max_ctx, const elmh_weight* w_o,
-                                    const elmh_weight* wg, const elmh_weight* wu, int act) {
-  return oproj_pair_ok(head_dim, n_heads, max_ctx, w_o, wg, wu, act) ? 1 : 0;
-}
-
-size_t elmh_oproj_partials_bytes(const elmh_weight* w_o) {
-  return w_o ? (size_t)w_o->w.rows * oproj_pstride(w_o->w) * sizeof(float) : 0;
-}
-
-int elmh_attention_oproj_dev(elmh_ctx* c, const float* q, const float* k, const float* v, float* out, int pos0,
-                             const int32_t* pos_dev, int n_heads, int n_kv, int head_dim, float* k_cache,
-                             float* v_cache, int max_ctx, const float* rope_cos, const float* rope_sin,
-                             const elmh_weight* w_o, float* partials) {
-  const int rc = check_attention(c, q, k, v, out, 1, pos_dev ? 0 : pos0, n_heads, n_kv, head_dim, k_cache, v_cache,
-                                 max_ctx, rope_cos, rope_sin);
-  if (rc) return rc;
-  if (!w_o || !partials) return fail(c, ELMH_ERR_ARG, "attention_oproj: null weight/partials");
-  const DevWeight& o = w_o->w;
-  if (head_dim != 64 || !a8_applies(o) || o.cols != (int64_t)n_heads * 64 || o.nb != 2 * n_heads || o.rows > 8192 ||
-      !attention_oproj_ok(max_ctx))
-    return fail(c, ELMH_ERR_UNSUPPORTED, "attention_oproj: head_dim %d, %lldx%lld weight, max_ctx %d", head_dim,
-                (long long)o.rows, (long long)o.cols, max_ctx);
-  DeviceGuard g(c);
-  const OprojArgs op{o.data, o.scales, partials, o.dtype, (int)o.rows, (int)o.nb, o.H, oproj_pstride(o)};
-  HIP_OR_FAIL(c, launch_attention(q, k, v, out, 1, pos_dev ? 0 : pos0, pos_dev, n_heads, n_kv, head_dim, k_cache,
-                                  v_cache, max_ctx, rope_cos, rope_sin, c->stream, nullptr, nullptr, 0, nullptr, nullptr,
-                                  &op));
-  return ELMH_OK;
-}
-
-int elmh_oproj_rmsnorm_swiglu_dev(elmh_ctx* c, const float* partials, const elmh_weight* w_o, const float* residual,
-                                  float* x1, const float* norm_w, float eps, const elmh_weight* wg,
-                                  const elmh_weight* wu, float* y, int act, int mode) {
-  if (!c || !partials || !w_o || !x1 || !norm_w || !wg || !wu || !y)
-    return fail(c, ELMH_ERR_ARG, "oproj_rmsnorm_swiglu: null pointer");
-  const DevWeight& o = w_o->w;
-  if (!oproj_pair_ok(64, (int)(o.cols / 64), 1, w_o, wg, wu, act))
-    return fail(c, ELMH_ERR_UNSUPPORTED, "oproj_rmsnorm_swiglu: %lldx%lld o weight with this FFN is off the fused path",
-                (long long)o.rows, (long long)o.cols);
-  DeviceGuard g(c);
-  GemvArgs pre{};
-  pre.pre_p = partials;
-  pre.pre_ws = o.dtype == ELMH_Q8 ? o.scales : nullptr;
-  pre.pre_res = residual;
-  pre.pre_out = x1;
-  pre.pre_stride = oproj_pstride(o);
-  pre.pre_nb = (int)o.nb;
-  return run_swiglu(c, x1, 1, o.rows, wg, wu, y, act, mode, norm_w, eps, &pre);
 }
 
 int elmh_attention_step_supported(int head_dim, int max_ctx) {

@@ -66,17 +66,6 @@ struct GemvTarget {
   int tiles;         // rows_pad / H
 };
 
-// A decode step's o projection formed inside the attention kernel (head size 64, one token): the
-// workgroup of head h quantizes its output's 32-blocks 2h and 2h + 1 as quantize_act_row does and
-// writes the item product of every weight row with each of them (the small GEMV's products) to
-// p[n * pstride + b]. The consumer folds each row's products in block order (PreFold).
-struct OprojArgs {
-  const uint8_t* data;  // repacked q8 / q4 weight: [rows_pad / H][nb][H][G] bytes
-  const float* scales;
-  float* p;             // [N][pstride] products; null: no o projection
-  int dtype, N, nb, H, pstride;
-};
-
 struct GemvArgs {
   GemvTarget tg[kMaxTargets];
   int tile_start[kMaxTargets + 1];  // prefix sums of tiles (matmul); swiglu uses tg[0]/tg[1]
@@ -92,14 +81,6 @@ struct GemvArgs {
   const float* xd;    // f32 [T][nb]
   const int32_t* xs;  // int32 [T][nb] block sums of q
   int T, K, nb;
-  // small kernel with nw, T = 1, K <= 1024: x is not read; element n of x is the fold of the products
-  // pre_p[n * pre_stride + 0 .. pre_nb - 1] in block order, times pre_ws[n] (q8 rows; null for q4),
-  // plus pre_res[n] (null: none), exactly the small GEMV's epilogue; workgroup 0 writes it to pre_out
-  const float* pre_p;
-  const float* pre_ws;
-  const float* pre_res;
-  float* pre_out;
-  int pre_stride, pre_nb;
 };
 
 struct GemmTarget {
@@ -180,15 +161,10 @@ size_t attention_global_score_bytes(int T, int pos0, bool pos_dev, int n_heads, 
 // *quantized; otherwise *quantized is false and xq, xd are untouched.
 // gscores: attention_global_score_bytes() of device memory where that is not 0 (score rows longer than
 // LDS holds); without it such a call fails with hipErrorInvalidValue.
-// op (T = 1, head size 64, the score row within attention_decode_lds_bytes): the o projection's
-// products as well (OprojArgs); a call that cannot form them fails with hipErrorInvalidValue.
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
                             const int* pos_dev, int n_heads, int n_kv, int hd, float* kc, float* vc, int max_ctx,
                             const float* rcos, const float* rsin, hipStream_t s, int8_t* xq = nullptr,
-                            float* xd = nullptr, int Tpad = 0, bool* quantized = nullptr, float* gscores = nullptr,
-                            const OprojArgs* op = nullptr);
-// true if launch_attention takes an OprojArgs for one token at head size 64 with this score row
-bool attention_oproj_ok(int n_cap);
+                            float* xd = nullptr, int Tpad = 0, bool* quantized = nullptr, float* gscores = nullptr);
 hipError_t launch_embed(const int32_t* tok, int T, const DevWeight& w, float* y, hipStream_t s);
 // dst[0, bytes) = value (a kernel: capturable in a HIP graph, unlike hipMemsetAsync)
 hipError_t launch_fill(void* dst, int value, size_t bytes, hipStream_t s);

@@ -435,43 +435,6 @@ __device__ __forceinline__ GemvTarget gemv_target(const GemvArgs& a, int& wg) {
 constexpr int kSmallPass = kGemvThreads * 4;
 constexpr int kSmallMaxAct = 4 * kSmallPass;
 
-// Elements e .. e + 3 of x given as products (GemvArgs::pre_p, at most kPreMaxQ float4 per row): each
-// row's products folded in block order (fold_chain's order), times the row scale (q8), plus the
-// residual: the small GEMV's epilogue. Every load is issued before the first add; workgroup 0 also
-// writes the four values to pre_out.
-constexpr int kPreMaxQ = 5;  // products per row up to 20 (ten heads of 64)
-__device__ __forceinline__ void pre_fold4(const GemvArgs& a, int e, float (&v)[4]) {
-  const int nq = (a.pre_nb + 3) >> 2;  // float4 per row holding products
-  float4 pv[4][kPreMaxQ];
-  float ws[4] = {1.f, 1.f, 1.f, 1.f}, rs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float4* row = reinterpret_cast<const float4*>(a.pre_p + (int64_t)(e + i) * a.pre_stride);
-#pragma unroll
-    for (int k = 0; k < kPreMaxQ; ++k) pv[i][k] = row[min(k, nq - 1)];
-    if (a.pre_ws) ws[i] = a.pre_ws[e + i];
-    if (a.pre_res) rs[i] = a.pre_res[e + i];
-  }
-  const int tail = a.pre_nb & 3;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float acc = 0.f;
-#pragma unroll
-    for (int k = 0; k < kPreMaxQ; ++k) {
-      if (k < nq - (tail ? 1 : 0)) {
-        add4(acc, pv[i][k]);
-      } else if (k == nq - 1) {  // the last nb % 4 products
-        acc = acc + pv[i][k].x;
-        if (tail > 1) acc = acc + pv[i][k].y;
-        if (tail > 2) acc = acc + pv[i][k].z;
-      }
-    }
-    if (a.pre_ws) acc = acc * ws[i];
-    v[i] = a.pre_res ? acc + rs[i] : acc;
-  }
-  if (blockIdx.x == 0) *reinterpret_cast<float4*>(a.pre_out + e) = make_float4(v[0], v[1], v[2], v[3]);
-}
-
 // NORM: x is the un-normalized row and the workgroup applies edgelm's RMSNORM to it first
 // (cpu::rmsnorm, kernels_cpu.cpp:326-335, in the order of rmsnorm_kernel: squares grouped by
 // dot_f32_scalar's four accumulators, four in-order sums, (s0 + s1) + (s2 + s3), then
@@ -496,19 +459,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f);
   float4 xv[XP], nv[XP];
   if (NORM) {
-    // a.pre_p (one token): element n of x is the small GEMV epilogue of products row n (the o
-    // projection's, formed by the attention kernel): fold in block order, x row scale (q8), + residual
-    const bool pre = a.pre_p != nullptr;
 #pragma unroll
     for (int p = 0; p < XP; ++p) {
       const int e = min(p * kSmallPass + e0, nel - 4);
-      if (pre) {
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
-        if (p == 0 && e0 < nel) pre_fold4(a, e, v);  // x of at most kSmallPass elements (one pass)
-        xv[p] = make_float4(v[0], v[1], v[2], v[3]);
-      } else {
-        xv[p] = *reinterpret_cast<const float4*>(a.x + e);
-      }
+      xv[p] = *reinterpret_cast<const float4*>(a.x + e);
       nv[p] = *reinterpret_cast<const float4*>(a.nw + (e - e / K * K));
     }
   } else if (e0 < nel) {

@@ -10,7 +10,6 @@
 #include "elm_dma.h"
 #include "elm_dpp.h"
 #include "elm_expf.h"
-#include "elm_gemv.h"
 #include "elm_quant.h"
 #include "elmh_internal.hpp"
 
@@ -467,20 +466,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
 // buffer, values alternating between both, the next chunk in flight while wave 0 adds the current.
 // LDS (dynamic): keys [C][64], values [C][64], scores [n_cap rounded up to 256], q [64], the
 // step's rotated key [64].
-// With op.p (OprojArgs), the workgroup then forms the o projection's products for its head's two
-// 32-blocks of the output (lanes 0-31 of wave 0 hold block 2h, lanes 32-63 block 2h + 1): they are
-// quantized with edgelm's rounding (as the small GEMV would quantize the whole row) and every
-// thread takes items (row n, block j) with the small GEMV's item_product. The first kOprojPre items
-// of each thread have their weights requested once the keys have landed, to arrive during the
-// scores and the sums.
 constexpr int kDecRows = 256;  // C: rows per LDS buffer, one per thread
-constexpr int kOprojPre = 5;   // weight items per thread requested early (SmolLM2: 1152 items)
-
-// item (row n, block b) of a repacked weight: its index in the [rows_pad / H][nb][H] layout
-__device__ __forceinline__ int64_t oproj_item(const OprojArgs& op, int n, int b) {
-  const int lgH = __builtin_ctz(op.H);
-  return ((int64_t)(n >> lgH) * op.nb + b) * op.H + (n & (op.H - 1));
-}
 
 // dot_f32_scalar's order (four strided accumulators, then (s0 + s1) + (s2 + s3)) of q and a row
 // in LDS whose chunk u sits in slot u ^ swz
@@ -586,8 +572,7 @@ done:
 __global__ __launch_bounds__(256) void attention_decode64_kernel(
     const float* __restrict__ q, float* __restrict__ out, float* __restrict__ kc, float* __restrict__ vc, int pos0,
     const int* __restrict__ pos_dev, int n_heads, int n_kv, int max_ctx, int n_cap, const float* __restrict__ rcos,
-    const float* __restrict__ rsin, const float* __restrict__ knew, const float* __restrict__ vnew,
-    const OprojArgs op) {
+    const float* __restrict__ rsin, const float* __restrict__ knew, const float* __restrict__ vnew) {
   constexpr int HD = 64, H2 = 32, C = kDecRows, ROWB = HD * 4;
   extern __shared__ __align__(16) float lds[];
   float* const kb = lds;
@@ -630,25 +615,6 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
     sr = rsin[(int64_t)pos * H2 + ih];
   }
   wait_vm<0>();  // the keys, q, k, v and the rotation's cos / sin
-  // the o projection's first weight items (item it: block 2h + it / N, row it % N)
-  const int op_items = op.p ? 2 * op.N : 0;  // uniform
-  v4u ow0[kOprojPre], ow1[kOprojPre];
-  float ows[kOprojPre];
-#pragma unroll
-  for (int u = 0; u < kOprojPre; ++u) {
-    ow0[u] = ow1[u] = v4u{0u, 0u, 0u, 0u};
-    ows[u] = 0.f;
-    const int it = tid + 256 * u;
-    if (it < op_items) {
-      const int j = it >= op.N, n = it - j * op.N;
-      const int64_t gi = oproj_item(op, n, 2 * h + j);
-      const v4u* src = reinterpret_cast<const v4u*>(op.data + gi * (op.dtype == 1 ? 32 : 16));
-      ow0[u] = src[0];
-      if (op.dtype == 1) ow1[u] = src[1];
-      else ows[u] = op.scales[gi];
-    }
-  }
-  asm volatile("" ::: "memory");  // requested here, not at their first use
   if (tid < H2) {
     // cpu::attention step 1 (kv_append_kernel's arithmetic) and q's rotation
     const float q0 = rcos ? qa * cr - qz * sr : qa, q1 = rcos ? qz * cr + qa * sr : qz;
@@ -742,56 +708,7 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
       __syncthreads();
     }
   }
-  const float o = acc + sc[nc] * vlast;  // wave 0: position n - 1, the step's own value
-  if (wave == 0) out[h * HD + lane] = o;
-  if (!op.p) return;  // uniform
-
-  // o projection: the head's two blocks quantized as quantize_act_row (amax / 127, edgelm's
-  // rounding: elm_q8_group) with their sums of q, then the products of every row with each
-  __shared__ __align__(16) int8_t oq[HD];
-  __shared__ float od[2];
-  __shared__ int osum[2];
-  if (wave == 0) {
-    float a = fmaxf(0.f, fabsf(o));
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) a = fmaxf(a, __shfl_xor(a, m, 64));
-    const float scl = a / 127.0f;
-    int qv;
-    elm_q8_group<1>(&o, scl == 0.f ? 1.f : scl, &qv);
-    int sm = qv;
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) sm += __shfl_xor(sm, m, 64);
-    oq[lane] = (int8_t)qv;
-    if ((lane & 31) == 0) {
-      od[lane >> 5] = scl;
-      osum[lane >> 5] = sm;
-    }
-  }
-  __syncthreads();
-  for (int u = 0; 256 * u < op_items; ++u) {
-    const int it = tid + 256 * u;
-    if (it >= op_items) break;
-    const int j = it >= op.N, n = it - j * op.N, b = 2 * h + j;
-    v4u w0 = ow0[0], w1 = ow1[0];
-    float ws = ows[0];
-#pragma unroll
-    for (int k = 1; k < kOprojPre; ++k)
-      if (u == k) {
-        w0 = ow0[k];
-        w1 = ow1[k];
-        ws = ows[k];
-      }
-    if (u >= kOprojPre) {
-      const int64_t gi = oproj_item(op, n, b);
-      const v4u* src = reinterpret_cast<const v4u*>(op.data + gi * (op.dtype == 1 ? 32 : 16));
-      w0 = src[0];
-      if (op.dtype == 1) w1 = src[1];
-      else ws = op.scales[gi];
-    }
-    const float pr = op.dtype == 1 ? item_product<1>(w0, w1, ws, oq + 32 * j, od[j], osum[j])
-                                   : item_product<2>(w0, w1, ws, oq + 32 * j, od[j], osum[j]);
-    op.p[(int64_t)n * op.pstride + b] = pr;
-  }
+  if (wave == 0) out[h * HD + lane] = acc + sc[nc] * vlast;  // position n - 1: the step's own value
 }
 
 // Prefill (T > 1, head size 64): one workgroup per (head, kAttnQ consecutive query tokens), wave w
@@ -1455,8 +1372,6 @@ size_t attention_decode_lds_bytes(int n_cap) {
   return ((size_t)2 * kDecRows * 64 + (size_t)((n_cap + 255) & ~255) + 128) * sizeof(float);
 }
 
-bool attention_oproj_ok(int n_cap) { return attention_decode_lds_bytes(n_cap) <= kMaxAttnLds; }
-
 size_t attention_lds_bytes(int hd, int n_max) {
   const size_t hdp = (size_t)((hd + 3) & ~3);
   return (2 * hdp + (size_t)((n_max + 63) & ~63) + (size_t)attn_chunk_pos(hd) * hd) * sizeof(float);
@@ -1490,7 +1405,7 @@ bool raise_lds_limit() {
 hipError_t launch_attention(const float* q, const float* k, const float* v, float* out, int T, int pos0,
                             const int* pos_dev, int n_heads, int n_kv, int hd, float* kc, float* vc, int max_ctx,
                             const float* rcos, const float* rsin, hipStream_t s, int8_t* xq, float* xd, int Tpad,
-                            bool* quantized, float* gscores, const OprojArgs* op) {
+                            bool* quantized, float* gscores) {
   if (quantized) *quantized = false;
   // with the position in device memory the score buffer covers the whole cache
   const int n_cap = pos_dev ? max_ctx : pos0 + T;  // score slots
@@ -1532,17 +1447,9 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
   const bool in_lds = attention_lds_bytes(hd, n_cap) <= kMaxAttnLds;
   if (!in_lds && !gscores) return hipErrorInvalidValue;  // a score row past LDS needs the global rows
   const size_t lds_gs = attention_gs_lds_bytes(hd), lds = attention_lds_bytes(hd, n_cap);
-  const bool dec64 = fuse && hd == 64 && attention_decode_lds_bytes(n_cap) <= kMaxAttnLds;
-  if (op && op->p) {
-    // the o projection's products need the decode kernel and a head's output to be two whole blocks
-    if (!dec64 || op->nb != 2 * n_heads || op->N < 1 || op->H < 1 || (op->H & (op->H - 1)) ||
-        op->pstride < op->nb || (op->dtype != 1 && op->dtype != 2))
-      return hipErrorInvalidValue;
-  }
-  const OprojArgs no_op{nullptr, nullptr, nullptr, 0, 0, 0, 1, 0};
-  if (dec64)
+  if (fuse && hd == 64 && attention_decode_lds_bytes(n_cap) <= kMaxAttnLds)
     attention_decode64_kernel<<<n_heads, 256, attention_decode_lds_bytes(n_cap), s>>>(
-        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, max_ctx, n_cap, rcos, rsin, k, v, op ? *op : no_op);
+        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, max_ctx, n_cap, rcos, rsin, k, v);
   else if (hd == 64 && in_lds)
     attention_kernel<64, false><<<T * n_heads, kAttnThreads, lds, s>>>(
         q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin, kn, vn, nullptr);

@@ -272,32 +272,6 @@ class Context:
                                                   C.c_int(T), C.c_int64(K), wg.h, wu.h, C.c_void_p(y_ptr),
                                                   C.c_int(act), C.c_int(mode)))
 
-    def attention_oproj_supported(self, head_dim, n_heads, max_ctx, w_o, wg, wu, act=ACT_INT8):
-        return bool(lib().elmh_attention_oproj_supported(C.c_int(head_dim), C.c_int(n_heads), C.c_int(max_ctx), w_o.h,
-                                                         wg.h, wu.h, C.c_int(act)))
-
-    @staticmethod
-    def oproj_partials_bytes(w_o):
-        lib().elmh_oproj_partials_bytes.restype = C.c_size_t
-        return int(lib().elmh_oproj_partials_bytes(w_o.h))
-
-    def attention_oproj_dev(self, q_ptr, k_ptr, v_ptr, out_ptr, pos0, pos_ptr, n_heads, n_kv, head_dim, kc_ptr, vc_ptr,
-                            max_ctx, cos_ptr, sin_ptr, w_o, partials_ptr):
-        """elmh_attention_oproj_dev: one token's attention (position *pos_ptr, or pos0 when pos_ptr is None) and the
-        o projection's per-block products."""
-        self._check(lib().elmh_attention_oproj_dev(
-            self.h, C.c_void_p(q_ptr), C.c_void_p(k_ptr), C.c_void_p(v_ptr), C.c_void_p(out_ptr), C.c_int(pos0),
-            C.c_void_p(pos_ptr), C.c_int(n_heads), C.c_int(n_kv), C.c_int(head_dim), C.c_void_p(kc_ptr),
-            C.c_void_p(vc_ptr), C.c_int(max_ctx), C.c_void_p(cos_ptr), C.c_void_p(sin_ptr), w_o.h,
-            C.c_void_p(partials_ptr)))
-
-    def oproj_rmsnorm_swiglu_dev(self, partials_ptr, w_o, res_ptr, x1_ptr, nw_ptr, eps, wg, wu, y_ptr, act=ACT_INT8,
-                                 mode=EXACT):
-        """elmh_oproj_rmsnorm_swiglu_dev: x1 = fold of the products (+ residual), then RMSNORM + FFN_SWIGLU into y."""
-        self._check(lib().elmh_oproj_rmsnorm_swiglu_dev(
-            self.h, C.c_void_p(partials_ptr), w_o.h, C.c_void_p(res_ptr), C.c_void_p(x1_ptr), C.c_void_p(nw_ptr),
-            C.c_float(eps), wg.h, wu.h, C.c_void_p(y_ptr), C.c_int(act), C.c_int(mode)))
-
     def attention_dev(self, q_ptr, k_ptr, v_ptr, out_ptr, T, pos0, n_heads, n_kv, head_dim, kc_ptr, vc_ptr, max_ctx,
                       cos_ptr=None, sin_ptr=None):
         self._check(lib().elmh_attention_dev(

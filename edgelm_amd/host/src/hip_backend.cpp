@@ -21,11 +21,6 @@
 // position, launches the graph, and copies back what the host reads (the logits). A buffer that
 // has to grow (a longer prefill) drops the graphs. EDGELM_HIP_GRAPHS=0 turns graphs off.
 //
-// A decode step's ATTENTION -> o projection -> RMSNORM -> FFN_SWIGLU runs as two calls: the attention
-// workgroups also form the o projection's per-block products, and the RMSNORM + FFN_SWIGLU call folds
-// them with the residual (writing the o projection's output for its later readers), so the o
-// projection takes no launch of its own. EDGELM_HIP_OPROJ=0 runs it on its own (same bits).
-//
 // keep_output() and argmax_output() (the greedy-sampling hooks) leave the logits in HBM and hand
 // the host only the argmax of their last row.
 #include <algorithm>
@@ -51,8 +46,6 @@ class HipBackend : public Backend {
   HipBackend(int device, bool layer_ops) : layer_ops_(layer_ops) {
     const char* g = std::getenv("EDGELM_HIP_GRAPHS");
     graphs_on_ = !(g && g[0] == '0');
-    const char* op = std::getenv("EDGELM_HIP_OPROJ");  // 0: the decode step's o projection runs on its own
-    oproj_on_ = !(op && op[0] == '0');
     if (device < 0) return;
     if (elmh_create(device, &ctx_) != ELMH_OK)
       throw std::runtime_error(std::string("edgelm: hip backend unavailable: ") + elmh_last_error(nullptr));
@@ -70,7 +63,6 @@ class HipBackend : public Backend {
     }
     elmh_free(ctx_, rope_cos_);
     elmh_free(ctx_, rope_sin_);
-    elmh_free(ctx_, part_);
     elmh_free(ctx_, dev_tok_);
     elmh_free(ctx_, step_ring_);
     release_pins();
@@ -126,7 +118,6 @@ class HipBackend : public Backend {
       for (int t : op.in) ++readers[t];
     fuse_norm_.assign(g.ops.size(), 0);
     fuse_attn_.assign(g.ops.size(), 0);
-    fuse_oproj_.assign(g.ops.size(), 0);
     for (const Partition& p : parts) {
       if (p.backend != this) continue;
       for (int i = p.begin; i + 1 < p.end; ++i) {
@@ -140,16 +131,6 @@ class HipBackend : public Backend {
         // would run before the deferred kernel)
         fuse_attn_[i] = a.type == OpType::ATTENTION && !host_needed_[a.out[0]] && !b.in.empty() &&
                         b.in[0] == a.out[0] && (b.type == OpType::MATMUL || b.type == OpType::MATMUL_ADD);
-      }
-      // a decode step's ATTENTION -> o projection -> RMSNORM -> FFN_SWIGLU, all here: the attention call
-      // also forms the o projection's products and the RMSNORM + FFN_SWIGLU call folds them (the o
-      // projection's output x1 is written by that call, for its later readers on the device)
-      for (int i = p.begin; i + 3 < p.end; ++i) {
-        const Op &a = g.ops[i], &o = g.ops[i + 1], &n = g.ops[i + 2], &f = g.ops[i + 3];
-        fuse_oproj_[i] = fuse_attn_[i] && readers[a.out[0]] == 1 && o.out.size() == 1 && !host_needed_[o.out[0]] &&
-                         (o.type == OpType::MATMUL_ADD || o.type == OpType::MATMUL) && n.type == OpType::RMSNORM &&
-                         n.in[0] == o.out[0] && fuse_norm_[i + 2] && f.type == OpType::FFN_SWIGLU &&
-                         f.in[0] == n.out[0];
       }
     }
     act_.assign(nt, Buf{});
@@ -233,23 +214,11 @@ class HipBackend : public Backend {
     // a deferred ATTENTION (fuse_attn_) runs inside this matmul's call
     const bool attended = attn_.op == idx - 1 && attn_.op >= 0;
     if (!attended) attn_.op = -1;
-    // the o projection whose products the attention call formed (fuse_oproj_): folded two ops later
-    const bool oprojected = oproj_.op == idx && oproj_.op >= 0;
-    if (!oprojected) oproj_.op = -1;
-    const bool folded = fold_.op == idx - 2 && fold_.op >= 0 && normed;
-    if (!folded && fold_.op != idx - 1) fold_.op = -1;
     switch (op.type) {
       case OpType::FFN_SWIGLU: {
         const int T = static_cast<int>(c.rows(op.in[0]));
         const int64_t K = c.tensor(op.in[1]).cols;
-        EDGELM_CHECK(folded || fold_.op < 0, "hip: the o projection's fold lost its RMSNORM");
-        if (folded) {
-          check(elmh_oproj_rmsnorm_swiglu_dev(ctx_, fold_.part, fold_.wo, fold_.res, fold_.x1, norm_.w, norm_.eps,
-                                              weight(c.tensor(op.in[1])), weight(c.tensor(op.in[2])),
-                                              out(op.out[0], c), act(c), ELMH_EXACT),
-                op);
-          fold_.op = -1;
-        } else if (normed)
+        if (normed)
           check(elmh_rmsnorm_swiglu_dev(ctx_, norm_.x, norm_.w, norm_.eps, T, K, weight(c.tensor(op.in[1])),
                                         weight(c.tensor(op.in[2])), out(op.out[0], c), act(c), ELMH_EXACT),
                 op);
@@ -262,12 +231,6 @@ class HipBackend : public Backend {
       case OpType::MATMUL:
       case OpType::MATMUL_N:
       case OpType::MATMUL_ADD: {
-        if (oprojected) {  // its products exist; the RMSNORM + FFN_SWIGLU call two ops on folds them
-          fold_ = {idx, oproj_.part, oproj_.wo, op.type == OpType::MATMUL_ADD ? in(op.in[2], c) : nullptr,
-                   out(op.out[0], c)};
-          oproj_.op = -1;
-          return;  // its output is read by nothing on the host (fuse_oproj_)
-        }
         const int T = static_cast<int>(c.rows(op.in[0]));
         const int64_t K = c.tensor(op.in[1]).cols;
         const size_t n = op.type == OpType::MATMUL_N ? op.out.size() : 1;
@@ -314,7 +277,6 @@ class HipBackend : public Backend {
           norm_ = {idx, in(op.in[0], c), f32_weight(c.tensor(op.in[1])), op.fattr[0]};
           return;  // the next op runs it; its output is read by nothing else
         }
-        EDGELM_CHECK(fold_.op != idx - 1, "hip: RMSNORM of an o projection that has not been folded");
         check(elmh_rmsnorm_dev(ctx_, in(op.in[0], c), f32_weight(c.tensor(op.in[1])), out(op.out[0], c), rows, dim,
                                op.fattr[0]),
               op);
@@ -687,25 +649,6 @@ class HipBackend : public Backend {
     const float* k = in(op.in[1], c);
     const float* v = in(op.in[2], c);
     const int idx = static_cast<int>(&op - c.graph->ops.data());
-    if (prepared_ && oproj_on_ && fuse_oproj_[idx] && T == 1 && c.act_quant) {
-      const Graph& g = *c.graph;
-      elmh_weight* wo = weight(c.tensor(g.ops[idx + 1].in[1]));
-      elmh_weight* wg = weight(c.tensor(g.ops[idx + 3].in[1]));
-      elmh_weight* wu = weight(c.tensor(g.ops[idx + 3].in[2]));
-      const size_t need = elmh_oproj_partials_bytes(wo);
-      if (need > part_cap_ && !capturing_) {  // sized on an eager step, before any capture
-        elmh_free(ctx_, part_);
-        part_ = static_cast<float*>(alloc(need));
-        part_cap_ = need;
-      }
-      if (need <= part_cap_ && elmh_attention_oproj_supported(hd, nh, mc, wo, wg, wu, ELMH_ACT_INT8)) {
-        check(elmh_attention_oproj_dev(ctx_, q, k, v, out(op.out[0], c), c.pos0, capturing_ ? pos_dev_ : nullptr, nh,
-                                       nkv, hd, l.k, l.v, mc, rc, rs, wo, part_),
-              op);
-        oproj_ = {idx + 1, wo, part_};
-        return;
-      }
-    }
     if (prepared_ && fuse_attn_[idx] && !capturing_ && T > 1) {
       attn_ = {idx, q, k, v, out(op.out[0], c), T, c.pos0, nh, nkv, hd, l.k, l.v, mc, rc, rs};
       return;  // the next op (the o projection) runs it
@@ -718,7 +661,6 @@ class HipBackend : public Backend {
 
   bool layer_ops_;
   bool graphs_on_ = true;
-  bool oproj_on_ = true;
   bool capturing_ = false;
   uint64_t buffer_gen_ = 0;
   std::map<int, StepGraph> graphs_;  // by the partition's first op
@@ -746,21 +688,6 @@ class HipBackend : public Backend {
     int mc = 0;
     const float *rc = nullptr, *rs = nullptr;
   } attn_;
-  std::vector<char> fuse_oproj_;  // op index: an ATTENTION forming its o projection's products (decode)
-  struct PendingOproj {
-    int op = -1;  // the o projection whose products the attention call wrote
-    elmh_weight* wo = nullptr;
-    float* part = nullptr;
-  } oproj_;
-  struct PendingFold {
-    int op = -1;  // the o projection, folded by the FFN_SWIGLU two ops on
-    float* part = nullptr;
-    elmh_weight* wo = nullptr;
-    const float* res = nullptr;
-    float* x1 = nullptr;
-  } fold_;
-  float* part_ = nullptr;  // the o projection's products (elmh_oproj_partials_bytes)
-  size_t part_cap_ = 0;
   int output_ = -1;          // graph output when this backend writes it (prepare), else -1
   bool keep_out_ = false;    // keep_output(true): the output is not copied to the host arena
   int32_t* dev_tok_ = nullptr;  // argmax result

@@ -204,30 +204,6 @@ int elmh_attention_step_dev(elmh_ctx* ctx, const float* q, const float* k, const
  * (elmh_scratch_generation). No counterpart in edgelm. */
 int elmh_attention_step_supported(int head_dim, int max_ctx);
 
-/* A decode step's ATTENTION and the MATMUL_ADD (or MATMUL) o projection after it, split differently
- * across two calls so that the o projection needs no launch of its own (no counterpart in edgelm:
- * the same results as elmh_attention_step_dev / elmh_attention_dev, elmh_matmul_dev of the o weight
- * with the residual, and elmh_rmsnorm_swiglu_dev, bit for bit, for int8 activations):
- *  - elmh_attention_oproj_dev runs one token's attention (position *pos_dev when pos_dev is not NULL,
- *    else pos0; head_dim 64), writes out, and also quantizes each head's output (two 32-blocks, edgelm's
- *    rounding) and writes the o projection's per-block products to partials (elmh_oproj_partials_bytes);
- *  - elmh_oproj_rmsnorm_swiglu_dev folds each row's products in block order, applies the o weight's row
- *    scale (q8) and adds residual (may be NULL), which is the o projection's output x1 (written to x1),
- *    then runs RMSNORM(x1, norm_w, eps) and FFN_SWIGLU(wg, wu) into y.
- * elmh_attention_oproj_supported says whether the pair applies to these weights (q8 / q4 o weight of
- * n_heads * 64 columns, an FFN that takes the small GEMV with RMSNORM fused, act ELMH_ACT_INT8) and a
- * cache of max_ctx positions. */
-int elmh_attention_oproj_supported(int head_dim, int n_heads, int max_ctx, const elmh_weight* w_o,
-                                    const elmh_weight* wg, const elmh_weight* wu, int act);
-size_t elmh_oproj_partials_bytes(const elmh_weight* w_o);
-int elmh_attention_oproj_dev(elmh_ctx* ctx, const float* q, const float* k, const float* v, float* out, int pos0,
-                             const int32_t* pos_dev, int n_heads, int n_kv, int head_dim, float* k_cache,
-                             float* v_cache, int max_ctx, const float* rope_cos, const float* rope_sin,
-                             const elmh_weight* w_o, float* partials);
-int elmh_oproj_rmsnorm_swiglu_dev(elmh_ctx* ctx, const float* partials, const elmh_weight* w_o, const float* residual,
-                                  float* x1, const float* norm_w, float eps, const elmh_weight* wg,
-                                  const elmh_weight* wu, float* y, int act, int mode);
-
 /* Greedy sampling: argmax (tokenizer.cpp:187-189, std::max_element) of each row of x [rows, n]
  * (device pointers) into out [rows] (device int32): the first index of the largest value under
  * IEEE <, so NaNs after index 0 are never chosen and a NaN at index 0 is. Lets a caller take the

@@ -432,64 +432,3 @@ def test_argmax_matches_edgelm(ctx):
     assert np.array_equal(bo.download((6,), np.int32), O.argmax(x))
     bx.free()
     bo.free()
-
-
-@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
-@pytest.mark.parametrize("by_dev", [True, False])
-def test_attention_oproj_pair_matches_unfused(ctx, dt, by_dev):
-    """elmh_attention_oproj_dev + elmh_oproj_rmsnorm_swiglu_dev (the decode step's o projection formed by the
-    attention workgroups and folded by the RMSNORM + FFN_SWIGLU call) against the unfused calls they replace:
-    attention (step or positioned), the o projection with its residual through the small GEMV, then RMSNORM +
-    FFN_SWIGLU. Bit-identical attention output, x1, FFN output and KV caches, on SmolLM2 shapes, across
-    positions in and past the first 256-row chunk, and the position from device memory or from the call."""
-    nh, nkv, hd, mc, D, HID = 9, 3, 64, 600, 576, 1536
-    r = np.random.default_rng(1000 + dt + 10 * int(by_dev))
-    tab = O.rope_table(hd, mc, 100000.0)
-    wo = O.make_weight(r.normal(0, 0.05, (D, D)).astype(np.float32), dt)
-    wg = O.make_weight(r.normal(0, 0.05, (HID, D)).astype(np.float32), dt)
-    wu = O.make_weight(r.normal(0, 0.05, (HID, D)).astype(np.float32), dt)
-    dwo, dwg, dwu = (ctx.upload(w.dtype, w.rows, w.cols, w.data, w.scales) for w in (wo, wg, wu))
-    assert ctx.attention_oproj_supported(hd, nh, mc, dwo, dwg, dwu, E.ACT_INT8)
-    assert not ctx.attention_oproj_supported(hd, nh, mc, dwo, dwg, dwu, E.ACT_F32)
-    assert not ctx.attention_oproj_supported(32, nh, mc, dwo, dwg, dwu, E.ACT_INT8)
-    nw = (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
-    kc0 = r.normal(0, 1, (nkv, mc, hd)).astype(np.float32)
-    vc0 = r.normal(0, 1, (nkv, mc, hd)).astype(np.float32)
-    bufs = {n: dev(ctx, a) for n, a in (("kca", kc0), ("vca", vc0), ("kcb", kc0), ("vcb", vc0), ("cos", tab[0]),
-                                         ("sin", tab[1]), ("nw", nw))}
-    bpart = ctx.buffer(ctx.oproj_partials_bytes(dwo))
-    bpos = ctx.buffer(4)
-    for pos in (0, 37, 255, 256, 599):
-        print(f"[gpu] attention+oproj pair dt={dt} by_dev={by_dev} pos={pos}", flush=True)
-        q = r.normal(0, 1, (1, nh * hd)).astype(np.float32)
-        k = r.normal(0, 1, (1, nkv * hd)).astype(np.float32)
-        v = r.normal(0, 1, (1, nkv * hd)).astype(np.float32)
-        res = r.normal(0, 1, (1, D)).astype(np.float32)
-        bq, bk, bv, bres = dev(ctx, q), dev(ctx, k), dev(ctx, v), dev(ctx, res)
-        outs = {n: ctx.buffer(sz * 4) for n, sz in (("oa", nh * hd), ("ob", nh * hd), ("x1a", D), ("x1b", D),
-                                                     ("ya", HID), ("yb", HID))}
-        bpos.upload(np.array([pos], np.int32))
-        # unfused
-        if by_dev:
-            ctx.attention_step_dev(bq.ptr, bk.ptr, bv.ptr, outs["oa"].ptr, bpos.ptr, nh, nkv, hd, bufs["kca"].ptr,
-                                   bufs["vca"].ptr, mc, bufs["cos"].ptr, bufs["sin"].ptr)
-        else:
-            ctx.attention_dev(bq.ptr, bk.ptr, bv.ptr, outs["oa"].ptr, 1, pos, nh, nkv, hd, bufs["kca"].ptr,
-                              bufs["vca"].ptr, mc, bufs["cos"].ptr, bufs["sin"].ptr)
-        ctx.matmul_dev(outs["oa"].ptr, 1, D, [dwo], [outs["x1a"].ptr], [bres.ptr], act=E.ACT_INT8)
-        ctx.rmsnorm_swiglu_dev(outs["x1a"].ptr, bufs["nw"].ptr, 1e-5, 1, D, dwg, dwu, outs["ya"].ptr, act=E.ACT_INT8)
-        # the pair
-        ctx.attention_oproj_dev(bq.ptr, bk.ptr, bv.ptr, outs["ob"].ptr, pos, bpos.ptr if by_dev else None, nh, nkv,
-                                hd, bufs["kcb"].ptr, bufs["vcb"].ptr, mc, bufs["cos"].ptr, bufs["sin"].ptr, dwo,
-                                bpart.ptr)
-        ctx.oproj_rmsnorm_swiglu_dev(bpart.ptr, dwo, bres.ptr, outs["x1b"].ptr, bufs["nw"].ptr, 1e-5, dwg, dwu,
-                                     outs["yb"].ptr, act=E.ACT_INT8)
-        for a_, b_, n_ in (("oa", "ob", nh * hd), ("x1a", "x1b", D), ("ya", "yb", HID)):
-            ga, gb = outs[a_].download((n_,), np.float32), outs[b_].download((n_,), np.float32)
-            assert bits_equal(ga, gb), f"{a_} pos={pos}: max diff {np.abs(ga - gb).max()}"
-        for b in [bq, bk, bv, bres] + list(outs.values()):
-            b.free()
-    for a_, b_ in (("kca", "kcb"), ("vca", "vcb")):
-        assert bits_equal(bufs[a_].download(kc0.shape, np.float32), bufs[b_].download(kc0.shape, np.float32))
-    for b in list(bufs.values()) + [bpart, bpos, dwo, dwg, dwu]:
-        b.free()
