@@ -1059,7 +1059,72 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
 
   // per-token scales of the tile's tokens (the per-token mode's epilogue reads them from LDS)
   if (TOK && tid < TT) Lxdt[tid] = a.xd[t0 + tid];
-  if constexpr (R::KB == 1) {
+  if constexpr (WV == 8 && WDT == WQ4) {
+    // Eight waves, q4, edgelm's per-block rescale, pipelined by one block (block j in slot j % D): step b
+    // starts block b's MFMAs from operands read in step b - 1, reads block b's token scales from its
+    // slot, then block b + 1's operands, and rescales while those reads are in flight. Slot (b - 1) % D
+    // is refilled with block b + D - 1 after the barrier at the top of step b, when no wave reads it
+    // any more; block b + 1 has landed once at most D - 3 blocks are in flight. Measured at T = 512
+    // against the loop below: q4 4096 x 4096 60.4 -> 57.8 us, 4096 x 14336 174.0 -> 162.4 us; q8 lost
+    // (48.0 -> 51.7, 127.4 -> 146.4 us), and prefetching the 16 token scales as well spilled or lost.
+    static_assert(D >= 4, "ring too shallow for the eight-wave pipeline");
+    auto read_ops = [&](v4i (&A)[MT], v4i& B, float& c, int blk) {
+      const unsigned char* sb = ring + (blk % D) * R::SLOT;
+      const unsigned char* wb = sb + R::ACT;
+      const int rl = wr * 64 + nt0 * 32 + l32;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) A[mt] = *reinterpret_cast<const v4i*>(sb + ((wt * MT + mt) * 64 + lane) * 16);
+      c = 1.f;
+      if (WDT == WQ8) {
+        B = *reinterpret_cast<const v4i*>(wb + (2 * rl + (h ^ ((rl >> 3) & 1))) * 16);
+      } else {
+        B = q4_operand16(*reinterpret_cast<const uint4*>(wb + rl * 16), h);
+        c = reinterpret_cast<const float*>(wb + 2048)[rl];
+      }
+    };
+    auto step = [&](v4i (&A)[MT], v4i& B, float& c, v4i (&A2)[MT], v4i& B2, float& c2, int b) {
+      wait_vm<(D - 3) * R::P>();  // block b + 1 has landed (this wave's part)
+      lds_barrier();              // every wave's part; every wave is done with block b - 1
+      issue(b + D - 1, (b + D - 1) % D);
+      v16i S[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) S[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[mt], B, zero, 0, 0, 0);
+      const float* xs = reinterpret_cast<const float*>(ring + (b % D) * R::SLOT + R::ACT + R::WSEL);
+      float4 x4[MT][4];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) x4[mt][g] = *reinterpret_cast<const float4*>(&xs[wt * 32 * MT + mt * 32 + 8 * g + 4 * h]);
+      read_ops(A2, B2, c2, b + 1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float4 v = x4[mt][i >> 2];
+          const float xd = (i & 3) == 0 ? v.x : (i & 3) == 1 ? v.y : (i & 3) == 2 ? v.z : v.w;
+          // as block(): q8 p = float(S) * xd; q4 p = float(S) * (c * xd), 16 times edgelm's product
+          const float m = WDT == WQ8 ? xd : c * xd;
+          if (FAST) {
+            facc[0][mt][0][i] = __builtin_fmaf((float)S[mt][i], m, facc[0][mt][0][i]);
+          } else {
+            facc[0][mt][0][i] = facc[0][mt][0][i] + (float)S[mt][i] * m;
+          }
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < D - 1; ++i) issue(i, i);
+    wait_vm<(D - 2) * R::P>();  // block 0 has landed
+    lds_barrier();
+    v4i A0[MT], B0, A1[MT], B1;
+    float c0, c1;
+    read_ops(A0, B0, c0, 0);
+    int b = 0;
+    for (; b + 1 < nb; b += 2) {
+      step(A0, B0, c0, A1, B1, c1, b);
+      step(A1, B1, c1, A0, B0, c0, b + 1);
+    }
+    if (b < nb) step(A0, B0, c0, A1, B1, c1, b);  // reads block nb's slot (a repeat of the last block)
+  } else if constexpr (R::KB == 1) {
 #pragma unroll
     for (int i = 0; i < D - 1; ++i) issue(i, i);
     int cs = 0, is = D - 1;  // slot to compute, slot to fill
@@ -2471,15 +2536,17 @@ static void gemm_launch(const GemmArgs& a, dim3 grid, hipStream_t s) {
     gemm_a8_kernel<WDT, SW, TOK, false, MT, 0, WV><<<grid, 64 * WV, 0, s>>>(a);
 }
 
-// The ring GEMM with four or eight waves (eight: block-scale modes without SwiGLU, where the grid
-// gives at most one workgroup per CU, so that four waves would leave one wave per SIMD; measured at
-// T = 512: q8 4096 x 4096 59.2 -> 48.3 us, 4096 x 14336 173.4 -> 133.4 us, while 14336 x 4096 with
-// 448 workgroups went from 98.8 to 103.7 us; ELMH_GEMM_WAVES=4 or 8 forces one, same bits).
+// The ring GEMM with four or eight waves (eight: block-scale modes without SwiGLU; q8 where the grid
+// gives at most one workgroup per CU, so that four waves would leave one wave per SIMD, q4 always).
+// Measured at T = 512: q8 4096 x 4096 59.2 -> 48.3 us, 4096 x 14336 173.4 -> 133.4 us, while 14336 x
+// 4096 with 448 workgroups went from 98.8 to 103.7 us; q4 (pipelined eight-wave loop) 78.0 -> 60.6,
+// 228.7 -> 160.7 and, at 448 workgroups, 125.8 -> 120.2 us. ELMH_GEMM_WAVES=4 or 8 forces one, same
+// bits.
 template <int WDT, bool SW, bool TOK, int MT>
 static void gemm_launch_waves(const GemmArgs& a, int wgs, int cus, hipStream_t s) {
   const dim3 grid((wgs + 7) / 8 * 8);
   if constexpr (!TOK && !SW) {
-    bool eight = wgs <= cus;
+    bool eight = WDT == WQ4 || wgs <= cus;
     if (const char* ev = getenv("ELMH_GEMM_WAVES")) eight = ev[0] == '8' ? true : ev[0] == '4' ? false : eight;
     if (eight) return gemm_launch<WDT, SW, TOK, MT, 8>(a, grid, s);
   }
