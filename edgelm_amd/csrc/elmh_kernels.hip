@@ -452,21 +452,16 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   const int per_sel = H * nb, items = (SW ? 2 : 1) * per_sel;
   const int nel = T * K;
 
-  // 1. activation values (first: their wait does not cover the weight loads issued next); with
-  // NORM every pass's values and norm weights (loads past the end repeat the last float4)
+  // 1. every pass's activation values (first: their wait does not cover the weight loads issued
+  // next; loads past the end repeat the last float4), with NORM also the norm weights
   const int e0 = tid * 4;
-  constexpr int XP = NORM ? kSmallMaxAct / kSmallPass : 1;
-  float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f);
+  constexpr int XP = kSmallMaxAct / kSmallPass;
   float4 xv[XP], nv[XP];
-  if (NORM) {
 #pragma unroll
-    for (int p = 0; p < XP; ++p) {
-      const int e = min(p * kSmallPass + e0, nel - 4);
-      xv[p] = *reinterpret_cast<const float4*>(a.x + e);
-      nv[p] = *reinterpret_cast<const float4*>(a.nw + (e - e / K * K));
-    }
-  } else if (e0 < nel) {
-    x0 = *reinterpret_cast<const float4*>(a.x + e0);
+  for (int p = 0; p < XP; ++p) {
+    const int e = min(p * kSmallPass + e0, nel - 4);
+    xv[p] = *reinterpret_cast<const float4*>(a.x + e);  // unconditional: keeps the wait counts exact
+    if (NORM) nv[p] = *reinterpret_cast<const float4*>(a.nw + (e - e / K * K));
   }
   // 2. weights of this thread's first two items
   v4u w[2][G / 16];
@@ -549,20 +544,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
       }
     }
   };
-  if (NORM) {
 #pragma unroll
-    for (int p = 0; p < XP; ++p)
-      if (p * kSmallPass < nel) quantize(p * kSmallPass + e0, xv[p]);
-  } else {
-    for (int pass = 0; pass * kSmallPass < nel; ++pass) {
-      const int e = pass * kSmallPass + e0;
-      if (pass > 0) {
-        x0 = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (e < nel) x0 = *reinterpret_cast<const float4*>(a.x + e);
-      }
-      quantize(e, x0);
-    }
-  }
+  for (int p = 0; p < XP; ++p)
+    if (p * kSmallPass < nel) quantize(p * kSmallPass + e0, xv[p]);
   __syncthreads();
 
   // 5. products
