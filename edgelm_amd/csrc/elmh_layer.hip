@@ -598,13 +598,14 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
   const float* const vs = vnew + kvh * HD;
   const float qa = qs[ih], qz = qs[ih + H2], ka = ks[ih], kz = ks[ih + H2], va = vs[ih], vz = vs[ih + H2];
   const float vlast = vs[lane];
-  // key rows [0, R0): wave w moves 1 KB pieces w, w + 4, ... (4 rows each, lane -> row lane / 16,
-  // slot lane % 16); rows past R0 - 1 repeat it
-  const int R0 = min(C, max_ctx);
+  // key rows [0, CS) before the position is known: wave w moves 1 KB pieces w, w + 4, ... (4 rows
+  // each, lane -> row lane / 16, slot lane % 16); rows past RS - 1 repeat it
+  constexpr int CS = C / 2;
+  const int RS = min(CS, max_ctx);
 #pragma unroll
-  for (int i = 0; i < C / 16; ++i) {
+  for (int i = 0; i < CS / 16; ++i) {
     const int pc = wave + 4 * i, r = 4 * pc + (lane >> 4), s = lane & 15;
-    dma16s(kh, (uint32_t)(min(r, R0 - 1) * ROWB + ((s ^ (r & 15)) << 4)), kb_lds + pc * 1024);
+    dma16s(kh, (uint32_t)(min(r, RS - 1) * ROWB + ((s ^ (r & 15)) << 4)), kb_lds + pc * 1024);
   }
   __builtin_amdgcn_sched_barrier(0);
   // the caller keeps the position in range; stay in bounds anyway
@@ -613,6 +614,13 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
   if (rcos) {
     cr = rcos[(int64_t)pos * H2 + ih];
     sr = rsin[(int64_t)pos * H2 + ih];
+  }
+  // the first chunk's other cache rows, [CS, min(C, pos)), now that the position is known (the
+  // last piece repeats row min(C, pos) - 1)
+  const int n = pos + 1, nc = n - 1, rk = min(C, nc);
+  for (int pc = CS / 4 + wave; 4 * pc < rk; pc += 4) {
+    const int r = 4 * pc + (lane >> 4), s = lane & 15;
+    dma16s(kh, (uint32_t)(min(r, rk - 1) * ROWB + ((s ^ (r & 15)) << 4)), kb_lds + pc * 1024);
   }
   wait_vm<0>();  // the keys, q, k, v and the rotation's cos / sin
   if (tid < H2) {
@@ -632,13 +640,6 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
       vd[tid + H2] = vz;
     }
   }
-  // value rows [0, R0), unswizzled: lane i of wave 0 reads element i of a row
-#pragma unroll
-  for (int i = 0; i < C / 16; ++i) {
-    const int pc = wave + 4 * i, r = 4 * pc + (lane >> 4);
-    dma16s(vh, (uint32_t)(min(r, R0 - 1) * ROWB + ((lane & 15) << 4)), vb_lds + pc * 1024);
-  }
-  const int n = pos + 1, nc = n - 1;
   lds_barrier();  // keys (every wave waited for its own), q and the step's key in LDS
 
   // scores: thread j takes row j of each chunk of C positions; the cache rows are 0 .. n - 2
@@ -675,6 +676,14 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
     float sum = 0.f;
     for (int g0 = 0; g0 < n16; g0 += 256) sum = ordered_sum256(sc + g0, min(16, (n16 - g0) >> 4), sum);
     if (lane == 0) inv_s = 1.0f / sum;
+  } else {
+    // meanwhile waves 1-3 request the first chunk's value rows [0, min(C, n - 1)) into the value
+    // buffer (unswizzled: lane i of wave 0 reads element i of a row; the last piece repeats the
+    // last row): the key buffer may still hold the last key chunk, the value buffer is unused
+    for (int pc = wave - 1; 4 * pc < rk; pc += 3) {
+      const int r = 4 * pc + (lane >> 4);
+      dma16s(vh, (uint32_t)(min(r, rk - 1) * ROWB + ((lane & 15) << 4)), vb_lds + pc * 1024);
+    }
   }
   __syncthreads();
   const float inv = inv_s;
