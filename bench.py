@@ -245,18 +245,23 @@ def sweep_8b(ctx, E, reps=10, eager=False):
     ctx.reserve(4, 14336)
     total = sum(q_bytes(2, w.rows, w.cols) for w in W.values())
 
+    # h of the FFN, quantized by the SwiGLU launch for the down projection (edgelm quantizes the
+    # down projection's input once, as cpu::matmul's quantize_act_row)
+    hq, hd, hs = ctx.buffer(14336), ctx.buffer(448 * 4), ctx.buffer(448 * 4)
+
     def sweep():
         for l in range(8):
             ctx.matmul_dev(bx.ptr, 1, 4096, [W[f"{l}.q"], W[f"{l}.k"], W[f"{l}.v"]],
                            [by[0].ptr, by[1].ptr, by[2].ptr], act=E.ACT_INT8)
-            ctx.swiglu_dev(bx.ptr, 1, 4096, W[f"{l}.g"], W[f"{l}.u"], by[0].ptr, act=E.ACT_INT8)
-            ctx.matmul_dev(bx.ptr, 1, 14336, [W[f"{l}.d"]], [by[1].ptr], act=E.ACT_INT8)
+            ctx.swiglu_quant_dev(bx.ptr, 1, 4096, W[f"{l}.g"], W[f"{l}.u"], by[0].ptr, hq.ptr, hd.ptr, hs.ptr)
+            ctx.gemv_a8_dev(hq.ptr, hd.ptr, hs.ptr, 1, 14336, [W[f"{l}.d"]], [by[1].ptr])
 
     ms = (time_eager if eager else time_graph)(ctx, sweep, reps)
     gbs = total / (ms * 1e-3) / 1e9
     log(f"8B sweep {ms * 1e3:.1f} us for {total / 1e9:.3f} GB -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of peak)")
     # each op type alone over the 8 layers (includes the activation quantization: inside the GEMV
-    # for K = 4096, a separate launch before it for the down GEMV's K = 14336)
+    # for K = 4096; for the down GEMV's K = 14336 either in the SwiGLU launch before it, as the sweep
+    # runs it, or, for MATMUL down on an f32 activation, a separate launch before it)
     per_op = {}
     ops8 = {
         "MATMUL_N qkv 6144x4096": (lambda l: ctx.matmul_dev(bx.ptr, 1, 4096, [W[f"{l}.q"], W[f"{l}.k"], W[f"{l}.v"]],
@@ -264,6 +269,9 @@ def sweep_8b(ctx, E, reps=10, eager=False):
                                    sum(q_bytes(2, W[f"0.{n}"].rows, 4096) for n in "qkv")),
         "FFN_SWIGLU 2x14336x4096": (lambda l: ctx.swiglu_dev(bx.ptr, 1, 4096, W[f"{l}.g"], W[f"{l}.u"], by[0].ptr,
                                                              act=E.ACT_INT8), 2 * q_bytes(2, 14336, 4096)),
+        "FFN_SWIGLU 2x14336x4096 + quantized h": (
+            lambda l: ctx.swiglu_quant_dev(bx.ptr, 1, 4096, W[f"{l}.g"], W[f"{l}.u"], by[0].ptr, hq.ptr, hd.ptr,
+                                           hs.ptr), 2 * q_bytes(2, 14336, 4096)),
         "MATMUL down 4096x14336": (lambda l: ctx.matmul_dev(bx.ptr, 1, 14336, [W[f"{l}.d"]], [by[1].ptr], act=E.ACT_INT8),
                                    q_bytes(2, 4096, 14336)),
     }
@@ -284,7 +292,7 @@ def sweep_8b(ctx, E, reps=10, eager=False):
     dbytes = q_bytes(2, 4096, 14336) + 14336 + 448 * 8 + 4096 * 4
     dgbs = dbytes / (dms * 1e-3) / 1e9
     log(f"8B down GEMV {dms * 1e3:.2f} us -> {dgbs:.0f} GB/s")
-    for b in [bx, q, d, s] + by:
+    for b in [bx, q, d, s, hq, hd, hs] + by:
         b.free()
     m.free()
     return {"sweep_us": ms * 1e3, "bytes": total, "GBs": gbs, "frac_of_peak": gbs / HBM_PEAK_GBS, "per_op": per_op,

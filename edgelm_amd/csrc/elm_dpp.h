@@ -35,4 +35,15 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// Integer sum over the 64 lanes of the wave (every lane active); the result is wave-uniform (an
+// integer sum does not depend on its order).
+__device__ __forceinline__ int wave_sum_i(int v) {
+  v += dpp_i<kDppQuadXor1>(v);
+  v += dpp_i<kDppQuadXor2>(v);
+  v += dpp_i<kDppHalfMirror>(v);
+  v += dpp_i<kDppRowMirror>(v);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+         __builtin_amdgcn_readlane(v, 48);
+}
+
 }  // namespace elmh

@@ -25,6 +25,8 @@ inline int stream_producers(int nb) {
 // 8B down GEMV's K = 14336 (57 KB of f32 per workgroup) costs more than a separate quantizer
 // launch whose int8 result the workgroups copy (measured: 16.4 vs 11.6 us per call).
 constexpr int kStreamQinPasses = 8;
+// Producer waves of the streaming SwiGLU that also quantizes its output (32-row workgroups)
+constexpr int kStreamQoutWaves = 8;
 inline bool stream_qin_ok(int T, int K) {
   return K % kBlock == 0 && K / kBlock <= kStreamFoldWaveBlocks &&
          T * K <= kStreamQinPasses * 4 * stream_producers(K / kBlock);
@@ -81,6 +83,12 @@ struct GemvArgs {
   const float* xd;    // f32 [T][nb]
   const int32_t* xs;  // int32 [T][nb] block sums of q
   int T, K, nb;
+  // SwiGLU on the streaming kernel, one token, 32-row workgroups: the output row also quantized
+  // (row-major int8 [N], block scales and block sums [N / 32], as the activation quantizer writes
+  // them), or null
+  int8_t* oq;
+  float* od;
+  int32_t* os;
 };
 
 struct GemmTarget {

@@ -331,9 +331,14 @@ __device__ __forceinline__ int fold_lanes(int T, int R) {
 // Last phase of the small GEMV (and of the streaming GEMV without a fold wave): each fold lane
 // sums its chain's row of products (the workgroup's R rows start at weight row n0, of which
 // `rows` are real) and applies the epilogue. e_res and e_s come from chain_epilogue_operands.
-template <int WDT, int NT, bool SW>
+// QOUT (SwiGLU, one token, R = 32, n0 a multiple of 32: the fold lanes are wave 0 and its gate
+// lanes hold one 32-block of the output row): the block is also quantized as the activation
+// quantizer does it (quantize_act_row, kernels_ref.cpp:23-37: the amax, s = amax / 127, each value's
+// rounding that of its division, the block sum of q), for the next GEMV to take pre-quantized.
+template <int WDT, int NT, bool SW, bool QOUT = false>
 __device__ __forceinline__ void gemv_fold(const GemvArgs& a, const GemvLds& L, const GemvTarget& tg, int n0, int R,
                                           int rows, int tid, float e_res, float e_s) {
+  static_assert(!QOUT || SW, "quantized output: SwiGLU only");
   if ((tid & ~63) >= fold_lanes<SW>(a.T, R)) return;  // whole waves only: the swap needs every lane
   int sel, pr;
   fold_lane<SW>(tid, sel, pr);
@@ -343,7 +348,23 @@ __device__ __forceinline__ void gemv_fold(const GemvArgs& a, const GemvLds& L, c
   if (WDT == WQ8) v = v * e_s;
   if (SW) {
     const float up = row_swap8(v);
-    if (live && sel == 0) tg.y[(int64_t)ft * tg.N + fn] = silu_exact(v) * up;
+    const float hv = silu_exact(v) * up;
+    const bool mine = live && sel == 0;
+    if (mine) tg.y[(int64_t)ft * tg.N + fn] = hv;
+    if (QOUT && a.oq) {  // uniform; every lane of wave 0 runs the reductions
+      const float am = wave_max(mine ? fabsf(hv) : 0.f);
+      const float d = am / 127.0f;
+      int q;
+      elm_q8_group<1>(&hv, d == 0.f ? 1.f : d, &q);
+      const int sm = wave_sum_i(mine ? q : 0);
+      if (mine) {
+        a.oq[fn] = (int8_t)q;
+        if (fr == 0) {
+          a.od[fn / kBlock] = d;
+          a.os[fn / kBlock] = sm;
+        }
+      }
+    }
   } else if (live) {
     tg.y[(int64_t)ft * tg.N + fn] = tg.res ? v + e_res : v;
   }
@@ -612,8 +633,9 @@ __device__ __forceinline__ float fold_range(float acc, const float* row, int b0,
 // only the last batch's share is left once the last weight has arrived. Without the fold wave
 // (FW false: short rows, where the extra wave costs more than the chain) the producers fold at
 // the end, one lane per (token, row).
-template <int WDT, int NT, bool SW, int IPT, int NPW, int DEPTH, bool FW, bool QIN>
+template <int WDT, int NT, bool SW, int IPT, int NPW, int DEPTH, bool FW, bool QIN, bool QOUT = false>
 __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const GemvArgs a) {
+  static_assert(!QOUT || (SW && !FW && NT == 1), "quantized output: SwiGLU, one token, folds at the end");
   constexpr int P = 64 * NPW;  // producer threads
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int G = WDT == WQ8 ? 32 : 16;
@@ -821,7 +843,7 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
   if (!FW) {
     // 5. one lane per row chain folds its row in block order and applies the epilogue
     __syncthreads();
-    gemv_fold<WDT, NT, SW>(a, L, tg, tile0 * H, R, rows, tid, e_res, e_s);
+    gemv_fold<WDT, NT, SW, QOUT>(a, L, tg, tile0 * H, R, rows, tid, e_res, e_s);
   }
 }
 
@@ -2449,15 +2471,15 @@ int gemv_stream_ipt(int dtype, int items, int producers) {
   return per <= 4 ? 4 : per <= 8 ? 8 : 16;
 }
 
-template <int WDT, int NT, bool SW, int NPW, bool FW, bool QIN>
+template <int WDT, int NT, bool SW, int NPW, bool FW, bool QIN, bool QOUT = false>
 static hipError_t stream_launch(const GemvArgs& a, int wgs, size_t lds, int items, hipStream_t s) {
   constexpr int threads = 64 * (NPW + FW);
   switch (gemv_stream_ipt(WDT, items, 64 * NPW)) {
-    case 4: gemv_stream_kernel<WDT, NT, SW, 4, NPW, FW ? 2 : 4, FW, QIN><<<wgs, threads, lds, s>>>(a); break;
-    case 8: gemv_stream_kernel<WDT, NT, SW, 8, NPW, FW ? 2 : 4, FW, QIN><<<wgs, threads, lds, s>>>(a); break;
+    case 4: gemv_stream_kernel<WDT, NT, SW, 4, NPW, FW ? 2 : 4, FW, QIN, QOUT><<<wgs, threads, lds, s>>>(a); break;
+    case 8: gemv_stream_kernel<WDT, NT, SW, 8, NPW, FW ? 2 : 4, FW, QIN, QOUT><<<wgs, threads, lds, s>>>(a); break;
     case 16:
       if (WDT == WQ4) {
-        gemv_stream_kernel<WDT, NT, SW, 16, NPW, FW ? 2 : 4, FW, QIN><<<wgs, threads, lds, s>>>(a);
+        gemv_stream_kernel<WDT, NT, SW, 16, NPW, FW ? 2 : 4, FW, QIN, QOUT><<<wgs, threads, lds, s>>>(a);
         break;
       }
       return hipErrorInvalidValue;
@@ -2493,6 +2515,17 @@ static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
   if (a.tpw < 1 || a.T * a.tpw * a.H > kStreamFoldLanes || a.T * a.K > kStreamMaxAct || (a.K & 15) ||
       (a.H & (a.H - 1)) || a.H > 64 || a.tpw * a.nb > 4096 || (a.x && !stream_qin_ok(a.T, a.K)) || a.nw)
     return hipErrorInvalidValue;
+  if (SW && a.T == 1 && a.x && a.tpw * a.H == 32) {
+    // SwiGLU, one token, x quantized per workgroup, short rows (the fold at the end): 32-row
+    // workgroups of kStreamQoutWaves producer waves, the output row also quantized in the fold when
+    // oq is set
+    if constexpr (SW && NT == 1) {
+      if (a.nb > kStreamFoldWaveBlocks || (a.oq && (!a.od || !a.os || (a.tg[0].N & 31)))) return hipErrorInvalidValue;
+      return stream_launch<WDT, 1, true, kStreamQoutWaves, false, true, true>(a, tiles, lds, 2 * 32 * a.nb, s);
+    } else {
+      return hipErrorInvalidValue;
+    }
+  }
   const int items = (SW ? 2 : 1) * a.tpw * a.H * a.nb;
   if (a.nb > kStreamFoldWaveBlocks) return stream_go<WDT, NT, SW, kStreamWavesLong, true>(a, tiles, lds, items, s);
   return stream_go<WDT, NT, SW, kStreamWavesShort, false>(a, tiles, lds, items, s);

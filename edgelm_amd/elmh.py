@@ -238,6 +238,12 @@ class Context:
         self._check(lib().elmh_swiglu_dev(self.h, C.c_void_p(x_ptr), C.c_int(T), C.c_int64(K), wg.h, wu.h,
                                           C.c_void_p(y_ptr), C.c_int(act), C.c_int(mode)))
 
+    def swiglu_quant_dev(self, x_ptr, T, K, wg, wu, y_ptr, q_ptr, d_ptr, s_ptr):
+        """FFN_SWIGLU (int8 activations, exact) into y, and y quantized as quantize_act_dev would (q, d, s)."""
+        self._check(lib().elmh_swiglu_quant_dev(self.h, C.c_void_p(x_ptr), C.c_int(T), C.c_int64(K), wg.h, wu.h,
+                                                C.c_void_p(y_ptr), C.c_void_p(q_ptr), C.c_void_p(d_ptr),
+                                                C.c_void_p(s_ptr)))
+
     def quantize_act_dev(self, x_ptr, T, K, q_ptr, d_ptr, s_ptr):
         self._check(lib().elmh_quantize_act_dev(self.h, C.c_void_p(x_ptr), C.c_int(T), C.c_int64(K), C.c_void_p(q_ptr),
                                                 C.c_void_p(d_ptr), C.c_void_p(s_ptr)))

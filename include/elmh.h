@@ -138,6 +138,16 @@ int elmh_matmul_noalloc_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, int
 int elmh_quantize_act_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, int8_t* q, float* d, int32_t* s);
 int elmh_gemv_a8_dev(elmh_ctx* ctx, const int8_t* q, const float* d, const int32_t* s, int T, int64_t K,
                      int n_targets, elmh_weight* const* w, float* const* y, const float* const* residual);
+/* FFN_SWIGLU (int8 activations, exact mode) whose output row also comes back quantized for the next
+ * int8 GEMV: y as elmh_swiglu_dev(x, T, K, wg, wu, y, ELMH_ACT_INT8, ELMH_EXACT) writes it, and q / d / s
+ * as elmh_quantize_act_dev(y, T, N, q, d, s) then writes them (N = rows of wg, a multiple of 32), bit for
+ * bit. The pair FFN_SWIGLU -> MATMUL_ADD down of a layer (passes.cpp:100-104) quantizes h once between
+ * them (cpu::matmul's quantize_act_row of its input, kernels_cpu.cpp:339-377); where the streaming
+ * GEMV runs the SwiGLU (one token, long weights), each workgroup owns whole 32-blocks of h and
+ * quantizes them in its epilogue, so no quantizer launch runs; elsewhere the call launches it after
+ * the SwiGLU. Pass q / d / s to elmh_gemv_a8_dev for the down projection. */
+int elmh_swiglu_quant_dev(elmh_ctx* ctx, const float* x, int T, int64_t K, const elmh_weight* wg,
+                          const elmh_weight* wu, float* y, int8_t* q, float* d, int32_t* s);
 
 /* ---- the rest of a layer on the device (device pointers, asynchronous on the context stream) ----
  * Same float operations in the same order as edgelm's cpu backend, so results are bit-identical.

@@ -559,3 +559,49 @@ def test_rmsnorm_fused_into_matmul(ctx, dt):
         assert bits_equal(by.download((T, N), np.float32), O.cpu_swiglu(xn, wg, wu, act_quant=True)), f"T={T} K={K}"
         for b in (bx, bnw, bres, by, by2, dw, dw2, dg, du):
             b.free()
+
+
+# (dt, N, K, T): the streaming SwiGLU quantizing its own output (q4 at K = 4096, the 8B shape among
+# them; q8 at K = 2048 with more than 4 MB of weights), and calls that take the SwiGLU and then the
+# quantizer launch (two tokens; the small GEMV)
+SWQ_CASES = [(O.Q4, 320, 4096, 1), (O.Q4, 14336, 4096, 1), (O.Q8, 1024, 2048, 1), (O.Q4, 320, 4096, 2),
+             (O.Q8, 1536, 576, 1)]
+
+
+@pytest.mark.parametrize("case", SWQ_CASES)
+def test_swiglu_quant_exact(ctx, case):
+    """elmh_swiglu_quant_dev: y bit-identical to edgelm's cpu::swiglu with int8 activations, and q / d / s
+    to quantize_act_row of that y (the down projection's input), block sums included."""
+    dt, n, k, T = case
+    r = rng(500 + n + k + dt + T)
+    wg, wu = weight(r, n, k, dt), weight(r, n, k, dt)
+    dg, du = up(ctx, wg), up(ctx, wu)
+    x = r.normal(0, 1, (T, k)).astype(np.float32)
+    bx, by, bq, bd, bs = (ctx.buffer(T * k * 4), ctx.buffer(T * n * 4), ctx.buffer(T * n), ctx.buffer(T * n // 8),
+                          ctx.buffer(T * n // 8))
+    bx.upload(x)
+    print(f"[gpu] swiglu_quant dt={dt} {n}x{k} T={T}", flush=True)
+    ctx.swiglu_quant_dev(bx.ptr, T, k, dg, du, by.ptr, bq.ptr, bd.ptr, bs.ptr)
+    ctx.synchronize()
+    y = by.download((T, n), np.float32)
+    q = bq.download((T, n), np.int8)
+    d = bd.download((T, n // 32), np.float32)
+    s = bs.download((T, n // 32), np.int32)
+    want = O.cpu_swiglu(x, wg, wu, act_quant=True)
+    assert bits_equal(y, want)
+    qw, dw = O.quantize_act(want)
+    assert np.array_equal(q, qw) and bits_equal(d, dw)
+    assert np.array_equal(s, qw.reshape(T, n // 32, 32).astype(np.int32).sum(-1))
+    for b in (bx, by, bq, bd, bs, dg, du):
+        b.free()
+
+
+def test_swiglu_quant_refuses_partial_blocks(ctx):
+    r = rng(77)
+    wg, wu = weight(r, 40, 4096, O.Q4), weight(r, 40, 4096, O.Q4)
+    dg, du = up(ctx, wg), up(ctx, wu)
+    bufs = [ctx.buffer(4096 * 4), ctx.buffer(40 * 4), ctx.buffer(64), ctx.buffer(8), ctx.buffer(8)]
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        ctx.swiglu_quant_dev(bufs[0].ptr, 1, 4096, dg, du, *[b.ptr for b in bufs[1:]])
+    for b in bufs + [dg, du]:
+        b.free()
