@@ -245,16 +245,16 @@ def sweep_8b(ctx, E, reps=10, eager=False):
     ctx.reserve(4, 14336)
     total = sum(q_bytes(2, w.rows, w.cols) for w in W.values())
 
-    # h of the FFN, quantized by the SwiGLU launch for the down projection (edgelm quantizes the
-    # down projection's input once, as cpu::matmul's quantize_act_row)
+    # the FFN pair as the hip backend runs it (elmh_ffn_dev): FFN_SWIGLU into h, whose launch also
+    # quantizes h (edgelm quantizes the down projection's input once, cpu::matmul's quantize_act_row),
+    # then the down GEMV on the quantized h
     hq, hd, hs = ctx.buffer(14336), ctx.buffer(448 * 4), ctx.buffer(448 * 4)
 
     def sweep():
         for l in range(8):
             ctx.matmul_dev(bx.ptr, 1, 4096, [W[f"{l}.q"], W[f"{l}.k"], W[f"{l}.v"]],
                            [by[0].ptr, by[1].ptr, by[2].ptr], act=E.ACT_INT8)
-            ctx.swiglu_quant_dev(bx.ptr, 1, 4096, W[f"{l}.g"], W[f"{l}.u"], by[0].ptr, hq.ptr, hd.ptr, hs.ptr)
-            ctx.gemv_a8_dev(hq.ptr, hd.ptr, hs.ptr, 1, 14336, [W[f"{l}.d"]], [by[1].ptr])
+            ctx.ffn_dev(bx.ptr, 1, 4096, W[f"{l}.g"], W[f"{l}.u"], by[0].ptr, W[f"{l}.d"], by[1].ptr)
 
     ms = (time_eager if eager else time_graph)(ctx, sweep, reps)
     gbs = total / (ms * 1e-3) / 1e9

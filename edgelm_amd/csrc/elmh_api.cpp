@@ -56,12 +56,16 @@ struct elmh_ctx {
   DevBuf nrm;
   // attention score rows longer than LDS holds
   DevBuf asc;
+  // FFN pairs (elmh_ffn_dev): h quantized by the SwiGLU launch for the down projection
+  DevBuf hq, hd, hs;
   // bumped whenever a scratch buffer above moves (a graph captured before then holds stale addresses)
   uint64_t scratch_gen = 0;
   // this device's copy of the no-allocation scratch array
   unsigned char* noalloc = nullptr;
   // whether the last elmh_attention_matmul_dev call had the attention kernel write the GEMM's operand
   int attn_fused = 0;
+  // whether the last elmh_ffn_dev call had the SwiGLU launch quantize h for the down projection
+  int ffn_fused = 0;
   // the one-row argmax's per-workgroup posts and counter (the counter zero between launches)
   void* argmax_scratch = nullptr;
 };
@@ -702,7 +706,7 @@ void elmh_destroy(elmh_ctx* c) {
   if (!c) return;
   DeviceGuard g(c);
   (void)hipStreamSynchronize(c->stream);
-  for (DevBuf* b : {&c->x, &c->y, &c->res, &c->xq, &c->xd, &c->xs, &c->gu, &c->nrm, &c->asc})
+  for (DevBuf* b : {&c->x, &c->y, &c->res, &c->xq, &c->xd, &c->xs, &c->gu, &c->nrm, &c->asc, &c->hq, &c->hd, &c->hs})
     if (b->p) (void)hipFree(b->p);
   if (c->argmax_scratch) (void)hipFree(c->argmax_scratch);
   (void)hipStreamDestroy(c->stream);
@@ -923,21 +927,65 @@ int elmh_rmsnorm_matmul_dev(elmh_ctx* c, const float* x, const float* norm_w, fl
   return run_matmul(c, xn, T, K, n, w, y, res, act, mode);
 }
 
+// RMSNORM then FFN_SWIGLU: RMSNORM inside the SwiGLU's launch where that kernel path normalizes rows
+// itself, else into scratch first
+int run_rmsnorm_swiglu(elmh_ctx* c, const float* x, const float* norm_w, float eps, int T, int64_t K,
+                       const elmh_weight* wg, const elmh_weight* wu, float* y, int act, int mode, QuantOut* qo = nullptr) {
+  const elmh_weight* const ws[2] = {wg, wu};
+  if (wg->w.dtype == wu->w.dtype && wg->w.H == wu->w.H && wg->w.rows == wu->w.rows && wg->w.cols == K &&
+      wu->w.cols == K &&
+      (norm_fusable(T, K, 2, ws, 2, act) || norm_gemm(T, K, 2, ws, 2, act) || f32_norm_fusable(T, K, 2, ws, 2, act)))
+    return run_swiglu(c, x, T, K, wg, wu, y, act, mode, norm_w, eps, qo);
+  const float* xn;
+  int rc;
+  if ((rc = norm_to_scratch(c, x, norm_w, eps, T, K, &xn))) return rc;
+  return run_swiglu(c, xn, T, K, wg, wu, y, act, mode, nullptr, 0.f, qo);
+}
+
 int elmh_rmsnorm_swiglu_dev(elmh_ctx* c, const float* x, const float* norm_w, float eps, int T, int64_t K,
                             const elmh_weight* wg, const elmh_weight* wu, float* y, int act, int mode) {
   if (!c || !x || !norm_w || !wg || !wu || !y) return fail(c, ELMH_ERR_ARG, "null ctx/x/norm weight/weight/y");
   if (T < 1 || K < 1 || K > 8192) return fail(c, ELMH_ERR_ARG, "rmsnorm: bad shape T=%d dim=%lld", T, (long long)K);
   DeviceGuard g(c);
-  const elmh_weight* const ws[2] = {wg, wu};
-  if (wg->w.dtype == wu->w.dtype && wg->w.H == wu->w.H && wg->w.rows == wu->w.rows && wg->w.cols == K &&
-      wu->w.cols == K &&
-      (norm_fusable(T, K, 2, ws, 2, act) || norm_gemm(T, K, 2, ws, 2, act) || f32_norm_fusable(T, K, 2, ws, 2, act)))
-    return run_swiglu(c, x, T, K, wg, wu, y, act, mode, norm_w, eps);
-  const float* xn;
-  int rc;
-  if ((rc = norm_to_scratch(c, x, norm_w, eps, T, K, &xn))) return rc;
-  return run_swiglu(c, xn, T, K, wg, wu, y, act, mode);
+  return run_rmsnorm_swiglu(c, x, norm_w, eps, T, K, wg, wu, y, act, mode);
 }
+
+int elmh_ffn_dev(elmh_ctx* c, const float* x, const float* norm_w, float eps, int T, int64_t K, const elmh_weight* wg,
+                 const elmh_weight* wu, float* h, elmh_weight* wd, float* y, const float* res, int act, int mode) {
+  if (!c || !x || !wg || !wu || !h || !wd || !y) return fail(c, ELMH_ERR_ARG, "null ctx/x/weight/h/y");
+  if (norm_w && (T < 1 || K < 1 || K > 8192))
+    return fail(c, ELMH_ERR_ARG, "rmsnorm: bad shape T=%d dim=%lld", T, (long long)K);
+  const int64_t N = wg->w.rows;
+  elmh_weight* const ws[1] = {wd};
+  float* const ys[1] = {y};
+  const float* const rs[1] = {res};
+  int rc = check_targets(c, T, N, 1, ws, ys);
+  if (rc) return rc;
+  if (act < ELMH_ACT_F32 || act > ELMH_ACT_INT8_TOKEN) return fail(c, ELMH_ERR_ARG, "bad act mode %d", act);
+  DeviceGuard g(c);
+  c->ffn_fused = 0;
+  // h quantized by the SwiGLU launch (the streaming kernel at one token) when the down projection
+  // then takes the pre-quantized GEMV
+  const bool try_q = act == ELMH_ACT_INT8 && T == 1 && N % kBlock == 0 && a8_applies(wd->w) &&
+                     gemv_tokens(wd->w, 1, false) >= T;
+  QuantOut qo{nullptr, nullptr, nullptr, false};
+  if (try_q) {
+    const size_t nb = (size_t)(N / kBlock);
+    if ((rc = ensure(c, c->hq, (size_t)T * N)) || (rc = ensure(c, c->hd, (size_t)T * nb * sizeof(float))) ||
+        (rc = ensure(c, c->hs, (size_t)T * nb * sizeof(int32_t))))
+      return rc;
+    qo = {(int8_t*)c->hq.p, (float*)c->hd.p, (int32_t*)c->hs.p, false};
+  }
+  rc = norm_w ? run_rmsnorm_swiglu(c, x, norm_w, eps, T, K, wg, wu, h, act, mode, try_q ? &qo : nullptr)
+              : run_swiglu(c, x, T, K, wg, wu, h, act, mode, nullptr, 0.f, try_q ? &qo : nullptr);
+  if (rc) return rc;
+  if (!qo.done) return run_matmul(c, h, T, N, 1, ws, ys, res ? rs : nullptr, act, mode);
+  c->ffn_fused = 1;
+  const std::vector<int> idx = {0};
+  return run_gemv_group(c, nullptr, qo.q, qo.d, qo.s, T, N, idx, ws, ys, res ? rs : nullptr);
+}
+
+int elmh_ffn_fused(const elmh_ctx* c) { return c ? c->ffn_fused : 0; }
 
 int elmh_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight* const* w, float* const* y,
                 const float* const* res, int act, int mode) {

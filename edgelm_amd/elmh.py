@@ -244,6 +244,15 @@ class Context:
                                                 C.c_void_p(y_ptr), C.c_void_p(q_ptr), C.c_void_p(d_ptr),
                                                 C.c_void_p(s_ptr)))
 
+    def ffn_dev(self, x_ptr, T, K, wg, wu, h_ptr, wd, y_ptr, res_ptr=None, norm_w_ptr=None, eps=1e-5, act=ACT_INT8,
+                mode=EXACT):
+        """FFN_SWIGLU (after RMSNORM with norm_w) into h, then MATMUL(_ADD) of h by wd into y; returns whether
+        the SwiGLU launch quantized h for the down projection."""
+        self._check(lib().elmh_ffn_dev(self.h, C.c_void_p(x_ptr), C.c_void_p(norm_w_ptr), C.c_float(eps), C.c_int(T),
+                                       C.c_int64(K), wg.h, wu.h, C.c_void_p(h_ptr), wd.h, C.c_void_p(y_ptr),
+                                       C.c_void_p(res_ptr), C.c_int(act), C.c_int(mode)))
+        return bool(lib().elmh_ffn_fused(self.h))
+
     def quantize_act_dev(self, x_ptr, T, K, q_ptr, d_ptr, s_ptr):
         self._check(lib().elmh_quantize_act_dev(self.h, C.c_void_p(x_ptr), C.c_int(T), C.c_int64(K), C.c_void_p(q_ptr),
                                                 C.c_void_p(d_ptr), C.c_void_p(s_ptr)))

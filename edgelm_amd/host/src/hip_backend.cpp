@@ -118,6 +118,7 @@ class HipBackend : public Backend {
       for (int t : op.in) ++readers[t];
     fuse_norm_.assign(g.ops.size(), 0);
     fuse_attn_.assign(g.ops.size(), 0);
+    fuse_ffn_.assign(g.ops.size(), 0);
     for (const Partition& p : parts) {
       if (p.backend != this) continue;
       for (int i = p.begin; i + 1 < p.end; ++i) {
@@ -131,6 +132,10 @@ class HipBackend : public Backend {
         // would run before the deferred kernel)
         fuse_attn_[i] = a.type == OpType::ATTENTION && !host_needed_[a.out[0]] && !b.in.empty() &&
                         b.in[0] == a.out[0] && (b.type == OpType::MATMUL || b.type == OpType::MATMUL_ADD);
+        // FFN_SWIGLU whose output h only the next op (the down projection) multiplies: one call, in
+        // which the SwiGLU launch can hand h over quantized (it still writes h)
+        fuse_ffn_[i] = a.type == OpType::FFN_SWIGLU && !host_needed_[a.out[0]] && readers[a.out[0]] == 1 &&
+                       !b.in.empty() && b.in[0] == a.out[0] && (b.type == OpType::MATMUL || b.type == OpType::MATMUL_ADD);
       }
     }
     act_.assign(nt, Buf{});
@@ -214,10 +219,18 @@ class HipBackend : public Backend {
     // a deferred ATTENTION (fuse_attn_) runs inside this matmul's call
     const bool attended = attn_.op == idx - 1 && attn_.op >= 0;
     if (!attended) attn_.op = -1;
+    // a deferred FFN_SWIGLU (fuse_ffn_) runs inside this matmul's call
+    const bool ffned = ffn_.op == idx - 1 && ffn_.op >= 0;
+    if (!ffned) ffn_.op = -1;
     switch (op.type) {
       case OpType::FFN_SWIGLU: {
         const int T = static_cast<int>(c.rows(op.in[0]));
         const int64_t K = c.tensor(op.in[1]).cols;
+        if (prepared_ && fuse_ffn_[idx]) {
+          ffn_ = {idx, normed ? norm_.x : in(op.in[0], c), normed ? norm_.w : nullptr, normed ? norm_.eps : 0.f, T, K,
+                  c.tensor(op.in[1]).rows, weight(c.tensor(op.in[1])), weight(c.tensor(op.in[2])), out(op.out[0], c)};
+          return;  // the next op (the down projection) runs it
+        }
         if (normed)
           check(elmh_rmsnorm_swiglu_dev(ctx_, norm_.x, norm_.w, norm_.eps, T, K, weight(c.tensor(op.in[1])),
                                         weight(c.tensor(op.in[2])), out(op.out[0], c), act(c), ELMH_EXACT),
@@ -248,7 +261,13 @@ class HipBackend : public Backend {
           check(elmh_rmsnorm_matmul_dev(ctx_, norm_.x, norm_.w, norm_.eps, T, K, static_cast<int>(n), w_.data(),
                                         y_.data(), res, act(c), ELMH_EXACT),
                 op);
-        else if (attended) {
+        else if (ffned) {
+          const PendingFfn& f = ffn_;
+          EDGELM_CHECK(n == 1 && f.h == x && f.T == T && f.N == K, "ffn + matmul: operands do not match");
+          check(elmh_ffn_dev(ctx_, f.x, f.nw, f.eps, f.T, f.K, f.wg, f.wu, f.h, w_[0], y_[0], r_[0], act(c), ELMH_EXACT),
+                op);
+          ffn_.op = -1;
+        } else if (attended) {
           const PendingAttention& a = attn_;
           EDGELM_CHECK(n == 1 && a.out == x && a.T == T && static_cast<int64_t>(a.nh) * a.hd == K,
                        "attention + matmul: operands do not match");
@@ -688,6 +707,17 @@ class HipBackend : public Backend {
     int mc = 0;
     const float *rc = nullptr, *rs = nullptr;
   } attn_;
+  std::vector<char> fuse_ffn_;  // op index: an FFN_SWIGLU that the next op (a matmul) runs
+  struct PendingFfn {
+    int op = -1;
+    const float* x = nullptr;   // the FFN's input, or RMSNORM's when nw is set
+    const float* nw = nullptr;  // a deferred RMSNORM's weight
+    float eps = 0.f;
+    int T = 0;
+    int64_t K = 0, N = 0;  // FFN_SWIGLU's input width and output width (the rows of gate and up)
+    const elmh_weight *wg = nullptr, *wu = nullptr;
+    float* h = nullptr;
+  } ffn_;
   int output_ = -1;          // graph output when this backend writes it (prepare), else -1
   bool keep_out_ = false;    // keep_output(true): the output is not copied to the host arena
   int32_t* dev_tok_ = nullptr;  // argmax result

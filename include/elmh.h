@@ -174,6 +174,19 @@ int elmh_rmsnorm_matmul_dev(elmh_ctx* ctx, const float* x, const float* norm_w, 
                             int act, int mode);
 int elmh_rmsnorm_swiglu_dev(elmh_ctx* ctx, const float* x, const float* norm_w, float eps, int T, int64_t K,
                             const elmh_weight* wg, const elmh_weight* wu, float* y, int act, int mode);
+/* A layer's FFN pair as one call: FFN_SWIGLU of x (RMSNORM'd first when norm_w is given, as
+ * elmh_rmsnorm_swiglu_dev) into h [T, N] (N = rows of wg), then MATMUL of h by wd into y [T, rows of
+ * wd], plus res when given (MATMUL_ADD). The same results as elmh_rmsnorm_swiglu_dev /
+ * elmh_swiglu_dev into h and then elmh_matmul_dev on h, bit for bit, h included: the op pair
+ * FFN_SWIGLU -> MATMUL_ADD down of edgelm's fused layer (passes.cpp:100-104), the down projection
+ * quantizing its input h once (cpu::matmul's quantize_act_row, kernels_cpu.cpp:339-377). With int8
+ * activations at one token on the streaming GEMV (long rows) the SwiGLU launch quantizes h itself
+ * (elmh_swiglu_quant_dev) and the down projection takes it pre-quantized, so no quantizer launch runs
+ * between them; elmh_ffn_fused(ctx) returns 1 if the last call took that path, 0 otherwise. */
+int elmh_ffn_dev(elmh_ctx* ctx, const float* x, const float* norm_w, float eps, int T, int64_t K,
+                 const elmh_weight* wg, const elmh_weight* wu, float* h, elmh_weight* wd, float* y, const float* res,
+                 int act, int mode);
+int elmh_ffn_fused(const elmh_ctx* ctx);
 /* ATTENTION (cpu::attention, kernels_cpu.cpp:417-488; AttnArgs, kernels.hpp:28-36): appends this
  * step's keys (rotated when rope_cos/rope_sin, the RopeTable's [pos][head_dim/2] arrays, are given)
  * and values to the cache [n_kv][max_ctx][head_dim] at positions pos0 .. pos0+T-1, then

@@ -192,3 +192,25 @@ def test_greedy_steps_match_edgelm(smollm, backends):
         with pytest.raises(RuntimeError, match="token id out of range"):
             s.greedy_steps(bad, 3)
     s.close(), ref.close()
+
+
+@pytest.fixture(scope="module")
+def wide_ffn(tmp_path_factory):
+    """A model whose FFN runs on the streaming GEMV at one token (dim 2560 > 2048): its decode steps
+    take the FFN pair as one call, h handed to the down projection quantized by the SwiGLU launch."""
+    d = tmp_path_factory.mktemp("wide")
+    cfg = dict(S.TINY, dim=2560, hidden=2048, n_layers=2, n_heads=40, n_kv_heads=8, head_dim=64, max_seq=128)
+    p = str(d / "wide.q4.elm")
+    S.write_model(p, cfg, "q4", seed=77, sd=0.02, embed_sd=0.5)
+    return p
+
+
+@pytest.mark.parametrize("backends", ["hip,cpu", "hip-matmul,cpu"])
+def test_streaming_ffn_pair_bit_identical_to_edgelm(wide_ffn, backends):
+    ids = np.random.default_rng(8).integers(0, 320, 14).astype(np.int32)
+    m = host.Model(wide_ffn)
+    print(f"[gpu] e2e wide ffn {backends}", flush=True)
+    mine = host.Session(m, backends, threads=4, max_ctx=64, max_batch=8, all_logits=True, act_quant=True)
+    ref = O.RefSession(wide_ffn, "cpu", threads=4, max_ctx=64, max_batch=8, all_logits=True, act_quant=True)
+    got, want = run_all(mine, ids, 4, 4), run_all(ref, ids, 4, 4)
+    assert bits_equal(got, want), f"max diff {np.abs(got - want).max()}"

@@ -605,3 +605,41 @@ def test_swiglu_quant_refuses_partial_blocks(ctx):
         ctx.swiglu_quant_dev(bufs[0].ptr, 1, 4096, dg, du, *[b.ptr for b in bufs[1:]])
     for b in bufs + [dg, du]:
         b.free()
+
+
+# (dt, N, K, T, norm, residual, fused): elmh_ffn_dev, the FFN pair as one call; fused: the SwiGLU
+# launch hands h to the down projection quantized (one token on the streaming GEMV)
+FFN_CASES = [(O.Q4, 1024, 4096, 1, False, True, True), (O.Q4, 1024, 4096, 1, True, True, True),
+             (O.Q4, 2048, 2560, 1, True, False, True), (O.Q8, 1024, 2048, 1, False, True, True),
+             (O.Q4, 1024, 4096, 2, True, True, False), (O.Q4, 1536, 576, 1, True, True, False),
+             (O.Q4, 1536, 576, 9, False, True, False)]
+
+
+@pytest.mark.parametrize("case", FFN_CASES)
+def test_ffn_pair_exact(ctx, case):
+    """elmh_ffn_dev: h and y bit-identical to edgelm's cpu backend (RMSNORM, then cpu::swiglu, then
+    cpu::matmul with the residual), int8 activations; whether the quantized handoff ran."""
+    dt, n, k, T, norm, resid, fused = case
+    r = rng(900 + n + k + T + dt + 2 * norm)
+    wg, wu, wd = weight(r, n, k, dt), weight(r, n, k, dt), weight(r, k, n, dt)
+    dg, du, dd = up(ctx, wg), up(ctx, wu), up(ctx, wd)
+    x = r.normal(0, 1, (T, k)).astype(np.float32)
+    nw = (1 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    res = r.normal(0, 1, (T, k)).astype(np.float32)
+    bx, bn, bh, by, br = (ctx.buffer(T * k * 4), ctx.buffer(k * 4), ctx.buffer(T * n * 4), ctx.buffer(T * k * 4),
+                          ctx.buffer(T * k * 4))
+    bx.upload(x)
+    bn.upload(nw)
+    br.upload(res)
+    print(f"[gpu] ffn pair dt={dt} {n}x{k} T={T} norm={norm} res={resid}", flush=True)
+    got_fused = ctx.ffn_dev(bx.ptr, T, k, dg, du, bh.ptr, dd, by.ptr, br.ptr if resid else None,
+                            bn.ptr if norm else None, 1e-5)
+    ctx.synchronize()
+    assert got_fused == fused
+    xin = O.rmsnorm(x, nw, 1e-5) if norm else x
+    hw = O.cpu_swiglu(xin, wg, wu, act_quant=True)
+    yw = O.cpu_matmul(hw, [wd], [res] if resid else None, act_quant=True)[0]
+    assert bits_equal(bh.download((T, n), np.float32), hw)
+    assert bits_equal(by.download((T, k), np.float32), yw)
+    for b in (bx, bn, bh, by, br, dg, du, dd):
+        b.free()
