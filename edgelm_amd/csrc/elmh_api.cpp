@@ -440,12 +440,16 @@ int run_matmul(elmh_ctx* c, const float* x, int T, int64_t K, int n, elmh_weight
   return ELMH_OK;
 }
 
-// The SwiGLU output row quantized as elmh_quantize_act_dev does it, for the next GEMV: `done` is set
-// when the SwiGLU launch wrote it itself.
+// The SwiGLU output quantized for the next matmul by the SwiGLU launch itself: row-major as
+// elmh_quantize_act_dev writes it (q, d, s; the one-token GEMV), or with `frag` as the block-scale
+// GEMM's operand (fragments q [Tpad/32][N/32][1 KB], scales d [N/32][Tpad]); `done` is set when the
+// SwiGLU launch wrote it.
 struct QuantOut {
   int8_t* q;
   float* d;
   int32_t* s;
+  bool frag;
+  int Tpad;
   bool done;
 };
 
@@ -509,7 +513,7 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
     // one token on the streaming kernel: 32-row workgroups of eight producer waves, which also
     // quantize the output row when the caller asks for it (8B gate+up alone: 15.5-15.9 -> 15.4 us)
     const bool w32 = !qin && xin && T == 1 && !nw && stream_qout_ok(g, (int)K);
-    const bool qout = qo && w32;
+    const bool qout = qo && !qo->frag && w32;
     a.tpw = w32 ? 32 / g.H : 1;
     const int wgs = (tiles + a.tpw - 1) / a.tpw;
     a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, tiles};
@@ -554,6 +558,12 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
   a.K = (int)K;
   a.nb = (int)(K / kBlock);
   a.fast = mode == ELMH_FAST;
+  if (qo && qo->frag && !token && Tpad == qo->Tpad && gemm_qf_ok(g.dtype, T, a.nb, g.H, (int)g.rows, g.rows_pad)) {
+    a.oq = qo->q;
+    a.od = qo->d;
+    a.onb = (int)(g.rows / kBlock);
+    qo->done = true;
+  }
   HIP_OR_FAIL(c, launch_gemm_a8(g.dtype, 1, token, a, tiles, c->stream));
   return ELMH_OK;
 }
@@ -889,7 +899,7 @@ int elmh_swiglu_quant_dev(elmh_ctx* c, const float* x, int T, int64_t K, const e
   if (!c || !x || !q || !d || !s) return fail(c, ELMH_ERR_ARG, "null argument");
   if (!wg || wg->w.rows % kBlock) return fail(c, ELMH_ERR_ARG, "swiglu_quant: output rows must be a multiple of 32");
   DeviceGuard g(c);
-  QuantOut qo{q, d, s, false};
+  QuantOut qo{q, d, s, false, 0, false};
   int rc = run_swiglu(c, x, T, K, wg, wu, y, ELMH_ACT_INT8, ELMH_EXACT, nullptr, 0.f, &qo);
   if (rc) return rc;
   if (!qo.done) HIP_OR_FAIL(c, launch_act_quant_rows(y, T, (int)wg->w.rows, q, d, s, c->stream));
@@ -964,17 +974,26 @@ int elmh_ffn_dev(elmh_ctx* c, const float* x, const float* norm_w, float eps, in
   if (act < ELMH_ACT_F32 || act > ELMH_ACT_INT8_TOKEN) return fail(c, ELMH_ERR_ARG, "bad act mode %d", act);
   DeviceGuard g(c);
   c->ffn_fused = 0;
-  // h quantized by the SwiGLU launch (the streaming kernel at one token) when the down projection
-  // then takes the pre-quantized GEMV
-  const bool try_q = act == ELMH_ACT_INT8 && T == 1 && N % kBlock == 0 && a8_applies(wd->w) &&
-                     gemv_tokens(wd->w, 1, false) >= T;
-  QuantOut qo{nullptr, nullptr, nullptr, false};
-  if (try_q) {
-    const size_t nb = (size_t)(N / kBlock);
-    if ((rc = ensure(c, c->hq, (size_t)T * N)) || (rc = ensure(c, c->hd, (size_t)T * nb * sizeof(float))) ||
-        (rc = ensure(c, c->hs, (size_t)T * nb * sizeof(int32_t))))
+  // h quantized by the SwiGLU launch where the down projection then takes it pre-quantized: at one
+  // token the streaming SwiGLU writes it row-major for the GEMV; on the block-scale GEMM path the
+  // SwiGLU GEMM writes the down GEMM's fragments
+  const size_t onb = (size_t)(N / kBlock);
+  const bool down_a8 = act == ELMH_ACT_INT8 && N % kBlock == 0 && a8_applies(wd->w);
+  const bool down_gemm =
+      down_a8 && T > gemv_tokens(wd->w, 1, use_small_gemv(T, N, wd->w.data_bytes + wd->w.scale_bytes));
+  const int Tpad = (int)round_up(T, kGemmTileT);
+  QuantOut qo{nullptr, nullptr, nullptr, false, 0, false};
+  bool try_q = false;
+  if (down_a8 && T == 1 && gemv_tokens(wd->w, 1, false) >= T) {
+    if ((rc = ensure(c, c->hq, (size_t)T * N)) || (rc = ensure(c, c->hd, (size_t)T * onb * sizeof(float))) ||
+        (rc = ensure(c, c->hs, (size_t)T * onb * sizeof(int32_t))))
       return rc;
-    qo = {(int8_t*)c->hq.p, (float*)c->hd.p, (int32_t*)c->hs.p, false};
+    qo = {(int8_t*)c->hq.p, (float*)c->hd.p, (int32_t*)c->hs.p, false, 0, false};
+    try_q = true;
+  } else if (down_gemm) {
+    if ((rc = ensure(c, c->hq, (size_t)Tpad * N)) || (rc = ensure(c, c->hd, onb * Tpad * sizeof(float)))) return rc;
+    qo = {(int8_t*)c->hq.p, (float*)c->hd.p, nullptr, true, Tpad, false};
+    try_q = true;
   }
   rc = norm_w ? run_rmsnorm_swiglu(c, x, norm_w, eps, T, K, wg, wu, h, act, mode, try_q ? &qo : nullptr)
               : run_swiglu(c, x, T, K, wg, wu, h, act, mode, nullptr, 0.f, try_q ? &qo : nullptr);
@@ -982,6 +1001,7 @@ int elmh_ffn_dev(elmh_ctx* c, const float* x, const float* norm_w, float eps, in
   if (!qo.done) return run_matmul(c, h, T, N, 1, ws, ys, res ? rs : nullptr, act, mode);
   c->ffn_fused = 1;
   const std::vector<int> idx = {0};
+  if (qo.frag) return run_gemm_group(c, qo.q, qo.d, T, Tpad, N, idx, ws, ys, res ? rs : nullptr, 0, mode == ELMH_FAST);
   return run_gemv_group(c, nullptr, qo.q, qo.d, qo.s, T, N, idx, ws, ys, res ? rs : nullptr);
 }
 

@@ -109,6 +109,11 @@ struct GemmArgs {
   const float* xd;   // [nb][Tpad] (block mode) or [Tpad] (token mode)
   int T, Tpad, K, nb;
   int fast;          // 0: exact sequential mul+add; 1: fused multiply-add
+  // SwiGLU (block mode): h also quantized into the next GEMM's operand, fragments [Tpad/32][onb][1 KB]
+  // and block scales [onb][Tpad] (onb = N / 32), or null
+  int8_t* oq;
+  float* od;
+  int onb;
 };
 
 struct F32Args {
@@ -143,6 +148,7 @@ bool gemv_qin_ok(int T, int K);
 // Items per thread of the streaming GEMV for a tile of `items` items (0: too many).
 int gemv_stream_ipt(int dtype, int items, int producers);
 size_t gemv_lds_bytes(int nt, int K, int nb, int H, int nsel);
+bool gemm_qf_ok(int dtype, int T, int nb, int H, int N, int64_t rows_pad);
 hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_tiles, hipStream_t s);
 hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs& a, int total_tiles, hipStream_t s);
 hipError_t launch_f32act(int dtype, int swiglu, const F32Args& a, hipStream_t s);

@@ -1687,67 +1687,77 @@ __global__ __launch_bounds__(256) void gemm_wave16_kernel(const GemmArgs a) {
 // their block scales, the 16 rows' weight items and their q4 scales. gemm_wave16_kernel loads each
 // wave's operands from L2 eight blocks ahead, and its loop is bound by that latency (~150 ns per
 // 32-block with the operands in the Infinity Cache, measured at T = 128, K = 1536); here the loop
-// reads LDS. LDS: A [2][nb][1024] | XD [nb][64] f32 (token mode: [64]) | B[s] [nb][16][G] | BS[s]
-// (q4) [nb][16] f32, each region with room for kLds16Ahead more blocks and rounded up to 1 KB
+// reads LDS. LDS: A [TW/32][nb][1024] | XD [nb][TW] f32 (token mode: [64]) | B[s] [nb][RW][G] |
+// BS[s] (q4) [nb][RW] f32, each region with room for kLds16Ahead more blocks and rounded up to 1 KB
 // (gemm_lds16_bytes).
+// QF (SwiGLU in block mode, the quantized-h handoff): a workgroup is 32 rows x 32 tokens instead
+// (wave w: rows 16 (w & 1) .., tokens 16 (w >> 1) ..), so it holds whole 32-blocks of h; after the
+// stores, the two waves of a token group exchange their 16-row amax through LDS and each writes its
+// half of every block into the next GEMM's fragments with edgelm's rounding (act_quant_frag_kernel's
+// arithmetic: s = amax / 127, each value's rounding that of its division).
 __host__ __device__ constexpr int lds16_region_bytes(int bytes) { return (bytes + 1023) / 1024 * 1024; }
 constexpr int kLds16MaxBlocks = 48;  // K <= 1536
 constexpr int kLds16Ahead = 3;       // blocks read ahead; every region has room for them past nb
-template <int WDT, bool SW, bool TOK>
+template <int WDT, bool SW, bool TOK, bool QF = false>
 __host__ __device__ inline int gemm_lds16_bytes(int nb) {
   constexpr int G = WDT == WQ8 ? 32 : 16, NSEL = SW ? 2 : 1, P = kLds16Ahead;
-  const int xd = TOK ? 1024 : lds16_region_bytes((nb + P) * 64 * 4);
-  const int bw = lds16_region_bytes((nb + P) * 16 * G), bs = WDT == WQ4 ? lds16_region_bytes((nb + P) * 16 * 4) : 0;
-  return (2 * nb + P) * 1024 + xd + NSEL * (bw + bs);
+  constexpr int RW = QF ? 32 : 16, TW = QF ? 32 : 64;
+  const int xd = TOK ? 1024 : lds16_region_bytes((nb + P) * TW * 4);
+  const int bw = lds16_region_bytes((nb + P) * RW * G), bs = WDT == WQ4 ? lds16_region_bytes((nb + P) * RW * 4) : 0;
+  return (TW / 32 * nb + P) * 1024 + xd + NSEL * (bw + bs) + (QF ? 1024 : 0);
 }
 
-template <int WDT, bool SW, bool TOK, bool FAST>
+template <int WDT, bool SW, bool TOK, bool FAST, bool QF = false>
 __global__ __launch_bounds__(256) void gemm_lds16_kernel(const GemmArgs a) {
+  static_assert(!QF || (SW && !TOK), "quantized h: SwiGLU in block mode");
   typedef Wave16Ops<WDT, SW, TOK> Ops;
   constexpr int NSEL = Ops::NSEL, G = WDT == WQ8 ? 32 : 16;
   constexpr bool BLOCKX = Ops::BLOCKX;
+  constexpr int RW = QF ? 32 : 16, TW = QF ? 32 : 64;  // rows and tokens of a workgroup
   extern __shared__ __align__(16) unsigned char lds[];
   const int lane = threadIdx.x & 63, l16 = lane & 15, c4 = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int rh = QF ? wave & 1 : 0, tgw = QF ? wave >> 1 : wave;  // the wave's row half, token group
   const int nb = a.nb, H = a.H;
-  // workgroup -> (target, 16-row tile, 64-token chunk), chunk fastest
-  const int nchunk = (a.T + 63) / 64;
+  // workgroup -> (target, RW-row tile, TW-token chunk), chunk fastest
+  const int nchunk = (a.T + TW - 1) / TW;
   int rt = (int)blockIdx.x;
   const int ch = rt % nchunk;
   rt /= nchunk;
   int ti = 0;
   const int n = SW ? 1 : a.n_targets;
   for (; ti < n; ++ti) {
-    const int cnt = (a.tg[ti].N + kWave16 - 1) / kWave16;
+    const int cnt = (a.tg[ti].N + RW - 1) / RW;
     if (rt < cnt) break;
     rt -= cnt;
   }
   if (ti >= n) return;  // past the last tile (uniform per workgroup; no barrier below)
   const GemmTarget tg = SW ? a.tg[0] : gemm_target_at(ti);
-  const int r0 = rt * kWave16, tc = ch * 64;
+  const int r0 = rt * RW, tc = ch * TW;
   const uint8_t* const wd[2] = {tg.data, SW ? a.tg[1].data : tg.data};
   const float* const wsc[2] = {tg.scales, SW ? a.tg[1].scales : tg.scales};
   constexpr int P = kLds16Ahead;
-  const int xd_bytes = TOK ? 1024 : lds16_region_bytes((nb + P) * 64 * 4);
-  const int bw_bytes = lds16_region_bytes((nb + P) * 16 * G);
-  const int bs_bytes = WDT == WQ4 ? lds16_region_bytes((nb + P) * 16 * 4) : 0;
+  const int xd_bytes = TOK ? 1024 : lds16_region_bytes((nb + P) * TW * 4);
+  const int bw_bytes = lds16_region_bytes((nb + P) * RW * G);
+  const int bs_bytes = WDT == WQ4 ? lds16_region_bytes((nb + P) * RW * 4) : 0;
   unsigned char* const A = lds;
-  unsigned char* const XD = A + (2 * nb + P) * 1024;
+  unsigned char* const XD = A + (TW / 32 * nb + P) * 1024;
   unsigned char* const BW = XD + xd_bytes;             // [s] at BW + s * bw_bytes
   unsigned char* const BS = BW + NSEL * bw_bytes;      // [s] at BS + s * bs_bytes
   const unsigned base = (unsigned)(size_t)(LdsBytes)lds;
-  const unsigned xd_lds = base + (2 * nb + P) * 1024, bw_lds = xd_lds + xd_bytes, bs_lds = bw_lds + NSEL * bw_bytes;
+  const unsigned xd_lds = base + (TW / 32 * nb + P) * 1024, bw_lds = xd_lds + xd_bytes, bs_lds = bw_lds + NSEL * bw_bytes;
 
   // 1. every operand of the workgroup into LDS; instruction j of a region fills its KB j, and wave w
   // issues j = w, w + 4, ... Chunks past a region's end repeat its last one (into the padding).
   {
-    // activation fragments: the two 32-token groups are contiguous in xq ([Tpad/32][nb][1 KB])
+    // activation fragments: the token groups are contiguous in xq ([Tpad/32][nb][1 KB])
     const int8_t* const xs = a.xq + (int64_t)(tc >> 5) * nb * 1024;
-    for (int j = wave; j < 2 * nb; j += 4) dma16s(xs, (uint32_t)(j * 1024 + lane * 16), base + j * 1024);
-    if (BLOCKX) {  // XD[b][t]: lane -> block 4 j + lane / 16, tokens 4 (lane % 16) ..
-      for (int j = wave; 4 * j < nb; j += 4) {
-        const int b = min(4 * j + (lane >> 4), nb - 1);
-        dma16s(a.xd, (uint32_t)(((int64_t)b * a.Tpad + tc + 4 * l16) * 4), xd_lds + j * 1024);
+    for (int j = wave; j < TW / 32 * nb; j += 4) dma16s(xs, (uint32_t)(j * 1024 + lane * 16), base + j * 1024);
+    if (BLOCKX) {  // XD[b][t]: TW / 4 lanes per block (4 tokens each), 256 / TW blocks per instruction
+      constexpr int LPB = TW / 4, BPI = 64 / LPB;
+      for (int j = wave; BPI * j < nb; j += 4) {
+        const int b = min(BPI * j + lane / LPB, nb - 1);
+        dma16s(a.xd, (uint32_t)(((int64_t)b * a.Tpad + tc + 4 * (lane % LPB)) * 4), xd_lds + j * 1024);
       }
     } else if (wave == 0) {  // XD[t]
       dma16s(a.xd, (uint32_t)((tc + 4 * l16) * 4), xd_lds);
@@ -1756,7 +1766,7 @@ __global__ __launch_bounds__(256) void gemm_lds16_kernel(const GemmArgs a) {
     // keeps byte offsets below 2^31)
     const int lgH = __builtin_ctz(H);
     auto item = [&](int row, int b) { return (((row >> lgH) * nb + b) << lgH) + (row & (H - 1)); };
-    constexpr int CPB = G;  // 16-byte chunks per block of the 16 rows: 16 rows x G / 16
+    constexpr int CPB = RW * G / 16;  // 16-byte chunks per block of the RW rows
     const int nw = nb * CPB;
 #pragma unroll
     for (int s = 0; s < NSEL; ++s) {
@@ -1766,9 +1776,10 @@ __global__ __launch_bounds__(256) void gemm_lds16_kernel(const GemmArgs a) {
         dma16s(wd[s], (uint32_t)(item(r0 + row, b) * G + half * 16), bw_lds + s * bw_bytes + j * 1024);
       }
       if (WDT == WQ4) {  // BS[b][row]: 4 rows per chunk, consecutive items (H >= 4, r0 % 4 == 0)
-        const int ns = nb * 4;
+        constexpr int QPB = RW / 4;
+        const int ns = nb * QPB;
         for (int j = wave; 64 * j < ns; j += 4) {
-          const int c = min(64 * j + lane, ns - 1), b = c >> 2, q = c & 3;
+          const int c = min(64 * j + lane, ns - 1), b = c / QPB, q = c - b * QPB;
           dma16s(wsc[s], (uint32_t)(item(r0 + 4 * q, b) * 4), bs_lds + s * bs_bytes + j * 1024);
         }
       }
@@ -1777,24 +1788,24 @@ __global__ __launch_bounds__(256) void gemm_lds16_kernel(const GemmArgs a) {
     __syncthreads();
   }
 
-  // 2. the wave's 16 tokens against the 16 rows, block by block from LDS, D blocks read ahead
-  const int tw = wave * kWave16, t0 = tc + tw;
+  // 2. the wave's 16 tokens against its 16 rows, block by block from LDS, D blocks read ahead
+  const int tw = tgw * kWave16, t0 = tc + tw, rw0 = rh * 16;
   const unsigned char* const xa = A + (tw >> 5) * nb * 1024 + ((c4 >> 1) * 32 + (tw & 31) + l16) * 16 + (c4 & 1) * 8;
   auto load = [&](int blk, Ops& o) {
     // blocks nb .. nb + P - 1 (read ahead, never used) lie in the regions' padding
     o.A = *reinterpret_cast<const long*>(xa + blk * 1024);
 #pragma unroll
     for (int s = 0; s < NSEL; ++s) {
-      const unsigned char* const bw = BW + s * bw_bytes + (blk * 16 + l16) * G;
+      const unsigned char* const bw = BW + s * bw_bytes + (blk * RW + rw0 + l16) * G;
       if (WDT == WQ8) {
         o.B[s] = *reinterpret_cast<const long*>(bw + c4 * 8);
         o.c[s] = 1.f;
       } else {
         o.B[s] = q4_operand8(*reinterpret_cast<const uint2*>(bw + (c4 & 1) * 8), c4 >> 1);
-        o.c[s] = reinterpret_cast<const float*>(BS + s * bs_bytes)[blk * 16 + l16];
+        o.c[s] = reinterpret_cast<const float*>(BS + s * bs_bytes)[blk * RW + rw0 + l16];
       }
     }
-    if (BLOCKX) o.xv = *reinterpret_cast<const float4*>(XD + (blk * 64 + tw + 4 * c4) * 4);
+    if (BLOCKX) o.xv = *reinterpret_cast<const float4*>(XD + (blk * TW + tw + 4 * c4) * 4);
   };
   v4i iacc[NSEL];
   float facc[NSEL][4];
@@ -1861,7 +1872,47 @@ __global__ __launch_bounds__(256) void gemm_lds16_kernel(const GemmArgs a) {
   ELM_L16_STEP(42) ELM_L16_STEP(43) ELM_L16_STEP(44) ELM_L16_STEP(45) ELM_L16_STEP(46) ELM_L16_STEP(47)
 #undef ELM_L16_STEP
 done:
-  if (t0 < a.T) wave16_store<WDT, SW, TOK>(a, tg, r0, t0, lane, iacc, facc);
+  if constexpr (QF) {
+    if (t0 < a.T) wave16_store<WDT, SW, TOK>(a, tg, r0 + rw0, t0, lane, iacc, facc);
+    // h for tokens t0 + 4 c4 + i, row r0 + rw0 + l16 (tokens past T were computed from the zero
+    // fragments of the padding; the next GEMM never stores them)
+    const int rc = min(r0 + rw0 + l16, tg.N - 1);
+    const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f, wsu = WDT == WQ8 ? a.tg[1].scales[rc] : 1.f;
+    float hv[4], am[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // wave16_store's value: q8 facc * ws, q4 facc / 16, then silu(gate) * up
+      const float g = WDT == WQ8 ? facc[0][i] * ws : facc[0][i] * 0.0625f;
+      const float u = WDT == WQ8 ? facc[1][i] * wsu : facc[1][i] * 0.0625f;
+      hv[i] = silu_exact(g) * u;
+      // the amax over the wave's 16 rows (the 16 lanes of each row of the wave)
+      float v = fabsf(hv[i]);
+      v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+      v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+      v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+      am[i] = fmaxf(v, dpp_f<kDppRowMirror>(v));
+    }
+    float* const ex = reinterpret_cast<float*>(BS + NSEL * bs_bytes);  // [token group][row half][16 tokens]
+    if (l16 == 0)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ex[(tgw * 2 + rh) * 16 + 4 * c4 + i] = am[i];
+    __syncthreads();
+    const int b = r0 / kBlock;  // the workgroup's 32 rows are block b of h
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float amax = fmaxf(am[i], ex[(tgw * 2 + (rh ^ 1)) * 16 + 4 * c4 + i]);
+      const float d = amax / 127.0f;
+      int q;
+      elm_q8_group<1>(&hv[i], d == 0.f ? 1.f : d, &q);
+      const int t = t0 + 4 * c4 + i;
+      if (r0 + rw0 + l16 < tg.N && t < a.Tpad) {
+        a.oq[elm_frag_offset(t, b, rh, a.onb) + l16] = (int8_t)q;
+        if (l16 == 0 && rh == 0) a.od[(int64_t)b * a.Tpad + t] = d;
+      }
+    }
+  } else {
+    if (t0 < a.T) wave16_store<WDT, SW, TOK>(a, tg, r0, t0, lane, iacc, facc);
+  }
 }
 
 // ---------------------------------------------------------------- f32-activation paths
@@ -2595,26 +2646,40 @@ static void gemm_wave16_launch(const GemmArgs& a, hipStream_t s) {
 }
 
 // gemm_lds16_kernel when its LDS fits (K <= 1536 or so); false otherwise
-template <int WDT, bool SW, bool TOK>
+template <int WDT, bool SW, bool TOK, bool QF = false>
 static bool gemm_lds16_launch(const GemmArgs& a, hipStream_t s) {
-  const int bytes = gemm_lds16_bytes<WDT, SW, TOK>(a.nb);
+  const int bytes = gemm_lds16_bytes<WDT, SW, TOK, QF>(a.nb);
   if (a.nb > kLds16MaxBlocks || bytes > (int)kMaxLds - 1024 || a.H < 4 || (a.H & (a.H - 1))) return false;
-  const void* k = a.fast && !(TOK && WDT == WQ8) ? (const void*)gemm_lds16_kernel<WDT, SW, TOK, true>
-                                                  : (const void*)gemm_lds16_kernel<WDT, SW, TOK, false>;
+  const void* k = a.fast && !(TOK && WDT == WQ8) ? (const void*)gemm_lds16_kernel<WDT, SW, TOK, true, QF>
+                                                  : (const void*)gemm_lds16_kernel<WDT, SW, TOK, false, QF>;
   static bool raised[2] = {false, false};  // the LDS limit, once per kernel
   const int which = a.fast && !(TOK && WDT == WQ8) ? 1 : 0;
   if (!raised[which]) {
     if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds - 1024) != hipSuccess) return false;
     raised[which] = true;
   }
+  constexpr int RW = QF ? 32 : 16, TW = QF ? 32 : 64;
   int rows = 0;
-  for (int i = 0; i < (SW ? 1 : a.n_targets); ++i) rows += (a.tg[i].N + kWave16 - 1) / kWave16;
-  const dim3 grid(rows * ((a.T + 63) / 64));
+  for (int i = 0; i < (SW ? 1 : a.n_targets); ++i) rows += (a.tg[i].N + RW - 1) / RW;
+  const dim3 grid(rows * ((a.T + TW - 1) / TW));
   if (which)
-    gemm_lds16_kernel<WDT, SW, TOK, true><<<grid, 256, bytes, s>>>(a);
+    gemm_lds16_kernel<WDT, SW, TOK, true, QF><<<grid, 256, bytes, s>>>(a);
   else
-    gemm_lds16_kernel<WDT, SW, TOK, false><<<grid, 256, bytes, s>>>(a);
+    gemm_lds16_kernel<WDT, SW, TOK, false, QF><<<grid, 256, bytes, s>>>(a);
   return true;
+}
+
+// Whether a SwiGLU GEMM in block mode can write h's quantized fragments itself (gemm_lds16_kernel's
+// 32 x 32 workgroups): where the 16 x 16 wave kernels would run it anyway (few token tiles) and
+// their LDS holds it, N a multiple of 32
+bool gemm_qf_ok(int dtype, int T, int nb, int H, int N, int64_t rows_pad) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return false;
+  const int tiles = (int)((rows_pad + kGemmTileN - 1) / kGemmTileN);
+  const int bytes = dtype == WQ8 ? gemm_lds16_bytes<WQ8, true, false, true>(nb) : gemm_lds16_bytes<WQ4, true, false, true>(nb);
+  return tiles * ((T + 63) / 64) < cus / 2 && nb <= kLds16MaxBlocks && bytes <= (int)kMaxLds - 1024 && H >= 4 &&
+         !(H & (H - 1)) && N % kBlock == 0 && !getenv("ELMH_GEMM_KERNEL") && !getenv("ELMH_GEMM_TOKEN_TILE");
 }
 
 template <int WDT, bool SW, bool TOK>
@@ -2625,6 +2690,14 @@ static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
   // the epilogue's buffer resources span 128 tokens x N floats in 31 bits
   for (int i = 0; i < (SW ? 2 : a.n_targets); ++i)
     if (a.tg[i].N < 1 || a.tg[i].N >= (1 << 22)) return hipErrorInvalidValue;
+  if (a.oq) {  // h's quantized fragments out of the SwiGLU GEMM (gemm_qf_ok holds)
+    if constexpr (SW && !TOK) {
+      if (!a.od || a.tg[0].N % kBlock || a.onb != a.tg[0].N / kBlock) return hipErrorInvalidValue;
+      return gemm_lds16_launch<WDT, SW, TOK, true>(a, s) ? hipGetLastError() : hipErrorInvalidValue;
+    } else {
+      return hipErrorInvalidValue;
+    }
+  }
   // one workgroup per (row tile, token tile), numbered in 8 XCD-contiguous ranges; 64-token tiles
   // when 128-token tiles would leave compute units idle
   int dev = 0, cus = 0;

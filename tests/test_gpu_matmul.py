@@ -608,11 +608,14 @@ def test_swiglu_quant_refuses_partial_blocks(ctx):
 
 
 # (dt, N, K, T, norm, residual, fused): elmh_ffn_dev, the FFN pair as one call; fused: the SwiGLU
-# launch hands h to the down projection quantized (one token on the streaming GEMV)
+# launch hands h to the down projection quantized (one token on the streaming GEMV; the GEMM's
+# fragments on the 16 x 16 wave path, T > 4 and K <= 1536)
 FFN_CASES = [(O.Q4, 1024, 4096, 1, False, True, True), (O.Q4, 1024, 4096, 1, True, True, True),
              (O.Q4, 2048, 2560, 1, True, False, True), (O.Q8, 1024, 2048, 1, False, True, True),
              (O.Q4, 1024, 4096, 2, True, True, False), (O.Q4, 1536, 576, 1, True, True, False),
-             (O.Q4, 1536, 576, 9, False, True, False)]
+             (O.Q4, 1536, 576, 9, False, True, True), (O.Q4, 1536, 576, 128, True, True, True),
+             (O.Q8, 1536, 576, 70, False, True, True), (O.Q8, 160, 96, 33, True, True, True),
+             (O.Q4, 2048, 2560, 64, True, False, False)]
 
 
 @pytest.mark.parametrize("case", FFN_CASES)
