@@ -722,6 +722,13 @@ def pmc_workload(ctx, E):
             ctx.gemv_a8_dev(q.ptr, d.ptr, s.ptr, 1, 14336, [m.w[f"{l}.d"]], [by.ptr])
     ctx.synchronize()
     m.free()
+    # the 8B gate+up SwiGLU that also quantizes h (32-row workgroups), 8 distinct layers
+    m = Model(ctx, 12, {f"{l}.{n}": (14336, 4096) for l in range(8) for n in "gu"}, lambda n: 2)
+    for _ in range(4):
+        for l in range(8):
+            ctx.swiglu_quant_dev(bx.ptr, 1, 4096, m.w[f"{l}.g"], m.w[f"{l}.u"], by.ptr, q.ptr, d.ptr, s.ptr)
+    ctx.synchronize()
+    m.free()
     n = 64 << 20
     src, dst = ctx.buffer(n), ctx.buffer(n)
     ctx.memset_dev(src.ptr, 1, n)
@@ -734,23 +741,24 @@ def pmc_workload(ctx, E):
 
 
 def pmc_gemm_workload(ctx, E):
-    """The configs[4] T = 512 prefill GEMMs alone (q8 weights; per-token scale, then edgelm's per-block scales),
-    four eager launches per shape, for rocprofv3 --pmc passes (MFMA busy cycles, LDS bank conflicts, VALU and
-    MFMA instruction counts)."""
+    """The configs[4] T = 512 prefill GEMMs alone (q8 weights with the per-token scale, then with edgelm's
+    per-block scales, then q4 weights with per-block scales), four eager launches per shape, for rocprofv3
+    --pmc passes (MFMA busy cycles, LDS bank conflicts, VALU and MFMA instruction counts)."""
     b8 = [(4096, 4096), (14336, 4096), (4096, 14336)]
-    m = Model(ctx, 5, {f"{i}": sh for i, sh in enumerate(b8)}, lambda n: 1)
     bx = ctx.buffer(512 * 14336 * 4)
     bx.upload(np.random.default_rng(3).standard_normal(512 * 14336, dtype=np.float32))
     by = ctx.buffer(512 * 14336 * 4)
     ctx.reserve(512, 14336)
-    for act in (E.ACT_INT8_TOKEN, E.ACT_INT8):
-        for i, (n, k) in enumerate(b8):
-            for _ in range(4):
-                ctx.matmul_dev(bx.ptr, 512, k, [m.w[f"{i}"]], [by.ptr], act=act)
-            ctx.synchronize()
+    for dt, acts in ((1, (E.ACT_INT8_TOKEN, E.ACT_INT8)), (2, (E.ACT_INT8,))):
+        m = Model(ctx, 5, {f"{i}": sh for i, sh in enumerate(b8)}, lambda n: dt)
+        for act in acts:
+            for i, (n, k) in enumerate(b8):
+                for _ in range(4):
+                    ctx.matmul_dev(bx.ptr, 512, k, [m.w[f"{i}"]], [by.ptr], act=act)
+                ctx.synchronize()
+        m.free()
     bx.free()
     by.free()
-    m.free()
     log("pmc gemm workload done")
 
 
