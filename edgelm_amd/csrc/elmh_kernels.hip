@@ -1873,18 +1873,32 @@ __global__ __launch_bounds__(256) void gemm_lds16_kernel(const GemmArgs a) {
 #undef ELM_L16_STEP
 done:
   if constexpr (QF) {
-    if (t0 < a.T) wave16_store<WDT, SW, TOK>(a, tg, r0 + rw0, t0, lane, iacc, facc);
-    // h for tokens t0 + 4 c4 + i, row r0 + rw0 + l16 (tokens past T were computed from the zero
-    // fragments of the padding; the next GEMM never stores them)
-    const int rc = min(r0 + rw0 + l16, tg.N - 1);
+    // h for tokens t0 + 4 c4 + i, row r0 + rw0 + l16, as wave16_store forms and stores it (tokens past
+    // T were computed from the padding's fragments; nothing stores them but the fragments, which the
+    // next GEMM never stores either)
+    const int r = r0 + rw0 + l16, rc = min(r, tg.N - 1);
     const float ws = WDT == WQ8 ? tg.scales[rc] : 1.f, wsu = WDT == WQ8 ? a.tg[1].scales[rc] : 1.f;
     float hv[4], am[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      // wave16_store's value: q8 facc * ws, q4 facc / 16, then silu(gate) * up
+      // q8 facc * ws, q4 facc / 16, then silu(gate) * up
       const float g = WDT == WQ8 ? facc[0][i] * ws : facc[0][i] * 0.0625f;
       const float u = WDT == WQ8 ? facc[1][i] * wsu : facc[1][i] * 0.0625f;
       hv[i] = silu_exact(g) * u;
+    }
+    if (t0 < a.T) {  // wave-uniform; the stores bounded by T and N as in wave16_store
+      const int tv = min(kWave16, a.T - t0);
+      const uint32_t tbytes = (uint32_t)tv * (uint32_t)tg.N * 4u;
+      const __amdgpu_buffer_rsrc_t ry =
+          __builtin_amdgcn_make_buffer_rsrc(tg.y + (int64_t)t0 * tg.N, (short)0, (int)tbytes, 0x00020000);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int off = r < tg.N ? ((4 * c4 + i) * tg.N + r) * 4 : 0x7FFFFFF0;
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, hv[i]), ry, off, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
       // the amax over the wave's 16 rows (the 16 lanes of each row of the wave)
       float v = fabsf(hv[i]);
       v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
@@ -1896,7 +1910,7 @@ done:
     if (l16 == 0)
 #pragma unroll
       for (int i = 0; i < 4; ++i) ex[(tgw * 2 + rh) * 16 + 4 * c4 + i] = am[i];
-    __syncthreads();
+    lds_barrier();  // the partner wave's amax is in LDS (the h stores stay in flight)
     const int b = r0 / kBlock;  // the workgroup's 32 rows are block b of h
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
