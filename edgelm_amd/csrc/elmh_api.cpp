@@ -113,6 +113,14 @@ int ensure(elmh_ctx* c, DevBuf& b, size_t bytes) {
 
 int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+// Rows per workgroup of the small GEMV (workgroup-quantizing, K <= 2048) for weights of H-row tiles:
+// H (one tile per workgroup) unless ELMH_GEMV_ROWS names a power of two below it (same bits).
+int small_rows(int H) {
+  const char* v = getenv("ELMH_GEMV_ROWS");
+  const int r = v && *v ? atoi(v) : 0;
+  return r > 0 && r < H && !(r & (r - 1)) ? r : H;
+}
+
 
 // Row-tile height of the repacked layout, chosen from dtype and K only (so every weight sharing an
 // input — MATMUL_N, gate/up — agrees). Short rows (K <= 2048) use 8-row tiles: many small decode
@@ -226,14 +234,17 @@ int run_gemv_group(elmh_ctx* c, const float* x, const int8_t* xq, const float* x
     const DevWeight& w0 = w[idx[i0]]->w;
     int all_tiles = 0, tiles[kMaxTargets];
     for (size_t j = 0; j < n; ++j) all_tiles += tiles[j] = (int)(w[idx[i0 + j]]->w.rows_pad / w0.H);
-    a.tpw = x && !stream ? 1 : stream_tpw(w0, T, all_tiles, 1);
+    const bool small = x && !stream;
+    a.tpw = small ? 1 : stream_tpw(w0, T, all_tiles, 1);
+    a.rsub = small ? small_rows(w0.H) : 0;
+    const int split = small ? w0.H / a.rsub : 1;  // small kernel: workgroups per tile
     int wgs = 0;
     a.H = w0.H;
     for (size_t j = 0; j < n; ++j) {
       const DevWeight& wd = w[idx[i0 + j]]->w;
       a.tg[j] = {wd.data, wd.scales, y[idx[i0 + j]], res ? res[idx[i0 + j]] : nullptr, (int)wd.rows, tiles[j]};
       a.tile_start[j] = wgs;
-      wgs += (tiles[j] + a.tpw - 1) / a.tpw;
+      wgs += small ? tiles[j] * split : (tiles[j] + a.tpw - 1) / a.tpw;
     }
     a.tile_start[n] = wgs;
     a.n_targets = (int)n;
@@ -515,7 +526,8 @@ int run_swiglu(elmh_ctx* c, const float* x, int T, int64_t K, const elmh_weight*
     const bool w32 = !qin && xin && T == 1 && !nw && stream_qout_ok(g, (int)K);
     const bool qout = qo && !qo->frag && w32;
     a.tpw = w32 ? 32 / g.H : 1;
-    const int wgs = (tiles + a.tpw - 1) / a.tpw;
+    a.rsub = qin ? small_rows(g.H) : 0;
+    const int wgs = qin ? tiles * (g.H / a.rsub) : (tiles + a.tpw - 1) / a.tpw;
     a.tg[0] = {g.data, g.scales, y, nullptr, (int)g.rows, tiles};
     a.tg[1] = {u.data, u.scales, y, nullptr, (int)u.rows, tiles};
     a.n_targets = 2;

@@ -75,6 +75,8 @@ struct GemvArgs {
   int total_tiles;
   int H;
   int tpw;            // tiles per workgroup (streaming kernel; tile_start then counts workgroups)
+  int rsub;           // small kernel: rows per workgroup, a power of two dividing H (0: H); tile_start
+                      // then counts workgroups
   const float* x;     // f32 [T][K] (quantized inside each workgroup) or null
   int stream;         // with x: the streaming kernel (else the small one) quantizes it
   const float* nw;    // small kernel: x is RMSNORM's input; nw [K] its weight, eps its epsilon

@@ -464,13 +464,17 @@ template <int WDT, int NT, bool SW, bool NORM>
 __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int G = WDT == WQ8 ? 32 : 16;
-  const int K = a.K, nb = a.nb, T = a.T, H = a.H, lgH = __builtin_ctz(H), tid = threadIdx.x;
+  const int K = a.K, nb = a.nb, T = a.T, H = a.H, tid = threadIdx.x;
   const GemvLds L = gemv_lds<NT>(smem, K, nb);
-  int tile = blockIdx.x;
-  const GemvTarget tg = gemv_target<SW>(a, tile);
+  // a workgroup takes RS rows (a power of two dividing H) of an H-row tile: part `part` of tile `tile`
+  const int RS = a.rsub ? a.rsub : H, lgRS = __builtin_ctz(RS), lgsplit = __builtin_ctz(H) - lgRS;
+  int wg = blockIdx.x;
+  const GemvTarget tg = gemv_target<SW>(a, wg);
+  const int tile = wg >> lgsplit, part = wg & ((1 << lgsplit) - 1), n0 = tile * H + part * RS;
+  const int64_t ibase = (int64_t)tile * H * nb + part * RS;  // item (row n0, block 0); (row n0 + r, block b) at + b H + r
   const uint8_t* const wd1 = SW ? a.tg[1].data : tg.data;
   const float* const ws1 = SW ? a.tg[1].scales : tg.scales;
-  const int per_sel = H * nb, items = (SW ? 2 : 1) * per_sel;
+  const int per_sel = RS * nb, items = (SW ? 2 : 1) * per_sel;
   const int nel = T * K;
 
   // 1. every pass's activation values (first: their wait does not cover the weight loads issued
@@ -492,7 +496,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
     const int it = u * kGemvThreads + tid;
     if (it < items) {
       const int sel = SW ? (it >= per_sel) : 0;
-      const int64_t gi = (int64_t)tile * per_sel + (it - sel * per_sel);
+      const int j = it - sel * per_sel;
+      const int64_t gi = ibase + (int64_t)(j >> lgRS) * H + (j & (RS - 1));
       const v4u* src = reinterpret_cast<const v4u*>((sel ? wd1 : tg.data) + gi * G);
       w[u][0] = src[0];
       if (G == 32) w[u][G / 16 - 1] = src[1];
@@ -501,13 +506,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   }
   // 3. epilogue operands of the folding lanes
   float e_res, e_s;
-  chain_epilogue_operands<WDT, SW>(a, tg, tile * H, H, H, tid, e_res, e_s);
+  chain_epilogue_operands<WDT, SW>(a, tg, n0, RS, RS, tid, e_res, e_s);
   if (NORM) {
     // 3b. RMSNORM of the T rows: squares to LDS as [t][accumulator][rowlen] (zero-padded: adding
     // +0.0 to a sum of squares changes nothing), lanes 4t .. 4t+3 sum row t's four accumulators,
     // inv_t = 1 / sqrt(ss / K + eps); then every value becomes (x * inv_t) * w
     const int K4 = K >> 2, rowlen = (K4 + 31) & ~31;
-    float* sq = L.p + (SW ? 2 : 1) * NT * H * L.pst;
+    float* sq = L.p + (SW ? 2 : 1) * NT * RS * L.pst;
     float* inv_l = sq + NT * 4 * rowlen;
 #pragma unroll
     for (int p = 0; p < XP; ++p) {
@@ -576,26 +581,26 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
     const int j = it - sel * per_sel;
     v4u w0, w1;
     float ws;
+    const int b = j >> lgRS, r = j & (RS - 1);
     if (u < 2) {
       w0 = u ? w[1][0] : w[0][0];
       w1 = u ? w[1][G / 16 - 1] : w[0][G / 16 - 1];
       ws = u ? wsc[1] : wsc[0];
     } else {
-      const int64_t gi = (int64_t)tile * per_sel + j;
+      const int64_t gi = ibase + (int64_t)b * H + r;
       const v4u* src = reinterpret_cast<const v4u*>((sel ? wd1 : tg.data) + gi * G);
       w0 = src[0];
       w1 = G == 32 ? src[1] : w0;
       ws = WDT == WQ4 ? (sel ? ws1 : tg.scales)[gi] : 0.f;
     }
-    const int b = j >> lgH, r = j & (H - 1);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
       if (t < T)
-        L.p[((sel * NT + t) * H + r) * L.pst + b] =
+        L.p[((sel * NT + t) * RS + r) * L.pst + b] =
             item_product<WDT>(w0, w1, ws, L.q + t * L.kpad + b * kBlock, L.d[t * nb + b], L.s[t * nb + b]);
   }
   __syncthreads();
-  gemv_fold<WDT, NT, SW>(a, L, tg, tile * H, H, H, tid, e_res, e_s);
+  gemv_fold<WDT, NT, SW>(a, L, tg, n0, RS, RS, tid, e_res, e_s);
 }
 
 // Streaming GEMV: T * K <= kStreamMaxAct activation bytes (staged in LDS).
@@ -2562,10 +2567,12 @@ static hipError_t stream_go(const GemvArgs& a, int wgs, size_t lds, int items, h
 template <int WDT, int NT, bool SW>
 static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
   if (a.T > NT) return hipErrorInvalidValue;
-  const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.x && !a.stream ? a.H : a.tpw * a.H, SW ? 2 : 1);
+  const int rs = a.rsub ? a.rsub : a.H;  // small kernel: rows per workgroup
+  const size_t lds = gemv_lds_bytes(NT, a.K, a.nb, a.x && !a.stream ? rs : a.tpw * a.H, SW ? 2 : 1);
   if (lds > 64 * 1024) return hipErrorInvalidValue;
   if (a.x && !a.stream) {
-    if (!gemv_qin_ok(a.T, a.K) || (a.K & 31) || (a.H & (a.H - 1)) || a.T * a.H * (SW ? 2 : 1) > kGemvThreads)
+    if (!gemv_qin_ok(a.T, a.K) || (a.K & 31) || (a.H & (a.H - 1)) || (rs & (rs - 1)) || rs > a.H ||
+        a.T * rs * (SW ? 2 : 1) > kGemvThreads)
       return hipErrorInvalidValue;
     if (a.nw) {
       const size_t rowlen = ((size_t)(a.K / 4) + 31) & ~(size_t)31;
