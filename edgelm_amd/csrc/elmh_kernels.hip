@@ -375,14 +375,18 @@ __device__ __forceinline__ void gemv_fold(const GemvArgs& a, const GemvLds& L, c
 template <int WDT, bool SW>
 __device__ __forceinline__ void chain_epilogue_operands(const GemvArgs& a, const GemvTarget& tg, int n0, int R, int rows,
                                                         int tid, float& e_res, float& e_s) {
-  e_res = 0.f;
-  e_s = 1.f;
   int sel, pr;
   fold_lane<SW>(tid, sel, pr);
   const int ft = pr / R, fr = pr - ft * R, fn = n0 + fr;
-  if (tid < fold_lanes<SW>(a.T, R) && pr < a.T * R && fr < rows && fn < tg.N) {
-    if (WDT == WQ8) e_s = (sel ? a.tg[1].scales : tg.scales)[fn];
-    if (!SW && tg.res) e_res = tg.res[(int64_t)ft * tg.N + fn];
+  const bool ok = tid < fold_lanes<SW>(a.T, R) && pr < a.T * R && fr < rows && fn < tg.N;
+  // unconditional loads from clamped indices (a conditional load makes the compiler's earlier waits
+  // cover it); lanes that fold nothing drop the values
+  const int fc = min(fn, tg.N - 1), tc = min(ft, a.T - 1);
+  e_s = WDT == WQ8 ? (sel ? a.tg[1].scales : tg.scales)[fc] : 1.f;
+  e_res = !SW && tg.res ? tg.res[(int64_t)tc * tg.N + fc] : 0.f;
+  if (!ok) {
+    e_s = 1.f;
+    e_res = 0.f;
   }
 }
 
@@ -493,16 +497,16 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   float wsc[2] = {0.f, 0.f};
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    const int it = u * kGemvThreads + tid;
-    if (it < items) {
-      const int sel = SW ? (it >= per_sel) : 0;
-      const int j = it - sel * per_sel;
-      const int64_t gi = ibase + (int64_t)(j >> lgRS) * H + (j & (RS - 1));
-      const v4u* src = reinterpret_cast<const v4u*>((sel ? wd1 : tg.data) + gi * G);
-      w[u][0] = src[0];
-      if (G == 32) w[u][G / 16 - 1] = src[1];
-      if (WDT == WQ4) wsc[u] = (sel ? ws1 : tg.scales)[gi];
-    }
+    // unconditional (items past the last repeat it, unused): conditional loads would make the
+    // compiler's waits for x cover these too
+    const int it = min(u * kGemvThreads + tid, items - 1);
+    const int sel = SW ? (it >= per_sel) : 0;
+    const int j = it - sel * per_sel;
+    const int64_t gi = ibase + (int64_t)(j >> lgRS) * H + (j & (RS - 1));
+    const v4u* src = reinterpret_cast<const v4u*>((sel ? wd1 : tg.data) + gi * G);
+    w[u][0] = src[0];
+    if (G == 32) w[u][G / 16 - 1] = src[1];
+    if (WDT == WQ4) wsc[u] = (sel ? ws1 : tg.scales)[gi];
   }
   // 3. epilogue operands of the folding lanes
   float e_res, e_s;
@@ -526,9 +530,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
         r[3 * rowlen] = xv[p].w * xv[p].w;
       }
     }
-    const int padw = rowlen - K4;
-    for (int i = tid; i < T * 4 * padw; i += kGemvThreads) sq[(i / padw) * rowlen + K4 + i % padw] = 0.f;
-    __syncthreads();
+    const int padw = rowlen - K4;  // < 32
+    for (int i = tid; i < T * 4 * 32; i += kGemvThreads)
+      if ((i & 31) < padw) sq[(i >> 5) * rowlen + K4 + (i & 31)] = 0.f;
+    lds_barrier();  // LDS only: the weight items stay in flight through the sums
     if (tid < 4 * T) {
       const float4* row = reinterpret_cast<const float4*>(sq + tid * rowlen);
       float sacc = 0.f;
@@ -548,7 +553,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
       const float ss = s01 + dpp_f<kDppQuadXor2>(s01);
       if ((tid & 3) == 0) inv_l[tid >> 2] = 1.0f / sqrtf(ss / (float)K + a.eps);
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int p = 0; p < XP; ++p) {
       const float inv = inv_l[min(p * kSmallPass + e0, nel - 4) / K];
