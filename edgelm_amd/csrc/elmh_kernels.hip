@@ -17,6 +17,7 @@
 #include "elmh_internal.hpp"
 #include "elm_gemv.h"
 #include "elm_dma.h"
+#include "elm_sum.h"
 
 #include <cstring>
 
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_frag_kernel(const float* __
                                                                  int8_t* __restrict__ xq, float* __restrict__ xd) {
   extern __shared__ __align__(16) float nq_lds[];
   __shared__ float inv_l[kNqTok];
-  const int K4 = K >> 2, rowlen = (K4 + 31) & ~31, nb = K / kBlock;
+  const int K4 = K >> 2, rowlen = norm_rowlen(K), nb = K / kBlock;
   float* sq = nq_lds;  // [kNqTok][4][rowlen]
   const int t0 = blockIdx.x * kNqTok, tid = threadIdx.x, items = kNqTok * nb * 2;
   float4 xv[kNqItems][4], wv[kNqItems][4];
@@ -180,24 +181,12 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_frag_kernel(const float* __
       }
     }
   }
-  const int padw = rowlen - K4;
-  for (int i = tid; i < kNqTok * 4 * padw; i += 256) sq[(i / padw) * rowlen + K4 + i % padw] = 0.f;
+  // +0.0 up to the next multiple of 16 terms
+  for (int i = tid; i < kNqTok * 4 * 16; i += 256)
+    if (K4 + (i & 15) < ((K4 + 15) & ~15)) sq[(i >> 4) * rowlen + K4 + (i & 15)] = 0.f;
   __syncthreads();
   if (tid < 4 * kNqTok) {
-    const float4* row = reinterpret_cast<const float4*>(sq + tid * rowlen);
-    float sacc = 0.f;
-    for (int q0 = 0; q0 < (rowlen >> 2); q0 += 8) {
-      float4 v[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = row[q0 + i];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        sacc = sacc + v[i].x;
-        sacc = sacc + v[i].y;
-        sacc = sacc + v[i].z;
-        sacc = sacc + v[i].w;
-      }
-    }
+    const float sacc = ordered_sum(sq + tid * rowlen, K4, 0.f);
     const float s01 = sacc + dpp_f<kDppQuadXor1>(sacc);
     const float ss = s01 + dpp_f<kDppQuadXor2>(s01);
     if ((tid & 3) == 0) inv_l[tid >> 2] = 1.0f / sqrtf(ss / (float)K + eps);
@@ -515,7 +504,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
     // 3b. RMSNORM of the T rows: squares to LDS as [t][accumulator][rowlen] (zero-padded: adding
     // +0.0 to a sum of squares changes nothing), lanes 4t .. 4t+3 sum row t's four accumulators,
     // inv_t = 1 / sqrt(ss / K + eps); then every value becomes (x * inv_t) * w
-    const int K4 = K >> 2, rowlen = (K4 + 31) & ~31;
+    const int K4 = K >> 2, rowlen = norm_rowlen(K);
     float* sq = L.p + (SW ? 2 : 1) * NT * RS * L.pst;
     float* inv_l = sq + NT * 4 * rowlen;
 #pragma unroll
@@ -530,25 +519,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
         r[3 * rowlen] = xv[p].w * xv[p].w;
       }
     }
-    const int padw = rowlen - K4;  // < 32
-    for (int i = tid; i < T * 4 * 32; i += kGemvThreads)
-      if ((i & 31) < padw) sq[(i >> 5) * rowlen + K4 + (i & 31)] = 0.f;
+    // +0.0 up to the next multiple of 16 terms
+    for (int i = tid; i < T * 4 * 16; i += kGemvThreads)
+      if (K4 + (i & 15) < ((K4 + 15) & ~15)) sq[(i >> 4) * rowlen + K4 + (i & 15)] = 0.f;
     lds_barrier();  // LDS only: the weight items stay in flight through the sums
     if (tid < 4 * T) {
-      const float4* row = reinterpret_cast<const float4*>(sq + tid * rowlen);
-      float sacc = 0.f;
-      for (int q0 = 0; q0 < (rowlen >> 2); q0 += 8) {
-        float4 v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = row[q0 + i];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          sacc = sacc + v[i].x;
-          sacc = sacc + v[i].y;
-          sacc = sacc + v[i].z;
-          sacc = sacc + v[i].w;
-        }
-      }
+      const float sacc = ordered_sum(sq + tid * rowlen, K4, 0.f);
       const float s01 = sacc + dpp_f<kDppQuadXor1>(sacc);
       const float ss = s01 + dpp_f<kDppQuadXor2>(s01);
       if ((tid & 3) == 0) inv_l[tid >> 2] = 1.0f / sqrtf(ss / (float)K + a.eps);
@@ -1986,28 +1962,15 @@ __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
     // squares as [accumulator][rowlen] (zero-padded: adding +0.0 to a sum of squares changes
     // nothing); K % 4 == 0 here (K = 32 nb)
     float* const sq = f32q4_lds + ((((K + 3) & ~3) + NSEL * RT * pst + 3) & ~3);
-    const int K4 = K >> 2, rowlen = (K4 + 31) & ~31;
-    for (int i = threadIdx.x; i < 4 * rowlen; i += 256) {
-      const int c = i / rowlen, j = i - c * rowlen;
+    const int K4 = K >> 2, rowlen = norm_rowlen(K), n16 = (K4 + 15) & ~15;
+    for (int i = threadIdx.x; i < 4 * n16; i += 256) {
+      const int c = i / n16, j = i - c * n16;
       const float v = j < K4 ? a.x[4 * j + c] : 0.f;
-      sq[i] = v * v;
+      sq[c * rowlen + j] = v * v;
     }
     __syncthreads();
     if (threadIdx.x < 4) {
-      const float4* row = reinterpret_cast<const float4*>(sq + threadIdx.x * rowlen);
-      float s = 0.f;
-      for (int q0 = 0; q0 < (rowlen >> 2); q0 += 8) {
-        float4 v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = row[q0 + i];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          s = s + v[i].x;
-          s = s + v[i].y;
-          s = s + v[i].z;
-          s = s + v[i].w;
-        }
-      }
+      const float s = ordered_sum(sq + threadIdx.x * rowlen, K4, 0.f);
       const float s01 = s + dpp_f<kDppQuadXor1>(s);  // lane 0: s0 + s1, lane 2: s2 + s3
       const float ss = s01 + dpp_f<kDppQuadXor2>(s01);
       if (threadIdx.x == 0) inv_s = 1.0f / sqrtf(ss / (float)K + a.eps);
@@ -2504,7 +2467,7 @@ hipError_t launch_act_quant_frag(const float* x, int T, int Tpad, int K, int8_t*
 hipError_t launch_rmsnorm_quant_frag(const float* x, const float* nw, float eps, int T, int Tpad, int K, int8_t* xq,
                                      float* xd, hipStream_t s) {
   if (K % kBlock || K > 2048 || Tpad % kNqTok) return hipErrorInvalidValue;
-  const size_t rowlen = ((size_t)(K / 4) + 31) & ~(size_t)31;
+  const size_t rowlen = (size_t)norm_rowlen(K);
   const size_t lds = (size_t)kNqTok * 4 * rowlen * sizeof(float);
   rmsnorm_quant_frag_kernel<<<Tpad / kNqTok, 256, lds, s>>>(x, nw, eps, T, Tpad, K, xq, xd);
   return hipGetLastError();
@@ -2580,7 +2543,7 @@ static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
         a.T * rs * (SW ? 2 : 1) > kGemvThreads)
       return hipErrorInvalidValue;
     if (a.nw) {
-      const size_t rowlen = ((size_t)(a.K / 4) + 31) & ~(size_t)31;
+      const size_t rowlen = (size_t)norm_rowlen(a.K);
       const size_t ldsn = lds + ((size_t)NT * 4 * rowlen + 4) * sizeof(float);
       if (ldsn > 64 * 1024) return hipErrorInvalidValue;
       gemv_small_kernel<WDT, NT, SW, true><<<tiles, kGemvThreads, ldsn, s>>>(a);
@@ -2781,7 +2744,7 @@ hipError_t launch_gemm_a8(int dtype, int swiglu, int token_mode, const GemmArgs&
 // LDS of gemv_f32act_q4_kernel: x, the (selection, row, group) products and, with RMSNORM, the squares
 static size_t f32q4_lds_bytes(int K, int nb, int H, int nsel, bool norm) {
   const size_t base = ((size_t)((K + 3) & ~3) + (size_t)nsel * H * (nb + 1) + 3) & ~(size_t)3;
-  return (base + (norm ? 4 * (size_t)(((K >> 2) + 31) & ~31) : 0)) * sizeof(float);
+  return (base + (norm ? 4 * (size_t)norm_rowlen(K) : 0)) * sizeof(float);
 }
 
 // Rows per workgroup of gemv_f32act_q4_kernel (a divisor of H): the most rows whose (selection, row,

@@ -11,6 +11,7 @@
 #include "elm_dpp.h"
 #include "elm_expf.h"
 #include "elm_quant.h"
+#include "elm_sum.h"
 #include "elmh_internal.hpp"
 
 namespace elmh {
@@ -483,38 +484,6 @@ __device__ __forceinline__ float dot64_lds(const float* __restrict__ q, const fl
     s3 = s3 + q[4 * u + 3] * kv[u].w;
   }
   return (s0 + s1) + (s2 + s3);
-}
-
-// acc + x_0 + x_1 + ... + x_{16 nbt - 1} in order (nbt <= 16), x_k = row[k]; all 256 values of
-// the row lie in LDS (those past 16 nbt are read ahead but never added). Straight-line code over
-// batches of 16: batch b + 2 is read before batch b is added, and every read is unconditional
-// once its step is reached (the empty asm keeps the compiler from sinking it past the exits), so
-// the wait before a batch's adds covers that batch only. (A loop with the same reads ahead waits
-// for every read at its head: the compiler's wait-count pass merges the exit path's state.)
-__device__ __forceinline__ float ordered_sum256(const float* __restrict__ row, int nbt, float acc) {
-  float4 b[3][4];
-#define ELM_SUM_LOAD(bt)                                                                           \
-  _Pragma("unroll") for (int u = 0; u < 4; ++u) b[(bt) % 3][u] =                                   \
-      *reinterpret_cast<const float4*>(row + 16 * (bt) + 4 * u);                                   \
-  asm volatile("" ::: "memory");
-#define ELM_SUM_STEP(bt)                                                                           \
-  if (nbt <= (bt)) goto done;                                                                      \
-  if ((bt) + 2 < 16) { ELM_SUM_LOAD((bt) + 2) }                                                    \
-  _Pragma("unroll") for (int u = 0; u < 4; ++u) {                                                  \
-    acc = acc + b[(bt) % 3][u].x;                                                                  \
-    acc = acc + b[(bt) % 3][u].y;                                                                  \
-    acc = acc + b[(bt) % 3][u].z;                                                                  \
-    acc = acc + b[(bt) % 3][u].w;                                                                  \
-  }
-  ELM_SUM_LOAD(0)
-  ELM_SUM_LOAD(1)
-  ELM_SUM_STEP(0) ELM_SUM_STEP(1) ELM_SUM_STEP(2) ELM_SUM_STEP(3) ELM_SUM_STEP(4) ELM_SUM_STEP(5)
-  ELM_SUM_STEP(6) ELM_SUM_STEP(7) ELM_SUM_STEP(8) ELM_SUM_STEP(9) ELM_SUM_STEP(10) ELM_SUM_STEP(11)
-  ELM_SUM_STEP(12) ELM_SUM_STEP(13) ELM_SUM_STEP(14) ELM_SUM_STEP(15)
-#undef ELM_SUM_STEP
-#undef ELM_SUM_LOAD
-done:
-  return acc;
 }
 
 // acc + p_0 v_0 + p_1 v_1 + ... + p_k v_k in order, k < 16 nbt (nbt <= NB): each product rounded,
