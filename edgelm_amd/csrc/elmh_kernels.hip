@@ -902,7 +902,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
   typedef GemmRing<WDT, SW, TOK, MT, KBO> R;
   constexpr int TT = R::TT, NSEL = R::NSEL, D = R::D;
   constexpr bool BLOCKX = R::BLOCKX;
-  static_assert(WV == 4 || (WV == 8 && BLOCKX && !SW && R::KB == 1), "eight waves: block-scale modes without SwiGLU");
+  static_assert(WV == 4 || (WV == 8 && !SW && (R::KB == 1 || TOK)), "eight waves: without SwiGLU");
   constexpr int NTW = WV == 8 ? 1 : 2;  // 32-row MFMA tiles per wave
   __shared__ __align__(16) unsigned char ring[R::BYTES];
   __shared__ __align__(16) float Lxdt[TOK ? TT : 4];
@@ -1051,7 +1051,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
 
   // per-token scales of the tile's tokens (the per-token mode's epilogue reads them from LDS)
   if (TOK && tid < TT) Lxdt[tid] = a.xd[t0 + tid];
-  if constexpr (WV == 8 && WDT == WQ4) {
+  if constexpr (WV == 8 && WDT == WQ4 && BLOCKX) {
     // Eight waves, q4, edgelm's per-block rescale, pipelined by one block (block j in slot j % D): step b
     // starts block b's MFMAs from operands read in step b - 1, reads block b's token scales from its
     // slot, then block b + 1's operands, and rescales while those reads are in flight. Slot (b - 1) % D
@@ -1138,17 +1138,17 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
     // are read but add zero.
     constexpr int KB = R::KB;
     static_assert(D % KB == 0, "the ring holds whole groups");
-    auto read_group = [&](v4i (&A)[KB][MT], v4i (&B)[KB][2], int blk0, int k) {
+    auto read_group = [&](v4i (&A)[KB][MT], v4i (&B)[KB][NTW], int blk0, int k) {
       const unsigned char* sb = ring + ((blk0 % D) + k) * R::SLOT;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) A[k][mt] = *reinterpret_cast<const v4i*>(sb + ((wt * MT + mt) * 64 + lane) * 16);
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int rl = wr * 64 + nt * 32 + l32;
+      for (int nt = 0; nt < NTW; ++nt) {
+        const int rl = wr * 64 + (nt0 + nt) * 32 + l32;
         B[k][nt] = *reinterpret_cast<const v4i*>(sb + R::ACT + (2 * rl + (h ^ ((rl >> 3) & 1))) * 16);
       }
     };
-    auto step = [&](v4i (&A)[KB][MT], v4i (&B)[KB][2], v4i (&A2)[KB][MT], v4i (&B2)[KB][2], int b) {
+    auto step = [&](v4i (&A)[KB][MT], v4i (&B)[KB][NTW], v4i (&A2)[KB][MT], v4i (&B2)[KB][NTW], int b) {
       wait_vm<(D - 2 * KB) * R::P>();  // group b + KB has landed (this wave's part)
       lds_barrier();                   // every wave's part; every wave holds group b in registers
       const bool full = b + KB <= nb;  // uniform
@@ -1159,7 +1159,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
         for (int mt = 0; mt < MT; ++mt) {
           const v4i a4 = ok ? A[k][mt] : v4i{0, 0, 0, 0};
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
+          for (int nt = 0; nt < NTW; ++nt)
             iacc[0][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, B[k][nt], iacc[0][mt][nt], 0, 0, 0);
         }
         read_group(A2, B2, b + KB, k);
@@ -1171,7 +1171,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
     for (int i = 0; i < D; ++i) issue(i, i);
     wait_vm<(D - KB) * R::P>();  // group 0 has landed
     lds_barrier();
-    v4i A0[KB][MT], B0[KB][2], A1[KB][MT], B1[KB][2];
+    v4i A0[KB][MT], B0[KB][NTW], A1[KB][MT], B1[KB][NTW];
 #pragma unroll
     for (int k = 0; k < KB; ++k) read_group(A0, B0, 0, k);
     int b = 0;
@@ -2593,8 +2593,11 @@ static void gemm_launch(const GemmArgs& a, dim3 grid, hipStream_t s) {
     gemm_a8_kernel<WDT, SW, TOK, false, MT, 0, WV><<<grid, 64 * WV, 0, s>>>(a);
 }
 
-// The ring GEMM with four or eight waves (eight: block-scale modes without SwiGLU; q8 where the grid
-// gives at most one workgroup per CU, so that four waves would leave one wave per SIMD, q4 always).
+// The ring GEMM with four or eight waves (eight: without SwiGLU; q8 in the block-scale mode where the
+// grid gives at most one workgroup per CU, so that four waves would leave one wave per SIMD, q4
+// always; per-token q8, whose loop is all MFMA, measured slower with eight: 26.4 -> 28.4 us at
+// 4096 x 4096, 61.8 -> 65.4 us at 4096 x 14336, while per-token q4 gained: 63.8 -> 51.5, 99.7 -> 97.8,
+// 189.7 -> 140.1 us).
 // Measured at T = 512: q8 4096 x 4096 59.2 -> 48.3 us, 4096 x 14336 173.4 -> 133.4 us, while 14336 x
 // 4096 with 448 workgroups went from 98.8 to 103.7 us; q4 (pipelined eight-wave loop) 78.0 -> 60.6,
 // 228.7 -> 160.7 and, at 448 workgroups, 125.8 -> 120.2 us. ELMH_GEMM_WAVES=4 or 8 forces one, same
@@ -2602,8 +2605,8 @@ static void gemm_launch(const GemmArgs& a, dim3 grid, hipStream_t s) {
 template <int WDT, bool SW, bool TOK, int MT>
 static void gemm_launch_waves(const GemmArgs& a, int wgs, int cus, hipStream_t s) {
   const dim3 grid((wgs + 7) / 8 * 8);
-  if constexpr (!TOK && !SW) {
-    bool eight = WDT == WQ4 || wgs <= cus;
+  if constexpr (!SW) {
+    bool eight = WDT == WQ4 || (!TOK && wgs <= cus);
     if (const char* ev = getenv("ELMH_GEMM_WAVES")) eight = ev[0] == '8' ? true : ev[0] == '4' ? false : eight;
     if (eight) return gemm_launch<WDT, SW, TOK, MT, 8>(a, grid, s);
   }
