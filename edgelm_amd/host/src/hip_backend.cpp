@@ -18,8 +18,11 @@
 // at least kMinGraphOps ops as one HIP graph: the first such step runs op by op (allocating
 // buffers and uploading weights), the second is captured, with attention reading the position
 // from device memory; every later step uploads the host-side inputs (token ids) and the
-// position, launches the graph, and copies back what the host reads (the logits). A buffer that
-// has to grow (a longer prefill) drops the graphs. EDGELM_HIP_GRAPHS=0 turns graphs off.
+// position, launches the graph, and copies back what the host reads (the logits). Prefill
+// forwards (T > 1) replay graphs the same way, one per (partition, T, first position), since
+// their kernels take the length and the position as arguments; at most kMaxPrefillGraphs are
+// kept. A buffer that has to grow (a longer prefill) drops the graphs. EDGELM_HIP_GRAPHS=0 turns
+// graphs off, EDGELM_HIP_PREFILL_GRAPHS=0 the prefill graphs only.
 //
 // keep_output() and argmax_output() (the greedy-sampling hooks) leave the logits in HBM and hand
 // the host only the argmax of their last row.
@@ -27,6 +30,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <tuple>
 #include <unordered_map>
 
 #include "edgelm/backend.hpp"
@@ -46,6 +50,8 @@ class HipBackend : public Backend {
   HipBackend(int device, bool layer_ops) : layer_ops_(layer_ops) {
     const char* g = std::getenv("EDGELM_HIP_GRAPHS");
     graphs_on_ = !(g && g[0] == '0');
+    const char* pg = std::getenv("EDGELM_HIP_PREFILL_GRAPHS");
+    prefill_graphs_on_ = !(pg && pg[0] == '0');
     if (device < 0) return;
     if (elmh_create(device, &ctx_) != ELMH_OK)
       throw std::runtime_error(std::string("edgelm: hip backend unavailable: ") + elmh_last_error(nullptr));
@@ -150,10 +156,14 @@ class HipBackend : public Backend {
   // overrides where Backend declares it; false: the Session runs the partition op by op
   bool run_partition(const Partition& p, ExecContext& c) {
     // a graph launch costs ~100 us of host time: only long partitions gain from replaying one
-    if (!graphs_on_ || !ctx_ || !prepared_ || c.T != 1 || c.L != 1 || p.end - p.begin < kMinGraphOps) return false;
+    if (!graphs_on_ || !ctx_ || !prepared_ || c.L != 1 || p.end - p.begin < kMinGraphOps) return false;
+    const bool step = c.T == 1;
+    if (!step && !prefill_graphs_on_) return false;
     const Graph& g = *c.graph;
-    StepGraph& sg = graphs_[p.begin];
-    if (sg.warm == 0) {
+    const auto pkey = std::make_tuple(p.begin, c.T, c.pos0);
+    if (!step && prefill_.size() >= kMaxPrefillGraphs && !prefill_.count(pkey)) drop_prefill_graphs();
+    StepGraph& sg = step ? graphs_[p.begin] : prefill_[pkey];
+    if (step && sg.warm == 0) {
       // a captured step reads its position from device memory and sizes attention's score row for the
       // whole cache; past the kernel's limit the partition runs op by op, sized by the position in use
       for (int i = p.begin; i < p.end; ++i) {
@@ -519,6 +529,12 @@ class HipBackend : public Backend {
     for (auto& kv : graphs_)
       if (kv.second.exec) elmh_graph_destroy(ctx_, kv.second.exec);
     graphs_.clear();
+    drop_prefill_graphs();
+  }
+  void drop_prefill_graphs() {
+    for (auto& kv : prefill_)
+      if (kv.second.exec) elmh_graph_destroy(ctx_, kv.second.exec);
+    prefill_.clear();
   }
   // what run() checks on the host each time, for a replayed step: token ids and positions in range
   void step_checks(const Partition& p, const ExecContext& c) const {
@@ -526,11 +542,12 @@ class HipBackend : public Backend {
     for (int i = p.begin; i < p.end; ++i) {
       const Op& op = g.ops[i];
       if (op.type == OpType::EMBED) {
-        const int32_t tok = *reinterpret_cast<const int32_t*>(c.f(op.in[0]));
-        EDGELM_CHECK(tok >= 0 && tok < c.tensor(op.in[1]).rows, "token id out of range");
+        const int32_t* tok = reinterpret_cast<const int32_t*>(c.f(op.in[0]));
+        for (int t = 0; t < c.T; ++t)
+          EDGELM_CHECK(tok[t] >= 0 && tok[t] < c.tensor(op.in[1]).rows, "token id out of range");
       } else if (op.type == OpType::ATTENTION) {
-        EDGELM_CHECK(c.pos0 + 1 <= c.kv[op.iattr[0]].max_ctx, "context overflow");
-        EDGELM_CHECK(!op.iattr[3] || c.pos0 + 1 <= rope_pos_, "position beyond rope table");
+        EDGELM_CHECK(c.pos0 + c.T <= c.kv[op.iattr[0]].max_ctx, "context overflow");
+        EDGELM_CHECK(!op.iattr[3] || c.pos0 + c.T <= rope_pos_, "position beyond rope table");
       }
     }
   }
@@ -683,6 +700,11 @@ class HipBackend : public Backend {
   bool capturing_ = false;
   uint64_t buffer_gen_ = 0;
   std::map<int, StepGraph> graphs_;  // by the partition's first op
+  // prefill forwards (T > 1) replayed as graphs, by (the partition's first op, T, first position):
+  // their kernels take the length and the position as arguments
+  bool prefill_graphs_on_ = true;
+  static constexpr size_t kMaxPrefillGraphs = 8;
+  std::map<std::tuple<int, int, int>, StepGraph> prefill_;
   int32_t* pos_dev_ = nullptr;
   elmh_ctx* ctx_ = nullptr;
   bool prepared_ = false;

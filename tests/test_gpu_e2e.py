@@ -162,6 +162,34 @@ def test_decode_graphs_survive_larger_forwards(tiny, dt):
     mine.close(), ref.close()
 
 
+def test_prefill_graphs_replay_bit_identical_to_edgelm(smollm):
+    """Prefill forwards (T > 1) of a whole partition replay a HIP graph per (length, first position)
+    from the second forward of that shape on: a replay must take the new forward's token ids, and a
+    chunk at another position must not replay the first chunk's graph. Five rounds of a 24-token
+    prompt at position 0, a 24-token chunk at position 24 and a decode step, with fresh tokens every
+    round (round 0 runs op by op, round 1 captures, rounds 2-4 replay): every row of every forward's
+    logits bit-identical to edgelm's session."""
+    m = host.Model(smollm)
+    mine = host.Session(m, "hip,cpu", threads=8, max_ctx=64, max_batch=24, all_logits=True, act_quant=True)
+    ref = O.RefSession(smollm, "cpu", threads=16, max_ctx=64, max_batch=24, all_logits=True, act_quant=True)
+    r = np.random.default_rng(31)
+    for rnd in range(5):
+        mine.reset(), ref.reset()
+        for what, n in (("prompt", 24), ("chunk", 24), ("decode", 1)):
+            toks = r.integers(0, 49152, n).astype(np.int32)
+            print(f"[gpu] prefill graphs round {rnd}: {what} of {n} at position {mine.pos()}", flush=True)
+            a, b = mine.forward(toks), ref.forward(toks)
+            assert bits_equal(a, b), f"round {rnd} {what}: max diff {np.abs(a - b).max()}"
+    assert mine.pos() == 49
+    # a replayed prefill checks every token id on the host, as run() and edgelm's Session do
+    mine.reset()
+    bad = r.integers(0, 49152, 24).astype(np.int32)
+    bad[5] = 49152
+    with pytest.raises(RuntimeError, match="token id out of range"):
+        mine.forward(bad)
+    mine.close(), ref.close()
+
+
 @pytest.mark.parametrize("backends", ["hip,cpu", "hip-matmul,cpu"])
 def test_greedy_steps_match_edgelm(smollm, backends):
     """Session::greedy_steps: with "hip,cpu" the steps are queued back to back, each one's token fed to the
