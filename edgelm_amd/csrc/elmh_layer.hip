@@ -551,7 +551,8 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
   float* const kn = qb + HD;
   __shared__ float red[4];
   __shared__ float inv_s;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index as a scalar: loops over it stay scalar loops instead of divergent ones
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.x, grp = n_heads / n_kv, kvh = h / grp;
   const float* const kh = kc + (int64_t)kvh * max_ctx * HD;
   const float* const vh = vc + (int64_t)kvh * max_ctx * HD;
@@ -864,7 +865,8 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
   float* const vb = kb + R * HD;         // [R][64]
   float* const sc = vb + R * HD;         // [kAttnQ][scs]
   float* const qb = sc + kAttnQ * scs;   // [kAttnQ][64]
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // the wave index as a scalar: loops over it stay scalar loops instead of divergent ones
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ngr = (T + kAttnQ - 1) / kAttnQ;
   const int h = blockIdx.x / ngr, t0 = (blockIdx.x - h * ngr) * kAttnQ;
   const int nq = min(kAttnQ, T - t0);                                   // queries in this group
@@ -877,13 +879,17 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
   // rows [c0, c0 + rows) of a cache (or, from pos0 on, of the step's rows of kv head kvh) into a
   // buffer: wave w moves 1 KB pieces w, w + 4, ... (4 rows each, lane -> row lane / 16, slot
   // lane % 16); the last piece repeats the last row
+  // (each lane's source is picked without a branch, so that the copies issue back to back)
   auto dma_rows = [&](const float* cache, const float* step, int c0, int rows, float* dst, bool swz) {
+    const int64_t sstride = (int64_t)n_kv * HD;
+    const float* const sbase = (fresh ? step : cache) + (fresh ? (int64_t)kvh * HD - (int64_t)pos0 * sstride : 0);
     for (int pc = w; 4 * pc < rows; pc += 4) {
       const int r = 4 * pc + (lane >> 4), s = lane & 15, p = c0 + min(r, rows - 1);
       const int ch = (swz ? s ^ (r & 15) : s) * 4;
-      const float* const src = fresh && p >= pos0 ? step + ((int64_t)(p - pos0) * n_kv + kvh) * HD + ch
-                                                  : cache + (int64_t)p * HD + ch;
-      dma16(src, reinterpret_cast<unsigned char*>(dst) + pc * 1024);
+      const bool st = fresh && p >= pos0;
+      const int64_t off = (int64_t)p * (st ? sstride : (int64_t)HD) + ch;
+      const uint64_t src = st ? (uint64_t)(size_t)sbase : (uint64_t)(size_t)cache;
+      dma16(reinterpret_cast<const float*>(src) + off, reinterpret_cast<unsigned char*>(dst) + pc * 1024);
     }
   };
   // the step's key rows of [c0, c0 + rows) rotated in place, pairs (i, i + 32): thread task
