@@ -897,7 +897,17 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
   // are loaded at the start (cpre)
   constexpr int kRotTasks = R * 8 / 256;
   float4 cpre[kRotTasks][2];
+  // Every task's pair is read before the first is written (the tasks' slots are disjoint), so the
+  // reads wait for LDS once instead of once per task.
   auto rotate_rows = [&](int c0, int rows, bool pre) {
+    float4 a[kRotTasks], b[kRotTasks];
+#pragma unroll
+    for (int m = 0; m < kRotTasks; ++m) {
+      const int task = tid + 256 * m, r = task >> 3, u = task & 7;
+      const float* const row = kb + min(r, rows - 1) * HD;
+      a[m] = *reinterpret_cast<const float4*>(row + ((u ^ (r & 15)) << 2));
+      b[m] = *reinterpret_cast<const float4*>(row + (((u + 8) ^ (r & 15)) << 2));
+    }
 #pragma unroll
     for (int m = 0; m < kRotTasks; ++m) {
       const int task = tid + 256 * m, r = task >> 3, u = task & 7, p = c0 + r;
@@ -907,9 +917,9 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
         float4* const hi = reinterpret_cast<float4*>(row + (((u + 8) ^ (r & 15)) << 2));
         const float4 c = pre ? cpre[m][0] : *reinterpret_cast<const float4*>(rcos + (int64_t)p * H2 + 4 * u);
         const float4 sn = pre ? cpre[m][1] : *reinterpret_cast<const float4*>(rsin + (int64_t)p * H2 + 4 * u);
-        const float4 a = *lo, b = *hi;
-        *lo = make_float4(a.x * c.x - b.x * sn.x, a.y * c.y - b.y * sn.y, a.z * c.z - b.z * sn.z, a.w * c.w - b.w * sn.w);
-        *hi = make_float4(b.x * c.x + a.x * sn.x, b.y * c.y + a.y * sn.y, b.z * c.z + a.z * sn.z, b.w * c.w + a.w * sn.w);
+        const float4 x = a[m], y = b[m];
+        *lo = make_float4(x.x * c.x - y.x * sn.x, x.y * c.y - y.y * sn.y, x.z * c.z - y.z * sn.z, x.w * c.w - y.w * sn.w);
+        *hi = make_float4(y.x * c.x + x.x * sn.x, y.y * c.y + x.y * sn.y, y.z * c.z + x.z * sn.z, y.w * c.w + x.w * sn.w);
       }
     }
   };
@@ -969,6 +979,12 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
   static_assert(R == 128 && kAttnQ == 4, "two threads per key row, two queries each");
   const float scale = 1.0f / sqrtf((float)HD);
   const int srow = tid & (R - 1), sq0 = 2 * (tid >> 7);
+  // the wave's two queries in registers, read once (every lane reads the same values)
+  float4 qv[2][16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int u = 0; u < 16; ++u) qv[i][u] = *reinterpret_cast<const float4*>(qb + (sq0 + i) * HD + 4 * u);
   for (int c0 = 0; c0 < nmax; c0 += R) {
     if (c0 > 0) {  // the next key chunk, once every thread has scored the previous one
       __syncthreads();
@@ -988,16 +1004,16 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
 #pragma unroll
       for (int u = 0; u < 16; ++u) kv[u] = *reinterpret_cast<const float4*>(row + ((u ^ sw) << 2));
 #pragma unroll
-      for (int qi = sq0; qi < sq0 + 2; ++qi) {
+      for (int i = 0; i < 2; ++i) {
+        const int qi = sq0 + i;
         if (qi < nq && j <= pos0 + t0 + qi) {
-          const float* const qq = qb + qi * HD;
           float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
           for (int u = 0; u < 16; ++u) {
-            s0 = s0 + qq[4 * u] * kv[u].x;
-            s1 = s1 + qq[4 * u + 1] * kv[u].y;
-            s2 = s2 + qq[4 * u + 2] * kv[u].z;
-            s3 = s3 + qq[4 * u + 3] * kv[u].w;
+            s0 = s0 + qv[i][u].x * kv[u].x;
+            s1 = s1 + qv[i][u].y * kv[u].y;
+            s2 = s2 + qv[i][u].z * kv[u].z;
+            s3 = s3 + qv[i][u].w * kv[u].w;
           }
           sc[qi * scs + j] = ((s0 + s1) + (s2 + s3)) * scale;
         }
