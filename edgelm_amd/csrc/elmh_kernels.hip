@@ -430,13 +430,14 @@ __device__ __forceinline__ GemvTarget target_at(const GemvArgs& a, int ti) {
   return t;
 }
 
-// The target owning workgroup (or tile) index `wg`, which is made relative to that target. The
-// tile starts are fetched with the other launch arguments in one batch of scalar loads; the
-// target's fields then take one more (uniform) load.
-template <bool SW>
+// The target owning workgroup (or tile) index `wg`, which is made relative to that target. A launch
+// of one target (MT false: every call but a fused QKV) reads the first target's fields with its other
+// launch arguments in one batch of scalar loads; with more, the tile starts pick the target and its
+// fields take one more (uniform) load.
+template <bool SW, bool MT = true>
 __device__ __forceinline__ GemvTarget gemv_target(const GemvArgs& a, int& wg) {
-  if (SW) return a.tg[0];
-  const int n = pin_sgpr(a.n_targets);
+  if (SW || !MT) return a.tg[0];
+  const int n = a.n_targets;
   const int ts1 = pin_sgpr(a.tile_start[1]), ts2 = pin_sgpr(a.tile_start[2]), ts3 = pin_sgpr(a.tile_start[3]);
   const int ti = (n > 1 && wg >= ts1) + (n > 2 && wg >= ts2) + (n > 3 && wg >= ts3);
   wg -= ti == 0 ? 0 : ti == 1 ? ts1 : ti == 2 ? ts2 : ts3;
@@ -453,16 +454,27 @@ constexpr int kSmallMaxAct = 4 * kSmallPass;
 // (cpu::rmsnorm, kernels_cpu.cpp:326-335, in the order of rmsnorm_kernel: squares grouped by
 // dot_f32_scalar's four accumulators, four in-order sums, (s0 + s1) + (s2 + s3), then
 // (x * inv) * w), so that RMSNORM and the matmul after it take one launch.
-template <int WDT, int NT, bool SW, bool NORM>
+template <int WDT, int NT, bool SW, bool NORM, bool MT>
 __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int G = WDT == WQ8 ? 32 : 16;
+  // every launch argument this kernel reads, in scalar registers before anything else: the
+  // compiler issues their loads as one batch (one round trip to the argument segment) instead of
+  // loading each near its first use, behind the waits for the ones before
+  if (MT && !SW)
+    asm volatile("" ::"s"(a.x), "s"(a.T), "s"(a.K), "s"(a.nb), "s"(a.H), "s"(a.rsub), "s"(a.n_targets),
+                 "s"(a.tile_start[1]), "s"(a.tile_start[2]), "s"(a.tile_start[3]), "s"(a.tile_start[4]));
+  else
+    asm volatile("" ::"s"(a.x), "s"(a.T), "s"(a.K), "s"(a.nb), "s"(a.H), "s"(a.rsub), "s"(a.tg[0].data),
+                 "s"(a.tg[0].scales), "s"(a.tg[0].y), "s"(a.tg[0].res), "s"(a.tg[0].N));
+  if (NORM) asm volatile("" ::"s"(a.nw), "s"(a.eps));
+  if (SW) asm volatile("" ::"s"(a.tg[1].data), "s"(a.tg[1].scales));
   const int K = a.K, nb = a.nb, T = a.T, H = a.H, tid = threadIdx.x;
   const GemvLds L = gemv_lds<NT>(smem, K, nb);
   // a workgroup takes RS rows (a power of two dividing H) of an H-row tile: part `part` of tile `tile`
   const int RS = a.rsub ? a.rsub : H, lgRS = __builtin_ctz(RS), lgsplit = __builtin_ctz(H) - lgRS;
   int wg = blockIdx.x;
-  const GemvTarget tg = gemv_target<SW>(a, wg);
+  const GemvTarget tg = gemv_target<SW, MT>(a, wg);
   const int tile = wg >> lgsplit, part = wg & ((1 << lgsplit) - 1), n0 = tile * H + part * RS;
   const int64_t ibase = (int64_t)tile * H * nb + part * RS;  // item (row n0, block 0); (row n0 + r, block b) at + b H + r
   const uint8_t* const wd1 = SW ? a.tg[1].data : tg.data;
@@ -2546,9 +2558,21 @@ static hipError_t gemv_go(const GemvArgs& a, int tiles, hipStream_t s) {
       const size_t rowlen = (size_t)norm_rowlen(a.K);
       const size_t ldsn = lds + ((size_t)NT * 4 * rowlen + 4) * sizeof(float);
       if (ldsn > 64 * 1024) return hipErrorInvalidValue;
-      gemv_small_kernel<WDT, NT, SW, true><<<tiles, kGemvThreads, ldsn, s>>>(a);
+      if constexpr (!SW) {
+        if (a.n_targets > 1) {
+          gemv_small_kernel<WDT, NT, false, true, true><<<tiles, kGemvThreads, ldsn, s>>>(a);
+          return hipGetLastError();
+        }
+      }
+      gemv_small_kernel<WDT, NT, SW, true, false><<<tiles, kGemvThreads, ldsn, s>>>(a);
     } else {
-      gemv_small_kernel<WDT, NT, SW, false><<<tiles, kGemvThreads, lds, s>>>(a);
+      if constexpr (!SW) {
+        if (a.n_targets > 1) {
+          gemv_small_kernel<WDT, NT, false, false, true><<<tiles, kGemvThreads, lds, s>>>(a);
+          return hipGetLastError();
+        }
+      }
+      gemv_small_kernel<WDT, NT, SW, false, false><<<tiles, kGemvThreads, lds, s>>>(a);
     }
     return hipGetLastError();
   }
