@@ -631,16 +631,31 @@ __device__ __forceinline__ float fold_range(float acc, const float* row, int b0,
 // only the last batch's share is left once the last weight has arrived. Without the fold wave
 // (FW false: short rows, where the extra wave costs more than the chain) the producers fold at
 // the end, one lane per (token, row).
-template <int WDT, int NT, bool SW, int IPT, int NPW, int DEPTH, bool FW, bool QIN, bool QOUT = false>
+template <int WDT, int NT, bool SW, int IPT, int NPW, int DEPTH, bool FW, bool QIN, bool QOUT, bool MT>
 __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const GemvArgs a) {
   static_assert(!QOUT || (SW && !FW && NT == 1), "quantized output: SwiGLU, one token, folds at the end");
   constexpr int P = 64 * NPW;  // producer threads
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int G = WDT == WQ8 ? 32 : 16;
+  // every launch argument the kernel reads, in scalar registers first: one batch of loads, one
+  // round trip to the argument segment (as the small GEMV)
+  asm volatile("" ::"s"(a.T), "s"(a.K), "s"(a.nb), "s"(a.H), "s"(a.tpw));
+  if (QIN)
+    asm volatile("" ::"s"(a.x));
+  else
+    asm volatile("" ::"s"(a.xq), "s"(a.xd), "s"(a.xs));
+  if (MT && !SW)
+    asm volatile("" ::"s"(a.n_targets), "s"(a.tile_start[1]), "s"(a.tile_start[2]), "s"(a.tile_start[3]),
+                 "s"(a.tile_start[4]));
+  else
+    asm volatile("" ::"s"(a.tg[0].data), "s"(a.tg[0].scales), "s"(a.tg[0].y), "s"(a.tg[0].res), "s"(a.tg[0].N),
+                 "s"(a.tg[0].tiles));
+  if (SW) asm volatile("" ::"s"(a.tg[1].data), "s"(a.tg[1].scales));
+  if (QOUT) asm volatile("" ::"s"(a.oq), "s"(a.od), "s"(a.os));
   const int K = a.K, nb = a.nb, T = a.T, H = a.H, tid = threadIdx.x;
   const GemvLds L = gemv_lds<NT>(smem, K, nb);
   int wg = blockIdx.x;
-  const GemvTarget tg = gemv_target<SW>(a, wg);
+  const GemvTarget tg = gemv_target<SW, MT>(a, wg);
   const int tile0 = wg * a.tpw;
   const int ntl = min(a.tpw, tg.tiles - tile0);
   const int R = a.tpw * H;      // LDS row slots per token
@@ -1705,9 +1720,27 @@ __host__ __device__ inline int gemm_lds16_bytes(int nb) {
   return (TW / 32 * nb + P) * 1024 + xd + NSEL * (bw + bs) + (QF ? 1024 : 0);
 }
 
-template <int WDT, bool SW, bool TOK, bool FAST, bool QF = false>
+template <int WDT, bool SW, bool TOK, bool FAST, bool QF, bool MT>
 __global__ __launch_bounds__(256) void gemm_lds16_kernel(const GemmArgs a) {
   static_assert(!QF || (SW && !TOK), "quantized h: SwiGLU in block mode");
+  // every launch argument the kernel reads, in scalar registers first, through one asm statement (loads
+  // feeding one statement go out as one batch: one round trip to the argument segment; the GEMVs do
+  // the same). MT: more than one target (a fused QKV).
+  // (T goes through the statement, so that the tile arithmetic on it cannot start before it)
+  int Ta = a.T;
+  if constexpr (MT)
+    asm volatile("" : "+s"(Ta) : "s"(a.xq), "s"(a.xd), "s"(a.Tpad), "s"(a.nb), "s"(a.H), "s"(a.n_targets),
+                 "s"(a.tg[0].N), "s"(a.tg[1].N), "s"(a.tg[2].N), "s"(a.tg[3].N));
+  else if constexpr (QF)
+    asm volatile("" : "+s"(Ta) : "s"(a.xq), "s"(a.xd), "s"(a.Tpad), "s"(a.nb), "s"(a.H), "s"(a.tg[0].N),
+                 "s"(a.tg[0].data), "s"(a.tg[0].scales), "s"(a.tg[0].y), "s"(a.tg[1].data), "s"(a.tg[1].scales),
+                 "s"(a.oq), "s"(a.od), "s"(a.onb));
+  else if constexpr (SW)
+    asm volatile("" : "+s"(Ta) : "s"(a.xq), "s"(a.xd), "s"(a.Tpad), "s"(a.nb), "s"(a.H), "s"(a.tg[0].N),
+                 "s"(a.tg[0].data), "s"(a.tg[0].scales), "s"(a.tg[0].y), "s"(a.tg[1].data), "s"(a.tg[1].scales));
+  else
+    asm volatile("" : "+s"(Ta) : "s"(a.xq), "s"(a.xd), "s"(a.Tpad), "s"(a.nb), "s"(a.H), "s"(a.tg[0].N),
+                 "s"(a.tg[0].data), "s"(a.tg[0].scales), "s"(a.tg[0].y), "s"(a.tg[0].res));
   typedef Wave16Ops<WDT, SW, TOK> Ops;
   constexpr int NSEL = Ops::NSEL, G = WDT == WQ8 ? 32 : 16;
   constexpr bool BLOCKX = Ops::BLOCKX;
@@ -1718,19 +1751,21 @@ __global__ __launch_bounds__(256) void gemm_lds16_kernel(const GemmArgs a) {
   const int rh = QF ? wave & 1 : 0, tgw = QF ? wave >> 1 : wave;  // the wave's row half, token group
   const int nb = a.nb, H = a.H;
   // workgroup -> (target, RW-row tile, TW-token chunk), chunk fastest
-  const int nchunk = (a.T + TW - 1) / TW;
+  const int nchunk = (Ta + TW - 1) / TW;
   int rt = (int)blockIdx.x;
   const int ch = rt % nchunk;
   rt /= nchunk;
-  int ti = 0;
-  const int n = SW ? 1 : a.n_targets;
-  for (; ti < n; ++ti) {
-    const int cnt = (a.tg[ti].N + RW - 1) / RW;
-    if (rt < cnt) break;
-    rt -= cnt;
-  }
+  // the target: with one, the first; with more, from every target's tile count (N's read in the
+  // first batch), then its fields at its index
+  const int n = MT ? a.n_targets : 1;
+  const int e1 = (pin_sgpr(a.tg[0].N) + RW - 1) / RW;
+  const int e2 = MT ? e1 + (pin_sgpr(a.tg[1].N) + RW - 1) / RW : e1;
+  const int e3 = MT ? e2 + (pin_sgpr(a.tg[2].N) + RW - 1) / RW : e2;
+  const int e4 = MT ? e3 + (pin_sgpr(a.tg[3].N) + RW - 1) / RW : e3;
+  const int ti = (rt >= e1) + (n > 1 && rt >= e2) + (n > 2 && rt >= e3) + (n > 3 && rt >= e4);
   if (ti >= n) return;  // past the last tile (uniform per workgroup; no barrier below)
-  const GemmTarget tg = SW ? a.tg[0] : gemm_target_at(ti);
+  rt -= ti == 0 ? 0 : ti == 1 ? e1 : ti == 2 ? e2 : e3;
+  const GemmTarget tg = MT ? gemm_target_at(ti) : a.tg[0];
   const int r0 = rt * RW, tc = ch * TW;
   const uint8_t* const wd[2] = {tg.data, SW ? a.tg[1].data : tg.data};
   const float* const wsc[2] = {tg.scales, SW ? a.tg[1].scales : tg.scales};
@@ -2521,21 +2556,30 @@ int gemv_stream_ipt(int dtype, int items, int producers) {
   return per <= 4 ? 4 : per <= 8 ? 8 : 16;
 }
 
-template <int WDT, int NT, bool SW, int NPW, bool FW, bool QIN, bool QOUT = false>
-static hipError_t stream_launch(const GemvArgs& a, int wgs, size_t lds, int items, hipStream_t s) {
+// MT: the launch has more than one target (a fused QKV); only such launches look the target up.
+template <int WDT, int NT, bool SW, int NPW, bool FW, bool QIN, bool QOUT, bool MT>
+static hipError_t stream_launch_mt(const GemvArgs& a, int wgs, size_t lds, int items, hipStream_t s) {
   constexpr int threads = 64 * (NPW + FW);
   switch (gemv_stream_ipt(WDT, items, 64 * NPW)) {
-    case 4: gemv_stream_kernel<WDT, NT, SW, 4, NPW, FW ? 2 : 4, FW, QIN, QOUT><<<wgs, threads, lds, s>>>(a); break;
-    case 8: gemv_stream_kernel<WDT, NT, SW, 8, NPW, FW ? 2 : 4, FW, QIN, QOUT><<<wgs, threads, lds, s>>>(a); break;
+    case 4: gemv_stream_kernel<WDT, NT, SW, 4, NPW, FW ? 2 : 4, FW, QIN, QOUT, MT><<<wgs, threads, lds, s>>>(a); break;
+    case 8: gemv_stream_kernel<WDT, NT, SW, 8, NPW, FW ? 2 : 4, FW, QIN, QOUT, MT><<<wgs, threads, lds, s>>>(a); break;
     case 16:
       if (WDT == WQ4) {
-        gemv_stream_kernel<WDT, NT, SW, 16, NPW, FW ? 2 : 4, FW, QIN, QOUT><<<wgs, threads, lds, s>>>(a);
+        gemv_stream_kernel<WDT, NT, SW, 16, NPW, FW ? 2 : 4, FW, QIN, QOUT, MT><<<wgs, threads, lds, s>>>(a);
         break;
       }
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int WDT, int NT, bool SW, int NPW, bool FW, bool QIN, bool QOUT = false>
+static hipError_t stream_launch(const GemvArgs& a, int wgs, size_t lds, int items, hipStream_t s) {
+  if constexpr (!SW) {
+    if (a.n_targets > 1) return stream_launch_mt<WDT, NT, false, NPW, FW, QIN, QOUT, true>(a, wgs, lds, items, s);
+  }
+  return stream_launch_mt<WDT, NT, SW, NPW, FW, QIN, QOUT, false>(a, wgs, lds, items, s);
 }
 
 template <int WDT, int NT, bool SW, int NPW, bool FW>
@@ -2666,22 +2710,29 @@ template <int WDT, bool SW, bool TOK, bool QF = false>
 static bool gemm_lds16_launch(const GemmArgs& a, hipStream_t s) {
   const int bytes = gemm_lds16_bytes<WDT, SW, TOK, QF>(a.nb);
   if (a.nb > kLds16MaxBlocks || bytes > (int)kMaxLds - 1024 || a.H < 4 || (a.H & (a.H - 1))) return false;
-  const void* k = a.fast && !(TOK && WDT == WQ8) ? (const void*)gemm_lds16_kernel<WDT, SW, TOK, true, QF>
-                                                  : (const void*)gemm_lds16_kernel<WDT, SW, TOK, false, QF>;
-  static bool raised[2] = {false, false};  // the LDS limit, once per kernel
-  const int which = a.fast && !(TOK && WDT == WQ8) ? 1 : 0;
+  const bool fast = a.fast && !(TOK && WDT == WQ8), mt = !SW && a.n_targets > 1;
+  // the kernel for (fast, more than one target); SwiGLU has one
+  const void* const ks[4] = {(const void*)gemm_lds16_kernel<WDT, SW, TOK, false, QF, false>,
+                             (const void*)gemm_lds16_kernel<WDT, SW, TOK, true, QF, false>,
+                             (const void*)gemm_lds16_kernel<WDT, SW, TOK, false, QF, !SW>,
+                             (const void*)gemm_lds16_kernel<WDT, SW, TOK, true, QF, !SW>};
+  static bool raised[4] = {false, false, false, false};  // the LDS limit, once per kernel
+  const int which = (mt ? 2 : 0) + (fast ? 1 : 0);
   if (!raised[which]) {
-    if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds - 1024) != hipSuccess) return false;
+    if (hipFuncSetAttribute(ks[which], hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds - 1024) != hipSuccess)
+      return false;
     raised[which] = true;
   }
   constexpr int RW = QF ? 32 : 16, TW = QF ? 32 : 64;
   int rows = 0;
   for (int i = 0; i < (SW ? 1 : a.n_targets); ++i) rows += (a.tg[i].N + RW - 1) / RW;
   const dim3 grid(rows * ((a.T + TW - 1) / TW));
-  if (which)
-    gemm_lds16_kernel<WDT, SW, TOK, true, QF><<<grid, 256, bytes, s>>>(a);
-  else
-    gemm_lds16_kernel<WDT, SW, TOK, false, QF><<<grid, 256, bytes, s>>>(a);
+  switch (which) {
+    case 0: gemm_lds16_kernel<WDT, SW, TOK, false, QF, false><<<grid, 256, bytes, s>>>(a); break;
+    case 1: gemm_lds16_kernel<WDT, SW, TOK, true, QF, false><<<grid, 256, bytes, s>>>(a); break;
+    case 2: gemm_lds16_kernel<WDT, SW, TOK, false, QF, !SW><<<grid, 256, bytes, s>>>(a); break;
+    default: gemm_lds16_kernel<WDT, SW, TOK, true, QF, !SW><<<grid, 256, bytes, s>>>(a); break;
+  }
   return true;
 }
 

@@ -543,6 +543,11 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
     const int* __restrict__ pos_dev, int n_heads, int n_kv, int max_ctx, int n_cap, const float* __restrict__ rcos,
     const float* __restrict__ rsin, const float* __restrict__ knew, const float* __restrict__ vnew) {
   constexpr int HD = 64, H2 = 32, C = kDecRows, ROWB = HD * 4;
+  // Every argument into scalar registers before anything else: their loads go out as one batch, so the
+  // first memory requests wait for one round trip to the argument segment (loaded near their first
+  // uses instead, they took three, one behind the other).
+  asm volatile("" ::"s"(q), "s"(out), "s"(kc), "s"(vc), "s"(pos0), "s"(pos_dev), "s"(n_heads), "s"(n_kv),
+               "s"(max_ctx), "s"(n_cap), "s"(rcos), "s"(rsin), "s"(knew), "s"(vnew));
   extern __shared__ __align__(16) float lds[];
   float* const kb = lds;
   float* const vb = kb + C * HD;
@@ -859,6 +864,9 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
     int8_t* __restrict__ xq, float* __restrict__ xd, int Tpad, const float* __restrict__ knew,
     const float* __restrict__ vnew) {
   constexpr int HD = 64, H2 = 32, R = kPfRows, ROWB = HD * 4;
+  // every argument into scalar registers first, in one batch of loads (as the decode kernel)
+  asm volatile("" ::"s"(q), "s"(out), "s"(kc), "s"(vc), "s"(pos0), "s"(T), "s"(n_heads), "s"(n_kv), "s"(max_ctx),
+               "s"(n_cap), "s"(rcos), "s"(rsin), "s"(xq), "s"(xd), "s"(Tpad), "s"(knew), "s"(vnew));
   extern __shared__ __align__(16) float lds[];
   const int scs = (n_cap + 255) & ~255;  // score row stride
   float* const kb = lds;                 // [R][64]
@@ -1082,6 +1090,9 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ 
                                                     const uint8_t* __restrict__ data,
                                                     const float* __restrict__ scales, int dtype, int64_t cols,
                                                     int64_t nb, int H, int64_t rows, float* __restrict__ y) {
+  // every argument into scalar registers first, in one batch of loads (as the attention kernels)
+  asm volatile("" ::"s"(tok), "s"(total), "s"(data), "s"(scales), "s"(dtype), "s"(cols), "s"(nb), "s"(H), "s"(rows),
+               "s"(y), "s"(gridDim.x));
   for (int64_t idx = blockIdx.x * 256ll + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
     const int64_t t = idx / cols, k = idx - t * cols;
     // ids are the caller's to check (edgelm checks them on the host); clamping keeps a bad id in bounds
