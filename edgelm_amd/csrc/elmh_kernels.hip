@@ -69,6 +69,9 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, const float* __re
 __global__ __launch_bounds__(256) void act_quant_rows_kernel(const float* __restrict__ x, int T, int K,
                                                              int8_t* __restrict__ xq, float* __restrict__ xd,
                                                              int32_t* __restrict__ xs) {
+  // every argument in scalar registers first, through one statement: their loads go out together and
+  // the arithmetic on T and K waits for the statement (one round trip to the argument segment)
+  asm volatile("" : "+s"(T), "+s"(K) : "s"(x), "s"(xq), "s"(xd), "s"(xs));
   const int nb = K / kBlock;
   const int g = blockIdx.x * 32 + (threadIdx.x >> 3), l = (threadIdx.x & 7) * 4;
   const bool ok = g < T * nb;
@@ -120,6 +123,8 @@ __device__ __forceinline__ int64_t frag_offset(int t, int b, int h, int nb) { re
 // writes one whole 1 KB fragment; the block scale comes from the amax of lanes L and L ^ 32.
 __global__ __launch_bounds__(256) void act_quant_frag_kernel(const float* __restrict__ x, int T, int Tpad, int K,
                                                              int8_t* __restrict__ xq, float* __restrict__ xd) {
+  // every argument in scalar registers first, through one statement (as act_quant_rows_kernel)
+  asm volatile("" : "+s"(T), "+s"(Tpad), "+s"(K) : "s"(x), "s"(xq), "s"(xd));
   const int nb = K / kBlock, g = blockIdx.x, lane = threadIdx.x & 63;
   const int b = blockIdx.y * 4 + (threadIdx.x >> 6);
   if (b >= nb) return;  // whole waves
@@ -1964,6 +1969,33 @@ done:
 
 // ---------------------------------------------------------------- f32-activation paths
 
+// The target owning tile `tile` of an f32-activation launch (tile made relative to it): the target
+// count and the tile starts, pinned in scalar registers, come with the kernel's other arguments in
+// one batch of scalar loads; the target's fields then take one more (uniform) load through the
+// argument segment, instead of the tile starts one per step of a search and an indexed copy.
+template <bool SW>
+__device__ __forceinline__ GemvTarget f32_target(const F32Args& a, int& tile) {
+  if (SW) return a.tg[0];
+  // one statement pins the lookup's values and takes the kernels' other arguments as inputs, so that
+  // all of their loads go out together
+  int n = a.n_targets, ts0 = a.tile_start[0], ts1 = a.tile_start[1], ts2 = a.tile_start[2], ts3 = a.tile_start[3];
+  asm volatile("" : "+s"(n), "+s"(ts0), "+s"(ts1), "+s"(ts2), "+s"(ts3)
+               : "s"(a.H), "s"(a.x), "s"(a.T), "s"(a.K), "s"(a.nb), "s"(a.nw), "s"(a.eps), "s"(a.rt));
+  const int ti = (n > 1 && tile >= ts1) + (n > 2 && tile >= ts2) + (n > 3 && tile >= ts3);
+  tile -= ti == 0 ? ts0 : ti == 1 ? ts1 : ti == 2 ? ts2 : ts3;
+  typedef const F32Args __attribute__((address_space(4)))* KernArgs;
+  const KernArgs ka = (KernArgs)__builtin_amdgcn_kernarg_segment_ptr();
+  GemvTarget t;
+  t.data = pin_global(ka->tg[ti].data);
+  t.scales = pin_global(ka->tg[ti].scales);
+  t.y = pin_global(ka->tg[ti].y);
+  t.res = pin_global(ka->tg[ti].res);
+  t.N = ka->tg[ti].N;
+  t.tiles = ka->tg[ti].tiles;
+  return t;
+}
+
+
 // T == 1, q4, one workgroup per H-row tile (of the target, or of gate and up with SW): dot_q4's
 // operations (kernels_cpu.cpp:397-399) spread over the groups instead of one lane walking the row.
 // Every (selection, row, group) item is (g0 + g1) * ws_g, g0 / g1 the in-order 16-term sums of the
@@ -1980,12 +2012,8 @@ __global__ __launch_bounds__(256) void gemv_f32act_q4_kernel(const F32Args a) {
   const int K = a.K, nb = a.nb, H = a.H, RT = a.rt, lgRT = __builtin_ctz(RT), pst = nb + 1;
   float* const sx = f32q4_lds;                // [K]
   float* const P = f32q4_lds + ((K + 3) & ~3);  // [NSEL][RT][nb + 1]
-  int ti = 0, tile = blockIdx.x;
-  if (!SW) {
-    while (ti + 1 < a.n_targets && tile >= a.tile_start[ti + 1]) ++ti;
-    tile -= a.tile_start[ti];
-  }
-  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  int tile = blockIdx.x;
+  const GemvTarget tg = f32_target<SW>(a, tile);
   const int per_sel = RT * nb, items = NSEL * per_sel, n0 = tile * RT;
   const int64_t ibase = (int64_t)(n0 / H) * nb * H + n0 % H;  // item (row n0, group 0)
   // the first item's weights go out before x is staged, so that the two loads overlap
@@ -2080,12 +2108,8 @@ __global__ __launch_bounds__(256) void gemv_f32act_q8_prod_kernel(const F32Args 
   extern __shared__ __align__(16) float q8p_lds[];
   constexpr int NSEL = SW ? 2 : 1;
   const int K = a.K, K4 = K & ~3, Lq = K4 >> 2, Lr = q8p_stride(K), H = a.H, nb = a.nb, tid = threadIdx.x;
-  int ti = 0, grp = blockIdx.x;
-  if (!SW) {
-    while (ti + 1 < a.n_targets && grp >= a.tile_start[ti + 1]) ++ti;
-    grp -= a.tile_start[ti];
-  }
-  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  int grp = blockIdx.x;
+  const GemvTarget tg = f32_target<SW>(a, grp);
   const int n0 = grp * kQ8PRows;  // rows past N: padding (rows_pad % 64 == 0)
   float* const sx = q8p_lds;
   float* const P = q8p_lds + ((K + 3) & ~3);  // [NSEL][kQ8PRows][4][Lr]
@@ -2161,12 +2185,8 @@ __global__ __launch_bounds__(64) void gemv_f32act_q8_lds_kernel(const F32Args a)
   extern __shared__ __align__(16) unsigned char q8l_lds[];
   constexpr int NSEL = SW ? 2 : 1;
   const int K = a.K, K4 = K & ~3, H = a.H, nb = a.nb, cpr = 2 * nb + 1, lane = threadIdx.x;
-  int ti = 0, grp = blockIdx.x;
-  if (!SW) {
-    while (ti + 1 < a.n_targets && grp >= a.tile_start[ti + 1]) ++ti;
-    grp -= a.tile_start[ti];
-  }
-  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  int grp = blockIdx.x;
+  const GemvTarget tg = f32_target<SW>(a, grp);
   const int n0 = grp * kQ8F32LdsRows;  // rows past N: padding (rows_pad % 64 == 0)
   const int nch = q8f32_chunks(nb, NSEL);
   unsigned char* const wl = q8l_lds;
@@ -2231,12 +2251,8 @@ template <bool SW>
 __global__ __launch_bounds__(64) void gemv_f32act_q8_kernel(const F32Args a) {
   extern __shared__ __align__(16) float f32q8_lds[];
   const int K = a.K, K4 = K & ~3, H = a.H;
-  int ti = 0, grp = blockIdx.x;
-  if (!SW) {
-    while (ti + 1 < a.n_targets && grp >= a.tile_start[ti + 1]) ++ti;
-    grp -= a.tile_start[ti];
-  }
-  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  int grp = blockIdx.x;
+  const GemvTarget tg = f32_target<SW>(a, grp);
   // rows past N: padding (rows_pad % 64 == 0)
   const int c = threadIdx.x & 3, n = grp * kQ8F32Rows + (threadIdx.x >> 2);
   const int64_t nbase = (int64_t)(n / H) * a.nb * H + (n % H);
@@ -2359,12 +2375,8 @@ constexpr int kF32Ahead = 4;  // 16-element steps whose weights are in flight
 template <int WDT, bool SW>
 __global__ __launch_bounds__(256) void gemm_f32act_kernel(const F32Args a) {
   __shared__ __align__(16) float sxp[kF32TT][4][kF32ChainStride];
-  int ti = 0, grp = blockIdx.y;
-  if (!SW) {
-    while (ti + 1 < a.n_targets && grp >= a.tile_start[ti + 1]) ++ti;
-    grp -= a.tile_start[ti];
-  }
-  const GemvTarget& tg = a.tg[SW ? 0 : ti];
+  int grp = blockIdx.y;
+  const GemvTarget tg = f32_target<SW>(a, grp);
   const int K = a.K, K4 = K & ~3, H = a.H, nb = a.nb, T = a.T;
   const int t0 = blockIdx.x * kF32TT, c = threadIdx.x & 3;
   const int n = grp * 64 + (threadIdx.x >> 2);  // rows past N: padding (rows_pad % 64 == 0)
