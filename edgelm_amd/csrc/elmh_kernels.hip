@@ -1733,9 +1733,18 @@ __global__ __launch_bounds__(256) void gemm_lds16_kernel(const GemmArgs a) {
   // the same). MT: more than one target (a fused QKV).
   // (T goes through the statement, so that the tile arithmetic on it cannot start before it)
   int Ta = a.T;
+  // MT: every target's fields, pinned through the statement, so that the target is picked by selects
+  // instead of a second load at its index
+  const uint8_t *d0 = a.tg[0].data, *d1 = a.tg[1].data, *d2 = a.tg[2].data, *d3 = a.tg[3].data;
+  const float *s0 = a.tg[0].scales, *s1 = a.tg[1].scales, *s2 = a.tg[2].scales, *s3 = a.tg[3].scales;
+  float *y0 = a.tg[0].y, *y1 = a.tg[1].y, *y2 = a.tg[2].y, *y3 = a.tg[3].y;
+  const float *q0 = a.tg[0].res, *q1 = a.tg[1].res, *q2 = a.tg[2].res, *q3 = a.tg[3].res;
   if constexpr (MT)
-    asm volatile("" : "+s"(Ta) : "s"(a.xq), "s"(a.xd), "s"(a.Tpad), "s"(a.nb), "s"(a.H), "s"(a.n_targets),
-                 "s"(a.tg[0].N), "s"(a.tg[1].N), "s"(a.tg[2].N), "s"(a.tg[3].N));
+    asm volatile(""
+                 : "+s"(Ta), "+s"(d0), "+s"(d1), "+s"(d2), "+s"(d3), "+s"(s0), "+s"(s1), "+s"(s2), "+s"(s3), "+s"(y0),
+                   "+s"(y1), "+s"(y2), "+s"(y3), "+s"(q0), "+s"(q1), "+s"(q2), "+s"(q3)
+                 : "s"(a.xq), "s"(a.xd), "s"(a.Tpad), "s"(a.nb), "s"(a.H), "s"(a.n_targets), "s"(a.tg[0].N),
+                   "s"(a.tg[1].N), "s"(a.tg[2].N), "s"(a.tg[3].N));
   else if constexpr (QF)
     asm volatile("" : "+s"(Ta) : "s"(a.xq), "s"(a.xd), "s"(a.Tpad), "s"(a.nb), "s"(a.H), "s"(a.tg[0].N),
                  "s"(a.tg[0].data), "s"(a.tg[0].scales), "s"(a.tg[0].y), "s"(a.tg[1].data), "s"(a.tg[1].scales),
@@ -1770,7 +1779,17 @@ __global__ __launch_bounds__(256) void gemm_lds16_kernel(const GemmArgs a) {
   const int ti = (rt >= e1) + (n > 1 && rt >= e2) + (n > 2 && rt >= e3) + (n > 3 && rt >= e4);
   if (ti >= n) return;  // past the last tile (uniform per workgroup; no barrier below)
   rt -= ti == 0 ? 0 : ti == 1 ? e1 : ti == 2 ? e2 : e3;
-  const GemmTarget tg = MT ? gemm_target_at(ti) : a.tg[0];
+  GemmTarget tg;
+  if constexpr (MT) {
+    tg.data = pin_global(ti == 0 ? d0 : ti == 1 ? d1 : ti == 2 ? d2 : d3);
+    tg.scales = pin_global(ti == 0 ? s0 : ti == 1 ? s1 : ti == 2 ? s2 : s3);
+    tg.y = pin_global(ti == 0 ? y0 : ti == 1 ? y1 : ti == 2 ? y2 : y3);
+    tg.res = pin_global(ti == 0 ? q0 : ti == 1 ? q1 : ti == 2 ? q2 : q3);
+    tg.N = ti == 0 ? a.tg[0].N : ti == 1 ? a.tg[1].N : ti == 2 ? a.tg[2].N : a.tg[3].N;
+    tg.ntiles = 0;  // not read here
+  } else {
+    tg = a.tg[0];
+  }
   const int r0 = rt * RW, tc = ch * TW;
   const uint8_t* const wd[2] = {tg.data, SW ? a.tg[1].data : tg.data};
   const float* const wsc[2] = {tg.scales, SW ? a.tg[1].scales : tg.scales};
