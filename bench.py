@@ -861,7 +861,7 @@ def main():
             # stream, and its algorithmic bytes are the down projection's (the larger of its two calls)
             dom_name = "MATMUL_ADD down"
             dom = per[dom_name]
-            roof = {"kernel": "gemv_small_kernel<2, 1, false, false> (" + dom_name + " 576x1536 q4 + residual, T=1)",
+            roof = {"kernel": "gemv_small_kernel<2, 1, false, false, false> (" + dom_name + " 576x1536 q4 + residual, T=1)",
                     "bound": "hbm", "achieved": round(dom["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(dom["GBs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_name),
                     "algorithmic_bytes_per_launch": dom["bytes"], "avg_launch_us": round(dom["us"], 3),
