@@ -486,16 +486,21 @@ __device__ __forceinline__ float dot64_lds(const float* __restrict__ q, const fl
   return (s0 + s1) + (s2 + s3);
 }
 
-// acc + p_0 v_0 + p_1 v_1 + ... + p_k v_k in order, k < 16 nbt (nbt <= NB): each product rounded,
-// then added (cpu::attention's o_i += p_j * v_j[i] without contraction), p_j = pj[j] and
-// v_j = vcol[64 j]; the reads stay below 16 NB values of each. Straight-line code over batches of
-// 16, as ordered_sum256: batch b + 2 is read and batch b + 1's products are formed while batch b's
+// acc + p_0 v_0 + p_1 v_1 + ... + p_{n-1} v_{n-1} in order (n <= 16 NB): each product rounded, then
+// added (cpu::attention's o_i += p_j * v_j[i] without contraction), p_j = pj[j] and v_j = vcol[64 j];
+// the reads stay below 16 NB values of each. Straight-line code over batches of 16, as
+// ordered_sum256: batch b + 2 is read and batch b + 1's products are formed while batch b's
 // products are added, so the dependent adds alternate with independent multiplies (the empty asm
-// keeps each product in its step instead of sunk to the step that adds it).
+// keeps each product in its step instead of sunk to the step that adds it). The last, partial
+// batch is added from the same registers, the products past n replaced by +0.0: acc starts at +0.0
+// and a sum of floats that starts at +0.0 is never -0.0 (x + y = -0.0 needs x = y = -0.0), so each
+// of those adds leaves acc unchanged (one loop step per position with its own LDS round trip cost
+// up to 0.5 us for the last 15 positions).
 template <int NB>
-__device__ __forceinline__ float ordered_dot_col(const float* __restrict__ pj, const float* __restrict__ vcol, int nbt,
+__device__ __forceinline__ float ordered_dot_col(const float* __restrict__ pj, const float* __restrict__ vcol, int n,
                                                  float acc) {
-  float pv[3][16], xv[3][16], pr[2][16];
+  const int nbt = n >> 4, rem = n & 15;
+  float pv[3][16], xv[3][16], pr[2][16], tl[16];
 #define ELM_DOT_LOAD(bt)                                                                           \
   _Pragma("unroll") for (int u = 0; u < 16; ++u) {                                                 \
     pv[(bt) % 3][u] = pj[16 * (bt) + u];                                                           \
@@ -503,7 +508,10 @@ __device__ __forceinline__ float ordered_dot_col(const float* __restrict__ pj, c
   }                                                                                                \
   asm volatile("" ::: "memory");
 #define ELM_DOT_STEP(bt)                                                                           \
-  if (nbt <= (bt)) goto done;                                                                      \
+  if (nbt <= (bt)) {                                                                               \
+    _Pragma("unroll") for (int u = 0; u < 16; ++u) tl[u] = pr[(bt) % 2][u];                        \
+    goto tail;                                                                                     \
+  }                                                                                                \
   if ((bt) + 2 < NB) { ELM_DOT_LOAD((bt) + 2) }                                                    \
   _Pragma("unroll") for (int u = 0; u < 16; ++u) {                                                 \
     if ((bt) + 1 < NB) {                                                                           \
@@ -534,7 +542,12 @@ __device__ __forceinline__ float ordered_dot_col(const float* __restrict__ pj, c
   if (NB > 15) { ELM_DOT_STEP(15) }
 #undef ELM_DOT_STEP
 #undef ELM_DOT_LOAD
-done:
+  return acc;
+tail:
+  if (rem > 0) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) acc = acc + (u < rem ? tl[u] : 0.f);
+  }
   return acc;
 }
 
@@ -680,12 +693,9 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
         dma16s(vh, (uint32_t)((nx + min(r, rows - 1)) * ROWB + ((lane & 15) << 4)), dst + pc * 1024);
       }
     }
-    if (wave == 0) {  // 16 positions per batch (C / 16 at most), then the rest one by one
-      const int m = min(C, nc - c0), nbt = m >> 4;
-      const float* const pj = sc + c0;
-      const float* const vcol = cur + lane;
-      acc = ordered_dot_col<kDecRows / 16>(pj, vcol, nbt, acc);
-      for (int j = nbt * 16; j < m; ++j) acc = acc + pj[j] * vcol[j * HD];
+    if (wave == 0) {  // 16 positions per batch (C / 16 at most), the last batch partial
+      const int m = min(C, nc - c0);
+      acc = ordered_dot_col<kDecRows / 16>(sc + c0, cur + lane, m, acc);
     }
     if (nx < nc) {
       wait_vm<0>();
@@ -1054,11 +1064,8 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
     const float* const cur = (ci & 1) ? kb : vb;
     const int nx = c0 + R;
     if (nx < nmax) dma_rows(vh, vnew, nx, min(R, nmax - nx), (ci & 1) ? vb : kb, false);
-    const int m = min(R, nw - c0), nbt = max(m, 0) >> 4;  // this query's positions in the chunk
-    const float* const pj = sw + c0;
-    const float* const vcol = cur + lane;
-    acc = ordered_dot_col<R / 16>(pj, vcol, nbt, acc);
-    for (int j = nbt * 16; j < m; ++j) acc = acc + pj[j] * vcol[j * HD];
+    const int m = max(min(R, nw - c0), 0);  // this query's positions in the chunk
+    acc = ordered_dot_col<R / 16>(sw + c0, cur + lane, m, acc);
     if (nx < nmax) {
       wait_vm<0>();
       __syncthreads();  // every wave is done with this chunk; the next one has landed
