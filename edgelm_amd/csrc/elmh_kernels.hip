@@ -878,7 +878,8 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
 // (direct to LDS: no staging registers, so D - 1 blocks are in flight). Every wave issues the same
 // P DMA instructions per slot, so "my part of block b has landed" is a fixed vmcnt((D - 2) * P);
 // one barrier per block then makes every part visible and frees the slot computed one block
-// earlier. Issues past the last block repeat the last block, which keeps the count fixed.
+// earlier (q8 in the per-block mode: one wait and one barrier per group of six blocks). Issues past
+// the last block repeat the last block, which keeps the count fixed.
 // Workgroups are numbered so that each XCD (workgroup index mod 8) takes a contiguous range of
 // (row tile, token tile) pairs, token tile fastest: an XCD's L2 keeps its own weight rows.
 //
@@ -914,7 +915,7 @@ struct GemmRing {
   static constexpr int WSEL = WDT == WQ8 ? kGemmTileN * 32 : kGemmTileN * 20;  // q8 [2][128][16]; q4 [128][16] + [128] f32
   static constexpr int XD = BLOCKX ? TT * 4 : 0;
   static constexpr int SLOT = ACT + NSEL * WSEL + XD;
-  // ring depth: whole block groups in the per-token q8 loop (KB below), one block otherwise
+  // ring depth: whole block groups where blocks are grouped per barrier (KB below), one block otherwise
   static constexpr int KBQ = TOK && WDT == WQ8 && !SW && KBO == 0 ? (MT == 1 ? 4 : 2) : (KBO ? KBO : 1);
   static constexpr int D0 = (76 * 1024) / SLOT < 4 ? 4 : (76 * 1024) / SLOT;
   static constexpr int D = KBQ > 1 ? D0 / KBQ * KBQ : D0;
@@ -922,7 +923,7 @@ struct GemmRing {
   // blocks per barrier: the per-token q8 loop is a few MFMAs per block, so its barrier, fragment
   // reads and DMA issues are grouped over KB blocks, and the ring holds whole groups
   static constexpr int KB = KBO ? KBO : TOK && WDT == WQ8 && !SW ? (MT == 1 ? 4 : 2) : 1;
-  static_assert(D >= 2 * KB + 1 || (KB > 1 && D >= 3 * KB), "ring too shallow for the block group");
+  static_assert(D >= 2 * KB + 1 || (KB > 1 && D >= 3 * KB) || (BLOCKX && D >= 2 * KB), "ring too shallow for the block group");
   static constexpr int EP = SW ? 4 * 2 * 32 * 32 * 4 : 16;                     // SwiGLU epilogue: gate and up per wave
   static constexpr int BYTES = D * SLOT > EP ? D * SLOT : EP;
   static_assert((D - KB) * P < 64, "vmcnt range");
@@ -934,7 +935,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
   typedef GemmRing<WDT, SW, TOK, MT, KBO> R;
   constexpr int TT = R::TT, NSEL = R::NSEL, D = R::D;
   constexpr bool BLOCKX = R::BLOCKX;
-  static_assert(WV == 4 || (WV == 8 && !SW && (R::KB == 1 || TOK)), "eight waves: without SwiGLU");
+  static_assert(WV == 4 || (WV == 8 && !SW && (R::KB == 1 || TOK || BLOCKX)), "eight waves: without SwiGLU");
   constexpr int NTW = WV == 8 ? 1 : 2;  // 32-row MFMA tiles per wave
   __shared__ __align__(16) unsigned char ring[R::BYTES];
   __shared__ __align__(16) float Lxdt[TOK ? TT : 4];
@@ -1148,6 +1149,25 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
       step(A1, B1, c1, A0, B0, c0, b + 1);
     }
     if (b < nb) step(A0, B0, c0, A1, B1, c1, b);  // reads block nb's slot (a repeat of the last block)
+  } else if constexpr (BLOCKX && R::KB > 1) {
+    // edgelm's per-block rescale with one wait and one barrier per group of KB blocks (block j in
+    // slot j % D, D a multiple of KB) instead of per block. Step g waits until group g has landed,
+    // refills group g - 1's slots (every wave is past them once the barrier opens) with the blocks
+    // D - KB further on, then computes group g's blocks in order; the waves may drift by up to a
+    // group between barriers. Blocks past the last are issued (repeats of it) but not computed.
+    constexpr int KB = R::KB;
+    static_assert(D % KB == 0 && D >= 2 * KB, "the ring holds whole groups, two at least");
+#pragma unroll
+    for (int i = 0; i < D - KB; ++i) issue(i, i);
+    for (int b = 0; b < nb; b += KB) {
+      wait_vm<(D - 2 * KB) * R::P>();  // group b / KB has landed (this wave's part)
+      lds_barrier();                   // every wave's part; every wave is done with the group before
+#pragma unroll
+      for (int k = 0; k < KB; ++k) issue(b + D - KB + k, (b + D - KB + k) % D);
+#pragma unroll
+      for (int k = 0; k < KB; ++k)
+        if (b + k < nb) block((b + k) % D);
+    }
   } else if constexpr (R::KB == 1) {
 #pragma unroll
     for (int i = 0; i < D - 1; ++i) issue(i, i);
@@ -2685,6 +2705,20 @@ hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_ti
 
 template <int WDT, bool SW, bool TOK, int MT, int WV = 4>
 static void gemm_launch(const GemmArgs& a, dim3 grid, hipStream_t s) {
+  // q8 in edgelm's per-block mode, 64-token tiles: one barrier per group of six blocks (measured at
+  // T = 512 against one per block: 4096 x 4096 47.7 -> 45.6 us, 4096 x 14336 126.1 -> 117.8 us,
+  // 14336 x 4096 95.0 -> 95.9 us; four blocks per group 46.3 / 121.1 / 96.5 us, two 51.3 / 144.6 /
+  // 98.4 us). ELMH_GEMM_KB=1 keeps one barrier per block; same bits.
+  if constexpr (WDT == WQ8 && !SW && !TOK && MT == 1) {
+    const char* ev = getenv("ELMH_GEMM_KB");
+    if (!(ev && ev[0] == '1')) {
+      if (a.fast)
+        gemm_a8_kernel<WDT, SW, TOK, true, MT, 6, WV><<<grid, 64 * WV, 0, s>>>(a);
+      else
+        gemm_a8_kernel<WDT, SW, TOK, false, MT, 6, WV><<<grid, 64 * WV, 0, s>>>(a);
+      return;
+    }
+  }
   // the per-token q8 accumulation is all-integer: FAST changes nothing there
   if (a.fast && !(TOK && WDT == WQ8))
     gemm_a8_kernel<WDT, SW, TOK, true, MT, 0, WV><<<grid, 64 * WV, 0, s>>>(a);

@@ -354,10 +354,13 @@ def test_gemm_token_tiles(ctx, dt, tile, monkeypatch):
     one) over several token tiles with a ragged last one and a partial last row tile: per-block
     int8 (exact, fast, residual), per-token int8 (block groups with a partial last group: K = 576
     is 18 blocks), MATMUL_N and FFN_SWIGLU. The tile height is forced with four and with eight waves
-    per workgroup (ELMH_GEMM_WAVES; eight serve the block-scale modes without SwiGLU)."""
+    per workgroup (ELMH_GEMM_WAVES; eight serve the block-scale modes without SwiGLU), and the q8
+    per-block ring with one barrier per block (ELMH_GEMM_KB=1) as well as per group of six blocks."""
     for waves in ("8", "4"):
         monkeypatch.setenv("ELMH_GEMM_WAVES", waves)
-        check_token_tiles(ctx, dt, tile, monkeypatch)
+        for kb in ("6", "1") if dt == O.Q8 else ("6",):
+            monkeypatch.setenv("ELMH_GEMM_KB", kb)
+            check_token_tiles(ctx, dt, tile, monkeypatch)
 
 
 def check_token_tiles(ctx, dt, tile, monkeypatch):
@@ -368,7 +371,8 @@ def check_token_tiles(ctx, dt, tile, monkeypatch):
     wg, wu = weight(r, n, k, dt), weight(r, n, k, dt)
     dw, dw2, dg, du = up(ctx, w), up(ctx, w2), up(ctx, wg), up(ctx, wu)
     for T in [65, 130, 257, 512]:
-        print(f"[gpu] gemm tile={tile} waves={os.environ.get('ELMH_GEMM_WAVES')} dt={dt} T={T}", flush=True)
+        print(f"[gpu] gemm tile={tile} waves={os.environ.get('ELMH_GEMM_WAVES')} kb={os.environ.get('ELMH_GEMM_KB')} "
+              f"dt={dt} T={T}", flush=True)
         x = r.normal(0, 1, (T, k)).astype(np.float32)
         res = r.normal(0, 1, (T, n)).astype(np.float32)
         got = ctx.matmul(x, [dw, dw2], [res, None], act=E.ACT_INT8, mode=E.EXACT)
