@@ -878,7 +878,7 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
 // (direct to LDS: no staging registers, so D - 1 blocks are in flight). Every wave issues the same
 // P DMA instructions per slot, so "my part of block b has landed" is a fixed vmcnt((D - 2) * P);
 // one barrier per block then makes every part visible and frees the slot computed one block
-// earlier (q8 in the per-block mode: one wait and one barrier per group of six blocks). Issues past
+// earlier (the per-block mode at 64-token tiles: one wait and one barrier per group of six blocks). Issues past
 // the last block repeat the last block, which keeps the count fixed.
 // Workgroups are numbered so that each XCD (workgroup index mod 8) takes a contiguous range of
 // (row tile, token tile) pairs, token tile fastest: an XCD's L2 keeps its own weight rows.
@@ -1084,7 +1084,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
 
   // per-token scales of the tile's tokens (the per-token mode's epilogue reads them from LDS)
   if (TOK && tid < TT) Lxdt[tid] = a.xd[t0 + tid];
-  if constexpr (WV == 8 && WDT == WQ4 && BLOCKX) {
+  if constexpr (WV == 8 && WDT == WQ4 && BLOCKX && R::KB == 1) {
     // Eight waves, q4, edgelm's per-block rescale, pipelined by one block (block j in slot j % D): step b
     // starts block b's MFMAs from operands read in step b - 1, reads block b's token scales from its
     // slot, then block b + 1's operands, and rescales while those reads are in flight. Slot (b - 1) % D
@@ -1092,6 +1092,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
     // any more; block b + 1 has landed once at most D - 3 blocks are in flight. Measured at T = 512
     // against the loop below: q4 4096 x 4096 60.4 -> 57.8 us, 4096 x 14336 174.0 -> 162.4 us; q8 lost
     // (48.0 -> 51.7, 127.4 -> 146.4 us), and prefetching the 16 token scales as well spilled or lost.
+    // (128-token tiles, and 64-token tiles with ELMH_GEMM_KB=1: the grouped loop below measured faster.)
     static_assert(D >= 4, "ring too shallow for the eight-wave pipeline");
     auto read_ops = [&](v4i (&A)[MT], v4i& B, float& c, int blk) {
       const unsigned char* sb = ring + (blk % D) * R::SLOT;
@@ -2705,11 +2706,12 @@ hipError_t launch_gemv_a8(int dtype, int swiglu, const GemvArgs& a, int total_ti
 
 template <int WDT, bool SW, bool TOK, int MT, int WV = 4>
 static void gemm_launch(const GemmArgs& a, dim3 grid, hipStream_t s) {
-  // q8 in edgelm's per-block mode, 64-token tiles: one barrier per group of six blocks (measured at
-  // T = 512 against one per block: 4096 x 4096 47.7 -> 45.6 us, 4096 x 14336 126.1 -> 117.8 us,
-  // 14336 x 4096 95.0 -> 95.9 us; four blocks per group 46.3 / 121.1 / 96.5 us, two 51.3 / 144.6 /
-  // 98.4 us). ELMH_GEMM_KB=1 keeps one barrier per block; same bits.
-  if constexpr (WDT == WQ8 && !SW && !TOK && MT == 1) {
+  // edgelm's per-block mode, 64-token tiles: one barrier per group of six blocks. Measured at T = 512
+  // against one per block: q8 4096 x 4096 47.7 -> 45.6 us, 4096 x 14336 126.1 -> 117.8 us, 14336 x
+  // 4096 95.0 -> 95.9 us (four blocks per group 46.3 / 121.1 / 96.5 us, two 51.3 / 144.6 / 98.4 us);
+  // q4 against its block-pipelined eight-wave loop 58.4 -> 56.7, 161.5 -> 154.8, 117.5 -> 117.6 us.
+  // ELMH_GEMM_KB=1 keeps one barrier per block (q4: the pipelined loop); same bits.
+  if constexpr (!SW && !TOK && MT == 1) {
     const char* ev = getenv("ELMH_GEMM_KB");
     if (!(ev && ev[0] == '1')) {
       if (a.fast)

@@ -354,11 +354,11 @@ def test_gemm_token_tiles(ctx, dt, tile, monkeypatch):
     one) over several token tiles with a ragged last one and a partial last row tile: per-block
     int8 (exact, fast, residual), per-token int8 (block groups with a partial last group: K = 576
     is 18 blocks), MATMUL_N and FFN_SWIGLU. The tile height is forced with four and with eight waves
-    per workgroup (ELMH_GEMM_WAVES; eight serve the block-scale modes without SwiGLU), and the q8
+    per workgroup (ELMH_GEMM_WAVES; eight serve the block-scale modes without SwiGLU), and the
     per-block ring with one barrier per block (ELMH_GEMM_KB=1) as well as per group of six blocks."""
     for waves in ("8", "4"):
         monkeypatch.setenv("ELMH_GEMM_WAVES", waves)
-        for kb in ("6", "1") if dt == O.Q8 else ("6",):
+        for kb in ("6", "1"):
             monkeypatch.setenv("ELMH_GEMM_KB", kb)
             check_token_tiles(ctx, dt, tile, monkeypatch)
 
