@@ -1158,6 +1158,65 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
     // group between barriers. Blocks past the last are issued (repeats of it) but not computed.
     constexpr int KB = R::KB;
     static_assert(D % KB == 0 && D >= 2 * KB, "the ring holds whole groups, two at least");
+    // Within a group the blocks are software-pipelined: block k + 2's operands are read from LDS
+    // and block k + 1's MFMAs issued before block k's rescale, so reads and MFMAs run under it.
+    struct Ops {
+      v4i A[MT];
+      v4i B[NTW];
+      float c[NTW];
+      float xv[MT][16];
+    };
+    auto read_ops = [&](Ops& o, int slot) {
+      const unsigned char* sb = ring + slot * R::SLOT;
+      const unsigned char* wb = sb + R::ACT;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) o.A[mt] = *reinterpret_cast<const v4i*>(sb + ((wt * MT + mt) * 64 + lane) * 16);
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) {
+        const int rl = wr * 64 + (nt0 + nt) * 32 + l32;
+        o.c[nt] = 1.f;
+        if (WDT == WQ8) {
+          o.B[nt] = *reinterpret_cast<const v4i*>(wb + (2 * rl + (h ^ ((rl >> 3) & 1))) * 16);
+        } else {
+          o.B[nt] = q4_operand16(*reinterpret_cast<const uint4*>(wb + rl * 16), h);
+          o.c[nt] = reinterpret_cast<const float*>(wb + 2048)[rl];
+        }
+      }
+      const float* xs = reinterpret_cast<const float*>(sb + R::ACT + NSEL * R::WSEL);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 x4 = *reinterpret_cast<const float4*>(&xs[wt * 32 * MT + mt * 32 + 8 * g + 4 * h]);
+          o.xv[mt][4 * g] = x4.x;
+          o.xv[mt][4 * g + 1] = x4.y;
+          o.xv[mt][4 * g + 2] = x4.z;
+          o.xv[mt][4 * g + 3] = x4.w;
+        }
+    };
+    // block()'s arithmetic on operands already read: the MFMAs, then the rescale (skipped for the
+    // repeats past the last block)
+    auto mfma = [&](const Ops& o, v16i (&S)[MT][NTW]) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) S[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.A[mt], o.B[nt], zero, 0, 0, 0);
+    };
+    auto rescale = [&](const Ops& o, const v16i (&S)[MT][NTW]) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float m = WDT == WQ8 ? o.xv[mt][i] : o.c[nt] * o.xv[mt][i];
+            if (FAST) {
+              facc[0][mt][nt][i] = __builtin_fmaf((float)S[mt][nt][i], m, facc[0][mt][nt][i]);
+            } else {
+              facc[0][mt][nt][i] = facc[0][mt][nt][i] + (float)S[mt][nt][i] * m;
+            }
+          }
+    };
 #pragma unroll
     for (int i = 0; i < D - KB; ++i) issue(i, i);
     for (int b = 0; b < nb; b += KB) {
@@ -1165,9 +1224,19 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(SW && M
       lds_barrier();                   // every wave's part; every wave is done with the group before
 #pragma unroll
       for (int k = 0; k < KB; ++k) issue(b + D - KB + k, (b + D - KB + k) % D);
+      const int s0 = b % D;  // the group's first slot (groups never wrap: D is a multiple of KB)
+      // step k: read block k + 2's operands, start block k + 1's MFMAs, rescale block k
+      Ops o[3];
+      v16i S[2][MT][NTW];
+      read_ops(o[0], s0);
+      read_ops(o[1], s0 + 1);
+      mfma(o[0], S[0]);
 #pragma unroll
-      for (int k = 0; k < KB; ++k)
-        if (b + k < nb) block((b + k) % D);
+      for (int k = 0; k < KB; ++k) {
+        if (k + 2 < KB) read_ops(o[(k + 2) % 3], s0 + k + 2);
+        if (k + 1 < KB) mfma(o[(k + 1) % 3], S[(k + 1) & 1]);
+        if (b + k < nb) rescale(o[k % 3], S[k & 1]);
+      }
     }
   } else if constexpr (R::KB == 1) {
 #pragma unroll
