@@ -2910,7 +2910,10 @@ static hipError_t gemm_go(const GemmArgs& a, int tiles, hipStream_t s) {
   // token tiles are counted from T, so every tile starts at a valid token (its store range is
   // min(TT, T - t0) >= 1 tokens)
   const int t128 = tiles * ((a.T + 127) / 128), t64 = tiles * ((a.T + 63) / 64);
-  bool small = t128 < cus;
+  // per-token q8 keeps 128-token tiles down to half the CUs: its loop is all MFMA, and two token
+  // groups per wave gained more than the idle CUs cost (T = 512: 4096 x 4096 26.4 -> 25.6 us,
+  // 4096 x 14336 62.3 -> 57.8 us; the per-block modes lost: 44.2 -> 61.6, 110.7 -> 183.4 us)
+  bool small = TOK && WDT == WQ8 && !SW ? t128 < cus / 2 : t128 < cus;
   // problems that give the ring kernel fewer workgroups than half the CUs: one wave per 32 x 32 tile
   bool wave = t64 < cus / 2;
   // ELMH_GEMM_TOKEN_TILE=64 or 128 forces the ring kernel with one tile height; ELMH_GEMM_KERNEL=wave
