@@ -219,28 +219,27 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_frag_kernel(const float* __
   }
 }
 
-// Per-token scale (extension): one workgroup per token row. NPER > 0: a thread keeps its NPER
-// half-blocks (j = tid + 256 i) in registers between the row amax and the rounding (K <= NPER * 4096);
-// NPER == 0 reads the row twice, the second time from cache.
-template <int NPER>
+// Per-token scale (extension): one workgroup per token row. NF > 0: thread tid keeps the row's
+// float4s f = tid + 256 i (i < NF; K <= 1024 NF) in registers between the row amax and the rounding,
+// so each load instruction of a wave reads 1 KB of consecutive floats, and four consecutive lanes
+// write a half-block's 16 bytes (the rounding of a value does not depend on its group: elm_q8_group
+// of 4 gives the same q as of 16). NF == 0 reads the row twice, the second time from cache.
+template <int NF>
 __global__ __launch_bounds__(256) void act_quant_frag_token_kernel(const float* __restrict__ x, int T, int Tpad, int K,
                                                                    int8_t* __restrict__ xq, float* __restrict__ xd) {
+  asm volatile("" ::"s"(x), "s"(T), "s"(Tpad), "s"(K), "s"(xq), "s"(xd));
   __shared__ float red[4];
-  const int t = blockIdx.x, nb = K / kBlock, hb = 2 * nb;
+  const int t = blockIdx.x, nb = K / kBlock, hb = 2 * nb, K4 = K >> 2;
   const float* row = x + (int64_t)t * K;
-  constexpr int NR = NPER > 0 ? NPER : 1;
-  float4 v[NR][4];
+  constexpr int NR = NF > 0 ? NF : 1;
+  float4 v[NR];
   float a = 0.f;
-  if (NPER > 0) {
+  if (NF > 0) {
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      const int j = threadIdx.x + 256 * i;
-      const bool ok = t < T && j < hb;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        v[i][u] = ok ? ld4(row + j * 16, u) : make_float4(0.f, 0.f, 0.f, 0.f);
-        a = amax4(v[i][u], a);
-      }
+      const int f = threadIdx.x + 256 * i;
+      v[i] = t < T && f < K4 ? ld4(row + 4 * f, 0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      a = amax4(v[i], a);
     }
   } else if (t < T) {
     for (int j = threadIdx.x; j < hb; j += 256) {
@@ -255,12 +254,16 @@ __global__ __launch_bounds__(256) void act_quant_frag_token_kernel(const float* 
   a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float sc = a / 127.0f;
   const float safe = sc == 0.f ? 1.f : sc;
-  if (NPER > 0) {
+  if (NF > 0) {
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      const int j = threadIdx.x + 256 * i;
-      if (j < hb)
-        *reinterpret_cast<uint4*>(xq + frag_offset(t, j >> 1, j & 1, nb)) = q8x16(v[i], safe);
+      const int f = threadIdx.x + 256 * i, j = f >> 2;
+      if (f < K4) {
+        const float fv[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        int q[4];
+        elm_q8_group<4>(fv, safe, q);
+        *reinterpret_cast<uint32_t*>(xq + frag_offset(t, j >> 1, j & 1, nb) + (f & 3) * 4) = pack_q4(q);
+      }
     }
   } else {
     for (int j = threadIdx.x; j < hb; j += 256) {
@@ -2642,13 +2645,13 @@ hipError_t launch_rmsnorm_quant_frag(const float* x, const float* nw, float eps,
 }
 
 hipError_t launch_act_quant_frag_token(const float* x, int T, int Tpad, int K, int8_t* xq, float* xd, hipStream_t s) {
-  const int hb = 2 * (K / kBlock);  // half-blocks per row
-  if (hb <= 256)
+  const int k4 = K / 4;  // float4s per row
+  if (k4 <= 256)
     act_quant_frag_token_kernel<1><<<Tpad, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
-  else if (hb <= 512)
-    act_quant_frag_token_kernel<2><<<Tpad, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
-  else if (hb <= 1024)
+  else if (k4 <= 1024)
     act_quant_frag_token_kernel<4><<<Tpad, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
+  else if (k4 <= 4096)
+    act_quant_frag_token_kernel<16><<<Tpad, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
   else
     act_quant_frag_token_kernel<0><<<Tpad, 256, 0, s>>>(x, T, Tpad, K, xq, xd);
   return hipGetLastError();
