@@ -899,6 +899,20 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
   // lane % 16); the last piece repeats the last row
   // (each lane's source is picked without a branch, so that the copies issue back to back)
   auto dma_rows = [&](const float* cache, const float* step, int c0, int rows, float* dst, bool swz) {
+    if (!fresh || c0 >= pos0 || c0 + rows <= pos0) {
+      // one source for the whole range (uniform): a scalar base and 32-bit lane offsets, a few
+      // instructions per copy (the per-lane 64-bit source select costs ~90 ns per copy)
+      const bool st = fresh && c0 >= pos0;
+      const float* const base = st ? step + (int64_t)kvh * HD : cache;
+      const int rstride = st ? n_kv * ROWB : ROWB, r00 = st ? c0 - pos0 : c0;
+      const unsigned dbase = (unsigned)(size_t)(LdsBytes)(unsigned char*)dst;
+      for (int pc = w; 4 * pc < rows; pc += 4) {
+        const int r = 4 * pc + (lane >> 4), s = lane & 15;
+        const int ch = swz ? s ^ (r & 15) : s;
+        dma16s(base, (uint32_t)((r00 + min(r, rows - 1)) * rstride + (ch << 4)), dbase + pc * 1024);
+      }
+      return;
+    }
     const int64_t sstride = (int64_t)n_kv * HD;
     const float* const sbase = (fresh ? step : cache) + (fresh ? (int64_t)kvh * HD - (int64_t)pos0 * sstride : 0);
     for (int pc = w; 4 * pc < rows; pc += 4) {
