@@ -424,6 +424,29 @@ def test_gemm_kernels_small_and_ragged(ctx, dt, kernel, monkeypatch):
             d.free()
 
 
+@pytest.mark.parametrize("dt", [O.Q8, O.Q4])
+def test_gemm_ring_short_rows(ctx, dt, monkeypatch):
+    """The LDS-ring GEMM in edgelm's per-block mode at rows shorter than one group of six blocks
+    (K = 32, 64: the only group is partial) and one full group plus a partial one (K = 224),
+    grouped and with one barrier per block (ELMH_GEMM_KB=1), exact and fast."""
+    monkeypatch.setenv("ELMH_GEMM_KERNEL", "ring")
+    r = rng(800 + dt)
+    for kb in ("6", "1"):
+        monkeypatch.setenv("ELMH_GEMM_KB", kb)
+        for n, k in [(72, 32), (130, 64), (200, 224)]:
+            w = weight(r, n, k, dt)
+            dw = up(ctx, w)
+            for T in [65, 130]:
+                print(f"[gpu] gemm ring short rows kb={kb} dt={dt} {n}x{k} T={T}", flush=True)
+                x = r.normal(0, 1, (T, k)).astype(np.float32)
+                res = r.normal(0, 1, (T, n)).astype(np.float32)
+                got = ctx.matmul(x, [dw], [res], act=E.ACT_INT8, mode=E.EXACT)[0]
+                assert bits_equal(got, O.cpu_matmul(x, [w], [res], act_quant=True)[0]), f"{n}x{k} T={T}"
+                fast = ctx.matmul(x, [dw], None, act=E.ACT_INT8, mode=E.FAST)[0]
+                assert rel_err(fast, O.cpu_matmul(x, [w], None, act_quant=True)[0]) < 1e-5
+            dw.free()
+
+
 @pytest.mark.parametrize("tile", ["64", "128"])
 def test_gemm_token_odd_block_count(ctx, tile, monkeypatch):
     """Per-token q8 GEMM at K = 1568 (49 blocks): the last group of 4 (64-token tiles) or 2
