@@ -339,7 +339,8 @@ __device__ __forceinline__ void gemv_fold(const GemvArgs& a, const GemvLds& L, c
   if ((tid & ~63) >= fold_lanes<SW>(a.T, R)) return;  // whole waves only: the swap needs every lane
   int sel, pr;
   fold_lane<SW>(tid, sel, pr);
-  const int ft = pr / R, fr = pr - ft * R, fn = n0 + fr;
+  // one token (NT == 1): every live lane has pr < R, so the division is skipped
+  const int ft = NT == 1 ? 0 : pr / R, fr = pr - ft * R, fn = n0 + fr;
   const bool live = pr < a.T * R && fr < rows && fn < tg.N;
   float v = fold_chain(L.p + (live ? (sel * NT + ft) * R + fr : 0) * L.pst, a.nb);
   if (WDT == WQ8) v = v * e_s;
@@ -531,7 +532,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
     for (int p = 0; p < XP; ++p) {
       const int e = p * kSmallPass + e0;
       if (e < nel) {
-        const int t = e / K;
+        const int t = NT == 1 ? 0 : e / K;  // one token: no division
         float* r = sq + t * 4 * rowlen + ((e - t * K) >> 2);
         r[0] = xv[p].x * xv[p].x;
         r[rowlen] = xv[p].y * xv[p].y;
@@ -552,7 +553,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
     lds_barrier();
 #pragma unroll
     for (int p = 0; p < XP; ++p) {
-      const float inv = inv_l[min(p * kSmallPass + e0, nel - 4) / K];
+      const float inv = inv_l[NT == 1 ? 0 : min(p * kSmallPass + e0, nel - 4) / K];
       xv[p] = make_float4((xv[p].x * inv) * nv[p].x, (xv[p].y * inv) * nv[p].y, (xv[p].z * inv) * nv[p].z,
                           (xv[p].w * inv) * nv[p].w);
     }
@@ -563,7 +564,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
     int qv[4], qs;
     const float sc = quant_block8x4(v, qv, qs);
     if (e < nel) {
-      const int g = e >> 5, t = g / nb, b = g - t * nb;
+      const int g = e >> 5, t = NT == 1 ? 0 : g / nb, b = g - t * nb;
       *reinterpret_cast<uint32_t*>(L.q + t * L.kpad + b * kBlock + (e & 31)) = pack_q4(qv);
       if ((e & 31) == 0) {
         L.d[t * nb + b] = sc;
