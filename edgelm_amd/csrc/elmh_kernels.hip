@@ -470,29 +470,44 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   // every launch argument this kernel reads, in scalar registers before anything else: the
   // compiler issues their loads as one batch (one round trip to the argument segment) instead of
   // loading each near its first use, behind the waits for the ones before
-  if (MT && !SW)
-    asm volatile("" ::"s"(a.x), "s"(a.T), "s"(a.K), "s"(a.nb), "s"(a.H), "s"(a.rsub), "s"(a.n_targets),
-                 "s"(a.tile_start[1]), "s"(a.tile_start[2]), "s"(a.tile_start[3]), "s"(a.tile_start[4]));
-  else
+  // MT (a fused QKV): every target's fields too, through one statement as outputs, so that the
+  // target is picked by selects instead of a second batch of loads at its index (which the first
+  // activation load would wait for)
+  int ts1 = a.tile_start[1], ts2 = a.tile_start[2], ts3 = a.tile_start[3], ntg = a.n_targets;
+  const uint8_t *d0 = a.tg[0].data, *d1 = a.tg[1].data, *d2 = a.tg[2].data, *d3 = a.tg[3].data;
+  const float *s0 = a.tg[0].scales, *s1 = a.tg[1].scales, *s2 = a.tg[2].scales, *s3 = a.tg[3].scales;
+  float *y0 = a.tg[0].y, *y1 = a.tg[1].y, *y2 = a.tg[2].y, *y3 = a.tg[3].y;
+  const float *q0 = a.tg[0].res, *q1 = a.tg[1].res, *q2 = a.tg[2].res, *q3 = a.tg[3].res;
+  int n0t = a.tg[0].N, n1t = a.tg[1].N, n2t = a.tg[2].N, n3t = a.tg[3].N;
+  // (the RMSNORM operands go through the same statement: a second statement's loads would be a
+  // second batch)
+  if constexpr (MT && !SW) {
+#define ELM_GS_MT_OUT                                                                                   \
+  "+s"(ts1), "+s"(ts2), "+s"(ts3), "+s"(ntg), "+s"(d0), "+s"(d1), "+s"(d2), "+s"(d3), "+s"(s0), "+s"(s1), \
+      "+s"(s2), "+s"(s3), "+s"(y0), "+s"(y1), "+s"(y2), "+s"(y3), "+s"(q0), "+s"(q1), "+s"(q2), "+s"(q3),  \
+      "+s"(n0t), "+s"(n1t), "+s"(n2t), "+s"(n3t)
+    if constexpr (NORM)
+      asm volatile("" : ELM_GS_MT_OUT
+                   : "s"(a.x), "s"(a.T), "s"(a.K), "s"(a.nb), "s"(a.H), "s"(a.rsub), "s"(a.nw), "s"(a.eps),
+                     "s"(a.tile_start[4]));
+    else
+      asm volatile("" : ELM_GS_MT_OUT
+                   : "s"(a.x), "s"(a.T), "s"(a.K), "s"(a.nb), "s"(a.H), "s"(a.rsub), "s"(a.tile_start[4]));
+#undef ELM_GS_MT_OUT
+  } else {
     asm volatile("" ::"s"(a.x), "s"(a.T), "s"(a.K), "s"(a.nb), "s"(a.H), "s"(a.rsub), "s"(a.tg[0].data),
                  "s"(a.tg[0].scales), "s"(a.tg[0].y), "s"(a.tg[0].res), "s"(a.tg[0].N));
-  if (NORM) asm volatile("" ::"s"(a.nw), "s"(a.eps));
-  if (SW) asm volatile("" ::"s"(a.tg[1].data), "s"(a.tg[1].scales));
+    if (NORM) asm volatile("" ::"s"(a.nw), "s"(a.eps));
+    if (SW) asm volatile("" ::"s"(a.tg[1].data), "s"(a.tg[1].scales));
+  }
   const int K = a.K, nb = a.nb, T = a.T, H = a.H, tid = threadIdx.x;
   const GemvLds L = gemv_lds<NT>(smem, K, nb);
   // a workgroup takes RS rows (a power of two dividing H) of an H-row tile: part `part` of tile `tile`
   const int RS = a.rsub ? a.rsub : H, lgRS = __builtin_ctz(RS), lgsplit = __builtin_ctz(H) - lgRS;
-  int wg = blockIdx.x;
-  const GemvTarget tg = gemv_target<SW, MT>(a, wg);
-  const int tile = wg >> lgsplit, part = wg & ((1 << lgsplit) - 1), n0 = tile * H + part * RS;
-  const int64_t ibase = (int64_t)tile * H * nb + part * RS;  // item (row n0, block 0); (row n0 + r, block b) at + b H + r
-  const uint8_t* const wd1 = SW ? a.tg[1].data : tg.data;
-  const float* const ws1 = SW ? a.tg[1].scales : tg.scales;
-  const int per_sel = RS * nb, items = (SW ? 2 : 1) * per_sel;
   const int nel = T * K;
-
-  // 1. every pass's activation values (first: their wait does not cover the weight loads issued
-  // next; loads past the end repeat the last float4), with NORM also the norm weights
+  // 1. every pass's activation values (first, before the target is picked: their wait does not
+  // cover the weight loads issued next; loads past the end repeat the last float4), with NORM also
+  // the norm weights
   const int e0 = tid * 4;
   constexpr int XP = kSmallMaxAct / kSmallPass;
   float4 xv[XP], nv[XP];
@@ -500,8 +515,29 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_small_kernel(const GemvArgs
   for (int p = 0; p < XP; ++p) {
     const int e = min(p * kSmallPass + e0, nel - 4);
     xv[p] = *reinterpret_cast<const float4*>(a.x + e);  // unconditional: keeps the wait counts exact
-    if (NORM) nv[p] = *reinterpret_cast<const float4*>(a.nw + (e - e / K * K));
+    if (NORM) nv[p] = *reinterpret_cast<const float4*>(a.nw + (NT == 1 ? e : e - e / K * K));  // one token: e < K
   }
+  __builtin_amdgcn_sched_barrier(0);  // the activation requests go out before the target selection
+  int wg = blockIdx.x;
+  GemvTarget tg;
+  if constexpr (MT && !SW) {
+    const int ti = (ntg > 1 && wg >= ts1) + (ntg > 2 && wg >= ts2) + (ntg > 3 && wg >= ts3);
+    wg -= ti == 0 ? 0 : ti == 1 ? ts1 : ti == 2 ? ts2 : ts3;
+    tg.data = pin_global(ti == 0 ? d0 : ti == 1 ? d1 : ti == 2 ? d2 : d3);
+    tg.scales = pin_global(ti == 0 ? s0 : ti == 1 ? s1 : ti == 2 ? s2 : s3);
+    tg.y = pin_global(ti == 0 ? y0 : ti == 1 ? y1 : ti == 2 ? y2 : y3);
+    tg.res = pin_global(ti == 0 ? q0 : ti == 1 ? q1 : ti == 2 ? q2 : q3);
+    tg.N = ti == 0 ? n0t : ti == 1 ? n1t : ti == 2 ? n2t : n3t;
+    tg.tiles = 0;  // not read here
+  } else {
+    tg = gemv_target<SW, MT>(a, wg);
+  }
+  const int tile = wg >> lgsplit, part = wg & ((1 << lgsplit) - 1), n0 = tile * H + part * RS;
+  const int64_t ibase = (int64_t)tile * H * nb + part * RS;  // item (row n0, block 0); (row n0 + r, block b) at + b H + r
+  const uint8_t* const wd1 = SW ? a.tg[1].data : tg.data;
+  const float* const ws1 = SW ? a.tg[1].scales : tg.scales;
+  const int per_sel = RS * nb, items = (SW ? 2 : 1) * per_sel;
+
   // 2. weights of this thread's first two items
   v4u w[2][G / 16];
   float wsc[2] = {0.f, 0.f};
