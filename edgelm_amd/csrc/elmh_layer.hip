@@ -553,13 +553,13 @@ tail:
 
 __global__ __launch_bounds__(256) void attention_decode64_kernel(
     const float* __restrict__ q, float* __restrict__ out, float* __restrict__ kc, float* __restrict__ vc, int pos0,
-    const int* __restrict__ pos_dev, int n_heads, int n_kv, int max_ctx, int n_cap, const float* __restrict__ rcos,
+    const int* __restrict__ pos_dev, int grp, int n_kv, int max_ctx, int n_cap, const float* __restrict__ rcos,
     const float* __restrict__ rsin, const float* __restrict__ knew, const float* __restrict__ vnew) {
   constexpr int HD = 64, H2 = 32, C = kDecRows, ROWB = HD * 4;
   // Every argument into scalar registers before anything else: their loads go out as one batch, so the
   // first memory requests wait for one round trip to the argument segment (loaded near their first
   // uses instead, they took three, one behind the other).
-  asm volatile("" ::"s"(q), "s"(out), "s"(kc), "s"(vc), "s"(pos0), "s"(pos_dev), "s"(n_heads), "s"(n_kv),
+  asm volatile("" ::"s"(q), "s"(out), "s"(kc), "s"(vc), "s"(pos0), "s"(pos_dev), "s"(grp), "s"(n_kv),
                "s"(max_ctx), "s"(n_cap), "s"(rcos), "s"(rsin), "s"(knew), "s"(vnew));
   extern __shared__ __align__(16) float lds[];
   float* const kb = lds;
@@ -571,7 +571,9 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
   __shared__ float inv_s;
   // the wave index as a scalar: loops over it stay scalar loops instead of divergent ones
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int h = blockIdx.x, grp = n_heads / n_kv, kvh = h / grp;
+  // workgroup (kv head, head of its group): the grid is n_kv x grp (grp = n_heads / n_kv, passed in),
+  // so the head needs no division
+  const int kvh = blockIdx.x, h = kvh * grp + blockIdx.y;
   const float* const kh = kc + (int64_t)kvh * max_ctx * HD;
   const float* const vh = vc + (int64_t)kvh * max_ctx * HD;
   const unsigned kb_lds = (unsigned)(size_t)(LdsBytes)(unsigned char*)kb;
@@ -619,7 +621,7 @@ __global__ __launch_bounds__(256) void attention_decode64_kernel(
     qb[tid + H2] = q1;
     kn[tid] = k0;
     kn[tid + H2] = k1;
-    if (h % grp == 0) {  // the kv group's first workgroup appends to the cache
+    if (blockIdx.y == 0) {  // the kv group's first workgroup appends to the cache
       float* const kd = kc + ((int64_t)kvh * max_ctx + pos) * HD;
       float* const vd = vc + ((int64_t)kvh * max_ctx + pos) * HD;
       kd[tid] = k0;
@@ -1480,8 +1482,8 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
   if (!in_lds && !gscores) return hipErrorInvalidValue;  // a score row past LDS needs the global rows
   const size_t lds_gs = attention_gs_lds_bytes(hd), lds = attention_lds_bytes(hd, n_cap);
   if (fuse && hd == 64 && attention_decode_lds_bytes(n_cap) <= kMaxAttnLds)
-    attention_decode64_kernel<<<n_heads, 256, attention_decode_lds_bytes(n_cap), s>>>(
-        q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, max_ctx, n_cap, rcos, rsin, k, v);
+    attention_decode64_kernel<<<dim3(n_kv, n_heads / n_kv), 256, attention_decode_lds_bytes(n_cap), s>>>(
+        q, out, kc, vc, pos0, pos_dev, n_heads / n_kv, n_kv, max_ctx, n_cap, rcos, rsin, k, v);
   else if (hd == 64 && in_lds)
     attention_kernel<64, false><<<T * n_heads, kAttnThreads, lds, s>>>(
         q, out, kc, vc, pos0, pos_dev, n_heads, n_kv, hd, max_ctx, n_cap, rcos, rsin, kn, vn, nullptr);
