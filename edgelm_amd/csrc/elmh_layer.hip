@@ -872,12 +872,12 @@ constexpr int kPfRows = 128;
 
 __global__ __launch_bounds__(256) void attention_prefill64_kernel(
     const float* __restrict__ q, float* __restrict__ out, float* __restrict__ kc, float* __restrict__ vc, int pos0,
-    int T, int n_heads, int n_kv, int max_ctx, int n_cap, const float* __restrict__ rcos, const float* __restrict__ rsin,
+    int T, int grp, int n_kv, int max_ctx, int n_cap, const float* __restrict__ rcos, const float* __restrict__ rsin,
     int8_t* __restrict__ xq, float* __restrict__ xd, int Tpad, const float* __restrict__ knew,
     const float* __restrict__ vnew) {
   constexpr int HD = 64, H2 = 32, R = kPfRows, ROWB = HD * 4;
   // every argument into scalar registers first, in one batch of loads (as the decode kernel)
-  asm volatile("" ::"s"(q), "s"(out), "s"(kc), "s"(vc), "s"(pos0), "s"(T), "s"(n_heads), "s"(n_kv), "s"(max_ctx),
+  asm volatile("" ::"s"(q), "s"(out), "s"(kc), "s"(vc), "s"(pos0), "s"(T), "s"(grp), "s"(n_kv), "s"(max_ctx),
                "s"(n_cap), "s"(rcos), "s"(rsin), "s"(xq), "s"(xd), "s"(Tpad), "s"(knew), "s"(vnew));
   extern __shared__ __align__(16) float lds[];
   const int scs = (n_cap + 255) & ~255;  // score row stride
@@ -887,12 +887,13 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
   float* const qb = sc + kAttnQ * scs;   // [kAttnQ][64]
   // the wave index as a scalar: loops over it stay scalar loops instead of divergent ones
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ngr = (T + kAttnQ - 1) / kAttnQ;
-  const int h = blockIdx.x / ngr, t0 = (blockIdx.x - h * ngr) * kAttnQ;
+  // workgroup (query group, head of its kv group, kv head): the grid is ngr x grp x n_kv (grp =
+  // n_heads / n_kv, passed in), so the head and kv head need no integer division
+  const int kvh = blockIdx.z, h = kvh * grp + blockIdx.y, t0 = blockIdx.x * kAttnQ, n_heads = grp * n_kv;
   const int nq = min(kAttnQ, T - t0);                                   // queries in this group
   const int tw = t0 + min(w, nq - 1), posw = pos0 + tw, nw = posw + 1;  // this wave's query
   const int nmax = pos0 + t0 + nq;                                      // the group's positions
-  const int qd = n_heads * HD, grp = n_heads / n_kv, kvh = h / grp;
+  const int qd = n_heads * HD;
   float* const kh = kc + (int64_t)kvh * max_ctx * HD;
   float* const vh = vc + (int64_t)kvh * max_ctx * HD;
   const bool fresh = knew != nullptr;  // rows from pos0 on: the step's keys and values, not the cache
@@ -967,7 +968,7 @@ __global__ __launch_bounds__(256) void attention_prefill64_kernel(
     }
   }
   // the append: token t0 + w's key element `lane`, rotated, and its value (kv group's first head)
-  const bool writer = fresh && h % grp == 0 && w < nq;
+  const bool writer = fresh && blockIdx.y == 0 && w < nq;
   float ak = 0.f, ap = 0.f, ac = 1.f, as = 0.f, av = 0.f;
   if (writer) {
     const float* const ks = knew + ((int64_t)(t0 + w) * n_kv + kvh) * HD;
@@ -1461,9 +1462,9 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, floa
   if (pf64) {
     const int ngr = (T + kAttnQ - 1) / kAttnQ;
     const bool quant = xq && xd && quantized;
-    attention_prefill64_kernel<<<n_heads * ngr, 256, lds_pf64, s>>>(q, out, kc, vc, pos0, T, n_heads, n_kv, max_ctx,
-                                                                    n_cap, rcos, rsin, quant ? xq : nullptr,
-                                                                    quant ? xd : nullptr, Tpad, k, v);
+    attention_prefill64_kernel<<<dim3(ngr, n_heads / n_kv, n_kv), 256, lds_pf64, s>>>(
+        q, out, kc, vc, pos0, T, n_heads / n_kv, n_kv, max_ctx, n_cap, rcos, rsin, quant ? xq : nullptr,
+        quant ? xd : nullptr, Tpad, k, v);
     const hipError_t e = hipGetLastError();
     if (e == hipSuccess && quant) *quantized = true;
     return e;
