@@ -717,7 +717,7 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
     // whenever it is ready, or it waits its turn behind their products on the same SIMD.
     __builtin_amdgcn_s_setprio(3);
     const int lane = tid - P;
-    const int ft = lane / R, fr = lane - ft * R, ftl = fr >> lgH;
+    const int ft = NT == 1 ? 0 : lane / R, fr = lane - ft * R, ftl = fr >> lgH;
     const bool folder = lane < T * R && fr < rows;
     const float* const frow_g = L.p + (ft * R + fr) * L.pst;
     const float* const frow_u = L.p + ((NT + ft) * R + fr) * L.pst;
@@ -845,7 +845,7 @@ __global__ __launch_bounds__(64 * (NPW + FW)) void gemv_stream_kernel(const Gemv
         for (int i = 0; i < QV; ++i) sm += q[i];
         sm += dpp_i<kDppQuadXor1>(sm);
         if (e < nel) {  // nel is a multiple of 32: both lanes of a block, or neither
-          const int g = e >> 5, t = g / nb, b = g - t * nb;
+          const int g = e >> 5, t = NT == 1 ? 0 : g / nb, b = g - t * nb;  // one token: g < nb
           uint4 pk;
           pk.x = pack_q4({q[0], q[1], q[2], q[3]});
           pk.y = pack_q4({q[4], q[5], q[6], q[7]});
